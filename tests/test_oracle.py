@@ -1,0 +1,445 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+Each oracle function is checked against something other than itself: the
+reference's golden vectors (gguf-py's decoded k-quant blocks, copied from the
+reference's tests/data/kquant_cases.json into tests/golden), the reference's
+own known-answer cases, an independent implementation (numpy's IEEE float16
+conversion; Hugging Face transformers' LlamaForCausalLM in float64), or
+closed forms and error bounds the mathematics fixes. CPU only.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from vkml_amd import gguf, synth
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def cases():
+    with open(os.path.join(HERE, "golden", "kquant_cases.json")) as f:
+        return {c["type"]: (bytes.fromhex(c["bytes"]), np.array(c["values"], np.float32)) for c in json.load(f)}
+
+
+# ---------------------------------------------------------------- f16 / bf16
+
+def test_f16_widening_matches_numpy_for_every_bit_pattern():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.f16_to_f32(bits)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f16_narrowing_matches_numpy_round_to_nearest_even():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 200000).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, 1e30, -1e30, np.inf, -np.inf,
+                  2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0000001, 2.0 ** -14, 2.0 ** -14 * 0.99999,
+                  1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11], np.float32),
+    ])
+    # every f16 value and the midpoints between neighbours (ties)
+    h = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    mids = ((h[:-1].astype(np.float64) + h[1:]) / 2).astype(np.float32)
+    x = np.concatenate([x, h, mids, -mids])
+    got = O.f32_to_f16(x)
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    # NaN: quiet, sign kept (host_quant.cpp:98)
+    assert O.f32_to_f16(np.array([np.nan], np.float32))[0] & 0x7E00 == 0x7E00
+
+
+# ---------------------------------------------------------------- k-quants
+
+@pytest.mark.parametrize("name,t", [("q4_1", O.GGML_Q4_1), ("q4_K", O.GGML_Q4_K), ("q6_K", O.GGML_Q6_K)])
+def test_block_decoders_match_gguf_py(name, t):
+    data, want = cases()[name]
+    got = O.dequantize_ggml(t, data)
+    assert got.shape == want.shape
+    assert np.all(np.abs(got - want) <= 1e-6 * (1 + np.abs(want)))  # test_gguf.cpp:276-280
+
+
+def test_q4_k_repacks_to_q4_1_with_f16_rounded_products():
+    data, want = cases()["q4_K"]
+    rows, cols = 1, want.size
+    quant, words, halves = O.load_quantized(O.GGML_Q4_K, data, rows, cols)
+    assert quant == O.Q4_1
+    # Independently: each sub-block's scale is f16(d * sc) and offset
+    # f16(-(dmin * m)), products exact in f32 (d has 11 bits, sc/m 6).
+    blocks = np.frombuffer(data, np.uint8).reshape(-1, 144)
+    for b, blk in enumerate(blocks):
+        d = np.frombuffer(blk[0:2].tobytes(), np.float16)[0].astype(np.float64)
+        dmin = np.frombuffer(blk[2:4].tobytes(), np.float16)[0].astype(np.float64)
+        q = blk[4:16]
+        for j in range(8):
+            if j < 4:
+                sc, m = q[j] & 63, q[j + 4] & 63
+            else:
+                sc, m = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4), (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
+            g = b * 8 + j
+            assert halves[2 * g] == np.float16(d * sc).view(np.uint16)
+            assert halves[2 * g + 1] == np.float16(-(dmin * m)).view(np.uint16)
+    got = O.dequantize(O.Q4_1, words, halves, rows, cols).ravel()
+    # test_gguf.cpp:365-376: within 2^-11 of 31 max|value| of the sub-block
+    for s in range(0, want.size, 32):
+        tol = 31 * np.abs(want[s:s + 32]).max() * 2.0 ** -11 + 1e-6
+        assert np.all(np.abs(got[s:s + 32] - want[s:s + 32]) <= tol)
+    # codes: nibble order of QuantizedMatrix (byte j: value j low, j + 4 high)
+    codes = np.array([(words[e // 8] >> (8 * (e % 4) + 4 * ((e // 4) % 2))) & 15 for e in range(cols)])
+    low = blocks[:, 16:].reshape(-1, 4, 32)
+    want_codes = np.stack([low & 15, low >> 4], axis=2).reshape(-1)
+    assert np.array_equal(codes, want_codes)
+
+
+def test_q4_1_loads_exactly():
+    data, want = cases()["q4_1"]
+    quant, words, halves = O.load_quantized(O.GGML_Q4_1, data, 1, want.size)
+    got = O.dequantize(O.Q4_1, words, halves, 1, want.size).ravel()
+    assert quant == O.Q4_1
+    assert np.all(np.abs(got - want) <= 1e-6 * np.abs(want).max() + 1e-6)
+
+
+def test_q6_k_requantizes_to_q8_0_within_half_a_step():
+    data, want = cases()["q6_K"]
+    rows, cols = 2, want.size // 2
+    words, halves = O.load_q8(O.GGML_Q6_K, data, rows, cols)
+    got = O.dequantize(O.Q8_0, words, halves, rows, cols).ravel()
+    for b in range(0, want.size, 32):
+        step = np.abs(want[b:b + 32]).max() / 127 * (1 + 2.0 ** -11)
+        assert np.all(np.abs(got[b:b + 32] - want[b:b + 32]) <= step * 0.5001 + 1e-7)  # test_gguf.cpp:323-331
+
+
+# ---------------------------------------------------------------- quantize
+
+def test_quantize_q8_known_answers():
+    # test_quantize.cpp:93-116: 1 comes back as 127 steps of f16(1/127); zero blocks are zero
+    ones = np.ones(64, np.float32)
+    w, s = O.quantize(O.Q8_0, ones, True)
+    back = O.dequantize(O.Q8_0, w, s, 1, 64).ravel()
+    one = np.float32(127) * np.float32(np.float16(np.float32(1) / np.float32(127)))
+    assert one != 1.0 and np.all(back == one)
+    x = np.concatenate([np.zeros(32, np.float32), -np.ones(64, np.float32)])
+    w, s = O.quantize(O.Q8_0, x, True)
+    back = O.dequantize(O.Q8_0, w, s, 1, 96).ravel()
+    assert np.all(back[:32] == 0) and np.all(back[32:] == -one) and s[0] == 0
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_quantize_q8_is_round_to_nearest_of_absmax_over_127(f16):
+    rng = np.random.default_rng(51)
+    x = (rng.standard_normal((5, 96)) * 0.1).astype(np.float32)
+    x[1, 8] = 3.0
+    w, s = O.quantize(O.Q8_0, x, f16)
+    scales = O.f16_to_f32(s) if f16 else s
+    back = O.dequantize(O.Q8_0, w, s, 5, 96)
+    all_codes = w.view(np.int8).reshape(-1, 32).astype(np.float32)
+    for b in range(15):
+        blk = x.reshape(-1, 32)[b]
+        d = scales[b]
+        exact = np.abs(blk).max() / 127
+        assert abs(d - exact) <= exact * (2.0 ** -11 if f16 else 2.0 ** -23)
+        codes = all_codes[b]
+        assert np.all(np.abs(codes) <= 127)
+        assert np.array_equal(back.reshape(-1, 32)[b], codes * np.float32(d))
+        assert np.all(np.abs(back.reshape(-1, 32)[b] - blk) <= 0.5 * d * 1.0001 + 1e-12)
+        # the block's absmax is exactly +-127 steps
+        i = np.argmax(np.abs(blk))
+        assert abs(codes[i]) == 127
+    # ties round to even: x * inv lands on k + 0.5 exactly for d = 1
+    t = np.zeros(32, np.float32)
+    t[0], t[1], t[2], t[3] = 127.0, 2.5, 3.5, -2.5
+    w, s = O.quantize(O.Q8_0, t, f16)
+    codes = O.dequantize(O.Q8_0, w, s, 1, 32).ravel()
+    assert list(codes[:4]) == [127.0, 2.0, 4.0, -2.0]
+
+
+def test_quantize_q4_0_and_q4_1_known_answers():
+    rng = np.random.default_rng(54)
+    x = (rng.standard_normal(3 * 64) * 0.1).astype(np.float32)
+    x[70], x[101] = -2.0, 1.5  # test_quantize.cpp:122-160
+    w, s = O.quantize(O.Q4_0, x, True)
+    back = O.dequantize(O.Q4_0, w, s, 3, 64).ravel()
+    assert back[70] == -2.0 and back[101] == 1.5
+    d = O.f16_to_f32(s)
+    for b in range(6):
+        blk = x[b * 32:(b + 1) * 32]
+        want = np.clip(np.round(blk / d[b]), -8, 7) * d[b]
+        assert np.all(np.abs(back[b * 32:(b + 1) * 32] - want) <= abs(d[b]) * 1e-5)
+    w, s = O.quantize(O.Q4_1, x, True)
+    back = O.dequantize(O.Q4_1, w, s, 3, 64).ravel()
+    for b in range(6):
+        blk = x[b * 32:(b + 1) * 32]
+        step = (blk.max() - blk.min()) / 15
+        assert np.all(np.abs(back[b * 32:(b + 1) * 32] - blk) <= 0.5 * step * 1.01 + abs(blk).max() * 2 ** -10)
+
+
+# ---------------------------------------------------------------- products
+
+def _weights(quant, n, k, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    words, scales = O.quantize(quant, w, True)
+    return words, scales, O.dequantize(quant, words, scales, n, k)
+
+
+@pytest.mark.parametrize("quant", [O.Q8_0, O.Q4_0, O.Q4_1])
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_gemv_dot_within_the_f32_dot_bound(quant, m):
+    # test_quantize.cpp:197-224: against double(dequantized W) x double(dequantized a_q)
+    n, k = 37, 320
+    bw, bs, wd = _weights(quant, n, k, 7)
+    a = np.random.default_rng(8).standard_normal((m, k)).astype(np.float32)
+    aw, asc = O.quantize(O.Q8_0, a, False)
+    ad = O.dequantize(O.Q8_0, aw, asc, m, k).astype(np.float64)
+    got = O.gemv_dot(quant, aw, asc, m, bw, bs, n, k)
+    want = ad @ wd.astype(np.float64).T
+    bound = 2 * k * 2.0 ** -24 * (np.abs(ad) @ np.abs(wd.astype(np.float64)).T)
+    if quant == O.Q4_1:
+        bound *= 3  # the offset term's extra rounding (test_quantize.cpp:210-214)
+    assert np.all(np.abs(got - want) <= bound + 1e-30)
+    got2 = O.matmul_dot(quant, aw, asc, m, bw, bs, n, k)
+    assert np.all(np.abs(got2 - want) <= bound + 1e-30)
+
+
+def test_gemv_dot_quarters_closed_form():
+    # vkml_bench.cpp:119-151,206-215: every weight 0.25, every output value * 0.25 * cols
+    k, n = 4096, 64
+    w = np.full((n, k), 0.25, np.float32)
+    bw, bs = O.quantize(O.Q8_0, w, True)
+    a = np.full((1, k), 1.0, np.float32)
+    aw, asc = O.quantize(O.Q8_0, a, False)
+    got = O.gemv_dot(O.Q8_0, aw, asc, 1, bw, bs, n, k)
+    ad = O.dequantize(O.Q8_0, aw, asc, 1, k)[0, 0]
+    wd = O.dequantize(O.Q8_0, bw, bs, n, k)[0, 0]
+    assert np.all(got == np.float32(ad) * np.float32(wd) * k)
+
+
+def test_gemv_dot_small_exact_integers():
+    # per-block scales of 1: integer codes multiply exactly
+    k = 64
+    a = np.arange(-32, 32, dtype=np.float32)
+    a[0] = -127
+    b = np.tile(np.arange(16, dtype=np.float32) - 8, 4)
+    b[0] = -8
+    aw, asc = O.quantize(O.Q8_0, a, False)
+    bw, bs = O.quantize(O.Q4_0, b[None, :], True)
+    got = O.gemv_dot(O.Q4_0, aw, asc, 1, bw, bs, 1, k)[0, 0]
+    ad = O.dequantize(O.Q8_0, aw, asc, 1, k).ravel().astype(np.float64)
+    bd = O.dequantize(O.Q4_0, bw, bs, 1, k).ravel().astype(np.float64)
+    assert abs(got - ad @ bd) <= 1e-4 * abs(ad @ bd)
+
+
+@pytest.mark.parametrize("t", [O.T_F32, O.T_F16, O.T_BF16, O.T_Q8, O.T_Q4, O.T_Q4_1])
+@pytest.mark.parametrize("k", [256, 688, 30])
+def test_gemv_float_within_the_f32_dot_bound(t, k):
+    if t >= O.T_Q8 and k % 32:
+        pytest.skip("quantized rows are whole blocks")
+    n, m = 41, 2
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    sc = None
+    if t == O.T_F32:
+        b, wd = w, w
+    elif t == O.T_F16:
+        b = w.astype(np.float16).view(np.uint16); wd = b.view(np.float16).astype(np.float32)
+    elif t == O.T_BF16:
+        b = (w.view(np.uint32) >> 16).astype(np.uint16); wd = (b.astype(np.uint32) << 16).view(np.float32)
+    else:
+        quant = {O.T_Q8: O.Q8_0, O.T_Q4: O.Q4_0, O.T_Q4_1: O.Q4_1}[t]
+        b, sc = O.quantize(quant, w, True); wd = O.dequantize(quant, b, sc, n, k)
+    got = O.gemv_float(t, a, b, sc, n, k)
+    want = a.astype(np.float64) @ wd.astype(np.float64).T
+    bound = 3 * k * 2.0 ** -24 * (np.abs(a.astype(np.float64)) @ np.abs(wd.astype(np.float64)).T)
+    assert np.all(np.abs(got - want) <= bound + 1e-30)
+
+
+# ---------------------------------------------------------------- small ops
+
+def test_rms_norm_matches_double():
+    rng = np.random.default_rng(3)
+    for cols in (1, 100, 4096, 14336):
+        x = rng.standard_normal((3, cols)).astype(np.float32)
+        w = rng.standard_normal(cols).astype(np.float32)
+        got = O.rms_norm(x, w, 1e-5)
+        xd = x.astype(np.float64)
+        want = xd / np.sqrt((xd * xd).mean(1, keepdims=True) + 1e-5) * w
+        assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+
+
+def test_rope_table_entries_and_rotation():
+    t = O.rope_table(3, 4, 100.0)
+    assert t[2, 1, 0] == np.float32(math.cos(0.2)) and t[2, 1, 1] == np.float32(math.sin(0.2))
+    x = np.random.default_rng(22).standard_normal((1, 3, 8)).astype(np.float32)
+    assert np.array_equal(O.rope(x, O.rope_table(4, 8, 1e4), 0, 1), x)
+    # interleaved rotation against double at a far position
+    table = O.rope_table(9000, 64, 1e6)
+    x = np.random.default_rng(5).standard_normal((1, 2, 64)).astype(np.float32)
+    got = O.rope(x, table, 8000, 0)
+    inv = 1e6 ** (-2.0 * np.arange(32) / 64)
+    ang = 8000 * inv
+    a, b = x[..., 0::2].astype(np.float64), x[..., 1::2].astype(np.float64)
+    want = np.empty_like(x, dtype=np.float64)
+    want[..., 0::2] = a * np.cos(ang) - b * np.sin(ang)
+    want[..., 1::2] = a * np.sin(ang) + b * np.cos(ang)
+    assert np.allclose(got, want, atol=1e-5)
+
+
+def test_argmax_rules():
+    inf = np.inf
+    assert O.argmax(np.array([-inf, -inf, -5.0, -inf])) == 2
+    assert O.argmax(np.array([1.0, inf, 2.0, 3.0])) == 1
+    assert O.argmax(np.array([np.nan, 1.0, 3.0, np.nan, 3.0])) == 2
+    assert O.argmax(np.array([np.nan, np.nan])) == 0
+    x = np.random.default_rng(11).standard_normal(262144).astype(np.float32) * 3
+    x[-1] = x[-2] = 100.0
+    assert O.argmax(x) == 262142
+
+
+@pytest.mark.parametrize("hd,heads,kv_heads,kv_len,f16", [(64, 4, 2, 5, False), (128, 32, 8, 300, True),
+                                                          (64, 8, 8, 1, True), (256, 2, 1, 200, False)])
+def test_attend_decode_matches_double(hd, heads, kv_heads, kv_len, f16):
+    rng = np.random.default_rng(hd + kv_len)
+    cap = kv_len + 3
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    k = rng.standard_normal((kv_heads, cap, hd)).astype(np.float32)
+    v = rng.standard_normal((kv_heads, cap, hd)).astype(np.float32)
+    if f16:
+        k, v = k.astype(np.float16), v.astype(np.float16)
+        kc, vc = k.view(np.uint16), v.view(np.uint16)
+    else:
+        kc, vc = k, v
+    got = O.attend_decode(q, kc, vc, 0, kv_len)
+    kd, vd = k.astype(np.float64), v.astype(np.float64)
+    want = np.empty((heads, hd))
+    for h in range(heads):
+        kh = h // (heads // kv_heads)
+        s = kd[kh, :kv_len] @ q[h].astype(np.float64) / math.sqrt(hd)
+        p = np.exp(s - s.max())
+        want[h] = p @ vd[kh, :kv_len] / p.sum()
+    assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+
+
+def test_attend_first_key_alone_returns_v0_exactly():
+    q = np.array([[1.0]], np.float32).repeat(4, 1)
+    k = np.random.default_rng(1).standard_normal((1, 3, 4)).astype(np.float32)
+    v = np.random.default_rng(2).standard_normal((1, 3, 4)).astype(np.float32)
+    assert np.array_equal(O.attend_decode(q, k, v, 0, 1)[0], v[0, 0])
+
+
+# ---------------------------------------------------------------- whole model
+
+def _hf_logits(path, tokens):
+    """Hugging Face's LlamaForCausalLM in float64 on the file's dequantized
+    weights: an implementation independent of the oracle. GGUF's llama
+    rotates interleaved pairs; HF rotates halves, so q and k rows are put
+    back in HF order (the inverse of llama.cpp's converter permutation)."""
+    torch = pytest.importorskip("torch")
+    tr = pytest.importorskip("transformers")
+    meta, ts = gguf.read(path)
+    L = int(meta["llama.block_count"]); d = int(meta["llama.embedding_length"])
+    H = int(meta["llama.attention.head_count"]); KV = int(meta["llama.attention.head_count_kv"])
+    hd = int(meta["llama.attention.key_length"]); ff = int(meta["llama.feed_forward_length"])
+    vocab = ts["token_embd.weight"][0][0]
+
+    def val(name):
+        shape, t, data = ts[name]
+        if t == gguf.F32:
+            return np.frombuffer(data.tobytes(), np.float32).reshape(shape).astype(np.float64)
+        quant, words, halves = O.load_quantized(t, data.tobytes(), shape[0], shape[1]) if t in (gguf.Q4_K, gguf.Q8_0, gguf.Q4_0, gguf.Q4_1) \
+            else (O.Q8_0,) + O.load_q8(t, data.tobytes(), shape[0], shape[1])
+        return O.dequantize(quant, words, halves, shape[0], shape[1]).astype(np.float64)
+
+    def unpermute(w, heads):
+        return w.reshape(heads, hd // 2, 2, -1).transpose(0, 2, 1, 3).reshape(heads * hd, -1)
+
+    cfg = tr.LlamaConfig(vocab_size=vocab, hidden_size=d, intermediate_size=ff, num_hidden_layers=L,
+                         num_attention_heads=H, num_key_value_heads=KV, head_dim=hd,
+                         rms_norm_eps=float(meta["llama.attention.layer_norm_rms_epsilon"]),
+                         rope_theta=float(meta["llama.rope.freq_base"]),
+                         max_position_embeddings=int(meta["llama.context_length"]),
+                         tie_word_embeddings="output.weight" not in ts, attention_bias=False, mlp_bias=False)
+    cfg._attn_implementation = "eager"
+    model = tr.LlamaForCausalLM(cfg).to(torch.float64).eval()
+    sd = {"model.embed_tokens.weight": val("token_embd.weight"), "model.norm.weight": val("output_norm.weight")}
+    sd["lm_head.weight"] = val("output.weight") if "output.weight" in ts else sd["model.embed_tokens.weight"]
+    for l in range(L):
+        p, g = f"model.layers.{l}.", f"blk.{l}."
+        sd[p + "input_layernorm.weight"] = val(g + "attn_norm.weight")
+        sd[p + "post_attention_layernorm.weight"] = val(g + "ffn_norm.weight")
+        sd[p + "self_attn.q_proj.weight"] = unpermute(val(g + "attn_q.weight"), H)
+        sd[p + "self_attn.k_proj.weight"] = unpermute(val(g + "attn_k.weight"), KV)
+        sd[p + "self_attn.v_proj.weight"] = val(g + "attn_v.weight")
+        sd[p + "self_attn.o_proj.weight"] = val(g + "attn_output.weight")
+        sd[p + "mlp.gate_proj.weight"] = val(g + "ffn_gate.weight")
+        sd[p + "mlp.up_proj.weight"] = val(g + "ffn_up.weight")
+        sd[p + "mlp.down_proj.weight"] = val(g + "ffn_down.weight")
+    model.load_state_dict({k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in sd.items()}, strict=False)
+    with torch.no_grad():
+        out = model(torch.tensor([list(tokens)], dtype=torch.long)).logits[0, -1]
+    return out.numpy()
+
+
+@pytest.fixture(scope="module")
+def tiny_f32(tmp_path_factory):
+    spec = synth.CONFIGS["cfg1"]
+    return synth.write_model(spec, str(tmp_path_factory.mktemp("m") / "cfg1.gguf"), seed=1)
+
+
+@pytest.fixture(scope="module")
+def tiny_q4k(tmp_path_factory):
+    spec = synth.ModelSpec("tiny-q4k", 2, 256, 4, 2, 64, 512, 1000, 10000.0, max_positions=512,
+                           matrix_type=gguf.Q4_K, embed_type=gguf.Q4_K, output_type=gguf.Q6_K)
+    return synth.write_model(spec, str(tmp_path_factory.mktemp("m") / "q4k.gguf"), seed=3)
+
+
+def test_f64_reference_matches_transformers(tiny_f32, tiny_q4k):
+    tokens = np.random.default_rng(2).integers(0, 4096, 9).astype(np.int32)
+    for path in (tiny_f32, tiny_q4k):
+        toks = tokens % (1000 if path == tiny_q4k else 4096)
+        ours = O.reference_f64(path, toks)
+        hf = _hf_logits(path, toks)
+        # HF builds its rope frequencies in float32 before the model is cast
+        # to float64, so angles carry ~1e-7 relative error; any structural
+        # slip (an index, a sign, a transposed operand) moves logits by O(1).
+        assert np.max(np.abs(ours - hf)) <= 2e-6 * (1 + np.abs(hf).max())
+
+
+def test_model_f32_matches_transformers_within_1e_4(tiny_f32):
+    # test_llama.cpp:758-764: 1e-4 * (1 + |want|); f32 KV, prompt then decode steps
+    tokens = np.random.default_rng(2).integers(0, 4096, 12).astype(np.int32)
+    m = O.Model(tiny_f32, 64, kv_f16=False)
+    got = m.forward(tokens[:9])
+    want = _hf_logits(tiny_f32, tokens[:9])
+    assert np.all(np.abs(got - want) <= 1e-4 * (1 + np.abs(want)))
+    for i in range(9, 12):
+        got = m.forward(tokens[i:i + 1])
+        want = _hf_logits(tiny_f32, tokens[:i + 1])
+        assert np.all(np.abs(got - want) <= 1e-4 * (1 + np.abs(want)))
+    assert m.position == 12
+
+
+def test_model_int8_path_tracks_the_double_reference(tiny_q4k):
+    # test_llama.cpp:1281-1312: quantized activations stay within a few % of
+    # the largest logit, and token-by-token equals the prompt at once closely.
+    tokens = np.random.default_rng(4).integers(0, 1000, 16).astype(np.int32)
+    want = O.reference_f64(tiny_q4k, tokens)
+    m = O.Model(tiny_q4k, 32, kv_f16=True)
+    got = m.forward(tokens)
+    top = np.abs(want).max()
+    assert np.max(np.abs(got - want)) <= 0.04 * top
+    m2 = O.Model(tiny_q4k, 32, kv_f16=True)
+    for t in tokens:
+        step = m2.forward(np.array([t]))
+    assert np.max(np.abs(step - got)) <= 1e-3 * np.abs(got).max()
+    with pytest.raises(RuntimeError, match="exceed the context length"):
+        m2.forward(np.zeros(17, np.int32))
+    with pytest.raises(RuntimeError, match="rewind"):
+        m2.rewind(17)
+    assert m2.rewind(3) == 3

@@ -1,0 +1,188 @@
+#!/usr/bin/env python3
+"""Batch-1 decode benchmark of vkml-mi355x on one MI355X (BASELINE.json's
+metric on its config 5): a Mistral-7B-shaped model (32 layers, hidden 4096,
+32/8 heads, head_dim 128, FFN 14336, vocab 32768, q4_K weights and a q6_K
+output matrix, seeded synthetic values), its f16 KV cache prefilled with
+4096 random-token positions, then greedy decoding. A step is one decode
+token; the timed steps replay the captured decode graph back to back with
+the weights and cache resident in HBM, and the host reads the tokens once
+at the end.
+
+Prints one JSON line: tokens/s, the whole step's algorithmic HBM rate (GGUF
+bytes of every weight plus the KV rows read) against 8 TB/s, a roofline
+entry for the dominant kernel from a HIP-event profile of extra steps, and
+the CPU oracle's decode rate on the host cores as a reported baseline.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "vkml-framework_amd", "python"))
+
+import numpy as np  # noqa: E402
+
+PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
+PROMPT = 4096
+
+# GGUF-native bytes per weight (q4_K 144 B / 256, q6_K 210 B / 256).
+Q4K, Q6K = 144 / 256, 210 / 256
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(spec):
+    """Per-token bytes: every weight once (GGUF-native sizes), the embedding
+    row, and per-position KV bytes read by attention."""
+    d, ff, L = spec.hidden, spec.ffn, spec.n_layers
+    qd, kvd = spec.heads * spec.head_dim, spec.kv_heads * spec.head_dim
+    per_layer = {"qkv": (qd + 2 * kvd) * d * Q4K, "o": d * qd * Q4K, "gate_up": 2 * ff * d * Q4K, "down": d * ff * Q4K}
+    weights = L * sum(per_layer.values()) + spec.vocab * d * Q6K + d * Q4K
+    kv_per_position = L * 2 * kvd * 2  # k and v rows, f16
+    return weights, kv_per_position, per_layer
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=PROMPT)
+    ap.add_argument("--profile-steps", type=int, default=16)
+    ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens the CPU oracle is timed on (0: skip)")
+    ap.add_argument("--layers", type=int, default=0, help="override the layer count (for quick local checks only)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (every GPU box here has one). "
+              "A second GPU would hold a replica (independent sequences) or a tensor-parallel shard; see DESIGN.md.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from vkml_amd import synth
+    from vkml_amd import llama as L
+
+    spec = synth.CONFIGS["cfg5"]
+    if args.layers:
+        spec = synth.ModelSpec(spec.name, args.layers, spec.hidden, spec.heads, spec.kv_heads, spec.head_dim, spec.ffn,
+                               spec.vocab, spec.theta, max_positions=spec.max_positions)
+    context = args.prompt + max(args.steps, args.profile_steps, args.warmup) + 1
+    path = os.path.join(synth.scratch_dir(), f"vkml_bench_cfg5_{os.getpid()}.gguf")
+    t0 = time.time()
+    synth.write_model(spec, path, seed=6)
+    log(f"model written in {time.time() - t0:.1f} s ({os.path.getsize(path) / 1e9:.2f} GB)")
+    try:
+        t0 = time.time()
+        model = L.Llama(path, context, kv_f16=True)
+        log(f"loaded in {time.time() - t0:.1f} s; kv cache {model.kv_cache_bytes / 1e6:.0f} MB")
+        prompt = np.random.default_rng(6).integers(0, spec.vocab, args.prompt).astype(np.int32)
+        t0 = time.time()
+        logits = model.forward(prompt)
+        log(f"prefill {args.prompt} tokens in {time.time() - t0:.1f} s")
+        first = int(np.argmax(logits))
+
+        # Warm-up, then rewind so the timed steps see positions 4096.. as configured.
+        if args.warmup:
+            model.generate_greedy(first, args.warmup)
+            model.rewind(args.prompt)
+        L.synchronize()
+        t0 = time.perf_counter()
+        tokens = model.generate_greedy(first, args.steps)  # returns after the device is done
+        elapsed = time.perf_counter() - t0
+        ms_per_step = elapsed * 1e3 / args.steps
+        tok_s = args.steps / elapsed
+        weights, kv_pos, per_layer = algorithmic_bytes(spec)
+        positions = np.arange(args.prompt + 1, args.prompt + args.steps + 1)
+        step_bytes = weights + kv_pos * positions.mean()
+        hbm = step_bytes / (ms_per_step * 1e-3) / 1e9
+        log(f"decode {args.steps} tokens: {ms_per_step:.3f} ms/token, {tok_s:.1f} tokens/s, {hbm:.0f} GB/s algorithmic")
+
+        # Per-kernel HIP-event profile of extra steps (eager launches on the same stream).
+        model.rewind(args.prompt)
+        L.set_profiling(True)
+        L.reset_profile()
+        model.generate_greedy(first, args.profile_steps)
+        L.synchronize()
+        prof = L.profile()
+        L.set_profiling(False)
+        n_layers = spec.n_layers
+        kv_mean = args.prompt + (args.profile_steps + 1) / 2
+        launch_bytes = {
+            "gemv_dot:qkv": per_layer["qkv"], "gemv_dot_add:o": per_layer["o"], "gemv_dot_swiglu:gate_up": per_layer["gate_up"],
+            "gemv_dot_add:down": per_layer["down"], "gemv_dot:lm_head": spec.vocab * spec.hidden * Q6K,
+            "attend:attention": kv_pos / n_layers * kv_mean,
+        }
+        rows = []
+        for name, calls, ms in prof:
+            avg_us = ms * 1e3 / max(calls, 1)
+            b = launch_bytes.get(name)
+            rows.append({"kernel": name, "calls": calls, "avg_us": round(avg_us, 3),
+                         "gb_s": round(b / (avg_us * 1e-6) / 1e9, 1) if b else None})
+        for r in sorted(rows, key=lambda r: -r["calls"] * r["avg_us"])[:14]:
+            log(f"  {r['kernel']:<28} calls {r['calls']:>6}  avg {r['avg_us']:9.2f} us  {r['gb_s'] or '':>8} GB/s")
+        dominant = max((r for r in rows if r["kernel"] in launch_bytes), key=lambda r: r["calls"] * r["avg_us"])
+        dom_bytes = launch_bytes[dominant["kernel"]]
+        achieved = dom_bytes / (dominant["avg_us"] * 1e-6) / 1e9
+        busy_ms = sum(ms for _, _, ms in prof) / args.profile_steps
+
+        cpu = None
+        if args.cpu_tokens > 0:
+            sys.path.insert(0, os.path.join(ROOT, "oracle"))
+            import oracle as O
+            threads = min(16, os.cpu_count() or 1)
+            O.set_threads(threads)
+            t0 = time.time()
+            ref = O.Model(path, context, kv_f16=True)
+            log(f"oracle loaded in {time.time() - t0:.1f} s")
+            ref.set_position(args.prompt)
+            t0 = time.perf_counter()
+            for i in range(args.cpu_tokens):
+                ref.forward(np.array([first], np.int32))
+            cpu_s = time.perf_counter() - t0
+            cpu = {"value": round(args.cpu_tokens / cpu_s, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+                   "sample": f"{args.cpu_tokens} decode tokens of the same model at positions {args.prompt}.. "
+                             f"(CPU oracle, int8 path, {threads} threads, {cpu_s:.1f} s)"}
+            ref.close()
+            log(f"cpu oracle: {cpu['value']} tokens/s on {threads} threads")
+
+        result = {
+            "metric": "batch-1 decode tokens/s + achieved HBM GB/s (% of 8 TB/s), 1xMI355X",
+            "value": round(tok_s, 2),
+            "unit": "tokens/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "int8",
+            "data": "synthetic",
+            "config": {"workload": "cfg5: Mistral-7B-shaped decoder, q4_K weights + q6_K output (GGUF), f16 KV prefilled "
+                                   f"with {args.prompt} random-token positions, {args.steps} greedy decode steps, batch 1",
+                       "layers": spec.n_layers, "hidden": spec.hidden, "heads": spec.heads, "kv_heads": spec.kv_heads,
+                       "head_dim": spec.head_dim, "ffn": spec.ffn, "vocab": spec.vocab, "seq_len": args.prompt},
+            "hbm_gb_s": round(hbm, 1),
+            "hbm_frac": round(hbm / PEAK_HBM, 4),
+            "bytes_per_step": round(step_bytes),
+            "gpu_busy_ms_per_step": round(busy_ms, 4),
+            "roofline": {"bound": "hbm", "kernel": dominant["kernel"], "achieved": round(achieved, 1), "peak": PEAK_HBM,
+                         "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                         "bytes_per_launch": round(dom_bytes), "avg_launch_us": dominant["avg_us"]},
+            "cpu_baseline": cpu,
+            "tokens_head": [int(t) for t in tokens[:8]],
+        }
+        print(json.dumps(result), flush=True)
+        model.close()
+    finally:
+        try:
+            os.remove(path)
+        except OSError:
+            pass
+
+
+if __name__ == "__main__":
+    main()

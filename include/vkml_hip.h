@@ -1,0 +1,389 @@
+/*
+ * vkml_hip.h -- the C ABI over HIP that replaces vkml's Vulkan HAL.
+ *
+ * The reference's ops reach the GPU through src/hal (Device, Buffer,
+ * ComputePipeline, Stream) and src/core/runtime.hpp. This library replaces
+ * that seam with plain C entry points on one HIP device and one in-order HIP
+ * stream: lifecycle and device info, device and pinned host memory, stream
+ * copies, a submit/wait fence timeline, per-kernel profiling, HIP graphs for
+ * the decode step, and one launch entry per kernel family whose parameter
+ * struct mirrors the reference's push constants. The C++ API (vkml::Context,
+ * vkml::Tensor, the ops, vkml::Llama) is built on these calls only.
+ *
+ * Conventions: every function returns VKML_OK (0) or an error code; the
+ * message of the last error on the calling thread is vkml_last_error().
+ * Pointers named d_* are device memory from vkml_malloc (or any HIP device
+ * allocation); all launches are asynchronous on the library's stream, in
+ * order. One vkml_init per process (the reference allows one live Context,
+ * src/hal/device.cpp:104-108). Sizes are counts of elements unless they say
+ * bytes. Not thread-safe: one thread drives the library, as one drives a
+ * vkml::Context (src/core/runtime.hpp:24).
+ */
+#ifndef VKML_HIP_H
+#define VKML_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VKML_ABI_VERSION 1
+
+enum vkml_status {
+    VKML_OK = 0,
+    VKML_ERROR_INVALID_ARGUMENT = 1,
+    VKML_ERROR_NO_DEVICE = 2,
+    VKML_ERROR_DEVICE = 3,
+    VKML_ERROR_STATE = 4,
+    VKML_ERROR_UNSUPPORTED = 5,
+    VKML_ERROR_OUT_OF_MEMORY = 6
+};
+
+/* Element and weight formats. 0-5 are the TYPE_ constants of the reference's
+ * shaders/include/halves.glsl:5-24; VKML_Q4_K is llama.cpp's q4_K kept in its
+ * own 256-value super-blocks (values: the 128 code bytes of each super-block;
+ * scales: its 16-byte header, f16 d, f16 dmin and 12 bytes of 6-bit scales
+ * and mins), decoded in-kernel to the Q4_1 values the reference repacks it
+ * into (src/io/gguf.cpp:596-627). */
+enum vkml_type {
+    VKML_F32 = 0, VKML_F16 = 1, VKML_BF16 = 2,
+    VKML_Q8_0 = 3, VKML_Q4_0 = 4, VKML_Q4_1 = 5, VKML_Q4_K = 6,
+    VKML_I32 = 7
+};
+
+/* ---------------------------------------------------------------------- */
+/* Device lifecycle: replaces hal::Device (src/hal/device.cpp:103-118,    */
+/* 234-286) and DeviceInfo (include/vkml/context.hpp:28-70).              */
+/* ---------------------------------------------------------------------- */
+
+typedef struct vkml_device_info {
+    char name[256];          /* marketing name, e.g. "AMD Instinct MI355X" */
+    char arch[64];           /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    char driver[64];         /* HIP runtime version */
+    uint64_t global_memory_bytes;
+    uint32_t compute_units;
+    uint32_t wave_size;
+    uint32_t max_threads_per_block;
+    uint32_t max_block_dims[3];
+    uint32_t max_grid_dims[3];
+    uint32_t lds_bytes_per_block;
+    uint32_t l2_bytes;
+    uint32_t clock_khz;
+    uint32_t memory_clock_khz;
+    uint32_t memory_bus_bits;
+    int32_t integer_dot_product; /* v_dot4_i32_i8 on gfx950: always 1 */
+    int32_t timestamps;          /* hipEvent timing available: always 1 */
+    double timestamp_period_ns;
+} vkml_device_info;
+
+const char* vkml_last_error(void);
+int vkml_abi_version(void);
+/* device_name: case-insensitive substring of the name or arch; NULL or "" means
+ * the VKML_DEVICE environment variable, then device 0 (context.cpp:24-26). */
+int vkml_init(const char* device_name);
+int vkml_shutdown(void);
+int vkml_is_initialized(void);
+int vkml_get_device_info(vkml_device_info* out);
+
+/* ---------------------------------------------------------------------- */
+/* Memory and copies: replaces hal::Buffer (src/hal/buffer.cpp:26-54) and */
+/* Stream::copy; copies are ordered on the stream.                        */
+/* ---------------------------------------------------------------------- */
+
+int vkml_malloc(uint64_t bytes, void** d_out);
+int vkml_free(void* d_ptr);
+int vkml_host_malloc(uint64_t bytes, void** h_out); /* pinned */
+int vkml_host_free(void* h_ptr);
+int vkml_memcpy_h2d(void* d_dst, const void* h_src, uint64_t bytes);
+int vkml_memcpy_d2h(void* h_dst, const void* d_src, uint64_t bytes);
+int vkml_memcpy_d2d(void* d_dst, const void* d_src, uint64_t bytes);
+/* words 32-bit words of value at d_dst, by a kernel (runtime.cpp:97-103). */
+int vkml_fill_u32(void* d_dst, uint32_t value, uint64_t words);
+
+/* ---------------------------------------------------------------------- */
+/* Timeline: Stream::submit/wait (src/hal/stream.cpp:156-206). A fence is */
+/* a monotonically increasing value; work submitted before it is done     */
+/* once vkml_completed reports it.                                        */
+/* ---------------------------------------------------------------------- */
+
+int vkml_submit(uint64_t* fence_out);
+int vkml_wait(uint64_t fence);
+int vkml_completed(uint64_t* fence_out);
+int vkml_synchronize(void);
+
+/* ---------------------------------------------------------------------- */
+/* Profiling: Context::set_profiling/profile/reset_profile               */
+/* (include/vkml/context.hpp:115-126, src/hal/stream.cpp:258-306). With   */
+/* profiling on, each launch is bracketed by HIP events and totalled per  */
+/* kernel label when waited on; graphs are not replayed while profiling.  */
+/* ---------------------------------------------------------------------- */
+
+typedef struct vkml_kernel_time {
+    char name[48];
+    uint64_t calls;
+    double milliseconds;
+} vkml_kernel_time;
+
+int vkml_set_profiling(int enabled);
+int vkml_get_profiling(void);
+/* While tag is non-empty, profiled launches are labelled "kernel:tag" (the
+ * model tags its projections: "gemv_dot:qkv", "gemv_dot_add:down", ...). */
+int vkml_set_profile_tag(const char* tag);
+/* Writes up to capacity entries, slowest first; *count gets the total. */
+int vkml_profile(vkml_kernel_time* out, uint32_t capacity, uint32_t* count);
+int vkml_reset_profile(void);
+
+/* ---------------------------------------------------------------------- */
+/* HIP graphs: capture launches on the stream into a replayable graph     */
+/* (the decode step). No reference counterpart: vkml records command     */
+/* buffers per step (src/hal/stream.cpp:86-141).                          */
+/* ---------------------------------------------------------------------- */
+
+int vkml_graph_begin(void);
+int vkml_graph_end(uint64_t* graph_out);
+int vkml_graph_launch(uint64_t graph);
+int vkml_graph_destroy(uint64_t graph);
+
+/* ---------------------------------------------------------------------- */
+/* Kernels. Each struct mirrors the push constants (and specialization     */
+/* constants) of the reference shader it replaces.                        */
+/* ---------------------------------------------------------------------- */
+
+/* shaders/quantize.comp, src/ops/quantize.cpp:21-63. x: [blocks * 32] of
+ * src_type (F32/F16/BF16); quant Q8_0/Q4_0/Q4_1; scale_type F32 or F16.
+ * values: 8 (Q8_0) or 4 words per block; scales: one per block, or
+ * (scale, offset) pairs for Q4_1. */
+typedef struct vkml_quantize_params {
+    uint32_t blocks;
+    uint32_t src_type;
+    uint32_t quant;
+    uint32_t scale_type;
+} vkml_quantize_params;
+int vkml_quantize(const vkml_quantize_params* p, const void* d_x, void* d_values, void* d_scales);
+
+/* shaders/dequantize.comp, src/ops/quantize.cpp:79-94: count values of a
+ * [rows, cols] matrix (cols given for Q4_K's super-block rows). */
+typedef struct vkml_dequantize_params {
+    uint32_t count;
+    uint32_t quant;
+    uint32_t scale_type;
+    uint32_t cols;
+} vkml_dequantize_params;
+int vkml_dequantize(const vkml_dequantize_params* p, const void* d_values, const void* d_scales,
+                    float* d_out);
+
+/* shaders/gemv_dot.comp, src/ops/matmul.cpp:225-245: c[m, n] = a_q[m] . b[n]
+ * for m <= 8 rows of Q8_0 activations (f32 scales) and weights b [n, k] of
+ * b_type Q8_0/Q4_0/Q4_1/Q4_K (scales F16, or F32 for Q8_0/Q4_0/Q4_1).
+ * Argument order is the reference's buffer order (matmul.cpp:234-237). */
+typedef struct vkml_gemv_dot_params {
+    uint32_t m, n, k;
+    uint32_t b_type;
+    uint32_t scale_type;
+} vkml_gemv_dot_params;
+int vkml_gemv_dot(const vkml_gemv_dot_params* p, const void* d_a_values, const void* d_b_values,
+                  float* d_out, const void* d_b_scales, const float* d_a_scales);
+/* As vkml_gemv_dot for m = 1, with the residual add that follows the o and
+ * down projections (llama.cpp:374,386) done in the epilogue:
+ * d_out[n] = d_residual[n] + a_q . b[n] (d_out may equal d_residual). */
+int vkml_gemv_dot_add(const vkml_gemv_dot_params* p, const void* d_a_values,
+                      const void* d_b_values, float* d_out, const void* d_b_scales,
+                      const float* d_a_scales, const float* d_residual);
+/* The SwiGLU MLP's first half for m = 1 (llama.cpp:380-382): with g = a_q .
+ * gate[n] and u = a_q . up[n], d_h[n] = silu(g) * u, silu(v) = v / (1 +
+ * exp(-v)) (shaders/unary.comp:21-24). gate and up share b_type/scale_type. */
+int vkml_gemv_dot_swiglu(const vkml_gemv_dot_params* p, const void* d_a_values,
+                         const float* d_a_scales, const void* d_gate_values,
+                         const void* d_gate_scales, const void* d_up_values,
+                         const void* d_up_scales, float* d_h);
+
+/* shaders/gemv.comp, src/ops/matmul.cpp:88-120: the float path, c[m, n] =
+ * a[m] . b[n] with f32 a (m <= 8) and b [n, k] of b_type F32/F16/BF16 or
+ * Q8_0/Q4_0/Q4_1/Q4_K decoded in registers (ContextOptions::
+ * integer_dot_product off, and f32 models). */
+typedef struct vkml_gemv_params {
+    uint32_t m, n, k;
+    uint32_t b_type;
+    uint32_t scale_type;
+} vkml_gemv_params;
+int vkml_gemv(const vkml_gemv_params* p, const float* d_a, const void* d_b, float* d_out,
+              const void* d_b_scales);
+
+/* shaders/matmul.comp (src/ops/matmul.cpp:44-120): c = a . b or a . b^T for
+ * f32 a [batches * b_group, m, k] and b [batches, k, n] (or [n, k]) of b_type
+ * F32/F16/BF16; b_stride elements between b's batches (0: shared b). */
+typedef struct vkml_matmul_params {
+    uint32_t m, n, k;
+    uint32_t b_stride;
+    uint32_t b_group;
+    uint32_t batches;
+    uint32_t b_transposed;
+    uint32_t b_type;
+} vkml_matmul_params;
+int vkml_matmul(const vkml_matmul_params* p, const float* d_a, const void* d_b, float* d_out);
+
+/* shaders/rms_norm.comp, src/ops/norms.cpp:230-253. */
+typedef struct vkml_rms_norm_params {
+    uint32_t rows, cols;
+    float eps;
+} vkml_rms_norm_params;
+int vkml_rms_norm(const vkml_rms_norm_params* p, const float* d_x, const float* d_w, float* d_out);
+/* rms_norm then quantize_q8 with f32 scales (the SharedInput of the next
+ * projections, matmul.cpp:229): d_out (optional, may be NULL) gets the f32
+ * normalized rows, d_values/d_a_scales their Q8_0 form. cols % 32 == 0. */
+int vkml_rms_norm_quantize(const vkml_rms_norm_params* p, const float* d_x, const float* d_w,
+                           float* d_out, void* d_values, float* d_scales);
+
+/* shaders/softmax.comp, src/ops/norms.cpp:176-211: rows of scale * x, with
+ * an optional causal mask (query row % q_len at key position offset + that)
+ * and window; -inf entries become 0. */
+typedef struct vkml_softmax_params {
+    uint32_t rows, cols;
+    float scale;
+    uint32_t causal;
+    uint32_t q_len;
+    uint32_t offset;
+    uint32_t window;
+    float softcap;
+} vkml_softmax_params;
+int vkml_softmax(const vkml_softmax_params* p, const float* d_x, float* d_out);
+
+/* shaders/argmax.comp, src/ops/norms.cpp:213-228: first index of each row's
+ * largest non-NaN entry; 0 if all are NaN. */
+int vkml_argmax(uint32_t rows, uint32_t cols, const float* d_x, int32_t* d_out);
+
+/* shaders/rope.comp, src/ops/rope.cpp:20-28,88-129. style 0 interleaved
+ * pairs (2i, 2i+1), 1 rotate-half (i, i + dim/2). */
+typedef struct vkml_rope_params {
+    uint32_t pairs;
+    uint32_t half_dim;
+    uint32_t dim;
+    uint32_t heads;
+    uint32_t seq;
+    uint32_t start_pos;
+    uint32_t copies;
+    uint32_t style;
+} vkml_rope_params;
+int vkml_rope(const vkml_rope_params* p, const float* d_x, const float* d_table, float* d_out);
+
+/* shaders/cast.comp, src/ops/cast.cpp:24-46: f32 -> f16/bf16 rounding to
+ * nearest even on the bits (no flush), f16/bf16 -> f32 exact, f32 copy. */
+int vkml_cast(uint32_t count, uint32_t src_type, uint32_t dst_type, const void* d_x, void* d_out);
+
+/* shaders/write_rows.comp, src/ops/attention.cpp:86-122 (CopyRowsParams):
+ * 32-bit words. */
+typedef struct vkml_copy_rows_params {
+    uint32_t count;
+    uint32_t block;
+    uint32_t src_stride;
+    uint32_t src_start;
+    uint32_t dst_stride;
+    uint32_t dst_start;
+} vkml_copy_rows_params;
+int vkml_copy_rows(const vkml_copy_rows_params* p, const void* d_src, void* d_dst);
+
+/* shaders/permute.comp, src/ops/permute.cpp:34-81: out dimension i is input
+ * dimension dims[i], up to 6 dimensions of 32-bit elements. */
+typedef struct vkml_permute_params {
+    uint32_t rank;
+    uint32_t count;
+    uint32_t in_shape[6];
+    uint32_t dims[6];
+} vkml_permute_params;
+int vkml_permute(const vkml_permute_params* p, const void* d_x, void* d_out);
+
+/* shaders/binary.comp and unary.comp (src/ops/elementwise.cpp:23-87).
+ * binary op: 0 add, 1 sub, 2 mul, 3 div, b repeating every b_count;
+ * unary op: 0 silu, 1 gelu (tanh), 2 softcap(param). */
+int vkml_binary(uint32_t op, uint32_t count, uint32_t b_count, const float* d_a, const float* d_b,
+                float* d_out);
+int vkml_unary(uint32_t op, uint32_t count, float param, const float* d_x, float* d_out);
+
+/* shaders/embedding.comp and embedding_quantized.comp (src/ops/
+ * embedding.cpp:19-91): rows ids of a [vocab, dim] table of table_type
+ * (F32/F16/BF16/Q8_0/Q4_0/Q4_1/Q4_K); out-of-range ids give zero rows. */
+typedef struct vkml_embedding_params {
+    uint32_t count; /* ids * dim */
+    uint32_t dim;
+    uint32_t vocab;
+    uint32_t table_type;
+    uint32_t scale_type;
+} vkml_embedding_params;
+int vkml_embedding(const vkml_embedding_params* p, const void* d_values, const void* d_scales,
+                   const int32_t* d_ids, float* d_out);
+
+/* ---------------------------------------------------------------------- */
+/* Decode attention (shaders/attend.comp + attend_merge.comp,             */
+/* src/ops/attention.cpp:22-84), GQA-aware: workgroup (s, g) reads the    */
+/* keys of split s of KV head g once for all of its heads / kv_heads query */
+/* heads. Keys kv_start..kv_len of caches [kv_heads, capacity, head_dim]  */
+/* (F32 or F16), position p at row p % capacity. With d_state non-NULL,   */
+/* kv_len is d_state->position + 1 (the decode graph).                    */
+/* partial: [kv_heads, splits, group, head_dim] f32; stats: [kv_heads,    */
+/* splits, group, 2] (max score, sum of exp).                             */
+/* ---------------------------------------------------------------------- */
+
+typedef struct vkml_decode_state {
+    int32_t token;    /* input token of the next step */
+    int32_t position; /* its position; the KV rows written by the step */
+    int32_t steps;    /* tokens appended to the log so far */
+    int32_t reserved;
+} vkml_decode_state;
+
+typedef struct vkml_attend_params {
+    uint32_t kv_start;
+    uint32_t kv_len;
+    uint32_t capacity;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t kv_type;
+    uint32_t splits;
+    float scale;
+    float softcap;
+} vkml_attend_params;
+int vkml_attend(const vkml_attend_params* p, const float* d_q, const void* d_k_cache,
+                const void* d_v_cache, float* d_partial, float* d_stats,
+                const vkml_decode_state* d_state);
+/* Merges the splits into out [heads, head_dim] f32 and, when d_values is
+ * non-NULL, its Q8_0 form with f32 scales (the o projection's input). */
+int vkml_attend_merge(const vkml_attend_params* p, const float* d_partial, const float* d_stats,
+                      float* d_out, void* d_values, float* d_scales);
+
+/* ---------------------------------------------------------------------- */
+/* Fused decode-step kernels (no single reference counterpart: each       */
+/* replaces a sequence of the reference's dispatches, cited).             */
+/* ---------------------------------------------------------------------- */
+
+/* heads_first + rope + cast + write_rows for one token (llama.cpp:320-355):
+ * qkv = [q (heads*hd) | k (kv_heads*hd) | v (kv_heads*hd)] f32; q is rotated
+ * into d_q; k rotated and v are rounded to the cache type and written at row
+ * position of every KV head. Position from d_state if non-NULL. */
+typedef struct vkml_rope_kv_params {
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t capacity;
+    uint32_t position;
+    uint32_t style;
+    uint32_t kv_type;
+    uint32_t rotate; /* 0: no rope in this layer */
+} vkml_rope_kv_params;
+int vkml_rope_kv_append(const vkml_rope_kv_params* p, const float* d_qkv, const float* d_table,
+                        float* d_q, void* d_k_cache, void* d_v_cache,
+                        const vkml_decode_state* d_state);
+
+/* Decode-state helpers for the replayable step: set the state, embed its
+ * token, and finish the step (argmax into the state and a token log, then
+ * position += 1; with d_logits NULL only the position advances). */
+int vkml_state_set(vkml_decode_state* d_state, int32_t token, int32_t position, int32_t steps);
+int vkml_embedding_state(const vkml_embedding_params* p, const void* d_values,
+                         const void* d_scales, const vkml_decode_state* d_state, float* d_out);
+int vkml_step_finish(uint32_t vocab, const float* d_logits, vkml_decode_state* d_state,
+                     int32_t* d_token_log, uint32_t log_capacity);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,88 @@
+/*
+ * vkml_llama.h -- C entry points over vkml::Llama (libvkml.so), for callers
+ * that bind a C ABI (ctypes, cgo, JNI, N-API) rather than C++.
+ *
+ * Each function stands for a member of the reference's public C++ API
+ * (include/vkml/llama.hpp:143-223 and context.hpp:104-134 there), with the
+ * same meaning and error behaviour: a non-zero status and a message from
+ * vkml_llama_last_error() where the C++ API throws vkml::Error (the
+ * messages are the reference's, e.g. "Llama::forward: ... exceed the context
+ * length of ..." and "Llama::rewind: cannot rewind to position ...").
+ *
+ * One process holds one device context (created by the first
+ * vkml_llama_load, destroyed by vkml_llama_shutdown after the last model is
+ * freed). Not thread-safe: serialize calls, as the reference's server does
+ * (apps/server.hpp:257 there).
+ */
+#ifndef VKML_LLAMA_H
+#define VKML_LLAMA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct vkml_llama vkml_llama;
+
+/* LlamaOptions (llama.hpp:118-139) plus ContextOptions::integer_dot_product
+ * (context.hpp:80-97) and this build's decode settings. */
+typedef struct vkml_llama_options {
+    int32_t kv_cache_f16;       /* 0: f32 KV cache (the reference's default), 1: f16 */
+    int32_t quantize;           /* -1 none; 0 q8_0, 1 q4_0, 2 q4_1: float weights on load */
+    int32_t integer_dot;        /* 1: int8 activations for quantized weights (default) */
+    int32_t use_graphs;         /* 1: replay the decode step as a HIP graph (default) */
+    int32_t attention_splits;   /* 0: from the CU count */
+    const char* device_name;    /* NULL or "": VKML_DEVICE, then device 0 */
+} vkml_llama_options;
+
+/* LlamaConfig (llama.hpp:29-116), the fields of the llama architecture. */
+typedef struct vkml_llama_config {
+    int64_t vocab_size, hidden_size, intermediate_size, num_layers, num_heads, num_kv_heads, head_dim, max_positions;
+    float rms_norm_eps, rope_theta;
+    int32_t tie_word_embeddings;
+    int32_t rope_interleaved;
+} vkml_llama_config;
+
+const char* vkml_llama_last_error(void);
+void vkml_llama_default_options(vkml_llama_options* out);
+
+/* Llama::load(Context&, path, context_length, options) (llama.hpp:149-150). */
+int vkml_llama_load(const char* gguf_path, int64_t context_length, const vkml_llama_options* options, vkml_llama** out);
+void vkml_llama_free(vkml_llama* model);
+/* Destroys the process's device context; fails while models are alive. */
+int vkml_llama_shutdown(void);
+
+/* Llama::config, context_length, position, kv_cache_bytes (llama.hpp:155-180). */
+int vkml_llama_get_config(const vkml_llama* model, vkml_llama_config* out);
+int64_t vkml_llama_context_length(const vkml_llama* model);
+int64_t vkml_llama_position(const vkml_llama* model);
+int64_t vkml_llama_kv_cache_bytes(const vkml_llama* model);
+
+/* Llama::forward: the last token's logits into logits[vocab_size]. */
+int vkml_llama_forward(vkml_llama* model, const int32_t* tokens, int64_t count, float* logits);
+/* Llama::forward_all: every token's logits into logits[count * vocab_size]. */
+int vkml_llama_forward_all(vkml_llama* model, const int32_t* tokens, int64_t count, float* logits);
+/* vkml::argmax(model.forward({&token, 1})) for count steps, on the device:
+ * tokens_out[i] is step i's argmax (the decode loop of apps/vkml_run.cpp:
+ * 282-298 there), with no host round trip between steps. */
+int vkml_llama_generate_greedy(vkml_llama* model, int32_t first, int64_t count, int32_t* tokens_out);
+/* Llama::reset and rewind (llama.hpp:171-177). *out gets the position. */
+int vkml_llama_reset(vkml_llama* model);
+int vkml_llama_rewind(vkml_llama* model, int64_t position, int64_t* out);
+/* Layer l's KV caches [kv_heads, context_length, head_dim] copied to the
+ * host (element size 2 for an f16 cache, 4 for f32). */
+int vkml_llama_read_kv_cache(const vkml_llama* model, int64_t layer, void* k_out, void* v_out, uint64_t bytes);
+
+/* Context::set_profiling / profile / reset_profile (context.hpp:120-126):
+ * up to capacity labels, slowest first; *count gets how many exist. */
+int vkml_llama_set_profiling(int32_t enabled);
+int vkml_llama_profile(char* names, uint32_t name_stride, uint64_t* calls, double* milliseconds, uint32_t capacity, uint32_t* count);
+int vkml_llama_reset_profile(void);
+/* Context::synchronize: waits for queued work. */
+int vkml_llama_synchronize(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

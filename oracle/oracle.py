@@ -73,6 +73,7 @@ def _declare(L):
         "orc_model_free": (None, [vp]),
         "orc_model_forward": (i32, [vp, vp, i64, vp]),
         "orc_model_position": (i64, [vp]),
+        "orc_model_set_position": (i32, [vp, i64]),
         "orc_model_rewind": (i64, [vp, i64]),
         "orc_model_reset": (None, [vp]),
         "orc_model_vocab": (i64, [vp]),
@@ -272,6 +273,10 @@ class Model:
     @property
     def position(self) -> int:
         return int(lib().orc_model_position(self._h))
+
+    def set_position(self, position: int) -> None:
+        if lib().orc_model_set_position(self._h, position) != 0:
+            raise RuntimeError("position %d outside the context" % position)
 
     def rewind(self, position: int) -> int:
         r = lib().orc_model_rewind(self._h, position)

@@ -308,6 +308,13 @@ orc_model* orc_model_load(const char* path, int64_t context_length, int kv_f16, 
 }
 
 int64_t orc_model_position(const orc_model* m) { return m->position; }
+/* Moves the sequence to position without computing it: for timing a decode
+ * step at a long context, whatever the (zero) cache rows hold. */
+int orc_model_set_position(orc_model* m, int64_t position) {
+    if (position < 0 || position >= m->context) return -1;
+    m->position = position;
+    return 0;
+}
 int64_t orc_model_vocab(const orc_model* m) { return m->vocab; }
 void orc_model_reset(orc_model* m) { m->position = 0; }
 int64_t orc_model_rewind(orc_model* m, int64_t position) {

@@ -127,6 +127,7 @@ void orc_model_free(orc_model* m);
  * Returns 0, or -1 with orc_last_error set (llama.cpp:300-305 errors). */
 int orc_model_forward(orc_model* m, const int32_t* tokens, int64_t t, float* logits);
 int64_t orc_model_position(const orc_model* m);
+int orc_model_set_position(orc_model* m, int64_t position); /* timing samples only */
 int64_t orc_model_rewind(orc_model* m, int64_t position); /* -1 on error */
 void orc_model_reset(orc_model* m);
 int64_t orc_model_vocab(const orc_model* m);

@@ -1,0 +1,427 @@
+"""Kernel parity on the MI355X: each HIP kernel through the C ABI against the
+CPU oracle on the same seeded inputs. Integer and bit-level results (codes,
+scales, casts, copies, argmax, embeddings of quantized tables) must be
+identical; f32 results whose sums run in another order must sit inside the
+f32 dot-product error bound the reference's own tests use
+(tests/test_quantize.cpp:197-224 there: 2 k 2^-24 sum|a b|)."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from vkml_amd import hip as H
+from vkml_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+_live = []  # device buffers of the running test: freed only after it synchronizes
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    H.init()
+    yield
+    H.synchronize()
+
+
+@pytest.fixture(autouse=True)
+def keep_buffers():
+    yield
+    H.synchronize()
+    _live.clear()
+
+
+def dev(a):
+    buf = H.to_device(np.ascontiguousarray(a))
+    _live.append(buf)
+    return buf
+
+
+def p(buf):
+    return buf.p if buf is not None else None
+
+
+# ---------------------------------------------------------------- helpers
+
+def q4k_layout(blocks: np.ndarray, rows: int, cols: int):
+    """GGUF q4_K blocks [rows, cols/256, 144] -> (codes [rows, cols/2] u8, headers [rows, cols/256, 16] u8)."""
+    b = blocks.reshape(rows, cols // 256, 144)
+    return np.ascontiguousarray(b[:, :, 16:]).reshape(rows, cols // 2), np.ascontiguousarray(b[:, :, :16])
+
+
+def weights(fmt, rows, cols, seed, f16_scales=True):
+    """(device values, device scales, oracle quant, oracle words, oracle halves/scales, host arrays)."""
+    rng = np.random.default_rng(seed)
+    if fmt == H.Q4_K:
+        blocks = synth.q4_k_blocks(rng, rows * cols // 256)
+        codes, hdr = q4k_layout(blocks, rows, cols)
+        quant, words, halves = O.load_quantized(O.GGML_Q4_K, blocks.tobytes(), rows, cols)
+        return dev(codes), dev(hdr), quant, words, halves
+    quant = {H.Q8_0: O.Q8_0, H.Q4_0: O.Q4_0, H.Q4_1: O.Q4_1}[fmt]
+    w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+    words, scales = O.quantize(quant, w, f16_scales)
+    return dev(words), dev(scales), quant, words, scales
+
+
+def activation(k, seed, m=1):
+    a = np.random.default_rng(seed).standard_normal((m, k)).astype(np.float32)
+    words, scales = O.quantize(O.Q8_0, a, False)
+    return a, words, scales
+
+
+def dot_bound(aw, asc, m, k, quant, words, scales, n):
+    ad = O.dequantize(O.Q8_0, aw, asc, m, k).astype(np.float64)
+    wd = O.dequantize(quant, words, scales, n, k).astype(np.float64)
+    return ad @ wd.T, 3 * k * 2.0 ** -24 * (np.abs(ad) @ np.abs(wd).T) + 1e-30
+
+
+# ---------------------------------------------------------------- quantize
+
+@pytest.mark.parametrize("quant,hq", [(O.Q8_0, H.Q8_0), (O.Q4_0, H.Q4_0), (O.Q4_1, H.Q4_1)])
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("src", [H.F32, H.F16, H.BF16])
+def test_quantize_bit_exact(quant, hq, f16, src):
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((7, 96)) * 0.3).astype(np.float32)
+    x[0, :32] = 0.0  # an all-zero block
+    x[1, 5] = 40.0   # an outlier
+    x[2, 32:64] = 2.0 ** -20 * rng.standard_normal(32)  # tiny: subnormal f16 scales
+    if src == H.F16:
+        host = x.astype(np.float16)
+        x = host.astype(np.float32)
+        xin = host.view(np.uint16)
+    elif src == H.BF16:
+        bits = (x.view(np.uint32) >> 16).astype(np.uint16)
+        x = (bits.astype(np.uint32) << 16).view(np.float32)
+        xin = bits
+    else:
+        xin = x
+    want_w, want_s = O.quantize(quant, x, f16)
+    blocks = x.size // 32
+    dw, ds = H.empty(want_w.nbytes), H.empty(want_s.nbytes)
+    H.call("vkml_quantize", H.QuantizeParams(blocks, src, hq, H.F16 if f16 else H.F32), p(dev(xin)), p(dw), p(ds))
+    assert np.array_equal(dw.download(np.uint32, want_w.shape), want_w)
+    assert np.array_equal(ds.download(want_s.dtype, want_s.shape).view(np.uint8), want_s.view(np.uint8))
+
+
+@pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_0, H.Q4_1, H.Q4_K])
+def test_dequantize_bit_exact(fmt):
+    rows, cols = 6, 512
+    v, s, quant, words, scales = weights(fmt, rows, cols, 5)
+    want = O.dequantize(quant, words, scales, rows, cols)
+    out = H.empty(want.nbytes)
+    H.call("vkml_dequantize", H.DequantizeParams(rows * cols, fmt, H.F16, cols), p(v), p(s), p(out))
+    assert np.array_equal(out.download(np.float32, want.shape).view(np.uint32), want.view(np.uint32))
+
+
+def test_q4_k_subnormal_and_extreme_scales_bit_exact():
+    rng = np.random.default_rng(9)
+    blocks = synth.q4_k_blocks(rng, 64)
+    d = np.array([2.0 ** -24, 3 * 2.0 ** -24, 6.0e-5, 1.0, 65504.0 / 64, 0.0, 2.0 ** -14, 7.0e-6] * 8, np.float16)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:4] = d[::-1].copy().view(np.uint8).reshape(-1, 2)
+    rows, cols = 8, 2048
+    codes, hdr = q4k_layout(blocks, rows, cols)
+    quant, words, halves = O.load_quantized(O.GGML_Q4_K, blocks.tobytes(), rows, cols)
+    want = O.dequantize(quant, words, halves, rows, cols)
+    out = H.empty(want.nbytes)
+    H.call("vkml_dequantize", H.DequantizeParams(rows * cols, H.Q4_K, H.F16, cols), p(dev(codes)), p(dev(hdr)), p(out))
+    got = out.download(np.float32, want.shape)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- GEMV
+
+GEMV_SHAPES = [(256, 256), (37 * 16, 1024), (4096, 4096), (14336, 4096), (4096, 14336)]
+
+
+@pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_0, H.Q4_1, H.Q4_K])
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+def test_gemv_dot_matches_oracle_within_the_dot_bound(fmt, n, k):
+    v, s, quant, words, scales = weights(fmt, n, k, n + k)
+    a, aw, asc = activation(k, 3)
+    out = H.empty(n * 4)
+    H.call("vkml_gemv_dot", H.GemvDotParams(1, n, k, fmt, H.F16), p(dev(aw)), p(v), p(out), p(s), p(dev(asc)))
+    got = out.download(np.float32, (1, n))
+    want = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)
+    exact, bound = dot_bound(aw, asc, 1, k, quant, words, scales, n)
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.all(np.abs(got - want) <= 2 * bound)
+
+
+@pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_0, H.Q4_1])
+def test_gemv_dot_f32_scales_and_several_rows(fmt):
+    n, k, m = 300, 512, 3
+    v, s, quant, words, scales = weights(fmt, n, k, 21, f16_scales=False)
+    a, aw, asc = activation(k, 4, m)
+    out = H.empty(m * n * 4)
+    H.call("vkml_gemv_dot", H.GemvDotParams(m, n, k, fmt, H.F32), p(dev(aw)), p(v), p(out), p(s), p(dev(asc)))
+    got = out.download(np.float32, (m, n))
+    exact, bound = dot_bound(aw, asc, m, k, quant, words, scales, n)
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+@pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_K])
+def test_gemv_dot_add_and_swiglu(fmt):
+    n, k = 1024, 4096
+    v, s, quant, words, scales = weights(fmt, n, k, 31)
+    v2, s2, _, words2, scales2 = weights(fmt, n, k, 32)
+    a, aw, asc = activation(k, 5)
+    res = np.random.default_rng(6).standard_normal(n).astype(np.float32)
+    out = dev(res)
+    H.call("vkml_gemv_dot_add", H.GemvDotParams(1, n, k, fmt, H.F16), p(dev(aw)), p(v), p(out), p(s), p(dev(asc)), p(out))
+    got = out.download(np.float32, n)
+    exact, bound = dot_bound(aw, asc, 1, k, quant, words, scales, n)
+    assert np.all(np.abs(got - (res + exact[0])) <= bound[0] + 2.0 ** -23 * np.abs(res + exact[0]))
+    h = H.empty(n * 4)
+    H.call("vkml_gemv_dot_swiglu", H.GemvDotParams(1, n, k, fmt, H.F16), p(dev(aw)), p(dev(asc)), p(v), p(s), p(v2), p(s2), p(h))
+    got = h.download(np.float32, n)
+    g = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)[0]
+    u = O.gemv_dot(quant, aw, asc, 1, words2, scales2, n, k)[0]
+    want = O.silu(g) * u
+    gd = g.astype(np.float64)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("bt", [H.F32, H.F16, H.BF16, H.Q8_0, H.Q4_0, H.Q4_1, H.Q4_K])
+def test_float_gemv_path(bt):
+    n, k, m = 100, 512, 2
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    sc = None
+    if bt == H.F32:
+        b = (rng.standard_normal((n, k)) * 0.05).astype(np.float32); wd = b; ot = O.T_F32
+    elif bt in (H.F16, H.BF16):
+        w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+        if bt == H.F16:
+            b = w.astype(np.float16).view(np.uint16); wd = b.view(np.float16).astype(np.float32); ot = O.T_F16
+        else:
+            b = (w.view(np.uint32) >> 16).astype(np.uint16); wd = (b.astype(np.uint32) << 16).view(np.float32); ot = O.T_BF16
+    else:
+        dv, ds, quant, words, scales = weights(bt, n, k, 8)
+        wd = O.dequantize(quant, words, scales, n, k)
+        b, sc = None, None
+    out = H.empty(m * n * 4)
+    if b is not None:
+        H.call("vkml_gemv", H.GemvParams(m, n, k, bt, H.F16), p(dev(a)), p(dev(b)), p(out), None)
+    else:
+        H.call("vkml_gemv", H.GemvParams(m, n, k, bt, H.F16), p(dev(a)), p(dv), p(out), p(ds))
+    got = out.download(np.float32, (m, n))
+    want = a.astype(np.float64) @ wd.astype(np.float64).T
+    bound = 3 * k * 2.0 ** -24 * (np.abs(a.astype(np.float64)) @ np.abs(wd.astype(np.float64)).T) + 1e-30
+    assert np.all(np.abs(got - want) <= bound)
+
+
+# ---------------------------------------------------------------- norms and rope
+
+@pytest.mark.parametrize("cols", [256, 4096, 14336, 2048])
+def test_rms_norm_quantize(cols):
+    rng = np.random.default_rng(cols)
+    x = (rng.standard_normal((2, cols)) * 3).astype(np.float32)
+    w = rng.standard_normal(cols).astype(np.float32)
+    y, vals, scs = H.empty(x.nbytes), H.empty(x.size), H.empty(x.size // 32 * 4)
+    H.call("vkml_rms_norm_quantize", H.RmsNormParams(2, cols, 1e-5), p(dev(x)), p(dev(w)), p(y), p(vals), p(scs))
+    got = y.download(np.float32, x.shape)
+    want = O.rms_norm(x, w, 1e-5)
+    assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+    # the quantized form is exactly the reference quantizer's of these f32 values
+    ww, ws = O.quantize(O.Q8_0, got, False)
+    assert np.array_equal(vals.download(np.uint32, ww.shape), ww)
+    assert np.array_equal(scs.download(np.float32, ws.shape).view(np.uint32), ws.view(np.uint32))
+    plain = H.empty(x.nbytes)
+    H.call("vkml_rms_norm", H.RmsNormParams(2, cols, 1e-5), p(dev(x)), p(dev(w)), p(plain))
+    assert np.all(np.abs(plain.download(np.float32, x.shape) - want) <= 1e-5 * (1 + np.abs(want)))
+
+
+@pytest.mark.parametrize("style", [0, 1])
+def test_rope_bit_exact(style):
+    seq, heads, dim = 3, 4, 128
+    x = np.random.default_rng(1).standard_normal((seq, heads, dim)).astype(np.float32)
+    table = O.rope_table(9000, dim, 1e6)
+    want = O.rope(x, table, 8000, style)
+    out = H.empty(x.nbytes)
+    rows = seq * heads
+    H.call("vkml_rope", H.RopeParams(rows * dim // 2, dim // 2, dim, heads, seq, 8000, 0, style), p(dev(x)), p(dev(table)), p(out))
+    assert np.array_equal(out.download(np.float32, x.shape).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("kv_type", [H.F16, H.F32])
+def test_rope_kv_append_bit_exact(kv_type):
+    heads, kvh, hd, cap, pos = 32, 8, 128, 64, 37
+    rng = np.random.default_rng(2)
+    qkv = rng.standard_normal((heads + 2 * kvh) * hd).astype(np.float32)
+    table = O.rope_table(cap, hd, 1e6)
+    dt = np.uint16 if kv_type == H.F16 else np.float32
+    kc, vc = H.empty(kvh * cap * hd * 4), H.empty(kvh * cap * hd * 4)
+    q = H.empty(heads * hd * 4)
+    H.call("vkml_rope_kv_append", H.RopeKvParams(heads, kvh, hd, cap, pos, 0, kv_type, 1), p(dev(qkv)), p(dev(table)),
+           p(q), p(kc), p(vc), None)
+    qr = O.rope(qkv[:heads * hd].reshape(1, heads, hd), table, pos, 0).ravel()
+    kr = O.rope(qkv[heads * hd:(heads + kvh) * hd].reshape(1, kvh, hd), table, pos, 0).reshape(kvh, hd)
+    vr = qkv[(heads + kvh) * hd:].reshape(kvh, hd)
+    assert np.array_equal(q.download(np.float32, heads * hd).view(np.uint32), qr.view(np.uint32))
+    kg = kc.download(dt, (kvh, cap, hd))[:, pos]
+    vg = vc.download(dt, (kvh, cap, hd))[:, pos]
+    if kv_type == H.F16:
+        assert np.array_equal(kg, O.f32_to_f16(kr)) and np.array_equal(vg, O.f32_to_f16(vr))
+    else:
+        assert np.array_equal(kg.view(np.uint32), kr.view(np.uint32)) and np.array_equal(vg.view(np.uint32), vr.view(np.uint32))
+
+
+# ---------------------------------------------------------------- attention
+
+@pytest.mark.parametrize("hd,heads,kvh,kv_len,kv_type,splits", [
+    (128, 32, 8, 4096, H.F16, 64), (128, 32, 8, 1, H.F16, 64), (64, 32, 8, 640, H.F16, 32),
+    (64, 4, 2, 45, H.F32, 4), (128, 32, 8, 300, H.F32, 16), (256, 8, 8, 200, H.F16, 2), (128, 8, 1, 1000, H.F16, 8)])
+def test_attend_matches_oracle(hd, heads, kvh, kv_len, kv_type, splits):
+    cap = kv_len + 7
+    rng = np.random.default_rng(kv_len)
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    k = rng.standard_normal((kvh, cap, hd)).astype(np.float32)
+    v = rng.standard_normal((kvh, cap, hd)).astype(np.float32)
+    if kv_type == H.F16:
+        kc, vc = k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16)
+    else:
+        kc, vc = k, v
+    prm = H.AttendParams(0, kv_len, cap, heads, kvh, hd, kv_type, splits, 1.0 / math.sqrt(hd), 0.0)
+    part, stats = H.empty(kvh * splits * (heads // kvh) * hd * 4), H.empty(kvh * splits * (heads // kvh) * 8)
+    out, vals, scs = H.empty(heads * hd * 4), H.empty(heads * hd), H.empty(heads * hd // 32 * 4)
+    H.call("vkml_attend", prm, p(dev(q)), p(dev(kc)), p(dev(vc)), p(part), p(stats), None)
+    H.call("vkml_attend_merge", prm, p(part), p(stats), p(out), p(vals), p(scs))
+    got = out.download(np.float32, (heads, hd))
+    want = O.attend_decode(q, kc, vc, 0, kv_len)
+    assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+    ww, ws = O.quantize(O.Q8_0, got, False)
+    assert np.array_equal(vals.download(np.uint32, ww.shape), ww)
+    assert np.array_equal(scs.download(np.float32, ws.shape).view(np.uint32), ws.view(np.uint32))
+
+
+def test_attend_reads_kv_len_from_the_decode_state():
+    hd, heads, kvh, cap = 128, 32, 8, 512
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    kc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    st = H.empty(16)
+    H.call("vkml_state_set", p(st), 5, 299, 0)
+    prm = H.AttendParams(0, 0, cap, heads, kvh, hd, H.F16, 16, 1.0 / math.sqrt(hd), 0.0)
+    part, stats, out = H.empty(kvh * 16 * 4 * hd * 4), H.empty(kvh * 16 * 4 * 8), H.empty(heads * hd * 4)
+    H.call("vkml_attend", prm, p(dev(q)), p(dev(kc)), p(dev(vc)), p(part), p(stats), p(st))
+    H.call("vkml_attend_merge", prm, p(part), p(stats), p(out), None, None)
+    want = O.attend_decode(q, kc, vc, 0, 300)
+    assert np.all(np.abs(out.download(np.float32, (heads, hd)) - want) <= 1e-5 * (1 + np.abs(want)))
+
+
+# ---------------------------------------------------------------- small ops
+
+def test_argmax_and_step_finish():
+    x = np.random.default_rng(11).standard_normal((3, 32768)).astype(np.float32) * 3
+    x[0, 5] = x[0, 900] = 100.0
+    x[1, :] = np.nan
+    x[2, 7] = np.inf
+    x[2, 9] = np.nan
+    out = H.empty(12)
+    H.call("vkml_argmax", 3, 32768, p(dev(x)), p(out))
+    assert list(out.download(np.int32, 3)) == [O.argmax(r) for r in x] == [5, 0, 7]
+    st, log = H.empty(16), H.empty(64)
+    H.call("vkml_state_set", p(st), 1, 10, 0)
+    H.call("vkml_step_finish", 32768, p(dev(x[0])), p(st), p(log), 16)
+    H.call("vkml_step_finish", 0, None, p(st), p(log), 16)
+    assert list(st.download(np.int32, 4)[:3]) == [5, 12, 1]
+    assert log.download(np.int32, 1)[0] == 5
+
+
+@pytest.mark.parametrize("tt", [H.F32, H.F16, H.BF16, H.Q8_0, H.Q4_0, H.Q4_1, H.Q4_K])
+def test_embedding_bit_exact(tt):
+    vocab, dim = 300, 512
+    ids = np.array([0, 299, 5, -1, 300, 17], np.int32)
+    if tt in (H.F32, H.F16, H.BF16):
+        t = np.random.default_rng(4).standard_normal((vocab, dim)).astype(np.float32)
+        if tt == H.F16:
+            vals = t.astype(np.float16).view(np.uint16); table = vals.view(np.float16).astype(np.float32)
+        elif tt == H.BF16:
+            vals = (t.view(np.uint32) >> 16).astype(np.uint16); table = (vals.astype(np.uint32) << 16).view(np.float32)
+        else:
+            vals = table = t
+        want = np.array([table[i] if 0 <= i < vocab else np.zeros(dim, np.float32) for i in ids])
+        dv, ds = dev(vals), None
+    else:
+        dv, ds, quant, words, halves = weights(tt, vocab, dim, 12)
+        want = O.embedding_quantized(quant, words, halves, vocab, dim, ids)
+    out = H.empty(ids.size * dim * 4)
+    H.call("vkml_embedding", H.EmbeddingParams(ids.size * dim, dim, vocab, tt, H.F16), p(dv), p(ds), p(dev(ids)), p(out))
+    assert np.array_equal(out.download(np.float32, want.shape).view(np.uint32), want.view(np.uint32))
+
+
+def test_cast_copy_permute_elementwise():
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(1000).astype(np.float32) * 1e3,
+                        np.array([65520.0, 65519.0, 2.0 ** -25, 3 * 2.0 ** -26, np.nan, -np.inf, 1e-40], np.float32)])
+    out = H.empty(x.size * 4)
+    H.call("vkml_cast", x.size, H.F32, H.F16, p(dev(x)), p(out))
+    assert np.array_equal(out.download(np.uint16, x.size), O.f32_to_f16(x))
+    h = O.f32_to_f16(x)
+    H.call("vkml_cast", x.size, H.F16, H.F32, p(dev(h)), p(out))
+    back = out.download(np.float32, x.size)
+    ref = O.f16_to_f32(h)
+    assert np.array_equal(np.isnan(back), np.isnan(ref)) and np.array_equal(back[~np.isnan(ref)], ref[~np.isnan(ref)])
+    # write_rows: rows 3..5 of a [2, 4, 6] word tensor into rows 1..3 of [2, 8, 6]
+    src = np.arange(2 * 4 * 6, dtype=np.uint32)
+    dst = np.zeros(2 * 8 * 6, np.uint32)
+    d = dev(dst)
+    H.call("vkml_copy_rows", H.CopyRowsParams(2 * 3 * 6, 3 * 6, 4 * 6, 1 * 6, 8 * 6, 1 * 6), p(dev(src)), p(d))
+    want = dst.reshape(2, 8, 6).copy()
+    want[:, 1:4] = src.reshape(2, 4, 6)[:, 1:4]
+    assert np.array_equal(d.download(np.uint32, want.shape), want)
+    # permute [2,3,4] -> dims (2, 0, 1)
+    t = np.arange(24, dtype=np.float32).reshape(2, 3, 4)
+    prm = H.PermuteParams(3, 24, (H.u32 * 6)(2, 3, 4, 1, 1, 1), (H.u32 * 6)(2, 0, 1, 0, 0, 0))
+    H.call("vkml_permute", prm, p(dev(t)), p(out))
+    assert np.array_equal(out.download(np.float32, (4, 2, 3)), t.transpose(2, 0, 1))
+    a = rng.standard_normal(1000).astype(np.float32)
+    b = rng.standard_normal(10).astype(np.float32)
+    for op, f in enumerate([np.add, np.subtract, np.multiply, np.divide]):
+        H.call("vkml_binary", op, 1000, 10, p(dev(a)), p(dev(b)), p(out))
+        assert np.array_equal(out.download(np.float32, 1000), f(a, np.tile(b, 100)).astype(np.float32))
+    H.call("vkml_unary", 0, 1000, 0.0, p(dev(a * 30)), p(out))
+    assert np.allclose(out.download(np.float32, 1000), O.silu(a * 30), rtol=2e-6, atol=1e-30)
+
+
+def test_softmax_and_matmul():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((8, 37)).astype(np.float32)
+    out = H.empty(x.nbytes)
+    H.call("vkml_softmax", H.SoftmaxParams(8, 37, 0.5, 1, 4, 33, 0, 0.0), p(dev(x)), p(out))
+    got = out.download(np.float32, x.shape)
+    for r in range(8):
+        vis = min(37, r % 4 + 33 + 1)
+        e = np.exp(x[r, :vis].astype(np.float64) * 0.5 - (x[r, :vis] * 0.5).max())
+        want = np.zeros(37)
+        want[:vis] = e / e.sum()
+        assert np.allclose(got[r], want, atol=1e-6)
+    a = rng.standard_normal((4, 3, 20)).astype(np.float32)
+    b = rng.standard_normal((2, 5, 20)).astype(np.float32)  # [2 kv batches, n=5, k=20], transposed, group 2
+    out = H.empty(4 * 3 * 5 * 4)
+    H.call("vkml_matmul", H.MatmulParams(3, 5, 20, 100, 2, 4, 1, H.F32), p(dev(a)), p(dev(b)), p(out))
+    want = np.stack([a[z] @ b[z // 2].T for z in range(4)])
+    assert np.allclose(out.download(np.float32, want.shape), want, atol=1e-5)
+
+
+def test_graph_replay_advances_the_state():
+    st, log = H.empty(16), H.empty(64)
+    logits = np.zeros(1000, np.float32)
+    logits[123] = 1.0
+    dl = dev(logits)
+    H.call("vkml_state_set", p(st), 0, 0, 0)
+    H.call("vkml_graph_begin")
+    H.call("vkml_step_finish", 1000, p(dl), p(st), p(log), 16)
+    g = H.u64()
+    H.call("vkml_graph_end", H.C.byref(g))
+    for _ in range(5):
+        H.call("vkml_graph_launch", g.value)
+    H.synchronize()
+    assert list(st.download(np.int32, 4)[:3]) == [123, 5, 5]
+    assert list(log.download(np.int32, 5)) == [123] * 5
+    H.call("vkml_graph_destroy", g.value)

@@ -1,0 +1,202 @@
+// device.hpp -- gfx950 device helpers shared by the kernels: 16-bit float
+// conversions, wave64 reductions, int8 dot products and the weight decoders.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vkml::dev {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- 16-bit floats
+
+// f16 bits to f32, exactly (v_cvt_f32_f16 keeps f16 subnormals: the f16
+// denormal mode is IEEE on gfx9).
+__device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// f32 to f16 and back, round to nearest even, as the reference rounds
+// q4_K's products (src/io/gguf.cpp:609-617); finite inputs only.
+__device__ __forceinline__ float round_to_f16(float x) {
+    return static_cast<float>(static_cast<_Float16>(x));
+}
+
+// f32 bits to f16 bits rounding to nearest even on the bits, so no input is
+// flushed (the reference's to_f16, shaders/include/halves.glsl:73-91).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(uint32_t bits) {
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const uint32_t a = bits & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return sign | 0x7E00u;
+    if (a >= 0x477FF000u) return sign | 0x7C00u;
+    if (a < 0x38800000u) {
+        const uint32_t e = a >> 23;
+        if (e < 102u) return sign;
+        const uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+        const uint32_t shift = 126u - e;
+        uint32_t q = m >> shift;
+        const uint32_t rest = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rest > half || (rest == half && (q & 1u) != 0u)) q += 1u;
+        return sign | q;
+    }
+    return sign | ((a + 0xFFFu + ((a >> 13) & 1u) - 0x38000000u) >> 13);
+}
+
+// shaders/cast.comp:30-35
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(uint32_t bits) {
+    if ((bits & 0x7FFFFFFFu) > 0x7F800000u) return (bits >> 16) | 0x40u;
+    return (bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ float half_to_float(uint32_t h, uint32_t type) {
+    return type == 2 ? bf16_bits_to_float(h) : f16_bits_to_float(h);
+}
+
+// ---------------------------------------------------------------- reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+// Sum over groups of `width` consecutive lanes (a power of two <= 64).
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+template <int width>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64, at most 1024; every
+// thread gets the result. scratch: 16 floats of LDS.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int waves = blockDim.x / kWave;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float s = lane < waves ? scratch[lane] : 0.0f;
+    return wave_sum(s);
+}
+__device__ __forceinline__ float block_max(float v, float* scratch) {
+    v = wave_max(v);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int waves = blockDim.x / kWave;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float s = lane < waves ? scratch[lane] : -__builtin_inff();
+    return wave_max(s);
+}
+
+// ---------------------------------------------------------------- int8 dot
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// Sum of the 16 signed bytes of v.
+__device__ __forceinline__ int byte_sum(uint4 v) {
+    const uint32_t ones = 0x01010101u;
+    return dot4(v.w, ones, dot4(v.z, ones, dot4(v.y, ones, dot4(v.x, ones, 0))));
+}
+
+// Activation quantization of one value given its block's inverse scale
+// (shaders/quantize.comp:210-221): round half to even, clamp to +-127.
+__device__ __forceinline__ int quant_code(float x, float inv) {
+    return static_cast<int>(fminf(fmaxf(__builtin_rintf(x * inv), -127.0f), 127.0f));
+}
+
+// ---------------------------------------------------------------- q4_K headers
+
+// Scale and offset of sub-blocks 2c and 2c+1 of a q4_K super-block whose
+// 16-byte header is hdr (d, dmin, 12 bytes of 6-bit scales and mins),
+// as the f32 values of the f16-rounded products f16(d * sc) and
+// f16(-(dmin * m)) (src/io/gguf.cpp:123-131,603-617).
+__device__ __forceinline__ void q4k_scales(uint4 hdr, uint32_t c, float& s0, float& o0, float& s1,
+                                           float& o1) {
+    const uint32_t shift = (c & 1u) * 16u;
+    const uint32_t Y = (hdr.y >> shift) & 0xFFFFu;
+    const uint32_t Z = (hdr.z >> shift) & 0xFFFFu;
+    const uint32_t W = (hdr.w >> shift) & 0xFFFFu;
+    uint32_t sc, mn;
+    if (c < 2) {
+        sc = Y & 0x3F3Fu;
+        mn = Z & 0x3F3Fu;
+    } else {
+        sc = (W & 0x0F0Fu) | ((Y & 0xC0C0u) >> 2);
+        mn = ((W >> 4) & 0x0F0Fu) | ((Z & 0xC0C0u) >> 2);
+    }
+    const float d = f16_bits_to_float(hdr.x & 0xFFFFu);
+    const float dmin = f16_bits_to_float(hdr.x >> 16);
+    s0 = round_to_f16(d * static_cast<float>(sc & 0xFFu));
+    s1 = round_to_f16(d * static_cast<float>(sc >> 8));
+    o0 = round_to_f16(-(dmin * static_cast<float>(mn & 0xFFu)));
+    o1 = round_to_f16(-(dmin * static_cast<float>(mn >> 8)));
+}
+
+// Bit offset of value i % 8 within a QuantizedMatrix q4 word
+// (shaders/include/halves.glsl:27).
+__device__ __forceinline__ uint32_t q4_shift(uint32_t i) { return 8u * (i & 3u) + 4u * ((i >> 2) & 1u); }
+
+// Value col of row `row` of a [rows, cols] weight matrix of `type` (the
+// reference's dequantize.comp:37-48 and load_b of gemv.comp:80-92). Products
+// and sums are rounded separately, never fused.
+__device__ __forceinline__ float weight_value(uint32_t type, uint32_t scale_type, const void* values,
+                                              const void* scales, uint64_t cols, uint64_t row,
+                                              uint64_t col) {
+#pragma clang fp contract(off)
+    const uint64_t e = row * cols + col;
+    const auto scale_at = [&](uint64_t i) -> float {
+        return scale_type == 1 ? f16_bits_to_float(static_cast<const uint16_t*>(scales)[i])
+                               : static_cast<const float*>(scales)[i];
+    };
+    switch (type) {
+        case 0: return static_cast<const float*>(values)[e];
+        case 1: return f16_bits_to_float(static_cast<const uint16_t*>(values)[e]);
+        case 2: return bf16_bits_to_float(static_cast<const uint16_t*>(values)[e]);
+        case 3: {
+            const int8_t q = static_cast<const int8_t*>(values)[e];
+            return __fmul_rn(static_cast<float>(q), scale_at(e / 32));
+        }
+        case 4: {
+            const uint32_t w = static_cast<const uint32_t*>(values)[e / 8];
+            const float q = static_cast<float>(static_cast<int>((w >> q4_shift(static_cast<uint32_t>(e))) & 15u) - 8);
+            return __fmul_rn(q, scale_at(e / 32));
+        }
+        case 5: {
+            const uint32_t w = static_cast<const uint32_t*>(values)[e / 8];
+            const float q = static_cast<float>((w >> q4_shift(static_cast<uint32_t>(e))) & 15u);
+            return __fadd_rn(__fmul_rn(q, scale_at(2 * (e / 32))), scale_at(2 * (e / 32) + 1));
+        }
+        case 6: {
+            // q4_K: super-block sb of the row, sub-block j, position l.
+            const uint64_t sb = col / 256, j = (col % 256) / 32, l = col % 32;
+            const uint8_t* qs = static_cast<const uint8_t*>(values) + row * (cols / 2) + sb * 128 + 32 * (j / 2);
+            const uint32_t code = (j % 2 == 0) ? (qs[l] & 15u) : (qs[l] >> 4);
+            const uint4 hdr = static_cast<const uint4*>(scales)[row * (cols / 256) + sb];
+            float s0, o0, s1, o1;
+            q4k_scales(hdr, static_cast<uint32_t>(j / 2), s0, o0, s1, o1);
+            const float s = (j % 2 == 0) ? s0 : s1, o = (j % 2 == 0) ? o0 : o1;
+            return __fadd_rn(__fmul_rn(static_cast<float>(code), s), o);
+        }
+        default: return 0.0f;
+    }
+}
+
+}  // namespace vkml::dev

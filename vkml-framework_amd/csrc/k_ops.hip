@@ -1,0 +1,713 @@
+// k_ops.hip -- the decode path's small kernels and the rest of the op set:
+// quantize/dequantize, RMSNorm (+ fused activation quantize), RoPE (+ fused
+// cast and KV append), cast, row copies, permute, elementwise, embeddings,
+// argmax, softmax and a tiled f32 matmul, plus the decode-state helpers.
+// Where the result is integer or bit-level (codes, scales, casts, copies,
+// argmax) it is exactly the reference's; products and sums that the
+// reference writes separately are rounded separately here (__fmul_rn,
+// __fadd_rn) so the compiler fuses none of them.
+#include <algorithm>
+#include <cmath>
+
+#include "device.hpp"
+#include "internal.hpp"
+
+// Bit-exact results need every product and sum the reference writes apart to
+// be rounded apart: no multiply-add fusion in this file.
+#pragma clang fp contract(off)
+
+using namespace vkml::dev;
+using vkml::abi::ProfileScope;
+
+namespace {
+
+hipStream_t S() { return vkml::abi::stream(); }
+
+uint32_t blocks_for(uint64_t n, uint32_t threads = 256, uint32_t cap = 65535) {
+    return static_cast<uint32_t>(std::max<uint64_t>(1, std::min<uint64_t>((n + threads - 1) / threads, cap)));
+}
+
+__device__ __forceinline__ float load_src(const void* x, uint64_t e, uint32_t type) {
+    if (type == VKML_F32) return static_cast<const float*>(x)[e];
+    return half_to_float(static_cast<const uint16_t*>(x)[e], type);
+}
+
+// ---------------------------------------------------------------- quantize
+
+// shaders/quantize.comp:153-247 for one block: codes into q, scale (and
+// offset) as kept (rounded to f16 with f16 scales), their f16 bits in bits.
+__device__ void quantize_block(const void* x, uint32_t src_type, uint32_t quant, bool f16, uint64_t b,
+                               uint32_t* q, float& d_out, float& m_out, uint32_t& bits_d, uint32_t& bits_m) {
+    const uint64_t base = b * 32;
+    const auto kept = [&](float v, uint32_t& bits) -> float {
+        if (!f16) {
+            bits = 0;
+            return v;
+        }
+        bits = f32_to_f16_bits(__float_as_uint(v));
+        return f16_bits_to_float(bits);
+    };
+    bits_m = 0;
+    if (quant == VKML_Q4_1) {
+        float lo = load_src(x, base, src_type), hi = lo;
+        for (int i = 1; i < 32; ++i) {
+            const float v = load_src(x, base + i, src_type);
+            lo = fminf(lo, v);
+            hi = fmaxf(hi, v);
+        }
+        const float m = kept(lo, bits_m);
+        const float d = kept((hi - lo) / 15.0f, bits_d);
+        const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+        for (int w = 0; w < 4; ++w) {
+            uint32_t word = 0;
+            for (uint32_t j = 0; j < 8; ++j) {
+                const float code = fminf(fmaxf(__builtin_rintf(__fmul_rn(load_src(x, base + 8 * w + j, src_type) - m, inv)), 0.0f), 15.0f);
+                word |= static_cast<uint32_t>(code) << q4_shift(j);
+            }
+            q[w] = word;
+        }
+        d_out = d;
+        m_out = m;
+        return;
+    }
+    if (quant == VKML_Q4_0) {
+        float m = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float v = load_src(x, base + i, src_type);
+            if (fabsf(v) > fabsf(m)) m = v;
+        }
+        const float d = kept(m / -8.0f, bits_d);
+        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        for (int w = 0; w < 4; ++w) {
+            uint32_t word = 0;
+            for (uint32_t j = 0; j < 8; ++j) {
+                const int v = static_cast<int>(fminf(fmaxf(__builtin_rintf(load_src(x, base + 8 * w + j, src_type) * inv), -8.0f), 7.0f));
+                word |= static_cast<uint32_t>(v + 8) << q4_shift(j);
+            }
+            q[w] = word;
+        }
+        d_out = d;
+        m_out = 0.0f;
+        return;
+    }
+    float absmax = 0.0f;
+    for (int i = 0; i < 32; ++i) absmax = fmaxf(absmax, fabsf(load_src(x, base + i, src_type)));
+    const float d = kept(absmax / 127.0f, bits_d);
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    for (int w = 0; w < 8; ++w) {
+        uint32_t word = 0;
+        for (int j = 0; j < 4; ++j) word |= (static_cast<uint32_t>(quant_code(load_src(x, base + 4 * w + j, src_type), inv)) & 0xFFu) << (8 * j);
+        q[w] = word;
+    }
+    d_out = d;
+    m_out = 0.0f;
+}
+
+__global__ void k_quantize(vkml_quantize_params p, const void* x, uint32_t* values, void* scales) {
+    const bool f16 = p.scale_type == VKML_F16;
+    const uint32_t per_word = p.quant == VKML_Q8_0 ? 8 : 4;
+    for (uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; b < p.blocks;
+         b += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        float d, m;
+        uint32_t bd, bm;
+        quantize_block(x, p.src_type, p.quant, f16, b, values + b * per_word, d, m, bd, bm);
+        if (!f16) {
+            float* s = static_cast<float*>(scales);
+            if (p.quant == VKML_Q4_1) {
+                s[2 * b] = d;
+                s[2 * b + 1] = m;
+            } else {
+                s[b] = d;
+            }
+        } else {
+            uint16_t* s = static_cast<uint16_t*>(scales);
+            if (p.quant == VKML_Q4_1) {
+                s[2 * b] = static_cast<uint16_t>(bd);
+                s[2 * b + 1] = static_cast<uint16_t>(bm);
+            } else {
+                s[b] = static_cast<uint16_t>(bd);
+            }
+        }
+    }
+}
+
+// Activations to Q8_0 with f32 scales, 8 lanes per block of 32.
+__global__ void k_quantize_act(uint32_t blocks, const float4* x, uint32_t* values, float* scales) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // float4 index
+    const bool live = i < static_cast<uint64_t>(blocks) * 8;
+    const float4 v = live ? x[i] : make_float4(0, 0, 0, 0);
+    const float absmax = group_max<8>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const float d = absmax / 127.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    if (!live) return;
+    values[i] = (static_cast<uint32_t>(quant_code(v.x, inv)) & 0xFFu) | ((static_cast<uint32_t>(quant_code(v.y, inv)) & 0xFFu) << 8) |
+                ((static_cast<uint32_t>(quant_code(v.z, inv)) & 0xFFu) << 16) | (static_cast<uint32_t>(quant_code(v.w, inv)) << 24);
+    if (i % 8 == 0) scales[i / 8] = d;
+}
+
+__global__ void k_dequantize(vkml_dequantize_params p, const void* values, const void* scales, float* out) {
+    for (uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < p.count;
+         e += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        out[e] = weight_value(p.quant, p.scale_type, values, scales, p.cols, e / p.cols, e % p.cols);
+    }
+}
+
+// ---------------------------------------------------------------- norms
+
+__global__ void k_rms_norm(vkml_rms_norm_params p, const float* x, const float* w, float* out) {
+    __shared__ float scratch[16];
+    for (uint32_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
+        const float* xr = x + static_cast<uint64_t>(row) * p.cols;
+        float s = 0.0f;
+        for (uint32_t c = threadIdx.x; c < p.cols; c += blockDim.x) s += xr[c] * xr[c];
+        s = block_sum(s, scratch);
+        const float scale = 1.0f / sqrtf(s / static_cast<float>(p.cols) + p.eps);
+        for (uint32_t c = threadIdx.x; c < p.cols; c += blockDim.x)
+            out[static_cast<uint64_t>(row) * p.cols + c] = __fmul_rn(__fmul_rn(xr[c], scale), w[c]);
+        __syncthreads();
+    }
+}
+
+// One block of 1024 per row; each thread a float4 of every 1024; the 8
+// lanes of a 32-value block quantize it together.
+__global__ void __launch_bounds__(1024) k_rms_norm_quantize(vkml_rms_norm_params p, const float4* x, const float4* w, float4* out,
+                                                            uint32_t* values, float* scales) {
+    __shared__ float scratch[16];
+    const uint32_t row = blockIdx.x, n4 = p.cols / 4;
+    const float4* xr = x + static_cast<uint64_t>(row) * n4;
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n4; i += blockDim.x) {
+        const float4 v = xr[i];
+        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    s = block_sum(s, scratch);
+    const float scale = 1.0f / sqrtf(s / static_cast<float>(p.cols) + p.eps);
+    for (uint32_t base = 0; base < n4; base += blockDim.x) {
+        const uint32_t i = base + threadIdx.x;
+        const bool live = i < n4;
+        float4 y = make_float4(0, 0, 0, 0);
+        if (live) {
+            const float4 v = xr[i], wv = w[i];
+            y = make_float4(__fmul_rn(__fmul_rn(v.x, scale), wv.x), __fmul_rn(__fmul_rn(v.y, scale), wv.y),
+                            __fmul_rn(__fmul_rn(v.z, scale), wv.z), __fmul_rn(__fmul_rn(v.w, scale), wv.w));
+            if (out) out[static_cast<uint64_t>(row) * n4 + i] = y;
+        }
+        const float absmax = group_max<8>(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+        const float d = absmax / 127.0f;
+        const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+        if (live) {
+            const uint64_t at = static_cast<uint64_t>(row) * n4 + i;
+            values[at] = (static_cast<uint32_t>(quant_code(y.x, inv)) & 0xFFu) | ((static_cast<uint32_t>(quant_code(y.y, inv)) & 0xFFu) << 8) |
+                         ((static_cast<uint32_t>(quant_code(y.z, inv)) & 0xFFu) << 16) | (static_cast<uint32_t>(quant_code(y.w, inv)) << 24);
+            if (i % 8 == 0) scales[at / 8] = d;
+        }
+    }
+}
+
+// shaders/softmax.comp:85-124 (no ring: causal rows see keys offset + row % q_len and before).
+__global__ void k_softmax(vkml_softmax_params p, const float* x, float* out) {
+    __shared__ float scratch[16];
+    for (uint32_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
+        const float* xr = x + static_cast<uint64_t>(row) * p.cols;
+        uint32_t visible = p.cols, first = 0;
+        if (p.causal) {
+            visible = min(p.cols, row % p.q_len + p.offset + 1);
+            if (p.window != 0 && visible > p.window) first = visible - p.window;
+        }
+        const auto score = [&](uint32_t c) {
+            const float s = xr[c] * p.scale;
+            return p.softcap > 0.0f ? p.softcap * tanhf(fminf(fmaxf(s / p.softcap, -10.0f), 10.0f)) : s;
+        };
+        float m = -__builtin_inff();
+        for (uint32_t c = first + threadIdx.x; c < visible; c += blockDim.x) m = fmaxf(m, score(c));
+        m = block_max(m, scratch);
+        float s = 0.0f;
+        for (uint32_t c = first + threadIdx.x; c < visible; c += blockDim.x) s += expf(score(c) - m);
+        s = block_sum(s, scratch);
+        const float inv = 1.0f / s;
+        for (uint32_t c = threadIdx.x; c < p.cols; c += blockDim.x)
+            out[static_cast<uint64_t>(row) * p.cols + c] = (c >= first && c < visible) ? expf(score(c) - m) * inv : 0.0f;
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------- argmax
+
+// (value, column) of the winner of two candidates: larger, or equal and
+// earlier; column -1 means none (all NaN so far). shaders/argmax.comp:145-148.
+__device__ __forceinline__ void better(float& v, int& c, float ov, int oc) {
+    if (oc >= 0 && (c < 0 || ov > v || (ov == v && oc < c))) {
+        v = ov;
+        c = oc;
+    }
+}
+
+__device__ int block_argmax(const float* x, uint32_t cols) {
+    __shared__ float s_v[16];
+    __shared__ int s_c[16];
+    float best = 0.0f;
+    int col = -1;
+    for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
+        const float v = x[c];
+        if (!__builtin_isnan(v) && (col < 0 || v > best)) {
+            best = v;
+            col = static_cast<int>(c);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) better(best, col, __shfl_xor(best, o, kWave), __shfl_xor(col, o, kWave));
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    __syncthreads();
+    if (lane == 0) {
+        s_v[wave] = best;
+        s_c[wave] = col;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int waves = blockDim.x / kWave;
+        best = lane < waves ? s_v[lane] : 0.0f;
+        col = lane < waves ? s_c[lane] : -1;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) better(best, col, __shfl_xor(best, o, kWave), __shfl_xor(col, o, kWave));
+    }
+    return col < 0 ? 0 : col;  // valid in thread 0
+}
+
+__global__ void __launch_bounds__(1024) k_argmax(uint32_t rows, uint32_t cols, const float* x, int32_t* out) {
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const int c = block_argmax(x + static_cast<uint64_t>(row) * cols, cols);
+        if (threadIdx.x == 0) out[row] = c;
+        __syncthreads();
+    }
+}
+
+__global__ void __launch_bounds__(1024) k_step_finish(uint32_t vocab, const float* logits, vkml_decode_state* st, int32_t* log,
+                                                      uint32_t cap) {
+    int tok = 0;
+    if (logits) tok = block_argmax(logits, vocab);
+    if (threadIdx.x == 0) {
+        if (logits) {
+            st->token = tok;
+            if (log && static_cast<uint32_t>(st->steps) < cap) log[st->steps] = tok;
+            st->steps += 1;
+        }
+        st->position += 1;
+    }
+}
+
+__global__ void k_state_set(vkml_decode_state* st, int32_t token, int32_t position, int32_t steps) {
+    st->token = token;
+    st->position = position;
+    st->steps = steps;
+    st->reserved = 0;
+}
+
+// ---------------------------------------------------------------- rope
+
+__global__ void k_rope(vkml_rope_params p, const float* x, const float* table, float* out) {
+    const uint32_t rest = p.dim - 2 * p.half_dim;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < static_cast<uint64_t>(p.pairs) + p.copies;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        if (i >= p.pairs) {
+            const uint64_t q = i - p.pairs;
+            const uint64_t at = (q / rest) * p.dim + 2 * p.half_dim + q % rest;
+            out[at] = x[at];
+            continue;
+        }
+        const uint64_t row = i / p.half_dim, k = i % p.half_dim;
+        const uint64_t pos = p.start_pos + (row / p.heads) % p.seq;
+        const uint64_t base = row * p.dim;
+        const uint64_t ia = base + (p.style == 0 ? 2 * k : k);
+        const uint64_t ib = base + (p.style == 0 ? 2 * k + 1 : k + p.half_dim);
+        const float c = table[(pos * p.half_dim + k) * 2], s = table[(pos * p.half_dim + k) * 2 + 1];
+        const float a = x[ia], b = x[ib];
+        out[ia] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+        out[ib] = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+    }
+}
+
+__device__ __forceinline__ void store_cache(void* cache, uint32_t type, uint64_t at, float v) {
+    if (type == VKML_F16) static_cast<uint16_t*>(cache)[at] = static_cast<uint16_t>(f32_to_f16_bits(__float_as_uint(v)));
+    else static_cast<float*>(cache)[at] = v;
+}
+
+// One thread per pair: q pairs, then k pairs (rotated, cast, appended), then v pairs.
+__global__ void k_rope_kv_append(vkml_rope_kv_params p, const float* qkv, const float* table, float* q_out, void* k_cache,
+                                 void* v_cache, const vkml_decode_state* st) {
+    const uint32_t half = p.head_dim / 2;
+    const uint32_t q_pairs = p.heads * half, kv_pairs = p.kv_heads * half;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= q_pairs + 2 * kv_pairs) return;
+    const uint32_t pos = st ? static_cast<uint32_t>(st->position) : p.position;
+    const uint32_t q_dim = p.heads * p.head_dim, kv_dim = p.kv_heads * p.head_dim;
+    const uint64_t cache_row = pos % p.capacity;
+    if (i < q_pairs + kv_pairs) {
+        const bool is_q = i < q_pairs;
+        const uint32_t j = is_q ? i : i - q_pairs;
+        const uint32_t head = j / half, k = j % half;
+        const uint32_t ia = head * p.head_dim + (p.style == 0 ? 2 * k : k);
+        const uint32_t ib = head * p.head_dim + (p.style == 0 ? 2 * k + 1 : k + half);
+        const float* src = qkv + (is_q ? 0 : q_dim);
+        float a = src[ia], b = src[ib];
+        if (p.rotate) {
+            const float c = table[(static_cast<uint64_t>(pos) * half + k) * 2], s = table[(static_cast<uint64_t>(pos) * half + k) * 2 + 1];
+            const float ra = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+            const float rb = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+            a = ra;
+            b = rb;
+        }
+        if (is_q) {
+            q_out[ia] = a;
+            q_out[ib] = b;
+        } else {
+            const uint64_t row = (static_cast<uint64_t>(head) * p.capacity + cache_row) * p.head_dim;
+            store_cache(k_cache, p.kv_type, row + (ia - head * p.head_dim), a);
+            store_cache(k_cache, p.kv_type, row + (ib - head * p.head_dim), b);
+        }
+    } else {
+        const uint32_t j = i - q_pairs - kv_pairs;
+        const uint32_t head = j / half, e = 2 * (j % half);
+        const float* v = qkv + q_dim + kv_dim + head * p.head_dim;
+        const uint64_t row = (static_cast<uint64_t>(head) * p.capacity + cache_row) * p.head_dim;
+        store_cache(v_cache, p.kv_type, row + e, v[e]);
+        store_cache(v_cache, p.kv_type, row + e + 1, v[e + 1]);
+    }
+}
+
+// ---------------------------------------------------------------- copies
+
+__global__ void k_cast(uint32_t count, uint32_t src, uint32_t dst, const void* x, void* out) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        if (dst == VKML_F32) {
+            static_cast<float*>(out)[i] = load_src(x, i, src);
+        } else {
+            const uint32_t bits = static_cast<const uint32_t*>(x)[i];
+            static_cast<uint16_t*>(out)[i] = static_cast<uint16_t>(dst == VKML_F16 ? f32_to_f16_bits(bits) : f32_to_bf16_bits(bits));
+        }
+    }
+}
+
+__global__ void k_copy_rows(vkml_copy_rows_params p, const uint32_t* src, uint32_t* dst) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < p.count; i += stride) {
+        const uint64_t batch = i / p.block, at = i % p.block;
+        dst[batch * p.dst_stride + p.dst_start + at] = src[batch * p.src_stride + p.src_start + at];
+    }
+}
+
+__global__ void k_permute(vkml_permute_params p, const uint32_t* x, uint32_t* out) {
+    uint64_t in_stride[6];
+    uint64_t s = 1;
+    for (int d = static_cast<int>(p.rank) - 1; d >= 0; --d) {
+        in_stride[d] = s;
+        s *= p.in_shape[d];
+    }
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < p.count; i += stride) {
+        uint64_t rem = i, src = 0;
+        for (int d = static_cast<int>(p.rank) - 1; d >= 0; --d) {
+            const uint32_t size = p.in_shape[p.dims[d]];
+            src += (rem % size) * in_stride[p.dims[d]];
+            rem /= size;
+        }
+        out[i] = x[src];
+    }
+}
+
+__global__ void k_binary(uint32_t op, uint32_t count, uint32_t b_count, const float* a, const float* b, float* out) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const float x = a[i], y = b[i % b_count];
+        out[i] = op == 0 ? __fadd_rn(x, y) : op == 1 ? __fsub_rn(x, y) : op == 2 ? __fmul_rn(x, y) : x / y;
+    }
+}
+
+__global__ void k_unary(uint32_t op, uint32_t count, float param, const float* x, float* out) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const float v = x[i];
+        float r;
+        if (op == 0) {
+            r = v / (1.0f + expf(-v));
+        } else if (op == 1) {
+            const float inner = fminf(fmaxf(0.7978845608f * (v + 0.044715f * v * v * v), -10.0f), 10.0f);
+            r = 0.5f * v * (1.0f + tanhf(inner));
+        } else {
+            r = param * tanhf(fminf(fmaxf(v / param, -10.0f), 10.0f));
+        }
+        out[i] = r;
+    }
+}
+
+__global__ void k_embedding(vkml_embedding_params p, const void* values, const void* scales, const int32_t* ids,
+                            const vkml_decode_state* st, float* out) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < p.count; i += stride) {
+        const int32_t id = st ? st->token : ids[i / p.dim];
+        const uint64_t col = i % p.dim;
+        out[i] = (id >= 0 && static_cast<uint32_t>(id) < p.vocab)
+                     ? weight_value(p.table_type, p.scale_type, values, scales, p.dim, static_cast<uint64_t>(id), col)
+                     : 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------- matmul
+
+// c = a . b (or b^T): 16x16 output tiles, K in steps of 16 through LDS.
+template <bool BT>
+__global__ void k_matmul(vkml_matmul_params p, const float* a, const void* b, float* c) {
+    __shared__ float ta[16][17], tb[16][17];
+    const uint32_t z = blockIdx.z;
+    const uint32_t row = blockIdx.y * 16 + threadIdx.y, col = blockIdx.x * 16 + threadIdx.x;
+    const float* az = a + static_cast<uint64_t>(z) * p.m * p.k;
+    const uint64_t b_off = static_cast<uint64_t>(z / p.b_group) * p.b_stride;
+    float acc = 0.0f;
+    for (uint32_t k0 = 0; k0 < p.k; k0 += 16) {
+        const uint32_t ka = k0 + threadIdx.x, kb = k0 + threadIdx.y;
+        ta[threadIdx.y][threadIdx.x] = (row < p.m && ka < p.k) ? az[static_cast<uint64_t>(row) * p.k + ka] : 0.0f;
+        float bv = 0.0f;
+        if (col < p.n && kb < p.k) {
+            const uint64_t e = b_off + (BT ? static_cast<uint64_t>(col) * p.k + kb : static_cast<uint64_t>(kb) * p.n + col);
+            bv = load_src(b, e, p.b_type);
+        }
+        tb[threadIdx.y][threadIdx.x] = bv;
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) acc += ta[threadIdx.y][kk] * tb[kk][threadIdx.x];
+        __syncthreads();
+    }
+    if (row < p.m && col < p.n) c[(static_cast<uint64_t>(z) * p.m + row) * p.n + col] = acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vkml_quantize(const vkml_quantize_params* p, const void* x, void* values, void* scales) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "quantize: null params");
+    VKML_CHECK_ARG(p->src_type <= VKML_BF16, "quantize: source must be f32, f16 or bf16");
+    VKML_CHECK_ARG(p->quant == VKML_Q8_0 || p->quant == VKML_Q4_0 || p->quant == VKML_Q4_1, "quantize: format must be q8_0, q4_0 or q4_1");
+    VKML_CHECK_ARG(p->scale_type == VKML_F32 || p->scale_type == VKML_F16, "quantize: scales must be f32 or f16");
+    if (p->blocks == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && values && scales, "quantize: null buffer");
+    if (p->src_type == VKML_F32 && p->quant == VKML_Q8_0 && p->scale_type == VKML_F32) {
+        ProfileScope prof("quantize");
+        const uint64_t threads = static_cast<uint64_t>(p->blocks) * 8;
+        hipLaunchKernelGGL(k_quantize_act, dim3(static_cast<uint32_t>((threads + 255) / 256)), dim3(256), 0, S(), p->blocks,
+                           static_cast<const float4*>(x), static_cast<uint32_t*>(values), static_cast<float*>(scales));
+        return vkml::abi::check_launch("quantize");
+    }
+    ProfileScope prof("quantize");
+    hipLaunchKernelGGL(k_quantize, dim3(blocks_for(p->blocks)), dim3(256), 0, S(), *p, x, static_cast<uint32_t*>(values), scales);
+    return vkml::abi::check_launch("quantize");
+}
+
+int vkml_dequantize(const vkml_dequantize_params* p, const void* values, const void* scales, float* out) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "dequantize: null params");
+    VKML_CHECK_ARG(p->quant >= VKML_Q8_0 && p->quant <= VKML_Q4_K, "dequantize: not a quantized format");
+    VKML_CHECK_ARG(p->cols > 0 && p->count % p->cols == 0 && p->cols % (p->quant == VKML_Q4_K ? 256 : 32) == 0,
+                   "dequantize: rows must be whole blocks");
+    if (p->count == 0) return VKML_OK;
+    VKML_CHECK_ARG(values && scales && out, "dequantize: null buffer");
+    ProfileScope prof("dequantize");
+    hipLaunchKernelGGL(k_dequantize, dim3(blocks_for(p->count)), dim3(256), 0, S(), *p, values, scales, out);
+    return vkml::abi::check_launch("dequantize");
+}
+
+int vkml_rms_norm(const vkml_rms_norm_params* p, const float* x, const float* w, float* out) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "rms_norm: null params");
+    if (p->rows == 0 || p->cols == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && w && out, "rms_norm: null buffer");
+    ProfileScope prof("rms_norm");
+    hipLaunchKernelGGL(k_rms_norm, dim3(std::min<uint32_t>(p->rows, 65535)), dim3(256), 0, S(), *p, x, w, out);
+    return vkml::abi::check_launch("rms_norm");
+}
+
+int vkml_rms_norm_quantize(const vkml_rms_norm_params* p, const float* x, const float* w, float* out, void* values,
+                           float* scales) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "rms_norm_quantize: null params");
+    VKML_CHECK_ARG(p->cols % 32 == 0, "rms_norm_quantize: columns must be a multiple of 32, got " + std::to_string(p->cols));
+    VKML_CHECK_ARG(p->rows <= 65535, "rms_norm_quantize: too many rows");
+    if (p->rows == 0 || p->cols == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && w && values && scales, "rms_norm_quantize: null buffer");
+    ProfileScope prof("rms_norm_quantize");
+    const uint32_t threads = std::min<uint32_t>(1024, std::max<uint32_t>(64, (p->cols / 4 + 63) / 64 * 64));
+    hipLaunchKernelGGL(k_rms_norm_quantize, dim3(p->rows), dim3(threads), 0, S(), *p, reinterpret_cast<const float4*>(x),
+                       reinterpret_cast<const float4*>(w), reinterpret_cast<float4*>(out), static_cast<uint32_t*>(values), scales);
+    return vkml::abi::check_launch("rms_norm_quantize");
+}
+
+int vkml_softmax(const vkml_softmax_params* p, const float* x, float* out) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "softmax: null params");
+    VKML_CHECK_ARG(!p->causal || p->q_len > 0, "softmax: causal rows need q_len");
+    if (p->rows == 0 || p->cols == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && out, "softmax: null buffer");
+    ProfileScope prof("softmax");
+    hipLaunchKernelGGL(k_softmax, dim3(std::min<uint32_t>(p->rows, 65535)), dim3(256), 0, S(), *p, x, out);
+    return vkml::abi::check_launch("softmax");
+}
+
+int vkml_argmax(uint32_t rows, uint32_t cols, const float* x, int32_t* out) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(cols > 0 || rows == 0, "argmax: the last dimension is empty");
+    if (rows == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && out, "argmax: null buffer");
+    ProfileScope prof("argmax");
+    hipLaunchKernelGGL(k_argmax, dim3(std::min<uint32_t>(rows, 65535)), dim3(1024), 0, S(), rows, cols, x, out);
+    return vkml::abi::check_launch("argmax");
+}
+
+int vkml_rope(const vkml_rope_params* p, const float* x, const float* table, float* out) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "rope: null params");
+    VKML_CHECK_ARG(p->half_dim > 0 && 2 * p->half_dim <= p->dim && p->heads > 0 && p->seq > 0, "rope: bad shape");
+    const uint64_t total = static_cast<uint64_t>(p->pairs) + p->copies;
+    if (total == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && table && out, "rope: null buffer");
+    ProfileScope prof("rope");
+    hipLaunchKernelGGL(k_rope, dim3(blocks_for(total)), dim3(256), 0, S(), *p, x, table, out);
+    return vkml::abi::check_launch("rope");
+}
+
+int vkml_rope_kv_append(const vkml_rope_kv_params* p, const float* qkv, const float* table, float* q, void* k_cache,
+                        void* v_cache, const vkml_decode_state* state) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "rope_kv_append: null params");
+    VKML_CHECK_ARG(p->head_dim % 2 == 0 && p->kv_heads > 0 && p->heads % p->kv_heads == 0 && p->capacity > 0,
+                   "rope_kv_append: bad head layout");
+    VKML_CHECK_ARG(p->kv_type == VKML_F16 || p->kv_type == VKML_F32, "rope_kv_append: caches must be f16 or f32");
+    VKML_CHECK_ARG(qkv && q && k_cache && v_cache && (table || !p->rotate), "rope_kv_append: null buffer");
+    const uint32_t n = (p->heads + 2 * p->kv_heads) * (p->head_dim / 2);
+    ProfileScope prof("rope_kv_append");
+    hipLaunchKernelGGL(k_rope_kv_append, dim3((n + 255) / 256), dim3(256), 0, S(), *p, qkv, table, q, k_cache, v_cache, state);
+    return vkml::abi::check_launch("rope_kv_append");
+}
+
+int vkml_cast(uint32_t count, uint32_t src, uint32_t dst, const void* x, void* out) {
+    VKML_REQUIRE_INIT();
+    const bool ok = (dst == VKML_F32 && src <= VKML_BF16) || (src == VKML_F32 && (dst == VKML_F16 || dst == VKML_BF16));
+    VKML_CHECK_ARG(ok, "cast: from " + std::to_string(src) + " to " + std::to_string(dst) + " is not implemented");
+    if (count == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && out, "cast: null buffer");
+    ProfileScope prof("cast");
+    hipLaunchKernelGGL(k_cast, dim3(blocks_for(count)), dim3(256), 0, S(), count, src, dst, x, out);
+    return vkml::abi::check_launch("cast");
+}
+
+int vkml_copy_rows(const vkml_copy_rows_params* p, const void* src, void* dst) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "copy_rows: null params");
+    if (p->count == 0) return VKML_OK;
+    VKML_CHECK_ARG(src && dst && p->block > 0, "copy_rows: null buffer");
+    ProfileScope prof("write_rows");
+    hipLaunchKernelGGL(k_copy_rows, dim3(blocks_for(p->count)), dim3(256), 0, S(), *p, static_cast<const uint32_t*>(src),
+                       static_cast<uint32_t*>(dst));
+    return vkml::abi::check_launch("copy_rows");
+}
+
+int vkml_permute(const vkml_permute_params* p, const void* x, void* out) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p && p->rank >= 1 && p->rank <= 6, "permute: rank must be 1 to 6");
+    uint32_t seen = 0;
+    for (uint32_t d = 0; d < p->rank; ++d) {
+        VKML_CHECK_ARG(p->dims[d] < p->rank && !(seen & (1u << p->dims[d])), "permute: dims must be a permutation");
+        seen |= 1u << p->dims[d];
+    }
+    if (p->count == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && out, "permute: null buffer");
+    ProfileScope prof("permute");
+    hipLaunchKernelGGL(k_permute, dim3(blocks_for(p->count)), dim3(256), 0, S(), *p, static_cast<const uint32_t*>(x),
+                       static_cast<uint32_t*>(out));
+    return vkml::abi::check_launch("permute");
+}
+
+int vkml_binary(uint32_t op, uint32_t count, uint32_t b_count, const float* a, const float* b, float* out) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(op <= 3, "binary: unknown op");
+    if (count == 0) return VKML_OK;
+    VKML_CHECK_ARG(b_count > 0 && a && b && out, "binary: null buffer");
+    ProfileScope prof("binary");
+    hipLaunchKernelGGL(k_binary, dim3(blocks_for(count)), dim3(256), 0, S(), op, count, b_count, a, b, out);
+    return vkml::abi::check_launch("binary");
+}
+
+int vkml_unary(uint32_t op, uint32_t count, float param, const float* x, float* out) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(op <= 2, "unary: unknown op");
+    VKML_CHECK_ARG(op != 2 || param > 0.0f, "softcap: the cap must be positive");
+    if (count == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && out, "unary: null buffer");
+    ProfileScope prof("unary");
+    hipLaunchKernelGGL(k_unary, dim3(blocks_for(count)), dim3(256), 0, S(), op, count, param, x, out);
+    return vkml::abi::check_launch("unary");
+}
+
+static int embedding_checks(const vkml_embedding_params* p) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "embedding: null params");
+    VKML_CHECK_ARG(p->table_type <= VKML_Q4_K, "embedding: unknown table type");
+    VKML_CHECK_ARG(p->dim > 0 && p->count % p->dim == 0, "embedding: count must be whole rows");
+    if (p->table_type >= VKML_Q8_0)
+        VKML_CHECK_ARG(p->dim % (p->table_type == VKML_Q4_K ? 256 : 32) == 0, "embedding: rows must be whole blocks");
+    return VKML_OK;
+}
+
+int vkml_embedding(const vkml_embedding_params* p, const void* values, const void* scales, const int32_t* ids, float* out) {
+    if (int r = embedding_checks(p)) return r;
+    if (p->count == 0) return VKML_OK;
+    VKML_CHECK_ARG(values && ids && out && (p->table_type < VKML_Q8_0 || scales), "embedding: null buffer");
+    ProfileScope prof("embedding");
+    hipLaunchKernelGGL(k_embedding, dim3(blocks_for(p->count)), dim3(256), 0, S(), *p, values, scales, ids,
+                       static_cast<const vkml_decode_state*>(nullptr), out);
+    return vkml::abi::check_launch("embedding");
+}
+
+int vkml_embedding_state(const vkml_embedding_params* p, const void* values, const void* scales, const vkml_decode_state* state,
+                         float* out) {
+    if (int r = embedding_checks(p)) return r;
+    VKML_CHECK_ARG(p->count == p->dim, "embedding_state: one row");
+    VKML_CHECK_ARG(values && state && out && (p->table_type < VKML_Q8_0 || scales), "embedding_state: null buffer");
+    ProfileScope prof("embedding");
+    hipLaunchKernelGGL(k_embedding, dim3(blocks_for(p->count)), dim3(256), 0, S(), *p, values, scales,
+                       static_cast<const int32_t*>(nullptr), state, out);
+    return vkml::abi::check_launch("embedding_state");
+}
+
+int vkml_state_set(vkml_decode_state* state, int32_t token, int32_t position, int32_t steps) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(state, "state_set: null state");
+    ProfileScope prof("state_set");
+    hipLaunchKernelGGL(k_state_set, dim3(1), dim3(1), 0, S(), state, token, position, steps);
+    return vkml::abi::check_launch("state_set");
+}
+
+int vkml_step_finish(uint32_t vocab, const float* logits, vkml_decode_state* state, int32_t* log, uint32_t cap) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(state, "step_finish: null state");
+    VKML_CHECK_ARG(!logits || vocab > 0, "step_finish: empty vocabulary");
+    ProfileScope prof(logits ? "argmax" : "step_finish");
+    hipLaunchKernelGGL(k_step_finish, dim3(1), dim3(1024), 0, S(), vocab, logits, state, log, cap);
+    return vkml::abi::check_launch("step_finish");
+}
+
+int vkml_matmul(const vkml_matmul_params* p, const float* a, const void* b, float* c) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "matmul: null params");
+    VKML_CHECK_ARG(p->b_type <= VKML_BF16, "matmul: b must be f32, f16 or bf16");
+    VKML_CHECK_ARG(p->b_group >= 1 && p->batches >= 1, "matmul: bad batching");
+    if (p->m == 0 || p->n == 0) return VKML_OK;
+    VKML_CHECK_ARG(a && b && c, "matmul: null buffer");
+    const dim3 grid((p->n + 15) / 16, (p->m + 15) / 16, p->batches);
+    ProfileScope prof("matmul");
+    if (p->b_transposed) hipLaunchKernelGGL(k_matmul<true>, grid, dim3(16, 16), 0, S(), *p, a, b, c);
+    else hipLaunchKernelGGL(k_matmul<false>, grid, dim3(16, 16), 0, S(), *p, a, b, c);
+    return vkml::abi::check_launch("matmul");
+}
+
+}  // extern "C"

@@ -1,0 +1,179 @@
+"""ctypes binding of libvkml.so's C API (include/vkml_llama.h): vkml::Llama
+from Python. Raises when the in-tree library is missing."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from .hip import LIB_DIR
+
+LIB_PATH = os.path.join(LIB_DIR, "libvkml.so")
+
+i32, i64, u32, u64, vp = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_void_p
+
+
+class Options(C.Structure):
+    _fields_ = [("kv_cache_f16", i32), ("quantize", i32), ("integer_dot", i32), ("use_graphs", i32),
+                ("attention_splits", i32), ("device_name", C.c_char_p)]
+
+
+class Config(C.Structure):
+    _fields_ = [(n, i64) for n in ("vocab_size", "hidden_size", "intermediate_size", "num_layers", "num_heads",
+                                   "num_kv_heads", "head_dim", "max_positions")] + \
+               [("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("tie_word_embeddings", i32), ("rope_interleaved", i32)]
+
+
+P = C.POINTER
+SIGNATURES = {
+    "vkml_llama_default_options": (None, [P(Options)]),
+    "vkml_llama_load": (C.c_int, [C.c_char_p, i64, P(Options), P(vp)]),
+    "vkml_llama_free": (None, [vp]),
+    "vkml_llama_shutdown": (C.c_int, []),
+    "vkml_llama_get_config": (C.c_int, [vp, P(Config)]),
+    "vkml_llama_context_length": (i64, [vp]),
+    "vkml_llama_position": (i64, [vp]),
+    "vkml_llama_kv_cache_bytes": (i64, [vp]),
+    "vkml_llama_forward": (C.c_int, [vp, vp, i64, vp]),
+    "vkml_llama_forward_all": (C.c_int, [vp, vp, i64, vp]),
+    "vkml_llama_generate_greedy": (C.c_int, [vp, i32, i64, vp]),
+    "vkml_llama_reset": (C.c_int, [vp]),
+    "vkml_llama_rewind": (C.c_int, [vp, i64, P(i64)]),
+    "vkml_llama_read_kv_cache": (C.c_int, [vp, i64, vp, vp, u64]),
+    "vkml_llama_set_profiling": (C.c_int, [i32]),
+    "vkml_llama_profile": (C.c_int, [vp, u32, vp, vp, u32, P(u32)]),
+    "vkml_llama_reset_profile": (C.c_int, []),
+    "vkml_llama_synchronize": (C.c_int, []),
+}
+
+_lib = None
+
+
+class VkmlError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise VkmlError(f"{LIB_PATH} is missing: build it (python -c 'import __graft_entry__ as g; g.build()')")
+        _lib = C.CDLL(LIB_PATH)
+        _lib.vkml_llama_last_error.restype = C.c_char_p
+        _lib.vkml_llama_last_error.argtypes = []
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise VkmlError(lib().vkml_llama_last_error().decode())
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(vp)
+
+
+class Llama:
+    def __init__(self, path: str, context: int, kv_f16: bool = False, quantize: int = -1, integer_dot: bool = True,
+                 use_graphs: bool = True, attention_splits: int = 0):
+        o = Options()
+        lib().vkml_llama_default_options(C.byref(o))
+        o.kv_cache_f16, o.quantize, o.integer_dot = int(kv_f16), int(quantize), int(integer_dot)
+        o.use_graphs, o.attention_splits = int(use_graphs), int(attention_splits)
+        self._h = vp()
+        _check(lib().vkml_llama_load(path.encode(), int(context), C.byref(o), C.byref(self._h)))
+        cfg = Config()
+        _check(lib().vkml_llama_get_config(self._h, C.byref(cfg)))
+        self.config = {f: getattr(cfg, f) for f, _ in Config._fields_}
+        self.vocab = int(cfg.vocab_size)
+        self.kv_f16 = kv_f16
+
+    def forward(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(self.vocab, np.float32)
+        _check(lib().vkml_llama_forward(self._h, _ptr(t), t.size, _ptr(out)))
+        return out
+
+    def forward_all(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((t.size, self.vocab), np.float32)
+        _check(lib().vkml_llama_forward_all(self._h, _ptr(t), t.size, _ptr(out)))
+        return out
+
+    def generate_greedy(self, first: int, count: int) -> np.ndarray:
+        out = np.empty(max(int(count), 0), np.int32)
+        _check(lib().vkml_llama_generate_greedy(self._h, int(first), int(count), _ptr(out)))
+        return out
+
+    @property
+    def position(self) -> int:
+        return int(lib().vkml_llama_position(self._h))
+
+    @property
+    def context_length(self) -> int:
+        return int(lib().vkml_llama_context_length(self._h))
+
+    @property
+    def kv_cache_bytes(self) -> int:
+        return int(lib().vkml_llama_kv_cache_bytes(self._h))
+
+    def reset(self) -> None:
+        _check(lib().vkml_llama_reset(self._h))
+
+    def rewind(self, position: int) -> int:
+        out = i64()
+        _check(lib().vkml_llama_rewind(self._h, int(position), C.byref(out)))
+        return int(out.value)
+
+    def read_kv_cache(self, layer: int):
+        c = self.config
+        shape = (c["num_kv_heads"], self.context_length, c["head_dim"])
+        dt = np.uint16 if self.kv_f16 else np.float32
+        k, v = np.empty(shape, dt), np.empty(shape, dt)
+        _check(lib().vkml_llama_read_kv_cache(self._h, int(layer), _ptr(k), _ptr(v), k.nbytes))
+        return k, v
+
+    def close(self) -> None:
+        if self._h:
+            lib().vkml_llama_free(self._h)
+            self._h = vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def set_profiling(on: bool) -> None:
+    _check(lib().vkml_llama_set_profiling(int(on)))
+
+
+def reset_profile() -> None:
+    _check(lib().vkml_llama_reset_profile())
+
+
+def synchronize() -> None:
+    _check(lib().vkml_llama_synchronize())
+
+
+def profile() -> list[tuple[str, int, float]]:
+    count = u32()
+    _check(lib().vkml_llama_profile(None, 0, None, None, 0, C.byref(count)))
+    n = count.value
+    stride = 64
+    names = C.create_string_buffer(stride * max(n, 1))
+    calls = np.zeros(max(n, 1), np.uint64)
+    ms = np.zeros(max(n, 1), np.float64)
+    _check(lib().vkml_llama_profile(names, stride, _ptr(calls), _ptr(ms), n, C.byref(count)))
+    raw = names.raw
+    return [(raw[i * stride:(i + 1) * stride].split(b"\0")[0].decode(), int(calls[i]), float(ms[i])) for i in range(n)]
+
+
+def shutdown() -> None:
+    _check(lib().vkml_llama_shutdown())

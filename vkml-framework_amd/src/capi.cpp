@@ -1,0 +1,185 @@
+// capi.cpp -- the C entry points of include/vkml_llama.h over vkml::Llama.
+#include <cstring>
+#include <memory>
+#include <string>
+
+#include "runtime.hpp"
+#include "vkml/llama.hpp"
+#include "vkml_llama.h"
+
+struct vkml_llama {
+    vkml::Llama model;
+};
+
+namespace {
+
+thread_local std::string g_error;
+std::unique_ptr<vkml::Context> g_context;
+int g_models = 0;
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return 1;
+    }
+}
+
+vkml::Context& context(const vkml_llama_options& o) {
+    if (!g_context) {
+        vkml::ContextOptions co;
+        co.device_name = o.device_name ? o.device_name : "";
+        g_context = std::make_unique<vkml::Context>(co);
+    }
+    return *g_context;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* vkml_llama_last_error(void) { return g_error.c_str(); }
+
+void vkml_llama_default_options(vkml_llama_options* out) {
+    if (!out) return;
+    *out = vkml_llama_options{0, -1, 1, 1, 0, nullptr};
+}
+
+int vkml_llama_load(const char* path, int64_t context_length, const vkml_llama_options* options, vkml_llama** out) {
+    return guarded([&] {
+        if (!path || !out) throw vkml::Error("vkml_llama_load: null argument");
+        vkml_llama_options o;
+        vkml_llama_default_options(&o);
+        if (options) o = *options;
+        vkml::LlamaOptions lo;
+        lo.kv_cache = o.kv_cache_f16 ? vkml::DType::F16 : vkml::DType::F32;
+        if (o.quantize >= 0) {
+            if (o.quantize > 2) throw vkml::Error("vkml_llama_load: quantize must be -1, 0 (q8_0), 1 (q4_0) or 2 (q4_1)");
+            lo.quantize = static_cast<vkml::QuantType>(o.quantize);
+        }
+        lo.use_graphs = o.use_graphs != 0;
+        lo.attention_splits = o.attention_splits;
+        lo.integer_dot_product = o.integer_dot != 0;
+        vkml::Context& ctx = context(o);
+        *out = new vkml_llama{vkml::Llama::load(ctx, path, context_length, lo)};
+        ++g_models;
+    });
+}
+
+void vkml_llama_free(vkml_llama* model) {
+    if (!model) return;
+    delete model;
+    --g_models;
+}
+
+int vkml_llama_shutdown(void) {
+    return guarded([] {
+        if (g_models > 0) throw vkml::Error("vkml_llama_shutdown: " + std::to_string(g_models) + " models are still alive");
+        g_context.reset();
+    });
+}
+
+int vkml_llama_get_config(const vkml_llama* m, vkml_llama_config* out) {
+    return guarded([&] {
+        if (!m || !out) throw vkml::Error("vkml_llama_get_config: null argument");
+        const vkml::LlamaConfig& c = m->model.config();
+        *out = vkml_llama_config{c.vocab_size, c.hidden_size, c.intermediate_size, c.num_layers, c.num_heads, c.num_kv_heads, c.head_dim,
+                                 c.max_positions, c.rms_norm_eps, c.rope_theta, c.tie_word_embeddings ? 1 : 0,
+                                 c.rope_style == vkml::RopeStyle::Interleaved ? 1 : 0};
+    });
+}
+
+int64_t vkml_llama_context_length(const vkml_llama* m) { return m ? m->model.context_length() : -1; }
+int64_t vkml_llama_position(const vkml_llama* m) { return m ? m->model.position() : -1; }
+int64_t vkml_llama_kv_cache_bytes(const vkml_llama* m) { return m ? m->model.kv_cache_bytes() : -1; }
+
+int vkml_llama_forward(vkml_llama* m, const int32_t* tokens, int64_t count, float* logits) {
+    return guarded([&] {
+        if (!m || (!tokens && count) || !logits) throw vkml::Error("vkml_llama_forward: null argument");
+        const std::vector<float> v = m->model.forward({tokens, static_cast<std::size_t>(count)}).to_vector<float>();
+        std::memcpy(logits, v.data(), v.size() * 4);
+    });
+}
+
+int vkml_llama_forward_all(vkml_llama* m, const int32_t* tokens, int64_t count, float* logits) {
+    return guarded([&] {
+        if (!m || (!tokens && count) || !logits) throw vkml::Error("vkml_llama_forward_all: null argument");
+        const std::vector<float> v = m->model.forward_all({tokens, static_cast<std::size_t>(count)}).to_vector<float>();
+        std::memcpy(logits, v.data(), v.size() * 4);
+    });
+}
+
+int vkml_llama_generate_greedy(vkml_llama* m, int32_t first, int64_t count, int32_t* tokens_out) {
+    return guarded([&] {
+        if (!m || (!tokens_out && count > 0)) throw vkml::Error("vkml_llama_generate_greedy: null argument");
+        const std::vector<int32_t> t = m->model.generate_greedy(first, count);
+        std::memcpy(tokens_out, t.data(), t.size() * 4);
+    });
+}
+
+int vkml_llama_reset(vkml_llama* m) {
+    return guarded([&] {
+        if (!m) throw vkml::Error("vkml_llama_reset: null model");
+        m->model.reset();
+    });
+}
+
+int vkml_llama_rewind(vkml_llama* m, int64_t position, int64_t* out) {
+    return guarded([&] {
+        if (!m) throw vkml::Error("vkml_llama_rewind: null model");
+        const int64_t p = m->model.rewind(position);
+        if (out) *out = p;
+    });
+}
+
+int vkml_llama_read_kv_cache(const vkml_llama* m, int64_t layer, void* k_out, void* v_out, uint64_t bytes) {
+    return guarded([&] {
+        if (!m) throw vkml::Error("vkml_llama_read_kv_cache: null model");
+        const vkml::Tensor& k = m->model.k_cache(layer);
+        const vkml::Tensor& v = m->model.v_cache(layer);
+        if (bytes != k.nbytes()) throw vkml::Error("vkml_llama_read_kv_cache: the caches hold " + std::to_string(k.nbytes()) + " bytes each");
+        const auto kb = k.to_bytes(), vb = v.to_bytes();
+        if (k_out) std::memcpy(k_out, kb.data(), kb.size());
+        if (v_out) std::memcpy(v_out, vb.data(), vb.size());
+    });
+}
+
+int vkml_llama_set_profiling(int32_t enabled) {
+    return guarded([&] {
+        if (!g_context) throw vkml::Error("vkml_llama_set_profiling: no context (load a model first)");
+        g_context->set_profiling(enabled != 0);
+    });
+}
+
+int vkml_llama_profile(char* names, uint32_t stride, uint64_t* calls, double* ms, uint32_t capacity, uint32_t* count) {
+    return guarded([&] {
+        if (!g_context) throw vkml::Error("vkml_llama_profile: no context (load a model first)");
+        const auto rows = g_context->profile();
+        if (count) *count = static_cast<uint32_t>(rows.size());
+        for (uint32_t i = 0; i < capacity && i < rows.size(); ++i) {
+            if (names && stride) {
+                std::strncpy(names + std::size_t(i) * stride, rows[i].name.c_str(), stride - 1);
+                names[std::size_t(i) * stride + stride - 1] = 0;
+            }
+            if (calls) calls[i] = rows[i].calls;
+            if (ms) ms[i] = rows[i].milliseconds;
+        }
+    });
+}
+
+int vkml_llama_reset_profile(void) {
+    return guarded([] {
+        if (g_context) g_context->reset_profile();
+    });
+}
+
+int vkml_llama_synchronize(void) {
+    return guarded([] {
+        if (g_context) g_context->synchronize();
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,638 @@
+// llama.cpp -- the Llama model on the MI355X: GGUF loading and the token
+// loop (the reference's src/models/llama.cpp:140-406, weights.cpp:26-159 and
+// config.cpp:14-140).
+//
+// The reference records ~29 dispatches per layer, each separated by a full
+// barrier. Here one decode step (t = 1) is nine kernels per layer, all
+// reading the step's token and position from a small device-side state:
+//   rms_norm + Q8_0 quantize -> q|k|v GEMV (one fused matrix) -> rope + f16
+//   cast + KV append -> split-K attention -> merge + Q8_0 quantize ->
+//   o GEMV + residual -> rms_norm + quantize -> gate|up GEMV + SwiGLU ->
+//   quantize -> down GEMV + residual,
+// then the final norm, the lm_head GEMV and (greedy) an argmax that writes
+// the next token into the state. The step is captured once as a HIP graph
+// and replayed, so a prompt or a greedy generation is a stream of graph
+// launches with no host round trip between tokens. Prompts run one token per
+// step through the same graph; the arithmetic per token is the reference's
+// (activations quantized per row, so one row at a time is the same sum).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+
+#include "gguf.hpp"
+#include "runtime.hpp"
+#include "vkml/llama.hpp"
+
+namespace vkml {
+
+using detail::check;
+using detail::Gguf;
+using detail::TensorAccess;
+
+namespace {
+
+std::uint32_t u32(std::int64_t v) { return static_cast<std::uint32_t>(v); }
+
+// A loaded weight matrix: float as stored, or quantized.
+struct Weight {
+    bool quantized = false;
+    Tensor t;           // float: f32, f16 or bf16 [rows, cols]
+    QuantizedMatrix q;  // quantized
+    std::int64_t rows = 0, cols = 0;
+
+    std::uint32_t type_code() const {
+        if (!quantized) return detail::type_code(t.dtype());
+        switch (q.type) {
+            case QuantType::q8_0: return VKML_Q8_0;
+            case QuantType::q4_0: return VKML_Q4_0;
+            case QuantType::q4_1: return VKML_Q4_1;
+            case QuantType::q4_K: return VKML_Q4_K;
+        }
+        return VKML_Q8_0;
+    }
+    std::uint32_t scale_code() const { return q.type == QuantType::q4_K ? std::uint32_t(VKML_F16) : detail::type_code(q.scales.dtype()); }
+    const void* values() const { return quantized ? q.values.data() : t.data(); }
+    const void* scales() const { return quantized ? q.scales.data() : nullptr; }
+    bool int_dot_ok() const { return quantized && cols % (q.type == QuantType::q4_K ? 256 : 64) == 0 && cols <= 32768; }
+};
+
+// Host-side form of a matrix before upload: bytes of values and scales.
+struct HostMatrix {
+    bool quantized = false;
+    QuantType type = QuantType::q8_0;
+    DType dtype = DType::F32;  // float matrices
+    std::vector<std::uint8_t> values, scales;
+    std::int64_t rows = 0, cols = 0;
+};
+
+// gguf.cpp:525-638 (load_quantized) and 503-523 (load_q8): a file's matrix
+// in QuantizedMatrix's layout. q4_K keeps its super-blocks, split into code
+// bytes and 16-byte headers.
+HostMatrix host_matrix(const Gguf& file, const std::string& name, std::int64_t rows, std::int64_t cols) {
+    const Gguf::Entry& e = file.entry(name);
+    if (e.shape != Shape{rows, cols}) {
+        throw Error("Llama: weight " + name + " is " + to_string(e.shape) + ", but the config needs " + to_string(Shape{rows, cols}));
+    }
+    const std::vector<std::uint8_t> data = file.read(name);
+    HostMatrix m;
+    m.rows = rows;
+    m.cols = cols;
+    const std::size_t count = std::size_t(rows * cols);
+    if (e.type == detail::kGgmlF32 || e.type == detail::kGgmlF16 || e.type == detail::kGgmlBF16) {
+        m.dtype = e.type == detail::kGgmlF32 ? DType::F32 : e.type == detail::kGgmlF16 ? DType::F16 : DType::BF16;
+        m.values = data;
+        return m;
+    }
+    m.quantized = true;
+    const std::size_t groups = count / 32;
+    const auto pack = [](std::uint8_t* out, const std::uint8_t codes[32]) {
+        for (int w = 0; w < 4; ++w)
+            for (int k = 0; k < 4; ++k) out[4 * w + k] = std::uint8_t(codes[8 * w + k] | (codes[8 * w + k + 4] << 4));
+    };
+    switch (e.type) {
+        case detail::kGgmlQ8_0:
+        case detail::kGgmlQ4_0:
+        case detail::kGgmlQ4_1: {
+            if (cols % 32) throw Error("gguf: tensor \"" + name + "\" of shape " + to_string(e.shape) + " is not a matrix of whole blocks");
+            const bool q8 = e.type == detail::kGgmlQ8_0, offset = e.type == detail::kGgmlQ4_1;
+            const std::size_t bsize = q8 ? 34 : offset ? 20 : 18;
+            m.type = q8 ? QuantType::q8_0 : offset ? QuantType::q4_1 : QuantType::q4_0;
+            m.values.resize(groups * (q8 ? 32 : 16));
+            m.scales.resize(groups * 2 * (offset ? 2 : 1));
+            auto* halves = reinterpret_cast<std::uint16_t*>(m.scales.data());
+            detail::parallel_for(groups, [&](std::size_t begin, std::size_t end) {
+                for (std::size_t b = begin; b < end; ++b) {
+                    const std::uint8_t* block = data.data() + b * bsize;
+                    if (offset) {
+                        std::memcpy(&halves[2 * b], block, 4);
+                    } else {
+                        std::memcpy(&halves[b], block, 2);
+                    }
+                    if (q8) {
+                        std::memcpy(&m.values[b * 32], block + 2, 32);
+                    } else {
+                        const std::uint8_t* qs = block + (offset ? 4 : 2);
+                        std::uint8_t codes[32];
+                        for (int j = 0; j < 16; ++j) {
+                            codes[j] = qs[j] & 0x0F;
+                            codes[j + 16] = qs[j] >> 4;
+                        }
+                        pack(&m.values[b * 16], codes);
+                    }
+                }
+            });
+            return m;
+        }
+        case detail::kGgmlQ4_K: {
+            if (cols % 256) throw Error("gguf: tensor \"" + name + "\" of shape " + to_string(e.shape) + " is not a matrix of whole blocks");
+            m.type = QuantType::q4_K;
+            const std::size_t blocks = count / 256;
+            m.values.resize(blocks * 128);
+            m.scales.resize(blocks * 16);
+            detail::parallel_for(blocks, [&](std::size_t begin, std::size_t end) {
+                for (std::size_t b = begin; b < end; ++b) {
+                    std::memcpy(&m.scales[b * 16], data.data() + b * 144, 16);
+                    std::memcpy(&m.values[b * 128], data.data() + b * 144 + 16, 128);
+                }
+            });
+            return m;
+        }
+        default: {
+            // q6_K and the other k-quants: decoded and requantized to Q8_0
+            // on the host, finer than any of them (weights.cpp:146-148).
+            if (cols % 32) throw Error("gguf: tensor \"" + name + "\" of shape " + to_string(e.shape) + " is not a matrix of whole Q8_0 blocks");
+            m.type = QuantType::q8_0;
+            m.values.resize(count);
+            m.scales.resize(groups * 2);
+            detail::requantize_q8(e.type, data.data(), rows, cols, reinterpret_cast<std::uint32_t*>(m.values.data()),
+                                  reinterpret_cast<std::uint16_t*>(m.scales.data()));
+            return m;
+        }
+    }
+}
+
+Weight upload(Context& context, const HostMatrix& h) {
+    Weight w;
+    w.rows = h.rows;
+    w.cols = h.cols;
+    w.quantized = h.quantized;
+    if (!h.quantized) {
+        w.t = Tensor::from_bytes(context, std::as_bytes(std::span{h.values}), {h.rows, h.cols}, h.dtype);
+        return w;
+    }
+    const std::int64_t per_word = h.type == QuantType::q8_0 ? 4 : 8;
+    w.q.rows = h.rows;
+    w.q.cols = h.cols;
+    w.q.type = h.type;
+    w.q.values = Tensor::from_bytes(context, std::as_bytes(std::span{h.values}), {h.rows, h.cols / per_word}, DType::I32);
+    if (h.type == QuantType::q4_K) {
+        w.q.scales = Tensor::from_bytes(context, std::as_bytes(std::span{h.scales}), {h.rows, h.cols / 256, 4}, DType::I32);
+    } else {
+        const Shape ss = h.type == QuantType::q4_1 ? Shape{h.rows, h.cols / 32, 2} : Shape{h.rows, h.cols / 32};
+        w.q.scales = Tensor::from_bytes(context, std::as_bytes(std::span{h.scales}), ss, DType::F16);
+    }
+    return w;
+}
+
+// Rows of a, then rows of b (same format): one matrix for one launch.
+HostMatrix stack_rows(std::vector<HostMatrix> parts) {
+    HostMatrix out = std::move(parts[0]);
+    for (std::size_t i = 1; i < parts.size(); ++i) {
+        out.values.insert(out.values.end(), parts[i].values.begin(), parts[i].values.end());
+        out.scales.insert(out.scales.end(), parts[i].scales.begin(), parts[i].scales.end());
+        out.rows += parts[i].rows;
+    }
+    return out;
+}
+
+bool same_format(const HostMatrix& a, const HostMatrix& b) {
+    return a.quantized == b.quantized && a.cols == b.cols && (a.quantized ? a.type == b.type : a.dtype == b.dtype);
+}
+
+std::vector<float> read_vector(const Gguf& file, const std::string& name, std::int64_t size) {
+    const Gguf::Entry& e = file.entry(name);
+    if (e.shape != Shape{size}) {
+        throw Error("Llama: weight " + name + " is " + to_string(e.shape) + ", but the config needs " + to_string(Shape{size}));
+    }
+    const std::vector<std::uint8_t> data = file.read(name);
+    std::vector<float> out(static_cast<std::size_t>(size));
+    for (std::size_t i = 0; i < out.size(); ++i) {
+        if (e.type == detail::kGgmlF32) {
+            std::memcpy(&out[i], &data[4 * i], 4);
+        } else if (e.type == detail::kGgmlF16 || e.type == detail::kGgmlBF16) {
+            std::uint16_t h;
+            std::memcpy(&h, &data[2 * i], 2);
+            if (e.type == detail::kGgmlF16) {
+                out[i] = detail::f16_to_float(h);
+            } else {
+                const std::uint32_t bits = std::uint32_t(h) << 16;
+                std::memcpy(&out[i], &bits, 4);
+            }
+        } else {
+            throw Error("Llama: vector " + name + " is " + file.type_name(name) + ", not a float type");
+        }
+    }
+    return out;
+}
+
+const LlamaConfig& validated(const LlamaConfig& c, std::int64_t context_length) {
+    const bool positive = c.vocab_size > 0 && c.hidden_size > 0 && c.intermediate_size > 0 && c.num_layers > 0 && c.num_heads > 0 &&
+                          c.num_kv_heads > 0 && c.head_dim > 0 && c.max_positions > 0;
+    if (!positive || c.num_heads % c.num_kv_heads != 0 || c.head_dim % 2 != 0) {
+        throw Error("Llama: config needs positive sizes, num_heads a multiple of num_kv_heads, and an even head_dim");
+    }
+    if (context_length < 1 || context_length > c.max_positions) {
+        throw Error("Llama: context length " + std::to_string(context_length) + " must be between 1 and max_position_embeddings (" +
+                    std::to_string(c.max_positions) + ")");
+    }
+    const std::int64_t group = c.num_heads / c.num_kv_heads;
+    if ((c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) || (group != 1 && group != 2 && group != 4 && group != 8)) {
+        throw Error("Llama: head_dim " + std::to_string(c.head_dim) + " with " + std::to_string(group) +
+                    " query heads per KV head is not implemented (head_dim 64, 128 or 256; 1, 2, 4 or 8 heads per KV head are)");
+    }
+    if (c.sliding_window || c.qkv_bias || c.o_bias || c.qk_norm || c.sandwich_norms || !c.pre_norms || c.embedding_scale != 1.0f ||
+        c.residual_scale != 1.0f || c.logit_divisor != 1.0f || c.attn_logit_softcap != 0.0f || c.final_logit_softcap != 0.0f ||
+        c.activation != Activation::silu || c.rotary_dim != 0 || c.norm_weight_offset != 0.0f || !c.rope_layers.empty() ||
+        c.query_pre_attn_scalar) {
+        throw Error("Llama: this config uses features of another model family, which this build does not implement");
+    }
+    return c;
+}
+
+}  // namespace
+
+// config.cpp:14-140, for the architectures this build runs.
+LlamaConfig LlamaConfig::from_gguf(const std::filesystem::path& path) {
+    const Gguf file{path};
+    const std::string where = "Llama: " + path.string();
+    const std::string arch = file.string("general.architecture", "?");
+    if (arch != "llama") {
+        throw Error(where + " is a " + arch + " model, which vkml does not implement in this build (llama is)");
+    }
+    const auto key = [&](const std::string& k) { return arch + "." + k; };
+    const auto need = [&](const std::string& k) -> std::int64_t {
+        if (!file.has(key(k))) throw Error(where + " has no " + key(k));
+        return static_cast<std::int64_t>(file.number(key(k), 0));
+    };
+    LlamaConfig c;
+    const std::string scaling = file.string(key("rope.scaling.type"), "none");
+    if (scaling == "linear") {
+        c.rope_linear_factor = static_cast<float>(file.number(key("rope.scaling.factor"), 1.0));
+    } else if (scaling != "none") {
+        throw Error(where + " scales rope (" + scaling + "), which vkml does not implement for GGUF files (linear it does)");
+    }
+    c.hidden_size = need("embedding_length");
+    c.intermediate_size = need("feed_forward_length");
+    c.num_layers = need("block_count");
+    c.num_heads = need("attention.head_count");
+    c.num_kv_heads = static_cast<std::int64_t>(file.number(key("attention.head_count_kv"), double(c.num_heads)));
+    c.head_dim = static_cast<std::int64_t>(file.number(key("attention.key_length"), c.num_heads > 0 ? double(c.hidden_size / c.num_heads) : 0.0));
+    c.max_positions = need("context_length");
+    c.rms_norm_eps = static_cast<float>(file.number(key("attention.layer_norm_rms_epsilon"), c.rms_norm_eps));
+    c.rope_theta = static_cast<float>(file.number(key("rope.freq_base"), c.rope_theta));
+    if (!file.contains("token_embd.weight")) throw Error(where + " has no token_embd.weight");
+    c.vocab_size = file.shape("token_embd.weight").at(0);
+    c.tie_word_embeddings = !file.contains("output.weight");
+    c.rope_style = RopeStyle::Interleaved;  // llama.cpp's converter reorders q and k rows for it
+    c.qkv_bias = file.contains("blk.0.attn_q.bias");
+    c.qk_norm = file.contains("blk.0.attn_q_norm.weight");
+    if (file.contains("rope_freqs.weight")) {
+        const Gguf::Entry& e = file.entry("rope_freqs.weight");
+        c.rope_freq_factors = read_vector(file, "rope_freqs.weight", e.shape.empty() ? 0 : e.shape[0]);
+    }
+    if (file.has("tokenizer.ggml.eos_token_id")) c.eos_token_ids = {static_cast<std::int32_t>(file.number("tokenizer.ggml.eos_token_id", 0))};
+    return c;
+}
+
+struct Llama::Impl {
+    Context* context = nullptr;
+    LlamaConfig config;
+    std::int64_t context_length = 0;
+    LlamaOptions options;
+    std::int64_t position = 0;
+    bool int_dot = true;
+
+    struct Layer {
+        Tensor attn_norm, ffn_norm;
+        std::vector<std::pair<Weight, std::int64_t>> qkv;  // fused q|k|v, or parts at row offsets
+        Weight o, gate, up, down;
+        Tensor k_cache, v_cache;
+    };
+    Weight embed;
+    std::shared_ptr<Weight> lm_head_own;  // when not tied to embed
+    bool tied = false;
+    Tensor final_norm, rope;
+    std::vector<Layer> layers;
+
+    // Decode buffers.
+    Tensor x, xn, xq, xs, qkv, q, attn, aq, as, partial, stats, h, hq, hs, gate_tmp, up_tmp, ytmp, logits, state, log;
+    std::int64_t splits = 1;
+    std::uint64_t graph_logits = 0, graph_greedy = 0;
+
+    const Weight& lm_head() const { return tied ? embed : *lm_head_own; }
+
+    ~Impl() {
+        if (graph_logits) (void)vkml_graph_destroy(graph_logits);
+        if (graph_greedy) (void)vkml_graph_destroy(graph_greedy);
+    }
+
+    void tag(const char* t) const { (void)vkml_set_profile_tag(t); }
+
+    // y = w . in (+ residual), in given as f32 (xn-like) and, for the int8
+    // path, Q8_0 (values, scales).
+    void project(const Weight& w, const Tensor& in_f32, const Tensor* in_values, const Tensor* in_scales, float* out, const float* residual,
+                 const char* t) const {
+        tag(t);
+        if (int_dot && w.int_dot_ok() && in_values) {
+            const vkml_gemv_dot_params p{1, u32(w.rows), u32(w.cols), w.type_code(), w.scale_code()};
+            if (residual) {
+                check(vkml_gemv_dot_add(&p, in_values->data(), w.values(), out, w.scales(), static_cast<const float*>(in_scales->data()), residual), t);
+            } else {
+                check(vkml_gemv_dot(&p, in_values->data(), w.values(), out, w.scales(), static_cast<const float*>(in_scales->data())), t);
+            }
+            return;
+        }
+        const vkml_gemv_params p{1, u32(w.rows), u32(w.cols), w.type_code(), w.scale_code()};
+        float* y = residual ? static_cast<float*>(ytmp.data()) : out;  // out may be the residual itself
+        check(vkml_gemv(&p, static_cast<const float*>(in_f32.data()), w.values(), y, w.scales()), t);
+        if (residual) check(vkml_binary(0, u32(w.rows), u32(w.rows), residual, y, out), t);
+    }
+
+    bool quantized_input(const Weight& w) const { return int_dot && w.int_dot_ok(); }
+
+    // One token: the state's token at the state's position.
+    void step(bool greedy) {
+        const LlamaConfig& c = config;
+        const std::int64_t d = c.hidden_size, hd = c.head_dim, ff = c.intermediate_size;
+        auto* xp = static_cast<float*>(x.data());
+        const auto* st = static_cast<const vkml_decode_state*>(state.data());
+        tag("embed");
+        const vkml_embedding_params ep{u32(d), u32(d), u32(c.vocab_size), embed.type_code(), embed.quantized ? embed.scale_code() : std::uint32_t(VKML_F16)};
+        check(vkml_embedding_state(&ep, embed.values(), embed.scales(), st, xp), "embedding");
+        const vkml_rms_norm_params np{1, u32(d), c.rms_norm_eps};
+        const bool quant_d = d % 32 == 0;
+        const auto norm = [&](const Tensor& w, const char* t) {
+            tag(t);
+            if (quant_d) {
+                check(vkml_rms_norm_quantize(&np, xp, static_cast<const float*>(w.data()), static_cast<float*>(xn.data()), xq.data(),
+                                             static_cast<float*>(xs.data())),
+                      "rms_norm");
+            } else {
+                check(vkml_rms_norm(&np, xp, static_cast<const float*>(w.data()), static_cast<float*>(xn.data())), "rms_norm");
+            }
+        };
+        const vkml_attend_params ap{0, 0, u32(context_length), u32(c.num_heads), u32(c.num_kv_heads), u32(hd),
+                                    detail::type_code(layers[0].k_cache.dtype()), u32(splits), 1.0f / std::sqrt(static_cast<float>(hd)), 0.0f};
+        for (const Layer& L : layers) {
+            norm(L.attn_norm, "attn_norm");
+            for (const auto& [w, row] : L.qkv)
+                project(w, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(qkv.data()) + row, nullptr, "qkv");
+            tag("rope_kv");
+            const vkml_rope_kv_params rp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(context_length), 0,
+                                         c.rope_style == RopeStyle::Interleaved ? 0u : 1u, detail::type_code(L.k_cache.dtype()), 1};
+            check(vkml_rope_kv_append(&rp, static_cast<const float*>(qkv.data()), static_cast<const float*>(rope.data()),
+                                      static_cast<float*>(q.data()), L.k_cache.data(), L.v_cache.data(), st),
+                  "rope_kv_append");
+            tag("attention");
+            check(vkml_attend(&ap, static_cast<const float*>(q.data()), L.k_cache.data(), L.v_cache.data(), static_cast<float*>(partial.data()),
+                              static_cast<float*>(stats.data()), st),
+                  "attention");
+            const bool o_q = quantized_input(L.o);
+            check(vkml_attend_merge(&ap, static_cast<const float*>(partial.data()), static_cast<const float*>(stats.data()),
+                                    static_cast<float*>(attn.data()), o_q ? aq.data() : nullptr, o_q ? static_cast<float*>(as.data()) : nullptr),
+                  "attention");
+            project(L.o, attn, o_q ? &aq : nullptr, &as, xp, xp, "o");
+            norm(L.ffn_norm, "ffn_norm");
+            auto* hp = static_cast<float*>(h.data());
+            if (quantized_input(L.gate) && quantized_input(L.up) && L.gate.type_code() == L.up.type_code() && quant_d) {
+                tag("gate_up");
+                const vkml_gemv_dot_params gp{1, u32(ff), u32(d), L.gate.type_code(), L.gate.scale_code()};
+                check(vkml_gemv_dot_swiglu(&gp, xq.data(), static_cast<const float*>(xs.data()), L.gate.values(), L.gate.scales(), L.up.values(),
+                                           L.up.scales(), hp),
+                      "gate_up");
+            } else {
+                project(L.gate, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(gate_tmp.data()), nullptr, "gate");
+                project(L.up, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(up_tmp.data()), nullptr, "up");
+                tag("swiglu");
+                check(vkml_unary(0, u32(ff), 0.0f, static_cast<const float*>(gate_tmp.data()), static_cast<float*>(gate_tmp.data())), "silu");
+                check(vkml_binary(2, u32(ff), u32(ff), static_cast<const float*>(gate_tmp.data()), static_cast<const float*>(up_tmp.data()), hp),
+                      "mul");
+            }
+            const bool down_q = quantized_input(L.down) && ff % 32 == 0;
+            if (down_q) {
+                tag("down_quantize");
+                const vkml_quantize_params qp{u32(ff / 32), VKML_F32, VKML_Q8_0, VKML_F32};
+                check(vkml_quantize(&qp, hp, hq.data(), hs.data()), "quantize");
+            }
+            project(L.down, h, down_q ? &hq : nullptr, &hs, xp, xp, "down");
+        }
+        norm(final_norm, "final_norm");
+        project(lm_head(), xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(logits.data()), nullptr, "lm_head");
+        tag("finish");
+        check(vkml_step_finish(u32(c.vocab_size), greedy ? static_cast<const float*>(logits.data()) : nullptr,
+                               static_cast<vkml_decode_state*>(state.data()), static_cast<std::int32_t*>(log.data()), u32(context_length)),
+              "step");
+        tag("");
+    }
+
+    void run_step(bool greedy) {
+        const bool graphs = options.use_graphs && !vkml_get_profiling();
+        if (!graphs) {
+            step(greedy);
+            return;
+        }
+        std::uint64_t& g = greedy ? graph_greedy : graph_logits;
+        if (!g) {
+            check(vkml_graph_begin(), "Llama: graph capture");
+            try {
+                step(greedy);
+            } catch (...) {
+                std::uint64_t dropped = 0;
+                (void)vkml_graph_end(&dropped);
+                if (dropped) (void)vkml_graph_destroy(dropped);
+                throw;
+            }
+            check(vkml_graph_end(&g), "Llama: graph capture");
+        }
+        check(vkml_graph_launch(g), "Llama: graph launch");
+    }
+
+    void set_state(std::int32_t token, std::int64_t pos) {
+        check(vkml_state_set(static_cast<vkml_decode_state*>(state.data()), token, static_cast<std::int32_t>(pos), 0), "Llama: state");
+    }
+
+    void check_room(std::int64_t t) const {
+        if (t == 0) throw Error("Llama::forward: no tokens");
+        if (position + t > context_length) {
+            throw Error("Llama::forward: " + std::to_string(position + t) + " tokens exceed the context length of " +
+                        std::to_string(context_length));
+        }
+    }
+};
+
+Llama::Llama(std::unique_ptr<Impl> impl) : impl_(std::move(impl)) {}
+Llama::Llama(Llama&&) noexcept = default;
+Llama& Llama::operator=(Llama&&) noexcept = default;
+Llama::~Llama() = default;
+
+Llama Llama::load(Context& context, const std::filesystem::path& path, std::int64_t context_length, LlamaOptions options) {
+    if (!std::filesystem::exists(path)) {
+        throw Error("Llama::load: no model at " + path.string() + ": give a .gguf file");
+    }
+    if (path.extension() != ".gguf") throw Error("Llama::load: " + path.string() + " is not a .gguf file (this build reads GGUF)");
+    if (options.kv_cache != DType::F32 && options.kv_cache != DType::F16) {
+        throw Error("Llama: a KV cache of " + std::string(to_string(options.kv_cache)) + " is not implemented (f32 and f16 are)");
+    }
+    auto impl = std::make_unique<Impl>();
+    Impl& m = *impl;
+    m.context = &context;
+    m.config = LlamaConfig::from_gguf(path);
+    validated(m.config, context_length);
+    m.context_length = context_length;
+    m.options = options;
+    m.int_dot = context.runtime().integer_dot() && options.integer_dot_product;
+    const LlamaConfig& c = m.config;
+    const Gguf file{path};
+    const std::int64_t d = c.hidden_size, ff = c.intermediate_size, hd = c.head_dim;
+    const std::int64_t qd = c.num_heads * hd, kvd = c.num_kv_heads * hd;
+
+    // A float matrix quantized on request (llama.cpp:24-34); the output
+    // projection keeps q8_0 unless q8_0 was asked (llama.cpp:95-99).
+    const auto finish = [&](Weight w, bool head) {
+        if (!options.quantize || w.quantized || w.cols % 32 != 0) return w;
+        QuantType qt = *options.quantize;
+        if (head && qt != QuantType::q8_0) qt = QuantType::q8_0;
+        Weight out;
+        out.rows = w.rows;
+        out.cols = w.cols;
+        out.quantized = true;
+        switch (qt) {
+            case QuantType::q4_0: out.q = quantize_q4(w.t); break;
+            case QuantType::q4_1: out.q = quantize_q4_1(w.t); break;
+            case QuantType::q8_0: out.q = quantize_q8(w.t); break;
+            case QuantType::q4_K: throw Error("Llama: quantizing to q4_K on load is not implemented (q8_0, q4_0 and q4_1 are)");
+        }
+        return out;
+    };
+    const auto matrix = [&](const std::string& name, std::int64_t rows, std::int64_t cols, bool head = false) {
+        return finish(upload(context, host_matrix(file, name, rows, cols)), head);
+    };
+    const auto vec = [&](const std::string& name) {
+        return Tensor::from_data<float>(context, read_vector(file, name, d), {d});
+    };
+
+    m.embed = upload(context, host_matrix(file, "token_embd.weight", c.vocab_size, d));
+    m.tied = c.tie_word_embeddings && (m.embed.quantized || !options.quantize);
+    if (!m.tied) {
+        m.lm_head_own = std::make_shared<Weight>(c.tie_word_embeddings ? finish(m.embed, true) : matrix("output.weight", c.vocab_size, d, true));
+    }
+    m.final_norm = vec("output_norm.weight");
+    std::vector<float> divisors = c.rope_freq_factors;
+    if (c.rope_linear_factor != 1.0f) {
+        if (divisors.empty()) divisors.assign(std::size_t(hd / 2), 1.0f);
+        for (float& f : divisors) f *= c.rope_linear_factor;
+    }
+    m.rope = rope_table(context, context_length, hd, c.rope_theta, c.rope_scaling, divisors);
+    const Shape cache_shape{c.num_kv_heads, context_length, hd};
+    for (std::int64_t l = 0; l < c.num_layers; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        Impl::Layer L;
+        L.attn_norm = vec(p + "attn_norm.weight");
+        L.ffn_norm = vec(p + "ffn_norm.weight");
+        HostMatrix hq = host_matrix(file, p + "attn_q.weight", qd, d);
+        HostMatrix hk = host_matrix(file, p + "attn_k.weight", kvd, d);
+        HostMatrix hv = host_matrix(file, p + "attn_v.weight", kvd, d);
+        if (!options.quantize && same_format(hq, hk) && same_format(hq, hv)) {
+            L.qkv.emplace_back(upload(context, stack_rows({std::move(hq), std::move(hk), std::move(hv)})), 0);
+        } else {
+            L.qkv.emplace_back(finish(upload(context, hq), false), 0);
+            L.qkv.emplace_back(finish(upload(context, hk), false), qd);
+            L.qkv.emplace_back(finish(upload(context, hv), false), qd + kvd);
+        }
+        L.o = matrix(p + "attn_output.weight", d, qd);
+        L.gate = matrix(p + "ffn_gate.weight", ff, d);
+        L.up = matrix(p + "ffn_up.weight", ff, d);
+        L.down = matrix(p + "ffn_down.weight", d, ff);
+        L.k_cache = Tensor::zeros(context, cache_shape, options.kv_cache);
+        L.v_cache = Tensor::zeros(context, cache_shape, options.kv_cache);
+        m.layers.push_back(std::move(L));
+    }
+
+    // Decode buffers.
+    const auto f32 = [&](std::int64_t n) { return Tensor::zeros(context, {n}, DType::F32); };
+    m.x = f32(d);
+    m.xn = f32(d);
+    m.xq = Tensor::zeros(context, {std::max<std::int64_t>(d / 4, 1)}, DType::I32);
+    m.xs = f32(std::max<std::int64_t>(d / 32, 1));
+    m.qkv = f32(qd + 2 * kvd);
+    m.q = f32(qd);
+    m.attn = f32(qd);
+    m.aq = Tensor::zeros(context, {qd / 4}, DType::I32);
+    m.as = f32(qd / 32);
+    m.h = f32(ff);
+    m.hq = Tensor::zeros(context, {std::max<std::int64_t>(ff / 4, 1)}, DType::I32);
+    m.hs = f32(std::max<std::int64_t>(ff / 32, 1));
+    m.gate_tmp = f32(ff);
+    m.up_tmp = f32(ff);
+    m.ytmp = f32(d);
+    m.logits = f32(c.vocab_size);
+    m.state = Tensor::zeros(context, {4}, DType::I32);
+    m.log = Tensor::zeros(context, {context_length}, DType::I32);
+    const std::int64_t cus = std::max<std::int64_t>(context.device_info().compute_units, 1);
+    m.splits = options.attention_splits > 0 ? options.attention_splits
+                                            : std::max<std::int64_t>((context_length + 1023) / 1024,
+                                                                     std::min<std::int64_t>(2 * cus / c.num_kv_heads, (context_length + 15) / 16));
+    m.splits = std::max<std::int64_t>(m.splits, (context_length + 1023) / 1024);
+    m.partial = f32(c.num_kv_heads * m.splits * (c.num_heads / c.num_kv_heads) * hd);
+    m.stats = f32(c.num_kv_heads * m.splits * (c.num_heads / c.num_kv_heads) * 2);
+    context.synchronize();
+    return Llama(std::move(impl));
+}
+
+const LlamaConfig& Llama::config() const noexcept { return impl_->config; }
+std::int64_t Llama::context_length() const noexcept { return impl_->context_length; }
+std::int64_t Llama::position() const noexcept { return impl_->position; }
+
+Tensor Llama::forward(std::span<const std::int32_t> tokens) {
+    Impl& m = *impl_;
+    const auto t = static_cast<std::int64_t>(tokens.size());
+    m.check_room(t);
+    for (std::int64_t i = 0; i < t; ++i) {
+        m.set_state(tokens[static_cast<std::size_t>(i)], m.position);
+        m.run_step(false);
+        ++m.position;
+    }
+    Tensor out = Tensor::empty(*m.context, {m.config.vocab_size}, DType::F32);
+    check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward");
+    return out;
+}
+
+Tensor Llama::forward_all(std::span<const std::int32_t> tokens) {
+    Impl& m = *impl_;
+    const auto t = static_cast<std::int64_t>(tokens.size());
+    m.check_room(t);
+    Tensor out = Tensor::empty(*m.context, {t, m.config.vocab_size}, DType::F32);
+    const std::uint64_t row = static_cast<std::uint64_t>(m.config.vocab_size) * 4;
+    for (std::int64_t i = 0; i < t; ++i) {
+        m.set_state(tokens[static_cast<std::size_t>(i)], m.position);
+        m.run_step(false);
+        ++m.position;
+        check(vkml_memcpy_d2d(static_cast<std::uint8_t*>(out.data()) + row * i, m.logits.data(), row), "Llama::forward_all");
+    }
+    return out;
+}
+
+std::vector<std::int32_t> Llama::generate_greedy(std::int32_t first, std::int64_t count) {
+    Impl& m = *impl_;
+    if (count <= 0) return {};
+    m.check_room(count);
+    m.set_state(first, m.position);
+    for (std::int64_t i = 0; i < count; ++i) m.run_step(true);
+    std::vector<std::int32_t> out(static_cast<std::size_t>(count));
+    check(vkml_memcpy_d2h(out.data(), m.log.data(), out.size() * 4), "Llama::generate_greedy");
+    m.position += count;
+    return out;
+}
+
+void Llama::reset() noexcept { impl_->position = 0; }
+
+std::int64_t Llama::rewind(std::int64_t position) {
+    Impl& m = *impl_;
+    if (position < 0 || position > m.position) {
+        throw Error("Llama::rewind: cannot rewind to position " + std::to_string(position) + " of a sequence at " + std::to_string(m.position));
+    }
+    m.position = position;
+    return position;
+}
+
+std::int64_t Llama::kv_cache_bytes() const noexcept {
+    std::int64_t bytes = 0;
+    for (const auto& L : impl_->layers) bytes += std::int64_t(L.k_cache.nbytes() + L.v_cache.nbytes());
+    return bytes;
+}
+
+const Tensor& Llama::k_cache(std::int64_t layer) const { return impl_->layers.at(static_cast<std::size_t>(layer)).k_cache; }
+const Tensor& Llama::v_cache(std::int64_t layer) const { return impl_->layers.at(static_cast<std::size_t>(layer)).v_cache; }
+
+}  // namespace vkml

@@ -1,0 +1,66 @@
+// runtime.hpp -- the C++ side of the backend seam (the reference's
+// src/core/runtime.hpp and storage.hpp), over the C ABI of libvkml_hip.so.
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "vkml/context.hpp"
+#include "vkml/error.hpp"
+#include "vkml/tensor.hpp"
+#include "vkml_hip.h"
+
+namespace vkml::detail {
+
+// Throws vkml::Error with the library's message unless status is VKML_OK.
+void check(int status, const char* what = nullptr);
+
+// Device memory pool: freed buffers are kept by rounded size and handed out
+// again. All work runs in order on one stream, so a buffer released while
+// kernels that use it are queued is safe to reuse for later work on the
+// same stream (the reference's retire-until-the-timeline-passes,
+// src/core/runtime.cpp:30-62, is what stream order gives here).
+class Runtime {
+public:
+    explicit Runtime(const ContextOptions& options);
+    ~Runtime();
+
+    void* acquire(std::uint64_t bytes, std::uint64_t& rounded);
+    void release(void* ptr, std::uint64_t rounded) noexcept;
+
+    const DeviceInfo& info() const noexcept { return info_; }
+    const ContextOptions& options() const noexcept { return options_; }
+    bool integer_dot() const noexcept { return options_.integer_dot_product && info_.integer_dot_product; }
+
+    void synchronize();
+
+private:
+    ContextOptions options_;
+    DeviceInfo info_;
+    std::multimap<std::uint64_t, void*> free_;
+    std::uint64_t pooled_bytes_ = 0;
+    bool owns_device_ = true;
+};
+
+struct Storage {
+    Runtime* runtime = nullptr;
+    void* ptr = nullptr;
+    std::uint64_t bytes = 0;  // as rounded by the pool
+    ~Storage();
+};
+
+struct TensorAccess {
+    static Runtime& runtime(const Tensor& t);
+    static void* ptr(const Tensor& t) { return t.data(); }
+    static Tensor empty(Runtime& runtime, Shape shape, DType dtype) { return Tensor::empty(runtime, std::move(shape), dtype); }
+};
+
+std::int64_t numel_of(const Shape& shape);
+
+// The vkml_type code of a dtype.
+std::uint32_t type_code(DType dtype);
+
+}  // namespace vkml::detail

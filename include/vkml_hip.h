@@ -315,13 +315,16 @@ int vkml_embedding(const vkml_embedding_params* p, const void* d_values, const v
 
 /* ---------------------------------------------------------------------- */
 /* Decode attention (shaders/attend.comp + attend_merge.comp,             */
-/* src/ops/attention.cpp:22-84), GQA-aware: workgroup (s, g) reads the    */
-/* keys of split s of KV head g once for all of its heads / kv_heads query */
-/* heads. Keys kv_start..kv_len of caches [kv_heads, capacity, head_dim]  */
-/* (F32 or F16), position p at row p % capacity. With d_state non-NULL,   */
-/* kv_len is d_state->position + 1 (the decode graph).                    */
-/* partial: [kv_heads, splits, group, head_dim] f32; stats: [kv_heads,    */
-/* splits, group, 2] (max score, sum of exp).                             */
+/* src/ops/attention.cpp:22-84). Keys kv_start..kv_len of caches          */
+/* [kv_heads, capacity, head_dim] (F32 or F16), key position p at row     */
+/* p % capacity, in the reference's chunks of 128 keys from kv_start.     */
+/* Workgroup (c, g) reads chunk c of KV head g once for all heads /       */
+/* kv_heads query heads of its group. With d_state non-NULL, kv_len is    */
+/* d_state->position + 1 (the replayed decode step) and the launch covers */
+/* the whole cache. chunks: the partial buffers' stride, at least         */
+/* ceil((kv_len - kv_start) / 128), or ceil((capacity - kv_start) / 128)  */
+/* with d_state. partial: [heads, chunks, head_dim] f32; stats: [heads,   */
+/* chunks, 2] (max score, sum of exp); chunks past kv_len get max -inf.   */
 /* ---------------------------------------------------------------------- */
 
 typedef struct vkml_decode_state {
@@ -339,14 +342,14 @@ typedef struct vkml_attend_params {
     uint32_t kv_heads;
     uint32_t head_dim;
     uint32_t kv_type;
-    uint32_t splits;
+    uint32_t chunks;
     float scale;
     float softcap;
 } vkml_attend_params;
 int vkml_attend(const vkml_attend_params* p, const float* d_q, const void* d_k_cache,
                 const void* d_v_cache, float* d_partial, float* d_stats,
                 const vkml_decode_state* d_state);
-/* Merges the splits into out [heads, head_dim] f32 and, when d_values is
+/* Merges the chunks into out [heads, head_dim] f32 and, when d_values is
  * non-NULL, its Q8_0 form with f32 scales (the o projection's input). */
 int vkml_attend_merge(const vkml_attend_params* p, const float* d_partial, const float* d_stats,
                       float* d_out, void* d_values, float* d_scales);

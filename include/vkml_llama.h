@@ -32,7 +32,6 @@ typedef struct vkml_llama_options {
     int32_t quantize;           /* -1 none; 0 q8_0, 1 q4_0, 2 q4_1: float weights on load */
     int32_t integer_dot;        /* 1: int8 activations for quantized weights (default) */
     int32_t use_graphs;         /* 1: replay the decode step as a HIP graph (default) */
-    int32_t attention_splits;   /* 0: from the CU count */
     const char* device_name;    /* NULL or "": VKML_DEVICE, then device 0 */
 } vkml_llama_options;
 

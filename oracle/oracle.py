@@ -63,6 +63,7 @@ def _declare(L):
         "orc_rms_norm": (None, [vp, vp, i64, i64, f32, vp]),
         "orc_rope_table": (None, [i64, i64, f32, vp]),
         "orc_rope": (None, [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp]),
+        "orc_expf_array": (None, [vp, vp, i64]),
         "orc_silu": (None, [vp, vp, i64]),
         "orc_binary": (None, [i32, vp, vp, i64, i64, vp]),
         "orc_argmax": (C.c_int32, [vp, i64]),
@@ -217,6 +218,14 @@ def rope(x, table, start_pos: int, style: int = 0) -> np.ndarray:
     out = np.empty_like(x)
     lib().orc_rope(_p(x), _p(table), rows, heads, seq, dim, table.shape[1], start_pos, style, _p(out))
     return out
+
+
+def expf(x) -> np.ndarray:
+    """The exp the oracle and the GPU kernels share (orc_expf)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_expf_array(_p(x), _p(y), x.size)
+    return y
 
 
 def silu(x) -> np.ndarray:

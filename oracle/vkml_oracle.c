@@ -112,6 +112,36 @@ uint16_t orc_f32_to_bf16(float f) {
     return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
 }
 
+/* e^x as a fixed sequence of f32 operations, shared bit for bit with the GPU
+ * kernels. The reference calls GLSL exp (unary.comp:22, attend.comp:129,
+ * attend_merge.comp:34, softmax.comp), whose accuracy its driver defines:
+ * parity with it is unpinned at the last bit; tests pin this function against
+ * libm's exp within 2 ulp. Method: Cody-Waite reduction x = n ln2 + r with ln2
+ * split into a 15-bit head 0.693145751953125 and a tail, |r| <= ln2/2; e^r by
+ * its degree-7 Taylor polynomial (coefficients 1/k! rounded to f32) in Horner
+ * form; 2^n through the exponent bits. */
+float orc_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -86.5f) return 0.0f;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187045037746429443359375e-6f;
+    float p = 1.98412701138295233249664306640625e-4f;
+    p = p * r + 1.388888922519981861114501953125e-3f;
+    p = p * r + 8.333333767950534820556640625e-3f;
+    p = p * r + 4.16666679084300994873046875e-2f;
+    p = p * r + 1.6666667163372039794921875e-1f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    const int e = (int)n;
+    if (e > 127) return p * 1.70141183460469231731687303715884105728e38f * 2.0f;
+    return p * u2f((uint32_t)(e + 127) << 23);
+}
+void orc_expf_array(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_expf(x[i]);
+}
+
 void orc_cast_f32_to_f16(const float* x, uint16_t* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = orc_f32_to_f16(x[i]);
 }
@@ -780,7 +810,7 @@ void orc_rope(const float* x, const float* table, int64_t rows, int64_t heads, i
 
 /* unary.comp:21-24 */
 void orc_silu(const float* x, float* y, int64_t n) {
-    for (int64_t i = 0; i < n; ++i) y[i] = x[i] / (1.0f + expf(-x[i]));
+    for (int64_t i = 0; i < n; ++i) y[i] = x[i] / (1.0f + orc_expf(-x[i]));
 }
 
 /* binary.comp:26-43: op 0 add, 1 sub, 2 mul, 3 div; b repeats. */
@@ -870,7 +900,7 @@ void orc_attend_decode(const float* q, int64_t heads, const void* k, const void*
             float m = -INFINITY;
             for (int64_t t = 0; t < n; ++t) m = fmaxf(m, p[t]);
             for (int64_t t = 0; t < WG; ++t) {
-                const float weight = t < n ? expf(p[t] - m) : 0.0f;
+                const float weight = t < n ? orc_expf(p[t] - m) : 0.0f;
                 if (t < n) p[t] = weight;
                 red[t] = weight;
             }
@@ -905,7 +935,7 @@ void orc_attend_decode(const float* q, int64_t heads, const void* k, const void*
             for (int64_t c = 1; c < chunks; ++c) top = fmaxf(top, stats[2 * c]);
             float sum = 0.0f, weight = 0.0f;
             for (int64_t c = 0; c < chunks; ++c) {
-                const float r = expf(stats[2 * c] - top);
+                const float r = orc_expf(stats[2 * c] - top);
                 sum += r * partial[c * hd + d];
                 weight += r * stats[2 * c + 1];
             }
@@ -938,9 +968,9 @@ void orc_attention_prefill(const float* q, int64_t heads, int64_t q_len, const v
             float m = -INFINITY;
             for (int64_t j = 0; j < visible; ++j) m = fmaxf(m, s[j] * scale);
             float sum = 0.0f;
-            for (int64_t j = 0; j < visible; ++j) sum += expf(s[j] * scale - m);
+            for (int64_t j = 0; j < visible; ++j) sum += orc_expf(s[j] * scale - m);
             const float inv = 1.0f / sum;
-            for (int64_t j = 0; j < kv_len; ++j) s[j] = j < visible ? expf(s[j] * scale - m) * inv : 0.0f;
+            for (int64_t j = 0; j < kv_len; ++j) s[j] = j < visible ? orc_expf(s[j] * scale - m) * inv : 0.0f;
             for (int64_t c = 0; c < hd; ++c) {
                 float acc = 0.0f;
                 for (int64_t j = 0; j < kv_len; ++j) acc += s[j] * kv_at(v, f16, (kv_row0 + j) * hd + c);

@@ -95,6 +95,8 @@ void orc_rms_norm(const float* x, const float* w, int64_t rows, int64_t cols, fl
 void orc_rope_table(int64_t positions, int64_t head_dim, float theta, float* table); /* rope.cpp:32-86 */
 void orc_rope(const float* x, const float* table, int64_t rows, int64_t heads, int64_t seq,
               int64_t dim, int64_t half_dim, int64_t start_pos, int style, float* out); /* rope.comp */
+float orc_expf(float x);   /* the exp shared with the GPU kernels; exp of unary.comp:22 and attend.comp:129 */
+void orc_expf_array(const float* x, float* y, int64_t n);
 void orc_silu(const float* x, float* y, int64_t n);                  /* unary.comp:21-24 */
 void orc_binary(int op, const float* a, const float* b, int64_t n, int64_t b_count,
                 float* out);                                          /* binary.comp */

@@ -1,9 +1,12 @@
 """Kernel parity on the MI355X: each HIP kernel through the C ABI against the
-CPU oracle on the same seeded inputs. Integer and bit-level results (codes,
-scales, casts, copies, argmax, embeddings of quantized tables) must be
-identical; f32 results whose sums run in another order must sit inside the
-f32 dot-product error bound the reference's own tests use
-(tests/test_quantize.cpp:197-224 there: 2 k 2^-24 sum|a b|)."""
+CPU oracle on the same seeded inputs. The kernels of the decode path keep the
+reference's order of f32 operations, so their results must be identical to
+the oracle's, bit for bit: codes, scales, casts, copies, argmax, embeddings,
+GEMV (int8 and float), RMSNorm, RoPE, SiLU, attention and its merge. GEMV
+results are also held to the f32 dot-product error bound against exact sums
+(tests/test_quantize.cpp:197-224 in the reference: 2 k 2^-24 sum|a b|), which
+pins the oracle itself. Only the matmul and softmax of the prefill-shaped ops,
+whose order this build does not follow, are checked within a tolerance."""
 import math
 
 import numpy as np
@@ -148,7 +151,11 @@ def test_gemv_dot_matches_oracle_within_the_dot_bound(fmt, n, k):
     want = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)
     exact, bound = dot_bound(aw, asc, 1, k, quant, words, scales, n)
     assert np.all(np.abs(got - exact) <= bound)
-    assert np.all(np.abs(got - want) <= 2 * bound)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def bits(x):
+    return np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
 
 
 @pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_0, H.Q4_1])
@@ -161,6 +168,7 @@ def test_gemv_dot_f32_scales_and_several_rows(fmt):
     got = out.download(np.float32, (m, n))
     exact, bound = dot_bound(aw, asc, m, k, quant, words, scales, n)
     assert np.all(np.abs(got - exact) <= bound)
+    assert np.array_equal(bits(got), bits(O.gemv_dot(quant, aw, asc, m, words, scales, n, k)))
 
 
 @pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_K])
@@ -173,16 +181,13 @@ def test_gemv_dot_add_and_swiglu(fmt):
     out = dev(res)
     H.call("vkml_gemv_dot_add", H.GemvDotParams(1, n, k, fmt, H.F16), p(dev(aw)), p(v), p(out), p(s), p(dev(asc)), p(out))
     got = out.download(np.float32, n)
-    exact, bound = dot_bound(aw, asc, 1, k, quant, words, scales, n)
-    assert np.all(np.abs(got - (res + exact[0])) <= bound[0] + 2.0 ** -23 * np.abs(res + exact[0]))
+    g = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)[0]
+    assert np.array_equal(bits(got), bits(res + g))
     h = H.empty(n * 4)
     H.call("vkml_gemv_dot_swiglu", H.GemvDotParams(1, n, k, fmt, H.F16), p(dev(aw)), p(dev(asc)), p(v), p(s), p(v2), p(s2), p(h))
     got = h.download(np.float32, n)
-    g = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)[0]
     u = O.gemv_dot(quant, aw, asc, 1, words2, scales2, n, k)[0]
-    want = O.silu(g) * u
-    gd = g.astype(np.float64)
-    assert np.allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+    assert np.array_equal(bits(got), bits(O.silu(g) * u))
 
 
 @pytest.mark.parametrize("bt", [H.F32, H.F16, H.BF16, H.Q8_0, H.Q4_0, H.Q4_1, H.Q4_K])
@@ -192,17 +197,20 @@ def test_float_gemv_path(bt):
     a = rng.standard_normal((m, k)).astype(np.float32)
     sc = None
     if bt == H.F32:
-        b = (rng.standard_normal((n, k)) * 0.05).astype(np.float32); wd = b; ot = O.T_F32
+        b = (rng.standard_normal((n, k)) * 0.05).astype(np.float32); wd = b; ot = O.T_F32; ob, osc = b, None
     elif bt in (H.F16, H.BF16):
         w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
         if bt == H.F16:
             b = w.astype(np.float16).view(np.uint16); wd = b.view(np.float16).astype(np.float32); ot = O.T_F16
         else:
             b = (w.view(np.uint32) >> 16).astype(np.uint16); wd = (b.astype(np.uint32) << 16).view(np.float32); ot = O.T_BF16
+        ob, osc = b, None
     else:
         dv, ds, quant, words, scales = weights(bt, n, k, 8)
         wd = O.dequantize(quant, words, scales, n, k)
         b, sc = None, None
+        # q4_K runs as the reference's q4_1 repack, which the oracle holds
+        ot, ob, osc = {O.Q8_0: O.T_Q8, O.Q4_0: O.T_Q4, O.Q4_1: O.T_Q4_1}[quant], words, scales
     out = H.empty(m * n * 4)
     if b is not None:
         H.call("vkml_gemv", H.GemvParams(m, n, k, bt, H.F16), p(dev(a)), p(dev(b)), p(out), None)
@@ -212,6 +220,7 @@ def test_float_gemv_path(bt):
     want = a.astype(np.float64) @ wd.astype(np.float64).T
     bound = 3 * k * 2.0 ** -24 * (np.abs(a.astype(np.float64)) @ np.abs(wd.astype(np.float64)).T) + 1e-30
     assert np.all(np.abs(got - want) <= bound)
+    assert np.array_equal(bits(got), bits(O.gemv_float(ot, a, ob, osc, n, k)))
 
 
 # ---------------------------------------------------------------- norms and rope
@@ -225,14 +234,14 @@ def test_rms_norm_quantize(cols):
     H.call("vkml_rms_norm_quantize", H.RmsNormParams(2, cols, 1e-5), p(dev(x)), p(dev(w)), p(y), p(vals), p(scs))
     got = y.download(np.float32, x.shape)
     want = O.rms_norm(x, w, 1e-5)
-    assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+    assert np.array_equal(bits(got), bits(want))
     # the quantized form is exactly the reference quantizer's of these f32 values
     ww, ws = O.quantize(O.Q8_0, got, False)
     assert np.array_equal(vals.download(np.uint32, ww.shape), ww)
     assert np.array_equal(scs.download(np.float32, ws.shape).view(np.uint32), ws.view(np.uint32))
     plain = H.empty(x.nbytes)
     H.call("vkml_rms_norm", H.RmsNormParams(2, cols, 1e-5), p(dev(x)), p(dev(w)), p(plain))
-    assert np.all(np.abs(plain.download(np.float32, x.shape) - want) <= 1e-5 * (1 + np.abs(want)))
+    assert np.array_equal(bits(plain.download(np.float32, x.shape)), bits(want))
 
 
 @pytest.mark.parametrize("style", [0, 1])
@@ -272,10 +281,11 @@ def test_rope_kv_append_bit_exact(kv_type):
 
 # ---------------------------------------------------------------- attention
 
-@pytest.mark.parametrize("hd,heads,kvh,kv_len,kv_type,splits", [
-    (128, 32, 8, 4096, H.F16, 64), (128, 32, 8, 1, H.F16, 64), (64, 32, 8, 640, H.F16, 32),
-    (64, 4, 2, 45, H.F32, 4), (128, 32, 8, 300, H.F32, 16), (256, 8, 8, 200, H.F16, 2), (128, 8, 1, 1000, H.F16, 8)])
-def test_attend_matches_oracle(hd, heads, kvh, kv_len, kv_type, splits):
+@pytest.mark.parametrize("hd,heads,kvh,kv_len,kv_type,extra", [
+    (128, 32, 8, 4096, H.F16, 0), (128, 32, 8, 1, H.F16, 3), (64, 32, 8, 640, H.F16, 0),
+    (64, 4, 2, 45, H.F32, 1), (128, 32, 8, 300, H.F32, 0), (256, 8, 8, 200, H.F16, 0), (128, 8, 1, 1000, H.F16, 2),
+    (256, 16, 2, 129, H.F32, 0), (64, 16, 4, 128, H.F16, 0)])
+def test_attend_bit_exact(hd, heads, kvh, kv_len, kv_type, extra):
     cap = kv_len + 7
     rng = np.random.default_rng(kv_len)
     q = rng.standard_normal((heads, hd)).astype(np.float32)
@@ -285,14 +295,15 @@ def test_attend_matches_oracle(hd, heads, kvh, kv_len, kv_type, splits):
         kc, vc = k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16)
     else:
         kc, vc = k, v
-    prm = H.AttendParams(0, kv_len, cap, heads, kvh, hd, kv_type, splits, 1.0 / math.sqrt(hd), 0.0)
-    part, stats = H.empty(kvh * splits * (heads // kvh) * hd * 4), H.empty(kvh * splits * (heads // kvh) * 8)
+    chunks = (kv_len + 127) // 128 + extra  # spare chunks come out empty
+    prm = H.AttendParams(0, kv_len, cap, heads, kvh, hd, kv_type, chunks, 1.0 / math.sqrt(hd), 0.0)
+    part, stats = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8)
     out, vals, scs = H.empty(heads * hd * 4), H.empty(heads * hd), H.empty(heads * hd // 32 * 4)
     H.call("vkml_attend", prm, p(dev(q)), p(dev(kc)), p(dev(vc)), p(part), p(stats), None)
     H.call("vkml_attend_merge", prm, p(part), p(stats), p(out), p(vals), p(scs))
     got = out.download(np.float32, (heads, hd))
     want = O.attend_decode(q, kc, vc, 0, kv_len)
-    assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+    assert np.array_equal(bits(got), bits(want))
     ww, ws = O.quantize(O.Q8_0, got, False)
     assert np.array_equal(vals.download(np.uint32, ww.shape), ww)
     assert np.array_equal(scs.download(np.float32, ws.shape).view(np.uint32), ws.view(np.uint32))
@@ -306,12 +317,29 @@ def test_attend_reads_kv_len_from_the_decode_state():
     vc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
     st = H.empty(16)
     H.call("vkml_state_set", p(st), 5, 299, 0)
-    prm = H.AttendParams(0, 0, cap, heads, kvh, hd, H.F16, 16, 1.0 / math.sqrt(hd), 0.0)
-    part, stats, out = H.empty(kvh * 16 * 4 * hd * 4), H.empty(kvh * 16 * 4 * 8), H.empty(heads * hd * 4)
+    chunks = cap // 128
+    prm = H.AttendParams(0, 0, cap, heads, kvh, hd, H.F16, chunks, 1.0 / math.sqrt(hd), 0.0)
+    part, stats, out = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8), H.empty(heads * hd * 4)
     H.call("vkml_attend", prm, p(dev(q)), p(dev(kc)), p(dev(vc)), p(part), p(stats), p(st))
     H.call("vkml_attend_merge", prm, p(part), p(stats), p(out), None, None)
     want = O.attend_decode(q, kc, vc, 0, 300)
-    assert np.all(np.abs(out.download(np.float32, (heads, hd)) - want) <= 1e-5 * (1 + np.abs(want)))
+    assert np.array_equal(bits(out.download(np.float32, (heads, hd))), bits(want))
+
+
+def test_attend_from_a_window_start():
+    # keys 100..499 (a sliding window's start), chunks of 128 from key 100
+    hd, heads, kvh, cap = 64, 8, 2, 512
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    kc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    chunks = (500 - 100 + 127) // 128
+    prm = H.AttendParams(100, 500, cap, heads, kvh, hd, H.F16, chunks, 1.0 / math.sqrt(hd), 0.0)
+    part, stats, out = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8), H.empty(heads * hd * 4)
+    H.call("vkml_attend", prm, p(dev(q)), p(dev(kc)), p(dev(vc)), p(part), p(stats), None)
+    H.call("vkml_attend_merge", prm, p(part), p(stats), p(out), None, None)
+    want = O.attend_decode(q, kc, vc, 100, 500)
+    assert np.array_equal(bits(out.download(np.float32, (heads, hd))), bits(want))
 
 
 # ---------------------------------------------------------------- small ops
@@ -386,7 +414,7 @@ def test_cast_copy_permute_elementwise():
         H.call("vkml_binary", op, 1000, 10, p(dev(a)), p(dev(b)), p(out))
         assert np.array_equal(out.download(np.float32, 1000), f(a, np.tile(b, 100)).astype(np.float32))
     H.call("vkml_unary", 0, 1000, 0.0, p(dev(a * 30)), p(out))
-    assert np.allclose(out.download(np.float32, 1000), O.silu(a * 30), rtol=2e-6, atol=1e-30)
+    assert np.array_equal(bits(out.download(np.float32, 1000)), bits(O.silu(a * 30)))
 
 
 def test_softmax_and_matmul():

@@ -1,11 +1,13 @@
 """Whole-model parity on the MI355X: vkml::Llama (through include/vkml_llama.h)
 against the CPU oracle's restatement of the reference's Llama::run on the
-same seeded GGUF files. Logits must sit within 1e-4 of the largest logit
-(the reference's own f32 test uses 1e-4 * (1 + |want|),
-tests/test_llama.cpp:758-764 there), greedy token ids must be identical
-unless the oracle's own top-2 margin at that step is inside that bound (a
-tie the two summation orders may break differently), and KV-cache rows must
-agree to f16 rounding."""
+same seeded GGUF files, token by token. Every kernel of the decode step keeps
+the reference's order of f32 operations, so logits, greedy token ids and
+KV-cache rows must be identical to the oracle's, bit for bit. (The north-star
+bound, logits within 1e-4 of the largest, is what a reordered sum would be
+allowed; the reference's own f32 test uses 1e-4 * (1 + |want|),
+tests/test_llama.cpp:758-764 there.) A whole prompt at once, which the
+reference runs through matmul_dot and softmax attention and this build runs
+token by token, is held to 1e-3 of the largest logit."""
 import os
 
 import numpy as np
@@ -51,24 +53,22 @@ def close(got, want, tol=1e-4):
     assert err <= tol * np.abs(want).max(), (err, np.abs(want).max())
 
 
+def same(got, want):
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+        bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+        err = np.max(np.abs(got - want))
+        raise AssertionError(f"{bad.size} of {got.size} logits differ (first at {bad[0]}), max |diff| {err:.3g}, "
+                             f"max |want| {np.abs(want).max():.3g}")
+
+
 def greedy_oracle(m, first, count):
-    out, margins = [], []
-    nxt = first
+    out, logits, nxt = [], None, first
     for _ in range(count):
         logits = m.forward(np.array([nxt]))
-        top2 = np.sort(logits)[-2:]
-        margins.append(top2[1] - top2[0])
         nxt = int(O.argmax(logits))
         out.append(nxt)
-    return np.array(out), np.array(margins), logits
-
-
-def check_greedy(got, want, margins, scale, tol=1e-4):
-    for i, (g, w) in enumerate(zip(got, want)):
-        if g != w:
-            assert margins[i] <= tol * scale, f"step {i}: {g} != {w} with a top-2 margin of {margins[i]}"
-            return i  # a near tie: later steps follow different tokens
-    return len(got)
+    return np.array(out), logits
 
 
 @pytest.mark.parametrize("name,ctx,kv_f16,prompt,steps", [
@@ -84,15 +84,15 @@ def test_prompt_then_greedy_matches_oracle(files, name, ctx, kv_f16, prompt, ste
     want = None
     for t in tokens:  # token by token: the same attention algorithm as the GPU's decode step
         want = ref.forward(np.array([t]))
-    close(got, want)
+    same(got, want)
     first = int(O.argmax(want))
-    toks, margins, last = greedy_oracle(ref, first, steps)
+    toks, last = greedy_oracle(ref, first, steps)
     g = gpu.generate_greedy(first, steps)
-    n = check_greedy(g, toks, margins, np.abs(want).max())
+    assert list(g) == list(toks)
     assert gpu.position == prompt + steps
-    if n == steps:  # logits of the last step, recomputed through forward
-        gpu.rewind(prompt + steps - 1)
-        close(gpu.forward(np.array([toks[-2] if steps > 1 else first])), last)
+    # logits of the last step, recomputed through forward
+    gpu.rewind(prompt + steps - 1)
+    same(gpu.forward(np.array([toks[-2] if steps > 1 else first])), last)
 
 
 def test_whole_prompt_matches_the_reference_prefill_path(files):
@@ -136,10 +136,7 @@ def test_kv_cache_rows_match_oracle(files):
     n = int(np.prod(kv_shape))
     kr = np.ctypeslib.as_array(ctypes.cast(O.lib().orc_model_k_cache(ref._h, 1), ctypes.POINTER(ctypes.c_uint16)), (n,)).reshape(kv_shape)
     vr = np.ctypeslib.as_array(ctypes.cast(O.lib().orc_model_v_cache(ref._h, 1), ctypes.POINTER(ctypes.c_uint16)), (n,)).reshape(kv_shape)
-    kf, kfr = k.view(np.float16).astype(np.float32)[:, :6], kr.view(np.float16).astype(np.float32)[:, :6]
-    vf, vfr = v.view(np.float16).astype(np.float32)[:, :6], vr.view(np.float16).astype(np.float32)[:, :6]
-    for got, want in ((kf, kfr), (vf, vfr)):
-        assert np.all(np.abs(got - want) <= 2 * 2.0 ** -11 * np.abs(want) + 1e-4 * np.abs(want).max())
+    assert np.array_equal(k[:, :6], kr[:, :6]) and np.array_equal(v[:, :6], vr[:, :6])
 
 
 def test_forward_all_reset_rewind_and_errors(files):
@@ -193,4 +190,4 @@ def test_no_dot_path_uses_f32_activations(files):
     ref = O.Model(path, 16, kv_f16=True, int_dot=False)
     for t in tokens:
         want = ref.forward(np.array([t]))
-    close(got, want)
+    same(got, want)

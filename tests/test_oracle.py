@@ -273,6 +273,28 @@ def test_rms_norm_matches_double():
         assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
 
 
+def test_expf_within_two_ulp_of_exp_and_special_values():
+    # Every 97th f32 from -86.5 to 88.72 (the range where it is finite and
+    # nonzero), against exp in double rounded once.
+    lo, hi = np.float32(-86.5).view(np.uint32), np.float32(88.72283935546875).view(np.uint32)
+    neg = np.arange(0x80000000, lo + 1, 97, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    pos = np.arange(0, hi + 1, 97, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = np.concatenate([neg, pos])
+    got = O.expf(x)
+    want = np.exp(x.astype(np.float64)).astype(np.float32)
+    ulp = np.spacing(want)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 2 * ulp)
+    special = np.array([0.0, -0.0, 1.0, np.inf, -np.inf, np.nan, 88.8, -86.6, -1e30, 1e30], np.float32)
+    g = O.expf(special)
+    assert g[0] == 1.0 and g[1] == 1.0 and abs(g[2] - np.float32(math.e)) <= np.spacing(np.float32(math.e))
+    assert g[3] == np.inf and g[4] == 0.0 and np.isnan(g[5]) and g[6] == np.inf
+    assert g[7] == 0.0 and g[8] == 0.0 and g[9] == np.inf
+    # silu is x / (1 + exp(-x)) with this exp
+    xs = np.random.default_rng(4).standard_normal(4096).astype(np.float32) * 8
+    sw = xs.astype(np.float64) / (1 + np.exp(-xs.astype(np.float64)))
+    assert np.all(np.abs(O.silu(xs) - sw) <= 4e-7 * (1 + np.abs(sw)))
+
+
 def test_rope_table_entries_and_rotation():
     t = O.rope_table(3, 4, 100.0)
     assert t[2, 1, 0] == np.float32(math.cos(0.2)) and t[2, 1, 1] == np.float32(math.sin(0.2))

@@ -55,6 +55,37 @@ __device__ __forceinline__ float half_to_float(uint32_t h, uint32_t type) {
     return type == 2 ? bf16_bits_to_float(h) : f16_bits_to_float(h);
 }
 
+// ---------------------------------------------------------------- exp
+
+// e^x in f32 with a fixed sequence of IEEE operations, so the CPU oracle
+// (oracle/vkml_oracle.c, orc_expf) computes the same bits: the reference's
+// GLSL exp has driver-defined accuracy, and softmax weights and SiLU feed
+// the int8 quantizer, where one ulp can move a code. Method: Cody-Waite
+// range reduction x = n ln2 + r, |r| <= ln2/2, with ln2 split in a 15-bit
+// head and a tail; e^r by its degree-7 Taylor polynomial in Horner form
+// (truncation below 6e-9 relative); the result scaled by 2^n through the
+// exponent bits. Below -86.5 (e^x < 2.7e-38) the result is 0, above
+// 88.72 infinity.
+__device__ __forceinline__ float vk_expf(float x) {
+#pragma clang fp contract(off)
+    if (!(x == x)) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -86.5f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+    const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187045037746429443359375e-6f;
+    float p = 1.98412701138295233249664306640625e-4f;
+    p = p * r + 1.388888922519981861114501953125e-3f;
+    p = p * r + 8.333333767950534820556640625e-3f;
+    p = p * r + 4.16666679084300994873046875e-2f;
+    p = p * r + 1.6666667163372039794921875e-1f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    const int e = static_cast<int>(n);
+    if (e > 127) return p * 1.70141183460469231731687303715884105728e38f * 2.0f;
+    return p * __int_as_float((e + 127) << 23);
+}
+
 // ---------------------------------------------------------------- reductions
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -172,17 +203,17 @@ __device__ __forceinline__ float weight_value(uint32_t type, uint32_t scale_type
         case 2: return bf16_bits_to_float(static_cast<const uint16_t*>(values)[e]);
         case 3: {
             const int8_t q = static_cast<const int8_t*>(values)[e];
-            return __fmul_rn(static_cast<float>(q), scale_at(e / 32));
+            return static_cast<float>(q) * scale_at(e / 32);
         }
         case 4: {
             const uint32_t w = static_cast<const uint32_t*>(values)[e / 8];
             const float q = static_cast<float>(static_cast<int>((w >> q4_shift(static_cast<uint32_t>(e))) & 15u) - 8);
-            return __fmul_rn(q, scale_at(e / 32));
+            return q * scale_at(e / 32);
         }
         case 5: {
             const uint32_t w = static_cast<const uint32_t*>(values)[e / 8];
             const float q = static_cast<float>((w >> q4_shift(static_cast<uint32_t>(e))) & 15u);
-            return __fadd_rn(__fmul_rn(q, scale_at(2 * (e / 32))), scale_at(2 * (e / 32) + 1));
+            return q * scale_at(2 * (e / 32)) + scale_at(2 * (e / 32) + 1);
         }
         case 6: {
             // q4_K: super-block sb of the row, sub-block j, position l.
@@ -193,7 +224,7 @@ __device__ __forceinline__ float weight_value(uint32_t type, uint32_t scale_type
             float s0, o0, s1, o1;
             q4k_scales(hdr, static_cast<uint32_t>(j / 2), s0, o0, s1, o1);
             const float s = (j % 2 == 0) ? s0 : s1, o = (j % 2 == 0) ? o0 : o1;
-            return __fadd_rn(__fmul_rn(static_cast<float>(code), s), o);
+            return static_cast<float>(code) * s + o;
         }
         default: return 0.0f;
     }

@@ -2,18 +2,26 @@
 // shaders/attend.comp + attend_merge.comp, src/ops/attention.cpp:54-84),
 // written for gfx950.
 //
-// The reference gives each (128-key chunk, query head) its own workgroup, so
-// with grouped-query attention every KV row is read once per query head of
-// its group. Here workgroup (s, g) owns split s of KV head g's keys and
-// computes all `group` query heads that share it, reading each K and V row
-// once: a key's row is spread over LPK lanes with 16-byte loads (f16 head_dim
-// 128: 16 lanes per key, 4 keys per wave64 per step), partial dot products
-// are summed across those lanes with shuffles, scores go to LDS, each
-// head's max and exp-sum come from wave reductions, and the weighted sum of
-// V reuses the same lane mapping. The merge combines the splits with the
-// online-softmax rescaling e^(m_s - M) and can quantize the result to Q8_0
-// for the o projection in the same pass.
+// Bit-exact by construction: keys are taken in the reference's chunks of 128
+// from kv_start, and every f32 value follows its order: each score sums four
+// partial dot products (vec4s i = g, g + 4, ... for part g) in turn
+// (attend.comp:97-116), the chunk's weight sum is the halving tree over 128
+// (:130-137), each output element sums weight * v over the chunk's keys in
+// key order, in head_dim-wide slices for heads narrower than 128 (:140-167),
+// and the merge walks the chunks in order (attend_merge.comp:30-38). exp is
+// vk_expf, which the CPU oracle shares.
+//
+// What changes is the mapping onto the machine. The reference gives each
+// (chunk, query head) a workgroup, so with grouped-query attention each K and
+// V row is read once per query head of its group; here workgroup (chunk, KV
+// head) computes all `group` query heads that share the KV head, reading each
+// row once. The chunk's V rows are loaded into registers while the scores are
+// computed and parked in LDS (rows up to 256 bytes), so the V pass waits on
+// no memory. Chunks past the live keys (the grid is sized by the cache, so a
+// replayed graph covers every position) write a max of -inf, which the merge
+// skips.
 #include <algorithm>
+#include <type_traits>
 
 #include "device.hpp"
 #include "internal.hpp"
@@ -23,32 +31,8 @@ using namespace vkml::dev;
 namespace {
 
 constexpr int kThreads = 256;
-constexpr uint32_t kMaxChunk = 1024;  // keys per split (LDS: group * chunk floats)
-
-template <int HD, bool F16>
-struct Layout {
-    static constexpr int kElemBytes = F16 ? 2 : 4;
-    static constexpr int kPerLane = 16 / kElemBytes;         // elements per 16-byte load
-    static constexpr int kLanesPerKey = HD * kElemBytes / 16;  // 4 .. 64
-    static constexpr int kKeysPerWave = kWave / kLanesPerKey;
-    static constexpr int kKeysPerStep = kKeysPerWave * (kThreads / kWave);
-};
-
-template <bool F16, int N>
-__device__ __forceinline__ void load_row(const void* base, uint64_t elem, float (&out)[N]) {
-    const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(base) + elem * (F16 ? 2 : 4));
-    if constexpr (F16) {
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            out[2 * i] = f16_bits_to_float(w[i] & 0xFFFFu);
-            out[2 * i + 1] = f16_bits_to_float(w[i] >> 16);
-        }
-    } else {
-        out[0] = __uint_as_float(v.x); out[1] = __uint_as_float(v.y);
-        out[2] = __uint_as_float(v.z); out[3] = __uint_as_float(v.w);
-    }
-}
+constexpr uint32_t kChunk = 128;  // attend.comp's CHUNK = WG
+constexpr int kLanes = 4;        // invocations per key while scoring
 
 struct AttendArgs {
     const float* q;
@@ -57,76 +41,128 @@ struct AttendArgs {
     float* partial;
     float* stats;
     const vkml_decode_state* state;
-    uint32_t kv_start, kv_len, capacity, splits;
+    uint32_t kv_start, kv_len, capacity, chunks;
     float scale, softcap;
 };
 
+// Four elements of a K row from vec4 index i, as stored (four f16, or four
+// f32), and widened exactly.
+template <bool F16>
+using KRaw = std::conditional_t<F16, uint2, float4>;
+
+template <bool F16>
+__device__ __forceinline__ KRaw<F16> load_k4(const void* base, uint64_t row_elem, uint32_t i) {
+    if constexpr (F16) return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + row_elem + 4 * i);
+    else return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + row_elem + 4 * i);
+}
+__device__ __forceinline__ float4 widen(uint2 w) {
+    return make_float4(f16_bits_to_float(w.x & 0xFFFFu), f16_bits_to_float(w.x >> 16),
+                       f16_bits_to_float(w.y & 0xFFFFu), f16_bits_to_float(w.y >> 16));
+}
+__device__ __forceinline__ float4 widen(float4 w) { return w; }
+
+// dot(a, b) as ((a.x b.x + a.y b.y) + a.z b.z) + a.w b.w.
+__device__ __forceinline__ float dot4f(float4 a, float4 b) {
+#pragma clang fp contract(off)
+    return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
 template <int HD, int G, bool F16>
 __global__ void __launch_bounds__(kThreads) k_attend(AttendArgs a) {
-    using L = Layout<HD, F16>;
-    constexpr int EPL = L::kPerLane, LPK = L::kLanesPerKey, KPW = L::kKeysPerWave, KPS = L::kKeysPerStep;
-    // Scores and weights [G][kMaxChunk]; after the V pass, the per-wave sums
-    // [waves][G][HD] reuse the same memory (HD <= 256 keeps them inside).
-    __shared__ float s_buf[G * kMaxChunk];
-    static_assert((kThreads / kWave) * HD <= kMaxChunk, "reduction space");
-    float (*s_p)[kMaxChunk] = reinterpret_cast<float (*)[kMaxChunk]>(s_buf);
-    float (*s_red)[G][HD] = reinterpret_cast<float (*)[G][HD]>(s_buf);
-    const uint32_t split = blockIdx.x, g = blockIdx.y;
-    const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t sub = lane % LPK, key_in_step = wave * KPW + lane / LPK;
+#pragma clang fp contract(off)
+    constexpr uint32_t EB = F16 ? 2 : 4;
+    constexpr uint32_t RB = HD * EB;                   // bytes per cache row
+    constexpr bool kStageV = RB <= 256;                // the chunk's V rows fit 32 KiB of LDS
+    constexpr uint32_t kVLoads = kStageV ? RB * kChunk / 16 / kThreads : 1;  // 16-byte loads per thread
+    constexpr uint32_t K4 = HD / 4;                    // vec4s per row
+    constexpr uint32_t KPL = K4 / kLanes;              // vec4s per lane per key
+    constexpr uint32_t kSlots = kThreads / kLanes;     // keys per scoring pass
+    constexpr uint32_t kPasses = kChunk / kSlots;
 
+    __shared__ float4 s_q[G][K4];
+    __shared__ float s_p[G][kChunk];      // scores, then weights
+    __shared__ float s_red[G][kChunk];    // per-slice sums of the V pass
+    __shared__ uint4 s_v[kStageV ? RB * kChunk / 16 : 1];
+    __shared__ float s_m[G], s_l[G];
+
+    const uint32_t chunk = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
     const uint32_t kv_len = a.state ? static_cast<uint32_t>(a.state->position) + 1u : a.kv_len;
-    const uint32_t total = kv_len > a.kv_start ? kv_len - a.kv_start : 0u;
-    const uint32_t chunk = (total + a.splits - 1) / a.splits;
-    const uint32_t k0 = a.kv_start + split * chunk;
-    const uint32_t n = k0 < kv_len ? min(chunk, kv_len - k0) : 0u;
-    const uint64_t row_base = static_cast<uint64_t>(g) * a.capacity;
-
-    // This lane's slice of each head's query.
-    float q[G][EPL];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        const float* qh = a.q + (static_cast<uint64_t>(g) * G + h) * HD + sub * EPL;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) q[h][e] = qh[e];
+    const uint32_t key0 = a.kv_start + chunk * kChunk;
+    const uint64_t head0 = static_cast<uint64_t>(g) * G;
+    if (key0 >= kv_len) {
+        // Past the live keys: nothing for the merge to take.
+        if (t < G) {
+            a.stats[((head0 + t) * a.chunks + chunk) * 2] = -__builtin_inff();
+            a.stats[((head0 + t) * a.chunks + chunk) * 2 + 1] = 0.0f;
+        }
+        return;
     }
+    const uint32_t n = min(kChunk, kv_len - key0);
+    const uint64_t kv_row0 = static_cast<uint64_t>(g) * a.capacity;
+    const auto row_elem = [&](uint32_t key) -> uint64_t { return (kv_row0 + (key0 + key) % a.capacity) * HD; };
 
-    // Scores.
-    for (uint32_t i = 0; i < n; i += KPS) {
-        const uint32_t key = i + key_in_step;
-        float part[G];
+    // Issue this thread's V loads first; they land while the scores are computed.
+    uint4 vreg[kVLoads];
+    if constexpr (kStageV) {
 #pragma unroll
-        for (int h = 0; h < G; ++h) part[h] = 0.0f;
-        if (key < n) {
-            float kf[EPL];
-            load_row<F16>(a.k, (row_base + (k0 + key) % a.capacity) * HD + sub * EPL, kf);
-#pragma unroll
-            for (int h = 0; h < G; ++h)
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) part[h] += q[h][e] * kf[e];
+        for (uint32_t j = 0; j < kVLoads; ++j) {
+            const uint32_t u = t + j * kThreads, key = u / (RB / 16), col = u % (RB / 16);
+            vreg[j] = key < n ? *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.v) + row_elem(key) * EB + 16 * col)
+                              : make_uint4(0, 0, 0, 0);
         }
+    }
+    // K: lane g of each key's four takes vec4s g, g + 4, ... of the row.
+    const uint32_t lane4 = t % kLanes, slot = t / kLanes;
+    KRaw<F16> kreg[kPasses][KPL];
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float s = group_sum<LPK>(part[h]) * a.scale;
-            if (a.softcap > 0.0f) s = a.softcap * tanhf(fminf(fmaxf(s / a.softcap, -10.0f), 10.0f));
-            if (key < n && sub == 0) s_p[h][key] = s;
-        }
+    for (uint32_t pass = 0; pass < kPasses; ++pass) {
+        const uint32_t key = pass * kSlots + slot;
+#pragma unroll
+        for (uint32_t j = 0; j < KPL; ++j) kreg[pass][j] = key < n ? load_k4<F16>(a.k, row_elem(key), lane4 + kLanes * j) : KRaw<F16>{};
+    }
+    for (uint32_t i = t; i < G * K4; i += kThreads) {
+        const float* qh = a.q + (head0 + i / K4) * HD + 4 * (i % K4);
+        s_q[i / K4][i % K4] = make_float4(qh[0], qh[1], qh[2], qh[3]);
     }
     __syncthreads();
 
-    // Per head: max score and the weights e^(s - m), summed.
-    __shared__ float s_m[G], s_l[G];
-    for (int h = wave; h < G; h += kThreads / kWave) {
-        float m = -__builtin_inff();
-        for (uint32_t k = lane; k < n; k += kWave) m = fmaxf(m, s_p[h][k]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (uint32_t k = lane; k < n; k += kWave) {
-            const float p = expf(s_p[h][k] - m);
-            s_p[h][k] = p;
-            l += p;
+    // Scores: part g, then ((0 + part0) + part1) + part2) + part3 in the key's first lane.
+#pragma unroll
+    for (uint32_t pass = 0; pass < kPasses; ++pass) {
+        const uint32_t key = pass * kSlots + slot;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float part = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < KPL; ++j) part += dot4f(s_q[h][lane4 + kLanes * j], widen(kreg[pass][j]));
+            const float p1 = __shfl_down(part, 1, kWave), p2 = __shfl_down(part, 2, kWave), p3 = __shfl_down(part, 3, kWave);
+            if (lane4 == 0 && key < n) {
+                const float dot_qk = 0.0f + part + p1 + p2 + p3;
+                const float s = dot_qk * a.scale;
+                s_p[h][key] = a.softcap > 0.0f ? a.softcap * tanhf(fminf(fmaxf(s / a.softcap, -10.0f), 10.0f)) : s;
+            }
         }
-        l = wave_sum(l);
+    }
+    if constexpr (kStageV) {
+#pragma unroll
+        for (uint32_t j = 0; j < kVLoads; ++j) s_v[t + j * kThreads] = vreg[j];
+    }
+    __syncthreads();
+
+    // Per head (a wave each): the max, each key's weight, and their sum by the
+    // halving tree: lane k first adds keys k and k + 64, then strides 32 .. 1.
+    const uint32_t wave = t / kWave, lane = t % kWave;
+    for (int h = wave; h < G; h += kThreads / kWave) {
+        const float s0 = lane < n ? s_p[h][lane] : -__builtin_inff();
+        const float s1 = lane + 64 < n ? s_p[h][lane + 64] : -__builtin_inff();
+        const float m = wave_max(fmaxf(s0, s1));
+        const float w0 = lane < n ? vk_expf(s0 - m) : 0.0f;
+        const float w1 = lane + 64 < n ? vk_expf(s1 - m) : 0.0f;
+        s_p[h][lane] = w0;
+        s_p[h][lane + 64] = w1;
+        float l = w0 + w1;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, kWave);
         if (lane == 0) {
             s_m[h] = m;
             s_l[h] = l;
@@ -134,80 +170,89 @@ __global__ void __launch_bounds__(kThreads) k_attend(AttendArgs a) {
     }
     __syncthreads();
 
-    // Weighted sum of V.
-    float acc[G][EPL];
+    const auto v_at = [&](uint32_t key, uint32_t d) -> float {
+        if constexpr (kStageV) {
+            if constexpr (F16) return f16_bits_to_float(reinterpret_cast<const uint16_t*>(s_v)[key * HD + d]);
+            else return reinterpret_cast<const float*>(s_v)[key * HD + d];
+        } else {
+            if constexpr (F16) return f16_bits_to_float(static_cast<const uint16_t*>(a.v)[row_elem(key) + d]);
+            else return static_cast<const float*>(a.v)[row_elem(key) + d];
+        }
+    };
+    const uint64_t out0 = head0 * a.chunks + chunk;  // (head0, chunk) in [heads, chunks]
+    if constexpr (HD > kChunk) {
+        // Heads wider than the workgroup of 128: element d over every key.
+        for (uint32_t d = t; d < HD; d += kThreads) {
+            float o[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+            for (int h = 0; h < G; ++h) o[h] = 0.0f;
+            for (uint32_t key = 0; key < n; ++key) {
+                const float v = v_at(key, d);
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[h][e] = 0.0f;
-    for (uint32_t i = 0; i < n; i += KPS) {
-        const uint32_t key = i + key_in_step;
-        if (key < n) {
-            float vf[EPL];
-            load_row<F16>(a.v, (row_base + (k0 + key) % a.capacity) * HD + sub * EPL, vf);
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float p = s_p[h][key];
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) acc[h][e] += p * vf[e];
+                for (int h = 0; h < G; ++h) o[h] += s_p[h][key] * v;
             }
+#pragma unroll
+            for (int h = 0; h < G; ++h) a.partial[(out0 + static_cast<uint64_t>(h) * a.chunks) * HD + d] = o[h];
+        }
+    } else {
+        // 128 / HD slices; slice i takes keys i, i + slices, ...; thread t
+        // computes slot t % 128 for heads t / 128, t / 128 + 2, ...
+        constexpr uint32_t slices = kChunk / HD;
+        const uint32_t c = t % kChunk, d = c % HD, sl = c / HD;
+        constexpr int HPT = G >= 2 ? G / 2 : 1;
+        const int h0 = static_cast<int>(t / kChunk);
+        if (G >= 2 || h0 == 0) {
+            float o[HPT];
+#pragma unroll
+            for (int j = 0; j < HPT; ++j) o[j] = 0.0f;
+            for (uint32_t key = sl; key < n; key += slices) {
+                const float v = v_at(key, d);
+#pragma unroll
+                for (int j = 0; j < HPT; ++j) o[j] += s_p[h0 + 2 * j][key] * v;
+            }
+#pragma unroll
+            for (int j = 0; j < HPT; ++j) s_red[h0 + 2 * j][c] = o[j];
+        }
+        __syncthreads();
+        for (uint32_t i = t; i < G * HD; i += kThreads) {
+            const uint32_t h = i / HD, e = i % HD;
+            float sum = 0.0f;
+#pragma unroll
+            for (uint32_t s = 0; s < slices; ++s) sum += s_red[h][s * HD + e];
+            a.partial[(out0 + static_cast<uint64_t>(h) * a.chunks) * HD + e] = sum;
         }
     }
-    // Sum the keys of this wave (lanes sub, sub + LPK, ...), then the waves.
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float v = acc[h][e];
-#pragma unroll
-            for (int o = LPK; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
-            acc[h][e] = v;
-        }
-    __syncthreads();  // every wave is done reading the weights in s_buf
-    if (lane < LPK) {
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) s_red[wave][h][sub * EPL + e] = acc[h][e];
-    }
-    __syncthreads();
-    const uint64_t out_base = (static_cast<uint64_t>(g) * a.splits + split) * G;
-    for (uint32_t i = threadIdx.x; i < G * HD; i += kThreads) {
-        const uint32_t h = i / HD, d = i % HD;
-        float s = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kThreads / kWave; ++w) s += s_red[w][h][d];
-        a.partial[(out_base + h) * HD + d] = s;
-    }
-    if (threadIdx.x < G) {
-        a.stats[(out_base + threadIdx.x) * 2] = s_m[threadIdx.x];
-        a.stats[(out_base + threadIdx.x) * 2 + 1] = s_l[threadIdx.x];
+    if (t < G) {
+        a.stats[(out0 + static_cast<uint64_t>(t) * a.chunks) * 2] = s_m[t];
+        a.stats[(out0 + static_cast<uint64_t>(t) * a.chunks) * 2 + 1] = s_l[t];
     }
 }
 
-// One block per query head, head_dim threads.
+// attend_merge.comp:25-38 for head blockIdx.x, element threadIdx.x; chunks
+// with a max of -inf hold no keys and are skipped. Optionally quantizes the
+// result to Q8_0 with f32 scales (quantize.comp:210-221), the o projection's
+// input.
 __global__ void k_attend_merge(const float* partial, const float* stats, float* out, uint8_t* values, float* scales,
-                               uint32_t splits, uint32_t group, uint32_t hd) {
+                               uint32_t chunks, uint32_t hd) {
+#pragma clang fp contract(off)
     const uint32_t h = blockIdx.x, d = threadIdx.x;
-    const uint32_t g = h / group, hh = h % group;
-    float top = -__builtin_inff();
-    for (uint32_t s = 0; s < splits; ++s) top = fmaxf(top, stats[((static_cast<uint64_t>(g) * splits + s) * group + hh) * 2]);
+    const uint64_t first = static_cast<uint64_t>(h) * chunks;
+    float top = stats[first * 2];
+    for (uint32_t c = 1; c < chunks; ++c) top = fmaxf(top, stats[(first + c) * 2]);
     float sum = 0.0f, weight = 0.0f;
-    for (uint32_t s = 0; s < splits; ++s) {
-        const uint64_t at = (static_cast<uint64_t>(g) * splits + s) * group + hh;
-        const float m = stats[at * 2];
-        if (m == -__builtin_inff()) continue;  // an empty split
-        const float r = expf(m - top);
-        sum += r * partial[at * hd + d];
-        weight += r * stats[at * 2 + 1];
+    for (uint32_t c = 0; c < chunks; ++c) {
+        const float m = stats[(first + c) * 2];
+        if (m == -__builtin_inff()) continue;
+        const float r = vk_expf(m - top);
+        sum += r * partial[(first + c) * hd + d];
+        weight += r * stats[(first + c) * 2 + 1];
     }
     const float o = sum / weight;
     out[static_cast<uint64_t>(h) * hd + d] = o;
     if (values) {
-        // Q8_0 with f32 scales over 32-value blocks (quantize.comp:210-221).
         const float absmax = group_max<32>(fabsf(o));
         const float ds = absmax / 127.0f;
-        const float inv = ds > 0.0f ? 1.0f / ds : 0.0f;
+        const float inv = ds != 0.0f ? 1.0f / ds : 0.0f;
         values[static_cast<uint64_t>(h) * hd + d] = static_cast<uint8_t>(static_cast<int8_t>(quant_code(o, inv)));
         if (d % 32 == 0) scales[(static_cast<uint64_t>(h) * hd + d) / 32] = ds;
     }
@@ -226,6 +271,17 @@ int launch_group(uint32_t group, dim3 grid, const AttendArgs& args) {
     return VKML_OK;
 }
 
+int check_layout(const vkml_attend_params* p, const char* what) {
+    VKML_CHECK_ARG(p, std::string(what) + ": null params");
+    VKML_CHECK_ARG(p->kv_heads > 0 && p->heads % p->kv_heads == 0,
+                   std::string(what) + ": q's " + std::to_string(p->heads) + " heads must be a multiple of k and v's " +
+                       std::to_string(p->kv_heads));
+    VKML_CHECK_ARG(p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256,
+                   std::string(what) + ": head_dim " + std::to_string(p->head_dim) + " is not 64, 128 or 256");
+    VKML_CHECK_ARG(p->chunks > 0, std::string(what) + ": chunks must be positive");
+    return VKML_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -233,21 +289,19 @@ extern "C" {
 int vkml_attend(const vkml_attend_params* p, const float* q, const void* k_cache, const void* v_cache,
                 float* partial, float* stats, const vkml_decode_state* state) {
     VKML_REQUIRE_INIT();
-    VKML_CHECK_ARG(p, "attend: null params");
-    VKML_CHECK_ARG(p->kv_heads > 0 && p->heads % p->kv_heads == 0,
-                   "attend: q's " + std::to_string(p->heads) + " heads must be a multiple of k and v's " + std::to_string(p->kv_heads));
-    VKML_CHECK_ARG(p->head_dim == 64 || p->head_dim == 128 || p->head_dim == 256,
-                   "attend: head_dim " + std::to_string(p->head_dim) + " is not 64, 128 or 256");
+    if (int r = check_layout(p, "attend")) return r;
     VKML_CHECK_ARG(p->kv_type == VKML_F16 || p->kv_type == VKML_F32, "attend: caches must be f16 or f32");
-    VKML_CHECK_ARG(p->splits > 0 && p->capacity > 0, "attend: splits and capacity must be positive");
+    VKML_CHECK_ARG(p->capacity > 0 && p->kv_start < p->capacity, "attend: kv_start must lie inside the cache");
     VKML_CHECK_ARG(state || (p->kv_len <= p->capacity && p->kv_start < p->kv_len),
                    "attend: keys " + std::to_string(p->kv_start) + ".." + std::to_string(p->kv_len) + " do not fit the cache");
-    // Every split must fit LDS: splits * kMaxChunk covers the longest range.
-    VKML_CHECK_ARG(static_cast<uint64_t>(p->splits) * kMaxChunk >= (state ? p->capacity : p->kv_len - p->kv_start),
-                   "attend: " + std::to_string(p->splits) + " splits leave more than " + std::to_string(kMaxChunk) + " keys per split");
+    // With a decode state, kv_len can reach the capacity: cover every chunk of it.
+    const uint64_t keys = state ? p->capacity - p->kv_start : p->kv_len - p->kv_start;
+    VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= keys,
+                   "attend: " + std::to_string(p->chunks) + " chunks of " + std::to_string(kChunk) + " keys do not cover " +
+                       std::to_string(keys) + " keys");
     VKML_CHECK_ARG(q && k_cache && v_cache && partial && stats, "attend: null buffer");
-    AttendArgs args{q, k_cache, v_cache, partial, stats, state, p->kv_start, p->kv_len, p->capacity, p->splits, p->scale, p->softcap};
-    const dim3 grid(p->splits, p->kv_heads);
+    AttendArgs args{q, k_cache, v_cache, partial, stats, state, p->kv_start, p->kv_len, p->capacity, p->chunks, p->scale, p->softcap};
+    const dim3 grid(p->chunks, p->kv_heads);
     const uint32_t group = p->heads / p->kv_heads;
     const bool f16 = p->kv_type == VKML_F16;
     vkml::abi::ProfileScope prof("attend");
@@ -264,13 +318,12 @@ int vkml_attend(const vkml_attend_params* p, const float* q, const void* k_cache
 int vkml_attend_merge(const vkml_attend_params* p, const float* partial, const float* stats, float* out, void* values,
                       float* scales) {
     VKML_REQUIRE_INIT();
-    VKML_CHECK_ARG(p && partial && stats && out, "attend_merge: null argument");
-    VKML_CHECK_ARG(p->kv_heads > 0 && p->heads % p->kv_heads == 0 && p->head_dim % 32 == 0 && p->head_dim <= 1024,
-                   "attend_merge: bad head layout");
+    if (int r = check_layout(p, "attend_merge")) return r;
+    VKML_CHECK_ARG(partial && stats && out, "attend_merge: null buffer");
     VKML_CHECK_ARG(!values || scales, "attend_merge: quantized output needs scales");
     vkml::abi::ProfileScope prof("attend_merge");
     hipLaunchKernelGGL(k_attend_merge, dim3(p->heads), dim3(p->head_dim), 0, vkml::abi::stream(), partial, stats, out,
-                       static_cast<uint8_t*>(values), scales, p->splits, p->heads / p->kv_heads, p->head_dim);
+                       static_cast<uint8_t*>(values), scales, p->chunks, p->head_dim);
     return vkml::abi::check_launch("attend_merge");
 }
 

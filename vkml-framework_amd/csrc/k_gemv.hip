@@ -1,18 +1,23 @@
 // k_gemv.hip -- quantized matrix-vector products for decoding (the
 // reference's shaders/gemv_dot.comp and gemv.comp), written for gfx950.
 //
-// int8 path (vkml_gemv_dot*): each workgroup stages the Q8_0 activation
-// vector once in LDS (codes plus, per 32-value block, its f32 scale and the
-// sum of its codes), then each wave64 computes RPW rows. A row is cut into
-// 64-value tasks; lane l takes tasks l, l + 64, ...: per task it loads the
-// weights with 128-bit loads (64 B of q8_0 codes, or 32 B of 4-bit codes)
-// plus the task's scales (an f16 pair, (scale, offset) pairs, or q4_K's
-// 16-byte super-block header), multiplies with v_dot4_i32_i8 against the
-// staged activations, and scales each 32-value block's exact integer sum in
-// f32 as the reference's matmul_dot.comp does (acc += sa * (D * s + S * o)
-// for q4_1/q4_K, D * (s * sa) for q8_0). A wave reduction then sums the
-// lanes, and the epilogue stores, adds the residual, or applies SwiGLU.
-// There is no MFMA here: these are matrix-vector products, bound by HBM.
+// Bit-exact by construction. The reference sums each output over 32
+// accumulators: accumulator l takes the terms of half-blocks (16 values) l,
+// l + 32, l + 64, ... in that order, each term an exact int8 dot product
+// scaled in f32 (gemv_dot.comp:349-363), and the 32 are added in a halving
+// tree (:370-375). Every f32 operation here happens in that order, so the
+// outputs are the reference's bits, and the Q8_0 codes the next layer
+// quantizes from them are too.
+//
+// The 32 accumulators of a row live in 8 lanes, 4 each: lane j takes the
+// 64-value tasks c = j, j + 8, ..., whose half-blocks 4c .. 4c + 3 are
+// exactly accumulators 4j .. 4j + 3. So each lane still streams its weights
+// with 128-bit loads (32 B of 4-bit codes, or 64 B of q8_0, plus the task's
+// scales or q4_K's 16-byte header), a wave64 covers 8 rows, and the tree's
+// strides 16, 8 and 4 are lane exchanges within the 8-lane group, 2 and 1
+// additions within a lane. The activation vector is staged once per
+// workgroup in LDS with each half-block's code sum. No MFMA: these are
+// matrix-vector products, bound by HBM.
 #include <algorithm>
 
 #include "device.hpp"
@@ -22,8 +27,7 @@ using namespace vkml::dev;
 
 namespace {
 
-constexpr uint32_t kMaxK = 32768;  // LDS staging: K + K / 4 bytes
-constexpr int kThreads = 256;
+constexpr uint32_t kMaxK = 32768;  // LDS staging: K + K / 16 * 4 + K / 32 * 4 bytes
 
 struct GemvArgs {
     const uint4* a_values;  // K bytes of activation codes
@@ -68,146 +72,163 @@ __device__ __forceinline__ void load_task(const void* bv, const void* bs, uint32
 
 constexpr uint32_t kLow = 0x0F0F0F0Fu;
 
-// Low (shift 0) or high (shift 4) nibbles of a 32-value block of
-// QuantizedMatrix q4 words (byte j: value j, high nibble value j + 4) dotted
-// with the block's 32 activation codes a0, a1.
-__device__ __forceinline__ int q4_block_dot(uint4 q, uint4 a0, uint4 a1) {
-    int d = dot4(q.x & kLow, a0.x, 0);
-    d = dot4((q.x >> 4) & kLow, a0.y, d);
-    d = dot4(q.y & kLow, a0.z, d);
-    d = dot4((q.y >> 4) & kLow, a0.w, d);
-    d = dot4(q.z & kLow, a1.x, d);
-    d = dot4((q.z >> 4) & kLow, a1.y, d);
-    d = dot4(q.w & kLow, a1.z, d);
-    d = dot4((q.w >> 4) & kLow, a1.w, d);
-    return d;
+// The exact dot product of one half-block: 16 weight codes as bytes (four
+// words) with 16 activation codes (gemv_dot.comp:352-353).
+__device__ __forceinline__ int half_dot(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint4 a) {
+    return dot4(w3, a.w, dot4(w2, a.z, dot4(w1, a.y, dot4(w0, a.x, 0))));
 }
 
+// Adds the task's four half-block terms to acc[0..3] with the reference's
+// expressions (gemv_dot.comp:354-362): q8_0/q4_0 float(d) * (scale * sa);
+// q4_1 (and q4_K, whose sub-blocks are q4_1's) sa * (float(d) * scale +
+// float(sum) * offset). S holds each half-block's activation code sum, sa
+// the two blocks' activation scales.
 template <int FMT, bool F16S>
-__device__ __forceinline__ float task_dot(const Wt& w, uint32_t t, const uint4 (&a)[4], float4 bi) {
-    // bi: (sa0, S0, sa1, S1) for the task's two activation blocks.
+__device__ __forceinline__ void task_terms(const Wt& w, uint32_t t, const uint4 (&a)[4], float4 S, float2 sa, float (&acc)[4]) {
+#pragma clang fp contract(off)
+    int d[4];
+    float s0, s1, o0 = 0.0f, o1 = 0.0f;
     if constexpr (FMT == VKML_Q8_0) {
-        int d0 = dot4(w.q[0].x, a[0].x, 0); d0 = dot4(w.q[0].y, a[0].y, d0); d0 = dot4(w.q[0].z, a[0].z, d0); d0 = dot4(w.q[0].w, a[0].w, d0);
-        d0 = dot4(w.q[1].x, a[1].x, d0); d0 = dot4(w.q[1].y, a[1].y, d0); d0 = dot4(w.q[1].z, a[1].z, d0); d0 = dot4(w.q[1].w, a[1].w, d0);
-        int d1 = dot4(w.q[2].x, a[2].x, 0); d1 = dot4(w.q[2].y, a[2].y, d1); d1 = dot4(w.q[2].z, a[2].z, d1); d1 = dot4(w.q[2].w, a[2].w, d1);
-        d1 = dot4(w.q[3].x, a[3].x, d1); d1 = dot4(w.q[3].y, a[3].y, d1); d1 = dot4(w.q[3].z, a[3].z, d1); d1 = dot4(w.q[3].w, a[3].w, d1);
-        float s0, s1;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) d[h] = half_dot(w.q[h].x, w.q[h].y, w.q[h].z, w.q[h].w, a[h]);
         if constexpr (F16S) { s0 = f16_bits_to_float(w.s.x & 0xFFFFu); s1 = f16_bits_to_float(w.s.x >> 16); }
         else { s0 = __uint_as_float(w.s.x); s1 = __uint_as_float(w.s.y); }
-        return static_cast<float>(d0) * (s0 * bi.x) + static_cast<float>(d1) * (s1 * bi.z);
     } else if constexpr (FMT == VKML_Q4_K) {
-        // Bytes 32c..32c+31 of the super-block's codes: low nibbles are
+        // Bytes 32c .. 32c + 31 of the super-block's codes: low nibbles are
         // sub-block 2c, high nibbles sub-block 2c + 1, each in value order.
-        int d0 = dot4(w.q[0].x & kLow, a[0].x, 0); d0 = dot4(w.q[0].y & kLow, a[0].y, d0);
-        d0 = dot4(w.q[0].z & kLow, a[0].z, d0); d0 = dot4(w.q[0].w & kLow, a[0].w, d0);
-        d0 = dot4(w.q[1].x & kLow, a[1].x, d0); d0 = dot4(w.q[1].y & kLow, a[1].y, d0);
-        d0 = dot4(w.q[1].z & kLow, a[1].z, d0); d0 = dot4(w.q[1].w & kLow, a[1].w, d0);
-        int d1 = dot4((w.q[0].x >> 4) & kLow, a[2].x, 0); d1 = dot4((w.q[0].y >> 4) & kLow, a[2].y, d1);
-        d1 = dot4((w.q[0].z >> 4) & kLow, a[2].z, d1); d1 = dot4((w.q[0].w >> 4) & kLow, a[2].w, d1);
-        d1 = dot4((w.q[1].x >> 4) & kLow, a[3].x, d1); d1 = dot4((w.q[1].y >> 4) & kLow, a[3].y, d1);
-        d1 = dot4((w.q[1].z >> 4) & kLow, a[3].z, d1); d1 = dot4((w.q[1].w >> 4) & kLow, a[3].w, d1);
-        float s0, o0, s1, o1;
+        const uint4 q0 = w.q[0], q1 = w.q[1];
+        d[0] = half_dot(q0.x & kLow, q0.y & kLow, q0.z & kLow, q0.w & kLow, a[0]);
+        d[1] = half_dot(q1.x & kLow, q1.y & kLow, q1.z & kLow, q1.w & kLow, a[1]);
+        d[2] = half_dot((q0.x >> 4) & kLow, (q0.y >> 4) & kLow, (q0.z >> 4) & kLow, (q0.w >> 4) & kLow, a[2]);
+        d[3] = half_dot((q1.x >> 4) & kLow, (q1.y >> 4) & kLow, (q1.z >> 4) & kLow, (q1.w >> 4) & kLow, a[3]);
         q4k_scales(w.s, t & 3u, s0, o0, s1, o1);
-        return bi.x * (static_cast<float>(d0) * s0 + bi.y * o0) + bi.z * (static_cast<float>(d1) * s1 + bi.w * o1);
     } else {
-        const int d0 = q4_block_dot(w.q[0], a[0], a[1]);
-        const int d1 = q4_block_dot(w.q[1], a[2], a[3]);
+        // QuantizedMatrix q4 words: byte j holds value j (low) and j + 4 (high).
+        const uint4 q0 = w.q[0], q1 = w.q[1];
+        d[0] = half_dot(q0.x & kLow, (q0.x >> 4) & kLow, q0.y & kLow, (q0.y >> 4) & kLow, a[0]);
+        d[1] = half_dot(q0.z & kLow, (q0.z >> 4) & kLow, q0.w & kLow, (q0.w >> 4) & kLow, a[1]);
+        d[2] = half_dot(q1.x & kLow, (q1.x >> 4) & kLow, q1.y & kLow, (q1.y >> 4) & kLow, a[2]);
+        d[3] = half_dot(q1.z & kLow, (q1.z >> 4) & kLow, q1.w & kLow, (q1.w >> 4) & kLow, a[3]);
         if constexpr (FMT == VKML_Q4_1) {
-            float s0, o0, s1, o1;
             if constexpr (F16S) {
                 s0 = f16_bits_to_float(w.s.x & 0xFFFFu); o0 = f16_bits_to_float(w.s.x >> 16);
                 s1 = f16_bits_to_float(w.s.y & 0xFFFFu); o1 = f16_bits_to_float(w.s.y >> 16);
             } else {
                 s0 = __uint_as_float(w.s.x); o0 = __uint_as_float(w.s.y); s1 = __uint_as_float(w.s.z); o1 = __uint_as_float(w.s.w);
             }
-            return bi.x * (static_cast<float>(d0) * s0 + bi.y * o0) + bi.z * (static_cast<float>(d1) * s1 + bi.w * o1);
-        } else {  // q4_0: codes are q + 8
-            float s0, s1;
+        } else {
             if constexpr (F16S) { s0 = f16_bits_to_float(w.s.x & 0xFFFFu); s1 = f16_bits_to_float(w.s.x >> 16); }
             else { s0 = __uint_as_float(w.s.x); s1 = __uint_as_float(w.s.y); }
-            const int e0 = d0 - 8 * static_cast<int>(bi.y), e1 = d1 - 8 * static_cast<int>(bi.w);
-            return static_cast<float>(e0) * (s0 * bi.x) + static_cast<float>(e1) * (s1 * bi.z);
+            // q4_0 codes are q + 8: the reference's signed bytes q4_bytes give
+            // the same exact sum, d - 8 * sum(a).
+            d[0] -= 8 * static_cast<int>(S.x); d[1] -= 8 * static_cast<int>(S.y);
+            d[2] -= 8 * static_cast<int>(S.z); d[3] -= 8 * static_cast<int>(S.w);
+        }
+    }
+    const float sum[4] = {S.x, S.y, S.z, S.w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const float scale = h < 2 ? s0 : s1, a_scale = h < 2 ? sa.x : sa.y;
+        if constexpr (FMT == VKML_Q4_1 || FMT == VKML_Q4_K) {
+            const float offset = h < 2 ? o0 : o1;
+            acc[h] += a_scale * (static_cast<float>(d[h]) * scale + sum[h] * offset);
+        } else {
+            acc[h] += static_cast<float>(d[h]) * (scale * a_scale);
         }
     }
 }
 
+// The halving tree over the 32 accumulators of the 8-lane group; the row's
+// sum ends in lane 0 of the group (gemv_dot.comp:370-375).
+__device__ __forceinline__ float tree32(float (&acc)[4]) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) acc[h] += __shfl_xor(acc[h], off, kWave);
+    acc[0] += acc[2];
+    acc[1] += acc[3];
+    return acc[0] + acc[1];
+}
+
 enum { kStore = 0, kAdd = 1, kSwiglu = 2 };
 
-template <int FMT, bool F16S, int RPW, int EPI>
-__global__ void __launch_bounds__(kThreads) k_gemv_dot(GemvArgs g) {
+template <int FMT, bool F16S, int EPI>
+__global__ void __launch_bounds__(256) k_gemv_dot(GemvArgs g) {
+#pragma clang fp contract(off)
     extern __shared__ uint4 smem[];
     const uint32_t K = g.k;
-    uint4* s_codes = smem;
-    float2* s_info = reinterpret_cast<float2*>(smem + K / 16);
-    for (uint32_t b = threadIdx.x; b < K / 32; b += kThreads) {
-        const uint4 c0 = g.a_values[2 * b], c1 = g.a_values[2 * b + 1];
-        s_codes[2 * b] = c0;
-        s_codes[2 * b + 1] = c1;
-        s_info[b] = make_float2(g.a_scales[b], static_cast<float>(byte_sum(c0) + byte_sum(c1)));
+    uint4* s_codes = smem;                                   // K / 16 half-blocks of codes
+    float* s_sum = reinterpret_cast<float*>(smem + K / 16);  // each half-block's code sum
+    float* s_sa = s_sum + K / 16;                            // each block's activation scale
+    for (uint32_t h = threadIdx.x; h < K / 16; h += blockDim.x) {
+        const uint4 c = g.a_values[h];
+        s_codes[h] = c;
+        s_sum[h] = static_cast<float>(byte_sum(c));
+        if (h % 2 == 0) s_sa[h / 2] = g.a_scales[h / 2];
     }
     __syncthreads();
-    const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t row0 = (blockIdx.x * (kThreads / kWave) + wave) * RPW;
-    if (row0 >= g.n) return;
+    const uint32_t lane8 = threadIdx.x % 8;
+    const uint32_t row = blockIdx.x * (blockDim.x / 8) + threadIdx.x / 8;
+    const uint32_t r = min(row, g.n - 1);
     constexpr int NM = EPI == kSwiglu ? 2 : 1;
-    float acc[NM][RPW];
+    constexpr int U = (FMT == VKML_Q8_0 || NM == 2) ? 2 : 4;  // tasks in flight per lane
+    float acc[NM][4];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[m][r] = 0.0f;
+        for (int h = 0; h < 4; ++h) acc[m][h] = 0.0f;
     const uint32_t tasks = K / 64;
-    const float4* info4 = reinterpret_cast<const float4*>(s_info);
-    for (uint32_t t = lane; t < tasks; t += kWave) {
-        Wt w[NM][RPW];
+    const float4* sum4 = reinterpret_cast<const float4*>(s_sum);
+    const float2* sa2 = reinterpret_cast<const float2*>(s_sa);
+    for (uint32_t t0 = lane8; t0 < tasks; t0 += 8 * U) {
+        Wt w[U][NM];
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const uint32_t row = min(row0 + r, g.n - 1);
-            load_task<FMT, F16S>(g.b_values, g.b_scales, K, row, t, w[0][r]);
-            if constexpr (EPI == kSwiglu) load_task<FMT, F16S>(g.b2_values, g.b2_scales, K, row, t, w[NM - 1][r]);
-        }
-        const uint4 a[4] = {s_codes[4 * t], s_codes[4 * t + 1], s_codes[4 * t + 2], s_codes[4 * t + 3]};
-        const float4 bi = info4[t];
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) acc[m][r] += task_dot<FMT, F16S>(w[m][r], t, a, bi);
-    }
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[m][r] = wave_sum(acc[m][r]);
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const uint32_t row = row0 + r;
-            if (row >= g.n) break;
-            if constexpr (EPI == kStore) {
-                g.out[row] = acc[0][r];
-            } else if constexpr (EPI == kAdd) {
-                g.out[row] = g.residual[row] + acc[0][r];
-            } else {
-                const float gate = acc[0][r], up = acc[NM - 1][r];
-                g.out[row] = gate / (1.0f + expf(-gate)) * up;
+        for (int u = 0; u < U; ++u) {
+            const uint32_t t = t0 + 8 * u;
+            if (t < tasks) {
+                load_task<FMT, F16S>(g.b_values, g.b_scales, K, r, t, w[u][0]);
+                if constexpr (NM == 2) load_task<FMT, F16S>(g.b2_values, g.b2_scales, K, r, t, w[u][NM - 1]);
             }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t t = t0 + 8 * u;
+            if (t < tasks) {
+                const uint4 a[4] = {s_codes[4 * t], s_codes[4 * t + 1], s_codes[4 * t + 2], s_codes[4 * t + 3]};
+                const float4 S = sum4[t];
+                const float2 sa = sa2[t];
+#pragma unroll
+                for (int m = 0; m < NM; ++m) task_terms<FMT, F16S>(w[u][m], t, a, S, sa, acc[m]);
+            }
+        }
+    }
+    float y[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) y[m] = tree32(acc[m]);
+    if (lane8 == 0 && row < g.n) {
+        if constexpr (EPI == kStore) {
+            g.out[row] = y[0];
+        } else if constexpr (EPI == kAdd) {
+            g.out[row] = g.residual[row] + y[0];  // add(x, attn_out), llama.cpp:374,386
+        } else {
+            // silu(gate) * up (unary.comp:21-24, then binary.comp's mul)
+            const float gate = y[0], up = y[NM - 1];
+            g.out[row] = gate / (1.0f + vk_expf(-gate)) * up;
         }
     }
 }
 
 template <int FMT, bool F16S, int EPI>
-int dispatch_rpw(const GemvArgs& g, const char* label) {
-    // Rows per wave: enough workgroups to cover the CUs a few times over.
+int dispatch(const GemvArgs& g, const char* label) {
+    // Rows per workgroup (8 per wave): enough workgroups to cover the CUs twice.
     const uint32_t cus = std::max<uint32_t>(vkml::abi::compute_units(), 1);
-    int rpw = 4;
-    while (rpw > 1 && (g.n + 4u * rpw - 1) / (4u * rpw) < 2 * cus) rpw /= 2;
-    const uint32_t rows_per_block = 4u * rpw;
-    const dim3 grid((g.n + rows_per_block - 1) / rows_per_block);
-    const size_t lds = g.k + g.k / 32 * 8;
+    uint32_t threads = 256;
+    while (threads > 64 && (g.n + threads / 8 - 1) / (threads / 8) < 2 * cus) threads /= 2;
+    const dim3 grid((g.n + threads / 8 - 1) / (threads / 8));
+    const size_t lds = g.k + g.k / 16 * 4 + g.k / 32 * 4;
     vkml::abi::ProfileScope prof(label);
-    switch (rpw) {
-        case 4: hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, 4, EPI>), grid, dim3(kThreads), lds, vkml::abi::stream(), g); break;
-        case 2: hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, 2, EPI>), grid, dim3(kThreads), lds, vkml::abi::stream(), g); break;
-        default: hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, 1, EPI>), grid, dim3(kThreads), lds, vkml::abi::stream(), g); break;
-    }
+    hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, EPI>), grid, dim3(threads), lds, vkml::abi::stream(), g);
     return vkml::abi::check_launch(label);
 }
 
@@ -215,10 +236,10 @@ template <int EPI>
 int dispatch_format(uint32_t b_type, uint32_t scale_type, const GemvArgs& g, const char* label) {
     const bool f16 = scale_type == VKML_F16;
     switch (b_type) {
-        case VKML_Q8_0: return f16 ? dispatch_rpw<VKML_Q8_0, true, EPI>(g, label) : dispatch_rpw<VKML_Q8_0, false, EPI>(g, label);
-        case VKML_Q4_0: return f16 ? dispatch_rpw<VKML_Q4_0, true, EPI>(g, label) : dispatch_rpw<VKML_Q4_0, false, EPI>(g, label);
-        case VKML_Q4_1: return f16 ? dispatch_rpw<VKML_Q4_1, true, EPI>(g, label) : dispatch_rpw<VKML_Q4_1, false, EPI>(g, label);
-        case VKML_Q4_K: return dispatch_rpw<VKML_Q4_K, true, EPI>(g, label);
+        case VKML_Q8_0: return f16 ? dispatch<VKML_Q8_0, true, EPI>(g, label) : dispatch<VKML_Q8_0, false, EPI>(g, label);
+        case VKML_Q4_0: return f16 ? dispatch<VKML_Q4_0, true, EPI>(g, label) : dispatch<VKML_Q4_0, false, EPI>(g, label);
+        case VKML_Q4_1: return f16 ? dispatch<VKML_Q4_1, true, EPI>(g, label) : dispatch<VKML_Q4_1, false, EPI>(g, label);
+        case VKML_Q4_K: return dispatch<VKML_Q4_K, true, EPI>(g, label);
         default: return vkml::abi::fail(VKML_ERROR_UNSUPPORTED, std::string(label) + ": no int8 kernel for weight type " + std::to_string(b_type));
     }
 }
@@ -239,25 +260,47 @@ int check_dot_params(const vkml_gemv_dot_params* p, const char* what) {
 
 // ---------------------------------------------------------------- float path
 
+// gemv.comp's order: 32 lanes per output, lane l taking the 4-element
+// groups l, l + 32, ... of its row (dot(a4, w) summed left to right), then
+// the halving tree over the 32 lanes (gemv.comp:117-212). Two rows a wave.
 template <int BT>
-__global__ void __launch_bounds__(256) k_gemv_float(const float* a, uint32_t m, const void* b, const void* bs,
-                                                    uint32_t st, float* out, uint32_t n, uint32_t k) {
-    const uint32_t wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t row = blockIdx.x * 4 + wave;
-    if (row >= n) return;
+__global__ void __launch_bounds__(256) k_gemv_float(const float* a, uint32_t m, const void* b, const void* bs, uint32_t st,
+                                                    float* out, uint32_t n, uint32_t k) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x % 32;
+    const uint32_t row = blockIdx.x * (blockDim.x / 32) + threadIdx.x / 32;
+    const uint32_t r = min(row, n - 1);
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (uint32_t col = lane; col < k; col += kWave) {
-        const float w = BT == VKML_F32 ? static_cast<const float*>(b)[static_cast<uint64_t>(row) * k + col]
-                                       : weight_value(BT, st, b, bs, k, row, col);
+    const auto w_at = [&](uint64_t col) -> float {
+        if constexpr (BT == VKML_F32) return static_cast<const float*>(b)[static_cast<uint64_t>(r) * k + col];
+        else return weight_value(BT, st, b, bs, k, r, col);
+    };
+    if (k % 4 == 0) {
+        for (uint32_t i = lane; i < k / 4; i += 32) {
+            const float w0 = w_at(4 * i), w1 = w_at(4 * i + 1), w2 = w_at(4 * i + 2), w3 = w_at(4 * i + 3);
 #pragma unroll
-        for (uint32_t r = 0; r < 8; ++r)
-            if (r < m) acc[r] += a[static_cast<uint64_t>(r) * k + col] * w;
+            for (uint32_t q = 0; q < 8; ++q) {
+                if (q < m) {
+                    const float* ar = a + static_cast<uint64_t>(q) * k + 4 * i;
+                    acc[q] += ar[0] * w0 + ar[1] * w1 + ar[2] * w2 + ar[3] * w3;
+                }
+            }
+        }
+    } else {
+        for (uint32_t col = lane; col < k; col += 32) {
+            const float w = w_at(col);
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q)
+                if (q < m) acc[q] += a[static_cast<uint64_t>(q) * k + col] * w;
+        }
     }
 #pragma unroll
-    for (uint32_t r = 0; r < 8; ++r) {
-        if (r >= m) break;
-        const float s = wave_sum(acc[r]);
-        if (lane == 0) out[static_cast<uint64_t>(r) * n + row] = s;
+    for (uint32_t q = 0; q < 8; ++q) {
+        if (q >= m) break;
+        float v = acc[q];
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+        if (lane == 0 && row < n) out[static_cast<uint64_t>(q) * n + row] = v;
     }
 }
 
@@ -314,7 +357,7 @@ int vkml_gemv(const vkml_gemv_params* p, const float* a, const void* b, float* o
     }
     if (p->n == 0) return VKML_OK;
     VKML_CHECK_ARG(a && b && out, "gemv: null buffer");
-    const dim3 grid((p->n + 3) / 4);
+    const dim3 grid((p->n + 7) / 8);
     vkml::abi::ProfileScope prof("gemv");
     hipStream_t s = vkml::abi::stream();
     switch (p->b_type) {

@@ -4,8 +4,9 @@
 // argmax, softmax and a tiled f32 matmul, plus the decode-state helpers.
 // Where the result is integer or bit-level (codes, scales, casts, copies,
 // argmax) it is exactly the reference's; products and sums that the
-// reference writes separately are rounded separately here (__fmul_rn,
-// __fadd_rn) so the compiler fuses none of them.
+// reference writes separately are rounded separately here (plain operators
+// under contract(off) below: HIP's __fmul_rn/__fadd_rn are ordinary header
+// functions whose products the backend would still fuse).
 #include <algorithm>
 #include <cmath>
 
@@ -61,7 +62,7 @@ __device__ void quantize_block(const void* x, uint32_t src_type, uint32_t quant,
         for (int w = 0; w < 4; ++w) {
             uint32_t word = 0;
             for (uint32_t j = 0; j < 8; ++j) {
-                const float code = fminf(fmaxf(__builtin_rintf(__fmul_rn(load_src(x, base + 8 * w + j, src_type) - m, inv)), 0.0f), 15.0f);
+                const float code = fminf(fmaxf(__builtin_rintf((load_src(x, base + 8 * w + j, src_type) - m) * inv), 0.0f), 15.0f);
                 word |= static_cast<uint32_t>(code) << q4_shift(j);
             }
             q[w] = word;
@@ -154,59 +155,77 @@ __global__ void k_dequantize(vkml_dequantize_params p, const void* values, const
 
 // ---------------------------------------------------------------- norms
 
-__global__ void k_rms_norm(vkml_rms_norm_params p, const float* x, const float* w, float* out) {
-    __shared__ float scratch[16];
+// The reference's workgroup reduction at its width of 256 (rms_norm.comp:19-33,
+// softmax.comp's reduce_sum): every invocation's value, then the halving
+// tree, strides 128 and 64 through LDS and 32 .. 1 within wave 0. Every
+// thread gets the result. scratch: 257 floats of LDS.
+constexpr uint32_t kRowThreads = 256;
+
+__device__ float tree256_sum(float v, float* scratch) {
+    const uint32_t t = threadIdx.x;
+    scratch[t] = v;
+    __syncthreads();
+    if (t < 64) {
+        float s = (scratch[t] + scratch[t + 128]) + (scratch[t + 64] + scratch[t + 192]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+        if (t == 0) scratch[256] = s;
+    }
+    __syncthreads();
+    const float r = scratch[256];
+    __syncthreads();
+    return r;
+}
+
+// rms_norm.comp:35-49: invocation t sums x[c]^2 over c = t, t + 256, ...;
+// scale = 1 / sqrt(sum / cols + eps); out = x * scale * w.
+__global__ void __launch_bounds__(kRowThreads) k_rms_norm(vkml_rms_norm_params p, const float* x, const float* w, float* out) {
+    __shared__ float scratch[kRowThreads + 1];
     for (uint32_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
         const float* xr = x + static_cast<uint64_t>(row) * p.cols;
         float s = 0.0f;
-        for (uint32_t c = threadIdx.x; c < p.cols; c += blockDim.x) s += xr[c] * xr[c];
-        s = block_sum(s, scratch);
+        for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads) s += xr[c] * xr[c];
+        s = tree256_sum(s, scratch);
         const float scale = 1.0f / sqrtf(s / static_cast<float>(p.cols) + p.eps);
-        for (uint32_t c = threadIdx.x; c < p.cols; c += blockDim.x)
-            out[static_cast<uint64_t>(row) * p.cols + c] = __fmul_rn(__fmul_rn(xr[c], scale), w[c]);
-        __syncthreads();
+        for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads)
+            out[static_cast<uint64_t>(row) * p.cols + c] = xr[c] * scale * w[c];
     }
 }
 
-// One block of 1024 per row; each thread a float4 of every 1024; the 8
-// lanes of a 32-value block quantize it together.
-__global__ void __launch_bounds__(1024) k_rms_norm_quantize(vkml_rms_norm_params p, const float4* x, const float4* w, float4* out,
-                                                            uint32_t* values, float* scales) {
-    __shared__ float scratch[16];
+// rms_norm followed by quantize.comp's Q8_0 with f32 scales (:100-111): the
+// sum in the reference's order, then each thread normalizes float4s of the
+// row and the 8 lanes of a 32-value block quantize it together.
+__global__ void __launch_bounds__(kRowThreads) k_rms_norm_quantize(vkml_rms_norm_params p, const float* x, const float4* w,
+                                                                   float4* out, uint32_t* values, float* scales) {
+    __shared__ float scratch[kRowThreads + 1];
     const uint32_t row = blockIdx.x, n4 = p.cols / 4;
-    const float4* xr = x + static_cast<uint64_t>(row) * n4;
+    const float* xr = x + static_cast<uint64_t>(row) * p.cols;
     float s = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n4; i += blockDim.x) {
-        const float4 v = xr[i];
-        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
-    s = block_sum(s, scratch);
+    for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads) s += xr[c] * xr[c];
+    s = tree256_sum(s, scratch);
     const float scale = 1.0f / sqrtf(s / static_cast<float>(p.cols) + p.eps);
-    for (uint32_t base = 0; base < n4; base += blockDim.x) {
-        const uint32_t i = base + threadIdx.x;
-        const bool live = i < n4;
-        float4 y = make_float4(0, 0, 0, 0);
-        if (live) {
-            const float4 v = xr[i], wv = w[i];
-            y = make_float4(__fmul_rn(__fmul_rn(v.x, scale), wv.x), __fmul_rn(__fmul_rn(v.y, scale), wv.y),
-                            __fmul_rn(__fmul_rn(v.z, scale), wv.z), __fmul_rn(__fmul_rn(v.w, scale), wv.w));
-            if (out) out[static_cast<uint64_t>(row) * n4 + i] = y;
-        }
+    const float4* xr4 = reinterpret_cast<const float4*>(xr);
+    for (uint32_t i = threadIdx.x; i < n4; i += kRowThreads) {
+        // n4 is a multiple of 8, so the 8 lanes of a block are live together.
+        const float4 v = xr4[i], wv = w[i];
+        const float4 y = make_float4(v.x * scale * wv.x, v.y * scale * wv.y, v.z * scale * wv.z, v.w * scale * wv.w);
+        const uint64_t at = static_cast<uint64_t>(row) * n4 + i;
+        if (out) out[at] = y;
         const float absmax = group_max<8>(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
         const float d = absmax / 127.0f;
         const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-        if (live) {
-            const uint64_t at = static_cast<uint64_t>(row) * n4 + i;
-            values[at] = (static_cast<uint32_t>(quant_code(y.x, inv)) & 0xFFu) | ((static_cast<uint32_t>(quant_code(y.y, inv)) & 0xFFu) << 8) |
-                         ((static_cast<uint32_t>(quant_code(y.z, inv)) & 0xFFu) << 16) | (static_cast<uint32_t>(quant_code(y.w, inv)) << 24);
-            if (i % 8 == 0) scales[at / 8] = d;
-        }
+        values[at] = (static_cast<uint32_t>(quant_code(y.x, inv)) & 0xFFu) | ((static_cast<uint32_t>(quant_code(y.y, inv)) & 0xFFu) << 8) |
+                     ((static_cast<uint32_t>(quant_code(y.z, inv)) & 0xFFu) << 16) | (static_cast<uint32_t>(quant_code(y.w, inv)) << 24);
+        if (i % 8 == 0) scales[at / 8] = d;
     }
 }
 
-// shaders/softmax.comp:85-124 (no ring: causal rows see keys offset + row % q_len and before).
-__global__ void k_softmax(vkml_softmax_params p, const float* x, float* out) {
-    __shared__ float scratch[16];
+// shaders/softmax.comp:85-124 (no ring: causal rows see keys offset + row %
+// q_len and before), with its order: strided per-invocation max and sum of
+// exp over 256 invocations, the halving tree, then exp(score - m) * (1 / s).
+__global__ void __launch_bounds__(kRowThreads) k_softmax(vkml_softmax_params p, const float* x, float* out) {
+    __shared__ float scratch[kRowThreads + 1];
+    __shared__ float s_max[16];
     for (uint32_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
         const float* xr = x + static_cast<uint64_t>(row) * p.cols;
         uint32_t visible = p.cols, first = 0;
@@ -215,18 +234,18 @@ __global__ void k_softmax(vkml_softmax_params p, const float* x, float* out) {
             if (p.window != 0 && visible > p.window) first = visible - p.window;
         }
         const auto score = [&](uint32_t c) {
-            const float s = xr[c] * p.scale;
+            const float s = p.scale * xr[c];
             return p.softcap > 0.0f ? p.softcap * tanhf(fminf(fmaxf(s / p.softcap, -10.0f), 10.0f)) : s;
         };
         float m = -__builtin_inff();
-        for (uint32_t c = first + threadIdx.x; c < visible; c += blockDim.x) m = fmaxf(m, score(c));
-        m = block_max(m, scratch);
+        for (uint32_t c = first + threadIdx.x; c < visible; c += kRowThreads) m = fmaxf(m, score(c));
+        m = block_max(m, s_max);
         float s = 0.0f;
-        for (uint32_t c = first + threadIdx.x; c < visible; c += blockDim.x) s += expf(score(c) - m);
-        s = block_sum(s, scratch);
+        for (uint32_t c = first + threadIdx.x; c < visible; c += kRowThreads) s += vk_expf(score(c) - m);
+        s = tree256_sum(s, scratch);
         const float inv = 1.0f / s;
-        for (uint32_t c = threadIdx.x; c < p.cols; c += blockDim.x)
-            out[static_cast<uint64_t>(row) * p.cols + c] = (c >= first && c < visible) ? expf(score(c) - m) * inv : 0.0f;
+        for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads)
+            out[static_cast<uint64_t>(row) * p.cols + c] = (c >= first && c < visible) ? vk_expf(score(c) - m) * inv : 0.0f;
         __syncthreads();
     }
 }
@@ -321,8 +340,8 @@ __global__ void k_rope(vkml_rope_params p, const float* x, const float* table, f
         const uint64_t ib = base + (p.style == 0 ? 2 * k + 1 : k + p.half_dim);
         const float c = table[(pos * p.half_dim + k) * 2], s = table[(pos * p.half_dim + k) * 2 + 1];
         const float a = x[ia], b = x[ib];
-        out[ia] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-        out[ib] = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+        out[ia] = a * c - b * s;
+        out[ib] = a * s + b * c;
     }
 }
 
@@ -351,8 +370,8 @@ __global__ void k_rope_kv_append(vkml_rope_kv_params p, const float* qkv, const 
         float a = src[ia], b = src[ib];
         if (p.rotate) {
             const float c = table[(static_cast<uint64_t>(pos) * half + k) * 2], s = table[(static_cast<uint64_t>(pos) * half + k) * 2 + 1];
-            const float ra = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-            const float rb = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+            const float ra = a * c - b * s;
+            const float rb = a * s + b * c;
             a = ra;
             b = rb;
         }
@@ -419,7 +438,7 @@ __global__ void k_binary(uint32_t op, uint32_t count, uint32_t b_count, const fl
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
         const float x = a[i], y = b[i % b_count];
-        out[i] = op == 0 ? __fadd_rn(x, y) : op == 1 ? __fsub_rn(x, y) : op == 2 ? __fmul_rn(x, y) : x / y;
+        out[i] = op == 0 ? x + y : op == 1 ? x - y : op == 2 ? x * y : x / y;
     }
 }
 
@@ -429,7 +448,7 @@ __global__ void k_unary(uint32_t op, uint32_t count, float param, const float* x
         const float v = x[i];
         float r;
         if (op == 0) {
-            r = v / (1.0f + expf(-v));
+            r = v / (1.0f + vk_expf(-v));
         } else if (op == 1) {
             const float inner = fminf(fmaxf(0.7978845608f * (v + 0.044715f * v * v * v), -10.0f), 10.0f);
             r = 0.5f * v * (1.0f + tanhf(inner));
@@ -523,7 +542,7 @@ int vkml_rms_norm(const vkml_rms_norm_params* p, const float* x, const float* w,
     if (p->rows == 0 || p->cols == 0) return VKML_OK;
     VKML_CHECK_ARG(x && w && out, "rms_norm: null buffer");
     ProfileScope prof("rms_norm");
-    hipLaunchKernelGGL(k_rms_norm, dim3(std::min<uint32_t>(p->rows, 65535)), dim3(256), 0, S(), *p, x, w, out);
+    hipLaunchKernelGGL(k_rms_norm, dim3(std::min<uint32_t>(p->rows, 65535)), dim3(kRowThreads), 0, S(), *p, x, w, out);
     return vkml::abi::check_launch("rms_norm");
 }
 
@@ -536,9 +555,8 @@ int vkml_rms_norm_quantize(const vkml_rms_norm_params* p, const float* x, const 
     if (p->rows == 0 || p->cols == 0) return VKML_OK;
     VKML_CHECK_ARG(x && w && values && scales, "rms_norm_quantize: null buffer");
     ProfileScope prof("rms_norm_quantize");
-    const uint32_t threads = std::min<uint32_t>(1024, std::max<uint32_t>(64, (p->cols / 4 + 63) / 64 * 64));
-    hipLaunchKernelGGL(k_rms_norm_quantize, dim3(p->rows), dim3(threads), 0, S(), *p, reinterpret_cast<const float4*>(x),
-                       reinterpret_cast<const float4*>(w), reinterpret_cast<float4*>(out), static_cast<uint32_t*>(values), scales);
+    hipLaunchKernelGGL(k_rms_norm_quantize, dim3(p->rows), dim3(kRowThreads), 0, S(), *p, x, reinterpret_cast<const float4*>(w),
+                       reinterpret_cast<float4*>(out), static_cast<uint32_t*>(values), scales);
     return vkml::abi::check_launch("rms_norm_quantize");
 }
 
@@ -549,7 +567,7 @@ int vkml_softmax(const vkml_softmax_params* p, const float* x, float* out) {
     if (p->rows == 0 || p->cols == 0) return VKML_OK;
     VKML_CHECK_ARG(x && out, "softmax: null buffer");
     ProfileScope prof("softmax");
-    hipLaunchKernelGGL(k_softmax, dim3(std::min<uint32_t>(p->rows, 65535)), dim3(256), 0, S(), *p, x, out);
+    hipLaunchKernelGGL(k_softmax, dim3(std::min<uint32_t>(p->rows, 65535)), dim3(kRowThreads), 0, S(), *p, x, out);
     return vkml::abi::check_launch("softmax");
 }
 

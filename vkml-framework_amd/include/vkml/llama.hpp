@@ -71,8 +71,6 @@ struct LlamaOptions {
     std::int64_t sliding_extra_rows = 1024;
     // Replay each decode step as a captured HIP graph.
     bool use_graphs = true;
-    // Key splits per KV head for decode attention; 0 picks from the CU count.
-    std::int64_t attention_splits = 0;
     // int8 activations for this model's quantized weights, when the Context
     // allows them too (ContextOptions::integer_dot_product).
     bool integer_dot_product = true;

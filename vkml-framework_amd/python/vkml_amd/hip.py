@@ -55,7 +55,7 @@ EmbeddingParams = _struct("EmbeddingParams", [("count", u32), ("dim", u32), ("vo
                                               ("scale_type", u32)])
 DecodeState = _struct("DecodeState", [("token", i32), ("position", i32), ("steps", i32), ("reserved", i32)])
 AttendParams = _struct("AttendParams", [("kv_start", u32), ("kv_len", u32), ("capacity", u32), ("heads", u32),
-                                        ("kv_heads", u32), ("head_dim", u32), ("kv_type", u32), ("splits", u32),
+                                        ("kv_heads", u32), ("head_dim", u32), ("kv_type", u32), ("chunks", u32),
                                         ("scale", f32), ("softcap", f32)])
 RopeKvParams = _struct("RopeKvParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
                                         ("position", u32), ("style", u32), ("kv_type", u32), ("rotate", u32)])

@@ -307,7 +307,7 @@ struct Llama::Impl {
 
     // Decode buffers.
     Tensor x, xn, xq, xs, qkv, q, attn, aq, as, partial, stats, h, hq, hs, gate_tmp, up_tmp, ytmp, logits, state, log;
-    std::int64_t splits = 1;
+    std::int64_t chunks = 1;  // decode attention's 128-key chunks over the whole cache
     std::uint64_t graph_logits = 0, graph_greedy = 0;
 
     const Weight& lm_head() const { return tied ? embed : *lm_head_own; }
@@ -363,7 +363,7 @@ struct Llama::Impl {
             }
         };
         const vkml_attend_params ap{0, 0, u32(context_length), u32(c.num_heads), u32(c.num_kv_heads), u32(hd),
-                                    detail::type_code(layers[0].k_cache.dtype()), u32(splits), 1.0f / std::sqrt(static_cast<float>(hd)), 0.0f};
+                                    detail::type_code(layers[0].k_cache.dtype()), u32(chunks), 1.0f / std::sqrt(static_cast<float>(hd)), 0.0f};
         for (const Layer& L : layers) {
             norm(L.attn_norm, "attn_norm");
             for (const auto& [w, row] : L.qkv)
@@ -559,13 +559,9 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
     m.logits = f32(c.vocab_size);
     m.state = Tensor::zeros(context, {4}, DType::I32);
     m.log = Tensor::zeros(context, {context_length}, DType::I32);
-    const std::int64_t cus = std::max<std::int64_t>(context.device_info().compute_units, 1);
-    m.splits = options.attention_splits > 0 ? options.attention_splits
-                                            : std::max<std::int64_t>((context_length + 1023) / 1024,
-                                                                     std::min<std::int64_t>(2 * cus / c.num_kv_heads, (context_length + 15) / 16));
-    m.splits = std::max<std::int64_t>(m.splits, (context_length + 1023) / 1024);
-    m.partial = f32(c.num_kv_heads * m.splits * (c.num_heads / c.num_kv_heads) * hd);
-    m.stats = f32(c.num_kv_heads * m.splits * (c.num_heads / c.num_kv_heads) * 2);
+    m.chunks = (context_length + 127) / 128;
+    m.partial = f32(c.num_heads * m.chunks * hd);
+    m.stats = f32(c.num_heads * m.chunks * 2);
     context.synchronize();
     return Llama(std::move(impl));
 }

@@ -412,21 +412,16 @@ Tensor matmul_transposed(const Tensor& a, const QuantizedMatrix& b) {
 namespace detail {
 
 // Decode attention for one query per head (attention.cpp:40-84): the
-// split-K kernel and its merge, splits sized to the CU count.
+// chunked kernel (128 keys a chunk, as the reference) and its merge.
 Tensor attend_one_query(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache, std::int64_t kv_start, std::int64_t kv_len,
                         float softcap) {
     const std::int64_t heads = q.shape()[0], hd = q.shape()[2], kv_heads = k_cache.shape()[0], capacity = k_cache.shape()[1];
-    Runtime& rt = TensorAccess::runtime(q);
-    const std::int64_t keys = kv_len - kv_start;
-    std::int64_t splits = std::max<std::int64_t>(1, 2 * rt.info().compute_units / std::max<std::int64_t>(kv_heads, 1));
-    splits = std::min<std::int64_t>(splits, std::max<std::int64_t>(1, keys / 16));
-    splits = std::max<std::int64_t>(splits, (keys + 1023) / 1024);
-    const std::int64_t group = heads / kv_heads;
-    Tensor partial = like(q, {kv_heads, splits, group, hd}, DType::F32);
-    Tensor stats = like(q, {kv_heads, splits, group, 2}, DType::F32);
+    const std::int64_t chunks = (kv_len - kv_start + 127) / 128;
+    Tensor partial = like(q, {heads, chunks, hd}, DType::F32);
+    Tensor stats = like(q, {heads, chunks, 2}, DType::F32);
     Tensor out = like(q, {heads, 1, hd}, DType::F32);
     const vkml_attend_params p{u32(kv_start), u32(kv_len), u32(capacity), u32(heads), u32(kv_heads), u32(hd), type_code(k_cache.dtype()),
-                               u32(splits), 1.0f / std::sqrt(static_cast<float>(hd)), softcap};
+                               u32(chunks), 1.0f / std::sqrt(static_cast<float>(hd)), softcap};
     check(vkml_attend(&p, static_cast<const float*>(q.data()), k_cache.data(), v_cache.data(), static_cast<float*>(partial.data()),
                       static_cast<float*>(stats.data()), nullptr),
           "attention");

@@ -111,6 +111,10 @@ int vkml_submit(uint64_t* fence_out);
 int vkml_wait(uint64_t fence);
 int vkml_completed(uint64_t* fence_out);
 int vkml_synchronize(void);
+/* The library's one in-order stream, as a hipStream_t, so a caller can
+ * order its own HIP work (events, copies) with the library's launches. No
+ * reference counterpart: the reference's Stream is internal to its HAL. */
+void* vkml_stream(void);
 
 /* ---------------------------------------------------------------------- */
 /* Profiling: Context::set_profiling/profile/reset_profile               */
@@ -317,9 +321,8 @@ int vkml_embedding(const vkml_embedding_params* p, const void* d_values, const v
 /* Decode attention (shaders/attend.comp + attend_merge.comp,             */
 /* src/ops/attention.cpp:22-84). Keys kv_start..kv_len of caches          */
 /* [kv_heads, capacity, head_dim] (F32 or F16), key position p at row     */
-/* p % capacity, in the reference's chunks of 128 keys from kv_start.     */
-/* Workgroup (c, g) reads chunk c of KV head g once for all heads /       */
-/* kv_heads query heads of its group. With d_state non-NULL, kv_len is    */
+/* p % capacity, in the reference's chunks of 128 keys from kv_start, a   */
+/* workgroup per (chunk, query head). With d_state non-NULL, kv_len is    */
 /* d_state->position + 1 (the replayed decode step) and the launch covers */
 /* the whole cache. chunks: the partial buffers' stride, at least         */
 /* ceil((kv_len - kv_start) / 128), or ceil((capacity - kv_start) / 128)  */
@@ -353,6 +356,33 @@ int vkml_attend(const vkml_attend_params* p, const float* d_q, const void* d_k_c
  * non-NULL, its Q8_0 form with f32 scales (the o projection's input). */
 int vkml_attend_merge(const vkml_attend_params* p, const float* d_partial, const float* d_stats,
                       float* d_out, void* d_values, float* d_scales);
+
+/* One layer's attention for a decode step: rope of q and of the new key,
+ * the new key and value appended at the position as vkml_rope_kv_append
+ * does, vkml_attend over keys kv_start..position, and vkml_attend_merge into
+ * d_out [heads, head_dim] f32 with its Q8_0 form in d_values / d_scales
+ * (when non-NULL): two launches, arithmetic that of those kernels
+ * (llama.cpp:320-369 in order). d_qkv = [q | k | v] f32 of this token.
+ * partial / stats as vkml_attend, chunks >= ceil((capacity - kv_start) /
+ * 128). Position from d_state if non-NULL. */
+typedef struct vkml_attend_step_params {
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t capacity;
+    uint32_t kv_start;
+    uint32_t position;
+    uint32_t kv_type;
+    uint32_t chunks;
+    uint32_t rope_style; /* 0 interleaved pairs, 1 rotate-half */
+    uint32_t rotate;     /* 0: no rope in this layer */
+    float scale;
+    float softcap;
+} vkml_attend_step_params;
+int vkml_attend_step(const vkml_attend_step_params* p, const float* d_qkv, const float* d_rope_table,
+                     void* d_k_cache, void* d_v_cache, float* d_partial, float* d_stats,
+                     float* d_out, void* d_values, float* d_scales, const vkml_decode_state* d_state);
+
 
 /* ---------------------------------------------------------------------- */
 /* Fused decode-step kernels (no single reference counterpart: each       */

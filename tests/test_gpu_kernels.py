@@ -284,7 +284,7 @@ def test_rope_kv_append_bit_exact(kv_type):
 @pytest.mark.parametrize("hd,heads,kvh,kv_len,kv_type,extra", [
     (128, 32, 8, 4096, H.F16, 0), (128, 32, 8, 1, H.F16, 3), (64, 32, 8, 640, H.F16, 0),
     (64, 4, 2, 45, H.F32, 1), (128, 32, 8, 300, H.F32, 0), (256, 8, 8, 200, H.F16, 0), (128, 8, 1, 1000, H.F16, 2),
-    (256, 16, 2, 129, H.F32, 0), (64, 16, 4, 128, H.F16, 0)])
+    (256, 16, 2, 129, H.F32, 0), (64, 16, 4, 128, H.F16, 0), (64, 8, 2, 9000, H.F16, 0)])
 def test_attend_bit_exact(hd, heads, kvh, kv_len, kv_type, extra):
     cap = kv_len + 7
     rng = np.random.default_rng(kv_len)
@@ -340,6 +340,43 @@ def test_attend_from_a_window_start():
     H.call("vkml_attend_merge", prm, p(part), p(stats), p(out), None, None)
     want = O.attend_decode(q, kc, vc, 100, 500)
     assert np.array_equal(bits(out.download(np.float32, (heads, hd))), bits(want))
+
+
+@pytest.mark.parametrize("hd,heads,kvh,pos,kv_type,style", [
+    (128, 32, 8, 4096, H.F16, 0), (64, 32, 8, 200, H.F16, 1), (64, 4, 2, 45, H.F32, 0), (128, 8, 8, 127, H.F16, 0),
+    (256, 8, 4, 300, H.F16, 1), (128, 16, 2, 700, H.F32, 0), (128, 32, 8, 0, H.F16, 0)])
+def test_attend_step_bit_exact(hd, heads, kvh, pos, kv_type, style):
+    # rope + append + attention + merge + quantize, two steps in a row,
+    # against the oracle's pieces
+    cap = pos + 67
+    chunks = (cap + 127) // 128
+    rng = np.random.default_rng(pos + hd)
+    dt = np.uint16 if kv_type == H.F16 else np.float32
+    prior = rng.standard_normal((2, kvh, cap, hd)).astype(np.float32)
+    caches = [prior[i].astype(np.float16).view(np.uint16) if kv_type == H.F16 else prior[i] for i in range(2)]
+    kc, vc = dev(caches[0]), dev(caches[1])
+    table = O.rope_table(cap, hd, 1e6)
+    dtab = dev(table)
+    part, stats = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8)
+    for step in range(2):
+        p_now = pos + step
+        qkv = rng.standard_normal((heads + 2 * kvh) * hd).astype(np.float32)
+        out, vals, scs = H.empty(heads * hd * 4), H.empty(heads * hd), H.empty(heads * hd // 32 * 4)
+        prm = H.AttendStepParams(heads, kvh, hd, cap, 0, p_now, kv_type, chunks, style, 1, 1.0 / math.sqrt(hd), 0.0)
+        H.call("vkml_attend_step", prm, p(dev(qkv)), p(dtab), p(kc), p(vc), p(part), p(stats), p(out), p(vals), p(scs), None)
+        q = O.rope(qkv[:heads * hd].reshape(1, heads, hd), table, p_now, style).reshape(heads, hd)
+        k = O.rope(qkv[heads * hd:(heads + kvh) * hd].reshape(1, kvh, hd), table, p_now, style).reshape(kvh, hd)
+        v = qkv[(heads + kvh) * hd:].reshape(kvh, hd)
+        for c, new in ((caches[0], k), (caches[1], v)):
+            c[:, p_now] = O.f32_to_f16(new) if kv_type == H.F16 else new
+        assert np.array_equal(kc.download(dt, caches[0].shape), caches[0])
+        assert np.array_equal(vc.download(dt, caches[1].shape), caches[1])
+        want = O.attend_decode(q, caches[0], caches[1], 0, p_now + 1)
+        got = out.download(np.float32, (heads, hd))
+        assert np.array_equal(bits(got), bits(want))
+        ww, ws = O.quantize(O.Q8_0, want, False)
+        assert np.array_equal(vals.download(np.uint32, ww.shape), ww)
+        assert np.array_equal(scs.download(np.float32, ws.shape).view(np.uint32), ws.view(np.uint32))
 
 
 # ---------------------------------------------------------------- small ops

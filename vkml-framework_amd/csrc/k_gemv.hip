@@ -2,22 +2,35 @@
 // reference's shaders/gemv_dot.comp and gemv.comp), written for gfx950.
 //
 // Bit-exact by construction. The reference sums each output over 32
-// accumulators: accumulator l takes the terms of half-blocks (16 values) l,
-// l + 32, l + 64, ... in that order, each term an exact int8 dot product
-// scaled in f32 (gemv_dot.comp:349-363), and the 32 are added in a halving
-// tree (:370-375). Every f32 operation here happens in that order, so the
-// outputs are the reference's bits, and the Q8_0 codes the next layer
-// quantizes from them are too.
+// accumulators: accumulator L takes the terms of half-blocks (16 values) L,
+// L + 32, L + 64, ... in that order, each term an exact int8 dot product
+// scaled in f32 (gemv_dot.comp:85-118), and the 32 are added in a halving
+// tree (:121-131). Every f32 operation here happens in that order, so the
+// outputs are the reference's bits, and so are the Q8_0 codes the next layer
+// quantizes from them.
 //
-// The 32 accumulators of a row live in 8 lanes, 4 each: lane j takes the
-// 64-value tasks c = j, j + 8, ..., whose half-blocks 4c .. 4c + 3 are
-// exactly accumulators 4j .. 4j + 3. So each lane still streams its weights
-// with 128-bit loads (32 B of 4-bit codes, or 64 B of q8_0, plus the task's
-// scales or q4_K's 16-byte header), a wave64 covers 8 rows, and the tree's
-// strides 16, 8 and 4 are lane exchanges within the 8-lane group, 2 and 1
-// additions within a lane. The activation vector is staged once per
-// workgroup in LDS with each half-block's code sum. No MFMA: these are
-// matrix-vector products, bound by HBM.
+// Mapping. A row's 32 accumulators live in LPR lanes (16 or 8), 32 / LPR
+// each. A "round" is the 32 half-blocks (512 values) that give every
+// accumulator its next term. Which accumulators a lane holds is chosen per
+// weight format so that a lane's share of a round is one or two contiguous
+// 16-byte loads and the LPR lanes of a row read one contiguous span:
+// - q4_K (16 lanes): lane 8p + 2c + h loads code bytes 16 lane of the
+//   round's two super-blocks; low nibbles are half-block 16p + 4c + h, high
+//   nibbles 16p + 4c + h + 2. (8 lanes: lane j loads bytes 32j .. 32j + 31,
+//   half-blocks 4j .. 4j + 3.)
+// - q4_0 / q4_1 (16 lanes): lane l loads block l of the round, half-blocks
+//   2l, 2l + 1. (8 lanes: blocks 2j, 2j + 1, half-blocks 4j .. 4j + 3.)
+// - q8_0 (16 lanes): lane l loads half-blocks l and l + 16. (8 lanes: j,
+//   j + 8, j + 16, j + 24.)
+// The halving tree's strides 16 .. 1 then become, per mapping, additions
+// within a lane or exchanges between lanes (xor shuffles).
+//
+// 16 lanes a row are used when 8 would leave SIMDs idle (the N = 4096
+// projections of a 7B model: 4096 rows x 16 lanes is one wave per SIMD).
+// Each lane keeps two batches of rounds in flight (the next batch loads while
+// the current one is summed), and the first batch is issued before the
+// workgroup stages the activation codes, their per-half-block sums and block
+// scales in LDS. No MFMA: these are matrix-vector products, bound by HBM.
 #include <algorithm>
 
 #include "device.hpp"
@@ -28,6 +41,8 @@ using namespace vkml::dev;
 namespace {
 
 constexpr uint32_t kMaxK = 32768;  // LDS staging: K + K / 16 * 4 + K / 32 * 4 bytes
+constexpr uint32_t kThreads = 128;
+constexpr uint32_t kLow = 0x0F0F0F0Fu;
 
 struct GemvArgs {
     const uint4* a_values;  // K bytes of activation codes
@@ -41,172 +56,305 @@ struct GemvArgs {
     uint32_t n, k;
 };
 
-// One row's weights for one 64-value task.
-struct Wt {
-    uint4 q[4];
-    uint4 s;
+// The accumulator (= half-block of the round) held in slot e of lane l.
+template <int FMT, int LPR>
+__device__ __forceinline__ constexpr uint32_t acc_index(uint32_t l, uint32_t e) {
+    if constexpr (FMT == VKML_Q8_0) return LPR == 16 ? l + 16 * e : l + 8 * e;
+    else if constexpr (FMT == VKML_Q4_K && LPR == 16) return 16 * (l / 8) + 4 * ((l / 2) % 4) + (l % 2) + 2 * e;
+    else return (32 / LPR) * l + e;  // q4_0 / q4_1, and q4_K with 8 lanes
+}
+
+template <int FMT, int LPR>
+struct Plan {
+    static constexpr int NS = 32 / LPR;                        // accumulators (slots) per lane
+    static constexpr int NQ = FMT == VKML_Q8_0 ? NS : NS / 2;  // 16-byte code loads per lane and round
 };
 
-template <int FMT, bool F16S>
-__device__ __forceinline__ void load_task(const void* bv, const void* bs, uint32_t K, uint32_t row, uint32_t t, Wt& w) {
-    const uint64_t r = row;
+// One lane's weights for one round of one matrix: codes, and scales (q4_K:
+// the super-block header; q8_0 / q4_0: one scale per slot or block; q4_1:
+// scale and offset per block), as raw bits.
+template <int FMT, int LPR>
+struct RoundW {
+    uint4 q[Plan<FMT, LPR>::NQ];
+    uint32_t s[FMT == VKML_Q4_K ? 4 : Plan<FMT, LPR>::NS];
+};
+
+__device__ __forceinline__ uint32_t ld16(const void* p, uint64_t i) { return static_cast<const uint16_t*>(p)[i]; }
+__device__ __forceinline__ uint32_t ld32(const void* p, uint64_t i) { return static_cast<const uint32_t*>(p)[i]; }
+__device__ __forceinline__ uint4 ld128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Loads lane l's share of round r of row `row`. Every load is issued
+// unconditionally (positions past the row's end, in a last round shorter
+// than 512 values, are clamped to its last block and their terms skipped),
+// so the compiler can count outstanding loads and wait for one batch while
+// the next is still in flight.
+template <int FMT, bool F16S, int LPR>
+__device__ __forceinline__ void load_round(const void* bv, const void* bs, uint32_t K, uint32_t row, uint32_t r, uint32_t l,
+                                           RoundW<FMT, LPR>& w) {
+    constexpr int NS = Plan<FMT, LPR>::NS;
+    const uint64_t R = row;
+    const uint8_t* codes = static_cast<const uint8_t*>(bv);
     if constexpr (FMT == VKML_Q8_0) {
-        const uint4* q = static_cast<const uint4*>(bv) + r * (K / 16) + 4 * t;
-        w.q[0] = q[0]; w.q[1] = q[1]; w.q[2] = q[2]; w.q[3] = q[3];
-        if constexpr (F16S) w.s.x = static_cast<const uint32_t*>(bs)[r * (K / 64) + t];
-        else { const uint2 s = static_cast<const uint2*>(bs)[r * (K / 64) + t]; w.s.x = s.x; w.s.y = s.y; }
-    } else {
-        const uint4* q = static_cast<const uint4*>(bv) + r * (K / 32) + 2 * t;
-        w.q[0] = q[0]; w.q[1] = q[1];
-        if constexpr (FMT == VKML_Q4_K) {
-            w.s = static_cast<const uint4*>(bs)[r * (K / 256) + t / 4];
-        } else if constexpr (FMT == VKML_Q4_1) {
-            if constexpr (F16S) { const uint2 s = static_cast<const uint2*>(bs)[r * (K / 64) + t]; w.s.x = s.x; w.s.y = s.y; }
-            else w.s = static_cast<const uint4*>(bs)[r * (K / 64) + t];
+        const uint8_t* base = codes + R * K;
+        const uint64_t blocks = R * (K / 32);
+#pragma unroll
+        for (int e = 0; e < NS; ++e) {
+            const uint32_t hb = min(32 * r + acc_index<FMT, LPR>(l, e), K / 16 - 1);
+            w.q[e] = ld128(base + 16ull * hb);
+            w.s[e] = F16S ? ld16(bs, blocks + hb / 2) : ld32(bs, blocks + hb / 2);
+        }
+    } else if constexpr (FMT == VKML_Q4_K) {
+        const uint32_t p = LPR == 16 ? l / 8 : l / 4;  // which super-block of the round
+        const uint32_t sb = min(2 * r + p, K / 256 - 1);
+        const uint8_t* base = codes + R * (K / 2) + 128ull * sb;
+        if constexpr (LPR == 16) {
+            w.q[0] = ld128(base + 16 * (l % 8));
         } else {
-            if constexpr (F16S) w.s.x = static_cast<const uint32_t*>(bs)[r * (K / 64) + t];
-            else { const uint2 s = static_cast<const uint2*>(bs)[r * (K / 64) + t]; w.s.x = s.x; w.s.y = s.y; }
+            w.q[0] = ld128(base + 32 * (l % 4));
+            w.q[1] = ld128(base + 32 * (l % 4) + 16);
+        }
+        const uint4 h = static_cast<const uint4*>(bs)[R * (K / 256) + sb];
+        w.s[0] = h.x; w.s[1] = h.y; w.s[2] = h.z; w.s[3] = h.w;
+    } else {
+        const uint8_t* base = codes + R * (K / 2);
+#pragma unroll
+        for (int b = 0; b < NS / 2; ++b) {
+            const uint32_t blk = min(16 * r + (LPR == 16 ? l : 2 * l) + b, K / 32 - 1);  // block of the row
+            const uint64_t block = R * (K / 32) + blk;
+            w.q[b] = ld128(base + 16ull * blk);
+            if constexpr (FMT == VKML_Q4_1) {
+                if constexpr (F16S) {
+                    w.s[2 * b] = ld32(bs, block);  // f16 scale | f16 offset << 16
+                } else {
+                    const uint2 so = static_cast<const uint2*>(bs)[block];
+                    w.s[2 * b] = so.x;
+                    w.s[2 * b + 1] = so.y;
+                }
+            } else {
+                w.s[b] = F16S ? ld16(bs, block) : ld32(bs, block);
+            }
         }
     }
 }
 
-constexpr uint32_t kLow = 0x0F0F0F0Fu;
-
 // The exact dot product of one half-block: 16 weight codes as bytes (four
-// words) with 16 activation codes (gemv_dot.comp:352-353).
+// words) with 16 activation codes (gemv_dot.comp:105-106).
 __device__ __forceinline__ int half_dot(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint4 a) {
     return dot4(w3, a.w, dot4(w2, a.z, dot4(w1, a.y, dot4(w0, a.x, 0))));
 }
 
-// Adds the task's four half-block terms to acc[0..3] with the reference's
-// expressions (gemv_dot.comp:354-362): q8_0/q4_0 float(d) * (scale * sa);
-// q4_1 (and q4_K, whose sub-blocks are q4_1's) sa * (float(d) * scale +
-// float(sum) * offset). S holds each half-block's activation code sum, sa
-// the two blocks' activation scales.
-template <int FMT, bool F16S>
-__device__ __forceinline__ void task_terms(const Wt& w, uint32_t t, const uint4 (&a)[4], float4 S, float2 sa, float (&acc)[4]) {
+__device__ __forceinline__ float scale_of(uint32_t bits, bool f16) {
+    return f16 ? f16_bits_to_float(bits & 0xFFFFu) : __uint_as_float(bits);
+}
+
+// Scale and offset of sub-blocks 2c (low nibbles) and 2c + 1 (high) of a
+// q4_K super-block with header h: f16(d * sc) and f16(-(dmin * m)), the
+// reference's rounding of its q4_1 repack (src/io/gguf.cpp:123-131,603-617),
+// computed as f16 products (exact operands, one rounding to nearest even).
+__device__ __forceinline__ void q4k_sub_scales(const uint32_t (&h)[4], uint32_t c, float& s0, float& o0, float& s1, float& o1) {
+    const uint32_t shift = (c & 1u) * 16u;
+    const uint32_t Y = (h[1] >> shift) & 0xFFFFu, Z = (h[2] >> shift) & 0xFFFFu, W = (h[3] >> shift) & 0xFFFFu;
+    uint32_t sc, mn;
+    if (c < 2) {
+        sc = Y & 0x3F3Fu;
+        mn = Z & 0x3F3Fu;
+    } else {
+        sc = (W & 0x0F0Fu) | ((Y & 0xC0C0u) >> 2);
+        mn = ((W >> 4) & 0x0F0Fu) | ((Z & 0xC0C0u) >> 2);
+    }
+    const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h[0] & 0xFFFFu));
+    const _Float16 nd = -__builtin_bit_cast(_Float16, static_cast<uint16_t>(h[0] >> 16));
+    s0 = static_cast<float>(d * static_cast<_Float16>(sc & 0xFFu));
+    s1 = static_cast<float>(d * static_cast<_Float16>(sc >> 8));
+    o0 = static_cast<float>(nd * static_cast<_Float16>(mn & 0xFFu));
+    o1 = static_cast<float>(nd * static_cast<_Float16>(mn >> 8));
+}
+
+// Adds one lane's terms of round r to acc[0 .. NS) with the reference's
+// expressions (gemv_dot.comp:112,114): q8_0 / q4_0 float(d) * (scale * sa);
+// q4_1 and q4_K sa * (float(d) * scale + float(sum) * offset). The
+// activation codes, half-block sums and block scales come from LDS.
+template <int FMT, bool F16S, int LPR>
+__device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t r, uint32_t l, uint32_t K,
+                                            const uint4* s_codes, const float* s_sum, const float* s_sa,
+                                            float (&acc)[Plan<FMT, LPR>::NS]) {
 #pragma clang fp contract(off)
-    int d[4];
-    float s0, s1, o0 = 0.0f, o1 = 0.0f;
+    constexpr int NS = Plan<FMT, LPR>::NS;
+    const uint32_t halves = K / 16;
+    float s[NS], o[NS];
+    int d[NS];
+    uint4 a[NS];
+    bool live[NS];
+#pragma unroll
+    for (int e = 0; e < NS; ++e) {
+        const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
+        live[e] = hb < halves;
+        a[e] = live[e] ? s_codes[hb] : make_uint4(0, 0, 0, 0);
+    }
     if constexpr (FMT == VKML_Q8_0) {
 #pragma unroll
-        for (int h = 0; h < 4; ++h) d[h] = half_dot(w.q[h].x, w.q[h].y, w.q[h].z, w.q[h].w, a[h]);
-        if constexpr (F16S) { s0 = f16_bits_to_float(w.s.x & 0xFFFFu); s1 = f16_bits_to_float(w.s.x >> 16); }
-        else { s0 = __uint_as_float(w.s.x); s1 = __uint_as_float(w.s.y); }
+        for (int e = 0; e < NS; ++e) {
+            d[e] = half_dot(w.q[e].x, w.q[e].y, w.q[e].z, w.q[e].w, a[e]);
+            s[e] = scale_of(w.s[e], F16S);
+        }
     } else if constexpr (FMT == VKML_Q4_K) {
-        // Bytes 32c .. 32c + 31 of the super-block's codes: low nibbles are
-        // sub-block 2c, high nibbles sub-block 2c + 1, each in value order.
-        const uint4 q0 = w.q[0], q1 = w.q[1];
-        d[0] = half_dot(q0.x & kLow, q0.y & kLow, q0.z & kLow, q0.w & kLow, a[0]);
-        d[1] = half_dot(q1.x & kLow, q1.y & kLow, q1.z & kLow, q1.w & kLow, a[1]);
-        d[2] = half_dot((q0.x >> 4) & kLow, (q0.y >> 4) & kLow, (q0.z >> 4) & kLow, (q0.w >> 4) & kLow, a[2]);
-        d[3] = half_dot((q1.x >> 4) & kLow, (q1.y >> 4) & kLow, (q1.z >> 4) & kLow, (q1.w >> 4) & kLow, a[3]);
-        q4k_scales(w.s, t & 3u, s0, o0, s1, o1);
+        const uint32_t c = LPR == 16 ? (l / 2) % 4 : l % 4;
+        float s0, o0, s1, o1;
+        q4k_sub_scales(w.s, c, s0, o0, s1, o1);
+        if constexpr (LPR == 16) {
+            const uint4 q = w.q[0];
+            d[0] = half_dot(q.x & kLow, q.y & kLow, q.z & kLow, q.w & kLow, a[0]);
+            d[1] = half_dot((q.x >> 4) & kLow, (q.y >> 4) & kLow, (q.z >> 4) & kLow, (q.w >> 4) & kLow, a[1]);
+            s[0] = s0; o[0] = o0; s[1] = s1; o[1] = o1;
+        } else {
+            const uint4 q0 = w.q[0], q1 = w.q[1];
+            d[0] = half_dot(q0.x & kLow, q0.y & kLow, q0.z & kLow, q0.w & kLow, a[0]);
+            d[1] = half_dot(q1.x & kLow, q1.y & kLow, q1.z & kLow, q1.w & kLow, a[1]);
+            d[2] = half_dot((q0.x >> 4) & kLow, (q0.y >> 4) & kLow, (q0.z >> 4) & kLow, (q0.w >> 4) & kLow, a[2]);
+            d[3] = half_dot((q1.x >> 4) & kLow, (q1.y >> 4) & kLow, (q1.z >> 4) & kLow, (q1.w >> 4) & kLow, a[3]);
+            s[0] = s0; o[0] = o0; s[1] = s0; o[1] = o0; s[2] = s1; o[2] = o1; s[3] = s1; o[3] = o1;
+        }
     } else {
         // QuantizedMatrix q4 words: byte j holds value j (low) and j + 4 (high).
-        const uint4 q0 = w.q[0], q1 = w.q[1];
-        d[0] = half_dot(q0.x & kLow, (q0.x >> 4) & kLow, q0.y & kLow, (q0.y >> 4) & kLow, a[0]);
-        d[1] = half_dot(q0.z & kLow, (q0.z >> 4) & kLow, q0.w & kLow, (q0.w >> 4) & kLow, a[1]);
-        d[2] = half_dot(q1.x & kLow, (q1.x >> 4) & kLow, q1.y & kLow, (q1.y >> 4) & kLow, a[2]);
-        d[3] = half_dot(q1.z & kLow, (q1.z >> 4) & kLow, q1.w & kLow, (q1.w >> 4) & kLow, a[3]);
-        if constexpr (FMT == VKML_Q4_1) {
-            if constexpr (F16S) {
-                s0 = f16_bits_to_float(w.s.x & 0xFFFFu); o0 = f16_bits_to_float(w.s.x >> 16);
-                s1 = f16_bits_to_float(w.s.y & 0xFFFFu); o1 = f16_bits_to_float(w.s.y >> 16);
+#pragma unroll
+        for (int b = 0; b < NS / 2; ++b) {
+            const uint4 q = w.q[b];
+            d[2 * b] = half_dot(q.x & kLow, (q.x >> 4) & kLow, q.y & kLow, (q.y >> 4) & kLow, a[2 * b]);
+            d[2 * b + 1] = half_dot(q.z & kLow, (q.z >> 4) & kLow, q.w & kLow, (q.w >> 4) & kLow, a[2 * b + 1]);
+            if constexpr (FMT == VKML_Q4_1) {
+                const float sc = F16S ? f16_bits_to_float(w.s[2 * b] & 0xFFFFu) : __uint_as_float(w.s[2 * b]);
+                const float of = F16S ? f16_bits_to_float(w.s[2 * b] >> 16) : __uint_as_float(w.s[2 * b + 1]);
+                s[2 * b] = s[2 * b + 1] = sc;
+                o[2 * b] = o[2 * b + 1] = of;
             } else {
-                s0 = __uint_as_float(w.s.x); o0 = __uint_as_float(w.s.y); s1 = __uint_as_float(w.s.z); o1 = __uint_as_float(w.s.w);
+                s[2 * b] = s[2 * b + 1] = scale_of(w.s[b], F16S);
             }
-        } else {
-            if constexpr (F16S) { s0 = f16_bits_to_float(w.s.x & 0xFFFFu); s1 = f16_bits_to_float(w.s.x >> 16); }
-            else { s0 = __uint_as_float(w.s.x); s1 = __uint_as_float(w.s.y); }
-            // q4_0 codes are q + 8: the reference's signed bytes q4_bytes give
-            // the same exact sum, d - 8 * sum(a).
-            d[0] -= 8 * static_cast<int>(S.x); d[1] -= 8 * static_cast<int>(S.y);
-            d[2] -= 8 * static_cast<int>(S.z); d[3] -= 8 * static_cast<int>(S.w);
         }
     }
-    const float sum[4] = {S.x, S.y, S.z, S.w};
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        const float scale = h < 2 ? s0 : s1, a_scale = h < 2 ? sa.x : sa.y;
+    for (int e = 0; e < NS; ++e) {
+        if (!live[e]) continue;
+        const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
+        const float sa = s_sa[hb / 2];
         if constexpr (FMT == VKML_Q4_1 || FMT == VKML_Q4_K) {
-            const float offset = h < 2 ? o0 : o1;
-            acc[h] += a_scale * (static_cast<float>(d[h]) * scale + sum[h] * offset);
+            acc[e] += sa * (static_cast<float>(d[e]) * s[e] + s_sum[hb] * o[e]);
         } else {
-            acc[h] += static_cast<float>(d[h]) * (scale * a_scale);
+            // q4_0 codes are q + 8: the reference's signed bytes (q4_bytes)
+            // give the same exact sum, d - 8 * sum(a).
+            if constexpr (FMT == VKML_Q4_0) d[e] -= 8 * static_cast<int>(s_sum[hb]);
+            acc[e] += static_cast<float>(d[e]) * (s[e] * sa);
         }
     }
 }
 
-// The halving tree over the 32 accumulators of the 8-lane group; the row's
-// sum ends in lane 0 of the group (gemv_dot.comp:370-375).
-__device__ __forceinline__ float tree32(float (&acc)[4]) {
+// The halving tree over the 32 accumulators of a row, strides 16, 8, 4, 2,
+// 1 (gemv_dot.comp:121-131), each an exchange between the row's lanes or an
+// addition within a lane as the mapping places accumulator L + stride.
+template <int FMT, int LPR>
+__device__ __forceinline__ float row_tree(float (&acc)[32 / LPR]) {
 #pragma clang fp contract(off)
+    const auto x = [&](int mask, int slots) {
 #pragma unroll
-    for (int off = 4; off >= 1; off >>= 1)
-#pragma unroll
-        for (int h = 0; h < 4; ++h) acc[h] += __shfl_xor(acc[h], off, kWave);
-    acc[0] += acc[2];
-    acc[1] += acc[3];
-    return acc[0] + acc[1];
+        for (int e = 0; e < 32 / LPR; ++e)
+            if (e < slots) acc[e] += __shfl_xor(acc[e], mask, kWave);
+    };
+    if constexpr (FMT == VKML_Q8_0 && LPR == 16) {  // L = l + 16e
+        acc[0] += acc[1];
+        x(8, 1); x(4, 1); x(2, 1); x(1, 1);
+    } else if constexpr (FMT == VKML_Q8_0) {  // L = j + 8e
+        acc[0] += acc[2]; acc[1] += acc[3];
+        acc[0] += acc[1];
+        x(4, 1); x(2, 1); x(1, 1);
+    } else if constexpr (FMT == VKML_Q4_K && LPR == 16) {  // L = 16p + 4c + h + 2e, l = 8p + 2c + h
+        x(8, 2); x(4, 2); x(2, 2);
+        acc[0] += acc[1];
+        x(1, 1);
+    } else if constexpr (LPR == 16) {  // q4_0 / q4_1: L = 2l + e
+        x(8, 2); x(4, 2); x(2, 2); x(1, 2);
+        acc[0] += acc[1];
+    } else {  // L = 4j + e: q4_0 / q4_1 / q4_K with 8 lanes
+        x(4, 4); x(2, 4); x(1, 4);
+        acc[0] += acc[2]; acc[1] += acc[3];
+        acc[0] += acc[1];
+    }
+    return acc[0];
 }
 
 enum { kStore = 0, kAdd = 1, kSwiglu = 2 };
 
-template <int FMT, bool F16S, int EPI>
-__global__ void __launch_bounds__(256) k_gemv_dot(GemvArgs g) {
+template <int FMT, bool F16S, int LPR, int EPI, int B>
+__global__ void __launch_bounds__(kThreads) k_gemv_dot(GemvArgs g) {
 #pragma clang fp contract(off)
+    constexpr int NS = Plan<FMT, LPR>::NS;
+    constexpr int NM = EPI == kSwiglu ? 2 : 1;
     extern __shared__ uint4 smem[];
     const uint32_t K = g.k;
+    const uint32_t rounds = (K + 511) / 512;
+    const uint32_t l = threadIdx.x % LPR;
+    const uint32_t row = blockIdx.x * (kThreads / LPR) + threadIdx.x / LPR;
+    const uint32_t r_row = min(row, g.n - 1);
+
+    RoundW<FMT, LPR> wa[B][NM], wb[B][NM];
+    const auto load_batch = [&](RoundW<FMT, LPR> (&w)[B][NM], uint32_t r0) {
+        // Rounds past the last reload the last one (cache hits): unconditional loads.
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const uint32_t r = min(r0 + i, rounds - 1);
+            load_round<FMT, F16S, LPR>(g.b_values, g.b_scales, K, r_row, r, l, w[i][0]);
+            if constexpr (NM == 2) load_round<FMT, F16S, LPR>(g.b2_values, g.b2_scales, K, r_row, r, l, w[i][NM - 1]);
+        }
+    };
+    // The first batch of weights is in flight while the activations are staged.
+    load_batch(wa, 0);
+
     uint4* s_codes = smem;                                   // K / 16 half-blocks of codes
     float* s_sum = reinterpret_cast<float*>(smem + K / 16);  // each half-block's code sum
     float* s_sa = s_sum + K / 16;                            // each block's activation scale
-    for (uint32_t h = threadIdx.x; h < K / 16; h += blockDim.x) {
-        const uint4 c = g.a_values[h];
-        s_codes[h] = c;
-        s_sum[h] = static_cast<float>(byte_sum(c));
-        if (h % 2 == 0) s_sa[h / 2] = g.a_scales[h / 2];
+    const uint32_t halves = K / 16;
+    for (uint32_t h0 = threadIdx.x; h0 < halves; h0 += 4 * kThreads) {
+        uint4 c[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t h = h0 + i * kThreads;
+            c[i] = h < halves ? g.a_values[h] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t h = h0 + i * kThreads;
+            if (h < halves) {
+                s_codes[h] = c[i];
+                s_sum[h] = static_cast<float>(byte_sum(c[i]));
+            }
+        }
     }
+    for (uint32_t b = threadIdx.x; b < K / 32; b += kThreads) s_sa[b] = g.a_scales[b];
     __syncthreads();
-    const uint32_t lane8 = threadIdx.x % 8;
-    const uint32_t row = blockIdx.x * (blockDim.x / 8) + threadIdx.x / 8;
-    const uint32_t r = min(row, g.n - 1);
-    constexpr int NM = EPI == kSwiglu ? 2 : 1;
-    constexpr int U = (FMT == VKML_Q8_0 || NM == 2) ? 2 : 4;  // tasks in flight per lane
-    float acc[NM][4];
+
+    float acc[NM][NS];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int h = 0; h < 4; ++h) acc[m][h] = 0.0f;
-    const uint32_t tasks = K / 64;
-    const float4* sum4 = reinterpret_cast<const float4*>(s_sum);
-    const float2* sa2 = reinterpret_cast<const float2*>(s_sa);
-    for (uint32_t t0 = lane8; t0 < tasks; t0 += 8 * U) {
-        Wt w[U][NM];
+        for (int e = 0; e < NS; ++e) acc[m][e] = 0.0f;
+    const auto sum_batch = [&](const RoundW<FMT, LPR> (&w)[B][NM], uint32_t r0) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t t = t0 + 8 * u;
-            if (t < tasks) {
-                load_task<FMT, F16S>(g.b_values, g.b_scales, K, r, t, w[u][0]);
-                if constexpr (NM == 2) load_task<FMT, F16S>(g.b2_values, g.b2_scales, K, r, t, w[u][NM - 1]);
+        for (int i = 0; i < B; ++i) {
+            if (r0 + i < rounds) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m) round_terms<FMT, F16S, LPR>(w[i][m], r0 + i, l, K, s_codes, s_sum, s_sa, acc[m]);
             }
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t t = t0 + 8 * u;
-            if (t < tasks) {
-                const uint4 a[4] = {s_codes[4 * t], s_codes[4 * t + 1], s_codes[4 * t + 2], s_codes[4 * t + 3]};
-                const float4 S = sum4[t];
-                const float2 sa = sa2[t];
-#pragma unroll
-                for (int m = 0; m < NM; ++m) task_terms<FMT, F16S>(w[u][m], t, a, S, sa, acc[m]);
-            }
-        }
+    };
+    for (uint32_t r0 = 0; r0 < rounds; r0 += 2 * B) {
+        load_batch(wb, r0 + B);
+        sum_batch(wa, r0);
+        load_batch(wa, r0 + 2 * B);
+        sum_batch(wb, r0 + B);
     }
+
     float y[NM];
 #pragma unroll
-    for (int m = 0; m < NM; ++m) y[m] = tree32(acc[m]);
-    if (lane8 == 0 && row < g.n) {
+    for (int m = 0; m < NM; ++m) y[m] = row_tree<FMT, LPR>(acc[m]);
+    if (l == 0 && row < g.n) {
         if constexpr (EPI == kStore) {
             g.out[row] = y[0];
         } else if constexpr (EPI == kAdd) {
@@ -219,17 +367,22 @@ __global__ void __launch_bounds__(256) k_gemv_dot(GemvArgs g) {
     }
 }
 
-template <int FMT, bool F16S, int EPI>
-int dispatch(const GemvArgs& g, const char* label) {
-    // Rows per workgroup (8 per wave): enough workgroups to cover the CUs twice.
-    const uint32_t cus = std::max<uint32_t>(vkml::abi::compute_units(), 1);
-    uint32_t threads = 256;
-    while (threads > 64 && (g.n + threads / 8 - 1) / (threads / 8) < 2 * cus) threads /= 2;
-    const dim3 grid((g.n + threads / 8 - 1) / (threads / 8));
+template <int FMT, bool F16S, int LPR, int EPI>
+int launch(const GemvArgs& g, const char* label) {
+    constexpr int B = LPR == 16 ? 4 : 2;  // rounds per batch
+    const dim3 grid((g.n + kThreads / LPR - 1) / (kThreads / LPR));
     const size_t lds = g.k + g.k / 16 * 4 + g.k / 32 * 4;
     vkml::abi::ProfileScope prof(label);
-    hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, EPI>), grid, dim3(threads), lds, vkml::abi::stream(), g);
+    hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B>), grid, dim3(kThreads), lds, vkml::abi::stream(), g);
     return vkml::abi::check_launch(label);
+}
+
+template <int FMT, bool F16S, int EPI>
+int dispatch(const GemvArgs& g, const char* label) {
+    // 8 lanes a row unless that leaves fewer than one wave per SIMD.
+    const uint64_t simds = 4ull * std::max<uint32_t>(vkml::abi::compute_units(), 1);
+    if ((g.n + 7) / 8 < simds) return launch<FMT, F16S, 16, EPI>(g, label);
+    return launch<FMT, F16S, 8, EPI>(g, label);
 }
 
 template <int EPI>

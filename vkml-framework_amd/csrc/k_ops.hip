@@ -177,16 +177,33 @@ __device__ float tree256_sum(float v, float* scratch) {
     return r;
 }
 
+// Invocation t's sum of x[c]^2 over c = t, t + 256, ... in that order
+// (rms_norm.comp:38), its loads issued eight at a time.
+__device__ __forceinline__ float strided_sum_sq(const float* xr, uint32_t cols) {
+    float s = 0.0f;
+    for (uint32_t c0 = threadIdx.x; c0 < cols; c0 += 8 * kRowThreads) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t c = c0 + j * kRowThreads;
+            v[j] = c < cols ? xr[c] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (c0 + j * kRowThreads < cols) s += v[j] * v[j];
+    }
+    return s;
+}
+
 // rms_norm.comp:35-49: invocation t sums x[c]^2 over c = t, t + 256, ...;
 // scale = 1 / sqrt(sum / cols + eps); out = x * scale * w.
 __global__ void __launch_bounds__(kRowThreads) k_rms_norm(vkml_rms_norm_params p, const float* x, const float* w, float* out) {
     __shared__ float scratch[kRowThreads + 1];
     for (uint32_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
         const float* xr = x + static_cast<uint64_t>(row) * p.cols;
-        float s = 0.0f;
-        for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads) s += xr[c] * xr[c];
-        s = tree256_sum(s, scratch);
+        const float s = tree256_sum(strided_sum_sq(xr, p.cols), scratch);
         const float scale = 1.0f / sqrtf(s / static_cast<float>(p.cols) + p.eps);
+#pragma unroll 4
         for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads)
             out[static_cast<uint64_t>(row) * p.cols + c] = xr[c] * scale * w[c];
     }
@@ -200,11 +217,10 @@ __global__ void __launch_bounds__(kRowThreads) k_rms_norm_quantize(vkml_rms_norm
     __shared__ float scratch[kRowThreads + 1];
     const uint32_t row = blockIdx.x, n4 = p.cols / 4;
     const float* xr = x + static_cast<uint64_t>(row) * p.cols;
-    float s = 0.0f;
-    for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads) s += xr[c] * xr[c];
-    s = tree256_sum(s, scratch);
+    const float s = tree256_sum(strided_sum_sq(xr, p.cols), scratch);
     const float scale = 1.0f / sqrtf(s / static_cast<float>(p.cols) + p.eps);
     const float4* xr4 = reinterpret_cast<const float4*>(xr);
+#pragma unroll 4
     for (uint32_t i = threadIdx.x; i < n4; i += kRowThreads) {
         // n4 is a multiple of 8, so the 8 lanes of a block are live together.
         const float4 v = xr4[i], wv = w[i];
@@ -261,17 +277,44 @@ __device__ __forceinline__ void better(float& v, int& c, float ov, int oc) {
     }
 }
 
+__device__ __forceinline__ void consider(float& best, int& col, float v, uint32_t c) {
+    if (!__builtin_isnan(v) && (col < 0 || v > best)) {
+        best = v;
+        col = static_cast<int>(c);
+    }
+}
+
+// Each thread visits its columns in increasing order (a float4 per step
+// when the row is 16-byte aligned, four steps' loads at a time), so ties
+// keep the earliest; the reduction breaks ties the same way.
 __device__ int block_argmax(const float* x, uint32_t cols) {
     __shared__ float s_v[16];
     __shared__ int s_c[16];
     float best = 0.0f;
     int col = -1;
-    for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
-        const float v = x[c];
-        if (!__builtin_isnan(v) && (col < 0 || v > best)) {
-            best = v;
-            col = static_cast<int>(c);
+    if (cols % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        const uint32_t n4 = cols / 4;
+        for (uint32_t i0 = threadIdx.x; i0 < n4; i0 += 4 * blockDim.x) {
+            float4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t i = i0 + j * blockDim.x;
+                v[j] = i < n4 ? x4[i] : make_float4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t i = i0 + j * blockDim.x;
+                if (i < n4) {
+                    consider(best, col, v[j].x, 4 * i);
+                    consider(best, col, v[j].y, 4 * i + 1);
+                    consider(best, col, v[j].z, 4 * i + 2);
+                    consider(best, col, v[j].w, 4 * i + 3);
+                }
+            }
         }
+    } else {
+        for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) consider(best, col, x[c], c);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) better(best, col, __shfl_xor(best, o, kWave), __shfl_xor(col, o, kWave));

@@ -343,6 +343,8 @@ int vkml_synchronize(void) {
     return VKML_OK;
 }
 
+void* vkml_stream(void) { return g.ready ? static_cast<void*>(g.stream) : nullptr; }
+
 int vkml_set_profiling(int enabled) {
     VKML_REQUIRE_INIT();
     g.profiling = enabled != 0;

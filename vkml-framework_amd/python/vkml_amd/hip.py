@@ -59,6 +59,9 @@ AttendParams = _struct("AttendParams", [("kv_start", u32), ("kv_len", u32), ("ca
                                         ("scale", f32), ("softcap", f32)])
 RopeKvParams = _struct("RopeKvParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
                                         ("position", u32), ("style", u32), ("kv_type", u32), ("rotate", u32)])
+AttendStepParams = _struct("AttendStepParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
+                                                ("kv_start", u32), ("position", u32), ("kv_type", u32), ("chunks", u32),
+                                                ("rope_style", u32), ("rotate", u32), ("scale", f32), ("softcap", f32)])
 
 P = C.POINTER
 # name -> argtypes (all return int status unless noted)
@@ -80,6 +83,7 @@ SIGNATURES = {
     "vkml_wait": [u64],
     "vkml_completed": [P(u64)],
     "vkml_synchronize": [],
+    "vkml_stream": [],
     "vkml_set_profiling": [C.c_int],
     "vkml_get_profiling": [],
     "vkml_set_profile_tag": [C.c_char_p],
@@ -110,6 +114,7 @@ SIGNATURES = {
     "vkml_attend": [P(AttendParams), vp, vp, vp, vp, vp, vp],
     "vkml_attend_merge": [P(AttendParams), vp, vp, vp, vp, vp],
     "vkml_rope_kv_append": [P(RopeKvParams), vp, vp, vp, vp, vp, vp],
+    "vkml_attend_step": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_state_set": [vp, i32, i32, i32],
     "vkml_embedding_state": [P(EmbeddingParams), vp, vp, vp, vp],
     "vkml_step_finish": [u32, vp, vp, vp, u32],
@@ -134,6 +139,7 @@ def lib() -> C.CDLL:
             fn = getattr(_lib, name)
             fn.argtypes = args
             fn.restype = C.c_int
+        _lib.vkml_stream.restype = C.c_void_p
     return _lib
 
 
@@ -163,6 +169,11 @@ def device_info() -> DeviceInfo:
 
 def synchronize() -> None:
     call("vkml_synchronize")
+
+
+def stream() -> int:
+    """The library's hipStream_t (an integer handle), or 0 before vkml_init."""
+    return lib().vkml_stream() or 0
 
 
 class Buffer:

@@ -362,25 +362,21 @@ struct Llama::Impl {
                 check(vkml_rms_norm(&np, xp, static_cast<const float*>(w.data()), static_cast<float*>(xn.data())), "rms_norm");
             }
         };
-        const vkml_attend_params ap{0, 0, u32(context_length), u32(c.num_heads), u32(c.num_kv_heads), u32(hd),
-                                    detail::type_code(layers[0].k_cache.dtype()), u32(chunks), 1.0f / std::sqrt(static_cast<float>(hd)), 0.0f};
         for (const Layer& L : layers) {
             norm(L.attn_norm, "attn_norm");
             for (const auto& [w, row] : L.qkv)
                 project(w, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(qkv.data()) + row, nullptr, "qkv");
-            tag("rope_kv");
-            const vkml_rope_kv_params rp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(context_length), 0,
-                                         c.rope_style == RopeStyle::Interleaved ? 0u : 1u, detail::type_code(L.k_cache.dtype()), 1};
-            check(vkml_rope_kv_append(&rp, static_cast<const float*>(qkv.data()), static_cast<const float*>(rope.data()),
-                                      static_cast<float*>(q.data()), L.k_cache.data(), L.v_cache.data(), st),
-                  "rope_kv_append");
-            tag("attention");
-            check(vkml_attend(&ap, static_cast<const float*>(q.data()), L.k_cache.data(), L.v_cache.data(), static_cast<float*>(partial.data()),
-                              static_cast<float*>(stats.data()), st),
-                  "attention");
             const bool o_q = quantized_input(L.o);
-            check(vkml_attend_merge(&ap, static_cast<const float*>(partial.data()), static_cast<const float*>(stats.data()),
-                                    static_cast<float*>(attn.data()), o_q ? aq.data() : nullptr, o_q ? static_cast<float*>(as.data()) : nullptr),
+            const uint32_t kv_code = detail::type_code(L.k_cache.dtype());
+            // rope, append and attention in one launch, then the merge
+            tag("attention");
+            const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(context_length), 0, 0, kv_code,
+                                             u32(chunks), c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
+                                             1.0f / std::sqrt(static_cast<float>(hd)), 0.0f};
+            check(vkml_attend_step(&sp, static_cast<const float*>(qkv.data()), static_cast<const float*>(rope.data()), L.k_cache.data(),
+                                   L.v_cache.data(), static_cast<float*>(partial.data()), static_cast<float*>(stats.data()),
+                                   static_cast<float*>(attn.data()), o_q ? aq.data() : nullptr,
+                                   o_q ? static_cast<float*>(as.data()) : nullptr, st),
                   "attention");
             project(L.o, attn, o_q ? &aq : nullptr, &as, xp, xp, "o");
             norm(L.ffn_norm, "ffn_norm");

@@ -3,12 +3,12 @@
 // config.cpp:14-140).
 //
 // The reference records ~29 dispatches per layer, each separated by a full
-// barrier. Here one decode step (t = 1) is nine kernels per layer, all
+// barrier. Here one decode step (t = 1) is eight kernels per layer, all
 // reading the step's token and position from a small device-side state:
-//   rms_norm + Q8_0 quantize -> q|k|v GEMV (one fused matrix) -> rope + f16
-//   cast + KV append -> split-K attention -> merge + Q8_0 quantize ->
-//   o GEMV + residual -> rms_norm + quantize -> gate|up GEMV + SwiGLU ->
-//   quantize -> down GEMV + residual,
+//   rms_norm + Q8_0 quantize -> q|k|v GEMV (one fused matrix) -> attention
+//   chunks (rope of q and k, f16 cast and KV append inside) -> merge + Q8_0
+//   quantize -> o GEMV + residual -> rms_norm + quantize -> gate|up GEMV +
+//   SwiGLU -> quantize -> down GEMV + residual,
 // then the final norm, the lm_head GEMV and (greedy) an argmax that writes
 // the next token into the state. The step is captured once as a HIP graph
 // and replayed, so a prompt or a greedy generation is a stream of graph
@@ -226,10 +226,8 @@ const LlamaConfig& validated(const LlamaConfig& c, std::int64_t context_length) 
         throw Error("Llama: context length " + std::to_string(context_length) + " must be between 1 and max_position_embeddings (" +
                     std::to_string(c.max_positions) + ")");
     }
-    const std::int64_t group = c.num_heads / c.num_kv_heads;
-    if ((c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) || (group != 1 && group != 2 && group != 4 && group != 8)) {
-        throw Error("Llama: head_dim " + std::to_string(c.head_dim) + " with " + std::to_string(group) +
-                    " query heads per KV head is not implemented (head_dim 64, 128 or 256; 1, 2, 4 or 8 heads per KV head are)");
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) {
+        throw Error("Llama: head_dim " + std::to_string(c.head_dim) + " is not implemented (64, 128 and 256 are)");
     }
     if (c.sliding_window || c.qkv_bias || c.o_bias || c.qk_norm || c.sandwich_norms || !c.pre_norms || c.embedding_scale != 1.0f ||
         c.residual_scale != 1.0f || c.logit_divisor != 1.0f || c.attn_logit_softcap != 0.0f || c.final_logit_softcap != 0.0f ||

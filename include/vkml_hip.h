@@ -202,6 +202,30 @@ int vkml_gemv_dot_swiglu(const vkml_gemv_dot_params* p, const void* d_a_values,
                          const void* d_gate_scales, const void* d_up_values,
                          const void* d_up_scales, float* d_h);
 
+/* vkml_gemv_dot with the steps around it folded in (no single reference
+ * counterpart: rms_norm.comp + quantize.comp before gemv_dot.comp, and
+ * binary/unary + quantize.comp after, as llama.cpp:313-386 dispatches them).
+ * norm = 1: d_a is the f32 row x [k], RMS-normalized with d_norm_weight and
+ * eps and quantized to Q8_0 inside the kernel (k <= 4096), bit for bit as
+ * vkml_rms_norm_quantize; norm = 0: d_a / d_a_scales are its Q8_0 codes and
+ * f32 scales. epilogue 0 stores y, 1 adds d_residual (not with norm), 2 is
+ * SwiGLU with the up matrix d_b2_*; quantize_out (SwiGLU, n % 32 == 0) also
+ * writes h's Q8_0 codes and f32 scales. m = 1. */
+typedef struct vkml_gemv_fused_params {
+    uint32_t n;
+    uint32_t k;
+    uint32_t b_type;
+    uint32_t scale_type;
+    uint32_t epilogue;
+    uint32_t norm;
+    float eps;
+    uint32_t quantize_out;
+} vkml_gemv_fused_params;
+int vkml_gemv_fused(const vkml_gemv_fused_params* p, const void* d_a, const float* d_a_scales,
+                    const float* d_norm_weight, const void* d_b_values, const void* d_b_scales,
+                    const void* d_b2_values, const void* d_b2_scales, const float* d_residual,
+                    float* d_out, void* d_out_values, float* d_out_scales);
+
 /* shaders/gemv.comp, src/ops/matmul.cpp:88-120: the float path, c[m, n] =
  * a[m] . b[n] with f32 a (m <= 8) and b [n, k] of b_type F32/F16/BF16 or
  * Q8_0/Q4_0/Q4_1/Q4_K decoded in registers (ContextOptions::

@@ -190,6 +190,48 @@ def test_gemv_dot_add_and_swiglu(fmt):
     assert np.array_equal(bits(got), bits(O.silu(g) * u))
 
 
+@pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 6144, 4096), (H.Q4_K, 384, 256), (H.Q8_0, 8192, 4096), (H.Q4_0, 1024, 2048)])
+def test_gemv_fused_norm_prologue_bit_exact(fmt, n, k):
+    # rms_norm + Q8_0 inside the GEMV == the separate kernels' results
+    v, s, quant, words, scales = weights(fmt, n, k, n + 7)
+    rng = np.random.default_rng(k)
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    nw = rng.standard_normal(k).astype(np.float32)
+    xn = O.rms_norm(x.reshape(1, k), nw, 1e-5)
+    aw, asc = O.quantize(O.Q8_0, xn, False)
+    want = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)[0]
+    out = H.empty(n * 4)
+    prm = H.GemvFusedParams(n, k, fmt, H.F16, 0, 1, 1e-5, 0)
+    H.call("vkml_gemv_fused", prm, p(dev(x)), None, p(dev(nw)), p(v), p(s), None, None, None, p(out), None, None)
+    assert np.array_equal(bits(out.download(np.float32, n)), bits(want))
+
+
+@pytest.mark.parametrize("norm", [0, 1])
+@pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 14336, 4096), (H.Q4_K, 512, 256), (H.Q8_0, 2048, 1024)])
+def test_gemv_fused_swiglu_quantized_output_bit_exact(norm, fmt, n, k):
+    v, s, quant, words, scales = weights(fmt, n, k, 41)
+    v2, s2, _, words2, scales2 = weights(fmt, n, k, 42)
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    nw = rng.standard_normal(k).astype(np.float32)
+    if norm:
+        aw, asc = O.quantize(O.Q8_0, O.rms_norm(x.reshape(1, k), nw, 1e-5), False)
+        a_in, a_sc = dev(x), None
+    else:
+        aw, asc = O.quantize(O.Q8_0, x.reshape(1, k), False)
+        a_in, a_sc = dev(aw), dev(asc)
+    g = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)[0]
+    u = O.gemv_dot(quant, aw, asc, 1, words2, scales2, n, k)[0]
+    want = O.silu(g) * u
+    hw, hs = O.quantize(O.Q8_0, want.reshape(1, n), False)
+    h, hv, hsc = H.empty(n * 4), H.empty(n), H.empty(n // 32 * 4)
+    prm = H.GemvFusedParams(n, k, fmt, H.F16, 2, norm, 1e-5, 1)
+    H.call("vkml_gemv_fused", prm, p(a_in), p(a_sc), p(dev(nw)), p(v), p(s), p(v2), p(s2), None, p(h), p(hv), p(hsc))
+    assert np.array_equal(bits(h.download(np.float32, n)), bits(want))
+    assert np.array_equal(hv.download(np.uint32, hw.shape), hw)
+    assert np.array_equal(hsc.download(np.float32, hs.shape).view(np.uint32), hs.view(np.uint32))
+
+
 @pytest.mark.parametrize("bt", [H.F32, H.F16, H.BF16, H.Q8_0, H.Q4_0, H.Q4_1, H.Q4_K])
 def test_float_gemv_path(bt):
     n, k, m = 100, 512, 2

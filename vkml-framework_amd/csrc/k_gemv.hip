@@ -41,7 +41,6 @@ using namespace vkml::dev;
 namespace {
 
 constexpr uint32_t kMaxK = 32768;  // LDS staging: K + K / 16 * 4 + K / 32 * 4 bytes
-constexpr uint32_t kThreads = 128;
 constexpr uint32_t kLow = 0x0F0F0F0Fu;
 
 struct GemvArgs {
@@ -54,6 +53,14 @@ struct GemvArgs {
     float* out;
     const float* residual;
     uint32_t n, k;
+    // With the RMSNorm prologue: the f32 input row, its norm weight and eps
+    // (the activation codes are then computed, not read).
+    const float* x;
+    const float* norm_weight;
+    float eps;
+    // SwiGLU with the Q8_0 epilogue: the codes and f32 scales of h.
+    uint8_t* out_values;
+    float* out_scales;
 };
 
 // The accumulator (= half-block of the round) held in slot e of lane l.
@@ -282,8 +289,98 @@ __device__ __forceinline__ float row_tree(float (&acc)[32 / LPR]) {
 
 enum { kStore = 0, kAdd = 1, kSwiglu = 2 };
 
-template <int FMT, bool F16S, int LPR, int EPI, int B>
-__global__ void __launch_bounds__(kThreads) k_gemv_dot(GemvArgs g) {
+// The prologue that replaces a separate rms_norm + quantize launch: RMSNorm
+// of x in rms_norm.comp's order at its workgroup width of 256 (invocation v
+// sums x[c]^2 over c = v, v + 256, ...; then the halving tree), emulated by
+// T threads; then y = x * scale * w and Q8_0 per 32 values
+// (quantize.comp:100-111), written to LDS as the activation codes,
+// half-block code sums and block scales: vkml_rms_norm_quantize's results
+// bit for bit. K <= 4096 and T >= 128, so a thread owns at most one 32-value
+// block; its block of x and w and its strided elements for the sum are all
+// loaded at once, into registers: one round trip.
+template <uint32_t T>
+struct NormLoads {
+    static constexpr uint32_t V = T >= 256 ? 1 : 256 / T;  // invocations per thread (t, t + T, ... below 256)
+    static constexpr uint32_t kMaxPer = 4096 / 256;        // elements per invocation at K <= 4096
+    float4 xb[8], wb[8];                                   // the thread's 32-value block of x and w
+    float xv[V][kMaxPer];                                  // its invocations' strided elements
+};
+
+template <uint32_t T>
+__device__ __forceinline__ void norm_loads(const float* x, const float* w, uint32_t K, NormLoads<T>& r) {
+    const uint32_t t = threadIdx.x, blk = t < K / 32 ? t : 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        r.xb[i] = reinterpret_cast<const float4*>(x)[8 * blk + i];
+        r.wb[i] = reinterpret_cast<const float4*>(w)[8 * blk + i];
+    }
+#pragma unroll
+    for (uint32_t v = 0; v < NormLoads<T>::V; ++v)
+#pragma unroll
+        for (uint32_t j = 0; j < NormLoads<T>::kMaxPer; ++j) r.xv[v][j] = x[min((t + v * T) % 256 + 256 * j, K - 1)];
+}
+
+template <uint32_t T>
+__device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float* s_sum, float* s_sa,
+                                       float* s_red) {
+#pragma clang fp contract(off)
+    static_assert(T >= 128, "workgroup width");
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (uint32_t v = 0; v < NormLoads<T>::V; ++v) {
+        const uint32_t inv = t + v * T;
+        float part = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < NormLoads<T>::kMaxPer; ++j)
+            if (inv + 256 * j < K) part += r.xv[v][j] * r.xv[v][j];
+        if (inv < 256) s_red[inv] = part;
+    }
+    // The halving tree over the 256 invocations: strides 128, 64, then 32 .. 1 in wave 0.
+    __syncthreads();
+    if (t < 128) s_red[t] = s_red[t] + s_red[t + 128];
+    __syncthreads();
+    if (t < 64) {
+        float v = s_red[t] + s_red[t + 64];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+        if (t == 0) s_red[256] = v;
+    }
+    __syncthreads();
+    if (t >= K / 32) return;
+    const uint32_t blk = t;
+    const float scale = 1.0f / sqrtf(s_red[256] / static_cast<float>(K) + eps);
+    float y[32];
+    float absmax = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        const float xs[4] = {r.xb[i].x, r.xb[i].y, r.xb[i].z, r.xb[i].w}, ws[4] = {r.wb[i].x, r.wb[i].y, r.wb[i].z, r.wb[i].w};
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) {
+            y[4 * i + e] = xs[e] * scale * ws[e];
+            absmax = fmaxf(absmax, fabsf(y[4 * i + e]));
+        }
+    }
+    const float d = absmax / 127.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    uint32_t words[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) {
+        words[q] = (static_cast<uint32_t>(quant_code(y[4 * q], inv)) & 0xFFu) |
+                   ((static_cast<uint32_t>(quant_code(y[4 * q + 1], inv)) & 0xFFu) << 8) |
+                   ((static_cast<uint32_t>(quant_code(y[4 * q + 2], inv)) & 0xFFu) << 16) |
+                   (static_cast<uint32_t>(quant_code(y[4 * q + 3], inv)) << 24);
+    }
+    const uint4 lo = make_uint4(words[0], words[1], words[2], words[3]);
+    const uint4 hi = make_uint4(words[4], words[5], words[6], words[7]);
+    s_codes[2 * blk] = lo;
+    s_codes[2 * blk + 1] = hi;
+    s_sum[2 * blk] = static_cast<float>(byte_sum(lo));
+    s_sum[2 * blk + 1] = static_cast<float>(byte_sum(hi));
+    s_sa[blk] = d;
+}
+
+template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool NORM, bool QOUT>
+__global__ void __launch_bounds__(T) k_gemv_dot(GemvArgs g) {
 #pragma clang fp contract(off)
     constexpr int NS = Plan<FMT, LPR>::NS;
     constexpr int NM = EPI == kSwiglu ? 2 : 1;
@@ -291,7 +388,7 @@ __global__ void __launch_bounds__(kThreads) k_gemv_dot(GemvArgs g) {
     const uint32_t K = g.k;
     const uint32_t rounds = (K + 511) / 512;
     const uint32_t l = threadIdx.x % LPR;
-    const uint32_t row = blockIdx.x * (kThreads / LPR) + threadIdx.x / LPR;
+    const uint32_t row = blockIdx.x * (T / LPR) + threadIdx.x / LPR;
     const uint32_t r_row = min(row, g.n - 1);
 
     RoundW<FMT, LPR> wa[B][NM], wb[B][NM];
@@ -311,23 +408,30 @@ __global__ void __launch_bounds__(kThreads) k_gemv_dot(GemvArgs g) {
     float* s_sum = reinterpret_cast<float*>(smem + K / 16);  // each half-block's code sum
     float* s_sa = s_sum + K / 16;                            // each block's activation scale
     const uint32_t halves = K / 16;
-    for (uint32_t h0 = threadIdx.x; h0 < halves; h0 += 4 * kThreads) {
-        uint4 c[4];
+    if constexpr (NORM) {
+        NormLoads<T> nl;
+        norm_loads<T>(g.x, g.norm_weight, K, nl);
+        float* s_red = s_sa + K / 32;  // 257 floats
+        norm_quantize_prologue<T>(nl, g.eps, K, s_codes, s_sum, s_sa, s_red);
+    } else {
+        for (uint32_t h0 = threadIdx.x; h0 < halves; h0 += 4 * T) {
+            uint4 c[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t h = h0 + i * kThreads;
-            c[i] = h < halves ? g.a_values[h] : make_uint4(0, 0, 0, 0);
-        }
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t h = h0 + i * T;
+                c[i] = h < halves ? g.a_values[h] : make_uint4(0, 0, 0, 0);
+            }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t h = h0 + i * kThreads;
-            if (h < halves) {
-                s_codes[h] = c[i];
-                s_sum[h] = static_cast<float>(byte_sum(c[i]));
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t h = h0 + i * T;
+                if (h < halves) {
+                    s_codes[h] = c[i];
+                    s_sum[h] = static_cast<float>(byte_sum(c[i]));
+                }
             }
         }
+        for (uint32_t b = threadIdx.x; b < K / 32; b += T) s_sa[b] = g.a_scales[b];
     }
-    for (uint32_t b = threadIdx.x; b < K / 32; b += kThreads) s_sa[b] = g.a_scales[b];
     __syncthreads();
 
     float acc[NM][NS];
@@ -354,45 +458,64 @@ __global__ void __launch_bounds__(kThreads) k_gemv_dot(GemvArgs g) {
     float y[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) y[m] = row_tree<FMT, LPR>(acc[m]);
+    float result = 0.0f;
     if (l == 0 && row < g.n) {
         if constexpr (EPI == kStore) {
-            g.out[row] = y[0];
+            result = y[0];
         } else if constexpr (EPI == kAdd) {
-            g.out[row] = g.residual[row] + y[0];  // add(x, attn_out), llama.cpp:374,386
+            result = g.residual[row] + y[0];  // add(x, attn_out), llama.cpp:374,386
         } else {
             // silu(gate) * up (unary.comp:21-24, then binary.comp's mul)
             const float gate = y[0], up = y[NM - 1];
-            g.out[row] = gate / (1.0f + vk_expf(-gate)) * up;
+            result = gate / (1.0f + vk_expf(-gate)) * up;
+        }
+        g.out[row] = result;
+    }
+    if constexpr (QOUT) {
+        // The workgroup's T / LPR = 32 rows are one Q8_0 block of the output
+        // (quantize.comp:100-111): its absmax, scale and codes.
+        static_assert(T / LPR == 32, "one Q8_0 block per workgroup");
+        __shared__ float s_out[32];
+        if (l == 0) s_out[threadIdx.x / LPR] = result;
+        __syncthreads();
+        if (threadIdx.x < 32) {
+            const float v = s_out[threadIdx.x];
+            const float absmax = group_max<32>(fabsf(v));
+            const float d = absmax / 127.0f;
+            const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+            g.out_values[blockIdx.x * 32 + threadIdx.x] = static_cast<uint8_t>(static_cast<int8_t>(quant_code(v, inv)));
+            if (threadIdx.x == 0) g.out_scales[blockIdx.x] = d;
         }
     }
 }
 
-template <int FMT, bool F16S, int LPR, int EPI>
+template <int FMT, bool F16S, int LPR, int EPI, bool NORM, bool QOUT>
 int launch(const GemvArgs& g, const char* label) {
     constexpr int B = LPR == 16 ? 4 : 2;  // rounds per batch
-    const dim3 grid((g.n + kThreads / LPR - 1) / (kThreads / LPR));
-    const size_t lds = g.k + g.k / 16 * 4 + g.k / 32 * 4;
+    constexpr uint32_t T = QOUT ? 32 * LPR : 128;
+    const dim3 grid((g.n + T / LPR - 1) / (T / LPR));
+    const size_t lds = g.k + g.k / 16 * 4 + g.k / 32 * 4 + (NORM ? 257 * 4 : 0);
     vkml::abi::ProfileScope prof(label);
-    hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B>), grid, dim3(kThreads), lds, vkml::abi::stream(), g);
+    hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT>), grid, dim3(T), lds, vkml::abi::stream(), g);
     return vkml::abi::check_launch(label);
 }
 
-template <int FMT, bool F16S, int EPI>
+template <int FMT, bool F16S, int EPI, bool NORM, bool QOUT>
 int dispatch(const GemvArgs& g, const char* label) {
     // 8 lanes a row unless that leaves fewer than one wave per SIMD.
     const uint64_t simds = 4ull * std::max<uint32_t>(vkml::abi::compute_units(), 1);
-    if ((g.n + 7) / 8 < simds) return launch<FMT, F16S, 16, EPI>(g, label);
-    return launch<FMT, F16S, 8, EPI>(g, label);
+    if ((g.n + 7) / 8 < simds) return launch<FMT, F16S, 16, EPI, NORM, QOUT>(g, label);
+    return launch<FMT, F16S, 8, EPI, NORM, QOUT>(g, label);
 }
 
-template <int EPI>
+template <int EPI, bool NORM = false, bool QOUT = false>
 int dispatch_format(uint32_t b_type, uint32_t scale_type, const GemvArgs& g, const char* label) {
     const bool f16 = scale_type == VKML_F16;
     switch (b_type) {
-        case VKML_Q8_0: return f16 ? dispatch<VKML_Q8_0, true, EPI>(g, label) : dispatch<VKML_Q8_0, false, EPI>(g, label);
-        case VKML_Q4_0: return f16 ? dispatch<VKML_Q4_0, true, EPI>(g, label) : dispatch<VKML_Q4_0, false, EPI>(g, label);
-        case VKML_Q4_1: return f16 ? dispatch<VKML_Q4_1, true, EPI>(g, label) : dispatch<VKML_Q4_1, false, EPI>(g, label);
-        case VKML_Q4_K: return dispatch<VKML_Q4_K, true, EPI>(g, label);
+        case VKML_Q8_0: return f16 ? dispatch<VKML_Q8_0, true, EPI, NORM, QOUT>(g, label) : dispatch<VKML_Q8_0, false, EPI, NORM, QOUT>(g, label);
+        case VKML_Q4_0: return f16 ? dispatch<VKML_Q4_0, true, EPI, NORM, QOUT>(g, label) : dispatch<VKML_Q4_0, false, EPI, NORM, QOUT>(g, label);
+        case VKML_Q4_1: return f16 ? dispatch<VKML_Q4_1, true, EPI, NORM, QOUT>(g, label) : dispatch<VKML_Q4_1, false, EPI, NORM, QOUT>(g, label);
+        case VKML_Q4_K: return dispatch<VKML_Q4_K, true, EPI, NORM, QOUT>(g, label);
         default: return vkml::abi::fail(VKML_ERROR_UNSUPPORTED, std::string(label) + ": no int8 kernel for weight type " + std::to_string(b_type));
     }
 }
@@ -496,6 +619,42 @@ int vkml_gemv_dot_swiglu(const vkml_gemv_dot_params* p, const void* a_values, co
                    "gemv_dot_swiglu: null buffer");
     GemvArgs g{static_cast<const uint4*>(a_values), a_scales, gate_values, gate_scales, up_values, up_scales, h, nullptr, p->n, p->k};
     return dispatch_format<kSwiglu>(p->b_type, p->scale_type, g, "gemv_dot_swiglu");
+}
+
+int vkml_gemv_fused(const vkml_gemv_fused_params* p, const void* a, const float* a_scales, const float* norm_weight,
+                    const void* b_values, const void* b_scales, const void* b2_values, const void* b2_scales,
+                    const float* residual, float* out, void* out_values, float* out_scales) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "gemv_fused: null params");
+    const vkml_gemv_dot_params dp{1, p->n, p->k, p->b_type, p->scale_type};
+    if (int r = check_dot_params(&dp, "gemv_fused")) return r;
+    VKML_CHECK_ARG(p->epilogue <= 2, "gemv_fused: epilogue must be 0 (store), 1 (+ residual) or 2 (SwiGLU)");
+    VKML_CHECK_ARG(!p->quantize_out || p->epilogue == 2, "gemv_fused: quantize_out needs the SwiGLU epilogue");
+    VKML_CHECK_ARG(!p->quantize_out || p->n % 32 == 0, "gemv_fused: quantize_out needs n a multiple of 32");
+    VKML_CHECK_ARG(!p->norm || p->k <= 4096, "gemv_fused: the RMSNorm prologue takes k up to 4096");
+    VKML_CHECK_ARG(!(p->norm && p->epilogue == 1), "gemv_fused: the RMSNorm prologue goes with the store or SwiGLU epilogue");
+    if (p->n == 0) return VKML_OK;
+    VKML_CHECK_ARG(a && b_values && b_scales && out, "gemv_fused: null buffer");
+    VKML_CHECK_ARG(p->norm ? norm_weight != nullptr : a_scales != nullptr, "gemv_fused: the input needs its norm weight or scales");
+    VKML_CHECK_ARG(p->epilogue != 1 || residual, "gemv_fused: the residual epilogue needs the residual");
+    VKML_CHECK_ARG(p->epilogue != 2 || (b2_values && b2_scales), "gemv_fused: SwiGLU needs the up matrix");
+    VKML_CHECK_ARG(!p->quantize_out || (out_values && out_scales), "gemv_fused: quantize_out needs its buffers");
+    GemvArgs g{p->norm ? nullptr : static_cast<const uint4*>(a), a_scales, b_values, b_scales, b2_values, b2_scales, out, residual,
+               p->n, p->k, p->norm ? static_cast<const float*>(a) : nullptr, norm_weight, p->eps,
+               static_cast<uint8_t*>(out_values), out_scales};
+    const char* label = "gemv_fused";
+    switch (p->epilogue) {
+        case 0: return p->norm ? dispatch_format<kStore, true>(p->b_type, p->scale_type, g, label)
+                               : dispatch_format<kStore>(p->b_type, p->scale_type, g, label);
+        case 1: return dispatch_format<kAdd>(p->b_type, p->scale_type, g, label);
+        default:
+            if (p->norm) {
+                return p->quantize_out ? dispatch_format<kSwiglu, true, true>(p->b_type, p->scale_type, g, label)
+                                       : dispatch_format<kSwiglu, true, false>(p->b_type, p->scale_type, g, label);
+            }
+            return p->quantize_out ? dispatch_format<kSwiglu, false, true>(p->b_type, p->scale_type, g, label)
+                                   : dispatch_format<kSwiglu>(p->b_type, p->scale_type, g, label);
+    }
 }
 
 int vkml_gemv(const vkml_gemv_params* p, const float* a, const void* b, float* out, const void* b_scales) {

@@ -59,6 +59,8 @@ AttendParams = _struct("AttendParams", [("kv_start", u32), ("kv_len", u32), ("ca
                                         ("scale", f32), ("softcap", f32)])
 RopeKvParams = _struct("RopeKvParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
                                         ("position", u32), ("style", u32), ("kv_type", u32), ("rotate", u32)])
+GemvFusedParams = _struct("GemvFusedParams", [("n", u32), ("k", u32), ("b_type", u32), ("scale_type", u32),
+                                              ("epilogue", u32), ("norm", u32), ("eps", f32), ("quantize_out", u32)])
 AttendStepParams = _struct("AttendStepParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
                                                 ("kv_start", u32), ("position", u32), ("kv_type", u32), ("chunks", u32),
                                                 ("rope_style", u32), ("rotate", u32), ("scale", f32), ("softcap", f32)])
@@ -114,6 +116,7 @@ SIGNATURES = {
     "vkml_attend": [P(AttendParams), vp, vp, vp, vp, vp, vp],
     "vkml_attend_merge": [P(AttendParams), vp, vp, vp, vp, vp],
     "vkml_rope_kv_append": [P(RopeKvParams), vp, vp, vp, vp, vp, vp],
+    "vkml_gemv_fused": [P(GemvFusedParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_state_set": [vp, i32, i32, i32],
     "vkml_embedding_state": [P(EmbeddingParams), vp, vp, vp, vp],

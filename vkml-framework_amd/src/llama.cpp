@@ -3,12 +3,13 @@
 // config.cpp:14-140).
 //
 // The reference records ~29 dispatches per layer, each separated by a full
-// barrier. Here one decode step (t = 1) is eight kernels per layer, all
-// reading the step's token and position from a small device-side state:
-//   rms_norm + Q8_0 quantize -> q|k|v GEMV (one fused matrix) -> attention
-//   chunks (rope of q and k, f16 cast and KV append inside) -> merge + Q8_0
-//   quantize -> o GEMV + residual -> rms_norm + quantize -> gate|up GEMV +
-//   SwiGLU -> quantize -> down GEMV + residual,
+// barrier. Here one decode step (t = 1) is six kernels per layer on the int8
+// path, all reading the step's token and position from a small device-side
+// state:
+//   q|k|v GEMV (one fused matrix; rms_norm + Q8_0 of x in its prologue) ->
+//   attention chunks (rope of q and k, f16 cast and KV append inside) ->
+//   merge + Q8_0 -> o GEMV + residual -> gate|up GEMV (rms_norm + Q8_0
+//   prologue, SwiGLU + Q8_0 epilogue) -> down GEMV + residual,
 // then the final norm, the lm_head GEMV and (greedy) an argmax that writes
 // the next token into the state. The step is captured once as a HIP graph
 // and replayed, so a prompt or a greedy generation is a stream of graph
@@ -360,10 +361,27 @@ struct Llama::Impl {
                 check(vkml_rms_norm(&np, xp, static_cast<const float*>(w.data()), static_cast<float*>(xn.data())), "rms_norm");
             }
         };
+        // A norm whose consumers all take the int8 path is folded into their
+        // GEMV (rms_norm + Q8_0 in the kernel's prologue, vkml_gemv_fused);
+        // not the lm_head's, whose thousands of workgroups would each redo it.
+        const bool fold = quant_d && d <= 4096;
+        const auto fused = [&](const Weight& w, const Tensor& nw, float* out, const char* t) {
+            tag(t);
+            const vkml_gemv_fused_params fp{u32(w.rows), u32(w.cols), w.type_code(), w.scale_code(), 0, 1, c.rms_norm_eps, 0};
+            check(vkml_gemv_fused(&fp, xp, nullptr, static_cast<const float*>(nw.data()), w.values(), w.scales(), nullptr, nullptr, nullptr,
+                                  out, nullptr, nullptr),
+                  t);
+        };
         for (const Layer& L : layers) {
-            norm(L.attn_norm, "attn_norm");
-            for (const auto& [w, row] : L.qkv)
-                project(w, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(qkv.data()) + row, nullptr, "qkv");
+            const bool fold_qkv =
+                fold && std::all_of(L.qkv.begin(), L.qkv.end(), [&](const auto& wr) { return quantized_input(wr.first); });
+            if (fold_qkv) {
+                for (const auto& [w, row] : L.qkv) fused(w, L.attn_norm, static_cast<float*>(qkv.data()) + row, "qkv");
+            } else {
+                norm(L.attn_norm, "attn_norm");
+                for (const auto& [w, row] : L.qkv)
+                    project(w, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(qkv.data()) + row, nullptr, "qkv");
+            }
             const bool o_q = quantized_input(L.o);
             const uint32_t kv_code = detail::type_code(L.k_cache.dtype());
             // rope, append and attention in one launch, then the merge
@@ -377,15 +395,22 @@ struct Llama::Impl {
                                    o_q ? static_cast<float*>(as.data()) : nullptr, st),
                   "attention");
             project(L.o, attn, o_q ? &aq : nullptr, &as, xp, xp, "o");
-            norm(L.ffn_norm, "ffn_norm");
             auto* hp = static_cast<float*>(h.data());
+            const bool down_q = quantized_input(L.down) && ff % 32 == 0;
+            bool h_quantized = false;
             if (quantized_input(L.gate) && quantized_input(L.up) && L.gate.type_code() == L.up.type_code() && quant_d) {
+                // gate|up GEMV + SwiGLU (+ the ffn norm before, + Q8_0 of h after)
+                if (!fold) norm(L.ffn_norm, "ffn_norm");
                 tag("gate_up");
-                const vkml_gemv_dot_params gp{1, u32(ff), u32(d), L.gate.type_code(), L.gate.scale_code()};
-                check(vkml_gemv_dot_swiglu(&gp, xq.data(), static_cast<const float*>(xs.data()), L.gate.values(), L.gate.scales(), L.up.values(),
-                                           L.up.scales(), hp),
+                const vkml_gemv_fused_params fp{u32(ff), u32(d), L.gate.type_code(), L.gate.scale_code(), 2, fold ? 1u : 0u,
+                                                c.rms_norm_eps, down_q ? 1u : 0u};
+                check(vkml_gemv_fused(&fp, fold ? static_cast<const void*>(xp) : xq.data(), fold ? nullptr : static_cast<const float*>(xs.data()),
+                                      static_cast<const float*>(L.ffn_norm.data()), L.gate.values(), L.gate.scales(), L.up.values(),
+                                      L.up.scales(), nullptr, hp, down_q ? hq.data() : nullptr, down_q ? static_cast<float*>(hs.data()) : nullptr),
                       "gate_up");
+                h_quantized = down_q;
             } else {
+                norm(L.ffn_norm, "ffn_norm");
                 project(L.gate, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(gate_tmp.data()), nullptr, "gate");
                 project(L.up, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(up_tmp.data()), nullptr, "up");
                 tag("swiglu");
@@ -393,8 +418,7 @@ struct Llama::Impl {
                 check(vkml_binary(2, u32(ff), u32(ff), static_cast<const float*>(gate_tmp.data()), static_cast<const float*>(up_tmp.data()), hp),
                       "mul");
             }
-            const bool down_q = quantized_input(L.down) && ff % 32 == 0;
-            if (down_q) {
+            if (down_q && !h_quantized) {
                 tag("down_quantize");
                 const vkml_quantize_params qp{u32(ff / 32), VKML_F32, VKML_Q8_0, VKML_F32};
                 check(vkml_quantize(&qp, hp, hq.data(), hs.data()), "quantize");

@@ -13,12 +13,14 @@ bytes of every weight plus the KV rows read) against 8 TB/s, a roofline
 entry for the dominant kernel, and the CPU oracle's decode rate on the host
 cores as a reported baseline.
 
-The dominant kernel is the SwiGLU gate/up GEMV (66 MB of q4_K weights a
-layer, the largest share of a step's bytes and of its time). Its average
-launch duration is measured here with two HIP events on the library's
-stream around back-to-back launches at the step's exact shape over 32
-distinct weight pairs (2.1 GB, more than any cache holds), the way the step
-streams one layer's matrices after another. A per-kernel table of extra
+The dominant kernel is the fused gate/up GEMV (66 MB of q4_K weights a
+layer, the largest share of a step's bytes and of its time): the ffn RMSNorm
+and the activation's Q8_0 in its prologue, gate and up dot products, SwiGLU,
+and h's Q8_0 in its epilogue, as the step launches it. Its average launch
+duration is measured here with two HIP events on the library's stream
+around back-to-back launches at the step's exact shape over 32 distinct
+weight pairs (2.1 GB, more than any cache holds), the way the step streams
+one layer's matrices after another. A per-kernel table of extra
 eager steps (HIP events around each launch, so with launch gaps) goes to
 stderr.
 """
@@ -35,6 +37,13 @@ import numpy as np  # noqa: E402
 
 PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
 PROMPT = 4096
+
+# HBM bytes one gate/up launch moves (reads + writes): FETCH_SIZE and
+# WRITE_SIZE passes of rocprofv3 over `bench.py --roofline-only`, each scaled
+# by the same counter's reading for a 256 MiB device copy; the readings and
+# commands are in profiles/gate_up_cfg5_hbm_traffic.md. Valid for the kernel
+# they were taken on; measured again after a change to it.
+GATE_UP_TRAFFIC = 66_694_776
 
 # GGUF-native bytes per weight (q4_K 144 B / 256, q6_K 210 B / 256).
 Q4K, Q6K = 144 / 256, 210 / 256
@@ -96,8 +105,9 @@ class _Events:
 
 
 def time_gate_up(spec, layers=32, rounds=3):
-    """Average duration of vkml_gemv_dot_swiglu at the step's shape (q4_K
-    gate and up [ffn, hidden], a Q8_0 activation), over `layers` distinct
+    """Average duration of vkml_gemv_fused at the step's gate/up call (q4_K
+    gate and up [ffn, hidden]; f32 residual stream in, RMSNorm + Q8_0 in the
+    prologue; SwiGLU and Q8_0 of h in the epilogue), over `layers` distinct
     weight pairs launched back to back, `rounds` times, between two events.
     Weight values do not change the kernel's work; the buffers are filled
     with fixed patterns (f16 scales finite)."""
@@ -111,13 +121,14 @@ def time_gate_up(spec, layers=32, rounds=3):
         return b
 
     mats = [(buf(codes, 0x5A3C96E1), buf(hdr, 0x2C1F2C00), buf(codes, 0x3C5A1E96), buf(hdr, 0x2C0F2C00)) for _ in range(layers)]
-    av, asc, out = buf(k, 0x03FD7F81), buf(k // 32 * 4, 0x3C000000), buf(n * 4, 0)
-    prm = H.GemvDotParams(1, n, k, H.Q4_K, H.F16)
+    x, nw = buf(k * 4, 0x3F000000), buf(k * 4, 0x3F800000)
+    out, hq, hs = buf(n * 4, 0), buf(n, 0), buf(n // 32 * 4, 0)
+    prm = H.GemvFusedParams(n, k, H.Q4_K, H.F16, 2, 1, 1e-5, 1)
 
     def launches():
         for _ in range(rounds):
             for g, gs, u, us in mats:
-                H.call("vkml_gemv_dot_swiglu", prm, av.p, asc.p, g.p, gs.p, u.p, us.p, out.p)
+                H.call("vkml_gemv_fused", prm, x.p, None, nw.p, g.p, gs.p, u.p, us.p, None, out.p, hq.p, hs.p)
 
     ev = _Events()
     try:
@@ -129,11 +140,32 @@ def time_gate_up(spec, layers=32, rounds=3):
         for m in mats:
             for b in m:
                 b.close()
-        for b in (av, asc, out):
+        for b in (x, nw, out, hq, hs):
             b.close()
     weight_bytes = 2 * (codes + hdr)
-    io_bytes = k + k // 32 * 4 + n * 4  # activation codes and scales in, h out
+    io_bytes = 2 * k * 4 + n * 4 + n + n // 32 * 4  # x and the norm weight in; h, its codes and scales out
     return ms * 1e3 / (layers * rounds), weight_bytes + io_bytes
+
+
+def roofline_only(spec):
+    """The dominant kernel's measurement alone, then a device copy of 256 MiB
+    (hipMemcpy device to device, the runtime's copy kernel) launched three
+    times: per dispatch it reads and writes exactly 268,435,456 bytes, the
+    known size against which a counter's reading is scaled."""
+    from vkml_amd import hip as H
+    H.init()
+    dom_us, dom_bytes = time_gate_up(spec, layers=32, rounds=1)
+    log(f"gemv_fused gate/up: {dom_us:.2f} us a launch, {dom_bytes / (dom_us * 1e-6) / 1e9:.0f} GB/s "
+        f"({dom_bytes} algorithmic bytes)")
+    n = 256 << 20
+    src, dst = H.Buffer(n), H.Buffer(n)
+    H.call("vkml_fill_u32", src.p, 0x01020304, n // 4)
+    for _ in range(3):
+        H.call("vkml_memcpy_d2d", dst.p, src.p, n)
+    H.synchronize()
+    src.close()
+    dst.close()
+    log(f"copy: 3 x {n} bytes")
 
 
 def main():
@@ -148,6 +180,10 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch every kernel from the host instead of replaying the captured step (for profilers "
                          "that cannot follow graph launches; the kernels are the same)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the dominant kernel's timed launches and a 256 MiB device copy of known size, "
+                         "for hardware-counter passes (FETCH_SIZE, WRITE_SIZE) that scale the kernel's HBM bytes "
+                         "by what the copy reads")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (every GPU box here has one). "
@@ -159,6 +195,9 @@ def main():
     from vkml_amd import llama as L
 
     spec = synth.CONFIGS["cfg5"]
+    if args.roofline_only:
+        roofline_only(spec)
+        return
     if args.layers:
         spec = synth.ModelSpec(spec.name, args.layers, spec.hidden, spec.heads, spec.kv_heads, spec.head_dim, spec.ffn,
                                spec.vocab, spec.theta, max_positions=spec.max_positions)
@@ -204,9 +243,9 @@ def main():
         n_layers = spec.n_layers
         kv_mean = args.prompt + (args.profile_steps + 1) / 2
         launch_bytes = {
-            "gemv_dot:qkv": per_layer["qkv"], "gemv_dot_add:o": per_layer["o"], "gemv_dot_swiglu:gate_up": per_layer["gate_up"],
+            "gemv_fused:qkv": per_layer["qkv"], "gemv_dot_add:o": per_layer["o"], "gemv_fused:gate_up": per_layer["gate_up"],
             "gemv_dot_add:down": per_layer["down"], "gemv_dot:lm_head": spec.vocab * spec.hidden * Q6K,
-            "attend:attention": kv_pos / n_layers * kv_mean,
+            "attend_step:attention": kv_pos / n_layers * kv_mean,
         }
         rows = []
         for name, calls, ms in prof:
@@ -220,7 +259,7 @@ def main():
         busy_ms = sum(ms for _, _, ms in prof) / args.profile_steps
         dom_us, dom_bytes = time_gate_up(spec)
         achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-        log(f"gemv_dot_swiglu (gate/up) back to back: {dom_us:.2f} us a launch, {achieved:.0f} GB/s")
+        log(f"gemv_fused (norm + gate/up + swiglu + q8_0) back to back: {dom_us:.2f} us a launch, {achieved:.0f} GB/s")
 
         cpu = None
         if args.cpu_tokens > 0:
@@ -263,9 +302,10 @@ def main():
             "hbm_frac": round(hbm / PEAK_HBM, 4),
             "bytes_per_step": round(step_bytes),
             "gpu_busy_ms_per_step": round(busy_ms, 4),
-            "roofline": {"bound": "hbm", "kernel": "gemv_dot_swiglu (k_gemv_dot<q4_K, f16, 8 lanes, swiglu>)",
+            "roofline": {"bound": "hbm", "kernel": "gemv_fused gate/up (k_gemv_dot<q4_K, f16, 8 lanes, swiglu, norm, q8_0 out>)",
                          "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s",
-                         "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                         "frac": round(achieved / PEAK_HBM, 4), "traffic": GATE_UP_TRAFFIC,
+                         "traffic_over_algorithmic": round(GATE_UP_TRAFFIC / dom_bytes, 4),
                          "bytes_per_launch": round(dom_bytes), "avg_launch_us": round(dom_us, 3)},
             "cpu_baseline": cpu,
             "tokens_head": [int(t) for t in tokens[:8]],

@@ -135,6 +135,58 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
     return wave_max(s);
 }
 
+// ---------------------------------------------------------------- coherent access
+
+// Loads and stores of the values one workgroup of a launch produces for
+// another (the persistent decode kernel's activations). Each XCD has its own
+// L2, which may hold a stale line of a buffer another XCD has since written;
+// agent-scope relaxed atomics (sc1 accesses) are coherent across XCDs. With
+// COH false these are plain accesses.
+template <bool COH>
+__device__ __forceinline__ uint32_t ld_u32(const uint32_t* p) {
+    if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+}
+template <bool COH>
+__device__ __forceinline__ uint64_t ld_u64(const uint64_t* p) {
+    if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+}
+template <bool COH>
+__device__ __forceinline__ float ld_f32(const float* p) {
+    return __uint_as_float(ld_u32<COH>(reinterpret_cast<const uint32_t*>(p)));
+}
+template <bool COH>
+__device__ __forceinline__ uint4 ld_u128(const uint4* p) {
+    if constexpr (COH) {
+        const uint64_t a = ld_u64<true>(reinterpret_cast<const uint64_t*>(p));
+        const uint64_t b = ld_u64<true>(reinterpret_cast<const uint64_t*>(p) + 1);
+        return make_uint4(static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b),
+                          static_cast<uint32_t>(b >> 32));
+    } else {
+        return *p;
+    }
+}
+template <bool COH>
+__device__ __forceinline__ float4 ld_f32x4(const float4* p) {
+    const uint4 u = ld_u128<COH>(reinterpret_cast<const uint4*>(p));
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+}
+template <bool COH>
+__device__ __forceinline__ void st_u32(uint32_t* p, uint32_t v) {
+    if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+template <bool COH>
+__device__ __forceinline__ void st_f32(float* p, float v) {
+    st_u32<COH>(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+template <bool COH>
+__device__ __forceinline__ void st_u8(uint8_t* p, uint8_t v) {
+    if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+
 // ---------------------------------------------------------------- int8 dot
 
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {

@@ -1,0 +1,519 @@
+// gemv.hpp -- the int8 GEMV's device code (the reference's
+// shaders/gemv_dot.comp), shared by the GEMV kernels (k_gemv.hip) and the
+// persistent decode kernel (k_decode.hip).
+//
+// Bit-exact by construction. The reference sums each output over 32
+// accumulators: accumulator L takes the terms of half-blocks (16 values) L,
+// L + 32, L + 64, ... in that order, each term an exact int8 dot product
+// scaled in f32 (gemv_dot.comp:85-118), and the 32 are added in a halving
+// tree (:121-131). Every f32 operation here happens in that order, so the
+// outputs are the reference's bits, and so are the Q8_0 codes the next layer
+// quantizes from them.
+//
+// Mapping. A row's 32 accumulators live in LPR lanes (16 or 8), 32 / LPR
+// each. A "round" is the 32 half-blocks (512 values) that give every
+// accumulator its next term. Which accumulators a lane holds is chosen per
+// weight format so that a lane's share of a round is one or two contiguous
+// 16-byte loads and the LPR lanes of a row read one contiguous span:
+// - q4_K (16 lanes): lane 8p + 2c + h loads code bytes 16 lane of the
+//   round's two super-blocks; low nibbles are half-block 16p + 4c + h, high
+//   nibbles 16p + 4c + h + 2. (8 lanes: lane j loads bytes 32j .. 32j + 31,
+//   half-blocks 4j .. 4j + 3.)
+// - q4_0 / q4_1 (16 lanes): lane l loads block l of the round, half-blocks
+//   2l, 2l + 1. (8 lanes: blocks 2j, 2j + 1, half-blocks 4j .. 4j + 3.)
+// - q8_0 (16 lanes): lane l loads half-blocks l and l + 16. (8 lanes: j,
+//   j + 8, j + 16, j + 24.)
+// The halving tree's strides 16 .. 1 then become, per mapping, additions
+// within a lane or exchanges between lanes (xor shuffles).
+//
+// Each lane keeps two batches of rounds in flight (the next batch loads while
+// the current one is summed); the first batch is issued before the workgroup
+// stages the activation codes, their per-half-block sums and block scales in
+// LDS (GemvRows::start, stage_activation, GemvRows::finish). No MFMA: these
+// are matrix-vector products, bound by HBM.
+#pragma once
+
+#include "../../include/vkml_hip.h"
+#include "device.hpp"
+
+namespace vkml::gemv {
+
+using namespace vkml::dev;
+
+constexpr uint32_t kMaxK = 32768;  // LDS staging: K + K / 16 * 4 + K / 32 * 4 bytes
+constexpr uint32_t kLow = 0x0F0F0F0Fu;
+
+struct GemvArgs {
+    const uint4* a_values;  // K bytes of activation codes
+    const float* a_scales;  // K / 32
+    const void* b_values;
+    const void* b_scales;
+    const void* b2_values;  // SwiGLU: the up matrix
+    const void* b2_scales;
+    float* out;
+    const float* residual;
+    uint32_t n, k;
+    // With the RMSNorm prologue: the f32 input row, its norm weight and eps
+    // (the activation codes are then computed, not read).
+    const float* x;
+    const float* norm_weight;
+    float eps;
+    // SwiGLU with the Q8_0 epilogue: the codes and f32 scales of h.
+    uint8_t* out_values;
+    float* out_scales;
+};
+
+// The accumulator (= half-block of the round) held in slot e of lane l.
+template <int FMT, int LPR>
+__device__ __forceinline__ constexpr uint32_t acc_index(uint32_t l, uint32_t e) {
+    if constexpr (FMT == VKML_Q8_0) return LPR == 16 ? l + 16 * e : l + 8 * e;
+    else if constexpr (FMT == VKML_Q4_K && LPR == 16) return 16 * (l / 8) + 4 * ((l / 2) % 4) + (l % 2) + 2 * e;
+    else return (32 / LPR) * l + e;  // q4_0 / q4_1, and q4_K with 8 lanes
+}
+
+template <int FMT, int LPR>
+struct Plan {
+    static constexpr int NS = 32 / LPR;                        // accumulators (slots) per lane
+    static constexpr int NQ = FMT == VKML_Q8_0 ? NS : NS / 2;  // 16-byte code loads per lane and round
+};
+
+// One lane's weights for one round of one matrix: codes, and scales (q4_K:
+// the super-block header; q8_0 / q4_0: one scale per slot or block; q4_1:
+// scale and offset per block), as raw bits.
+template <int FMT, int LPR>
+struct RoundW {
+    uint4 q[Plan<FMT, LPR>::NQ];
+    uint32_t s[FMT == VKML_Q4_K ? 4 : Plan<FMT, LPR>::NS];
+};
+
+__device__ __forceinline__ uint32_t ld16(const void* p, uint64_t i) { return static_cast<const uint16_t*>(p)[i]; }
+__device__ __forceinline__ uint32_t ld32(const void* p, uint64_t i) { return static_cast<const uint32_t*>(p)[i]; }
+__device__ __forceinline__ uint4 ld128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Loads lane l's share of round r of row `row`. Every load is issued
+// unconditionally (positions past the row's end, in a last round shorter
+// than 512 values, are clamped to its last block and their terms skipped),
+// so the compiler can count outstanding loads and wait for one batch while
+// the next is still in flight.
+template <int FMT, bool F16S, int LPR>
+__device__ __forceinline__ void load_round(const void* bv, const void* bs, uint32_t K, uint32_t row, uint32_t r, uint32_t l,
+                                           RoundW<FMT, LPR>& w) {
+    constexpr int NS = Plan<FMT, LPR>::NS;
+    const uint64_t R = row;
+    const uint8_t* codes = static_cast<const uint8_t*>(bv);
+    if constexpr (FMT == VKML_Q8_0) {
+        const uint8_t* base = codes + R * K;
+        const uint64_t blocks = R * (K / 32);
+#pragma unroll
+        for (int e = 0; e < NS; ++e) {
+            const uint32_t hb = min(32 * r + acc_index<FMT, LPR>(l, e), K / 16 - 1);
+            w.q[e] = ld128(base + 16ull * hb);
+            w.s[e] = F16S ? ld16(bs, blocks + hb / 2) : ld32(bs, blocks + hb / 2);
+        }
+    } else if constexpr (FMT == VKML_Q4_K) {
+        const uint32_t p = LPR == 16 ? l / 8 : l / 4;  // which super-block of the round
+        const uint32_t sb = min(2 * r + p, K / 256 - 1);
+        const uint8_t* base = codes + R * (K / 2) + 128ull * sb;
+        if constexpr (LPR == 16) {
+            w.q[0] = ld128(base + 16 * (l % 8));
+        } else {
+            w.q[0] = ld128(base + 32 * (l % 4));
+            w.q[1] = ld128(base + 32 * (l % 4) + 16);
+        }
+        const uint4 h = static_cast<const uint4*>(bs)[R * (K / 256) + sb];
+        w.s[0] = h.x; w.s[1] = h.y; w.s[2] = h.z; w.s[3] = h.w;
+    } else {
+        const uint8_t* base = codes + R * (K / 2);
+#pragma unroll
+        for (int b = 0; b < NS / 2; ++b) {
+            const uint32_t blk = min(16 * r + (LPR == 16 ? l : 2 * l) + b, K / 32 - 1);  // block of the row
+            const uint64_t block = R * (K / 32) + blk;
+            w.q[b] = ld128(base + 16ull * blk);
+            if constexpr (FMT == VKML_Q4_1) {
+                if constexpr (F16S) {
+                    w.s[2 * b] = ld32(bs, block);  // f16 scale | f16 offset << 16
+                } else {
+                    const uint2 so = static_cast<const uint2*>(bs)[block];
+                    w.s[2 * b] = so.x;
+                    w.s[2 * b + 1] = so.y;
+                }
+            } else {
+                w.s[b] = F16S ? ld16(bs, block) : ld32(bs, block);
+            }
+        }
+    }
+}
+
+// The exact dot product of one half-block: 16 weight codes as bytes (four
+// words) with 16 activation codes (gemv_dot.comp:105-106).
+__device__ __forceinline__ int half_dot(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint4 a) {
+    return dot4(w3, a.w, dot4(w2, a.z, dot4(w1, a.y, dot4(w0, a.x, 0))));
+}
+
+__device__ __forceinline__ float scale_of(uint32_t bits, bool f16) {
+    return f16 ? f16_bits_to_float(bits & 0xFFFFu) : __uint_as_float(bits);
+}
+
+// Scale and offset of sub-blocks 2c (low nibbles) and 2c + 1 (high) of a
+// q4_K super-block with header h: f16(d * sc) and f16(-(dmin * m)), the
+// reference's rounding of its q4_1 repack (src/io/gguf.cpp:123-131,603-617),
+// computed as f16 products (exact operands, one rounding to nearest even).
+__device__ __forceinline__ void q4k_sub_scales(const uint32_t (&h)[4], uint32_t c, float& s0, float& o0, float& s1, float& o1) {
+    const uint32_t shift = (c & 1u) * 16u;
+    const uint32_t Y = (h[1] >> shift) & 0xFFFFu, Z = (h[2] >> shift) & 0xFFFFu, W = (h[3] >> shift) & 0xFFFFu;
+    uint32_t sc, mn;
+    if (c < 2) {
+        sc = Y & 0x3F3Fu;
+        mn = Z & 0x3F3Fu;
+    } else {
+        sc = (W & 0x0F0Fu) | ((Y & 0xC0C0u) >> 2);
+        mn = ((W >> 4) & 0x0F0Fu) | ((Z & 0xC0C0u) >> 2);
+    }
+    const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h[0] & 0xFFFFu));
+    const _Float16 nd = -__builtin_bit_cast(_Float16, static_cast<uint16_t>(h[0] >> 16));
+    s0 = static_cast<float>(d * static_cast<_Float16>(sc & 0xFFu));
+    s1 = static_cast<float>(d * static_cast<_Float16>(sc >> 8));
+    o0 = static_cast<float>(nd * static_cast<_Float16>(mn & 0xFFu));
+    o1 = static_cast<float>(nd * static_cast<_Float16>(mn >> 8));
+}
+
+// Adds one lane's terms of round r to acc[0 .. NS) with the reference's
+// expressions (gemv_dot.comp:112,114): q8_0 / q4_0 float(d) * (scale * sa);
+// q4_1 and q4_K sa * (float(d) * scale + float(sum) * offset). The
+// activation codes, half-block sums and block scales come from LDS.
+template <int FMT, bool F16S, int LPR>
+__device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t r, uint32_t l, uint32_t K,
+                                            const uint4* s_codes, const float* s_sum, const float* s_sa,
+                                            float (&acc)[Plan<FMT, LPR>::NS]) {
+#pragma clang fp contract(off)
+    constexpr int NS = Plan<FMT, LPR>::NS;
+    const uint32_t halves = K / 16;
+    float s[NS], o[NS];
+    int d[NS];
+    uint4 a[NS];
+    bool live[NS];
+#pragma unroll
+    for (int e = 0; e < NS; ++e) {
+        const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
+        live[e] = hb < halves;
+        a[e] = live[e] ? s_codes[hb] : make_uint4(0, 0, 0, 0);
+    }
+    if constexpr (FMT == VKML_Q8_0) {
+#pragma unroll
+        for (int e = 0; e < NS; ++e) {
+            d[e] = half_dot(w.q[e].x, w.q[e].y, w.q[e].z, w.q[e].w, a[e]);
+            s[e] = scale_of(w.s[e], F16S);
+        }
+    } else if constexpr (FMT == VKML_Q4_K) {
+        const uint32_t c = LPR == 16 ? (l / 2) % 4 : l % 4;
+        float s0, o0, s1, o1;
+        q4k_sub_scales(w.s, c, s0, o0, s1, o1);
+        if constexpr (LPR == 16) {
+            const uint4 q = w.q[0];
+            d[0] = half_dot(q.x & kLow, q.y & kLow, q.z & kLow, q.w & kLow, a[0]);
+            d[1] = half_dot((q.x >> 4) & kLow, (q.y >> 4) & kLow, (q.z >> 4) & kLow, (q.w >> 4) & kLow, a[1]);
+            s[0] = s0; o[0] = o0; s[1] = s1; o[1] = o1;
+        } else {
+            const uint4 q0 = w.q[0], q1 = w.q[1];
+            d[0] = half_dot(q0.x & kLow, q0.y & kLow, q0.z & kLow, q0.w & kLow, a[0]);
+            d[1] = half_dot(q1.x & kLow, q1.y & kLow, q1.z & kLow, q1.w & kLow, a[1]);
+            d[2] = half_dot((q0.x >> 4) & kLow, (q0.y >> 4) & kLow, (q0.z >> 4) & kLow, (q0.w >> 4) & kLow, a[2]);
+            d[3] = half_dot((q1.x >> 4) & kLow, (q1.y >> 4) & kLow, (q1.z >> 4) & kLow, (q1.w >> 4) & kLow, a[3]);
+            s[0] = s0; o[0] = o0; s[1] = s0; o[1] = o0; s[2] = s1; o[2] = o1; s[3] = s1; o[3] = o1;
+        }
+    } else {
+        // QuantizedMatrix q4 words: byte j holds value j (low) and j + 4 (high).
+#pragma unroll
+        for (int b = 0; b < NS / 2; ++b) {
+            const uint4 q = w.q[b];
+            d[2 * b] = half_dot(q.x & kLow, (q.x >> 4) & kLow, q.y & kLow, (q.y >> 4) & kLow, a[2 * b]);
+            d[2 * b + 1] = half_dot(q.z & kLow, (q.z >> 4) & kLow, q.w & kLow, (q.w >> 4) & kLow, a[2 * b + 1]);
+            if constexpr (FMT == VKML_Q4_1) {
+                const float sc = F16S ? f16_bits_to_float(w.s[2 * b] & 0xFFFFu) : __uint_as_float(w.s[2 * b]);
+                const float of = F16S ? f16_bits_to_float(w.s[2 * b] >> 16) : __uint_as_float(w.s[2 * b + 1]);
+                s[2 * b] = s[2 * b + 1] = sc;
+                o[2 * b] = o[2 * b + 1] = of;
+            } else {
+                s[2 * b] = s[2 * b + 1] = scale_of(w.s[b], F16S);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < NS; ++e) {
+        if (!live[e]) continue;
+        const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
+        const float sa = s_sa[hb / 2];
+        if constexpr (FMT == VKML_Q4_1 || FMT == VKML_Q4_K) {
+            acc[e] += sa * (static_cast<float>(d[e]) * s[e] + s_sum[hb] * o[e]);
+        } else {
+            // q4_0 codes are q + 8: the reference's signed bytes (q4_bytes)
+            // give the same exact sum, d - 8 * sum(a).
+            if constexpr (FMT == VKML_Q4_0) d[e] -= 8 * static_cast<int>(s_sum[hb]);
+            acc[e] += static_cast<float>(d[e]) * (s[e] * sa);
+        }
+    }
+}
+
+// The halving tree over the 32 accumulators of a row, strides 16, 8, 4, 2,
+// 1 (gemv_dot.comp:121-131), each an exchange between the row's lanes or an
+// addition within a lane as the mapping places accumulator L + stride.
+template <int FMT, int LPR>
+__device__ __forceinline__ float row_tree(float (&acc)[32 / LPR]) {
+#pragma clang fp contract(off)
+    const auto x = [&](int mask, int slots) {
+#pragma unroll
+        for (int e = 0; e < 32 / LPR; ++e)
+            if (e < slots) acc[e] += __shfl_xor(acc[e], mask, kWave);
+    };
+    if constexpr (FMT == VKML_Q8_0 && LPR == 16) {  // L = l + 16e
+        acc[0] += acc[1];
+        x(8, 1); x(4, 1); x(2, 1); x(1, 1);
+    } else if constexpr (FMT == VKML_Q8_0) {  // L = j + 8e
+        acc[0] += acc[2]; acc[1] += acc[3];
+        acc[0] += acc[1];
+        x(4, 1); x(2, 1); x(1, 1);
+    } else if constexpr (FMT == VKML_Q4_K && LPR == 16) {  // L = 16p + 4c + h + 2e, l = 8p + 2c + h
+        x(8, 2); x(4, 2); x(2, 2);
+        acc[0] += acc[1];
+        x(1, 1);
+    } else if constexpr (LPR == 16) {  // q4_0 / q4_1: L = 2l + e
+        x(8, 2); x(4, 2); x(2, 2); x(1, 2);
+        acc[0] += acc[1];
+    } else {  // L = 4j + e: q4_0 / q4_1 / q4_K with 8 lanes
+        x(4, 4); x(2, 4); x(1, 4);
+        acc[0] += acc[2]; acc[1] += acc[3];
+        acc[0] += acc[1];
+    }
+    return acc[0];
+}
+
+enum { kStore = 0, kAdd = 1, kSwiglu = 2 };
+
+// The prologue that replaces a separate rms_norm + quantize launch: RMSNorm
+// of x in rms_norm.comp's order at its workgroup width of 256 (invocation v
+// sums x[c]^2 over c = v, v + 256, ...; then the halving tree), emulated by
+// T threads; then y = x * scale * w and Q8_0 per 32 values
+// (quantize.comp:100-111), written to LDS as the activation codes,
+// half-block code sums and block scales: vkml_rms_norm_quantize's results
+// bit for bit. K <= 4096 and T >= 128, so a thread owns at most one 32-value
+// block; its block of x and w and its strided elements for the sum are all
+// loaded at once, into registers: one round trip.
+template <uint32_t T>
+struct NormLoads {
+    static constexpr uint32_t V = T >= 256 ? 1 : 256 / T;  // invocations per thread (t, t + T, ... below 256)
+    static constexpr uint32_t kMaxPer = 4096 / 256;        // elements per invocation at K <= 4096
+    float4 xb[8], wb[8];                                   // the thread's 32-value block of x and w
+    float xv[V][kMaxPer];                                  // its invocations' strided elements
+};
+
+template <uint32_t T, bool COH>
+__device__ __forceinline__ void norm_loads(const float* x, const float* w, uint32_t K, NormLoads<T>& r) {
+    const uint32_t t = threadIdx.x, blk = t < K / 32 ? t : 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        r.xb[i] = ld_f32x4<COH>(reinterpret_cast<const float4*>(x) + 8 * blk + i);
+        r.wb[i] = reinterpret_cast<const float4*>(w)[8 * blk + i];
+    }
+#pragma unroll
+    for (uint32_t v = 0; v < NormLoads<T>::V; ++v)
+#pragma unroll
+        for (uint32_t j = 0; j < NormLoads<T>::kMaxPer; ++j) r.xv[v][j] = ld_f32<COH>(x + min((t + v * T) % 256 + 256 * j, K - 1));
+}
+
+template <uint32_t T>
+__device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float* s_sum, float* s_sa,
+                                       float* s_red) {
+#pragma clang fp contract(off)
+    static_assert(T >= 128, "workgroup width");
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (uint32_t v = 0; v < NormLoads<T>::V; ++v) {
+        const uint32_t inv = t + v * T;
+        float part = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < NormLoads<T>::kMaxPer; ++j)
+            if (inv + 256 * j < K) part += r.xv[v][j] * r.xv[v][j];
+        if (inv < 256) s_red[inv] = part;
+    }
+    // The halving tree over the 256 invocations: strides 128, 64, then 32 .. 1 in wave 0.
+    __syncthreads();
+    if (t < 128) s_red[t] = s_red[t] + s_red[t + 128];
+    __syncthreads();
+    if (t < 64) {
+        float v = s_red[t] + s_red[t + 64];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+        if (t == 0) s_red[256] = v;
+    }
+    __syncthreads();
+    if (t >= K / 32) return;
+    const uint32_t blk = t;
+    const float scale = 1.0f / sqrtf(s_red[256] / static_cast<float>(K) + eps);
+    float y[32];
+    float absmax = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        const float xs[4] = {r.xb[i].x, r.xb[i].y, r.xb[i].z, r.xb[i].w}, ws[4] = {r.wb[i].x, r.wb[i].y, r.wb[i].z, r.wb[i].w};
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) {
+            y[4 * i + e] = xs[e] * scale * ws[e];
+            absmax = fmaxf(absmax, fabsf(y[4 * i + e]));
+        }
+    }
+    const float d = absmax / 127.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    uint32_t words[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) {
+        words[q] = (static_cast<uint32_t>(quant_code(y[4 * q], inv)) & 0xFFu) |
+                   ((static_cast<uint32_t>(quant_code(y[4 * q + 1], inv)) & 0xFFu) << 8) |
+                   ((static_cast<uint32_t>(quant_code(y[4 * q + 2], inv)) & 0xFFu) << 16) |
+                   (static_cast<uint32_t>(quant_code(y[4 * q + 3], inv)) << 24);
+    }
+    const uint4 lo = make_uint4(words[0], words[1], words[2], words[3]);
+    const uint4 hi = make_uint4(words[4], words[5], words[6], words[7]);
+    s_codes[2 * blk] = lo;
+    s_codes[2 * blk + 1] = hi;
+    s_sum[2 * blk] = static_cast<float>(byte_sum(lo));
+    s_sum[2 * blk + 1] = static_cast<float>(byte_sum(hi));
+    s_sa[blk] = d;
+}
+
+
+// The rows of one item (T / LPR consecutive rows) of a GEMV: start() issues
+// the item's first batch of weight loads, which depend on nothing computed
+// at run time, so a caller can issue them early (before the activation is
+// staged, or before a grid barrier); finish() sums the rounds over the staged
+// activation and applies the epilogue. With COH, the outputs, the residual
+// and the Q8_0 output are accessed coherently across XCDs.
+template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool QOUT, bool COH>
+struct GemvRows {
+    static constexpr int NS = Plan<FMT, LPR>::NS;
+    static constexpr int NM = EPI == kSwiglu ? 2 : 1;
+    static constexpr uint32_t kRows = T / LPR;
+    RoundW<FMT, LPR> wa[B][NM], wb[B][NM];
+    uint32_t item, row, r_row, l, rounds;
+
+    __device__ __forceinline__ void load_batch(const GemvArgs& g, RoundW<FMT, LPR> (&w)[B][NM], uint32_t r0) {
+        // Rounds past the last reload the last one (cache hits): unconditional loads.
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const uint32_t r = min(r0 + i, rounds - 1);
+            load_round<FMT, F16S, LPR>(g.b_values, g.b_scales, g.k, r_row, r, l, w[i][0]);
+            if constexpr (NM == 2) load_round<FMT, F16S, LPR>(g.b2_values, g.b2_scales, g.k, r_row, r, l, w[i][NM - 1]);
+        }
+    }
+
+    __device__ __forceinline__ void start(const GemvArgs& g, uint32_t it) {
+        item = it;
+        rounds = (g.k + 511) / 512;
+        l = threadIdx.x % LPR;
+        row = it * kRows + threadIdx.x / LPR;
+        r_row = min(row, g.n - 1);
+        load_batch(g, wa, 0);
+    }
+
+    __device__ __forceinline__ void finish(const GemvArgs& g, const uint4* s_codes, const float* s_sum, const float* s_sa) {
+#pragma clang fp contract(off)
+        const uint32_t K = g.k;
+        float acc[NM][NS];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int e = 0; e < NS; ++e) acc[m][e] = 0.0f;
+        const auto sum_batch = [&](const RoundW<FMT, LPR> (&w)[B][NM], uint32_t r0) {
+#pragma unroll
+            for (int i = 0; i < B; ++i) {
+                if (r0 + i < rounds) {
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) round_terms<FMT, F16S, LPR>(w[i][m], r0 + i, l, K, s_codes, s_sum, s_sa, acc[m]);
+                }
+            }
+        };
+        for (uint32_t r0 = 0; r0 < rounds; r0 += 2 * B) {
+            load_batch(g, wb, r0 + B);
+            sum_batch(wa, r0);
+            load_batch(g, wa, r0 + 2 * B);
+            sum_batch(wb, r0 + B);
+        }
+
+        float y[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) y[m] = row_tree<FMT, LPR>(acc[m]);
+        float result = 0.0f;
+        if (l == 0 && row < g.n) {
+            if constexpr (EPI == kStore) {
+                result = y[0];
+            } else if constexpr (EPI == kAdd) {
+                result = ld_f32<COH>(g.residual + row) + y[0];  // add(x, attn_out), llama.cpp:374,386
+            } else {
+                // silu(gate) * up (unary.comp:21-24, then binary.comp's mul)
+                const float gate = y[0], up = y[NM - 1];
+                result = gate / (1.0f + vk_expf(-gate)) * up;
+            }
+            st_f32<COH>(g.out + row, result);
+        }
+        if constexpr (QOUT) {
+            // The item's T / LPR = 32 rows are one Q8_0 block of the output
+            // (quantize.comp:100-111): its absmax, scale and codes.
+            static_assert(T / LPR == 32, "one Q8_0 block per item");
+            __shared__ float s_out[32];
+            if (l == 0) s_out[threadIdx.x / LPR] = result;
+            __syncthreads();
+            if (threadIdx.x < 32) {
+                const float v = s_out[threadIdx.x];
+                const float absmax = group_max<32>(fabsf(v));
+                const float d = absmax / 127.0f;
+                const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+                st_u8<COH>(g.out_values + item * 32 + threadIdx.x, static_cast<uint8_t>(static_cast<int8_t>(quant_code(v, inv))));
+                if (threadIdx.x == 0) st_f32<COH>(g.out_scales + item, d);
+            }
+            __syncthreads();  // s_out is free for the next item
+        }
+    }
+};
+
+// LDS bytes stage_activation uses for K.
+__host__ __device__ constexpr uint32_t stage_bytes(uint32_t k, bool norm) { return k + k / 16 * 4 + k / 32 * 4 + (norm ? 257 * 4 : 0); }
+
+// Stages the activation in LDS (smem, 16-byte aligned): with NORM, RMSNorm +
+// Q8_0 of g.x computed here (norm_quantize_prologue); otherwise the codes
+// and scales read from g.a_values / g.a_scales. Ends with a barrier.
+template <uint32_t T, bool NORM, bool COH>
+__device__ __forceinline__ void stage_activation(const GemvArgs& g, uint4* smem) {
+    const uint32_t K = g.k;
+    uint4* s_codes = smem;                                   // K / 16 half-blocks of codes
+    float* s_sum = reinterpret_cast<float*>(smem + K / 16);  // each half-block's code sum
+    float* s_sa = s_sum + K / 16;                            // each block's activation scale
+    const uint32_t halves = K / 16;
+    if constexpr (NORM) {
+        NormLoads<T> nl;
+        norm_loads<T, COH>(g.x, g.norm_weight, K, nl);
+        float* s_red = s_sa + K / 32;  // 257 floats
+        norm_quantize_prologue<T>(nl, g.eps, K, s_codes, s_sum, s_sa, s_red);
+    } else {
+        for (uint32_t h0 = threadIdx.x; h0 < halves; h0 += 4 * T) {
+            uint4 c[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t h = h0 + i * T;
+                c[i] = h < halves ? ld_u128<COH>(g.a_values + h) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t h = h0 + i * T;
+                if (h < halves) {
+                    s_codes[h] = c[i];
+                    s_sum[h] = static_cast<float>(byte_sum(c[i]));
+                }
+            }
+        }
+        for (uint32_t b = threadIdx.x; b < K / 32; b += T) s_sa[b] = ld_f32<COH>(g.a_scales + b);
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ const float* staged_sums(const uint4* smem, uint32_t k) { return reinterpret_cast<const float*>(smem + k / 16); }
+__device__ __forceinline__ const float* staged_scales(const uint4* smem, uint32_t k) { return staged_sums(smem, k) + k / 16; }
+
+}  // namespace vkml::gemv

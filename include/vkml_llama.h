@@ -32,6 +32,7 @@ typedef struct vkml_llama_options {
     int32_t quantize;           /* -1 none; 0 q8_0, 1 q4_0, 2 q4_1: float weights on load */
     int32_t integer_dot;        /* 1: int8 activations for quantized weights (default) */
     int32_t use_graphs;         /* 1: replay the decode step as a HIP graph (default) */
+    int32_t persistent_layers;  /* 1: a step's layers in one persistent launch where the model allows (default 0) */
     const char* device_name;    /* NULL or "": VKML_DEVICE, then device 0 */
 } vkml_llama_options;
 

@@ -80,7 +80,7 @@ __device__ __forceinline__ void rotate_pair(float& x, float& y, float c, float s
 template <int HD, bool F16, int HPW>
 struct AttendSmem {
     static constexpr uint32_t kRowBytes = HD * (F16 ? 2 : 4);
-    static constexpr bool kStageV = kRowBytes <= 512;  // V tile in LDS (up to 64 KiB)
+    static constexpr bool kStageV = kRowBytes <= 512;  // V tile in LDS (up to 64 KiB); as ChunkShape
     float q[HPW][HD];
     uint32_t knew[HD], vnew[HD];  // the new key and value, as cache bits
     alignas(16) uint8_t v[kStageV ? kChunk * kRowBytes : 16];
@@ -89,27 +89,78 @@ struct AttendSmem {
     float m[HPW], l[HPW];
 };
 
+// Shapes of a chunk item's loads.
+template <int HD, bool F16>
+struct ChunkShape {
+    static constexpr uint32_t kRowBytes = HD * (F16 ? 2 : 4);
+    static constexpr bool kStageV = kRowBytes <= 512;                         // V tile in LDS
+    static constexpr uint32_t kVLoads = kStageV ? kRowBytes * kChunk / 16 / kThreads : 1;  // 16-byte V loads a thread
+    static constexpr uint32_t KPL = HD / 4 / kLanes;                          // vec4s per lane per key
+    static constexpr uint32_t kSlots = kThreads / kLanes;                     // keys per scoring pass
+    static constexpr uint32_t kPasses = kChunk / kSlots;
+};
+
+// A chunk's K rows (lane g of a key's four holds vec4s g, g + 4, ...) and,
+// when it is staged, its V tile, in registers: every load of the chunk,
+// issued at once. Keys past the live ones re-read the last live key.
+template <int HD, bool F16>
+struct ChunkLoads {
+    using S = ChunkShape<HD, F16>;
+    KRaw<F16> k[S::kPasses][S::KPL];
+    uint4 v[S::kVLoads];
+};
+
+template <int HD, bool F16>
+__device__ __forceinline__ void attend_chunk_load(const ChunkArgs& a, uint32_t chunk, uint32_t kvh, uint32_t kv_len,
+                                                  ChunkLoads<HD, F16>& r) {
+    using S = ChunkShape<HD, F16>;
+    constexpr uint32_t RB = S::kRowBytes;
+    const uint32_t t = thread_index();
+    const uint32_t key0 = a.kv_start + chunk * kChunk;
+    const uint32_t n = min(kChunk, kv_len - key0);
+    const uint64_t kv_row0 = static_cast<uint64_t>(kvh) * a.capacity;
+    const auto row_of = [&](uint32_t key) -> uint64_t { return kv_row0 + (key0 + key) % a.capacity; };
+    const uint32_t lane4 = t % kLanes, slot = t / kLanes;
+#pragma unroll
+    for (uint32_t p = 0; p < S::kPasses; ++p) {
+        const uint64_t row = row_of(min(p * S::kSlots + slot, n - 1)) * HD;
+#pragma unroll
+        for (uint32_t j = 0; j < S::KPL; ++j) {
+            const uint32_t i = lane4 + kLanes * j;
+            if constexpr (F16) r.k[p][j] = ldg(reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.k_cache) + row + 4 * i));
+            else r.k[p][j] = ldg(reinterpret_cast<const float4*>(static_cast<const float*>(a.k_cache) + row + 4 * i));
+        }
+    }
+    if constexpr (S::kStageV) {
+#pragma unroll
+        for (uint32_t j = 0; j < S::kVLoads; ++j) {
+            const uint32_t u = t + j * kThreads, key = min(u / (RB / 16), n - 1), col = u % (RB / 16);
+            r.v[j] = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.v_cache) + row_of(key) * RB + 16ull * col));
+        }
+    }
+}
+
 // One (chunk, KV head, head group hl) item of the chunk pass, for a chunk
-// holding live keys (key0 < kv_len): scores, softmax and V over its keys,
+// holding live keys (key0 < kv_len), given its loads: scores, softmax and V over its keys,
 // writing the HPW heads' partials and (max, weight sum); in a step, RoPE of
 // q and of the new key and the append of the new key and value. HPW query
-// heads (of one KV head) share the K registers and the V tile. With COH, q,
-// the new key and value (the q|k|v GEMV's outputs) are read, and the
-// partials and stats written, coherently across XCDs.
-template <int HD, bool F16, int HPW, bool COH>
+// heads (of one KV head) share the K registers and the V tile. With COH, the
+// partials and stats are stored write-through, coherently across XCDs, for
+// a merge in another workgroup of the same launch. KB: keys of a slice whose
+// weights and values the V pass holds in registers at once.
+template <int HD, bool F16, int HPW, bool COH, uint32_t KB = 32>
 __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t chunk, uint32_t kvh, uint32_t hl, uint32_t pos,
-                                                  uint32_t kv_len, AttendSmem<HD, F16, HPW>& sm) {
+                                                  uint32_t kv_len, const ChunkLoads<HD, F16>& ld, AttendSmem<HD, F16, HPW>& sm) {
 #pragma clang fp contract(off)
-    constexpr uint32_t EB = F16 ? 2 : 4;
-    constexpr uint32_t RB = HD * EB;               // bytes per cache row
-    constexpr bool kStageV = AttendSmem<HD, F16, HPW>::kStageV;
-    constexpr uint32_t kVLoads = kStageV ? RB * kChunk / 16 / kThreads : 1;
-    constexpr uint32_t K4 = HD / 4;                // vec4s per row
-    constexpr uint32_t KPL = K4 / kLanes;          // vec4s per lane per key
-    constexpr uint32_t kSlots = kThreads / kLanes; // keys per scoring pass
-    constexpr uint32_t kPasses = kChunk / kSlots;
+    using S = ChunkShape<HD, F16>;
+    constexpr uint32_t RB = S::kRowBytes;          // bytes per cache row
+    constexpr bool kStageV = S::kStageV;
+    constexpr uint32_t kVLoads = S::kVLoads;
+    constexpr uint32_t KPL = S::KPL;
+    constexpr uint32_t kSlots = S::kSlots;
+    constexpr uint32_t kPasses = S::kPasses;
     const uint32_t G = a.group, head0 = kvh * G + hl * HPW;
-    const uint32_t t = threadIdx.x;
+    const uint32_t t = thread_index();
     const uint32_t key0 = a.kv_start + chunk * kChunk;
     const auto stats_at = [&](uint32_t h) -> uint64_t { return static_cast<uint64_t>(head0 + h) * a.chunks + chunk; };
     const uint32_t n = min(kChunk, kv_len - key0);
@@ -117,31 +168,7 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     const uint64_t kv_row0 = static_cast<uint64_t>(kvh) * a.capacity;
     const auto row_of = [&](uint32_t key) -> uint64_t { return kv_row0 + (key0 + key) % a.capacity; };
 
-    // Issue every load of the chunk: K for both scoring passes (lane g of a
-    // key's four takes vec4s g, g + 4, ...), and the V tile straight into LDS
-    // (the compiler issues every load before the first store waits). Keys
-    // past n re-read key n - 1.
     const uint32_t lane4 = t % kLanes, slot = t / kLanes;
-    KRaw<F16> kreg[kPasses][KPL];
-#pragma unroll
-    for (uint32_t p = 0; p < kPasses; ++p) {
-        const uint64_t row = row_of(min(p * kSlots + slot, n - 1)) * HD;
-#pragma unroll
-        for (uint32_t j = 0; j < KPL; ++j) {
-            const uint32_t i = lane4 + kLanes * j;
-            if constexpr (F16) kreg[p][j] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.k_cache) + row + 4 * i);
-            else kreg[p][j] = *reinterpret_cast<const float4*>(static_cast<const float*>(a.k_cache) + row + 4 * i);
-        }
-    }
-    if constexpr (kStageV) {
-#pragma unroll
-        for (uint32_t j = 0; j < kVLoads; ++j) {
-            const uint32_t u = t + j * kThreads, key = min(u / (RB / 16), n - 1), col = u % (RB / 16);
-            reinterpret_cast<uint4*>(sm.v)[u] =
-                *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.v_cache) + row_of(key) * RB + 16ull * col);
-        }
-    }
-
     // The queries (rotated in a step), and in the chunk holding it the new
     // key and value, rounded to the cache type and appended by head group
     // 0's workgroup.
@@ -154,18 +181,18 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
         for (uint32_t i = t; i < (HPW + 1) * half; i += kThreads) {
             const uint32_t h = i / half, k = i % half;  // h == HPW: the new key
             const uint32_t ia = a.style == 0 ? 2 * k : k, ib = a.style == 0 ? 2 * k + 1 : k + half;
-            const float c = tab[2 * k], sn = tab[2 * k + 1];
+            const float c = ldg(tab + 2 * k), sn = ldg(tab + 2 * k + 1);
             if (h < HPW) {
                 const float* qsrc = a.q + static_cast<uint64_t>(head0 + h) * HD;
-                float qx = ld_f32<COH>(qsrc + ia), qy = ld_f32<COH>(qsrc + ib);
+                float qx = ldg(qsrc + ia), qy = ldg(qsrc + ib);
                 if (a.rotate) rotate_pair(qx, qy, c, sn);
                 sm.q[h][ia] = qx;
                 sm.q[h][ib] = qy;
             } else if (holds_new) {
-                float kx = ld_f32<COH>(ksrc + ia), ky = ld_f32<COH>(ksrc + ib);
+                float kx = ldg(ksrc + ia), ky = ldg(ksrc + ib);
                 if (a.rotate) rotate_pair(kx, ky, c, sn);
                 const uint32_t kb[2] = {cache_bits(kx, F16), cache_bits(ky, F16)};
-                const uint32_t vb[2] = {cache_bits(ld_f32<COH>(vsrc + ia), F16), cache_bits(ld_f32<COH>(vsrc + ib), F16)};
+                const uint32_t vb[2] = {cache_bits(ldg(vsrc + ia), F16), cache_bits(ldg(vsrc + ib), F16)};
                 const uint32_t el[2] = {ia, ib};
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
@@ -173,18 +200,22 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
                     sm.vnew[el[e]] = vb[e];
                     if (hl == 0) {
                         if constexpr (F16) {
-                            static_cast<uint16_t*>(a.k_cache)[new_row + el[e]] = static_cast<uint16_t>(kb[e]);
-                            static_cast<uint16_t*>(a.v_cache)[new_row + el[e]] = static_cast<uint16_t>(vb[e]);
+                            stg(static_cast<uint16_t*>(a.k_cache) + new_row + el[e], static_cast<uint16_t>(kb[e]));
+                            stg(static_cast<uint16_t*>(a.v_cache) + new_row + el[e], static_cast<uint16_t>(vb[e]));
                         } else {
-                            static_cast<uint32_t*>(a.k_cache)[new_row + el[e]] = kb[e];
-                            static_cast<uint32_t*>(a.v_cache)[new_row + el[e]] = vb[e];
+                            stg(static_cast<uint32_t*>(a.k_cache) + new_row + el[e], kb[e]);
+                            stg(static_cast<uint32_t*>(a.v_cache) + new_row + el[e], vb[e]);
                         }
                     }
                 }
             }
         }
     } else {
-        for (uint32_t i = t; i < HPW * HD; i += kThreads) sm.q[i / HD][i % HD] = ld_f32<COH>(a.q + static_cast<uint64_t>(head0) * HD + i);
+        for (uint32_t i = t; i < HPW * HD; i += kThreads) sm.q[i / HD][i % HD] = ldg(a.q + static_cast<uint64_t>(head0) * HD + i);
+    }
+    if constexpr (kStageV) {
+#pragma unroll
+        for (uint32_t j = 0; j < kVLoads; ++j) reinterpret_cast<uint4*>(sm.v)[t + j * kThreads] = ld.v[j];
     }
     __syncthreads();
     if (kStageV && holds_new) {
@@ -194,40 +225,45 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
         }
     }
 
-    // Scores: part g of each head, then ((0 + p0) + p1) + p2) + p3.
-    float4 qr[HPW][KPL];
+    // Scores: part g of each head, then ((0 + p0) + p1) + p2) + p3; heads
+    // two at a time (their q in registers), sharing the K registers.
+    constexpr int HB = HPW < 2 ? HPW : 2;
 #pragma unroll
-    for (int h = 0; h < HPW; ++h)
+    for (int hb = 0; hb < HPW; hb += HB) {
+        float4 qr[HB][KPL];
 #pragma unroll
-        for (uint32_t j = 0; j < KPL; ++j) {
-            const uint32_t i = lane4 + kLanes * j;
-            qr[h][j] = make_float4(sm.q[h][4 * i], sm.q[h][4 * i + 1], sm.q[h][4 * i + 2], sm.q[h][4 * i + 3]);
-        }
+        for (int h = 0; h < HB; ++h)
 #pragma unroll
-    for (uint32_t p = 0; p < kPasses; ++p) {
-        const uint32_t key = p * kSlots + slot;
-        const bool fresh = holds_new && key == n - 1;
-        float part[HPW];
-#pragma unroll
-        for (int h = 0; h < HPW; ++h) part[h] = 0.0f;
-#pragma unroll
-        for (uint32_t j = 0; j < KPL; ++j) {
-            float4 kv = widen(kreg[p][j]);
-            if (fresh) {
+            for (uint32_t j = 0; j < KPL; ++j) {
                 const uint32_t i = lane4 + kLanes * j;
-                if constexpr (F16) kv = widen(make_uint2(sm.knew[4 * i] | (sm.knew[4 * i + 1] << 16), sm.knew[4 * i + 2] | (sm.knew[4 * i + 3] << 16)));
-                else kv = make_float4(__uint_as_float(sm.knew[4 * i]), __uint_as_float(sm.knew[4 * i + 1]),
-                                      __uint_as_float(sm.knew[4 * i + 2]), __uint_as_float(sm.knew[4 * i + 3]));
+                qr[h][j] = make_float4(sm.q[hb + h][4 * i], sm.q[hb + h][4 * i + 1], sm.q[hb + h][4 * i + 2], sm.q[hb + h][4 * i + 3]);
             }
 #pragma unroll
-            for (int h = 0; h < HPW; ++h) part[h] += dot4f(qr[h][j], kv);
-        }
+        for (uint32_t p = 0; p < kPasses; ++p) {
+            const uint32_t key = p * kSlots + slot;
+            const bool fresh = holds_new && key == n - 1;
+            float part[HB];
 #pragma unroll
-        for (int h = 0; h < HPW; ++h) {
-            const float p1 = __shfl_down(part[h], 1, kWave), p2 = __shfl_down(part[h], 2, kWave), p3 = __shfl_down(part[h], 3, kWave);
-            if (lane4 == 0 && key < n) {
-                const float sc = (0.0f + part[h] + p1 + p2 + p3) * a.scale;
-                sm.p[h][key] = a.softcap > 0.0f ? a.softcap * tanhf(fminf(fmaxf(sc / a.softcap, -10.0f), 10.0f)) : sc;
+            for (int h = 0; h < HB; ++h) part[h] = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < KPL; ++j) {
+                float4 kv = widen(ld.k[p][j]);
+                if (fresh) {
+                    const uint32_t i = lane4 + kLanes * j;
+                    if constexpr (F16) kv = widen(make_uint2(sm.knew[4 * i] | (sm.knew[4 * i + 1] << 16), sm.knew[4 * i + 2] | (sm.knew[4 * i + 3] << 16)));
+                    else kv = make_float4(__uint_as_float(sm.knew[4 * i]), __uint_as_float(sm.knew[4 * i + 1]),
+                                          __uint_as_float(sm.knew[4 * i + 2]), __uint_as_float(sm.knew[4 * i + 3]));
+                }
+#pragma unroll
+                for (int h = 0; h < HB; ++h) part[h] += dot4f(qr[h][j], kv);
+            }
+#pragma unroll
+            for (int h = 0; h < HB; ++h) {
+                const float p1 = __shfl_down(part[h], 1, kWave), p2 = __shfl_down(part[h], 2, kWave), p3 = __shfl_down(part[h], 3, kWave);
+                if (lane4 == 0 && key < n) {
+                    const float sc = (0.0f + part[h] + p1 + p2 + p3) * a.scale;
+                    sm.p[hb + h][key] = a.softcap > 0.0f ? a.softcap * tanhf(fminf(fmaxf(sc / a.softcap, -10.0f), 10.0f)) : sc;
+                }
             }
         }
     }
@@ -260,7 +296,6 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     // together, and whole chunks need no per-key guard.
     constexpr uint32_t slices = HD >= kChunk ? 1 : kChunk / HD;
     constexpr uint32_t NP = HD / 2;  // element pairs
-    constexpr uint32_t KB = 32;      // keys of a slice per batch
     const auto v_pair = [&](uint32_t key, uint32_t dp, float& x, float& y) {
         if constexpr (kStageV) {
             if constexpr (F16) {
@@ -277,11 +312,11 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
                 x = F16 ? f16_bits_to_float(sm.vnew[2 * dp]) : __uint_as_float(sm.vnew[2 * dp]);
                 y = F16 ? f16_bits_to_float(sm.vnew[2 * dp + 1]) : __uint_as_float(sm.vnew[2 * dp + 1]);
             } else if constexpr (F16) {
-                const uint32_t w = static_cast<const uint32_t*>(a.v_cache)[(row_of(key) * HD) / 2 + dp];
+                const uint32_t w = ldg(static_cast<const uint32_t*>(a.v_cache) + (row_of(key) * HD) / 2 + dp);
                 x = f16_bits_to_float(w & 0xFFFFu);
                 y = f16_bits_to_float(w >> 16);
             } else {
-                const float2 w = static_cast<const float2*>(a.v_cache)[(row_of(key) * HD) / 2 + dp];
+                const float2 w = ldg(static_cast<const float2*>(a.v_cache) + (row_of(key) * HD) / 2 + dp);
                 x = w.x;
                 y = w.y;
             }
@@ -355,16 +390,18 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
 // exp(m_c - M) and weight sum; here each is computed once per head (the
 // factors by one thread per chunk, in parallel) and shared through LDS, which
 // leaves each element its chain sum += r_c * partial_c. Its partials are
-// loaded 64 chunks at a time with every load in flight. Optionally quantizes
+// loaded B chunks at a time with every load in flight. Optionally quantizes
 // the result to Q8_0 with f32 scales (quantize.comp:100-111), the o
 // projection's input. s_r, s_l: count floats of LDS each; s_wmax: nt / 64.
 // Every thread of the workgroup calls it (it synchronizes the workgroup).
-template <bool COH>
+// With COH, the partials and stats are read and the results stored
+// coherently across XCDs (they come from, and go to, other workgroups of
+// the same launch), and out may be null (no f32 output).
+template <bool COH, uint32_t B = 64>
 __device__ __forceinline__ void merge_head(const float* partial, const float* stats, float* out, uint8_t* values, float* scales,
                                            uint32_t h, uint32_t stride, uint32_t count, uint32_t hd, uint32_t d, float* s_r,
                                            float* s_l, float* s_wmax) {
 #pragma clang fp contract(off)
-    constexpr uint32_t B = 64;
     const uint32_t nt = hd;
     const uint64_t first = static_cast<uint64_t>(h) * stride;
     const uint64_t* st = reinterpret_cast<const uint64_t*>(stats) + first;  // (max, weight sum) pairs
@@ -410,7 +447,7 @@ __device__ __forceinline__ void merge_head(const float* partial, const float* st
         }
     }
     const float o = sum / weight;
-    st_f32<COH>(out + static_cast<uint64_t>(h) * hd + d, o);
+    if (!COH || out) st_f32<COH>(out + static_cast<uint64_t>(h) * hd + d, o);
     if (values) {
         const float absmax = group_max<32>(fabsf(o));
         const float ds = absmax / 127.0f;

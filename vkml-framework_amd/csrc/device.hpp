@@ -135,6 +135,41 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
     return wave_max(s);
 }
 
+// ---------------------------------------------------------------- code generation
+
+// threadIdx.x through an empty asm: what a function derives from it is
+// computed where that function runs, not hoisted to a kernel's entry and
+// kept live (or spilled) across the phases of a persistent kernel.
+__device__ __forceinline__ uint32_t thread_index() {
+    uint32_t t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// Loads and stores through a pointer cast to the global address space at the
+// access. Pointers a kernel reads from memory (not its arguments) are
+// generic to the compiler, and accesses through them would be flat_load /
+// flat_store, which the LDS counter also tracks: every workgroup barrier
+// would then wait for the weight loads a kernel keeps in flight across it.
+// HIP's vector types (uint4, float2, ...) are classes whose copies take a
+// generic reference, so 8- and 16-byte values move as native vectors.
+template <class T>
+using global_t = __attribute__((address_space(1))) T;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <class T>
+__device__ __forceinline__ T ldg(const T* p) {
+    if constexpr (sizeof(T) == 16) return __builtin_bit_cast(T, *(const global_t<u32x4>*)p);
+    else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, *(const global_t<u32x2>*)p);
+    else return *(const global_t<T>*)p;
+}
+template <class T>
+__device__ __forceinline__ void stg(T* p, T v) {
+    if constexpr (sizeof(T) == 16) *(global_t<u32x4>*)p = __builtin_bit_cast(u32x4, v);
+    else if constexpr (sizeof(T) == 8) *(global_t<u32x2>*)p = __builtin_bit_cast(u32x2, v);
+    else *(global_t<T>*)p = v;
+}
+
 // ---------------------------------------------------------------- coherent access
 
 // Loads and stores of the values one workgroup of a launch produces for
@@ -144,13 +179,13 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
 // COH false these are plain accesses.
 template <bool COH>
 __device__ __forceinline__ uint32_t ld_u32(const uint32_t* p) {
-    if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else return *p;
+    if constexpr (COH) return __hip_atomic_load((const global_t<uint32_t>*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return ldg(p);
 }
 template <bool COH>
 __device__ __forceinline__ uint64_t ld_u64(const uint64_t* p) {
-    if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else return *p;
+    if constexpr (COH) return __hip_atomic_load((const global_t<uint64_t>*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return ldg(p);
 }
 template <bool COH>
 __device__ __forceinline__ float ld_f32(const float* p) {
@@ -164,7 +199,7 @@ __device__ __forceinline__ uint4 ld_u128(const uint4* p) {
         return make_uint4(static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b),
                           static_cast<uint32_t>(b >> 32));
     } else {
-        return *p;
+        return ldg(p);
     }
 }
 template <bool COH>
@@ -174,8 +209,8 @@ __device__ __forceinline__ float4 ld_f32x4(const float4* p) {
 }
 template <bool COH>
 __device__ __forceinline__ void st_u32(uint32_t* p, uint32_t v) {
-    if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *p = v;
+    if constexpr (COH) __hip_atomic_store((global_t<uint32_t>*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else stg(p, v);
 }
 template <bool COH>
 __device__ __forceinline__ void st_f32(float* p, float v) {
@@ -183,8 +218,8 @@ __device__ __forceinline__ void st_f32(float* p, float v) {
 }
 template <bool COH>
 __device__ __forceinline__ void st_u8(uint8_t* p, uint8_t v) {
-    if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *p = v;
+    if constexpr (COH) __hip_atomic_store((global_t<uint8_t>*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else stg(p, v);
 }
 
 // ---------------------------------------------------------------- int8 dot

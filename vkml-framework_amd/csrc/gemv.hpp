@@ -23,6 +23,9 @@
 //   2l, 2l + 1. (8 lanes: blocks 2j, 2j + 1, half-blocks 4j .. 4j + 3.)
 // - q8_0 (16 lanes): lane l loads half-blocks l and l + 16. (8 lanes: j,
 //   j + 8, j + 16, j + 24.)
+// - 32 lanes (q4_K, q8_0): lane l holds accumulator l, half-block l of the
+//   round alone; for q4_K it loads the 16 code bytes that hold it in their
+//   low or high nibbles (so lanes l and l ^ 2 load the same bytes).
 // The halving tree's strides 16 .. 1 then become, per mapping, additions
 // within a lane or exchanges between lanes (xor shuffles).
 //
@@ -66,7 +69,8 @@ struct GemvArgs {
 // The accumulator (= half-block of the round) held in slot e of lane l.
 template <int FMT, int LPR>
 __device__ __forceinline__ constexpr uint32_t acc_index(uint32_t l, uint32_t e) {
-    if constexpr (FMT == VKML_Q8_0) return LPR == 16 ? l + 16 * e : l + 8 * e;
+    if constexpr (LPR == 32) return l;
+    else if constexpr (FMT == VKML_Q8_0) return LPR == 16 ? l + 16 * e : l + 8 * e;
     else if constexpr (FMT == VKML_Q4_K && LPR == 16) return 16 * (l / 8) + 4 * ((l / 2) % 4) + (l % 2) + 2 * e;
     else return (32 / LPR) * l + e;  // q4_0 / q4_1, and q4_K with 8 lanes
 }
@@ -74,7 +78,7 @@ __device__ __forceinline__ constexpr uint32_t acc_index(uint32_t l, uint32_t e) 
 template <int FMT, int LPR>
 struct Plan {
     static constexpr int NS = 32 / LPR;                        // accumulators (slots) per lane
-    static constexpr int NQ = FMT == VKML_Q8_0 ? NS : NS / 2;  // 16-byte code loads per lane and round
+    static constexpr int NQ = FMT == VKML_Q8_0 || LPR == 32 ? NS : NS / 2;  // 16-byte code loads per lane and round
 };
 
 // One lane's weights for one round of one matrix: codes, and scales (q4_K:
@@ -86,9 +90,9 @@ struct RoundW {
     uint32_t s[FMT == VKML_Q4_K ? 4 : Plan<FMT, LPR>::NS];
 };
 
-__device__ __forceinline__ uint32_t ld16(const void* p, uint64_t i) { return static_cast<const uint16_t*>(p)[i]; }
-__device__ __forceinline__ uint32_t ld32(const void* p, uint64_t i) { return static_cast<const uint32_t*>(p)[i]; }
-__device__ __forceinline__ uint4 ld128(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint32_t ld16(const void* p, uint64_t i) { return ldg(static_cast<const uint16_t*>(p) + i); }
+__device__ __forceinline__ uint32_t ld32(const void* p, uint64_t i) { return ldg(static_cast<const uint32_t*>(p) + i); }
+__device__ __forceinline__ uint4 ld128(const uint8_t* p) { return ldg(reinterpret_cast<const uint4*>(p)); }
 
 // Loads lane l's share of round r of row `row`. Every load is issued
 // unconditionally (positions past the row's end, in a last round shorter
@@ -111,16 +115,19 @@ __device__ __forceinline__ void load_round(const void* bv, const void* bs, uint3
             w.s[e] = F16S ? ld16(bs, blocks + hb / 2) : ld32(bs, blocks + hb / 2);
         }
     } else if constexpr (FMT == VKML_Q4_K) {
-        const uint32_t p = LPR == 16 ? l / 8 : l / 4;  // which super-block of the round
+        const uint32_t p = LPR == 32 ? l / 16 : LPR == 16 ? l / 8 : l / 4;  // which super-block of the round
         const uint32_t sb = min(2 * r + p, K / 256 - 1);
         const uint8_t* base = codes + R * (K / 2) + 128ull * sb;
-        if constexpr (LPR == 16) {
+        if constexpr (LPR == 32) {
+            const uint32_t h = l % 16;  // half-block h of the super-block: group h / 4, bytes 16 (h % 2) of it
+            w.q[0] = ld128(base + 32 * (h / 4) + 16 * (h % 2));
+        } else if constexpr (LPR == 16) {
             w.q[0] = ld128(base + 16 * (l % 8));
         } else {
             w.q[0] = ld128(base + 32 * (l % 4));
             w.q[1] = ld128(base + 32 * (l % 4) + 16);
         }
-        const uint4 h = static_cast<const uint4*>(bs)[R * (K / 256) + sb];
+        const uint4 h = ldg(static_cast<const uint4*>(bs) + R * (K / 256) + sb);
         w.s[0] = h.x; w.s[1] = h.y; w.s[2] = h.z; w.s[3] = h.w;
     } else {
         const uint8_t* base = codes + R * (K / 2);
@@ -133,7 +140,7 @@ __device__ __forceinline__ void load_round(const void* bv, const void* bs, uint3
                 if constexpr (F16S) {
                     w.s[2 * b] = ld32(bs, block);  // f16 scale | f16 offset << 16
                 } else {
-                    const uint2 so = static_cast<const uint2*>(bs)[block];
+                    const uint2 so = ldg(static_cast<const uint2*>(bs) + block);
                     w.s[2 * b] = so.x;
                     w.s[2 * b + 1] = so.y;
                 }
@@ -204,6 +211,17 @@ __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t 
             d[e] = half_dot(w.q[e].x, w.q[e].y, w.q[e].z, w.q[e].w, a[e]);
             s[e] = scale_of(w.s[e], F16S);
         }
+    } else if constexpr (FMT == VKML_Q4_K && LPR == 32) {
+        // Half-block h: low nibbles (sub-block 2c) for h % 4 < 2, else high (2c + 1).
+        const uint32_t h = l % 16, c = h / 4;
+        const bool hi = h % 4 >= 2;
+        float s0, o0, s1, o1;
+        q4k_sub_scales(w.s, c, s0, o0, s1, o1);
+        const uint4 q = w.q[0];
+        const uint32_t sh = hi ? 4 : 0;
+        d[0] = half_dot((q.x >> sh) & kLow, (q.y >> sh) & kLow, (q.z >> sh) & kLow, (q.w >> sh) & kLow, a[0]);
+        s[0] = hi ? s1 : s0;
+        o[0] = hi ? o1 : o0;
     } else if constexpr (FMT == VKML_Q4_K) {
         const uint32_t c = LPR == 16 ? (l / 2) % 4 : l % 4;
         float s0, o0, s1, o1;
@@ -265,7 +283,9 @@ __device__ __forceinline__ float row_tree(float (&acc)[32 / LPR]) {
         for (int e = 0; e < 32 / LPR; ++e)
             if (e < slots) acc[e] += __shfl_xor(acc[e], mask, kWave);
     };
-    if constexpr (FMT == VKML_Q8_0 && LPR == 16) {  // L = l + 16e
+    if constexpr (LPR == 32) {  // L = l
+        x(16, 1); x(8, 1); x(4, 1); x(2, 1); x(1, 1);
+    } else if constexpr (FMT == VKML_Q8_0 && LPR == 16) {  // L = l + 16e
         acc[0] += acc[1];
         x(8, 1); x(4, 1); x(2, 1); x(1, 1);
     } else if constexpr (FMT == VKML_Q8_0) {  // L = j + 8e
@@ -308,11 +328,11 @@ struct NormLoads {
 
 template <uint32_t T, bool COH>
 __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint32_t K, NormLoads<T>& r) {
-    const uint32_t t = threadIdx.x, blk = t < K / 32 ? t : 0;
+    const uint32_t t = thread_index(), blk = t < K / 32 ? t : 0;
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
         r.xb[i] = ld_f32x4<COH>(reinterpret_cast<const float4*>(x) + 8 * blk + i);
-        r.wb[i] = reinterpret_cast<const float4*>(w)[8 * blk + i];
+        r.wb[i] = ldg(reinterpret_cast<const float4*>(w) + 8 * blk + i);
     }
 #pragma unroll
     for (uint32_t v = 0; v < NormLoads<T>::V; ++v)
@@ -325,7 +345,7 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
                                        float* s_red) {
 #pragma clang fp contract(off)
     static_assert(T >= 128, "workgroup width");
-    const uint32_t t = threadIdx.x;
+    const uint32_t t = thread_index();
 #pragma unroll
     for (uint32_t v = 0; v < NormLoads<T>::V; ++v) {
         const uint32_t inv = t + v * T;
@@ -381,12 +401,14 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
 
 
 // The rows of one item (T / LPR consecutive rows) of a GEMV: start() issues
-// the item's first batch of weight loads, which depend on nothing computed
-// at run time, so a caller can issue them early (before the activation is
-// staged, or before a grid barrier); finish() sums the rounds over the staged
-// activation and applies the epilogue. With COH, the outputs, the residual
-// and the Q8_0 output are accessed coherently across XCDs.
-template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool QOUT, bool COH>
+// the item's first PRE batches of weight loads (1 or 2), which depend on
+// nothing computed at run time, so a caller can issue them early (before the
+// activation is staged, or before a grid barrier); finish() sums the rounds
+// over the staged activation and applies the epilogue, keeping two batches
+// in flight. With COH, the outputs (and the Q8_0 output) are stored
+// write-through, coherently across XCDs, for readers in other workgroups of
+// the same launch; g.out may then be null (no f32 output).
+template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool QOUT, bool COH, int PRE = 1>
 struct GemvRows {
     static constexpr int NS = Plan<FMT, LPR>::NS;
     static constexpr int NM = EPI == kSwiglu ? 2 : 1;
@@ -407,10 +429,12 @@ struct GemvRows {
     __device__ __forceinline__ void start(const GemvArgs& g, uint32_t it) {
         item = it;
         rounds = (g.k + 511) / 512;
-        l = threadIdx.x % LPR;
-        row = it * kRows + threadIdx.x / LPR;
+        const uint32_t t = thread_index();
+        l = t % LPR;
+        row = it * kRows + t / LPR;
         r_row = min(row, g.n - 1);
         load_batch(g, wa, 0);
+        if constexpr (PRE == 2) load_batch(g, wb, B);
     }
 
     __device__ __forceinline__ void finish(const GemvArgs& g, const uint4* s_codes, const float* s_sum, const float* s_sa) {
@@ -430,11 +454,25 @@ struct GemvRows {
                 }
             }
         };
-        for (uint32_t r0 = 0; r0 < rounds; r0 += 2 * B) {
-            load_batch(g, wb, r0 + B);
+        if constexpr (PRE == 2) {
+            // Both batches are in flight on entry; the last pair of batches
+            // is peeled so that no load is issued past the rows' end.
+            uint32_t r0 = 0;
+            for (; r0 + 2 * B < rounds; r0 += 2 * B) {
+                sum_batch(wa, r0);
+                load_batch(g, wa, r0 + 2 * B);
+                sum_batch(wb, r0 + B);
+                load_batch(g, wb, r0 + 3 * B);
+            }
             sum_batch(wa, r0);
-            load_batch(g, wa, r0 + 2 * B);
             sum_batch(wb, r0 + B);
+        } else {
+            for (uint32_t r0 = 0; r0 < rounds; r0 += 2 * B) {
+                load_batch(g, wb, r0 + B);
+                sum_batch(wa, r0);
+                load_batch(g, wa, r0 + 2 * B);
+                sum_batch(wb, r0 + B);
+            }
         }
 
         float y[NM];
@@ -445,28 +483,29 @@ struct GemvRows {
             if constexpr (EPI == kStore) {
                 result = y[0];
             } else if constexpr (EPI == kAdd) {
-                result = ld_f32<COH>(g.residual + row) + y[0];  // add(x, attn_out), llama.cpp:374,386
+                result = ldg(g.residual + row) + y[0];  // add(x, attn_out), llama.cpp:374,386
             } else {
                 // silu(gate) * up (unary.comp:21-24, then binary.comp's mul)
                 const float gate = y[0], up = y[NM - 1];
                 result = gate / (1.0f + vk_expf(-gate)) * up;
             }
-            st_f32<COH>(g.out + row, result);
+            if (!COH || g.out) st_f32<COH>(g.out + row, result);
         }
         if constexpr (QOUT) {
             // The item's T / LPR = 32 rows are one Q8_0 block of the output
             // (quantize.comp:100-111): its absmax, scale and codes.
             static_assert(T / LPR == 32, "one Q8_0 block per item");
             __shared__ float s_out[32];
-            if (l == 0) s_out[threadIdx.x / LPR] = result;
+            const uint32_t t = thread_index();
+            if (l == 0) s_out[t / LPR] = result;
             __syncthreads();
-            if (threadIdx.x < 32) {
-                const float v = s_out[threadIdx.x];
+            if (t < 32) {
+                const float v = s_out[t];
                 const float absmax = group_max<32>(fabsf(v));
                 const float d = absmax / 127.0f;
                 const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-                st_u8<COH>(g.out_values + item * 32 + threadIdx.x, static_cast<uint8_t>(static_cast<int8_t>(quant_code(v, inv))));
-                if (threadIdx.x == 0) st_f32<COH>(g.out_scales + item, d);
+                st_u8<COH>(g.out_values + item * 32 + t, static_cast<uint8_t>(static_cast<int8_t>(quant_code(v, inv))));
+                if (t == 0) st_f32<COH>(g.out_scales + item, d);
             }
             __syncthreads();  // s_out is free for the next item
         }
@@ -485,14 +524,14 @@ __device__ __forceinline__ void stage_activation(const GemvArgs& g, uint4* smem)
     uint4* s_codes = smem;                                   // K / 16 half-blocks of codes
     float* s_sum = reinterpret_cast<float*>(smem + K / 16);  // each half-block's code sum
     float* s_sa = s_sum + K / 16;                            // each block's activation scale
-    const uint32_t halves = K / 16;
+    const uint32_t halves = K / 16, t = thread_index();
     if constexpr (NORM) {
         NormLoads<T> nl;
         norm_loads<T, COH>(g.x, g.norm_weight, K, nl);
         float* s_red = s_sa + K / 32;  // 257 floats
         norm_quantize_prologue<T>(nl, g.eps, K, s_codes, s_sum, s_sa, s_red);
     } else {
-        for (uint32_t h0 = threadIdx.x; h0 < halves; h0 += 4 * T) {
+        for (uint32_t h0 = t; h0 < halves; h0 += 4 * T) {
             uint4 c[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -508,7 +547,7 @@ __device__ __forceinline__ void stage_activation(const GemvArgs& g, uint4* smem)
                 }
             }
         }
-        for (uint32_t b = threadIdx.x; b < K / 32; b += T) s_sa[b] = ld_f32<COH>(g.a_scales + b);
+        for (uint32_t b = t; b < K / 32; b += T) s_sa[b] = ld_f32<COH>(g.a_scales + b);
     }
     __syncthreads();
 }

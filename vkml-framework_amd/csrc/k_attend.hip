@@ -45,7 +45,9 @@ __global__ void __launch_bounds__(kThreads) k_attend_chunk(ChunkArgs a) {
         }
         return;
     }
-    attend_chunk_item<HD, F16, HPW, false>(a, chunk, kvh, hl, pos, kv_len, sm);
+    ChunkLoads<HD, F16> ld;
+    attend_chunk_load<HD, F16>(a, chunk, kvh, kv_len, ld);
+    attend_chunk_item<HD, F16, HPW, false>(a, chunk, kvh, hl, pos, kv_len, ld, sm);
 }
 
 constexpr uint32_t kMergeMaxChunks = 1024;  // 131072 keys

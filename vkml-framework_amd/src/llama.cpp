@@ -11,7 +11,10 @@
 //   merge + Q8_0 -> o GEMV + residual -> gate|up GEMV (rms_norm + Q8_0
 //   prologue, SwiGLU + Q8_0 epilogue) -> down GEMV + residual,
 // then the final norm, the lm_head GEMV and (greedy) an argmax that writes
-// the next token into the state. The step is captured once as a HIP graph
+// the next token into the state. When the model's formats and shapes allow
+// (q4_K matrices, f16 caches, head_dim 128: vkml_decode_layers), the layers
+// instead run as one persistent launch that walks the same phases between
+// grid barriers, with the same arithmetic. The step is captured once as a HIP graph
 // and replayed, so a prompt or a greedy generation is a stream of graph
 // launches with no host round trip between tokens. Prompts run one token per
 // step through the same graph; the arithmetic per token is the reference's
@@ -308,6 +311,10 @@ struct Llama::Impl {
     Tensor x, xn, xq, xs, qkv, q, attn, aq, as, partial, stats, h, hq, hs, gate_tmp, up_tmp, ytmp, logits, state, log;
     std::int64_t chunks = 1;  // decode attention's 128-key chunks over the whole cache
     std::uint64_t graph_logits = 0, graph_greedy = 0;
+    // The persistent layers launch (vkml_decode_layers): its per-layer
+    // pointer table and its barrier / error words, when the model allows it.
+    bool persistent = false;
+    Tensor layer_table, sync, work;
 
     const Weight& lm_head() const { return tied ? embed : *lm_head_own; }
 
@@ -340,6 +347,53 @@ struct Llama::Impl {
 
     bool quantized_input(const Weight& w) const { return int_dot && w.int_dot_ok(); }
 
+    // What vkml_decode_layers takes: every layer matrix q4_K on the int8
+    // path (q|k|v stacked), f16 caches, head_dim 128, a multiple of 4 query
+    // heads per KV head, hidden a multiple of 256 up to 4096, ffn a multiple
+    // of 256.
+    bool persistent_ok() const {
+        const LlamaConfig& c = config;
+        const auto q4k = [&](const Weight& w) { return quantized_input(w) && w.type_code() == VKML_Q4_K; };
+        if (!options.persistent_layers || !int_dot || options.kv_cache != DType::F16 || c.head_dim != 128) return false;
+        if (c.num_kv_heads <= 0 || c.num_heads % c.num_kv_heads != 0 || (c.num_heads / c.num_kv_heads) % 4 != 0) return false;
+        if (c.num_heads / 4 > 64) return false;
+        if (c.hidden_size % 256 != 0 || c.hidden_size > 4096 || c.intermediate_size % 256 != 0 || c.intermediate_size > 32768) return false;
+        if ((c.num_heads * c.head_dim) % 256 != 0 || chunks > 1024) return false;
+        return std::all_of(layers.begin(), layers.end(), [&](const Layer& L) {
+            return L.qkv.size() == 1 && q4k(L.qkv[0].first) && q4k(L.o) && q4k(L.gate) && q4k(L.up) && q4k(L.down);
+        });
+    }
+
+    // Uploads the layer table and clears the sync words.
+    void setup_persistent(Context& context) {
+        std::vector<vkml_decode_layer> table;
+        for (const Layer& L : layers) {
+            table.push_back({static_cast<const float*>(L.attn_norm.data()), static_cast<const float*>(L.ffn_norm.data()),
+                             L.qkv[0].first.values(), L.qkv[0].first.scales(), L.o.values(), L.o.scales(), L.gate.values(),
+                             L.gate.scales(), L.up.values(), L.up.scales(), L.down.values(), L.down.scales(),
+                             const_cast<void*>(L.k_cache.data()), const_cast<void*>(L.v_cache.data())});
+        }
+        const std::uint64_t bytes = table.size() * sizeof(vkml_decode_layer);
+        layer_table = Tensor::zeros(context, {static_cast<std::int64_t>((bytes + 3) / 4)}, DType::I32);
+        check(vkml_memcpy_h2d(layer_table.data(), table.data(), bytes), "Llama: layer table");
+        const vkml_decode_layers_params p = layers_params();
+        sync = Tensor::zeros(context, {static_cast<std::int64_t>(vkml_decode_sync_bytes(&p) / 4)}, DType::I32);
+        work = Tensor::zeros(context, {static_cast<std::int64_t>((vkml_decode_work_bytes(&p) + 3) / 4)}, DType::I32);
+    }
+
+    vkml_decode_layers_params layers_params() const {
+        const LlamaConfig& c = config;
+        return vkml_decode_layers_params{u32(c.num_layers), u32(c.hidden_size), u32(c.num_heads), u32(c.num_kv_heads), u32(c.head_dim),
+                                         u32(c.intermediate_size), VKML_Q4_K, VKML_F16, u32(context_length), u32(chunks),
+                                         c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1, c.rms_norm_eps,
+                                         1.0f / std::sqrt(static_cast<float>(c.head_dim))};
+    }
+
+    // Reports a grid barrier of the persistent launch that timed out.
+    void check_persistent() const {
+        if (persistent) check(vkml_decode_layers_check(static_cast<std::uint32_t*>(const_cast<void*>(sync.data()))), "Llama: decode step");
+    }
+
     // One token: the state's token at the state's position.
     void step(bool greedy) {
         const LlamaConfig& c = config;
@@ -365,6 +419,13 @@ struct Llama::Impl {
         // GEMV (rms_norm + Q8_0 in the kernel's prologue, vkml_gemv_fused);
         // not the lm_head's, whose thousands of workgroups would each redo it.
         const bool fold = quant_d && d <= 4096;
+        if (persistent) {
+            tag("layers");
+            const vkml_decode_layers_params lp = layers_params();
+            const vkml_decode_buffers b{xp, static_cast<float*>(partial.data()), static_cast<float*>(stats.data()), work.data(),
+                                        static_cast<const float*>(rope.data()), static_cast<std::uint32_t*>(sync.data())};
+            check(vkml_decode_layers(&lp, static_cast<const vkml_decode_layer*>(layer_table.data()), &b, st), "decode_layers");
+        }
         const auto fused = [&](const Weight& w, const Tensor& nw, float* out, const char* t) {
             tag(t);
             const vkml_gemv_fused_params fp{u32(w.rows), u32(w.cols), w.type_code(), w.scale_code(), 0, 1, c.rms_norm_eps, 0};
@@ -373,6 +434,7 @@ struct Llama::Impl {
                   t);
         };
         for (const Layer& L : layers) {
+            if (persistent) break;
             const bool fold_qkv =
                 fold && std::all_of(L.qkv.begin(), L.qkv.end(), [&](const auto& wr) { return quantized_input(wr.first); });
             if (fold_qkv) {
@@ -580,6 +642,8 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
     m.chunks = (context_length + 127) / 128;
     m.partial = f32(c.num_heads * m.chunks * hd);
     m.stats = f32(c.num_heads * m.chunks * 2);
+    m.persistent = m.persistent_ok();
+    if (m.persistent) m.setup_persistent(context);
     context.synchronize();
     return Llama(std::move(impl));
 }
@@ -599,6 +663,7 @@ Tensor Llama::forward(std::span<const std::int32_t> tokens) {
     }
     Tensor out = Tensor::empty(*m.context, {m.config.vocab_size}, DType::F32);
     check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward");
+    m.check_persistent();
     return out;
 }
 
@@ -614,6 +679,7 @@ Tensor Llama::forward_all(std::span<const std::int32_t> tokens) {
         ++m.position;
         check(vkml_memcpy_d2d(static_cast<std::uint8_t*>(out.data()) + row * i, m.logits.data(), row), "Llama::forward_all");
     }
+    m.check_persistent();
     return out;
 }
 
@@ -625,6 +691,7 @@ std::vector<std::int32_t> Llama::generate_greedy(std::int32_t first, std::int64_
     for (std::int64_t i = 0; i < count; ++i) m.run_step(true);
     std::vector<std::int32_t> out(static_cast<std::size_t>(count));
     check(vkml_memcpy_d2h(out.data(), m.log.data(), out.size() * 4), "Llama::generate_greedy");
+    m.check_persistent();
     m.position += count;
     return out;
 }

@@ -153,7 +153,6 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
                                                   uint32_t kv_len, const ChunkLoads<HD, F16>& ld, AttendSmem<HD, F16, HPW>& sm) {
 #pragma clang fp contract(off)
     using S = ChunkShape<HD, F16>;
-    constexpr uint32_t RB = S::kRowBytes;          // bytes per cache row
     constexpr bool kStageV = S::kStageV;
     constexpr uint32_t kVLoads = S::kVLoads;
     constexpr uint32_t KPL = S::KPL;

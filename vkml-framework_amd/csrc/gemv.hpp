@@ -94,6 +94,31 @@ __device__ __forceinline__ uint32_t ld16(const void* p, uint64_t i) { return ldg
 __device__ __forceinline__ uint32_t ld32(const void* p, uint64_t i) { return ldg(static_cast<const uint32_t*>(p) + i); }
 __device__ __forceinline__ uint4 ld128(const uint8_t* p) { return ldg(reinterpret_cast<const uint4*>(p)); }
 
+// A raw buffer over `bytes` bytes at p (the gfx9 descriptor word 3), and
+// loads at a lane offset plus a scalar offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 bload128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), 0));
+}
+__device__ __forceinline__ uint32_t bload32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+__device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+
+// Bytes of an [n, k] matrix's codes and scales (q4_K: 16-byte headers).
+template <int FMT>
+__host__ __device__ constexpr uint64_t code_bytes(uint64_t n, uint64_t k) {
+    return FMT == VKML_Q4_K || FMT == VKML_Q4_0 || FMT == VKML_Q4_1 ? n * k / 2 : n * k;
+}
+template <int FMT, bool F16S>
+__host__ __device__ constexpr uint64_t scale_bytes(uint64_t n, uint64_t k) {
+    return FMT == VKML_Q4_K ? n * (k / 256) * 16 : n * (k / 32) * (F16S ? 2 : 4) * (FMT == VKML_Q4_1 ? 2 : 1);
+}
+
 // Loads lane l's share of round r of row `row`. Every load is issued
 // unconditionally (positions past the row's end, in a last round shorter
 // than 512 values, are clamped to its last block and their terms skipped),
@@ -184,14 +209,29 @@ __device__ __forceinline__ void q4k_sub_scales(const uint32_t (&h)[4], uint32_t 
     o1 = static_cast<float>(nd * static_cast<_Float16>(mn >> 8));
 }
 
+// The same for sub-block j alone (0 .. 7): the 6-bit scale and min of the
+// reference's layout (bytes j, j + 4 of the 12; for j >= 4 their high bits
+// in bytes j - 4, j and the low nibbles in byte j + 4).
+__device__ __forceinline__ void q4k_sub_scale(const uint32_t (&h)[4], uint32_t j, float& s, float& o) {
+    const uint32_t sh = 8 * (j % 4);
+    const uint32_t b1 = (h[1] >> sh) & 0xFFu, b2 = (h[2] >> sh) & 0xFFu, b3 = (h[3] >> sh) & 0xFFu;
+    const uint32_t sc = j < 4 ? b1 & 63u : (b3 & 15u) | ((b1 >> 6) << 4);
+    const uint32_t mn = j < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
+    const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h[0] & 0xFFFFu));
+    const _Float16 nd = -__builtin_bit_cast(_Float16, static_cast<uint16_t>(h[0] >> 16));
+    s = static_cast<float>(d * static_cast<_Float16>(sc));
+    o = static_cast<float>(nd * static_cast<_Float16>(mn));
+}
+
 // Adds one lane's terms of round r to acc[0 .. NS) with the reference's
 // expressions (gemv_dot.comp:112,114): q8_0 / q4_0 float(d) * (scale * sa);
 // q4_1 and q4_K sa * (float(d) * scale + float(sum) * offset). The
-// activation codes, half-block sums and block scales come from LDS.
-template <int FMT, bool F16S, int LPR>
+// activation codes, and each half-block's code sum with its block's scale,
+// come from LDS. FULL: every half-block of the round is in the row (K a
+// multiple of 512).
+template <int FMT, bool F16S, int LPR, bool FULL = false>
 __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t r, uint32_t l, uint32_t K,
-                                            const uint4* s_codes, const float* s_sum, const float* s_sa,
-                                            float (&acc)[Plan<FMT, LPR>::NS]) {
+                                            const uint4* s_codes, const float2* s_ss, float (&acc)[Plan<FMT, LPR>::NS]) {
 #pragma clang fp contract(off)
     constexpr int NS = Plan<FMT, LPR>::NS;
     const uint32_t halves = K / 16;
@@ -202,7 +242,7 @@ __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t 
 #pragma unroll
     for (int e = 0; e < NS; ++e) {
         const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
-        live[e] = hb < halves;
+        live[e] = FULL || hb < halves;
         a[e] = live[e] ? s_codes[hb] : make_uint4(0, 0, 0, 0);
     }
     if constexpr (FMT == VKML_Q8_0) {
@@ -212,16 +252,12 @@ __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t 
             s[e] = scale_of(w.s[e], F16S);
         }
     } else if constexpr (FMT == VKML_Q4_K && LPR == 32) {
-        // Half-block h: low nibbles (sub-block 2c) for h % 4 < 2, else high (2c + 1).
-        const uint32_t h = l % 16, c = h / 4;
-        const bool hi = h % 4 >= 2;
-        float s0, o0, s1, o1;
-        q4k_sub_scales(w.s, c, s0, o0, s1, o1);
+        // Half-block hb of the super-block is in sub-block hb / 2: the low
+        // nibbles of its bytes for an even sub-block, the high for an odd one.
+        const uint32_t j = (l % 16) / 2, sh = 4 * (j % 2);
+        q4k_sub_scale(w.s, j, s[0], o[0]);
         const uint4 q = w.q[0];
-        const uint32_t sh = hi ? 4 : 0;
         d[0] = half_dot((q.x >> sh) & kLow, (q.y >> sh) & kLow, (q.z >> sh) & kLow, (q.w >> sh) & kLow, a[0]);
-        s[0] = hi ? s1 : s0;
-        o[0] = hi ? o1 : o0;
     } else if constexpr (FMT == VKML_Q4_K) {
         const uint32_t c = LPR == 16 ? (l / 2) % 4 : l % 4;
         float s0, o0, s1, o1;
@@ -260,13 +296,14 @@ __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t 
     for (int e = 0; e < NS; ++e) {
         if (!live[e]) continue;
         const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
-        const float sa = s_sa[hb / 2];
+        const float2 ss = s_ss[hb];  // (code sum, block scale)
+        const float sa = ss.y;
         if constexpr (FMT == VKML_Q4_1 || FMT == VKML_Q4_K) {
-            acc[e] += sa * (static_cast<float>(d[e]) * s[e] + s_sum[hb] * o[e]);
+            acc[e] += sa * (static_cast<float>(d[e]) * s[e] + ss.x * o[e]);
         } else {
             // q4_0 codes are q + 8: the reference's signed bytes (q4_bytes)
             // give the same exact sum, d - 8 * sum(a).
-            if constexpr (FMT == VKML_Q4_0) d[e] -= 8 * static_cast<int>(s_sum[hb]);
+            if constexpr (FMT == VKML_Q4_0) d[e] -= 8 * static_cast<int>(ss.x);
             acc[e] += static_cast<float>(d[e]) * (s[e] * sa);
         }
     }
@@ -341,8 +378,7 @@ __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint3
 }
 
 template <uint32_t T>
-__device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float* s_sum, float* s_sa,
-                                       float* s_red) {
+__device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float2* s_ss, float* s_red) {
 #pragma clang fp contract(off)
     static_assert(T >= 128, "workgroup width");
     const uint32_t t = thread_index();
@@ -394,9 +430,8 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
     const uint4 hi = make_uint4(words[4], words[5], words[6], words[7]);
     s_codes[2 * blk] = lo;
     s_codes[2 * blk + 1] = hi;
-    s_sum[2 * blk] = static_cast<float>(byte_sum(lo));
-    s_sum[2 * blk + 1] = static_cast<float>(byte_sum(hi));
-    s_sa[blk] = d;
+    s_ss[2 * blk] = make_float2(static_cast<float>(byte_sum(lo)), d);
+    s_ss[2 * blk + 1] = make_float2(static_cast<float>(byte_sum(hi)), d);
 }
 
 
@@ -407,22 +442,47 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
 // over the staged activation and applies the epilogue, keeping two batches
 // in flight. With COH, the outputs (and the Q8_0 output) are stored
 // write-through, coherently across XCDs, for readers in other workgroups of
-// the same launch; g.out may then be null (no f32 output).
-template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool QOUT, bool COH, int PRE = 1>
+// the same launch; g.out may then be null (no f32 output). FULL: K a
+// multiple of 512 (every round whole).
+//
+// At 32 lanes a row (q4_K, q8_0) the weights are read with buffer loads: a
+// lane's byte offset into the matrix is computed once per item, and each
+// round adds a scalar offset (the matrix must be under 4 GiB).
+template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool QOUT, bool COH, int PRE = 1, bool FULL = false>
 struct GemvRows {
     static constexpr int NS = Plan<FMT, LPR>::NS;
     static constexpr int NM = EPI == kSwiglu ? 2 : 1;
     static constexpr uint32_t kRows = T / LPR;
+    static constexpr bool kBuf = LPR == 32 && (FMT == VKML_Q4_K || FMT == VKML_Q8_0);
     RoundW<FMT, LPR> wa[B][NM], wb[B][NM];
     uint32_t item, row, r_row, l, rounds;
+    __amdgpu_buffer_rsrc_t rc[NM], rs[NM];  // kBuf: codes and scales of each matrix
+    uint32_t vq, vs;                        // kBuf: the lane's byte offsets at round 0
+
+    // Per-round byte strides of codes and scales (kBuf).
+    static constexpr uint32_t kCodeStride = FMT == VKML_Q4_K ? 256 : 512;
+    static constexpr uint32_t kScaleStride = FMT == VKML_Q4_K ? 32 : (F16S ? 32 : 64);
 
     __device__ __forceinline__ void load_batch(const GemvArgs& g, RoundW<FMT, LPR> (&w)[B][NM], uint32_t r0) {
         // Rounds past the last reload the last one (cache hits): unconditional loads.
 #pragma unroll
         for (int i = 0; i < B; ++i) {
             const uint32_t r = min(r0 + i, rounds - 1);
-            load_round<FMT, F16S, LPR>(g.b_values, g.b_scales, g.k, r_row, r, l, w[i][0]);
-            if constexpr (NM == 2) load_round<FMT, F16S, LPR>(g.b2_values, g.b2_scales, g.k, r_row, r, l, w[i][NM - 1]);
+            if constexpr (kBuf) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+                    w[i][m].q[0] = bload128(rc[m], vq, kCodeStride * r);
+                    if constexpr (FMT == VKML_Q4_K) {
+                        const uint4 h = bload128(rs[m], vs, kScaleStride * r);
+                        w[i][m].s[0] = h.x; w[i][m].s[1] = h.y; w[i][m].s[2] = h.z; w[i][m].s[3] = h.w;
+                    } else {
+                        w[i][m].s[0] = F16S ? bload16(rs[m], vs, kScaleStride * r) : bload32(rs[m], vs, kScaleStride * r);
+                    }
+                }
+            } else {
+                load_round<FMT, F16S, LPR>(g.b_values, g.b_scales, g.k, r_row, r, l, w[i][0]);
+                if constexpr (NM == 2) load_round<FMT, F16S, LPR>(g.b2_values, g.b2_scales, g.k, r_row, r, l, w[i][NM - 1]);
+            }
         }
     }
 
@@ -433,11 +493,28 @@ struct GemvRows {
         l = t % LPR;
         row = it * kRows + t / LPR;
         r_row = min(row, g.n - 1);
+        if constexpr (kBuf) {
+            const uint32_t K = g.k, R = r_row;
+            rc[0] = buffer_of(g.b_values, static_cast<uint32_t>(code_bytes<FMT>(g.n, K)));
+            rs[0] = buffer_of(g.b_scales, static_cast<uint32_t>(scale_bytes<FMT, F16S>(g.n, K)));
+            if constexpr (NM == 2) {
+                rc[1] = buffer_of(g.b2_values, static_cast<uint32_t>(code_bytes<FMT>(g.n, K)));
+                rs[1] = buffer_of(g.b2_scales, static_cast<uint32_t>(scale_bytes<FMT, F16S>(g.n, K)));
+            }
+            if constexpr (FMT == VKML_Q4_K) {
+                const uint32_t p = l / 16, hb = l % 16;  // super-block of the round, half-block in it
+                vq = R * (K / 2) + 128 * p + 32 * (hb / 4) + 16 * (hb % 2);
+                vs = (R * (K / 256) + p) * 16;
+            } else {
+                vq = R * K + 16 * l;
+                vs = (R * (K / 32) + l / 2) * (F16S ? 2 : 4);
+            }
+        }
         load_batch(g, wa, 0);
         if constexpr (PRE == 2) load_batch(g, wb, B);
     }
 
-    __device__ __forceinline__ void finish(const GemvArgs& g, const uint4* s_codes, const float* s_sum, const float* s_sa) {
+    __device__ __forceinline__ void finish(const GemvArgs& g, const uint4* s_codes, const float2* s_ss) {
 #pragma clang fp contract(off)
         const uint32_t K = g.k;
         float acc[NM][NS];
@@ -450,7 +527,7 @@ struct GemvRows {
             for (int i = 0; i < B; ++i) {
                 if (r0 + i < rounds) {
 #pragma unroll
-                    for (int m = 0; m < NM; ++m) round_terms<FMT, F16S, LPR>(w[i][m], r0 + i, l, K, s_codes, s_sum, s_sa, acc[m]);
+                    for (int m = 0; m < NM; ++m) round_terms<FMT, F16S, LPR, FULL>(w[i][m], r0 + i, l, K, s_codes, s_ss, acc[m]);
                 }
             }
         };
@@ -512,8 +589,9 @@ struct GemvRows {
     }
 };
 
-// LDS bytes stage_activation uses for K.
-__host__ __device__ constexpr uint32_t stage_bytes(uint32_t k, bool norm) { return k + k / 16 * 4 + k / 32 * 4 + (norm ? 257 * 4 : 0); }
+// LDS bytes stage_activation uses for K: the codes, then (code sum, block
+// scale) per half-block, then the norm's 257 floats.
+__host__ __device__ constexpr uint32_t stage_bytes(uint32_t k, bool norm) { return k + k / 16 * 8 + (norm ? 257 * 4 : 0); }
 
 // Stages the activation in LDS (smem, 16-byte aligned): with NORM, RMSNorm +
 // Q8_0 of g.x computed here (norm_quantize_prologue); otherwise the codes
@@ -521,38 +599,37 @@ __host__ __device__ constexpr uint32_t stage_bytes(uint32_t k, bool norm) { retu
 template <uint32_t T, bool NORM, bool COH>
 __device__ __forceinline__ void stage_activation(const GemvArgs& g, uint4* smem) {
     const uint32_t K = g.k;
-    uint4* s_codes = smem;                                   // K / 16 half-blocks of codes
-    float* s_sum = reinterpret_cast<float*>(smem + K / 16);  // each half-block's code sum
-    float* s_sa = s_sum + K / 16;                            // each block's activation scale
+    uint4* s_codes = smem;                                     // K / 16 half-blocks of codes
+    float2* s_ss = reinterpret_cast<float2*>(smem + K / 16);   // each half-block's (code sum, block scale)
     const uint32_t halves = K / 16, t = thread_index();
     if constexpr (NORM) {
         NormLoads<T> nl;
         norm_loads<T, COH>(g.x, g.norm_weight, K, nl);
-        float* s_red = s_sa + K / 32;  // 257 floats
-        norm_quantize_prologue<T>(nl, g.eps, K, s_codes, s_sum, s_sa, s_red);
+        float* s_red = reinterpret_cast<float*>(s_ss + K / 16);  // 257 floats
+        norm_quantize_prologue<T>(nl, g.eps, K, s_codes, s_ss, s_red);
     } else {
         for (uint32_t h0 = t; h0 < halves; h0 += 4 * T) {
             uint4 c[4];
+            float sa[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t h = h0 + i * T;
                 c[i] = h < halves ? ld_u128<COH>(g.a_values + h) : make_uint4(0, 0, 0, 0);
+                sa[i] = h < halves ? ld_f32<COH>(g.a_scales + h / 2) : 0.0f;
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t h = h0 + i * T;
                 if (h < halves) {
                     s_codes[h] = c[i];
-                    s_sum[h] = static_cast<float>(byte_sum(c[i]));
+                    s_ss[h] = make_float2(static_cast<float>(byte_sum(c[i])), sa[i]);
                 }
             }
         }
-        for (uint32_t b = t; b < K / 32; b += T) s_sa[b] = ld_f32<COH>(g.a_scales + b);
     }
     __syncthreads();
 }
 
-__device__ __forceinline__ const float* staged_sums(const uint4* smem, uint32_t k) { return reinterpret_cast<const float*>(smem + k / 16); }
-__device__ __forceinline__ const float* staged_scales(const uint4* smem, uint32_t k) { return staged_sums(smem, k) + k / 16; }
+__device__ __forceinline__ const float2* staged_ss(const uint4* smem, uint32_t k) { return reinterpret_cast<const float2*>(smem + k / 16); }
 
 }  // namespace vkml::gemv

@@ -248,10 +248,9 @@ __device__ __forceinline__ void gemv_phase(const GemvArgs& g, Rows& rows, uint32
     const uint32_t items = items_of<Rows>(g);
     if (wg >= items) return;
     stage_activation<kT, NORM, false>(g, pool);
-    const float* s_sum = staged_sums(pool, g.k);
-    const float* s_sa = staged_scales(pool, g.k);
+    const float2* s_ss = staged_ss(pool, g.k);
     for (uint32_t it = wg;;) {
-        rows.finish(g, pool, s_sum, s_sa);
+        rows.finish(g, pool, s_ss);
         it += G;
         if (it >= items) break;
         rows.start(g, it);

@@ -16,13 +16,13 @@ using namespace vkml::gemv;
 
 namespace {
 
-template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool NORM, bool QOUT>
+template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool NORM, bool QOUT, bool FULL>
 __global__ void __launch_bounds__(T) k_gemv_dot(GemvArgs g) {
     extern __shared__ uint4 smem[];
-    GemvRows<FMT, F16S, LPR, EPI, B, T, QOUT, false> rows;
+    GemvRows<FMT, F16S, LPR, EPI, B, T, QOUT, false, 1, FULL> rows;
     rows.start(g, blockIdx.x);  // the first batch of weights is in flight while the activation is staged
     stage_activation<T, NORM, false>(g, smem);
-    rows.finish(g, smem, staged_sums(smem, g.k), staged_scales(smem, g.k));
+    rows.finish(g, smem, staged_ss(smem, g.k));
 }
 
 template <int FMT, bool F16S, int LPR, int EPI, bool NORM, bool QOUT>
@@ -32,7 +32,12 @@ int launch(const GemvArgs& g, const char* label) {
     const dim3 grid((g.n + T / LPR - 1) / (T / LPR));
     const size_t lds = stage_bytes(g.k, NORM);
     vkml::abi::ProfileScope prof(label);
-    hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT>), grid, dim3(T), lds, vkml::abi::stream(), g);
+    // Whole rounds (K a multiple of 512) need no per-lane tail check; only
+    // the 32-lane kernels are built both ways.
+    if (LPR == 32 && g.k % 512 == 0)
+        hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT, LPR == 32>), grid, dim3(T), lds, vkml::abi::stream(), g);
+    else
+        hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT, false>), grid, dim3(T), lds, vkml::abi::stream(), g);
     return vkml::abi::check_launch(label);
 }
 
@@ -44,7 +49,9 @@ int dispatch(const GemvArgs& g, const char* label) {
     // of a 7B model: measured 13-18% faster than 16 lanes).
     const uint64_t simds = 4ull * std::max<uint32_t>(vkml::abi::compute_units(), 1);
     if constexpr ((FMT == VKML_Q4_K || FMT == VKML_Q8_0) && !QOUT) {
-        if ((g.n + 3) / 4 < 2 * simds) return launch<FMT, F16S, 32, EPI, NORM, QOUT>(g, label);
+        // (buffer loads address a matrix under 4 GiB)
+        const bool fits = code_bytes<FMT>(g.n, g.k) < (1ull << 32) && scale_bytes<FMT, F16S>(g.n, g.k) < (1ull << 32);
+        if ((g.n + 3) / 4 < 2 * simds && fits) return launch<FMT, F16S, 32, EPI, NORM, QOUT>(g, label);
     }
     if ((g.n + 7) / 8 < simds) return launch<FMT, F16S, 16, EPI, NORM, QOUT>(g, label);
     return launch<FMT, F16S, 8, EPI, NORM, QOUT>(g, label);

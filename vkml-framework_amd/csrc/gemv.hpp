@@ -445,15 +445,15 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
 // the same launch; g.out may then be null (no f32 output). FULL: K a
 // multiple of 512 (every round whole).
 //
-// At 32 lanes a row (q4_K, q8_0) the weights are read with buffer loads: a
-// lane's byte offset into the matrix is computed once per item, and each
-// round adds a scalar offset (the matrix must be under 4 GiB).
+// q4_K and q8_0 weights are read with buffer loads: a lane's byte offset
+// into the matrix is computed once per item, and each round adds a scalar
+// offset (the matrix must be under 4 GiB).
 template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool QOUT, bool COH, int PRE = 1, bool FULL = false>
 struct GemvRows {
     static constexpr int NS = Plan<FMT, LPR>::NS;
     static constexpr int NM = EPI == kSwiglu ? 2 : 1;
     static constexpr uint32_t kRows = T / LPR;
-    static constexpr bool kBuf = LPR == 32 && (FMT == VKML_Q4_K || FMT == VKML_Q8_0);
+    static constexpr bool kBuf = FMT == VKML_Q4_K || FMT == VKML_Q8_0;
     RoundW<FMT, LPR> wa[B][NM], wb[B][NM];
     uint32_t item, row, r_row, l, rounds;
     __amdgpu_buffer_rsrc_t rc[NM], rs[NM];  // kBuf: codes and scales of each matrix
@@ -463,6 +463,16 @@ struct GemvRows {
     static constexpr uint32_t kCodeStride = FMT == VKML_Q4_K ? 256 : 512;
     static constexpr uint32_t kScaleStride = FMT == VKML_Q4_K ? 32 : (F16S ? 32 : 64);
 
+    // Byte distance from slot 0's code / scale load to slot e's (kBuf): q4_K
+    // at 8 lanes loads bytes 32j .. 32j + 31 as two 16-byte loads; q8_0 slot e
+    // is half-block acc_index(l, e) = acc_index(l, 0) + (32 / LPR) ... apart.
+    static constexpr uint32_t code_delta(int e) {
+        return FMT == VKML_Q4_K ? 16u * e : 16u * (acc_index<FMT, LPR>(0, e) - acc_index<FMT, LPR>(0, 0));
+    }
+    static constexpr uint32_t scale_delta(int e) {
+        return (F16S ? 2u : 4u) * ((acc_index<FMT, LPR>(0, e) - acc_index<FMT, LPR>(0, 0)) / 2);
+    }
+
     __device__ __forceinline__ void load_batch(const GemvArgs& g, RoundW<FMT, LPR> (&w)[B][NM], uint32_t r0) {
         // Rounds past the last reload the last one (cache hits): unconditional loads.
 #pragma unroll
@@ -471,12 +481,16 @@ struct GemvRows {
             if constexpr (kBuf) {
 #pragma unroll
                 for (int m = 0; m < NM; ++m) {
-                    w[i][m].q[0] = bload128(rc[m], vq, kCodeStride * r);
+#pragma unroll
+                    for (int e = 0; e < Plan<FMT, LPR>::NQ; ++e) w[i][m].q[e] = bload128(rc[m], vq + code_delta(e), kCodeStride * r);
                     if constexpr (FMT == VKML_Q4_K) {
                         const uint4 h = bload128(rs[m], vs, kScaleStride * r);
                         w[i][m].s[0] = h.x; w[i][m].s[1] = h.y; w[i][m].s[2] = h.z; w[i][m].s[3] = h.w;
                     } else {
-                        w[i][m].s[0] = F16S ? bload16(rs[m], vs, kScaleStride * r) : bload32(rs[m], vs, kScaleStride * r);
+#pragma unroll
+                        for (int e = 0; e < NS; ++e)
+                            w[i][m].s[e] = F16S ? bload16(rs[m], vs + scale_delta(e), kScaleStride * r)
+                                                : bload32(rs[m], vs + scale_delta(e), kScaleStride * r);
                     }
                 }
             } else {
@@ -502,12 +516,15 @@ struct GemvRows {
                 rs[1] = buffer_of(g.b2_scales, static_cast<uint32_t>(scale_bytes<FMT, F16S>(g.n, K)));
             }
             if constexpr (FMT == VKML_Q4_K) {
-                const uint32_t p = l / 16, hb = l % 16;  // super-block of the round, half-block in it
-                vq = R * (K / 2) + 128 * p + 32 * (hb / 4) + 16 * (hb % 2);
+                // the lane's super-block of the round and its first code byte in it
+                const uint32_t p = LPR == 32 ? l / 16 : LPR == 16 ? l / 8 : l / 4;
+                const uint32_t off = LPR == 32 ? 32 * ((l % 16) / 4) + 16 * (l % 2) : LPR == 16 ? 16 * (l % 8) : 32 * (l % 4);
+                vq = R * (K / 2) + 128 * p + off;
                 vs = (R * (K / 256) + p) * 16;
             } else {
-                vq = R * K + 16 * l;
-                vs = (R * (K / 32) + l / 2) * (F16S ? 2 : 4);
+                const uint32_t hb = acc_index<FMT, LPR>(l, 0);  // slot 0's half-block of the round
+                vq = R * K + 16 * hb;
+                vs = (R * (K / 32) + hb / 2) * (F16S ? 2 : 4);
             }
         }
         load_batch(g, wa, 0);

@@ -32,10 +32,11 @@ int launch(const GemvArgs& g, const char* label) {
     const dim3 grid((g.n + T / LPR - 1) / (T / LPR));
     const size_t lds = stage_bytes(g.k, NORM);
     vkml::abi::ProfileScope prof(label);
-    // Whole rounds (K a multiple of 512) need no per-lane tail check; only
-    // the 32-lane kernels are built both ways.
-    if (LPR == 32 && g.k % 512 == 0)
-        hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT, LPR == 32>), grid, dim3(T), lds, vkml::abi::stream(), g);
+    // Whole rounds (K a multiple of 512) need no per-lane tail check (q4_K
+    // and q8_0 kernels are built both ways).
+    constexpr bool kWhole = FMT == VKML_Q4_K || FMT == VKML_Q8_0;
+    if (kWhole && g.k % 512 == 0)
+        hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT, kWhole>), grid, dim3(T), lds, vkml::abi::stream(), g);
     else
         hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT, false>), grid, dim3(T), lds, vkml::abi::stream(), g);
     return vkml::abi::check_launch(label);
@@ -48,10 +49,13 @@ int dispatch(const GemvArgs& g, const char* label) {
     // arithmetic overlaps another's loads (the N = 4096 and 6144 projections
     // of a 7B model: measured 13-18% faster than 16 lanes).
     const uint64_t simds = 4ull * std::max<uint32_t>(vkml::abi::compute_units(), 1);
-    if constexpr ((FMT == VKML_Q4_K || FMT == VKML_Q8_0) && !QOUT) {
-        // (buffer loads address a matrix under 4 GiB)
-        const bool fits = code_bytes<FMT>(g.n, g.k) < (1ull << 32) && scale_bytes<FMT, F16S>(g.n, g.k) < (1ull << 32);
-        if ((g.n + 3) / 4 < 2 * simds && fits) return launch<FMT, F16S, 32, EPI, NORM, QOUT>(g, label);
+    if constexpr (FMT == VKML_Q4_K || FMT == VKML_Q8_0) {
+        // (their buffer loads address a matrix under 4 GiB)
+        if (code_bytes<FMT>(g.n, g.k) >= (1ull << 32) || scale_bytes<FMT, F16S>(g.n, g.k) >= (1ull << 32))
+            return vkml::abi::fail(VKML_ERROR_UNSUPPORTED, std::string(label) + ": a matrix of 4 GiB or more");
+        if constexpr (!QOUT) {
+            if ((g.n + 3) / 4 < 2 * simds) return launch<FMT, F16S, 32, EPI, NORM, QOUT>(g, label);
+        }
     }
     if ((g.n + 7) / 8 < simds) return launch<FMT, F16S, 16, EPI, NORM, QOUT>(g, label);
     return launch<FMT, F16S, 8, EPI, NORM, QOUT>(g, label);

@@ -350,26 +350,30 @@ enum { kStore = 0, kAdd = 1, kSwiglu = 2 };
 // of x in rms_norm.comp's order at its workgroup width of 256 (invocation v
 // sums x[c]^2 over c = v, v + 256, ...; then the halving tree), emulated by
 // T threads; then y = x * scale * w and Q8_0 per 32 values
-// (quantize.comp:100-111), written to LDS as the activation codes,
-// half-block code sums and block scales: vkml_rms_norm_quantize's results
-// bit for bit. K <= 4096 and T >= 128, so a thread owns at most one 32-value
-// block; its block of x and w and its strided elements for the sum are all
-// loaded at once, into registers: one round trip.
+// (quantize.comp:100-111), written to LDS as the activation codes and each
+// half-block's (code sum, block scale): vkml_rms_norm_quantize's results bit
+// for bit. K <= 4096 and T >= 128. Every load is coalesced and issued at
+// once, into registers: the strided elements of the sum (lanes take
+// consecutive c), and x and w four values a lane (lane q of the workgroup
+// takes values 4q .. 4q + 3, so a 32-value block is 8 consecutive lanes,
+// whose absmax is a shuffle reduction among them).
 template <uint32_t T>
 struct NormLoads {
     static constexpr uint32_t V = T >= 256 ? 1 : 256 / T;  // invocations per thread (t, t + T, ... below 256)
     static constexpr uint32_t kMaxPer = 4096 / 256;        // elements per invocation at K <= 4096
-    float4 xb[8], wb[8];                                   // the thread's 32-value block of x and w
+    static constexpr uint32_t Q4 = 4096 / 4 / T;           // float4s of x (and w) per thread
+    float4 xq[Q4], wq[Q4];                                 // x and w at float4 t + T i
     float xv[V][kMaxPer];                                  // its invocations' strided elements
 };
 
 template <uint32_t T, bool COH>
 __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint32_t K, NormLoads<T>& r) {
-    const uint32_t t = thread_index(), blk = t < K / 32 ? t : 0;
+    const uint32_t t = thread_index();
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-        r.xb[i] = ld_f32x4<COH>(reinterpret_cast<const float4*>(x) + 8 * blk + i);
-        r.wb[i] = ldg(reinterpret_cast<const float4*>(w) + 8 * blk + i);
+    for (uint32_t i = 0; i < NormLoads<T>::Q4; ++i) {
+        const uint32_t q = min(t + T * i, K / 4 - 1);
+        r.xq[i] = ld_f32x4<COH>(reinterpret_cast<const float4*>(x) + q);
+        r.wq[i] = ldg(reinterpret_cast<const float4*>(w) + q);
     }
 #pragma unroll
     for (uint32_t v = 0; v < NormLoads<T>::V; ++v)
@@ -380,7 +384,7 @@ __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint3
 template <uint32_t T>
 __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float2* s_ss, float* s_red) {
 #pragma clang fp contract(off)
-    static_assert(T >= 128, "workgroup width");
+    static_assert(T >= 128 && T % 64 == 0, "workgroup width");
     const uint32_t t = thread_index();
 #pragma unroll
     for (uint32_t v = 0; v < NormLoads<T>::V; ++v) {
@@ -402,36 +406,33 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
         if (t == 0) s_red[256] = v;
     }
     __syncthreads();
-    if (t >= K / 32) return;
-    const uint32_t blk = t;
     const float scale = 1.0f / sqrtf(s_red[256] / static_cast<float>(K) + eps);
-    float y[32];
-    float absmax = 0.0f;
+    uint32_t* s_words = reinterpret_cast<uint32_t*>(s_codes);
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-        const float xs[4] = {r.xb[i].x, r.xb[i].y, r.xb[i].z, r.xb[i].w}, ws[4] = {r.wb[i].x, r.wb[i].y, r.wb[i].z, r.wb[i].w};
+    for (uint32_t i = 0; i < NormLoads<T>::Q4; ++i) {
+        const uint32_t q = t + T * i;  // values 4q .. 4q + 3: block q / 8, half-block q / 4
+        const float xs[4] = {r.xq[i].x, r.xq[i].y, r.xq[i].z, r.xq[i].w}, ws[4] = {r.wq[i].x, r.wq[i].y, r.wq[i].z, r.wq[i].w};
+        float y[4];
+        float absmax = 0.0f;
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e) {
-            y[4 * i + e] = xs[e] * scale * ws[e];
-            absmax = fmaxf(absmax, fabsf(y[4 * i + e]));
+            y[e] = xs[e] * scale * ws[e];
+            absmax = fmaxf(absmax, fabsf(y[e]));
+        }
+        absmax = group_max<8>(absmax);  // the block's 8 lanes (T is a multiple of 8)
+        const float d = absmax / 127.0f;
+        const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+        const uint32_t word = (static_cast<uint32_t>(quant_code(y[0], inv)) & 0xFFu) |
+                              ((static_cast<uint32_t>(quant_code(y[1], inv)) & 0xFFu) << 8) |
+                              ((static_cast<uint32_t>(quant_code(y[2], inv)) & 0xFFu) << 16) |
+                              (static_cast<uint32_t>(quant_code(y[3], inv)) << 24);
+        const int part = dot4(word, 0x01010101u, 0);
+        const int sum = part + __shfl_xor(part, 1, kWave) + __shfl_xor(part, 2, kWave) + __shfl_xor(part, 3, kWave);
+        if (q < K / 4) {
+            s_words[q] = word;
+            if (q % 4 == 0) s_ss[q / 4] = make_float2(static_cast<float>(sum), d);
         }
     }
-    const float d = absmax / 127.0f;
-    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-    uint32_t words[8];
-#pragma unroll
-    for (uint32_t q = 0; q < 8; ++q) {
-        words[q] = (static_cast<uint32_t>(quant_code(y[4 * q], inv)) & 0xFFu) |
-                   ((static_cast<uint32_t>(quant_code(y[4 * q + 1], inv)) & 0xFFu) << 8) |
-                   ((static_cast<uint32_t>(quant_code(y[4 * q + 2], inv)) & 0xFFu) << 16) |
-                   (static_cast<uint32_t>(quant_code(y[4 * q + 3], inv)) << 24);
-    }
-    const uint4 lo = make_uint4(words[0], words[1], words[2], words[3]);
-    const uint4 hi = make_uint4(words[4], words[5], words[6], words[7]);
-    s_codes[2 * blk] = lo;
-    s_codes[2 * blk + 1] = hi;
-    s_ss[2 * blk] = make_float2(static_cast<float>(byte_sum(lo)), d);
-    s_ss[2 * blk + 1] = make_float2(static_cast<float>(byte_sum(hi)), d);
 }
 
 

@@ -289,44 +289,29 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     }
     __syncthreads();
 
-    // V: chain (head, element d, slice sl) over the slice's keys in order. A
-    // thread carries two neighbouring elements (one 32-bit V read a key) and
-    // reads the weights four keys at a time; 32 keys' reads are in flight
-    // together, and whole chunks need no per-key guard.
+    // V: chain (head, element d, slice sl) over the slice's keys in order,
+    // one chain a thread (HPW * slices * HD chains: at head_dim 128 with two
+    // heads a workgroup, one for each of its 256 threads, so every wave
+    // works); the weights are read four keys at a time (one address for the
+    // whole wave), KB keys' V reads are in flight together, and whole chunks
+    // need no per-key guard.
     constexpr uint32_t slices = HD >= kChunk ? 1 : kChunk / HD;
-    constexpr uint32_t NP = HD / 2;  // element pairs
-    const auto v_pair = [&](uint32_t key, uint32_t dp, float& x, float& y) {
+    const auto v_elem = [&](uint32_t key, uint32_t d) -> float {
         if constexpr (kStageV) {
-            if constexpr (F16) {
-                const uint32_t w = reinterpret_cast<const uint32_t*>(sm.v)[key * NP + dp];
-                x = f16_bits_to_float(w & 0xFFFFu);
-                y = f16_bits_to_float(w >> 16);
-            } else {
-                const float2 w = reinterpret_cast<const float2*>(sm.v)[key * NP + dp];
-                x = w.x;
-                y = w.y;
-            }
+            if constexpr (F16) return f16_bits_to_float(reinterpret_cast<const uint16_t*>(sm.v)[key * HD + d]);
+            else return reinterpret_cast<const float*>(sm.v)[key * HD + d];
         } else {
-            if (holds_new && key == n - 1) {
-                x = F16 ? f16_bits_to_float(sm.vnew[2 * dp]) : __uint_as_float(sm.vnew[2 * dp]);
-                y = F16 ? f16_bits_to_float(sm.vnew[2 * dp + 1]) : __uint_as_float(sm.vnew[2 * dp + 1]);
-            } else if constexpr (F16) {
-                const uint32_t w = ldg(static_cast<const uint32_t*>(a.v_cache) + (row_of(key) * HD) / 2 + dp);
-                x = f16_bits_to_float(w & 0xFFFFu);
-                y = f16_bits_to_float(w >> 16);
-            } else {
-                const float2 w = ldg(static_cast<const float2*>(a.v_cache) + (row_of(key) * HD) / 2 + dp);
-                x = w.x;
-                y = w.y;
-            }
+            if (holds_new && key == n - 1) return F16 ? f16_bits_to_float(sm.vnew[d]) : __uint_as_float(sm.vnew[d]);
+            if constexpr (F16) return f16_bits_to_float(ldg(static_cast<const uint16_t*>(a.v_cache) + row_of(key) * HD + d));
+            else return ldg(static_cast<const float*>(a.v_cache) + row_of(key) * HD + d);
         }
     };
-    for (uint32_t c = t; c < HPW * slices * NP; c += kThreads) {
-        const uint32_t dp = c % NP, sl = (c / NP) % slices, h = c / (NP * slices);
+    for (uint32_t c = t; c < HPW * slices * HD; c += kThreads) {
+        const uint32_t d = c % HD, sl = (c / HD) % slices, h = c / (HD * slices);
         const uint32_t keys = n > sl ? (n - sl + slices - 1) / slices : 0;  // this slice's keys: sl, sl + slices, ...
-        float o0 = 0.0f, o1 = 0.0f;
+        float o = 0.0f;
         for (uint32_t j0 = 0; j0 < keys; j0 += KB) {
-            float w[KB], x[KB], y[KB];
+            float w[KB], x[KB];
             const float4* wp = reinterpret_cast<const float4*>(&sm.p[h][slices * j0]);
 #pragma unroll
             for (uint32_t m = 0; m < KB * slices / 4; ++m) {
@@ -339,30 +324,20 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
                 }
             }
 #pragma unroll
-            for (uint32_t jj = 0; jj < KB; ++jj) v_pair(min(sl + slices * (j0 + jj), n - 1), dp, x[jj], y[jj]);
+            for (uint32_t jj = 0; jj < KB; ++jj) x[jj] = v_elem(min(sl + slices * (j0 + jj), n - 1), d);
             if (j0 + KB <= keys) {
 #pragma unroll
-                for (uint32_t jj = 0; jj < KB; ++jj) {
-                    o0 += w[jj] * x[jj];
-                    o1 += w[jj] * y[jj];
-                }
+                for (uint32_t jj = 0; jj < KB; ++jj) o += w[jj] * x[jj];
             } else {
 #pragma unroll
-                for (uint32_t jj = 0; jj < KB; ++jj) {
-                    if (j0 + jj < keys) {
-                        o0 += w[jj] * x[jj];
-                        o1 += w[jj] * y[jj];
-                    }
-                }
+                for (uint32_t jj = 0; jj < KB; ++jj)
+                    if (j0 + jj < keys) o += w[jj] * x[jj];
             }
         }
         if constexpr (HD > kChunk) {
-            // heads wider than the reference's workgroup: no slice sum
-            st_f32<COH>(a.partial + stats_at(h) * HD + 2 * dp, o0);
-            st_f32<COH>(a.partial + stats_at(h) * HD + 2 * dp + 1, o1);
+            st_f32<COH>(a.partial + stats_at(h) * HD + d, o);  // heads wider than the reference's workgroup: no slice sum
         } else {
-            sm.red[h][sl * HD + 2 * dp] = o0;
-            sm.red[h][sl * HD + 2 * dp + 1] = o1;
+            sm.red[h][sl * HD + d] = o;
         }
     }
     if constexpr (HD <= kChunk) {

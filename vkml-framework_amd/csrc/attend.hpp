@@ -323,8 +323,13 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
                     w[2 * m + 1] = sl ? q.w : q.z;
                 }
             }
+            if (n == kChunk) {  // a whole chunk: no key past the last
 #pragma unroll
-            for (uint32_t jj = 0; jj < KB; ++jj) x[jj] = v_elem(min(sl + slices * (j0 + jj), n - 1), d);
+                for (uint32_t jj = 0; jj < KB; ++jj) x[jj] = v_elem(sl + slices * (j0 + jj), d);
+            } else {
+#pragma unroll
+                for (uint32_t jj = 0; jj < KB; ++jj) x[jj] = v_elem(min(sl + slices * (j0 + jj), n - 1), d);
+            }
             if (j0 + KB <= keys) {
 #pragma unroll
                 for (uint32_t jj = 0; jj < KB; ++jj) o += w[jj] * x[jj];

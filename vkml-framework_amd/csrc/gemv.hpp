@@ -211,27 +211,59 @@ __device__ __forceinline__ void q4k_sub_scales(const uint32_t (&h)[4], uint32_t 
 
 // The same for sub-block j alone (0 .. 7): the 6-bit scale and min of the
 // reference's layout (bytes j, j + 4 of the 12; for j >= 4 their high bits
-// in bytes j - 4, j and the low nibbles in byte j + 4).
-__device__ __forceinline__ void q4k_sub_scale(const uint32_t (&h)[4], uint32_t j, float& s, float& o) {
-    const uint32_t sh = 8 * (j % 4);
-    const uint32_t b1 = (h[1] >> sh) & 0xFFu, b2 = (h[2] >> sh) & 0xFFu, b3 = (h[3] >> sh) & 0xFFu;
-    const uint32_t sc = j < 4 ? b1 & 63u : (b3 & 15u) | ((b1 >> 6) << 4);
-    const uint32_t mn = j < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
+// in bytes j - 4, j and the low nibbles in byte j + 4). A lane's j is fixed,
+// so the bit-field positions are computed once (Q4kField) and each round
+// costs two selects and four field extracts.
+struct Q4kField {
+    uint32_t hi;                   // j >= 4: low bits from word 3
+    uint32_t pos_sc, pos_mn, wlo;  // first field: position in its word (scale, min) and width
+    uint32_t pos_top, wtop;        // j >= 4: the two high bits in words 1 and 2 (width 0 otherwise)
+};
+__device__ __forceinline__ Q4kField q4k_field(uint32_t j) {
+    const uint32_t b = 8 * (j % 4);
+    if (j < 4) return {0u, b, b, 6u, 0u, 0u};
+    return {1u, b, b + 4, 4u, b + 6, 2u};
+}
+__device__ __forceinline__ void q4k_sub_scale(const uint32_t (&h)[4], const Q4kField& f, float& s, float& o) {
+    const uint32_t wsc = f.hi ? h[3] : h[1], wmn = f.hi ? h[3] : h[2];
+    const uint32_t sc = __builtin_amdgcn_ubfe(wsc, f.pos_sc, f.wlo) | (__builtin_amdgcn_ubfe(h[1], f.pos_top, f.wtop) << 4);
+    const uint32_t mn = __builtin_amdgcn_ubfe(wmn, f.pos_mn, f.wlo) | (__builtin_amdgcn_ubfe(h[2], f.pos_top, f.wtop) << 4);
     const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h[0] & 0xFFFFu));
     const _Float16 nd = -__builtin_bit_cast(_Float16, static_cast<uint16_t>(h[0] >> 16));
-    s = static_cast<float>(d * static_cast<_Float16>(sc));
-    o = static_cast<float>(nd * static_cast<_Float16>(mn));
+    s = static_cast<float>(d * static_cast<_Float16>(static_cast<uint16_t>(sc)));
+    o = static_cast<float>(nd * static_cast<_Float16>(static_cast<uint16_t>(mn)));
+}
+
+// One lane's activation operands of one round: each slot's 16 codes and its
+// half-block's (code sum, block scale), read from LDS before the round's
+// arithmetic so a batch's reads are in flight together.
+template <int FMT, int LPR>
+struct RoundA {
+    uint4 a[Plan<FMT, LPR>::NS];
+    float2 ss[Plan<FMT, LPR>::NS];
+};
+
+template <int FMT, int LPR, bool FULL>
+__device__ __forceinline__ void fetch_act(uint32_t r, uint32_t l, uint32_t K, const uint4* s_codes, const float2* s_ss,
+                                          RoundA<FMT, LPR>& x) {
+#pragma unroll
+    for (int e = 0; e < Plan<FMT, LPR>::NS; ++e) {
+        const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
+        const bool live = FULL || hb < K / 16;
+        x.a[e] = live ? s_codes[hb] : make_uint4(0, 0, 0, 0);
+        x.ss[e] = live ? s_ss[hb] : make_float2(0.0f, 0.0f);
+    }
 }
 
 // Adds one lane's terms of round r to acc[0 .. NS) with the reference's
 // expressions (gemv_dot.comp:112,114): q8_0 / q4_0 float(d) * (scale * sa);
 // q4_1 and q4_K sa * (float(d) * scale + float(sum) * offset). The
 // activation codes, and each half-block's code sum with its block's scale,
-// come from LDS. FULL: every half-block of the round is in the row (K a
-// multiple of 512).
+// come from LDS (fetch_act). FULL: every half-block of the round is in the
+// row (K a multiple of 512). jf: the lane's q4_K sub-block fields (32 lanes).
 template <int FMT, bool F16S, int LPR, bool FULL = false>
-__device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t r, uint32_t l, uint32_t K,
-                                            const uint4* s_codes, const float2* s_ss, float (&acc)[Plan<FMT, LPR>::NS]) {
+__device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, const RoundA<FMT, LPR>& x, uint32_t r, uint32_t l,
+                                            uint32_t K, const Q4kField& jf, float (&acc)[Plan<FMT, LPR>::NS]) {
 #pragma clang fp contract(off)
     constexpr int NS = Plan<FMT, LPR>::NS;
     const uint32_t halves = K / 16;
@@ -241,9 +273,8 @@ __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t 
     bool live[NS];
 #pragma unroll
     for (int e = 0; e < NS; ++e) {
-        const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
-        live[e] = FULL || hb < halves;
-        a[e] = live[e] ? s_codes[hb] : make_uint4(0, 0, 0, 0);
+        live[e] = FULL || 32 * r + acc_index<FMT, LPR>(l, e) < halves;
+        a[e] = x.a[e];
     }
     if constexpr (FMT == VKML_Q8_0) {
 #pragma unroll
@@ -254,8 +285,8 @@ __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t 
     } else if constexpr (FMT == VKML_Q4_K && LPR == 32) {
         // Half-block hb of the super-block is in sub-block hb / 2: the low
         // nibbles of its bytes for an even sub-block, the high for an odd one.
-        const uint32_t j = (l % 16) / 2, sh = 4 * (j % 2);
-        q4k_sub_scale(w.s, j, s[0], o[0]);
+        const uint32_t sh = 4 * ((l / 2) % 2);
+        q4k_sub_scale(w.s, jf, s[0], o[0]);
         const uint4 q = w.q[0];
         d[0] = half_dot((q.x >> sh) & kLow, (q.y >> sh) & kLow, (q.z >> sh) & kLow, (q.w >> sh) & kLow, a[0]);
     } else if constexpr (FMT == VKML_Q4_K) {
@@ -295,8 +326,7 @@ __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, uint32_t 
 #pragma unroll
     for (int e = 0; e < NS; ++e) {
         if (!live[e]) continue;
-        const uint32_t hb = 32 * r + acc_index<FMT, LPR>(l, e);
-        const float2 ss = s_ss[hb];  // (code sum, block scale)
+        const float2 ss = x.ss[e];  // (code sum, block scale)
         const float sa = ss.y;
         if constexpr (FMT == VKML_Q4_1 || FMT == VKML_Q4_K) {
             acc[e] += sa * (static_cast<float>(d[e]) * s[e] + ss.x * o[e]);
@@ -444,7 +474,8 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
 // in flight. With COH, the outputs (and the Q8_0 output) are stored
 // write-through, coherently across XCDs, for readers in other workgroups of
 // the same launch; g.out may then be null (no f32 output). FULL: K a
-// multiple of 512 (every round whole).
+// multiple of 1024 B (every round whole, and the rounds whole pairs of
+// batches, so no round is skipped).
 //
 // q4_K and q8_0 weights are read with buffer loads: a lane's byte offset
 // into the matrix is computed once per item, and each round adds a scalar
@@ -540,12 +571,26 @@ struct GemvRows {
         for (int m = 0; m < NM; ++m)
 #pragma unroll
             for (int e = 0; e < NS; ++e) acc[m][e] = 0.0f;
+        const Q4kField jf = q4k_field((l % 16) / 2);
         const auto sum_batch = [&](const RoundW<FMT, LPR> (&w)[B][NM], uint32_t r0) {
+            if constexpr (FULL && LPR == 32) {
+                // one slot a lane: the batch's activation reads fit in registers
+                RoundA<FMT, LPR> x[B];
 #pragma unroll
-            for (int i = 0; i < B; ++i) {
-                if (r0 + i < rounds) {
+                for (int i = 0; i < B; ++i) fetch_act<FMT, LPR, true>(r0 + i, l, K, s_codes, s_ss, x[i]);
 #pragma unroll
-                    for (int m = 0; m < NM; ++m) round_terms<FMT, F16S, LPR, FULL>(w[i][m], r0 + i, l, K, s_codes, s_ss, acc[m]);
+                for (int i = 0; i < B; ++i)
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) round_terms<FMT, F16S, LPR, true>(w[i][m], x[i], r0 + i, l, K, jf, acc[m]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < B; ++i) {
+                    if (r0 + i < rounds) {
+                        RoundA<FMT, LPR> x;
+                        fetch_act<FMT, LPR, FULL>(r0 + i, l, K, s_codes, s_ss, x);
+#pragma unroll
+                        for (int m = 0; m < NM; ++m) round_terms<FMT, F16S, LPR, FULL>(w[i][m], x, r0 + i, l, K, jf, acc[m]);
+                    }
                 }
             }
         };
@@ -562,10 +607,15 @@ struct GemvRows {
             sum_batch(wa, r0);
             sum_batch(wb, r0 + B);
         } else {
+            // (the scheduling barriers keep each batch's loads issued before
+            // the arithmetic on the previous batch, which would otherwise be
+            // hoisted above them together with its wait for the loads)
             for (uint32_t r0 = 0; r0 < rounds; r0 += 2 * B) {
                 load_batch(g, wb, r0 + B);
+                __builtin_amdgcn_sched_barrier(0);
                 sum_batch(wa, r0);
                 load_batch(g, wa, r0 + 2 * B);
+                __builtin_amdgcn_sched_barrier(0);
                 sum_batch(wb, r0 + B);
             }
         }

@@ -32,10 +32,11 @@ int launch(const GemvArgs& g, const char* label) {
     const dim3 grid((g.n + T / LPR - 1) / (T / LPR));
     const size_t lds = stage_bytes(g.k, NORM);
     vkml::abi::ProfileScope prof(label);
-    // Whole rounds (K a multiple of 512) need no per-lane tail check (q4_K
-    // and q8_0 kernels are built both ways).
+    // Whole pairs of whole batches (K a multiple of 1024 B) need no per-lane
+    // tail check and no per-round test (q4_K and q8_0 kernels are built both
+    // ways).
     constexpr bool kWhole = FMT == VKML_Q4_K || FMT == VKML_Q8_0;
-    if (kWhole && g.k % 512 == 0)
+    if (kWhole && g.k % (1024 * B) == 0)
         hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT, kWhole>), grid, dim3(T), lds, vkml::abi::stream(), g);
     else
         hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT, false>), grid, dim3(T), lds, vkml::abi::stream(), g);

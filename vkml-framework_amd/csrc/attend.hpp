@@ -13,7 +13,8 @@
 // vk_expf, which the CPU oracle shares.
 //
 // Within a chunk item every load is issued before any is used: K into
-// registers (four lanes a key, as the reference splits it), V into LDS. In a
+// registers (four lanes a key, as the reference splits it), V into
+// registers and, once the scores are done, LDS. In a
 // decode step the item also rotates q and the new key (RoPE) and appends the
 // new key and value to the caches, the work of rope + cast + write_rows in
 // llama.cpp:320-355: the item whose chunk holds the new position computes
@@ -140,6 +141,46 @@ __device__ __forceinline__ void attend_chunk_load(const ChunkArgs& a, uint32_t c
     }
 }
 
+// The item's query operands, loaded by attend_q_load: in a step, per
+// rotation item (a query pair, or the new key's pair with its value pair)
+// the pair and its cos/sin; otherwise q itself. Loaded before the item's K
+// and V where q is ready by then, so that waiting for them does not wait
+// for K and V.
+template <int HD, int HPW>
+struct QLoads {
+    static constexpr uint32_t kRot = (HPW + 1) * HD / 2;  // rotation items: HPW heads' pairs, then the new key's
+    static constexpr uint32_t kItems = ((kRot > HPW * HD ? kRot : HPW * HD) + kThreads - 1) / kThreads;
+    float x[kItems], y[kItems], c[kItems], s[kItems], vx[kItems], vy[kItems];
+};
+
+template <int HD, int HPW>
+__device__ __forceinline__ void attend_q_load(const ChunkArgs& a, uint32_t kvh, uint32_t hl, uint32_t pos, QLoads<HD, HPW>& r) {
+    using Q = QLoads<HD, HPW>;
+    const uint32_t t = thread_index(), head0 = kvh * a.group + hl * HPW, half = HD / 2;
+    if (a.step) {
+        const float* tab = a.table + static_cast<uint64_t>(pos) * half * 2;
+        const float* ksrc = a.q + static_cast<uint64_t>(a.heads) * HD + static_cast<uint64_t>(kvh) * HD;
+        const float* vsrc = a.q + static_cast<uint64_t>(a.heads + a.kv_heads) * HD + static_cast<uint64_t>(kvh) * HD;
+#pragma unroll
+        for (uint32_t u = 0; u < Q::kItems; ++u) {
+            const uint32_t i = min(t + u * kThreads, static_cast<uint32_t>(Q::kRot - 1));
+            const uint32_t h = i / half, k = i % half;  // h == HPW: the new key
+            const uint32_t ia = a.style == 0 ? 2 * k : k, ib = a.style == 0 ? 2 * k + 1 : k + half;
+            const float* src = h < HPW ? a.q + static_cast<uint64_t>(head0 + h) * HD : ksrc;
+            r.c[u] = ldg(tab + 2 * k);
+            r.s[u] = ldg(tab + 2 * k + 1);
+            r.x[u] = ldg(src + ia);
+            r.y[u] = ldg(src + ib);
+            r.vx[u] = ldg(vsrc + ia);
+            r.vy[u] = ldg(vsrc + ib);
+        }
+    } else {
+#pragma unroll
+        for (uint32_t u = 0; u < Q::kItems; ++u)
+            r.x[u] = ldg(a.q + static_cast<uint64_t>(head0) * HD + min(t + u * kThreads, static_cast<uint32_t>(HPW * HD - 1)));
+    }
+}
+
 // One (chunk, KV head, head group hl) item of the chunk pass, for a chunk
 // holding live keys (key0 < kv_len), given its loads: scores, softmax and V over its keys,
 // writing the HPW heads' partials and (max, weight sum); in a step, RoPE of
@@ -150,7 +191,8 @@ __device__ __forceinline__ void attend_chunk_load(const ChunkArgs& a, uint32_t c
 // weights and values the V pass holds in registers at once.
 template <int HD, bool F16, int HPW, bool COH, uint32_t KB = 32>
 __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t chunk, uint32_t kvh, uint32_t hl, uint32_t pos,
-                                                  uint32_t kv_len, const ChunkLoads<HD, F16>& ld, AttendSmem<HD, F16, HPW>& sm) {
+                                                  uint32_t kv_len, const QLoads<HD, HPW>& qv, const ChunkLoads<HD, F16>& ld,
+                                                  AttendSmem<HD, F16, HPW>& sm) {
 #pragma clang fp contract(off)
     using S = ChunkShape<HD, F16>;
     constexpr bool kStageV = S::kStageV;
@@ -172,26 +214,26 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     // key and value, rounded to the cache type and appended by head group
     // 0's workgroup.
     const uint32_t half = HD / 2;
+    using Q = QLoads<HD, HPW>;
     if (a.step) {
-        const float* tab = a.table + static_cast<uint64_t>(pos) * half * 2;
-        const float* ksrc = a.q + static_cast<uint64_t>(a.heads) * HD + static_cast<uint64_t>(kvh) * HD;
-        const float* vsrc = a.q + static_cast<uint64_t>(a.heads + a.kv_heads) * HD + static_cast<uint64_t>(kvh) * HD;
         const uint64_t new_row = (kv_row0 + pos % a.capacity) * HD;
-        for (uint32_t i = t; i < (HPW + 1) * half; i += kThreads) {
+#pragma unroll
+        for (uint32_t u = 0; u < Q::kItems; ++u) {
+            const uint32_t i = t + u * kThreads;
+            if (i >= Q::kRot) break;
             const uint32_t h = i / half, k = i % half;  // h == HPW: the new key
             const uint32_t ia = a.style == 0 ? 2 * k : k, ib = a.style == 0 ? 2 * k + 1 : k + half;
-            const float c = ldg(tab + 2 * k), sn = ldg(tab + 2 * k + 1);
+            const float c = qv.c[u], sn = qv.s[u];
             if (h < HPW) {
-                const float* qsrc = a.q + static_cast<uint64_t>(head0 + h) * HD;
-                float qx = ldg(qsrc + ia), qy = ldg(qsrc + ib);
+                float qx = qv.x[u], qy = qv.y[u];
                 if (a.rotate) rotate_pair(qx, qy, c, sn);
                 sm.q[h][ia] = qx;
                 sm.q[h][ib] = qy;
             } else if (holds_new) {
-                float kx = ldg(ksrc + ia), ky = ldg(ksrc + ib);
+                float kx = qv.x[u], ky = qv.y[u];
                 if (a.rotate) rotate_pair(kx, ky, c, sn);
                 const uint32_t kb[2] = {cache_bits(kx, F16), cache_bits(ky, F16)};
-                const uint32_t vb[2] = {cache_bits(ldg(vsrc + ia), F16), cache_bits(ldg(vsrc + ib), F16)};
+                const uint32_t vb[2] = {cache_bits(qv.vx[u], F16), cache_bits(qv.vy[u], F16)};
                 const uint32_t el[2] = {ia, ib};
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
@@ -210,19 +252,13 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
             }
         }
     } else {
-        for (uint32_t i = t; i < HPW * HD; i += kThreads) sm.q[i / HD][i % HD] = ldg(a.q + static_cast<uint64_t>(head0) * HD + i);
-    }
-    if constexpr (kStageV) {
 #pragma unroll
-        for (uint32_t j = 0; j < kVLoads; ++j) reinterpret_cast<uint4*>(sm.v)[t + j * kThreads] = ld.v[j];
-    }
-    __syncthreads();
-    if (kStageV && holds_new) {
-        for (uint32_t i = t; i < HD; i += kThreads) {
-            if constexpr (F16) reinterpret_cast<uint16_t*>(sm.v)[(n - 1) * HD + i] = static_cast<uint16_t>(sm.vnew[i]);
-            else reinterpret_cast<uint32_t*>(sm.v)[(n - 1) * HD + i] = sm.vnew[i];
+        for (uint32_t u = 0; u < Q::kItems; ++u) {
+            const uint32_t i = t + u * kThreads;
+            if (i < HPW * HD) sm.q[i / HD][i % HD] = qv.x[u];
         }
     }
+    __syncthreads();
 
     // Scores: part g of each head, then ((0 + p0) + p1) + p2) + p3; heads
     // two at a time (their q in registers), sharing the K registers.
@@ -266,7 +302,19 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
             }
         }
     }
+    // V goes to LDS only now: the scores wait for the K loads alone, while
+    // the V loads (issued last) are still in flight.
+    if constexpr (kStageV) {
+#pragma unroll
+        for (uint32_t j = 0; j < kVLoads; ++j) reinterpret_cast<uint4*>(sm.v)[t + j * kThreads] = ld.v[j];
+    }
     __syncthreads();
+    if (kStageV && holds_new) {
+        for (uint32_t i = t; i < HD; i += kThreads) {
+            if constexpr (F16) reinterpret_cast<uint16_t*>(sm.v)[(n - 1) * HD + i] = static_cast<uint16_t>(sm.vnew[i]);
+            else reinterpret_cast<uint32_t*>(sm.v)[(n - 1) * HD + i] = sm.vnew[i];
+        }
+    }
 
     // Per head (a wave each): max, weights and their halving-tree sum.
     const uint32_t wave = t / kWave, lane = t % kWave;

@@ -303,7 +303,9 @@ __device__ __forceinline__ void attention_phase(const DecodeArgs& a, const vkml_
         uint32_t chunk, kvh, hl;
         if (!attn_item(a, n, it, chunk, kvh, hl)) continue;
         if (it != wg) attend_chunk_load<kHd, true>(ca, chunk, kvh, n.kv_len, ld);
-        attend_chunk_item<kHd, true, kHpw, true, 16>(ca, chunk, kvh, hl, pos, n.kv_len, ld, sm);
+        QLoads<kHd, kHpw> qv;  // q comes from this launch's q|k|v phase: loaded after the barrier
+        attend_q_load<kHd, kHpw>(ca, kvh, hl, pos, qv);
+        attend_chunk_item<kHd, true, kHpw, true, 16>(ca, chunk, kvh, hl, pos, n.kv_len, qv, ld, sm);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         const uint32_t j = kvh * n.groups + hl;

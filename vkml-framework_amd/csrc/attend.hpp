@@ -294,7 +294,7 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
             }
 #pragma unroll
             for (int h = 0; h < HB; ++h) {
-                const float p1 = __shfl_down(part[h], 1, kWave), p2 = __shfl_down(part[h], 2, kWave), p3 = __shfl_down(part[h], 3, kWave);
+                const float p1 = dpp_f<dpp::shl(1)>(part[h]), p2 = dpp_f<dpp::shl(2)>(part[h]), p3 = dpp_f<dpp::shl(3)>(part[h]);
                 if (lane4 == 0 && key < n) {
                     const float sc = (0.0f + part[h] + p1 + p2 + p3) * a.scale;
                     sm.p[hb + h][key] = a.softcap > 0.0f ? a.softcap * tanhf(fminf(fmaxf(sc / a.softcap, -10.0f), 10.0f)) : sc;
@@ -327,9 +327,13 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
         const float w1 = lane + 64 < n ? vk_expf(s1 - m) : 0.0f;
         sm.p[h][lane] = w0;
         sm.p[h][lane + 64] = w1;
-        float l = w0 + w1;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, kWave);
+        float l = w0 + w1;  // the tree's stride 64; then 32 .. 1 toward lane 0
+        l += lane_down<32>(l);
+        l += lane_down<16>(l);
+        l += lane_down<8>(l);
+        l += lane_down<4>(l);
+        l += lane_down<2>(l);
+        l += lane_down<1>(l);
         if (lane == 0) {
             sm.m[h] = m;
             sm.l[h] = l;

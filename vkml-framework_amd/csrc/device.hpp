@@ -86,6 +86,56 @@ __device__ __forceinline__ float vk_expf(float x) {
     return p * __int_as_float((e + 127) << 23);
 }
 
+// ---------------------------------------------------------------- lane moves
+
+// Cross-lane moves that stay in the VALU: DPP (gfx9 controls: quad
+// permutations, mirrors within 8 and 16 lanes, shifts within a 16-lane row)
+// and gfx950's v_permlane16_swap / v_permlane32_swap, instead of
+// ds_bpermute's round trip through the LDS unit.
+namespace dpp {
+constexpr int kXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kXor3 = 0x1B;        // quad_perm [3, 2, 1, 0]
+constexpr int kHalfMirror = 0x141;  // lane i of 8 reads lane 7 - i
+constexpr int kMirror = 0x140;      // lane i of 16 reads lane 15 - i
+constexpr int shl(int n) { return 0x100 + n; }  // lane i reads lane i + n of its row (0 past the row)
+}  // namespace dpp
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __uint_as_float(dpp_u<CTRL>(__float_as_uint(v))); }
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return static_cast<int>(dpp_u<CTRL>(static_cast<uint32_t>(v))); }
+
+// A swap of v between neighbouring 16-lane rows (W = 16: rows 0/1, 2/3) or
+// wave halves (W = 32): .x is v on the lower row or half and the partner's v
+// on the upper; .y the partner's v on the lower and v on the upper. So
+// {.x, .y} is {own, partner} on every lane, and .y carries lane i + W to
+// lane i of the lower one.
+template <int W>
+__device__ __forceinline__ uint2 swap_rows(uint32_t v) {
+    if constexpr (W == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return make_uint2(r[0], r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return make_uint2(r[0], r[1]);
+    }
+}
+
+// Lane i + O's value (O a power of two <= 32) on lanes 0 .. O - 1 of every
+// 2 O-lane group: what a halving tree's step at stride O reads. Other lanes
+// get unspecified values, so a tree of descending strides over them is
+// valid at each group's first lane.
+template <int O>
+__device__ __forceinline__ float lane_down(float v) {
+    if constexpr (O >= 16) return __uint_as_float(swap_rows<O>(__float_as_uint(v)).y);
+    else return dpp_f<dpp::shl(O)>(v);
+}
+
 // ---------------------------------------------------------------- reductions
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -93,22 +143,30 @@ __device__ __forceinline__ float wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+// Max over groups of `width` consecutive lanes (a power of two <= 64), on
+// every lane of the group (max is exact in any order).
+template <int width>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (width >= 2) v = fmaxf(v, dpp_f<dpp::kXor1>(v));
+    if constexpr (width >= 4) v = fmaxf(v, dpp_f<dpp::kXor2>(v));
+    if constexpr (width >= 8) v = fmaxf(v, dpp_f<dpp::kHalfMirror>(v));
+    if constexpr (width >= 16) v = fmaxf(v, dpp_f<dpp::kMirror>(v));
+    if constexpr (width >= 32) {
+        const uint2 r = swap_rows<16>(__float_as_uint(v));
+        v = fmaxf(__uint_as_float(r.x), __uint_as_float(r.y));
+    }
+    if constexpr (width >= 64) {
+        const uint2 r = swap_rows<32>(__float_as_uint(v));
+        v = fmaxf(__uint_as_float(r.x), __uint_as_float(r.y));
+    }
     return v;
 }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 // Sum over groups of `width` consecutive lanes (a power of two <= 64).
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
     for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-template <int width>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
     return v;
 }
 

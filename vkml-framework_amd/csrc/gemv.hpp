@@ -340,15 +340,25 @@ __device__ __forceinline__ void round_terms(const RoundW<FMT, LPR>& w, const Rou
 }
 
 // The halving tree over the 32 accumulators of a row, strides 16, 8, 4, 2,
-// 1 (gemv_dot.comp:121-131), each an exchange between the row's lanes or an
-// addition within a lane as the mapping places accumulator L + stride.
+// 1 (gemv_dot.comp:121-131), each a move from lane l + stride down to lane
+// l or an addition within a lane as the mapping places accumulator
+// L + stride. The row's sum lands on its lane 0 (the only one read).
 template <int FMT, int LPR>
 __device__ __forceinline__ float row_tree(float (&acc)[32 / LPR]) {
 #pragma clang fp contract(off)
+    const auto down = [](float v, int mask) {
+        switch (mask) {
+            case 16: return lane_down<16>(v);
+            case 8: return lane_down<8>(v);
+            case 4: return lane_down<4>(v);
+            case 2: return lane_down<2>(v);
+            default: return lane_down<1>(v);
+        }
+    };
     const auto x = [&](int mask, int slots) {
 #pragma unroll
         for (int e = 0; e < 32 / LPR; ++e)
-            if (e < slots) acc[e] += __shfl_xor(acc[e], mask, kWave);
+            if (e < slots) acc[e] += down(acc[e], mask);
     };
     if constexpr (LPR == 32) {  // L = l
         x(16, 1); x(8, 1); x(4, 1); x(2, 1); x(1, 1);
@@ -431,8 +441,12 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
     __syncthreads();
     if (t < 64) {
         float v = s_red[t] + s_red[t + 64];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+        v += lane_down<32>(v);
+        v += lane_down<16>(v);
+        v += lane_down<8>(v);
+        v += lane_down<4>(v);
+        v += lane_down<2>(v);
+        v += lane_down<1>(v);
         if (t == 0) s_red[256] = v;
     }
     __syncthreads();
@@ -457,7 +471,7 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
                               ((static_cast<uint32_t>(quant_code(y[2], inv)) & 0xFFu) << 16) |
                               (static_cast<uint32_t>(quant_code(y[3], inv)) << 24);
         const int part = dot4(word, 0x01010101u, 0);
-        const int sum = part + __shfl_xor(part, 1, kWave) + __shfl_xor(part, 2, kWave) + __shfl_xor(part, 3, kWave);
+        const int sum = part + dpp_i<dpp::shl(1)>(part) + dpp_i<dpp::shl(2)>(part) + dpp_i<dpp::shl(3)>(part);  // on lanes q % 4 == 0
         if (q < K / 4) {
             s_words[q] = word;
             if (q % 4 == 0) s_ss[q / 4] = make_float2(static_cast<float>(sum), d);

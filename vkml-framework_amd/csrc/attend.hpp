@@ -327,13 +327,7 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
         const float w1 = lane + 64 < n ? vk_expf(s1 - m) : 0.0f;
         sm.p[h][lane] = w0;
         sm.p[h][lane + 64] = w1;
-        float l = w0 + w1;  // the tree's stride 64; then 32 .. 1 toward lane 0
-        l += lane_down<32>(l);
-        l += lane_down<16>(l);
-        l += lane_down<8>(l);
-        l += lane_down<4>(l);
-        l += lane_down<2>(l);
-        l += lane_down<1>(l);
+        const float l = tree_to_first<64>(w0 + w1);  // the tree's stride 64, then 32 .. 1 toward lane 0
         if (lane == 0) {
             sm.m[h] = m;
             sm.l[h] = l;
@@ -348,22 +342,27 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     // whole wave), KB keys' V reads are in flight together, and whole chunks
     // need no per-key guard.
     constexpr uint32_t slices = HD >= kChunk ? 1 : kChunk / HD;
-    const auto v_elem = [&](uint32_t key, uint32_t d) -> float {
-        if constexpr (kStageV) {
-            if constexpr (F16) return f16_bits_to_float(reinterpret_cast<const uint16_t*>(sm.v)[key * HD + d]);
-            else return reinterpret_cast<const float*>(sm.v)[key * HD + d];
-        } else {
-            if (holds_new && key == n - 1) return F16 ? f16_bits_to_float(sm.vnew[d]) : __uint_as_float(sm.vnew[d]);
-            if constexpr (F16) return f16_bits_to_float(ldg(static_cast<const uint16_t*>(a.v_cache) + row_of(key) * HD + d));
-            else return ldg(static_cast<const float*>(a.v_cache) + row_of(key) * HD + d);
-        }
+    const auto v_elem = [&](uint32_t key, uint32_t d) -> float {  // V rows not staged: from the cache
+        if (holds_new && key == n - 1) return F16 ? f16_bits_to_float(sm.vnew[d]) : __uint_as_float(sm.vnew[d]);
+        if constexpr (F16) return f16_bits_to_float(ldg(static_cast<const uint16_t*>(a.v_cache) + row_of(key) * HD + d));
+        else return ldg(static_cast<const float*>(a.v_cache) + row_of(key) * HD + d);
+    };
+    // w * v as fma(w, v, -0): the same rounded product (exact plus -0 keeps
+    // every result, signed zeros included), and with an f16 v one
+    // v_fma_mix_f32 that widens v as it multiplies. -0 comes through an asm
+    // so that the fma is not folded back into a multiply.
+    float nz = -0.0f;
+    asm volatile("" : "+v"(nz));
+    const auto prod = [&](float w, float x) {
+        if constexpr (F16 && kStageV) return __builtin_fmaf(w, x, nz);
+        else return w * x;
     };
     for (uint32_t c = t; c < HPW * slices * HD; c += kThreads) {
         const uint32_t d = c % HD, sl = (c / HD) % slices, h = c / (HD * slices);
         const uint32_t keys = n > sl ? (n - sl + slices - 1) / slices : 0;  // this slice's keys: sl, sl + slices, ...
-        float o = 0.0f;
-        for (uint32_t j0 = 0; j0 < keys; j0 += KB) {
-            float w[KB], x[KB];
+        // the chain's V column in LDS: key sl + slices j at j * slices * HD (immediate offsets)
+        const auto vcol = reinterpret_cast<const std::conditional_t<F16, _Float16, float>*>(sm.v) + sl * HD + d;
+        const auto weights = [&](uint32_t j0, float (&w)[KB]) {  // keys j0 .. j0 + KB - 1 of the slice
             const float4* wp = reinterpret_cast<const float4*>(&sm.p[h][slices * j0]);
 #pragma unroll
             for (uint32_t m = 0; m < KB * slices / 4; ++m) {
@@ -375,20 +374,32 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
                     w[2 * m + 1] = sl ? q.w : q.z;
                 }
             }
-            if (n == kChunk) {  // a whole chunk: no key past the last
+        };
+        float o = 0.0f;
+        if (kStageV && n == kChunk) {
+            // A whole chunk: kChunk / slices keys a chain, whole batches, no
+            // bound on a key; each product reads its V element itself.
+#pragma unroll 1
+            for (uint32_t j0 = 0; j0 < kChunk / slices; j0 += KB) {
+                float w[KB];
+                weights(j0, w);
 #pragma unroll
-                for (uint32_t jj = 0; jj < KB; ++jj) x[jj] = v_elem(sl + slices * (j0 + jj), d);
-            } else {
-#pragma unroll
-                for (uint32_t jj = 0; jj < KB; ++jj) x[jj] = v_elem(min(sl + slices * (j0 + jj), n - 1), d);
+                for (uint32_t jj = 0; jj < KB; ++jj) o += prod(w[jj], static_cast<float>(vcol[(j0 + jj) * slices * HD]));
             }
-            if (j0 + KB <= keys) {
+        } else {
+            for (uint32_t j0 = 0; j0 < keys; j0 += KB) {
+                float w[KB], x[KB];
+                weights(j0, w);
+                if constexpr (kStageV) {
 #pragma unroll
-                for (uint32_t jj = 0; jj < KB; ++jj) o += w[jj] * x[jj];
-            } else {
+                    for (uint32_t jj = 0; jj < KB; ++jj) x[jj] = static_cast<float>(vcol[min(j0 + jj, keys - 1) * slices * HD]);
+                } else {
+#pragma unroll
+                    for (uint32_t jj = 0; jj < KB; ++jj) x[jj] = v_elem(min(sl + slices * (j0 + jj), n - 1), d);
+                }
 #pragma unroll
                 for (uint32_t jj = 0; jj < KB; ++jj)
-                    if (j0 + jj < keys) o += w[jj] * x[jj];
+                    if (j0 + jj < keys) o += prod(w[jj], x[jj]);
             }
         }
         if constexpr (HD > kChunk) {

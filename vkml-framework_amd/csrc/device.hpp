@@ -131,9 +131,28 @@ __device__ __forceinline__ uint2 swap_rows(uint32_t v) {
 // get unspecified values, so a tree of descending strides over them is
 // valid at each group's first lane.
 template <int O>
-__device__ __forceinline__ float lane_down(float v) {
-    if constexpr (O >= 16) return __uint_as_float(swap_rows<O>(__float_as_uint(v)).y);
-    else return dpp_f<dpp::shl(O)>(v);
+__device__ __forceinline__ uint32_t lane_down_u(uint32_t v) {
+    if constexpr (O >= 16) return swap_rows<O>(v).y;
+    else return dpp_u<dpp::shl(O)>(v);
+}
+template <int O>
+__device__ __forceinline__ float lane_down(float v) { return __uint_as_float(lane_down_u<O>(__float_as_uint(v))); }
+template <int O>
+__device__ __forceinline__ int lane_down_i(int v) { return static_cast<int>(lane_down_u<O>(static_cast<uint32_t>(v))); }
+
+// A halving tree's strides W / 2 .. 1 toward the first lane of each W-lane
+// group: lane j < o adds lane j + o, which is also its butterfly partner
+// j ^ o, so the first lane's sum is the one a shuffle-xor tree gives it.
+template <int W>
+__device__ __forceinline__ float tree_to_first(float v) {
+#pragma clang fp contract(off)
+    if constexpr (W >= 64) v += lane_down<32>(v);
+    if constexpr (W >= 32) v += lane_down<16>(v);
+    if constexpr (W >= 16) v += lane_down<8>(v);
+    if constexpr (W >= 8) v += lane_down<4>(v);
+    if constexpr (W >= 4) v += lane_down<2>(v);
+    if constexpr (W >= 2) v += lane_down<1>(v);
+    return v;
 }
 
 // ---------------------------------------------------------------- reductions

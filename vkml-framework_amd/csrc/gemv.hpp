@@ -440,13 +440,7 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
     if (t < 128) s_red[t] = s_red[t] + s_red[t + 128];
     __syncthreads();
     if (t < 64) {
-        float v = s_red[t] + s_red[t + 64];
-        v += lane_down<32>(v);
-        v += lane_down<16>(v);
-        v += lane_down<8>(v);
-        v += lane_down<4>(v);
-        v += lane_down<2>(v);
-        v += lane_down<1>(v);
+        const float v = tree_to_first<64>(s_red[t] + s_red[t + 64]);
         if (t == 0) s_red[256] = v;
     }
     __syncthreads();

@@ -127,9 +127,7 @@ __global__ void __launch_bounds__(256) k_gemv_float(const float* a, uint32_t m, 
 #pragma unroll
     for (uint32_t q = 0; q < 8; ++q) {
         if (q >= m) break;
-        float v = acc[q];
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+        const float v = tree_to_first<32>(acc[q]);  // strides 16 .. 1 toward the row's lane 0
         if (lane == 0 && row < n) out[static_cast<uint64_t>(q) * n + row] = v;
     }
 }

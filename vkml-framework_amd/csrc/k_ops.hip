@@ -166,9 +166,7 @@ __device__ float tree256_sum(float v, float* scratch) {
     scratch[t] = v;
     __syncthreads();
     if (t < 64) {
-        float s = (scratch[t] + scratch[t + 128]) + (scratch[t + 64] + scratch[t + 192]);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+        const float s = tree_to_first<64>((scratch[t] + scratch[t + 128]) + (scratch[t + 64] + scratch[t + 192]));
         if (t == 0) scratch[256] = s;
     }
     __syncthreads();
@@ -277,6 +275,18 @@ __device__ __forceinline__ void better(float& v, int& c, float ov, int oc) {
     }
 }
 
+// The wave's best (value, column) toward lane 0: strides 32 .. 1, lane j
+// comparing itself with lane j + o (its butterfly partner j ^ o), so lane 0
+// ends with what a shuffle-xor reduction gives it.
+__device__ __forceinline__ void argmax_to_first(float& best, int& col) {
+    better(best, col, lane_down<32>(best), lane_down_i<32>(col));
+    better(best, col, lane_down<16>(best), lane_down_i<16>(col));
+    better(best, col, lane_down<8>(best), lane_down_i<8>(col));
+    better(best, col, lane_down<4>(best), lane_down_i<4>(col));
+    better(best, col, lane_down<2>(best), lane_down_i<2>(col));
+    better(best, col, lane_down<1>(best), lane_down_i<1>(col));
+}
+
 __device__ __forceinline__ void consider(float& best, int& col, float v, uint32_t c) {
     if (!__builtin_isnan(v) && (col < 0 || v > best)) {
         best = v;
@@ -316,8 +326,7 @@ __device__ int block_argmax(const float* x, uint32_t cols) {
     } else {
         for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) consider(best, col, x[c], c);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) better(best, col, __shfl_xor(best, o, kWave), __shfl_xor(col, o, kWave));
+    argmax_to_first(best, col);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     __syncthreads();
     if (lane == 0) {
@@ -329,8 +338,7 @@ __device__ int block_argmax(const float* x, uint32_t cols) {
         const int waves = blockDim.x / kWave;
         best = lane < waves ? s_v[lane] : 0.0f;
         col = lane < waves ? s_c[lane] : -1;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) better(best, col, __shfl_xor(best, o, kWave), __shfl_xor(col, o, kWave));
+        argmax_to_first(best, col);
     }
     return col < 0 ? 0 : col;  // valid in thread 0
 }

@@ -407,6 +407,27 @@ int vkml_attend_step(const vkml_attend_step_params* p, const float* d_qkv, const
                      void* d_k_cache, void* d_v_cache, float* d_partial, float* d_stats,
                      float* d_out, void* d_values, float* d_scales, const vkml_decode_state* d_state);
 
+/* vkml_attend_step, then the o projection with its residual add,
+ * d_x[n] += o[n] . (the attention output's Q8_0 form) as vkml_gemv_dot_add
+ * (llama.cpp:320-374): bit for bit those calls. The merge and the GEMV
+ * share a launch where the o weights are q4_K or q8_0 with f16 scales, the
+ * GEMV reads every attention output (o->k = heads * head_dim) and the grid
+ * fits the GPU at once: the merge's workgroups publish the Q8_0 output and
+ * the GEMV's, their first weight loads issued, wait for it on d_sync (a
+ * bounded wait; vkml_attend_o_check reports one that gave up). Otherwise
+ * the three launches. d_values / d_scales are required (the o input).
+ * d_sync: vkml_attend_o_sync_bytes() bytes, zeroed once before first use;
+ * one per stream of calls (the chunk pass clears it for the launch after). */
+uint64_t vkml_attend_o_sync_bytes(void);
+int vkml_attend_step_o(const vkml_attend_step_params* p, const float* d_qkv, const float* d_rope_table,
+                       void* d_k_cache, void* d_v_cache, float* d_partial, float* d_stats, float* d_out,
+                       void* d_values, float* d_scales, const vkml_decode_state* d_state,
+                       const vkml_gemv_dot_params* o, const void* d_o_values, const void* d_o_scales,
+                       float* d_x, uint32_t* d_sync);
+/* Synchronizes, then reports (VKML_ERROR_DEVICE) and clears a wait of an
+ * earlier vkml_attend_step_o on this sync buffer that timed out. */
+int vkml_attend_o_check(uint32_t* d_sync);
+
 
 /* ---------------------------------------------------------------------- */
 /* Fused decode-step kernels (no single reference counterpart: each       */

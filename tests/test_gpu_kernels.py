@@ -421,6 +421,63 @@ def test_attend_step_bit_exact(hd, heads, kvh, pos, kv_type, style):
         assert np.array_equal(scs.download(np.float32, ws.shape).view(np.uint32), ws.view(np.uint32))
 
 
+@pytest.mark.parametrize("hd,heads,kvh,pos,kv_type,fmt,n", [
+    (128, 32, 8, 4096, H.F16, H.Q4_K, 4096), (128, 32, 8, 300, H.F16, H.Q8_0, 4096), (64, 32, 8, 200, H.F16, H.Q4_K, 2048),
+    (256, 8, 4, 300, H.F16, H.Q4_K, 2048), (128, 16, 2, 700, H.F32, H.Q4_K, 1024), (128, 16, 4, 130, H.F16, H.Q4_0, 2048)])
+def test_attend_step_o_bit_exact(hd, heads, kvh, pos, kv_type, fmt, n):
+    # attention + merge + Q8_0 + the o GEMV + residual in one call (the
+    # merge and the GEMV in one launch, except q4_0, which takes the three
+    # launches), two steps in a row: against the oracle and against
+    # vkml_attend_step + vkml_gemv_dot_add on a second copy of the caches
+    k = heads * hd
+    cap = pos + 67
+    chunks = (cap + 127) // 128
+    rng = np.random.default_rng(pos + hd + n)
+    dt = np.uint16 if kv_type == H.F16 else np.float32
+    prior = rng.standard_normal((2, kvh, cap, hd)).astype(np.float32)
+    caches = [prior[i].astype(np.float16).view(np.uint16) if kv_type == H.F16 else prior[i] for i in range(2)]
+    kc, vc, kc2, vc2 = dev(caches[0]), dev(caches[1]), dev(caches[0]), dev(caches[1])
+    table = O.rope_table(cap, hd, 1e6)
+    dtab = dev(table)
+    v, s_, quant, words, scales = weights(fmt, n, k, pos + 3)
+    x0 = rng.standard_normal(n).astype(np.float32)
+    x, x2 = dev(x0), dev(x0)
+    sync = H.empty(H.lib().vkml_attend_o_sync_bytes())
+    H.call("vkml_fill_u32", p(sync), 0, H.lib().vkml_attend_o_sync_bytes() // 4)
+    part, stats = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8)
+    part2, stats2 = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8)
+    op = H.GemvDotParams(1, n, k, fmt, H.F16)
+    want_x = x0.copy()
+    for step in range(2):
+        p_now = pos + step
+        qkv = rng.standard_normal((heads + 2 * kvh) * hd).astype(np.float32)
+        dq = dev(qkv)
+        out, vals, scs = H.empty(k * 4), H.empty(k), H.empty(k // 32 * 4)
+        out2, vals2, scs2 = H.empty(k * 4), H.empty(k), H.empty(k // 32 * 4)
+        prm = H.AttendStepParams(heads, kvh, hd, cap, 0, p_now, kv_type, chunks, 0, 1, 1.0 / math.sqrt(hd), 0.0)
+        H.call("vkml_attend_step_o", prm, p(dq), p(dtab), p(kc), p(vc), p(part), p(stats), p(out), p(vals), p(scs), None,
+               op, p(v), p(s_), p(x), p(sync))
+        H.call("vkml_attend_step", prm, p(dq), p(dtab), p(kc2), p(vc2), p(part2), p(stats2), p(out2), p(vals2), p(scs2), None)
+        H.call("vkml_gemv_dot_add", op, p(vals2), p(v), p(x2), p(s_), p(scs2), p(x2))
+        H.call("vkml_attend_o_check", p(sync))  # no wait gave up
+        q = O.rope(qkv[:k].reshape(1, heads, hd), table, p_now, 0).reshape(heads, hd)
+        kn = O.rope(qkv[k:k + kvh * hd].reshape(1, kvh, hd), table, p_now, 0).reshape(kvh, hd)
+        vn = qkv[k + kvh * hd:].reshape(kvh, hd)
+        for c, new in ((caches[0], kn), (caches[1], vn)):
+            c[:, p_now] = O.f32_to_f16(new) if kv_type == H.F16 else new
+        assert np.array_equal(kc.download(dt, caches[0].shape), caches[0])
+        assert np.array_equal(vc.download(dt, caches[1].shape), caches[1])
+        want = O.attend_decode(q, caches[0], caches[1], 0, p_now + 1)
+        assert np.array_equal(bits(out.download(np.float32, (heads, hd))), bits(want))
+        ww, ws = O.quantize(O.Q8_0, want.reshape(1, k), False)
+        assert np.array_equal(vals.download(np.uint32, ww.shape), ww)
+        assert np.array_equal(scs.download(np.float32, ws.shape).view(np.uint32), ws.view(np.uint32))
+        want_x = want_x + O.gemv_dot(quant, ww, ws, 1, words, scales, n, k)[0]
+        got = x.download(np.float32, n)
+        assert np.array_equal(bits(got), bits(want_x))
+        assert np.array_equal(bits(got), bits(x2.download(np.float32, n)))
+
+
 # ---------------------------------------------------------------- small ops
 
 def test_argmax_and_step_finish():

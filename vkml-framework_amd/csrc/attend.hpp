@@ -46,6 +46,22 @@ struct ChunkArgs {
     uint32_t heads, kv_heads, group, capacity, kv_start, kv_len, position, chunks;
     uint32_t step, style, rotate;
     float scale, softcap;
+    // When non-null: the sync words of the merge + o launch that follows
+    // (OSync), whose counter and flags workgroup 0 zeroes.
+    uint32_t* o_sync;
+};
+
+// Sync words of the launch that merges the chunks and runs the o GEMV on
+// the result (one 256-byte line each): [0] a sticky error flag, then kCopies
+// copies of the merge workgroups' arrival counter (each merging workgroup
+// adds to every copy; a GEMV workgroup polls copy wg % kCopies, so no one
+// line serves every poll).
+struct OSync {
+    static constexpr uint32_t kLine = 64;
+    static constexpr uint32_t kCopies = 16;
+    static constexpr uint32_t kWords = kLine * (1 + kCopies);
+    __device__ static uint32_t* error(uint32_t* s) { return s; }
+    __device__ static uint32_t* counter(uint32_t* s, uint32_t i) { return s + kLine * (1 + i); }
 };
 
 // Four elements of a cache row, as stored (four f16, or four f32), and widened exactly.

@@ -11,10 +11,23 @@
 // CU, so one's loads overlap another's arithmetic. The merge is its own
 // launch, every load of a head's chunks issued at once, and can quantize its
 // output to Q8_0 for the o projection.
+//
+// Merge + o. In a decode step the merge can share a launch with the o
+// projection that consumes it (vkml_attend_step_o): the grid's first
+// workgroups merge (two heads each at head_dim 128) and publish the Q8_0
+// attention output, and the GEMV's workgroups, which issue their first
+// weight loads at once, wait for it. The merge's latency then overlaps the
+// GEMV's weight fetch, and the step loses a launch. The wait is on one of
+// 16 copies of an arrival counter, to which every merging workgroup adds
+// once its write-through stores have completed; it is bounded (a sticky
+// error flag past the spin limit, which vkml_attend_o_check reports), and
+// the launch is made only when the whole grid is resident at once, so no
+// waiting workgroup can hold the slot a merging one needs.
 #include <algorithm>
 
 #include "attend.hpp"
 #include "device.hpp"
+#include "gemv.hpp"
 #include "internal.hpp"
 
 using namespace vkml::dev;
@@ -29,6 +42,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_chunk(ChunkArgs a) {
     // (chunk, KV head) pair get numbers 8 apart, so the same XCD.
     const uint32_t G = a.group, groups = G / HPW, pairs = a.chunks * a.kv_heads;
     const uint32_t L = blockIdx.x, pair_lo = L % kXcds, rest = L / kXcds;
+    if (a.o_sync && L == 0 && threadIdx.x < OSync::kCopies) OSync::counter(a.o_sync, threadIdx.x)[0] = 0u;
     const uint32_t hl = rest % groups, pair = (rest / groups) * kXcds + pair_lo;
     if (pair >= pairs) return;
     const uint32_t chunk = pair / a.kv_heads, kvh = pair % a.kv_heads, head0 = kvh * G + hl * HPW;
@@ -92,6 +106,111 @@ int launch_merge(uint32_t heads, uint32_t head_dim, uint32_t chunks, const float
     return VKML_OK;
 }
 
+// ---------------------------------------------------------------- merge + o
+
+struct MergeOArgs {
+    const float* partial;
+    const float* stats;
+    float* out;
+    uint8_t* values;
+    float* scales;
+    uint32_t hd, chunks, merge_wgs;
+    uint32_t* sync;
+};
+
+constexpr uint32_t kOSpinCap = 1u << 20;
+
+// Lane 0 polls counter copy wg % kCopies until every merging workgroup has
+// arrived; false if the wait gave up (the spin limit, or another
+// workgroup's error). Called by every thread; ends with a workgroup barrier
+// (the weight loads issued before it stay in flight).
+__device__ bool await_merged(uint32_t* sync, uint32_t wg, uint32_t arrivals) {
+    __shared__ uint32_t s_ok;
+    if (threadIdx.x == 0) {
+        uint32_t ok = 1;
+        uint32_t* c = OSync::counter(sync, wg % OSync::kCopies);
+        for (uint32_t spins = 0;; ++spins) {
+            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= arrivals) break;
+            if (spins % 64 == 63 && __hip_atomic_load(OSync::error(sync), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                ok = 0;
+                break;
+            }
+            if (spins >= kOSpinCap) {
+                __hip_atomic_store(OSync::error(sync), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        s_ok = ok;
+    }
+    __syncthreads();
+    return s_ok != 0;
+}
+
+// Workgroups [0, merge_wgs): the merge (kThreads / hd heads each, thread
+// element d of head h), its Q8_0 output stored write-through; then the
+// arrival on every counter copy. The rest: the o GEMV (32
+// lanes a row, + residual) on that output, as k_gemv_dot runs it.
+template <int FMT, bool FULL>
+__global__ void __launch_bounds__(kThreads) k_merge_o(MergeOArgs m, vkml::gemv::GemvArgs g) {
+    extern __shared__ uint4 smem[];
+    if (blockIdx.x < m.merge_wgs) {
+        const uint32_t hpw = kThreads / m.hd, half = threadIdx.x / m.hd, d = threadIdx.x % m.hd;
+        float* f = reinterpret_cast<float*>(smem);
+        float* s_r = f + half * 2 * m.chunks;
+        float* s_l = s_r + m.chunks;
+        float* s_wmax = f + hpw * 2 * m.chunks + half * (m.hd / kWave);
+        merge_head<true, 48>(m.partial, m.stats, m.out, m.values, m.scales, blockIdx.x * hpw + half, m.chunks, m.chunks, m.hd, d, s_r,
+                         s_l, s_wmax);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the write-through stores have completed
+        __syncthreads();
+        if (threadIdx.x < OSync::kCopies)
+            __hip_atomic_fetch_add(OSync::counter(m.sync, threadIdx.x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const uint32_t wg = blockIdx.x - m.merge_wgs;
+    vkml::gemv::GemvRows<FMT, true, 32, vkml::gemv::kAdd, 2, kThreads, false, false, 1, FULL> rows;
+    rows.start(g, wg);
+    if (!await_merged(m.sync, wg, m.merge_wgs)) return;
+    vkml::gemv::stage_activation<kThreads, false, true>(g, smem);
+    rows.finish(g, smem, vkml::gemv::staged_ss(smem, g.k));
+}
+
+template <int FMT, bool FULL>
+bool launch_merge_o_as(const MergeOArgs& m, const vkml::gemv::GemvArgs& g, uint32_t grid, size_t lds) {
+    const void* fn = reinterpret_cast<const void*>(&k_merge_o<FMT, FULL>);
+    static int per_cu = -1;  // resident workgroups a CU at this LDS size
+    static size_t per_cu_lds = 0;
+    if (per_cu < 0 || per_cu_lds != lds) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, lds) != hipSuccess) per_cu = 0;
+        per_cu_lds = lds;
+    }
+    if (static_cast<uint64_t>(per_cu) * vkml::abi::compute_units() < grid) return false;
+    hipLaunchKernelGGL((k_merge_o<FMT, FULL>), dim3(grid), dim3(kThreads), lds, vkml::abi::stream(), m, g);
+    return true;
+}
+
+// The merge + o launch, if the shapes allow it and the grid is resident at
+// once; false otherwise (nothing launched).
+bool launch_merge_o(const MergeOArgs& m, const vkml::gemv::GemvArgs& g, uint32_t heads, uint32_t b_type, uint32_t scale_type) {
+    using namespace vkml::gemv;
+    if (b_type != VKML_Q4_K && !(b_type == VKML_Q8_0 && scale_type == VKML_F16)) return false;
+    const uint32_t hpw = kThreads / m.hd;
+    if (heads % hpw != 0 || g.k != heads * m.hd || g.n == 0) return false;
+    const bool q4k = b_type == VKML_Q4_K;
+    if ((q4k ? code_bytes<VKML_Q4_K>(g.n, g.k) : code_bytes<VKML_Q8_0>(g.n, g.k)) >= (1ull << 32) ||
+        (q4k ? scale_bytes<VKML_Q4_K, true>(g.n, g.k) : scale_bytes<VKML_Q8_0, true>(g.n, g.k)) >= (1ull << 32))
+        return false;
+    const size_t merge_lds = (static_cast<size_t>(hpw) * 2 * m.chunks + hpw * (m.hd / kWave)) * 4;
+    const size_t lds = std::max<size_t>(stage_bytes(g.k, false), merge_lds);
+    if (lds > 64 * 1024) return false;
+    const uint32_t grid = m.merge_wgs + (g.n + kThreads / 32 - 1) / (kThreads / 32);
+    const bool full = g.k % 2048 == 0;  // whole pairs of 2-round batches
+    if (q4k) return full ? launch_merge_o_as<VKML_Q4_K, true>(m, g, grid, lds) : launch_merge_o_as<VKML_Q4_K, false>(m, g, grid, lds);
+    return full ? launch_merge_o_as<VKML_Q8_0, true>(m, g, grid, lds) : launch_merge_o_as<VKML_Q8_0, false>(m, g, grid, lds);
+}
+
 int check_heads(uint32_t heads, uint32_t kv_heads, uint32_t head_dim, const char* what) {
     VKML_CHECK_ARG(kv_heads > 0 && heads % kv_heads == 0,
                    std::string(what) + ": q's " + std::to_string(heads) + " heads must be a multiple of k and v's " + std::to_string(kv_heads));
@@ -121,7 +240,7 @@ int vkml_attend(const vkml_attend_params* p, const float* q, const void* k_cache
     VKML_CHECK_ARG(q && k_cache && v_cache && partial && stats, "attend: null buffer");
     ChunkArgs args{q, nullptr, const_cast<void*>(k_cache), const_cast<void*>(v_cache), partial, stats, state,
                    p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity, p->kv_start, p->kv_len, 0, p->chunks,
-                   0, 0, 0, p->scale, p->softcap};
+                   0, 0, 0, p->scale, p->softcap, nullptr};
     vkml::abi::ProfileScope prof("attend");
     launch_chunks(p->head_dim, p->kv_type == VKML_F16, args);
     return vkml::abi::check_launch("attend");
@@ -141,22 +260,43 @@ int vkml_attend_merge(const vkml_attend_params* p, const float* partial, const f
     return vkml::abi::check_launch("attend_merge");
 }
 
+}  // extern "C"
+
+namespace {
+
+int check_step(const vkml_attend_step_params* p, const float* qkv, const float* rope_table, const void* k_cache, const void* v_cache,
+               const float* partial, const float* stats, const float* out, const void* values, const float* scales,
+               const vkml_decode_state* state, const char* what) {
+    VKML_REQUIRE_INIT();
+    const std::string w(what);
+    VKML_CHECK_ARG(p, w + ": null params");
+    if (int r = check_heads(p->heads, p->kv_heads, p->head_dim, what)) return r;
+    VKML_CHECK_ARG(p->kv_type == VKML_F16 || p->kv_type == VKML_F32, w + ": caches must be f16 or f32");
+    VKML_CHECK_ARG(p->capacity > 0 && p->kv_start < p->capacity, w + ": kv_start must lie inside the cache");
+    VKML_CHECK_ARG(state || (p->position < p->capacity && p->kv_start <= p->position),
+                   w + ": position " + std::to_string(p->position) + " is outside the cache");
+    VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= p->capacity - p->kv_start && p->chunks <= kMergeMaxChunks,
+                   w + ": " + std::to_string(p->chunks) + " chunks do not cover the cache (or exceed " +
+                       std::to_string(kMergeMaxChunks) + ")");
+    VKML_CHECK_ARG(qkv && rope_table && k_cache && v_cache && partial && stats && out, w + ": null buffer");
+    VKML_CHECK_ARG(!values || scales, w + ": quantized output needs scales");
+    return VKML_OK;
+}
+
+ChunkArgs step_args(const vkml_attend_step_params* p, const float* qkv, const float* rope_table, void* k_cache, void* v_cache,
+                    float* partial, float* stats, const vkml_decode_state* state, uint32_t* o_sync) {
+    return ChunkArgs{qkv, rope_table, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads,
+                     p->capacity, p->kv_start, 0, p->position, p->chunks, 1, p->rope_style, p->rotate, p->scale, p->softcap, o_sync};
+}
+
+}  // namespace
+
+extern "C" {
+
 int vkml_attend_step(const vkml_attend_step_params* p, const float* qkv, const float* rope_table, void* k_cache, void* v_cache,
                      float* partial, float* stats, float* out, void* values, float* scales, const vkml_decode_state* state) {
-    VKML_REQUIRE_INIT();
-    VKML_CHECK_ARG(p, "attend_step: null params");
-    if (int r = check_heads(p->heads, p->kv_heads, p->head_dim, "attend_step")) return r;
-    VKML_CHECK_ARG(p->kv_type == VKML_F16 || p->kv_type == VKML_F32, "attend_step: caches must be f16 or f32");
-    VKML_CHECK_ARG(p->capacity > 0 && p->kv_start < p->capacity, "attend_step: kv_start must lie inside the cache");
-    VKML_CHECK_ARG(state || (p->position < p->capacity && p->kv_start <= p->position),
-                   "attend_step: position " + std::to_string(p->position) + " is outside the cache");
-    VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= p->capacity - p->kv_start && p->chunks <= kMergeMaxChunks,
-                   "attend_step: " + std::to_string(p->chunks) + " chunks do not cover the cache (or exceed " +
-                       std::to_string(kMergeMaxChunks) + ")");
-    VKML_CHECK_ARG(qkv && rope_table && k_cache && v_cache && partial && stats && out, "attend_step: null buffer");
-    VKML_CHECK_ARG(!values || scales, "attend_step: quantized output needs scales");
-    ChunkArgs args{qkv, rope_table, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads,
-                   p->capacity, p->kv_start, 0, p->position, p->chunks, 1, p->rope_style, p->rotate, p->scale, p->softcap};
+    if (int r = check_step(p, qkv, rope_table, k_cache, v_cache, partial, stats, out, values, scales, state, "attend_step")) return r;
+    const ChunkArgs args = step_args(p, qkv, rope_table, k_cache, v_cache, partial, stats, state, nullptr);
     {
         vkml::abi::ProfileScope prof("attend_step");
         launch_chunks(p->head_dim, p->kv_type == VKML_F16, args);
@@ -165,6 +305,54 @@ int vkml_attend_step(const vkml_attend_step_params* p, const float* qkv, const f
     vkml::abi::ProfileScope prof("attend_merge");
     launch_merge(p->heads, p->head_dim, p->chunks, partial, stats, out, values, scales);
     return vkml::abi::check_launch("attend_merge");
+}
+
+uint64_t vkml_attend_o_sync_bytes(void) { return static_cast<uint64_t>(OSync::kWords) * 4; }
+
+int vkml_attend_step_o(const vkml_attend_step_params* p, const float* qkv, const float* rope_table, void* k_cache, void* v_cache,
+                       float* partial, float* stats, float* out, void* values, float* scales, const vkml_decode_state* state,
+                       const vkml_gemv_dot_params* o, const void* o_values, const void* o_scales, float* x, uint32_t* sync) {
+    if (int r = check_step(p, qkv, rope_table, k_cache, v_cache, partial, stats, out, values, scales, state, "attend_step_o")) return r;
+    VKML_CHECK_ARG(o && values && scales && o_values && o_scales && x && sync, "attend_step_o: null buffer");
+    VKML_CHECK_ARG(o->m == 1 && o->k == p->heads * p->head_dim,
+                   "attend_step_o: the o projection must take the " + std::to_string(p->heads * p->head_dim) + " attention outputs");
+    const MergeOArgs m{partial, stats, out, static_cast<uint8_t*>(values), scales, p->head_dim, p->chunks,
+                       p->heads / (kThreads / p->head_dim), sync};
+    const vkml::gemv::GemvArgs g{static_cast<const uint4*>(values), scales, o_values, o_scales, nullptr, nullptr, x, x, o->n, o->k};
+    // The chunk pass clears the merge + o sync words only when that launch follows.
+    const bool fusable = o->b_type == VKML_Q4_K || (o->b_type == VKML_Q8_0 && o->scale_type == VKML_F16);
+    const ChunkArgs args = step_args(p, qkv, rope_table, k_cache, v_cache, partial, stats, state, fusable ? sync : nullptr);
+    {
+        vkml::abi::ProfileScope prof("attend_step");
+        launch_chunks(p->head_dim, p->kv_type == VKML_F16, args);
+        if (int r = vkml::abi::check_launch("attend_step")) return r;
+    }
+    if (fusable) {
+        vkml::abi::ProfileScope prof("attend_merge_o");
+        if (launch_merge_o(m, g, p->heads, o->b_type, o->scale_type)) return vkml::abi::check_launch("attend_merge_o");
+    }
+    {
+        vkml::abi::ProfileScope prof("attend_merge");
+        launch_merge(p->heads, p->head_dim, p->chunks, partial, stats, out, values, scales);
+        if (int r = vkml::abi::check_launch("attend_merge")) return r;
+    }
+    return vkml_gemv_dot_add(o, values, o_values, x, o_scales, scales, x);
+}
+
+int vkml_attend_o_check(uint32_t* sync) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(sync, "attend_o_check: null buffer");
+    hipStream_t s = vkml::abi::stream();
+    uint32_t flag = 0;
+    hipError_t e = hipMemcpyAsync(&flag, sync, 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_o_check");
+    if (flag == 0) return VKML_OK;
+    const uint32_t zero = 0;
+    e = hipMemcpyAsync(sync, &zero, 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_o_check");
+    return vkml::abi::fail(VKML_ERROR_DEVICE, "attend_step_o: the o GEMV's wait for the merge timed out; the step's results are invalid");
 }
 
 }  // extern "C"

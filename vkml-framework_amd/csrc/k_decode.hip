@@ -285,7 +285,8 @@ __device__ __forceinline__ bool attn_item(const DecodeArgs& a, const AttnItems& 
 }
 __device__ __forceinline__ ChunkArgs chunk_args(const DecodeArgs& a, const vkml_decode_layer& L, uint32_t l) {
     return ChunkArgs{qkv_at(a, l), a.rope, L.k_cache, L.v_cache, a.partial, a.stats, nullptr, opaque(a.heads), opaque(a.kv_heads),
-                     a.heads / a.kv_heads, opaque(a.capacity), 0, 0, 0, opaque(a.chunks), 1, a.style, a.rotate, a.scale, 0.0f};
+                     a.heads / a.kv_heads, opaque(a.capacity), 0, 0, 0, opaque(a.chunks), 1, a.style, a.rotate, a.scale, 0.0f,
+                     nullptr};
 }
 
 // The attention phase. The workgroup's first item's K and V were loaded by

@@ -129,6 +129,9 @@ SIGNATURES = {
     "vkml_rope_kv_append": [P(RopeKvParams), vp, vp, vp, vp, vp, vp],
     "vkml_gemv_fused": [P(GemvFusedParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "vkml_attend_step_o": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp],
+    "vkml_attend_o_check": [vp],
+    "vkml_attend_o_sync_bytes": [],
     "vkml_state_set": [vp, i32, i32, i32],
     "vkml_embedding_state": [P(EmbeddingParams), vp, vp, vp, vp],
     "vkml_step_finish": [u32, vp, vp, vp, u32],
@@ -155,6 +158,7 @@ def lib() -> C.CDLL:
             fn.restype = C.c_int
         _lib.vkml_stream.restype = C.c_void_p
         _lib.vkml_decode_sync_bytes.restype = C.c_uint64
+        _lib.vkml_attend_o_sync_bytes.restype = C.c_uint64
         _lib.vkml_decode_work_bytes.restype = C.c_uint64
     return _lib
 

@@ -309,6 +309,7 @@ struct Llama::Impl {
 
     // Decode buffers.
     Tensor x, xn, xq, xs, qkv, q, attn, aq, as, partial, stats, h, hq, hs, gate_tmp, up_tmp, ytmp, logits, state, log;
+    Tensor o_sync;  // vkml_attend_step_o: the merge + o launch's sync words
     std::int64_t chunks = 1;  // decode attention's 128-key chunks over the whole cache
     std::uint64_t graph_logits = 0, graph_greedy = 0;
     // The persistent layers launch (vkml_decode_layers): its per-layer
@@ -392,6 +393,8 @@ struct Llama::Impl {
     // Reports a grid barrier of the persistent launch that timed out.
     void check_persistent() const {
         if (persistent) check(vkml_decode_layers_check(static_cast<std::uint32_t*>(const_cast<void*>(sync.data()))), "Llama: decode step");
+        if (!persistent && int_dot)
+            check(vkml_attend_o_check(static_cast<std::uint32_t*>(const_cast<void*>(o_sync.data()))), "Llama: decode step");
     }
 
     // One token: the state's token at the state's position.
@@ -451,12 +454,23 @@ struct Llama::Impl {
             const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(context_length), 0, 0, kv_code,
                                              u32(chunks), c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
                                              1.0f / std::sqrt(static_cast<float>(hd)), 0.0f};
-            check(vkml_attend_step(&sp, static_cast<const float*>(qkv.data()), static_cast<const float*>(rope.data()), L.k_cache.data(),
-                                   L.v_cache.data(), static_cast<float*>(partial.data()), static_cast<float*>(stats.data()),
-                                   static_cast<float*>(attn.data()), o_q ? aq.data() : nullptr,
-                                   o_q ? static_cast<float*>(as.data()) : nullptr, st),
-                  "attention");
-            project(L.o, attn, o_q ? &aq : nullptr, &as, xp, xp, "o");
+            if (int_dot && o_q && L.o.int_dot_ok()) {
+                // ... and the merge shares a launch with the o projection + residual
+                const vkml_gemv_dot_params op{1, u32(L.o.rows), u32(L.o.cols), L.o.type_code(), L.o.scale_code()};
+                check(vkml_attend_step_o(&sp, static_cast<const float*>(qkv.data()), static_cast<const float*>(rope.data()),
+                                         L.k_cache.data(), L.v_cache.data(), static_cast<float*>(partial.data()),
+                                         static_cast<float*>(stats.data()), static_cast<float*>(attn.data()), aq.data(),
+                                         static_cast<float*>(as.data()), st, &op, L.o.values(), L.o.scales(), xp,
+                                         static_cast<std::uint32_t*>(o_sync.data())),
+                      "attention");
+            } else {
+                check(vkml_attend_step(&sp, static_cast<const float*>(qkv.data()), static_cast<const float*>(rope.data()), L.k_cache.data(),
+                                       L.v_cache.data(), static_cast<float*>(partial.data()), static_cast<float*>(stats.data()),
+                                       static_cast<float*>(attn.data()), o_q ? aq.data() : nullptr,
+                                       o_q ? static_cast<float*>(as.data()) : nullptr, st),
+                      "attention");
+                project(L.o, attn, o_q ? &aq : nullptr, &as, xp, xp, "o");
+            }
             auto* hp = static_cast<float*>(h.data());
             const bool down_q = quantized_input(L.down) && ff % 32 == 0;
             bool h_quantized = false;
@@ -638,6 +652,7 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
     m.ytmp = f32(d);
     m.logits = f32(c.vocab_size);
     m.state = Tensor::zeros(context, {4}, DType::I32);
+    m.o_sync = Tensor::zeros(context, {static_cast<std::int64_t>(vkml_attend_o_sync_bytes() / 4)}, DType::I32);
     m.log = Tensor::zeros(context, {context_length}, DType::I32);
     m.chunks = (context_length + 127) / 128;
     m.partial = f32(c.num_heads * m.chunks * hd);

@@ -464,19 +464,24 @@ __device__ __forceinline__ void merge_head(const float* partial, const float* st
     const uint64_t first = static_cast<uint64_t>(h) * stride;
     const uint64_t* st = reinterpret_cast<const uint64_t*>(stats) + first;  // (max, weight sum) pairs
     const float* pc = partial + first * hd + d;
+    // This thread's first chunk's (max, weight sum), loaded before the
+    // partials so that waiting for it does not wait for them, and kept for
+    // the factors below (later chunks of a thread, past hd chunks, are
+    // loaded again there).
+    const uint64_t ml0 = ld_u64<COH>(st + min(d, count - 1));
     float p[B];
 #pragma unroll
     for (uint32_t j = 0; j < B; ++j) p[j] = ld_f32<COH>(pc + static_cast<uint64_t>(min(j, count - 1)) * hd);
     // M = max over the chunks' maxima (exact in any order).
-    float m = -__builtin_inff();
-    for (uint32_t c = d; c < count; c += nt) m = fmaxf(m, __uint_as_float(static_cast<uint32_t>(ld_u64<COH>(st + c))));
+    float m = d < count ? __uint_as_float(static_cast<uint32_t>(ml0)) : -__builtin_inff();
+    for (uint32_t c = d + nt; c < count; c += nt) m = fmaxf(m, __uint_as_float(static_cast<uint32_t>(ld_u64<COH>(st + c))));
     m = wave_max(m);
     if (d % kWave == 0) s_wmax[d / kWave] = m;
     __syncthreads();
     float top = s_wmax[0];
     for (uint32_t w = 1; w < (nt + kWave - 1) / kWave; ++w) top = fmaxf(top, s_wmax[w]);
     for (uint32_t c = d; c < count; c += nt) {
-        const uint64_t ml = ld_u64<COH>(st + c);
+        const uint64_t ml = c == d ? ml0 : ld_u64<COH>(st + c);
         const float mc = __uint_as_float(static_cast<uint32_t>(ml)), lc = __uint_as_float(static_cast<uint32_t>(ml >> 32));
         s_r[c] = mc == -__builtin_inff() ? -1.0f : vk_expf(mc - top);
         s_l[c] = lc;

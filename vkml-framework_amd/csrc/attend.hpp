@@ -80,6 +80,18 @@ __device__ __forceinline__ float dot4f(float4 a, float4 b) {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
+// The same with b four f16 values (two per word), each product as
+// fma(a, b, nz) with nz = -0: exact products rounded once, as a * b, where
+// the f16 operand is widened inside v_fma_mix_f32 (nz comes from an asm, so
+// the fma is not folded back into a multiply).
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot4h(float4 a, uint2 b, float nz) {
+#pragma clang fp contract(off)
+    const half2_t lo = __builtin_bit_cast(half2_t, b.x), hi = __builtin_bit_cast(half2_t, b.y);
+    return __builtin_fmaf(a.x, static_cast<float>(lo.x), nz) + __builtin_fmaf(a.y, static_cast<float>(lo.y), nz) +
+           __builtin_fmaf(a.z, static_cast<float>(hi.x), nz) + __builtin_fmaf(a.w, static_cast<float>(hi.y), nz);
+}
+
 __device__ __forceinline__ uint32_t cache_bits(float v, bool f16) {
     return f16 ? f32_to_f16_bits(__float_as_uint(v)) : __float_as_uint(v);
 }
@@ -276,6 +288,9 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     }
     __syncthreads();
 
+    // -0 for the products of f32 and f16 values taken as fma(a, b, -0) (dot4h)
+    float nz = -0.0f;
+    asm volatile("" : "+v"(nz));
     // Scores: part g of each head, then ((0 + p0) + p1) + p2) + p3; heads
     // two at a time (their q in registers), sharing the K registers.
     constexpr int HB = HPW < 2 ? HPW : 2;
@@ -298,15 +313,18 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
             for (int h = 0; h < HB; ++h) part[h] = 0.0f;
 #pragma unroll
             for (uint32_t j = 0; j < KPL; ++j) {
-                float4 kv = widen(ld.k[p][j]);
+                KRaw<F16> kw = ld.k[p][j];
                 if (fresh) {
                     const uint32_t i = lane4 + kLanes * j;
-                    if constexpr (F16) kv = widen(make_uint2(sm.knew[4 * i] | (sm.knew[4 * i + 1] << 16), sm.knew[4 * i + 2] | (sm.knew[4 * i + 3] << 16)));
-                    else kv = make_float4(__uint_as_float(sm.knew[4 * i]), __uint_as_float(sm.knew[4 * i + 1]),
+                    if constexpr (F16) kw = make_uint2(sm.knew[4 * i] | (sm.knew[4 * i + 1] << 16), sm.knew[4 * i + 2] | (sm.knew[4 * i + 3] << 16));
+                    else kw = make_float4(__uint_as_float(sm.knew[4 * i]), __uint_as_float(sm.knew[4 * i + 1]),
                                           __uint_as_float(sm.knew[4 * i + 2]), __uint_as_float(sm.knew[4 * i + 3]));
                 }
 #pragma unroll
-                for (int h = 0; h < HB; ++h) part[h] += dot4f(qr[h][j], kv);
+                for (int h = 0; h < HB; ++h) {
+                    if constexpr (F16) part[h] += dot4h(qr[h][j], kw, nz);
+                    else part[h] += dot4f(qr[h][j], kw);
+                }
             }
 #pragma unroll
             for (int h = 0; h < HB; ++h) {
@@ -363,12 +381,7 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
         if constexpr (F16) return f16_bits_to_float(ldg(static_cast<const uint16_t*>(a.v_cache) + row_of(key) * HD + d));
         else return ldg(static_cast<const float*>(a.v_cache) + row_of(key) * HD + d);
     };
-    // w * v as fma(w, v, -0): the same rounded product (exact plus -0 keeps
-    // every result, signed zeros included), and with an f16 v one
-    // v_fma_mix_f32 that widens v as it multiplies. -0 comes through an asm
-    // so that the fma is not folded back into a multiply.
-    float nz = -0.0f;
-    asm volatile("" : "+v"(nz));
+    // w * v as fma(w, v, -0) for an f16 v, as in dot4h.
     const auto prod = [&](float w, float x) {
         if constexpr (F16 && kStageV) return __builtin_fmaf(w, x, nz);
         else return w * x;

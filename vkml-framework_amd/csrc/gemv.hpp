@@ -36,6 +36,8 @@
 // are matrix-vector products, bound by HBM.
 #pragma once
 
+#include <type_traits>
+
 #include "../../include/vkml_hip.h"
 #include "device.hpp"
 
@@ -669,22 +671,58 @@ struct GemvRows {
 // scale) per half-block, then the norm's 257 floats.
 __host__ __device__ constexpr uint32_t stage_bytes(uint32_t k, bool norm) { return k + k / 16 * 8 + (norm ? 257 * 4 : 0); }
 
-// Stages the activation in LDS (smem, 16-byte aligned): with NORM, RMSNorm +
-// Q8_0 of g.x computed here (norm_quantize_prologue); otherwise the codes
-// and scales read from g.a_values / g.a_scales. Ends with a barrier.
+// The activation's loads (the Q8_0 codes and scales of up to 4 T
+// half-blocks; or with NORM, the prologue's loads), issued by a kernel
+// before its first weight loads: loads complete in order, so waiting for
+// these then does not wait for the weights, which stay in flight while the
+// activation is staged.
+template <uint32_t T>
+struct ActLoads {
+    uint4 c[4];
+    float sa[4];
+};
+template <uint32_t T, bool NORM>
+using StageLoads = std::conditional_t<NORM, NormLoads<T>, ActLoads<T>>;
+
 template <uint32_t T, bool NORM, bool COH>
-__device__ __forceinline__ void stage_activation(const GemvArgs& g, uint4* smem) {
+__device__ __forceinline__ void stage_load(const GemvArgs& g, StageLoads<T, NORM>& r) {
+    if constexpr (NORM) {
+        norm_loads<T, COH>(g.x, g.norm_weight, g.k, r);
+    } else {
+        const uint32_t halves = g.k / 16, t = thread_index();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t h = t + i * T;
+            r.c[i] = h < halves ? ld_u128<COH>(g.a_values + h) : make_uint4(0, 0, 0, 0);
+            r.sa[i] = h < halves ? ld_f32<COH>(g.a_scales + h / 2) : 0.0f;
+        }
+    }
+}
+
+// Stages the activation in LDS (smem, 16-byte aligned) from stage_load's
+// registers: with NORM, RMSNorm + Q8_0 of g.x computed here
+// (norm_quantize_prologue); otherwise the codes, and per half-block its
+// (code sum, block scale), with half-blocks past 4 T loaded here. Ends with
+// a barrier.
+template <uint32_t T, bool NORM, bool COH>
+__device__ __forceinline__ void stage_store(const GemvArgs& g, uint4* smem, const StageLoads<T, NORM>& r) {
     const uint32_t K = g.k;
     uint4* s_codes = smem;                                     // K / 16 half-blocks of codes
     float2* s_ss = reinterpret_cast<float2*>(smem + K / 16);   // each half-block's (code sum, block scale)
     const uint32_t halves = K / 16, t = thread_index();
     if constexpr (NORM) {
-        NormLoads<T> nl;
-        norm_loads<T, COH>(g.x, g.norm_weight, K, nl);
         float* s_red = reinterpret_cast<float*>(s_ss + K / 16);  // 257 floats
-        norm_quantize_prologue<T>(nl, g.eps, K, s_codes, s_ss, s_red);
+        norm_quantize_prologue<T>(r, g.eps, K, s_codes, s_ss, s_red);
     } else {
-        for (uint32_t h0 = t; h0 < halves; h0 += 4 * T) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t h = t + i * T;
+            if (h < halves) {
+                s_codes[h] = r.c[i];
+                s_ss[h] = make_float2(static_cast<float>(byte_sum(r.c[i])), r.sa[i]);
+            }
+        }
+        for (uint32_t h0 = t + 4 * T; h0 < halves; h0 += 4 * T) {
             uint4 c[4];
             float sa[4];
 #pragma unroll
@@ -704,6 +742,14 @@ __device__ __forceinline__ void stage_activation(const GemvArgs& g, uint4* smem)
         }
     }
     __syncthreads();
+}
+
+// stage_load then stage_store.
+template <uint32_t T, bool NORM, bool COH>
+__device__ __forceinline__ void stage_activation(const GemvArgs& g, uint4* smem) {
+    StageLoads<T, NORM> r;
+    stage_load<T, NORM, COH>(g, r);
+    stage_store<T, NORM, COH>(g, smem, r);
 }
 
 __device__ __forceinline__ const float2* staged_ss(const uint4* smem, uint32_t k) { return reinterpret_cast<const float2*>(smem + k / 16); }

@@ -417,10 +417,12 @@ __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint3
         r.xq[i] = ld_f32x4<COH>(reinterpret_cast<const float4*>(x) + q);
         r.wq[i] = ldg(reinterpret_cast<const float4*>(w) + q);
     }
+    if (T <= 256 || t < 256) {  // threads past the 256 invocations load none
 #pragma unroll
-    for (uint32_t v = 0; v < NormLoads<T>::V; ++v)
+        for (uint32_t v = 0; v < NormLoads<T>::V; ++v)
 #pragma unroll
-        for (uint32_t j = 0; j < NormLoads<T>::kMaxPer; ++j) r.xv[v][j] = ld_f32<COH>(x + min((t + v * T) % 256 + 256 * j, K - 1));
+            for (uint32_t j = 0; j < NormLoads<T>::kMaxPer; ++j) r.xv[v][j] = ld_f32<COH>(x + min((t + v * T) % 256 + 256 * j, K - 1));
+    }
 }
 
 template <uint32_t T>

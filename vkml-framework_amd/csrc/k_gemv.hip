@@ -36,7 +36,9 @@ __global__ void __launch_bounds__(T) k_gemv_dot(GemvArgs g) {
 template <int FMT, bool F16S, int LPR, int EPI, bool NORM, bool QOUT>
 int launch(const GemvArgs& g, const char* label) {
     constexpr int B = LPR == 16 ? 4 : 2;  // rounds per batch (2 measured best at 32 lanes)
-    constexpr uint32_t T = QOUT ? 32 * LPR : LPR == 32 ? 256 : 128;
+    // (512 threads with the norm prologue at 32 lanes: half the workgroups
+    // redo RMSNorm + Q8_0 of x, each over twice the threads)
+    constexpr uint32_t T = QOUT ? 32 * LPR : LPR == 32 ? (NORM ? 512 : 256) : 128;
     const dim3 grid((g.n + T / LPR - 1) / (T / LPR));
     const size_t lds = stage_bytes(g.k, NORM);
     vkml::abi::ProfileScope prof(label);

@@ -207,8 +207,9 @@ def test_gemv_fused_norm_prologue_bit_exact(fmt, n, k):
 
 
 @pytest.mark.parametrize("norm", [0, 1])
-@pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 14336, 4096), (H.Q4_K, 512, 256), (H.Q8_0, 2048, 1024)])
+@pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 14336, 4096), (H.Q4_K, 512, 256), (H.Q8_0, 2048, 1024), (H.Q4_K, 1056, 512)])
 def test_gemv_fused_swiglu_quantized_output_bit_exact(norm, fmt, n, k):
+    # (n = 1056: 33 of the epilogue's 32-row Q8_0 blocks)
     v, s, quant, words, scales = weights(fmt, n, k, 41)
     v2, s2, _, words2, scales2 = weights(fmt, n, k, 42)
     rng = np.random.default_rng(n)

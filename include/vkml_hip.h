@@ -188,6 +188,15 @@ typedef struct vkml_gemv_dot_params {
 } vkml_gemv_dot_params;
 int vkml_gemv_dot(const vkml_gemv_dot_params* p, const void* d_a_values, const void* d_b_values,
                   float* d_out, const void* d_b_scales, const float* d_a_scales);
+/* shaders/matmul_dot.comp (src/ops/matmul.cpp:246-259): c = a_q . b^T for
+ * any m (the reference's path for m > 8: prompts), in its order: each
+ * output sums K's 32-value blocks in order, the block's exact integer dot
+ * product scaled in f32 (q8_0 / q4_0: float(sum) * (sa * sb); q4_1 / q4_K:
+ * sa * (float(sum) * sb + float(asum) * offset)). Arguments as
+ * vkml_gemv_dot's; k a multiple of 32 (q4_K: 256). On the matrix cores
+ * (v_mfma_i32_16x16x32_i8: one block of a 16 x 16 tile). */
+int vkml_matmul_dot(const vkml_gemv_dot_params* p, const void* d_a_values, const void* d_b_values,
+                    float* d_out, const void* d_b_scales, const float* d_a_scales);
 /* As vkml_gemv_dot for m = 1, with the residual add that follows the o and
  * down projections (llama.cpp:374,386) done in the epilogue:
  * d_out[n] = d_residual[n] + a_q . b[n] (d_out may equal d_residual). */

@@ -171,6 +171,23 @@ def test_gemv_dot_f32_scales_and_several_rows(fmt):
     assert np.array_equal(bits(got), bits(O.gemv_dot(quant, aw, asc, m, words, scales, n, k)))
 
 
+@pytest.mark.parametrize("fmt,f16", [(H.Q8_0, True), (H.Q8_0, False), (H.Q4_0, True), (H.Q4_1, True), (H.Q4_1, False), (H.Q4_K, True)])
+@pytest.mark.parametrize("m,n,k", [(9, 64, 256), (37, 100, 512), (130, 1000, 2048), (512, 4096, 4096)])
+def test_matmul_dot_bit_exact(fmt, f16, m, n, k):
+    # matmul_dot.comp's order (the reference's int8 product for m > 8) on the
+    # matrix cores, against the oracle bit for bit, and within the f32 dot
+    # bound of the exact product; ragged tiles at m = 9, 37, 130 and n = 100, 1000
+    v, s, quant, words, scales = weights(fmt, n, k, m + n, f16_scales=f16)
+    a, aw, asc = activation(k, m, m)
+    out = H.empty(m * n * 4)
+    H.call("vkml_matmul_dot", H.GemvDotParams(m, n, k, fmt, H.F16 if f16 else H.F32), p(dev(aw)), p(v), p(out), p(s), p(dev(asc)))
+    got = out.download(np.float32, (m, n))
+    assert np.array_equal(bits(got), bits(O.matmul_dot(quant, aw, asc, m, words, scales, n, k)))
+    if m <= 130:
+        exact, bound = dot_bound(aw, asc, m, k, quant, words, scales, n)
+        assert np.all(np.abs(got - exact) <= bound)
+
+
 @pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_K])
 def test_gemv_dot_add_and_swiglu(fmt):
     n, k = 1024, 4096

@@ -1,0 +1,214 @@
+// k_matmul.hip -- the int8 matrix product for many rows (prefill): the
+// reference's shaders/matmul_dot.comp (src/ops/matmul.cpp:246-259), c = a b^T
+// with a [M, K] Q8_0 activations (f32 scales) and b [N, K] quantized weights,
+// on gfx950's matrix cores.
+//
+// Order (matmul_dot.comp:134-160). Each output is a sum over K's 32-value
+// blocks in order: the block's exact integer dot product of the two codes,
+// scaled in f32 and added to the output's accumulator,
+//   q8_0 / q4_0: acc += float(sum) * (sa * sb)
+//   q4_1 / q4_K: acc += sa * (float(sum) * sb + float(asum) * ob)
+// (asum: the block's sum of a's codes; q4_K as its q4_1 form, scale
+// f16(d sc) and offset f16(-dmin m) per 32 values, src/io/gguf.cpp:603-617).
+// One v_mfma_i32_16x16x32_i8 computes the integer sums of one block for a
+// 16 x 16 tile of outputs exactly, so the matrix cores do the dot products
+// and the VALU applies the scales per block, in the reference's order.
+//
+// Mapping. A workgroup (four waves) computes a 64 x 64 tile of c, each wave
+// 32 x 32 (2 x 2 matrix instructions). Lane l of a wave holds, for a 16 x 16
+// instruction, a's row l % 16 and b's column l % 16 at the block's values
+// 8 (l / 16) .. 8 (l / 16) + 7 (one 8-byte operand each), and the results for
+// rows 4 (l / 16) .. + 3 of column l % 16. The operands are loaded straight
+// from memory (L2 serves the reuse across workgroups); each block's per-row
+// (code sum, scale) of a is staged in LDS once per workgroup.
+#include <algorithm>
+
+#include "../../include/vkml_hip.h"
+#include "device.hpp"
+#include "internal.hpp"
+
+using namespace vkml::dev;
+
+namespace {
+
+constexpr uint32_t kT = 256;      // four waves
+constexpr uint32_t kTileM = 64, kTileN = 64;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct MatmulDotArgs {
+    const uint8_t* a;     // [M, K] activation codes
+    const float* a_scales;  // [M, K / 32]
+    const uint8_t* b;     // weight codes (layout per format)
+    const void* b_scales;  // per-block scales (q4_K: the 16-byte super-block headers)
+    float* out;           // [M, N]
+    uint32_t m, n, k;
+};
+
+__device__ __forceinline__ float f16_at(const void* p, uint64_t i) { return f16_bits_to_float(ldg(static_cast<const uint16_t*>(p) + i)); }
+
+// Four Q4_0 values as signed bytes, the low (shift 0) or high (shift 4)
+// nibbles of a word minus 8 (matmul_dot.comp:71-73).
+__device__ __forceinline__ uint32_t q4_signed(uint32_t word, uint32_t shift) {
+    return (((word >> shift) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+}
+
+// Column n's operand for block blk: its 8 codes at values 8 g .. 8 g + 7 of
+// the block, as int8 (q4: codes 0 .. 15, or minus 8 for q4_0), and the
+// block's scale and offset.
+template <int FMT, bool F16S>
+__device__ __forceinline__ long b_operand(const MatmulDotArgs& p, uint32_t n, uint32_t blk, uint32_t g, float& s, float& o) {
+    const uint32_t blocks = p.k / 32;
+    const uint64_t block = static_cast<uint64_t>(n) * blocks + blk;
+    uint32_t lo, hi;
+    o = 0.0f;
+    if constexpr (FMT == VKML_Q8_0) {
+        const uint2 w = ldg(reinterpret_cast<const uint2*>(p.b + static_cast<uint64_t>(n) * p.k + blk * 32 + 8 * g));
+        lo = w.x;
+        hi = w.y;
+        s = F16S ? f16_at(p.b_scales, block) : ldg(static_cast<const float*>(p.b_scales) + block);
+    } else if constexpr (FMT == VKML_Q4_K) {
+        // sub-block j = blk % 8 of super-block blk / 8: low (j even) or high
+        // nibbles of bytes 32 (j / 2) .. of its 128
+        const uint32_t j = blk % 8, sb = blk / 8;
+        const uint2 w = ldg(reinterpret_cast<const uint2*>(p.b + static_cast<uint64_t>(n) * (p.k / 2) + sb * 128 + 32 * (j / 2) + 8 * g));
+        const uint32_t sh = 4 * (j % 2);
+        lo = (w.x >> sh) & 0x0F0F0F0Fu;
+        hi = (w.y >> sh) & 0x0F0F0F0Fu;
+        const uint4 h = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.b_scales) +
+                                                           (static_cast<uint64_t>(n) * (p.k / 256) + sb) * 16));
+        const uint32_t b = 8 * (j % 4);
+        const uint32_t b1 = (h.y >> b) & 0xFFu, b2 = (h.z >> b) & 0xFFu, b3 = (h.w >> b) & 0xFFu;
+        const uint32_t sc = j < 4 ? b1 & 63u : (b3 & 15u) | ((b1 >> 6) << 4);
+        const uint32_t mn = j < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
+        const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h.x & 0xFFFFu));
+        const _Float16 nd = -__builtin_bit_cast(_Float16, static_cast<uint16_t>(h.x >> 16));
+        s = static_cast<float>(d * static_cast<_Float16>(static_cast<uint16_t>(sc)));
+        o = static_cast<float>(nd * static_cast<_Float16>(static_cast<uint16_t>(mn)));
+    } else {
+        // QuantizedMatrix q4 words: word w' of the block holds values 8 w' .. 8 w' + 7,
+        // low nibbles the first four, high the last four
+        const uint32_t q = ldg(reinterpret_cast<const uint32_t*>(p.b + static_cast<uint64_t>(n) * (p.k / 2) + blk * 16 + 4 * g));
+        if constexpr (FMT == VKML_Q4_0) {
+            lo = q4_signed(q, 0);
+            hi = q4_signed(q, 4);
+            s = F16S ? f16_at(p.b_scales, block) : ldg(static_cast<const float*>(p.b_scales) + block);
+        } else {
+            lo = q & 0x0F0F0F0Fu;
+            hi = (q >> 4) & 0x0F0F0F0Fu;
+            if constexpr (F16S) {
+                const uint32_t so = ldg(static_cast<const uint32_t*>(p.b_scales) + block);  // f16 scale | f16 offset << 16
+                s = f16_bits_to_float(so & 0xFFFFu);
+                o = f16_bits_to_float(so >> 16);
+            } else {
+                const float2 so = ldg(static_cast<const float2*>(p.b_scales) + block);
+                s = so.x;
+                o = so.y;
+            }
+        }
+    }
+    return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <int FMT, bool F16S>
+__global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
+#pragma clang fp contract(off)
+    constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
+    __shared__ float2 s_row[2][kTileM];  // per block: each row's (code sum, scale), double-buffered
+    const uint32_t t = thread_index(), lane = t % kWave, wave = t / kWave;
+    const uint32_t g = lane / 16, li = lane % 16;
+    const uint32_t row0 = blockIdx.y * kTileM, col0 = blockIdx.x * kTileN;
+    const uint32_t wr = row0 + 32 * (wave / 2), wc = col0 + 32 * (wave % 2);  // the wave's 32 x 32 tile
+    const uint32_t blocks = p.k / 32;
+    float acc[2][2][4];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[r][c][i] = 0.0f;
+    for (uint32_t blk = 0; blk < blocks; ++blk) {
+        float2* rows = s_row[blk % 2];
+        if (t < kTileM) {
+            const uint32_t row = min(row0 + t, p.m - 1);
+            const uint4* codes = reinterpret_cast<const uint4*>(p.a + static_cast<uint64_t>(row) * p.k + blk * 32);
+            const float sa = ldg(p.a_scales + static_cast<uint64_t>(row) * blocks + blk);
+            float sum = 0.0f;
+            if constexpr (kOffset) sum = static_cast<float>(byte_sum(ldg(codes)) + byte_sum(ldg(codes + 1)));
+            rows[t] = make_float2(sum, sa);
+        }
+        long av[2], bv[2];
+        float sb[2], ob[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const uint32_t row = min(wr + 16 * r + li, p.m - 1);
+            av[r] = static_cast<long>(__builtin_bit_cast(uint64_t, ldg(reinterpret_cast<const uint2*>(p.a + static_cast<uint64_t>(row) * p.k +
+                                                                                                      blk * 32 + 8 * g))));
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) bv[c] = b_operand<FMT, F16S>(p, min(wc + 16 * c + li, p.n - 1), blk, g, sb[c], ob[c]);
+        __syncthreads();  // rows[] of this block is written (the other buffer's readers finished a block ago)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float2 ra = rows[32 * (wave / 2) + 16 * r + 4 * g + i];  // (code sum, scale) of the output's row
+                    if constexpr (kOffset) {
+                        acc[r][c][i] += ra.y * (static_cast<float>(d[i]) * sb[c] + ra.x * ob[c]);
+                    } else {
+                        acc[r][c][i] += static_cast<float>(d[i]) * (ra.y * sb[c]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint32_t col = wc + 16 * c + li;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t row = wr + 16 * r + 4 * g + i;
+                if (row < p.m && col < p.n) p.out[static_cast<uint64_t>(row) * p.n + col] = acc[r][c][i];
+            }
+        }
+}
+
+template <int FMT, bool F16S>
+void launch(const MatmulDotArgs& p) {
+    const dim3 grid((p.n + kTileN - 1) / kTileN, (p.m + kTileM - 1) / kTileM);
+    hipLaunchKernelGGL((k_matmul_dot<FMT, F16S>), grid, dim3(kT), 0, vkml::abi::stream(), p);
+}
+
+}  // namespace
+
+extern "C" {
+
+int vkml_matmul_dot(const vkml_gemv_dot_params* p, const void* a_values, const void* b_values, float* out, const void* b_scales,
+                    const float* a_scales) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "matmul_dot: null params");
+    VKML_CHECK_ARG(p->b_type == VKML_Q8_0 || p->b_type == VKML_Q4_0 || p->b_type == VKML_Q4_1 || p->b_type == VKML_Q4_K,
+                   "matmul_dot: weights must be q8_0, q4_0, q4_1 or q4_K, got type " + std::to_string(p->b_type));
+    VKML_CHECK_ARG(p->b_type == VKML_Q4_K || p->scale_type == VKML_F16 || p->scale_type == VKML_F32, "matmul_dot: scales must be f16 or f32");
+    const uint32_t unit = p->b_type == VKML_Q4_K ? 256 : 32;
+    VKML_CHECK_ARG(p->k > 0 && p->k % unit == 0, "matmul_dot: k = " + std::to_string(p->k) + " must be a positive multiple of " + std::to_string(unit));
+    if (p->m == 0 || p->n == 0) return VKML_OK;
+    VKML_CHECK_ARG(a_values && b_values && out && b_scales && a_scales, "matmul_dot: null buffer");
+    const MatmulDotArgs args{static_cast<const uint8_t*>(a_values), a_scales, static_cast<const uint8_t*>(b_values), b_scales, out,
+                             p->m, p->n, p->k};
+    vkml::abi::ProfileScope prof("matmul_dot");
+    const bool f16 = p->scale_type == VKML_F16;
+    switch (p->b_type) {
+        case VKML_Q8_0: f16 ? launch<VKML_Q8_0, true>(args) : launch<VKML_Q8_0, false>(args); break;
+        case VKML_Q4_0: f16 ? launch<VKML_Q4_0, true>(args) : launch<VKML_Q4_0, false>(args); break;
+        case VKML_Q4_1: f16 ? launch<VKML_Q4_1, true>(args) : launch<VKML_Q4_1, false>(args); break;
+        default: launch<VKML_Q4_K, true>(args); break;
+    }
+    return vkml::abi::check_launch("matmul_dot");
+}
+
+}  // extern "C"

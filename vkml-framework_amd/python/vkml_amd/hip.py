@@ -110,6 +110,7 @@ SIGNATURES = {
     "vkml_dequantize": [P(DequantizeParams), vp, vp, vp],
     "vkml_gemv_dot": [P(GemvDotParams), vp, vp, vp, vp, vp],
     "vkml_gemv_dot_add": [P(GemvDotParams), vp, vp, vp, vp, vp, vp],
+    "vkml_matmul_dot": [P(GemvDotParams), vp, vp, vp, vp, vp],
     "vkml_gemv_dot_swiglu": [P(GemvDotParams), vp, vp, vp, vp, vp, vp, vp],
     "vkml_gemv": [P(GemvParams), vp, vp, vp, vp],
     "vkml_matmul": [P(MatmulParams), vp, vp, vp],

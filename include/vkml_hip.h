@@ -238,18 +238,29 @@ int vkml_gemv_fused(const vkml_gemv_fused_params* p, const void* d_a, const floa
 /* shaders/gemv.comp, src/ops/matmul.cpp:88-120: the float path, c[m, n] =
  * a[m] . b[n] with f32 a (m <= 8) and b [n, k] of b_type F32/F16/BF16 or
  * Q8_0/Q4_0/Q4_1/Q4_K decoded in registers (ContextOptions::
- * integer_dot_product off, and f32 models). */
+ * integer_dot_product off, and f32 models). With batches > 1 (float b
+ * only) as gemv.comp's z: a [batches, m, k], c [batches, m, n], batch z
+ * against b's batch z / b_group, b_stride elements apart (attention's
+ * scores for up to 8 queries, matmul.cpp:96). batches and b_group 0 mean 1. */
 typedef struct vkml_gemv_params {
     uint32_t m, n, k;
     uint32_t b_type;
     uint32_t scale_type;
+    uint32_t b_stride;
+    uint32_t b_group;
+    uint32_t batches;
 } vkml_gemv_params;
 int vkml_gemv(const vkml_gemv_params* p, const float* d_a, const void* d_b, float* d_out,
               const void* d_b_scales);
 
 /* shaders/matmul.comp (src/ops/matmul.cpp:44-120): c = a . b or a . b^T for
  * f32 a [batches * b_group, m, k] and b [batches, k, n] (or [n, k]) of b_type
- * F32/F16/BF16; b_stride elements between b's batches (0: shared b). */
+ * F32/F16/BF16; b_stride elements between b's batches (0: shared b). Each
+ * output sums its k products in k order. b may also be one transposed
+ * quantized matrix (Q8_0/Q4_0/Q4_1/Q4_K, scales of scale_type in d_b_scales,
+ * values widened as vkml_gemv's): the float path's projections of more than
+ * 8 rows (matmul.cpp:96-97). Argument order is the reference's buffers
+ * (a, b, c, scales; matmul.cpp:107). */
 typedef struct vkml_matmul_params {
     uint32_t m, n, k;
     uint32_t b_stride;
@@ -257,8 +268,10 @@ typedef struct vkml_matmul_params {
     uint32_t batches;
     uint32_t b_transposed;
     uint32_t b_type;
+    uint32_t scale_type;
 } vkml_matmul_params;
-int vkml_matmul(const vkml_matmul_params* p, const float* d_a, const void* d_b, float* d_out);
+int vkml_matmul(const vkml_matmul_params* p, const float* d_a, const void* d_b, float* d_out,
+                const void* d_b_scales);
 
 /* shaders/rms_norm.comp, src/ops/norms.cpp:230-253. */
 typedef struct vkml_rms_norm_params {
@@ -460,6 +473,14 @@ typedef struct vkml_rope_kv_params {
 int vkml_rope_kv_append(const vkml_rope_kv_params* p, const float* d_qkv, const float* d_table,
                         float* d_q, void* d_k_cache, void* d_v_cache,
                         const vkml_decode_state* d_state);
+/* The same for a prompt of `tokens` tokens at positions p->position..: row
+ * t of d_qkv (row_stride floats apart) holds token t's q | k | v; q is
+ * rotated into d_q [heads, tokens, head_dim] (heads first, llama.cpp:
+ * 320-327), k rotated and v rounded to the cache type and written at rows
+ * position + t (llama.cpp:344-355). position + tokens <= capacity. */
+int vkml_rope_kv_prompt(const vkml_rope_kv_params* p, uint32_t tokens, uint32_t row_stride,
+                        const float* d_qkv, const float* d_table, float* d_q, void* d_k_cache,
+                        void* d_v_cache);
 
 /* Decode-state helpers for the replayable step: set the state, embed its
  * token, and finish the step (argmax into the state and a token log, then

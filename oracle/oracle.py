@@ -60,6 +60,7 @@ def _declare(L):
         "orc_gemv_dot": (None, [i32, i32, vp, vp, i64, vp, vp, i64, i64, vp]),
         "orc_matmul_dot": (None, [i32, i32, vp, vp, i64, vp, vp, i64, i64, vp]),
         "orc_gemv_float": (None, [i32, i32, vp, i64, vp, vp, i64, i64, vp]),
+        "orc_matmul_float": (None, [i32, i32, vp, i64, vp, vp, i64, i64, vp]),
         "orc_rms_norm": (None, [vp, vp, i64, i64, f32, vp]),
         "orc_rope_table": (None, [i64, i64, f32, vp]),
         "orc_rope": (None, [vp, vp, i64, i64, i64, i64, i64, i64, i32, vp]),
@@ -69,10 +70,12 @@ def _declare(L):
         "orc_argmax": (C.c_int32, [vp, i64]),
         "orc_embedding_quantized": (None, [i32, vp, vp, i64, i64, vp, i64, vp]),
         "orc_attend_decode": (None, [vp, i64, vp, vp, i32, i64, i64, i64, i64, i64, f32, vp]),
-        "orc_attention_prefill": (None, [vp, i64, i64, vp, vp, i32, i64, i64, i64, i64, vp]),
+        "orc_attention_prefill": (None, [vp, i64, i64, vp, vp, i32, i64, i64, i64, i64, i64, vp]),
         "orc_model_load": (vp, [C.c_char_p, i64, i32, i32]),
         "orc_model_free": (None, [vp]),
         "orc_model_forward": (i32, [vp, vp, i64, vp]),
+        "orc_model_forward_all": (i32, [vp, vp, i64, vp]),
+        "orc_model_set_max_score_bytes": (None, [vp, i64]),
         "orc_model_position": (i64, [vp]),
         "orc_model_set_position": (i32, [vp, i64]),
         "orc_model_rewind": (i64, [vp, i64]),
@@ -194,6 +197,32 @@ def gemv_float(b_type, a, b, b_scales, N, K) -> np.ndarray:
     return out
 
 
+def matmul_float(b_type, a, b, b_scales, N, K) -> np.ndarray:
+    """matmul.comp with b [N, K] transposed: a [M, K] f32, sums in k order."""
+    a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1, K)
+    b = np.ascontiguousarray(b)
+    sc = None if b_scales is None else np.ascontiguousarray(b_scales)
+    f16 = int(sc is not None and sc.dtype == np.uint16)
+    out = np.empty((a.shape[0], N), np.float32)
+    lib().orc_matmul_float(b_type, f16, _p(a), a.shape[0], _p(b), _p(sc), N, K, _p(out))
+    return out
+
+
+def attention_prefill(q, k_cache, v_cache, kv_len: int, max_score_bytes: int = 64 << 20) -> np.ndarray:
+    """q [heads, q_len, hd] f32; caches [kv_heads, capacity, hd] f32 or uint16
+    (f16 bits); query i at key position kv_len - q_len + i."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    heads, q_len, hd = q.shape
+    kv_heads, capacity = k_cache.shape[0], k_cache.shape[1]
+    f16 = int(k_cache.dtype == np.uint16)
+    k = np.ascontiguousarray(k_cache)
+    v = np.ascontiguousarray(v_cache)
+    out = np.empty((heads, q_len, hd), np.float32)
+    lib().orc_attention_prefill(_p(q), heads, q_len, _p(k), _p(v), f16, kv_heads, capacity, hd, kv_len,
+                                max_score_bytes, _p(out))
+    return out
+
+
 def rms_norm(x, w, eps: float) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     w = np.ascontiguousarray(w, dtype=np.float32)
@@ -278,6 +307,16 @@ class Model:
         if lib().orc_model_forward(self._h, _p(t), t.size, _p(out)) != 0:
             raise RuntimeError(last_error())
         return out
+
+    def forward_all(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((t.size, self.vocab), np.float32)
+        if lib().orc_model_forward_all(self._h, _p(t), t.size, _p(out)) != 0:
+            raise RuntimeError(last_error())
+        return out
+
+    def set_max_score_bytes(self, n: int) -> None:
+        lib().orc_model_set_max_score_bytes(self._h, int(n))
 
     @property
     def position(self) -> int:

@@ -164,6 +164,7 @@ struct orc_model {
     float* rope;
     layer* layers;
     int64_t position;
+    int64_t max_score_bytes; /* attention's score budget (ORC_MAX_SCORE_BYTES) */
 };
 
 static void weight_free(weight* w) { free(w->data); free(w->scales); }
@@ -249,6 +250,7 @@ orc_model* orc_model_load(const char* path, int64_t context_length, int kv_f16, 
         return NULL;
     }
     orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
+    m->max_score_bytes = ORC_MAX_SCORE_BYTES;
     int ok = 1, f;
     m->d = (int64_t)kv_num(g, "llama.embedding_length", 0, &f); ok &= f;
     m->ff = (int64_t)kv_num(g, "llama.feed_forward_length", 0, &f); ok &= f;
@@ -346,7 +348,8 @@ static void project(const orc_model* m, const float* x, int64_t t, act_q* aq, co
     }
     const int elem = w->kind == W_QUANT ? (w->quant == ORC_Q8_0 ? ORC_T_Q8 : w->quant == ORC_Q4_0 ? ORC_T_Q4 : ORC_T_Q4_1)
                                         : w->elem;
-    orc_gemv_float(elem, 1, x, t, w->data, w->scales, w->rows, w->cols, y);
+    if (t <= 8) orc_gemv_float(elem, 1, x, t, w->data, w->scales, w->rows, w->cols, y);
+    else orc_matmul_float(elem, 1, x, t, w->data, w->scales, w->rows, w->cols, y);
 }
 
 static void act_free(act_q* a) { free(a->words); free(a->scales); a->words = NULL; a->scales = NULL; }
@@ -373,8 +376,9 @@ static void embed_rows(const orc_model* m, const int32_t* ids, int64_t t, float*
 }
 
 /* llama.cpp:299-406 for the llama architecture (no biases, q/k norms,
- * sandwich norms, soft caps or sliding windows). */
-int orc_model_forward(orc_model* m, const int32_t* tokens, int64_t t, float* logits) {
+ * sandwich norms, soft caps or sliding windows). all: every row's logits
+ * [t, vocab] (forward_all), else the last row's. */
+static int model_run(orc_model* m, const int32_t* tokens, int64_t t, int all, float* logits) {
     if (t == 0) { orc_error("Llama::forward: no tokens%s", "", 0, 0); return -1; }
     if (m->position + t > m->context) {
         orc_error("Llama::forward: %s%lld tokens exceed the context length of %lld", "",
@@ -429,7 +433,8 @@ int orc_model_forward(orc_model* m, const int32_t* tokens, int64_t t, float* log
         /* detail::attention (attention.cpp:167-227): the fused decode kernel
          * for one query, attention_block otherwise. */
         if (t == 1) orc_attend_decode(qh, H, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, 0, end, 0.0f, att);
-        else orc_attention_prefill(qh, H, t, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, end, att);
+        else orc_attention_prefill(qh, H, t, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, end,
+                                   m->max_score_bytes, att);
         for (int64_t i = 0; i < t; ++i)
             for (int64_t hh = 0; hh < H; ++hh)
                 memcpy(merged + (i * H + hh) * hd, att + (hh * t + i) * hd, (size_t)hd * 4);
@@ -450,14 +455,31 @@ int orc_model_forward(orc_model* m, const int32_t* tokens, int64_t t, float* log
         orc_binary(0, x, y, t * d, t * d, x);
     }
     m->position = end;
-    orc_rms_norm(x + (t - 1) * d, m->final_norm, 1, d, m->eps, h);
+    /* llama.cpp:392-405: the final norm of every row; all rows through the
+     * output projection, or the last row alone. */
     act_q al = {0};
-    project(m, h, 1, &al, &m->lm_head, logits);
+    if (all) {
+        orc_rms_norm(x, m->final_norm, t, d, m->eps, h);
+        project(m, h, t, &al, &m->lm_head, logits);
+    } else {
+        orc_rms_norm(x + (t - 1) * d, m->final_norm, 1, d, m->eps, h);
+        project(m, h, 1, &al, &m->lm_head, logits);
+    }
     act_free(&al);
     free(x); free(h); free(q); free(k); free(v); free(tmp); free(qh); free(att); free(merged);
     free(y); free(gate); free(up);
     return 0;
 }
+
+int orc_model_forward(orc_model* m, const int32_t* tokens, int64_t t, float* logits) {
+    return model_run(m, tokens, t, 0, logits);
+}
+
+int orc_model_forward_all(orc_model* m, const int32_t* tokens, int64_t t, float* logits) {
+    return model_run(m, tokens, t, 1, logits);
+}
+
+void orc_model_set_max_score_bytes(orc_model* m, int64_t bytes) { m->max_score_bytes = bytes; }
 
 /* ------------------------------------------------------------------------ */
 /* Double-precision reference: tests/test_llama.cpp:585-755                  */

@@ -747,6 +747,26 @@ void orc_gemv_float(int t, int f16, const float* a, int64_t M, const void* b, co
     parallel_for(N, gemv_float_range, &c);
 }
 
+/* matmul.comp:117-142 with B_TRANSPOSED: each output sums a[m][k] * b(n, k)
+ * in k order, b widened as load_b does (matmul.comp:74-84); the tiles' zero
+ * padding adds nothing. */
+static void matmul_float_range(void* p, int64_t n0, int64_t n1) {
+    const prod_ctx* c = (const prod_ctx*)p;
+    for (int64_t n = n0; n < n1; ++n) {
+        for (int64_t r = 0; r < c->M; ++r) {
+            float acc = 0.0f;
+            for (int64_t k = 0; k < c->K; ++k) acc += c->af[r * c->K + k] * load_b1(c->t, c->f16, c->b, c->sc, n * c->K + k);
+            c->out[r * c->N + n] = acc;
+        }
+    }
+}
+
+void orc_matmul_float(int t, int f16, const float* a, int64_t M, const void* b, const void* sc,
+                      int64_t N, int64_t K, float* out) {
+    prod_ctx c = {0, f16, NULL, NULL, M, b, sc, N, K, a, t, out};
+    parallel_for(N, matmul_float_range, &c);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Norms, rope, activations, argmax, embeddings                              */
 /* ------------------------------------------------------------------------ */
@@ -946,37 +966,76 @@ void orc_attend_decode(const float* q, int64_t heads, const void* k, const void*
     free(stats);
 }
 
-/* attention.cpp:127-138: scores q k^T, softmax.comp's causal rows (max,
- * sum of exp, times 1/sum), then probs v. Sums run in key order. */
+/* attention.cpp:127-138 (attention_block) for queries q0..q0+rows of head
+ * h against keys 0..keys: scores q k^T through gemv.comp for rows <= 8
+ * (matmul.cpp:96, kGemvMaxRows) and matmul.comp's k order otherwise;
+ * softmax.comp's causal rows (max; sum of exp in the shader's 256-wide
+ * order; times 1/sum); then probs v in key order (matmul.comp). */
+static void prefill_block(const float* q, int64_t q_len, int64_t q0, int64_t rows, int64_t h, const void* k,
+                          const void* v, int f16, int64_t capacity, int64_t hd, int64_t keys,
+                          int64_t kv_row0, float* s, float* out) {
+    const float scale = 1.0f / sqrtf((float)hd);
+    const float* qh = q + (h * q_len + q0) * hd;
+    if (rows <= 8) {
+        const void* kh = f16 ? (const void*)((const uint16_t*)k + kv_row0 * hd) : (const void*)((const float*)k + kv_row0 * hd);
+        orc_gemv_float(f16 ? ORC_T_F16 : ORC_T_F32, 0, qh, rows, kh, NULL, keys, hd, s);
+    } else {
+        for (int64_t i = 0; i < rows; ++i)
+            for (int64_t j = 0; j < keys; ++j) {
+                float acc = 0.0f;
+                for (int64_t c = 0; c < hd; ++c) acc += qh[i * hd + c] * kv_at(k, f16, (kv_row0 + j) * hd + c);
+                s[i * keys + j] = acc;
+            }
+    }
+    (void)capacity;
+    for (int64_t i = 0; i < rows; ++i) {
+        float* si = s + i * keys;
+        const int64_t position = i + keys - rows;
+        const int64_t visible = position + 1 < keys ? position + 1 : keys;
+        float m = -INFINITY;
+        for (int64_t j = 0; j < visible; ++j) m = fmaxf(m, si[j] * scale);
+        /* softmax.comp:104-108: invocation t of 256 sums keys t, t+256, ..;
+         * then the halving tree over the 256 partial sums. */
+        float part[256];
+        for (int64_t t = 0; t < 256; ++t) {
+            float acc = 0.0f;
+            for (int64_t j = t; j < visible; j += 256) acc += orc_expf(si[j] * scale - m);
+            part[t] = acc;
+        }
+        for (int64_t n = 256; n > 1;) {
+            const int64_t half = (n + 1) / 2;
+            for (int64_t t = 0; t < n - half; ++t) part[t] += part[t + half];
+            n = half;
+        }
+        const float inv = 1.0f / part[0];
+        for (int64_t j = 0; j < keys; ++j) si[j] = j < visible ? orc_expf(si[j] * scale - m) * inv : 0.0f;
+        for (int64_t c = 0; c < hd; ++c) {
+            float acc = 0.0f;
+            for (int64_t j = 0; j < keys; ++j) acc += si[j] * kv_at(v, f16, (kv_row0 + j) * hd + c);
+            out[(h * q_len + q0 + i) * hd + c] = acc;
+        }
+    }
+}
+
+/* detail::attention for q_len > 1 (attention.cpp:205-226): queries in chunks
+ * whose scores [heads, rows, kv_len] f32 fit max_score_bytes (a multiple of
+ * 64 rows when at least 64), each chunk over the keys its last query sees. */
 void orc_attention_prefill(const float* q, int64_t heads, int64_t q_len, const void* k,
                            const void* v, int f16, int64_t kv_heads, int64_t capacity, int64_t hd,
-                           int64_t kv_len, float* out) {
+                           int64_t kv_len, int64_t max_score_bytes, float* out) {
     const int64_t group = heads / kv_heads;
-    const float scale = 1.0f / sqrtf((float)hd);
-    float* s = (float*)malloc(sizeof(float) * (size_t)(kv_len > 0 ? kv_len : 1));
-    for (int64_t h = 0; h < heads; ++h) {
-        const int64_t kv_row0 = (h / group) * capacity;
-        for (int64_t i = 0; i < q_len; ++i) {
-            const float* qi = q + (h * q_len + i) * hd;
-            const int64_t position = i + kv_len - q_len;
-            const int64_t visible = position + 1 < kv_len ? position + 1 : kv_len;
-            for (int64_t j = 0; j < kv_len; ++j) {
-                float acc = 0.0f;
-                for (int64_t c = 0; c < hd; ++c) acc += qi[c] * kv_at(k, f16, (kv_row0 + j) * hd + c);
-                s[j] = acc;
-            }
-            float m = -INFINITY;
-            for (int64_t j = 0; j < visible; ++j) m = fmaxf(m, s[j] * scale);
-            float sum = 0.0f;
-            for (int64_t j = 0; j < visible; ++j) sum += orc_expf(s[j] * scale - m);
-            const float inv = 1.0f / sum;
-            for (int64_t j = 0; j < kv_len; ++j) s[j] = j < visible ? orc_expf(s[j] * scale - m) * inv : 0.0f;
-            for (int64_t c = 0; c < hd; ++c) {
-                float acc = 0.0f;
-                for (int64_t j = 0; j < kv_len; ++j) acc += s[j] * kv_at(v, f16, (kv_row0 + j) * hd + c);
-                out[(h * q_len + i) * hd + c] = acc;
-            }
-        }
+    const int64_t row_bytes = heads * (kv_len > 1 ? kv_len : 1) * 4;
+    int64_t chunk = max_score_bytes / row_bytes;
+    if (chunk < 1) chunk = 1;
+    if (chunk >= 64) chunk -= chunk % 64;
+    if (q_len <= chunk) chunk = q_len;
+    float* s = (float*)malloc(sizeof(float) * (size_t)(chunk * (kv_len > 0 ? kv_len : 1)));
+    const int64_t first_position = kv_len - q_len;
+    for (int64_t q0 = 0; q0 < q_len; q0 += chunk) {
+        const int64_t rows = chunk < q_len - q0 ? chunk : q_len - q0;
+        const int64_t keys = q_len <= chunk ? kv_len : first_position + q0 + rows;
+        for (int64_t h = 0; h < heads; ++h)
+            prefill_block(q, q_len, q0, rows, h, k, v, f16, capacity, hd, keys, (h / group) * capacity, s, out);
     }
     free(s);
 }

@@ -88,6 +88,10 @@ void orc_matmul_dot(int quant, int scale_f16, const uint32_t* a_words, const flo
  * a f32 [M, K]; b [N, K] of b_type (ORC_T_*); b_scales for quantized b. */
 void orc_gemv_float(int b_type, int scale_f16, const float* a, int64_t M, const void* b,
                     const void* b_scales, int64_t N, int64_t K, float* out);
+/* ---- float matrix product: shaders/matmul.comp, b transposed [N, K] ----
+ * the path for M > 8 rows (matmul.cpp:96); sums in k order. */
+void orc_matmul_float(int b_type, int scale_f16, const float* a, int64_t M, const void* b,
+                      const void* b_scales, int64_t N, int64_t K, float* out);
 
 /* ---- norms, rope, activations ---- */
 void orc_rms_norm(const float* x, const float* w, int64_t rows, int64_t cols, float eps,
@@ -110,14 +114,17 @@ void orc_embedding_quantized(int quant, const uint32_t* words, const uint16_t* h
 /* ---- attention over a KV cache [kv_heads, capacity, hd] (f32, or f16 bits) ----
  * orc_attend_decode: one query per head, attend.comp + attend_merge.comp
  * (chunks of 128 keys, merged). orc_attention_prefill: q [heads, q_len, hd],
- * query i at position kv_len - q_len + i, attention_block's matmul + softmax +
+ * query i at position kv_len - q_len + i, in the reference's chunks of
+ * queries (attention.cpp:205-226), each attention_block's matmul + softmax +
  * matmul (src/ops/attention.cpp:127-138, shaders/softmax.comp). */
 void orc_attend_decode(const float* q, int64_t heads, const void* k, const void* v, int kv_f16,
                        int64_t kv_heads, int64_t capacity, int64_t hd, int64_t kv_start,
                        int64_t kv_len, float softcap, float* out);
 void orc_attention_prefill(const float* q, int64_t heads, int64_t q_len, const void* k,
                            const void* v, int kv_f16, int64_t kv_heads, int64_t capacity,
-                           int64_t hd, int64_t kv_len, float* out);
+                           int64_t hd, int64_t kv_len, int64_t max_score_bytes, float* out);
+/* The reference's score budget per attention call (ops/internal.hpp:92). */
+#define ORC_MAX_SCORE_BYTES ((int64_t)64 << 20)
 
 /* ---- whole model: src/models/llama.cpp:170-406 (GGUF llama architecture) ----
  * int_dot: 1 quantizes activations for quantized weights (gemv_dot /
@@ -128,6 +135,12 @@ void orc_model_free(orc_model* m);
 /* Runs t tokens after those processed; logits of the last token -> logits[vocab].
  * Returns 0, or -1 with orc_last_error set (llama.cpp:300-305 errors). */
 int orc_model_forward(orc_model* m, const int32_t* tokens, int64_t t, float* logits);
+/* As orc_model_forward with every row's logits -> logits[t * vocab]
+ * (Llama::forward_all, llama.cpp:393-396). */
+int orc_model_forward_all(orc_model* m, const int32_t* tokens, int64_t t, float* logits);
+/* Sets the score budget of the model's attention calls (a test hook that
+ * makes short prompts take the chunked path). */
+void orc_model_set_max_score_bytes(orc_model* m, int64_t bytes);
 int64_t orc_model_position(const orc_model* m);
 int orc_model_set_position(orc_model* m, int64_t position); /* timing samples only */
 int64_t orc_model_rewind(orc_model* m, int64_t position); /* -1 on error */

@@ -586,9 +586,120 @@ def test_softmax_and_matmul():
     a = rng.standard_normal((4, 3, 20)).astype(np.float32)
     b = rng.standard_normal((2, 5, 20)).astype(np.float32)  # [2 kv batches, n=5, k=20], transposed, group 2
     out = H.empty(4 * 3 * 5 * 4)
-    H.call("vkml_matmul", H.MatmulParams(3, 5, 20, 100, 2, 4, 1, H.F32), p(dev(a)), p(dev(b)), p(out))
+    H.call("vkml_matmul", H.MatmulParams(3, 5, 20, 100, 2, 4, 1, H.F32), p(dev(a)), p(dev(b)), p(out), None)
     want = np.stack([a[z] @ b[z // 2].T for z in range(4)])
     assert np.allclose(out.download(np.float32, want.shape), want, atol=1e-5)
+
+
+def _float_b(bt, n, k, rng):
+    """(device values, device scales, oracle type, oracle values, oracle scales) of a float or quantized [n, k]."""
+    if bt in (H.F32, H.F16, H.BF16):
+        w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+        if bt == H.F32:
+            b, ot = w, O.T_F32
+        elif bt == H.F16:
+            b, ot = w.astype(np.float16).view(np.uint16), O.T_F16
+        else:
+            b, ot = (w.view(np.uint32) >> 16).astype(np.uint16), O.T_BF16
+        return dev(b), None, ot, b, None
+    dv, ds, quant, words, scales = weights(bt, n, k, int(rng.integers(1 << 30)))
+    # q4_K runs as the reference's q4_1 repack, which the oracle holds
+    return dv, ds, {O.Q8_0: O.T_Q8, O.Q4_0: O.T_Q4, O.Q4_1: O.T_Q4_1}[quant], words, scales
+
+
+@pytest.mark.parametrize("bt", [H.F32, H.F16, H.BF16, H.Q8_0, H.Q4_0, H.Q4_1, H.Q4_K])
+@pytest.mark.parametrize("m,n,k", [(9, 100, 512), (70, 64, 256), (130, 193, 768)])
+def test_matmul_projection_bit_exact(bt, m, n, k):
+    """vkml_matmul with a transposed weight (the float path's projections of
+    more than 8 rows): each output in matmul.comp's k order, as the oracle."""
+    rng = np.random.default_rng(m + n + bt)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    dv, ds, ot, ob, osc = _float_b(bt, n, k, rng)
+    out = H.empty(m * n * 4)
+    H.call("vkml_matmul", H.MatmulParams(m, n, k, 0, 1, 1, 1, bt, H.F16), p(dev(a)), p(dv), p(out), p(ds))
+    want = O.matmul_float(ot, a, ob, osc, n, k)
+    assert np.array_equal(bits(out.download(np.float32, (m, n))), bits(want))
+
+
+@pytest.mark.parametrize("kv_type", [H.F16, H.F32])
+@pytest.mark.parametrize("rows,keys", [(9, 40), (64, 64), (130, 300), (200, 129)])
+def test_matmul_attention_shapes_bit_exact(kv_type, rows, keys):
+    """Scores q k^T and probs v as attention_block runs them: a batch per
+    query head against its KV head's cache rows (b_group, b_stride), the
+    first `keys` rows of a larger cache; k order per output."""
+    heads, kvh, hd, cap = 8, 2, 64, keys + 7
+    g = heads // kvh
+    rng = np.random.default_rng(rows * keys)
+    q = rng.standard_normal((heads, rows, hd)).astype(np.float32)
+    dt = np.float16 if kv_type == H.F16 else np.float32
+    kc = rng.standard_normal((kvh, cap, hd)).astype(dt)
+    vc = rng.standard_normal((kvh, cap, hd)).astype(dt)
+    ot = O.T_F16 if kv_type == H.F16 else O.T_F32
+    kb = kc.view(np.uint16) if kv_type == H.F16 else kc
+    vb = vc.view(np.uint16) if kv_type == H.F16 else vc
+    scores = H.empty(heads * rows * keys * 4)
+    H.call("vkml_matmul", H.MatmulParams(rows, keys, hd, cap * hd, g, heads, 1, kv_type, H.F16), p(dev(q)), p(dev(kb)),
+           p(scores), None)
+    got = scores.download(np.float32, (heads, rows, keys))
+    for h in range(heads):
+        want = O.matmul_float(ot, q[h], np.ascontiguousarray(kb[h // g, :keys]), None, keys, hd)
+        assert np.array_equal(bits(got[h]), bits(want)), h
+    probs = rng.random((heads, rows, keys)).astype(np.float32)
+    out = H.empty(heads * rows * hd * 4)
+    H.call("vkml_matmul", H.MatmulParams(rows, hd, keys, cap * hd, g, heads, 0, kv_type, H.F16), p(dev(probs)), p(dev(vb)),
+           p(out), None)
+    got = out.download(np.float32, (heads, rows, hd))
+    for h in range(heads):
+        # b [k, n] in k order equals b^T [n, k] in k order
+        want = O.matmul_float(ot, probs[h], np.ascontiguousarray(vb[h // g, :keys].T), None, hd, keys)
+        assert np.array_equal(bits(got[h]), bits(want)), h
+
+
+@pytest.mark.parametrize("rows", [1, 5, 8])
+def test_gemv_batched_scores_bit_exact(rows):
+    """Up to 8 queries' scores through gemv.comp's order, one batch per
+    query head against its KV head (gemv's z, b_group, b_stride)."""
+    heads, kvh, hd, keys, cap = 8, 2, 128, 77, 90
+    g = heads // kvh
+    rng = np.random.default_rng(rows)
+    q = rng.standard_normal((heads, rows, hd)).astype(np.float32)
+    kc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    out = H.empty(heads * rows * keys * 4)
+    H.call("vkml_gemv", H.GemvParams(rows, keys, hd, H.F16, H.F16, cap * hd, g, heads), p(dev(q)), p(dev(kc)), p(out), None)
+    got = out.download(np.float32, (heads, rows, keys))
+    for h in range(heads):
+        want = O.gemv_float(O.T_F16, q[h], np.ascontiguousarray(kc[h // g, :keys]), None, keys, hd)
+        assert np.array_equal(bits(got[h]), bits(want)), h
+
+
+@pytest.mark.parametrize("kv_type", [H.F16, H.F32])
+@pytest.mark.parametrize("style", [0, 1])
+def test_rope_kv_prompt_bit_exact(kv_type, style):
+    """A prompt's rope + heads-first q + KV append in one launch, as the
+    reference's rope, permute, cast and write_rows (llama.cpp:320-355)."""
+    heads, kvh, hd, cap, pos, t = 8, 2, 64, 40, 3, 13
+    width = (heads + 2 * kvh) * hd
+    stride = width + 32
+    rng = np.random.default_rng(4 + style)
+    rows = rng.standard_normal((t, stride)).astype(np.float32)
+    table = O.rope_table(cap, hd, 1e4)
+    dt = np.uint16 if kv_type == H.F16 else np.float32
+    kc, vc = H.empty(kvh * cap * hd * 4), H.empty(kvh * cap * hd * 4)
+    H.call("vkml_fill_u32", kc.p, 0, kvh * cap * hd)
+    H.call("vkml_fill_u32", vc.p, 0, kvh * cap * hd)
+    q = H.empty(heads * t * hd * 4)
+    H.call("vkml_rope_kv_prompt", H.RopeKvParams(heads, kvh, hd, cap, pos, style, kv_type, 1), t, stride, p(dev(rows)),
+           p(dev(table)), p(q), p(kc), p(vc))
+    qr = O.rope(np.ascontiguousarray(rows[:, :heads * hd]).reshape(t, heads, hd), table, pos, style)
+    kr = O.rope(np.ascontiguousarray(rows[:, heads * hd:(heads + kvh) * hd]).reshape(t, kvh, hd), table, pos, style)
+    vr = rows[:, (heads + kvh) * hd:width].reshape(t, kvh, hd)
+    assert np.array_equal(bits(q.download(np.float32, (heads, t, hd))), bits(qr.transpose(1, 0, 2)))
+    kg = kc.download(dt, (kvh, cap, hd))
+    vg = vc.download(dt, (kvh, cap, hd))
+    cast = (lambda x: O.f32_to_f16(x)) if kv_type == H.F16 else (lambda x: x)
+    assert np.array_equal(kg[:, pos:pos + t], cast(kr.transpose(1, 0, 2)))
+    assert np.array_equal(vg[:, pos:pos + t], cast(vr.transpose(1, 0, 2)))
+    assert not kg[:, :pos].any() and not kg[:, pos + t:].any()
 
 
 def test_graph_replay_advances_the_state():

@@ -260,6 +260,97 @@ def test_gemv_float_within_the_f32_dot_bound(t, k):
     assert np.all(np.abs(got - want) <= bound + 1e-30)
 
 
+@pytest.mark.parametrize("t", [O.T_F32, O.T_F16, O.T_Q8, O.T_Q4_1])
+def test_matmul_float_within_the_f32_dot_bound(t):
+    n, m, k = 37, 11, 256
+    rng = np.random.default_rng(19)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    sc = None
+    if t == O.T_F32:
+        b, wd = w, w
+    elif t == O.T_F16:
+        b = w.astype(np.float16).view(np.uint16); wd = b.view(np.float16).astype(np.float32)
+    else:
+        quant = {O.T_Q8: O.Q8_0, O.T_Q4_1: O.Q4_1}[t]
+        b, sc = O.quantize(quant, w, True); wd = O.dequantize(quant, b, sc, n, k)
+    got = O.matmul_float(t, a, b, sc, n, k)
+    want = a.astype(np.float64) @ wd.astype(np.float64).T
+    bound = k * 2.0 ** -24 * (np.abs(a.astype(np.float64)) @ np.abs(wd.astype(np.float64)).T)
+    assert np.all(np.abs(got - want) <= bound + 1e-30)
+
+
+def test_matmul_float_sums_in_k_order():
+    # matmul.comp adds its products one k at a time: 2^24 + 1 rounds back to
+    # 2^24 (ties to even), so [2^24, 1, 1, -2^24] sums to 0 in k order, where
+    # pairing (2^24 + 1) + (1 - 2^24) would give 1 and the exact sum is 2.
+    a = np.ones((1, 4), np.float32)
+    b = np.array([[2.0 ** 24, 1.0, 1.0, -2.0 ** 24]], np.float32)
+    assert O.matmul_float(O.T_F32, a, b, None, 1, 4)[0, 0] == 0.0
+    # 32 lanes of gemv.comp split the same row differently: lane 0 takes
+    # k = 0..3 as one left-to-right dot, so it gives 0 as well, while a row
+    # whose large terms sit in different lanes is order-sensitive there
+    b2 = np.zeros((1, 256), np.float32)
+    b2[0, 0], b2[0, 4], b2[0, 8], b2[0, 128] = 2.0 ** 24, 1.0, 1.0, -2.0 ** 24
+    a2 = np.ones((1, 256), np.float32)
+    assert O.matmul_float(O.T_F32, a2, b2, None, 1, 256)[0, 0] == 0.0
+    assert O.gemv_float(O.T_F32, a2, b2, None, 1, 256)[0, 0] == 2.0
+
+
+def _attention_f64(q, k, v, kv_len):
+    heads, q_len, hd = q.shape
+    group = heads // k.shape[0]
+    out = np.empty((heads, q_len, hd))
+    for h in range(heads):
+        kh = k[h // group, :kv_len].astype(np.float64)
+        vh = v[h // group, :kv_len].astype(np.float64)
+        for i in range(q_len):
+            vis = kv_len - q_len + i + 1
+            s = kh[:vis] @ q[h, i].astype(np.float64) / math.sqrt(hd)
+            e = np.exp(s - s.max())
+            out[h, i] = e @ vh[:vis] / e.sum()
+    return out
+
+
+@pytest.mark.parametrize("heads,kv_heads,q_len,kv_len,f16,budget", [
+    (4, 2, 5, 9, True, 64 << 20),        # one block, gemv's scores (5 rows)
+    (4, 2, 40, 40, False, 64 << 20),     # one block, matmul.comp's scores
+    (8, 2, 300, 300, True, 8 * 300 * 4 * 70),  # chunks of 64 rows, then 44
+    (2, 1, 133, 140, False, 2 * 140 * 4 * 64),  # chunks of 64, 64 and a gemv chunk of 5
+    (4, 4, 6, 6, True, 1),               # one query a chunk
+])
+def test_attention_prefill_matches_double(heads, kv_heads, q_len, kv_len, f16, budget):
+    hd, cap = 64, kv_len + 3
+    rng = np.random.default_rng(q_len + kv_len)
+    q = rng.standard_normal((heads, q_len, hd)).astype(np.float32)
+    k = rng.standard_normal((kv_heads, cap, hd)).astype(np.float32)
+    v = rng.standard_normal((kv_heads, cap, hd)).astype(np.float32)
+    if f16:
+        k, v = k.astype(np.float16), v.astype(np.float16)
+        kc, vc = k.view(np.uint16), v.view(np.uint16)
+    else:
+        kc, vc = k, v
+    got = O.attention_prefill(q, kc, vc, kv_len, budget)
+    want = _attention_f64(q, k, v, kv_len)
+    assert np.all(np.abs(got - want) <= 2e-5 * (1 + np.abs(want)))
+
+
+def test_attention_prefill_chunks_of_many_rows_change_nothing():
+    # keys past a chunk's last query carry probability exactly 0, and chunks
+    # of more than 8 rows keep matmul.comp's order: chunked == one block
+    heads, q_len, hd = 4, 192, 64
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((heads, q_len, hd)).astype(np.float32)
+    k = rng.standard_normal((2, q_len, hd)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((2, q_len, hd)).astype(np.float16).view(np.uint16)
+    whole = O.attention_prefill(q, k, v, q_len)
+    chunked = O.attention_prefill(q, k, v, q_len, heads * q_len * 4 * 64)
+    assert np.array_equal(whole.view(np.uint32), chunked.view(np.uint32))
+    # a query sees keys up to its own position only: key 0 alone for query 0
+    assert np.array_equal(whole[:, 0].view(np.uint32),
+                          np.repeat(v.view(np.float16)[:, 0].astype(np.float32), 2, 0).view(np.uint32))
+
+
 # ---------------------------------------------------------------- small ops
 
 def test_rms_norm_matches_double():

@@ -103,10 +103,18 @@ int check_dot_params(const vkml_gemv_dot_params* p, const char* what) {
 // gemv.comp's order: 32 lanes per output, lane l taking the 4-element
 // groups l, l + 32, ... of its row (dot(a4, w) summed left to right), then
 // the halving tree over the 32 lanes (gemv.comp:117-212). Two rows a wave.
+// Batch blockIdx.y multiplies its a by float b's batch y / b_group.
 template <int BT>
 __global__ void __launch_bounds__(256) k_gemv_float(const float* a, uint32_t m, const void* b, const void* bs, uint32_t st,
-                                                    float* out, uint32_t n, uint32_t k) {
+                                                    float* out, uint32_t n, uint32_t k, uint32_t b_group, uint64_t b_stride) {
 #pragma clang fp contract(off)
+    const uint32_t z = blockIdx.y;
+    a += static_cast<uint64_t>(z) * m * k;
+    out += static_cast<uint64_t>(z) * m * n;
+    if constexpr (BT <= VKML_BF16) {
+        const uint64_t off = static_cast<uint64_t>(z / b_group) * b_stride * (BT == VKML_F32 ? 4 : 2);
+        b = static_cast<const uint8_t*>(b) + off;
+    }
     const uint32_t lane = threadIdx.x % 32;
     const uint32_t row = blockIdx.x * (blockDim.x / 32) + threadIdx.x / 32;
     const uint32_t r = min(row, n - 1);
@@ -224,25 +232,32 @@ int vkml_gemv(const vkml_gemv_params* p, const float* a, const void* b, float* o
     VKML_CHECK_ARG(p, "gemv: null params");
     VKML_CHECK_ARG(p->m >= 1 && p->m <= 8, "gemv: m must be 1 to 8, got " + std::to_string(p->m));
     VKML_CHECK_ARG(p->b_type <= VKML_Q4_K, "gemv: unknown weight type " + std::to_string(p->b_type));
+    const uint32_t batches = std::max(p->batches, 1u), group = std::max(p->b_group, 1u);
+    VKML_CHECK_ARG(batches <= 65535, "gemv: too many batches");
     if (p->b_type >= VKML_Q8_0) {
         const uint32_t unit = p->b_type == VKML_Q4_K ? 256 : 32;
         VKML_CHECK_ARG(p->k % unit == 0, "gemv: k = " + std::to_string(p->k) + " is not whole blocks of " + std::to_string(unit));
         VKML_CHECK_ARG(b_scales, "gemv: quantized weights need scales");
+        VKML_CHECK_ARG(batches == 1, "gemv: batches need a float b");
     }
     if (p->n == 0) return VKML_OK;
     VKML_CHECK_ARG(a && b && out, "gemv: null buffer");
-    const dim3 grid((p->n + 7) / 8);
+    const dim3 grid((p->n + 7) / 8, batches);
     vkml::abi::ProfileScope prof("gemv");
     hipStream_t s = vkml::abi::stream();
+    const uint64_t bst = p->b_stride;
+#define VKML_GEMV_LAUNCH(T) \
+    hipLaunchKernelGGL(k_gemv_float<T>, grid, dim3(256), 0, s, a, p->m, b, b_scales, p->scale_type, out, p->n, p->k, group, bst)
     switch (p->b_type) {
-        case VKML_F32: hipLaunchKernelGGL(k_gemv_float<VKML_F32>, grid, dim3(256), 0, s, a, p->m, b, b_scales, p->scale_type, out, p->n, p->k); break;
-        case VKML_F16: hipLaunchKernelGGL(k_gemv_float<VKML_F16>, grid, dim3(256), 0, s, a, p->m, b, b_scales, p->scale_type, out, p->n, p->k); break;
-        case VKML_BF16: hipLaunchKernelGGL(k_gemv_float<VKML_BF16>, grid, dim3(256), 0, s, a, p->m, b, b_scales, p->scale_type, out, p->n, p->k); break;
-        case VKML_Q8_0: hipLaunchKernelGGL(k_gemv_float<VKML_Q8_0>, grid, dim3(256), 0, s, a, p->m, b, b_scales, p->scale_type, out, p->n, p->k); break;
-        case VKML_Q4_0: hipLaunchKernelGGL(k_gemv_float<VKML_Q4_0>, grid, dim3(256), 0, s, a, p->m, b, b_scales, p->scale_type, out, p->n, p->k); break;
-        case VKML_Q4_1: hipLaunchKernelGGL(k_gemv_float<VKML_Q4_1>, grid, dim3(256), 0, s, a, p->m, b, b_scales, p->scale_type, out, p->n, p->k); break;
-        default: hipLaunchKernelGGL(k_gemv_float<VKML_Q4_K>, grid, dim3(256), 0, s, a, p->m, b, b_scales, p->scale_type, out, p->n, p->k); break;
+        case VKML_F32: VKML_GEMV_LAUNCH(VKML_F32); break;
+        case VKML_F16: VKML_GEMV_LAUNCH(VKML_F16); break;
+        case VKML_BF16: VKML_GEMV_LAUNCH(VKML_BF16); break;
+        case VKML_Q8_0: VKML_GEMV_LAUNCH(VKML_Q8_0); break;
+        case VKML_Q4_0: VKML_GEMV_LAUNCH(VKML_Q4_0); break;
+        case VKML_Q4_1: VKML_GEMV_LAUNCH(VKML_Q4_1); break;
+        default: VKML_GEMV_LAUNCH(VKML_Q4_K); break;
     }
+#undef VKML_GEMV_LAUNCH
     return vkml::abi::check_launch("gemv");
 }
 

@@ -401,46 +401,53 @@ __device__ __forceinline__ void store_cache(void* cache, uint32_t type, uint64_t
     else static_cast<float*>(cache)[at] = v;
 }
 
-// One thread per pair: q pairs, then k pairs (rotated, cast, appended), then v pairs.
-__global__ void k_rope_kv_append(vkml_rope_kv_params p, const float* qkv, const float* table, float* q_out, void* k_cache,
-                                 void* v_cache, const vkml_decode_state* st) {
+// One thread per (token, pair): q pairs, then k pairs (rotated, cast,
+// appended), then v pairs. Token t's row of q | k | v starts row_stride
+// floats after token t - 1's; q goes heads first, [heads, tokens, head_dim].
+__global__ void k_rope_kv_append(vkml_rope_kv_params p, uint32_t tokens, uint32_t row_stride, const float* qkv, const float* table,
+                                 float* q_out, void* k_cache, void* v_cache, const vkml_decode_state* st) {
     const uint32_t half = p.head_dim / 2;
-    const uint32_t q_pairs = p.heads * half, kv_pairs = p.kv_heads * half;
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= q_pairs + 2 * kv_pairs) return;
-    const uint32_t pos = st ? static_cast<uint32_t>(st->position) : p.position;
+    const uint32_t q_pairs = p.heads * half, kv_pairs = p.kv_heads * half, per = q_pairs + 2 * kv_pairs;
     const uint32_t q_dim = p.heads * p.head_dim, kv_dim = p.kv_heads * p.head_dim;
-    const uint64_t cache_row = pos % p.capacity;
-    if (i < q_pairs + kv_pairs) {
-        const bool is_q = i < q_pairs;
-        const uint32_t j = is_q ? i : i - q_pairs;
-        const uint32_t head = j / half, k = j % half;
-        const uint32_t ia = head * p.head_dim + (p.style == 0 ? 2 * k : k);
-        const uint32_t ib = head * p.head_dim + (p.style == 0 ? 2 * k + 1 : k + half);
-        const float* src = qkv + (is_q ? 0 : q_dim);
-        float a = src[ia], b = src[ib];
-        if (p.rotate) {
-            const float c = table[(static_cast<uint64_t>(pos) * half + k) * 2], s = table[(static_cast<uint64_t>(pos) * half + k) * 2 + 1];
-            const float ra = a * c - b * s;
-            const float rb = a * s + b * c;
-            a = ra;
-            b = rb;
-        }
-        if (is_q) {
-            q_out[ia] = a;
-            q_out[ib] = b;
+    const uint32_t pos0 = st ? static_cast<uint32_t>(st->position) : p.position;
+    const uint64_t total = static_cast<uint64_t>(tokens) * per;
+    for (uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < total;
+         g += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint32_t t = static_cast<uint32_t>(g / per), i = static_cast<uint32_t>(g % per);
+        const uint32_t pos = pos0 + t;
+        const uint64_t cache_row = pos % p.capacity;
+        const float* row = qkv + static_cast<uint64_t>(t) * row_stride;
+        if (i < q_pairs + kv_pairs) {
+            const bool is_q = i < q_pairs;
+            const uint32_t j = is_q ? i : i - q_pairs;
+            const uint32_t head = j / half, k = j % half;
+            const uint32_t ia = p.style == 0 ? 2 * k : k, ib = p.style == 0 ? 2 * k + 1 : k + half;
+            const float* src = row + (is_q ? 0 : q_dim) + head * p.head_dim;
+            float a = src[ia], b = src[ib];
+            if (p.rotate) {
+                const float c = table[(static_cast<uint64_t>(pos) * half + k) * 2], s = table[(static_cast<uint64_t>(pos) * half + k) * 2 + 1];
+                const float ra = a * c - b * s;
+                const float rb = a * s + b * c;
+                a = ra;
+                b = rb;
+            }
+            if (is_q) {
+                float* dst = q_out + (static_cast<uint64_t>(head) * tokens + t) * p.head_dim;
+                dst[ia] = a;
+                dst[ib] = b;
+            } else {
+                const uint64_t at = (static_cast<uint64_t>(head) * p.capacity + cache_row) * p.head_dim;
+                store_cache(k_cache, p.kv_type, at + ia, a);
+                store_cache(k_cache, p.kv_type, at + ib, b);
+            }
         } else {
-            const uint64_t row = (static_cast<uint64_t>(head) * p.capacity + cache_row) * p.head_dim;
-            store_cache(k_cache, p.kv_type, row + (ia - head * p.head_dim), a);
-            store_cache(k_cache, p.kv_type, row + (ib - head * p.head_dim), b);
+            const uint32_t j = i - q_pairs - kv_pairs;
+            const uint32_t head = j / half, e = 2 * (j % half);
+            const float* v = row + q_dim + kv_dim + head * p.head_dim;
+            const uint64_t at = (static_cast<uint64_t>(head) * p.capacity + cache_row) * p.head_dim;
+            store_cache(v_cache, p.kv_type, at + e, v[e]);
+            store_cache(v_cache, p.kv_type, at + e + 1, v[e + 1]);
         }
-    } else {
-        const uint32_t j = i - q_pairs - kv_pairs;
-        const uint32_t head = j / half, e = 2 * (j % half);
-        const float* v = qkv + q_dim + kv_dim + head * p.head_dim;
-        const uint64_t row = (static_cast<uint64_t>(head) * p.capacity + cache_row) * p.head_dim;
-        store_cache(v_cache, p.kv_type, row + e, v[e]);
-        store_cache(v_cache, p.kv_type, row + e + 1, v[e + 1]);
     }
 }
 
@@ -524,30 +531,76 @@ __global__ void k_embedding(vkml_embedding_params p, const void* values, const v
 
 // ---------------------------------------------------------------- matmul
 
-// c = a . b (or b^T): 16x16 output tiles, K in steps of 16 through LDS.
-template <bool BT>
-__global__ void k_matmul(vkml_matmul_params p, const float* a, const void* b, float* c) {
-    __shared__ float ta[16][17], tb[16][17];
-    const uint32_t z = blockIdx.z;
-    const uint32_t row = blockIdx.y * 16 + threadIdx.y, col = blockIdx.x * 16 + threadIdx.x;
+// matmul.comp's order: every output sums a[m][k] * b(k, n) in k order, a
+// product and an add at a time (matmul.comp:131-140). A 256-thread
+// workgroup computes a 64 x 64 block of c, each thread the 4 x 4 outputs at
+// rows 4 ty.., columns 4 tx..; K steps by 16 through LDS, both tiles stored
+// k-major so a thread reads its 4 rows and 4 columns as one 16-byte word
+// each. b is f32/f16/bf16, or (transposed, one batch) a quantized matrix
+// widened as gemv's weights are.
+template <bool BT, uint32_t BTYPE>
+__global__ void __launch_bounds__(256) k_matmul(vkml_matmul_params p, const float* a, const void* b, const void* bs, float* c) {
+    // Rows of 68: stores that run along k hit 16 different banks.
+    __shared__ __align__(16) float ta[16][68], tb[16][68];
+    const uint32_t tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
+    const uint32_t row0 = blockIdx.y * 64, col0 = blockIdx.x * 64, z = blockIdx.z;
     const float* az = a + static_cast<uint64_t>(z) * p.m * p.k;
     const uint64_t b_off = static_cast<uint64_t>(z / p.b_group) * p.b_stride;
-    float acc = 0.0f;
-    for (uint32_t k0 = 0; k0 < p.k; k0 += 16) {
-        const uint32_t ka = k0 + threadIdx.x, kb = k0 + threadIdx.y;
-        ta[threadIdx.y][threadIdx.x] = (row < p.m && ka < p.k) ? az[static_cast<uint64_t>(row) * p.k + ka] : 0.0f;
-        float bv = 0.0f;
-        if (col < p.n && kb < p.k) {
-            const uint64_t e = b_off + (BT ? static_cast<uint64_t>(col) * p.k + kb : static_cast<uint64_t>(kb) * p.n + col);
-            bv = load_src(b, e, p.b_type);
+    const auto b_at = [&](uint32_t n, uint32_t k) -> float {
+        if constexpr (BTYPE >= VKML_Q8_0) {
+            return weight_value(BTYPE, p.scale_type, b, bs, p.k, n, k);
+        } else {
+            const uint64_t e = b_off + (BT ? static_cast<uint64_t>(n) * p.k + k : static_cast<uint64_t>(k) * p.n + n);
+            return load_src(b, e, BTYPE);
         }
-        tb[threadIdx.y][threadIdx.x] = bv;
+    };
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (uint32_t k0 = 0; k0 < p.k; k0 += 16) {
+        // Out-of-range elements are zeros, which add nothing.
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t e = tid + 256 * u;
+            const uint32_t r = e / 16, kk = e % 16, row = row0 + r, k = k0 + kk;
+            ta[kk][r] = (row < p.m && k < p.k) ? az[static_cast<uint64_t>(row) * p.k + k] : 0.0f;
+            uint32_t col, kb;
+            if (BT) {  // b is [n, k]: run along k
+                col = e / 16;
+                kb = e % 16;
+            } else {  // b is [k, n]: run along n
+                kb = e / 64;
+                col = e % 64;
+            }
+            const uint32_t n = col0 + col, kg = k0 + kb;
+            tb[kb][col] = (n < p.n && kg < p.k) ? b_at(n, kg) : 0.0f;
+        }
         __syncthreads();
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) acc += ta[threadIdx.y][kk] * tb[kk][threadIdx.x];
+        for (uint32_t kk = 0; kk < 16; ++kk) {
+            const float4 av = *reinterpret_cast<const float4*>(&ta[kk][4 * ty]);
+            const float4 bv = *reinterpret_cast<const float4*>(&tb[kk][4 * tx]);
+            const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] += ar[i] * br[j];
+        }
         __syncthreads();
     }
-    if (row < p.m && col < p.n) c[(static_cast<uint64_t>(z) * p.m + row) * p.n + col] = acc;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t row = row0 + 4 * ty + i;
+        if (row >= p.m) continue;
+        float* cr = c + (static_cast<uint64_t>(z) * p.m + row) * p.n;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t col = col0 + 4 * tx + j;
+            if (col < p.n) cr[col] = acc[i][j];
+        }
+    }
 }
 
 }  // namespace
@@ -654,9 +707,30 @@ int vkml_rope_kv_append(const vkml_rope_kv_params* p, const float* qkv, const fl
     VKML_CHECK_ARG(qkv && q && k_cache && v_cache && (table || !p->rotate), "rope_kv_append: null buffer");
     const uint32_t n = (p->heads + 2 * p->kv_heads) * (p->head_dim / 2);
     ProfileScope prof("rope_kv_append");
-    hipLaunchKernelGGL(k_rope_kv_append, dim3((n + 255) / 256), dim3(256), 0, S(), *p, qkv, table, q, k_cache, v_cache, state);
+    hipLaunchKernelGGL(k_rope_kv_append, dim3((n + 255) / 256), dim3(256), 0, S(), *p, 1u, 0u, qkv, table, q, k_cache, v_cache, state);
     return vkml::abi::check_launch("rope_kv_append");
 }
+
+int vkml_rope_kv_prompt(const vkml_rope_kv_params* p, uint32_t tokens, uint32_t row_stride, const float* qkv, const float* table,
+                        float* q, void* k_cache, void* v_cache) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "rope_kv_prompt: null params");
+    VKML_CHECK_ARG(p->head_dim % 2 == 0 && p->kv_heads > 0 && p->heads % p->kv_heads == 0 && p->capacity > 0,
+                   "rope_kv_prompt: bad head layout");
+    VKML_CHECK_ARG(p->kv_type == VKML_F16 || p->kv_type == VKML_F32, "rope_kv_prompt: caches must be f16 or f32");
+    VKML_CHECK_ARG(row_stride >= (p->heads + 2 * p->kv_heads) * p->head_dim, "rope_kv_prompt: rows overlap");
+    VKML_CHECK_ARG(static_cast<uint64_t>(p->position) + tokens <= p->capacity,
+                   "rope_kv_prompt: positions " + std::to_string(p->position) + ".." + std::to_string(p->position + tokens) +
+                       " do not fit a cache of " + std::to_string(p->capacity) + " rows");
+    if (tokens == 0) return VKML_OK;
+    VKML_CHECK_ARG(qkv && q && k_cache && v_cache && (table || !p->rotate), "rope_kv_prompt: null buffer");
+    const uint64_t n = static_cast<uint64_t>(tokens) * (p->heads + 2 * p->kv_heads) * (p->head_dim / 2);
+    ProfileScope prof("rope_kv_prompt");
+    hipLaunchKernelGGL(k_rope_kv_append, dim3(blocks_for(n)), dim3(256), 0, S(), *p, tokens, row_stride, qkv, table, q, k_cache, v_cache,
+                       nullptr);
+    return vkml::abi::check_launch("rope_kv_prompt");
+}
+
 
 int vkml_cast(uint32_t count, uint32_t src, uint32_t dst, const void* x, void* out) {
     VKML_REQUIRE_INIT();
@@ -765,18 +839,46 @@ int vkml_step_finish(uint32_t vocab, const float* logits, vkml_decode_state* sta
     return vkml::abi::check_launch("step_finish");
 }
 
-int vkml_matmul(const vkml_matmul_params* p, const float* a, const void* b, float* c) {
+int vkml_matmul(const vkml_matmul_params* p, const float* a, const void* b, float* c, const void* b_scales) {
     VKML_REQUIRE_INIT();
     VKML_CHECK_ARG(p, "matmul: null params");
-    VKML_CHECK_ARG(p->b_type <= VKML_BF16, "matmul: b must be f32, f16 or bf16");
+    VKML_CHECK_ARG(p->b_type <= VKML_Q4_K, "matmul: unknown b type " + std::to_string(p->b_type));
     VKML_CHECK_ARG(p->b_group >= 1 && p->batches >= 1, "matmul: bad batching");
+    const bool quant = p->b_type >= VKML_Q8_0;
+    if (quant) {
+        VKML_CHECK_ARG(p->b_transposed && p->batches == 1, "matmul: quantized b must be one transposed [n, k] matrix");
+        const uint32_t unit = p->b_type == VKML_Q4_K ? 256 : 32;
+        VKML_CHECK_ARG(p->k % unit == 0, "matmul: k = " + std::to_string(p->k) + " is not whole blocks of " + std::to_string(unit));
+        VKML_CHECK_ARG(p->scale_type == VKML_F16 || (p->scale_type == VKML_F32 && p->b_type != VKML_Q4_K),
+                       "matmul: bad scale type");
+        VKML_CHECK_ARG(b_scales, "matmul: quantized b needs scales");
+    }
     if (p->m == 0 || p->n == 0) return VKML_OK;
     VKML_CHECK_ARG(a && b && c, "matmul: null buffer");
-    const dim3 grid((p->n + 15) / 16, (p->m + 15) / 16, p->batches);
+    VKML_CHECK_ARG((p->m + 63) / 64 <= 65535 && p->batches <= 65535, "matmul: too many rows or batches");
+    const dim3 grid((p->n + 63) / 64, (p->m + 63) / 64, p->batches);
     ProfileScope prof("matmul");
-    if (p->b_transposed) hipLaunchKernelGGL(k_matmul<true>, grid, dim3(16, 16), 0, S(), *p, a, b, c);
-    else hipLaunchKernelGGL(k_matmul<false>, grid, dim3(16, 16), 0, S(), *p, a, b, c);
+    const bool t = p->b_transposed != 0;
+    switch (p->b_type) {
+        case VKML_F32:
+            if (t) hipLaunchKernelGGL((k_matmul<true, VKML_F32>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c);
+            else hipLaunchKernelGGL((k_matmul<false, VKML_F32>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c);
+            break;
+        case VKML_F16:
+            if (t) hipLaunchKernelGGL((k_matmul<true, VKML_F16>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c);
+            else hipLaunchKernelGGL((k_matmul<false, VKML_F16>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c);
+            break;
+        case VKML_BF16:
+            if (t) hipLaunchKernelGGL((k_matmul<true, VKML_BF16>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c);
+            else hipLaunchKernelGGL((k_matmul<false, VKML_BF16>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c);
+            break;
+        case VKML_Q8_0: hipLaunchKernelGGL((k_matmul<true, VKML_Q8_0>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c); break;
+        case VKML_Q4_0: hipLaunchKernelGGL((k_matmul<true, VKML_Q4_0>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c); break;
+        case VKML_Q4_1: hipLaunchKernelGGL((k_matmul<true, VKML_Q4_1>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c); break;
+        default: hipLaunchKernelGGL((k_matmul<true, VKML_Q4_K>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c); break;
+    }
     return vkml::abi::check_launch("matmul");
 }
+
 
 }  // extern "C"

@@ -40,9 +40,10 @@ def _struct(name, fields):
 QuantizeParams = _struct("QuantizeParams", [("blocks", u32), ("src_type", u32), ("quant", u32), ("scale_type", u32)])
 DequantizeParams = _struct("DequantizeParams", [("count", u32), ("quant", u32), ("scale_type", u32), ("cols", u32)])
 GemvDotParams = _struct("GemvDotParams", [("m", u32), ("n", u32), ("k", u32), ("b_type", u32), ("scale_type", u32)])
-GemvParams = GemvDotParams
+GemvParams = _struct("GemvParams", [("m", u32), ("n", u32), ("k", u32), ("b_type", u32), ("scale_type", u32),
+                                    ("b_stride", u32), ("b_group", u32), ("batches", u32)])
 MatmulParams = _struct("MatmulParams", [("m", u32), ("n", u32), ("k", u32), ("b_stride", u32), ("b_group", u32),
-                                        ("batches", u32), ("b_transposed", u32), ("b_type", u32)])
+                                        ("batches", u32), ("b_transposed", u32), ("b_type", u32), ("scale_type", u32)])
 RmsNormParams = _struct("RmsNormParams", [("rows", u32), ("cols", u32), ("eps", f32)])
 SoftmaxParams = _struct("SoftmaxParams", [("rows", u32), ("cols", u32), ("scale", f32), ("causal", u32),
                                           ("q_len", u32), ("offset", u32), ("window", u32), ("softcap", f32)])
@@ -113,7 +114,7 @@ SIGNATURES = {
     "vkml_matmul_dot": [P(GemvDotParams), vp, vp, vp, vp, vp],
     "vkml_gemv_dot_swiglu": [P(GemvDotParams), vp, vp, vp, vp, vp, vp, vp],
     "vkml_gemv": [P(GemvParams), vp, vp, vp, vp],
-    "vkml_matmul": [P(MatmulParams), vp, vp, vp],
+    "vkml_matmul": [P(MatmulParams), vp, vp, vp, vp],
     "vkml_rms_norm": [P(RmsNormParams), vp, vp, vp],
     "vkml_rms_norm_quantize": [P(RmsNormParams), vp, vp, vp, vp, vp],
     "vkml_softmax": [P(SoftmaxParams), vp, vp],
@@ -128,6 +129,7 @@ SIGNATURES = {
     "vkml_attend": [P(AttendParams), vp, vp, vp, vp, vp, vp],
     "vkml_attend_merge": [P(AttendParams), vp, vp, vp, vp, vp],
     "vkml_rope_kv_append": [P(RopeKvParams), vp, vp, vp, vp, vp, vp],
+    "vkml_rope_kv_prompt": [P(RopeKvParams), u32, u32, vp, vp, vp, vp, vp],
     "vkml_gemv_fused": [P(GemvFusedParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step_o": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp],

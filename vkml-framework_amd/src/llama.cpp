@@ -340,7 +340,7 @@ struct Llama::Impl {
             }
             return;
         }
-        const vkml_gemv_params p{1, u32(w.rows), u32(w.cols), w.type_code(), w.scale_code()};
+        const vkml_gemv_params p{1, u32(w.rows), u32(w.cols), w.type_code(), w.scale_code(), 0, 1, 1};
         float* y = residual ? static_cast<float*>(ytmp.data()) : out;  // out may be the residual itself
         check(vkml_gemv(&p, static_cast<const float*>(in_f32.data()), w.values(), y, w.scales()), t);
         if (residual) check(vkml_binary(0, u32(w.rows), u32(w.rows), residual, y, out), t);
@@ -510,6 +510,154 @@ struct Llama::Impl {
         tag("");
     }
 
+    // The Q8_0 form of a shared input (detail::SharedInput, matmul.cpp:
+    // 225-229): made once, for every projection of that input.
+    struct Rows {
+        Tensor f;         // f32 [t, k]
+        Tensor values;    // Q8_0 codes, t * k bytes
+        Tensor scales;    // f32, one per 32 values
+        bool quantized = false;
+    };
+
+    Rows rows_of(const Tensor& f, std::int64_t t, std::int64_t k, bool quantize) const {
+        Rows r{f, {}, {}, false};
+        if (!quantize) return r;
+        r.values = Tensor::empty(*context, {t * k / 4}, DType::I32);
+        r.scales = Tensor::empty(*context, {t * k / 32}, DType::F32);
+        const vkml_quantize_params qp{u32(t * k / 32), VKML_F32, VKML_Q8_0, VKML_F32};
+        check(vkml_quantize(&qp, f.data(), r.values.data(), r.scales.data()), "quantize");
+        r.quantized = true;
+        return r;
+    }
+
+    // The rows of x normalized (and their Q8_0 form when a consumer takes it).
+    Rows norm_rows(const Tensor& x, const Tensor& w, std::int64_t t, bool quantize) const {
+        const std::int64_t d = config.hidden_size;
+        const vkml_rms_norm_params np{u32(t), u32(d), config.rms_norm_eps};
+        Rows r{Tensor::empty(*context, {t, d}, DType::F32), {}, {}, false};
+        if (quantize && d % 32 == 0) {
+            r.values = Tensor::empty(*context, {t * d / 4}, DType::I32);
+            r.scales = Tensor::empty(*context, {t * d / 32}, DType::F32);
+            check(vkml_rms_norm_quantize(&np, static_cast<const float*>(x.data()), static_cast<const float*>(w.data()),
+                                         static_cast<float*>(r.f.data()), r.values.data(), static_cast<float*>(r.scales.data())),
+                  "rms_norm");
+            r.quantized = true;
+        } else {
+            check(vkml_rms_norm(&np, static_cast<const float*>(x.data()), static_cast<const float*>(w.data()), static_cast<float*>(r.f.data())),
+                  "rms_norm");
+        }
+        return r;
+    }
+
+    // out [t, w.rows] = in . w^T (SharedInput::times_transposed, matmul.cpp:
+    // 207-272): the int8 product (gemv_dot for up to 8 rows, matmul_dot on
+    // the matrix cores beyond) when in has its Q8_0 form and w takes it,
+    // else f32 rows against the widened weights (gemv, or matmul.comp).
+    void project_rows(const Weight& w, const Rows& in, std::int64_t t, float* out, const char* what) const {
+        tag(what);
+        if (in.quantized && quantized_input(w)) {
+            const vkml_gemv_dot_params p{u32(t), u32(w.rows), u32(w.cols), w.type_code(), w.scale_code()};
+            const auto* as = static_cast<const float*>(in.scales.data());
+            if (t <= 8) check(vkml_gemv_dot(&p, in.values.data(), w.values(), out, w.scales(), as), what);
+            else check(vkml_matmul_dot(&p, in.values.data(), w.values(), out, w.scales(), as), what);
+            return;
+        }
+        const auto* a = static_cast<const float*>(in.f.data());
+        if (t <= 8) {
+            const vkml_gemv_params p{u32(t), u32(w.rows), u32(w.cols), w.type_code(), w.scale_code(), 0, 1, 1};
+            check(vkml_gemv(&p, a, w.values(), out, w.scales()), what);
+        } else {
+            const vkml_matmul_params p{u32(t), u32(w.rows), u32(w.cols), 0, 1, 1, 1, w.type_code(), w.scale_code()};
+            check(vkml_matmul(&p, a, w.values(), out, w.scales()), what);
+        }
+    }
+
+    bool any_quantized(const std::vector<std::pair<Weight, std::int64_t>>& ws) const {
+        return std::any_of(ws.begin(), ws.end(), [&](const auto& wr) { return quantized_input(wr.first); });
+    }
+
+    // t > 1 tokens at once, as the reference's Llama::run (llama.cpp:
+    // 299-406): every projection over all t rows, rope + the KV append for
+    // all of them in one launch, attention as scores + causal softmax +
+    // probs v in the reference's query chunks. The last row's logits go to
+    // `logits`, or with all every row's to *all [t, vocab].
+    void prefill(std::span<const std::int32_t> tokens, Tensor* all) {
+        const LlamaConfig& c = config;
+        Context& ctx = *context;
+        const auto t = static_cast<std::int64_t>(tokens.size());
+        const std::int64_t d = c.hidden_size, hd = c.head_dim, ff = c.intermediate_size;
+        const std::int64_t heads = c.num_heads, qd = heads * hd, kvd = c.num_kv_heads * hd, width = qd + 2 * kvd;
+        const std::int64_t end = position + t;
+        const auto f32 = [&](Shape shape) { return Tensor::empty(ctx, std::move(shape), DType::F32); };
+        const Tensor ids = Tensor::from_data<std::int32_t>(ctx, tokens, {t});
+        Tensor x = f32({t, d});
+        tag("embed");
+        const vkml_embedding_params ep{u32(t * d), u32(d), u32(c.vocab_size), embed.type_code(),
+                                       embed.quantized ? embed.scale_code() : std::uint32_t(VKML_F16)};
+        check(vkml_embedding(&ep, embed.values(), embed.scales(), static_cast<const std::int32_t*>(ids.data()), static_cast<float*>(x.data())),
+              "embedding");
+        auto* xp = static_cast<float*>(x.data());
+        Tensor qkv_rows = f32({t, width}), y = f32({t, d}), gate = f32({t, ff}), up = f32({t, ff});
+        auto* yp = static_cast<float*>(y.data());
+        for (const Layer& L : layers) {
+            tag("attn_norm");
+            const Rows h = norm_rows(x, L.attn_norm, t, int_dot && any_quantized(L.qkv));
+            auto* qkv_p = static_cast<float*>(qkv_rows.data());
+            if (L.qkv.size() == 1) {
+                project_rows(L.qkv[0].first, h, t, qkv_p, "qkv");
+            } else {
+                for (const auto& [w, at] : L.qkv) {
+                    Tensor part = f32({t, w.rows});
+                    project_rows(w, h, t, static_cast<float*>(part.data()), "qkv");
+                    const vkml_copy_rows_params cp{u32(t * w.rows), u32(w.rows), u32(w.rows), 0, u32(width), u32(at)};
+                    check(vkml_copy_rows(&cp, part.data(), qkv_p), "qkv");
+                }
+            }
+            // heads_first + rope of q and k, k and v to the caches' type at
+            // rows position.. (llama.cpp:320-355)
+            tag("rope_kv");
+            Tensor q = f32({heads, t, hd});
+            const vkml_rope_kv_params rp{u32(heads), u32(c.num_kv_heads), u32(hd), u32(context_length), u32(position),
+                                         c.rope_style == RopeStyle::Interleaved ? 0u : 1u, detail::type_code(L.k_cache.dtype()), 1};
+            check(vkml_rope_kv_prompt(&rp, u32(t), u32(width), qkv_p, static_cast<const float*>(rope.data()), static_cast<float*>(q.data()),
+                                      const_cast<void*>(L.k_cache.data()), const_cast<void*>(L.v_cache.data())),
+                  "rope_kv");
+            tag("attention");
+            const Tensor attn = detail::attention_prompt(q, L.k_cache, L.v_cache, end, true, 0, 0.0f, detail::kMaxScoreBytes);
+            const Tensor merged = permute(attn, {1, 0, 2}).reshape({t, qd});
+            const Rows m_in = rows_of(merged, t, qd, int_dot && quantized_input(L.o) && qd % 32 == 0);
+            project_rows(L.o, m_in, t, yp, "o");
+            check(vkml_binary(0, u32(t * d), u32(t * d), xp, yp, xp), "add");
+            tag("ffn_norm");
+            const Rows h2 = norm_rows(x, L.ffn_norm, t, int_dot && (quantized_input(L.gate) || quantized_input(L.up)));
+            auto* gp = static_cast<float*>(gate.data());
+            auto* up_p = static_cast<float*>(up.data());
+            project_rows(L.gate, h2, t, gp, "gate");
+            project_rows(L.up, h2, t, up_p, "up");
+            tag("swiglu");
+            check(vkml_unary(0, u32(t * ff), 0.0f, gp, gp), "silu");
+            check(vkml_binary(2, u32(t * ff), u32(t * ff), gp, up_p, gp), "mul");
+            const Rows g_in = rows_of(gate, t, ff, int_dot && quantized_input(L.down) && ff % 32 == 0);
+            project_rows(L.down, g_in, t, yp, "down");
+            check(vkml_binary(0, u32(t * d), u32(t * d), xp, yp, xp), "add");
+        }
+        position = end;
+        // The final norm; every row through the output projection, or the
+        // last row alone (llama.cpp:392-405).
+        tag("final_norm");
+        const bool q_head = int_dot && quantized_input(lm_head());
+        if (all) {
+            const Rows hn = norm_rows(x, final_norm, t, q_head);
+            project_rows(lm_head(), hn, t, static_cast<float*>(all->data()), "lm_head");
+        } else {
+            Tensor row = f32({1, d});
+            check(vkml_memcpy_d2d(row.data(), xp + (t - 1) * d, static_cast<std::uint64_t>(d) * 4), "final_norm");
+            const Rows hn = norm_rows(row, final_norm, 1, q_head);
+            project_rows(lm_head(), hn, 1, static_cast<float*>(logits.data()), "lm_head");
+        }
+        tag("");
+    }
+
     void run_step(bool greedy) {
         const bool graphs = options.use_graphs && !vkml_get_profiling();
         if (!graphs) {
@@ -671,10 +819,14 @@ Tensor Llama::forward(std::span<const std::int32_t> tokens) {
     Impl& m = *impl_;
     const auto t = static_cast<std::int64_t>(tokens.size());
     m.check_room(t);
-    for (std::int64_t i = 0; i < t; ++i) {
-        m.set_state(tokens[static_cast<std::size_t>(i)], m.position);
+    if (t == 1) {
+        // One token: the decode step (fused decode attention, llama.cpp:
+        // 366 with attention.cpp:199-203).
+        m.set_state(tokens[0], m.position);
         m.run_step(false);
         ++m.position;
+    } else {
+        m.prefill(tokens, nullptr);
     }
     Tensor out = Tensor::empty(*m.context, {m.config.vocab_size}, DType::F32);
     check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward");
@@ -687,12 +839,13 @@ Tensor Llama::forward_all(std::span<const std::int32_t> tokens) {
     const auto t = static_cast<std::int64_t>(tokens.size());
     m.check_room(t);
     Tensor out = Tensor::empty(*m.context, {t, m.config.vocab_size}, DType::F32);
-    const std::uint64_t row = static_cast<std::uint64_t>(m.config.vocab_size) * 4;
-    for (std::int64_t i = 0; i < t; ++i) {
-        m.set_state(tokens[static_cast<std::size_t>(i)], m.position);
+    if (t == 1) {
+        m.set_state(tokens[0], m.position);
         m.run_step(false);
         ++m.position;
-        check(vkml_memcpy_d2d(static_cast<std::uint8_t*>(out.data()) + row * i, m.logits.data(), row), "Llama::forward_all");
+        check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward_all");
+    } else {
+        m.prefill(tokens, &out);
     }
     m.check_persistent();
     return out;

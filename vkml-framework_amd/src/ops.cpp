@@ -287,7 +287,7 @@ namespace detail {
 
 // a [..., M, K] times b [K, N] (or [N, K] transposed), b shared when 2-D,
 // batched otherwise; b_group as the reference (src/ops/matmul.cpp:124-195).
-Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transposed, std::int64_t b_group = 1, std::int64_t b_rows = -1) {
+Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transposed, std::int64_t b_group, std::int64_t b_rows) {
     const Shape& as = a.shape();
     Shape bs = b.shape();
     const std::string b_desc = (transposed ? "transposed " : "") + to_string(bs);
@@ -331,14 +331,17 @@ Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transpose
         check(vkml_fill_u32(out.data(), 0u, static_cast<std::uint64_t>(out.numel())), name);
         return out;
     }
-    if (transposed && batches == 1 && m <= kGemvMaxRows) {
-        const vkml_gemv_params p{u32(m), u32(n), u32(k), detail::type_code(b.dtype()), VKML_F16};
+    // gemv.comp for a few rows against a transposed b, matmul.comp
+    // otherwise (matmul.cpp:96), each batch z against b's z / b_group.
+    const std::uint32_t group = u32(std::max<std::int64_t>(b_group, 1));
+    if (transposed && m <= kGemvMaxRows) {
+        const vkml_gemv_params p{u32(m), u32(n), u32(k), detail::type_code(b.dtype()), VKML_F16, u32(b_stride), group, u32(batches)};
         check(vkml_gemv(&p, static_cast<const float*>(a.data()), b.data(), static_cast<float*>(out.data()), nullptr), name);
         return out;
     }
-    const vkml_matmul_params p{u32(m), u32(n), u32(k), u32(b_stride), u32(std::max<std::int64_t>(b_group, 1)), u32(batches),
-                               transposed ? 1u : 0u, detail::type_code(b.dtype())};
-    check(vkml_matmul(&p, static_cast<const float*>(a.data()), b.data(), static_cast<float*>(out.data())), name);
+    const vkml_matmul_params p{u32(m), u32(n), u32(k), u32(b_stride), group, u32(batches), transposed ? 1u : 0u,
+                               detail::type_code(b.dtype()), VKML_F32};
+    check(vkml_matmul(&p, static_cast<const float*>(a.data()), b.data(), static_cast<float*>(out.data()), nullptr), name);
     return out;
 }
 
@@ -386,25 +389,26 @@ Tensor matmul_transposed(const Tensor& a, const QuantizedMatrix& b) {
     const std::uint32_t type = quant_code(b.type), st = scale_code(b);
     detail::Runtime& rt = TensorAccess::runtime(a);
     const bool dot_ok = b.cols % (b.type == QuantType::q4_K ? 256 : 64) == 0;
+    float* c = static_cast<float*>(out.data());
     if (rt.integer_dot() && dot_ok) {
-        // Quantize a too and multiply int8 by int8 (matmul.cpp:225-245), eight rows per launch.
+        // Quantize a too and multiply int8 by int8 (matmul.cpp:225-259):
+        // gemv_dot for up to 8 rows, matmul_dot on the matrix cores beyond.
         const QuantizedMatrix aq = detail::quantize_q8_f32(a.reshape({m, b.cols}));
-        for (std::int64_t r0 = 0; r0 < m; r0 += kGemvMaxRows) {
-            const std::int64_t rows = std::min(kGemvMaxRows, m - r0);
-            const vkml_gemv_dot_params p{u32(rows), u32(b.rows), u32(b.cols), type, st};
-            check(vkml_gemv_dot(&p, static_cast<const std::uint8_t*>(aq.values.data()) + r0 * b.cols, b.values.data(),
-                                static_cast<float*>(out.data()) + r0 * b.rows, b.scales.data(),
-                                static_cast<const float*>(aq.scales.data()) + r0 * (b.cols / 32)),
-                  "matmul_transposed");
-        }
+        const vkml_gemv_dot_params p{u32(m), u32(b.rows), u32(b.cols), type, st};
+        const auto* av = aq.values.data();
+        const auto* as_ = static_cast<const float*>(aq.scales.data());
+        if (m <= kGemvMaxRows) check(vkml_gemv_dot(&p, av, b.values.data(), c, b.scales.data(), as_), "matmul_transposed");
+        else check(vkml_matmul_dot(&p, av, b.values.data(), c, b.scales.data(), as_), "matmul_transposed");
         return out;
     }
-    for (std::int64_t r0 = 0; r0 < m; r0 += kGemvMaxRows) {
-        const std::int64_t rows = std::min(kGemvMaxRows, m - r0);
-        const vkml_gemv_params p{u32(rows), u32(b.rows), u32(b.cols), type, st};
-        check(vkml_gemv(&p, static_cast<const float*>(a.data()) + r0 * b.cols, b.values.data(), static_cast<float*>(out.data()) + r0 * b.rows,
-                        b.scales.data()),
-              "matmul_transposed");
+    // f32 a against the widened weights: gemv.comp for up to 8 rows,
+    // matmul.comp beyond (matmul.cpp:96, 263-270).
+    if (m <= kGemvMaxRows) {
+        const vkml_gemv_params p{u32(m), u32(b.rows), u32(b.cols), type, st, 0, 1, 1};
+        check(vkml_gemv(&p, static_cast<const float*>(a.data()), b.values.data(), c, b.scales.data()), "matmul_transposed");
+    } else {
+        const vkml_matmul_params p{u32(m), u32(b.rows), u32(b.cols), 0, 1, 1, 1, type, st};
+        check(vkml_matmul(&p, static_cast<const float*>(a.data()), b.values.data(), c, b.scales.data()), "matmul_transposed");
     }
     return out;
 }
@@ -428,6 +432,57 @@ Tensor attend_one_query(const Tensor& q, const Tensor& k_cache, const Tensor& v_
     check(vkml_attend_merge(&p, static_cast<const float*>(partial.data()), static_cast<const float*>(stats.data()),
                             static_cast<float*>(out.data()), nullptr, nullptr),
           "attention");
+    return out;
+}
+
+// Rows start.. of every batch of src [B, *, width] into rows at.. of dst
+// [B, *, width], 32-bit words (attention.cpp:103-122).
+void copy_rows(const Tensor& src, std::int64_t start, const Tensor& dst, std::int64_t at, std::int64_t rows) {
+    const std::int64_t batches = src.shape()[0], width = src.shape()[2] * std::int64_t(element_size(src.dtype())) / 4;
+    const vkml_copy_rows_params p{u32(batches * rows * width), u32(rows * width), u32(src.shape()[1] * width), u32(start * width),
+                                  u32(dst.shape()[1] * width), u32(at * width)};
+    if (p.count == 0) return;
+    check(vkml_copy_rows(&p, src.data(), const_cast<void*>(dst.data())), "attention");
+}
+
+// attention_block (attention.cpp:127-138): scores q k^T over keys 0..keys
+// of the caches, the causal softmax with query i at key position keys -
+// rows + i, then probs v.
+Tensor attention_block(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache, std::int64_t keys, bool causal,
+                       std::int64_t window, float softcap) {
+    const std::int64_t heads = q.shape()[0], rows = q.shape()[1], hd = q.shape()[2];
+    const std::int64_t group = heads / k_cache.shape()[0];
+    const Tensor scores = matmul("attention", q, k_cache, true, group, keys);
+    Tensor probs = like(q, scores.shape(), DType::F32);
+    if (probs.numel() > 0) {
+        const vkml_softmax_params p{u32(heads * rows), u32(keys), 1.0f / std::sqrt(static_cast<float>(hd)), causal ? 1u : 0u,
+                                    u32(rows), u32(keys - rows), u32(window), softcap};
+        check(vkml_softmax(&p, static_cast<const float*>(scores.data()), static_cast<float*>(probs.data())), "attention");
+    }
+    return matmul("attention", probs, v_cache, false, group, keys);
+}
+
+// detail::attention for more than one query (attention.cpp:205-226): the
+// queries in chunks whose scores [heads, rows, kv_len] f32 fit
+// max_score_bytes (whole 64s of rows when at least 64), each against the
+// keys its last query sees. The chunks leave every value as one call would
+// give it but for gemv's order on a last chunk of 8 rows or fewer.
+Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache, std::int64_t kv_len, bool causal,
+                        std::int64_t window, float softcap, std::int64_t max_score_bytes) {
+    const std::int64_t heads = q.shape()[0], q_len = q.shape()[1];
+    const std::int64_t row_bytes = heads * std::max<std::int64_t>(kv_len, 1) * 4;
+    std::int64_t chunk = std::max<std::int64_t>(1, max_score_bytes / row_bytes);
+    if (chunk >= 64) chunk -= chunk % 64;
+    if (q_len <= chunk) return attention_block(q, k_cache, v_cache, kv_len, causal, window, softcap);
+    Tensor out = like(q, q.shape(), DType::F32);
+    const std::int64_t first = kv_len - q_len;  // key position of query 0
+    for (std::int64_t q0 = 0; q0 < q_len; q0 += chunk) {
+        const std::int64_t rows = std::min(chunk, q_len - q0);
+        const std::int64_t keys = causal ? first + q0 + rows : kv_len;
+        Tensor part = like(q, {heads, rows, q.shape()[2]}, DType::F32);
+        copy_rows(q, q0, part, 0, rows);
+        copy_rows(attention_block(part, k_cache, v_cache, keys, causal, window, softcap), 0, out, q0, rows);
+    }
     return out;
 }
 
@@ -463,15 +518,7 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
         const std::int64_t start = window > 0 && kv_len > window ? kv_len - window : 0;
         return detail::attend_one_query(q, k, v, start, kv_len, softcap);
     }
-    // Scores, masked softmax, weighted sum (attention.cpp:127-138).
-    const Tensor scores = detail::matmul("attention", q, k, true, group);
-    Tensor probs = like(q, scores.shape(), DType::F32);
-    if (probs.numel() > 0) {
-        const vkml_softmax_params p{u32(heads * q_len), u32(kv_len), 1.0f / std::sqrt(static_cast<float>(hd)), causal ? 1u : 0u,
-                                    u32(q_len), u32(kv_len - q_len), u32(window), softcap};
-        check(vkml_softmax(&p, static_cast<const float*>(scores.data()), static_cast<float*>(probs.data())), "attention");
-    }
-    return detail::matmul("attention", probs, v, false, group);
+    return detail::attention_prompt(q, k, v, kv_len, causal, window, softcap, detail::kMaxScoreBytes);
 }
 
 }  // namespace vkml

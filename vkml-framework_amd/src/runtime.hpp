@@ -63,4 +63,19 @@ std::int64_t numel_of(const Shape& shape);
 // The vkml_type code of a dtype.
 std::uint32_t type_code(DType dtype);
 
+// ops.cpp's internals the model shares (the reference's src/ops/internal.hpp).
+
+// Attention's budget for one call's scores (ops/internal.hpp:92).
+inline constexpr std::int64_t kMaxScoreBytes = std::int64_t{64} << 20;
+
+// a [..., M, K] times b [K, N] (or [N, K] transposed); with b_group > 1, a's
+// batch z against b's z / b_group; b_rows >= 0 uses b's first rows only.
+Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transposed, std::int64_t b_group = 1, std::int64_t b_rows = -1);
+
+// Queries q [heads, q_len, hd] against keys 0..kv_len of caches [kv_heads,
+// capacity, hd], query i at key position kv_len - q_len + i, in the
+// reference's query chunks (attention.cpp:205-226).
+Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache, std::int64_t kv_len, bool causal,
+                        std::int64_t window, float softcap, std::int64_t max_score_bytes);
+
 }  // namespace vkml::detail

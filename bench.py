@@ -36,6 +36,7 @@ sys.path.insert(0, os.path.join(ROOT, "vkml-framework_amd", "python"))
 import numpy as np  # noqa: E402
 
 PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0  # dense int8 MFMA, TOP/s
 PROMPT = 4096
 
 # HBM bytes one gate/up launch moves (reads + writes): FETCH_SIZE and
@@ -168,6 +169,60 @@ def roofline_only(spec):
     log(f"copy: 3 x {n} bytes")
 
 
+def matrix_macs(spec):
+    """Multiply-accumulates of one token's layer projections (q|k|v, o,
+    gate, up, down) over all layers: matmul_dot's work per prompt row."""
+    qkv = (spec.heads + 2 * spec.kv_heads) * spec.head_dim * spec.hidden
+    o = spec.hidden * spec.heads * spec.head_dim
+    ffn = 3 * spec.ffn * spec.hidden
+    return spec.n_layers * (qkv + o + ffn)
+
+
+def prefill_rates(model, spec, prompt, lengths, L):
+    """Prompts of the given lengths at once from position 0 (the cache rows
+    they write are the decode run's, which is over): a warm-up pass, a timed
+    pass, and a HIP-event profile pass. MFMA utilisation is matmul_dot's
+    int8 operations (2 per multiply-accumulate) over its event time, against
+    the 5.0 POP/s dense int8 peak."""
+    out = []
+    for n in [n for n in lengths if 1 < n <= len(prompt)]:
+        toks = prompt[:n]
+        model.rewind(0)
+        model.forward(toks)
+        model.rewind(0)
+        L.synchronize()
+        t0 = time.perf_counter()
+        model.forward(toks)
+        L.synchronize()
+        secs = time.perf_counter() - t0
+        model.rewind(0)
+        L.set_profiling(True)
+        L.reset_profile()
+        model.forward(toks)
+        L.synchronize()
+        prof = L.profile()
+        L.set_profiling(False)
+        by_kernel = {}
+        for name, calls, ms in prof:
+            k = name.split(":")[0]
+            c, t = by_kernel.get(k, (0, 0.0))
+            by_kernel[k] = (c + calls, t + ms)
+        mm_ms = by_kernel.get("matmul_dot", (0, 0.0))[1]
+        ops = 2.0 * n * matrix_macs(spec)
+        tops = ops / (mm_ms * 1e-3) / 1e12 if mm_ms else None
+        top = sorted(by_kernel.items(), key=lambda kv: -kv[1][1])[:8]
+        log(f"prefill {n} tokens: {secs * 1e3:.1f} ms, {n / secs:.0f} tokens/s; matmul_dot {mm_ms:.2f} ms "
+            f"({tops or 0:.0f} TOP/s int8, {100 * (tops or 0) / PEAK_INT8_TOPS:.1f}% of peak)")
+        for k, (c, t) in top:
+            log(f"    {k:<20} calls {c:>6}  {t:9.3f} ms")
+        out.append({"tokens": n, "ms": round(secs * 1e3, 3), "tokens_per_s": round(n / secs, 1),
+                    "matmul_dot_ms": round(mm_ms, 3),
+                    "mfma": {"kernel": "matmul_dot (v_mfma_i32_16x16x32_i8)", "achieved": round(tops, 1) if tops else None,
+                             "peak": PEAK_INT8_TOPS, "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4) if tops else None},
+                    "kernels_ms": {k: round(t, 3) for k, (c, t) in top}})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,6 +237,8 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch every kernel from the host instead of replaying the captured step (for profilers "
                          "that cannot follow graph launches; the kernels are the same)")
+    ap.add_argument("--prefill", type=int, nargs="*", default=[512, 4096],
+                    help="prompt lengths whose prefill rate is measured after the decode run (none: skip)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the dominant kernel's timed launches and a 256 MiB device copy of known size, "
                          "for hardware-counter passes (FETCH_SIZE, WRITE_SIZE) that scale the kernel's HBM bytes "
@@ -263,6 +320,8 @@ def main():
         achieved = dom_bytes / (dom_us * 1e-6) / 1e9
         log(f"gemv_fused (norm + gate/up + swiglu + q8_0) back to back: {dom_us:.2f} us a launch, {achieved:.0f} GB/s")
 
+        pre = prefill_rates(model, spec, prompt, args.prefill, L) if args.prefill else None
+
         cpu = None
         if args.cpu_tokens > 0:
             sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -310,6 +369,7 @@ def main():
                          "traffic_over_algorithmic": round(GATE_UP_TRAFFIC / dom_bytes, 4),
                          "bytes_per_launch": round(dom_bytes), "avg_launch_us": round(dom_us, 3)},
             "cpu_baseline": cpu,
+            "prefill": pre,
             "tokens_head": [int(t) for t in tokens[:8]],
         }
         print(json.dumps(result), flush=True)

@@ -14,13 +14,17 @@
 // 16 x 16 tile of outputs exactly, so the matrix cores do the dot products
 // and the VALU applies the scales per block, in the reference's order.
 //
-// Mapping. A workgroup (four waves) computes a 64 x 64 tile of c, each wave
-// 32 x 32 (2 x 2 matrix instructions). Lane l of a wave holds, for a 16 x 16
-// instruction, a's row l % 16 and b's column l % 16 at the block's values
-// 8 (l / 16) .. 8 (l / 16) + 7 (one 8-byte operand each), and the results for
-// rows 4 (l / 16) .. + 3 of column l % 16. The operands are loaded straight
-// from memory (L2 serves the reuse across workgroups); each block's per-row
-// (code sum, scale) of a is staged in LDS once per workgroup.
+// Mapping. A workgroup (four waves) computes a 64 x 128 tile of c, each wave
+// all 64 rows and 32 of the columns (4 x 2 matrix instructions a block).
+// Lane l of a wave holds, for a 16 x 16 instruction, a's row l % 16 and b's
+// column l % 16 at the block's values 8 (l / 16) .. 8 (l / 16) + 7 (one
+// 8-byte operand each), and gets the results for rows 4 (l / 16) .. + 3 of
+// column l % 16. The operands are loaded straight from memory (L2 serves the
+// reuse across workgroups), each block's while the block before is scaled.
+// K runs in chunks of 8 blocks: every row's (scale, code sum) and every
+// column's (scale, offset) per block are staged in LDS for a chunk,
+// double-buffered, their loads in flight during the chunk before, one
+// barrier a chunk; the scaling reads four rows' values as one 16-byte word.
 #include <algorithm>
 
 #include "../../include/vkml_hip.h"
@@ -32,7 +36,7 @@ using namespace vkml::dev;
 namespace {
 
 constexpr uint32_t kT = 256;      // four waves
-constexpr uint32_t kTileM = 64, kTileN = 64;
+constexpr uint32_t kTileM = 64, kTileN = 128;
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct MatmulDotArgs {
@@ -53,19 +57,14 @@ __device__ __forceinline__ uint32_t q4_signed(uint32_t word, uint32_t shift) {
 }
 
 // Column n's operand for block blk: its 8 codes at values 8 g .. 8 g + 7 of
-// the block, as int8 (q4: codes 0 .. 15, or minus 8 for q4_0), and the
-// block's scale and offset.
-template <int FMT, bool F16S>
-__device__ __forceinline__ long b_operand(const MatmulDotArgs& p, uint32_t n, uint32_t blk, uint32_t g, float& s, float& o) {
-    const uint32_t blocks = p.k / 32;
-    const uint64_t block = static_cast<uint64_t>(n) * blocks + blk;
+// the block, as int8 (q4: codes 0 .. 15, or minus 8 for q4_0).
+template <int FMT>
+__device__ __forceinline__ long b_codes(const MatmulDotArgs& p, uint32_t n, uint32_t blk, uint32_t g) {
     uint32_t lo, hi;
-    o = 0.0f;
     if constexpr (FMT == VKML_Q8_0) {
         const uint2 w = ldg(reinterpret_cast<const uint2*>(p.b + static_cast<uint64_t>(n) * p.k + blk * 32 + 8 * g));
         lo = w.x;
         hi = w.y;
-        s = F16S ? f16_at(p.b_scales, block) : ldg(static_cast<const float*>(p.b_scales) + block);
     } else if constexpr (FMT == VKML_Q4_K) {
         // sub-block j = blk % 8 of super-block blk / 8: low (j even) or high
         // nibbles of bytes 32 (j / 2) .. of its 128
@@ -74,16 +73,6 @@ __device__ __forceinline__ long b_operand(const MatmulDotArgs& p, uint32_t n, ui
         const uint32_t sh = 4 * (j % 2);
         lo = (w.x >> sh) & 0x0F0F0F0Fu;
         hi = (w.y >> sh) & 0x0F0F0F0Fu;
-        const uint4 h = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.b_scales) +
-                                                           (static_cast<uint64_t>(n) * (p.k / 256) + sb) * 16));
-        const uint32_t b = 8 * (j % 4);
-        const uint32_t b1 = (h.y >> b) & 0xFFu, b2 = (h.z >> b) & 0xFFu, b3 = (h.w >> b) & 0xFFu;
-        const uint32_t sc = j < 4 ? b1 & 63u : (b3 & 15u) | ((b1 >> 6) << 4);
-        const uint32_t mn = j < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
-        const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h.x & 0xFFFFu));
-        const _Float16 nd = -__builtin_bit_cast(_Float16, static_cast<uint16_t>(h.x >> 16));
-        s = static_cast<float>(d * static_cast<_Float16>(static_cast<uint16_t>(sc)));
-        o = static_cast<float>(nd * static_cast<_Float16>(static_cast<uint16_t>(mn)));
     } else {
         // QuantizedMatrix q4 words: word w' of the block holds values 8 w' .. 8 w' + 7,
         // low nibbles the first four, high the last four
@@ -91,87 +80,213 @@ __device__ __forceinline__ long b_operand(const MatmulDotArgs& p, uint32_t n, ui
         if constexpr (FMT == VKML_Q4_0) {
             lo = q4_signed(q, 0);
             hi = q4_signed(q, 4);
-            s = F16S ? f16_at(p.b_scales, block) : ldg(static_cast<const float*>(p.b_scales) + block);
         } else {
             lo = q & 0x0F0F0F0Fu;
             hi = (q >> 4) & 0x0F0F0F0Fu;
-            if constexpr (F16S) {
-                const uint32_t so = ldg(static_cast<const uint32_t*>(p.b_scales) + block);  // f16 scale | f16 offset << 16
-                s = f16_bits_to_float(so & 0xFFFFu);
-                o = f16_bits_to_float(so >> 16);
-            } else {
-                const float2 so = ldg(static_cast<const float2*>(p.b_scales) + block);
-                s = so.x;
-                o = so.y;
-            }
         }
     }
     return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Column n's scale and offset for block blk (q8_0 / q4_0: offset unused).
+template <int FMT, bool F16S>
+__device__ __forceinline__ void b_block_scale(const MatmulDotArgs& p, uint32_t n, uint32_t blk, float& s, float& o) {
+    const uint64_t block = static_cast<uint64_t>(n) * (p.k / 32) + blk;
+    o = 0.0f;
+    if constexpr (FMT == VKML_Q8_0 || FMT == VKML_Q4_0) {
+        s = F16S ? f16_at(p.b_scales, block) : ldg(static_cast<const float*>(p.b_scales) + block);
+    } else if constexpr (F16S) {
+        const uint32_t so = ldg(static_cast<const uint32_t*>(p.b_scales) + block);  // f16 scale | f16 offset << 16
+        s = f16_bits_to_float(so & 0xFFFFu);
+        o = f16_bits_to_float(so >> 16);
+    } else {
+        const float2 so = ldg(static_cast<const float2*>(p.b_scales) + block);
+        s = so.x;
+        o = so.y;
+    }
+}
+
+// q4_K: sub-block j's scale f16(d sc_j) and offset f16(-dmin m_j) from the
+// super-block's 16-byte header (gguf.cpp:603-617).
+__device__ __forceinline__ void q4k_block_scale(const uint4& h, uint32_t j, float& s, float& o) {
+    const uint32_t b = 8 * (j % 4);
+    const uint32_t b1 = (h.y >> b) & 0xFFu, b2 = (h.z >> b) & 0xFFu, b3 = (h.w >> b) & 0xFFu;
+    const uint32_t sc = j < 4 ? b1 & 63u : (b3 & 15u) | ((b1 >> 6) << 4);
+    const uint32_t mn = j < 4 ? b2 & 63u : (b3 >> 4) | ((b2 >> 6) << 4);
+    const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h.x & 0xFFFFu));
+    const _Float16 nd = -__builtin_bit_cast(_Float16, static_cast<uint16_t>(h.x >> 16));
+    s = static_cast<float>(d * static_cast<_Float16>(static_cast<uint16_t>(sc)));
+    o = static_cast<float>(nd * static_cast<_Float16>(static_cast<uint16_t>(mn)));
+}
+
+constexpr uint32_t kChunk = 8;  // blocks of K a chunk (a q4_K super-block)
+
+// A thread's share of one chunk's statistics, loaded ahead of the chunk:
+// two (row, block) entries and one column's four blocks.
+template <int FMT, bool F16S>
+struct ChunkStats {
+    static constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
+    float sa[2];
+    uint4 codes[2][2];  // the two rows' 32 codes (code sums, for offsets)
+    uint4 header;       // q4_K: the column's super-block header
+    float s[4], o[4];   // other formats: the column's four blocks
+
+    __device__ __forceinline__ void load(const MatmulDotArgs& p, uint32_t t, uint32_t c0, uint32_t row0, uint32_t col0) {
+        const uint32_t blocks = p.k / 32;
+#pragma unroll
+        for (uint32_t u = 0; u < 2; ++u) {
+            const uint32_t e = t + kT * u, r = e % kTileM, blk = min(c0 + e / kTileM, blocks - 1);
+            const uint32_t row = min(row0 + r, p.m - 1);
+            sa[u] = ldg(p.a_scales + static_cast<uint64_t>(row) * blocks + blk);
+            if constexpr (kOffset) {
+                const uint4* c = reinterpret_cast<const uint4*>(p.a + static_cast<uint64_t>(row) * p.k + blk * 32);
+                codes[u][0] = ldg(c);
+                codes[u][1] = ldg(c + 1);
+            }
+        }
+        const uint32_t col = min(col0 + t / 2, p.n - 1), b0 = 4 * (t % 2);
+        if constexpr (FMT == VKML_Q4_K) {
+            header = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.b_scales) +
+                                                        (static_cast<uint64_t>(col) * (p.k / 256) + c0 / 8) * 16));
+        } else {
+#pragma unroll
+            for (uint32_t b = 0; b < 4; ++b) b_block_scale<FMT, F16S>(p, col, min(c0 + b0 + b, blocks - 1), s[b], o[b]);
+        }
+    }
+
+    template <class L>
+    __device__ __forceinline__ void store(L& lds, uint32_t t) const {
+#pragma unroll
+        for (uint32_t u = 0; u < 2; ++u) {
+            const uint32_t e = t + kT * u, r = e % kTileM, b = e / kTileM;
+            lds.sa[b][r] = sa[u];
+            if constexpr (kOffset) lds.asum[b][r] = static_cast<float>(byte_sum(codes[u][0]) + byte_sum(codes[u][1]));
+        }
+        const uint32_t cl = t / 2, b0 = 4 * (t % 2);
+#pragma unroll
+        for (uint32_t b = 0; b < 4; ++b) {
+            float sv = s[b], ov = o[b];
+            if constexpr (FMT == VKML_Q4_K) q4k_block_scale(header, b0 + b, sv, ov);
+            lds.sb[b0 + b][cl] = sv;
+            if constexpr (kOffset) lds.ob[b0 + b][cl] = ov;
+        }
+    }
+};
+
+// One chunk's statistics in LDS, [block of the chunk][row or column].
+template <bool kOffset>
+struct ChunkLds {
+    float sa[kChunk][kTileM];
+    float asum[kChunk][kOffset ? kTileM : 4];
+    float sb[kChunk][kTileN];
+    float ob[kChunk][kOffset ? kTileN : 1];
+};
+
 template <int FMT, bool F16S>
 __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
 #pragma clang fp contract(off)
     constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
-    __shared__ float2 s_row[2][kTileM];  // per block: each row's (code sum, scale), double-buffered
+    __shared__ __align__(16) ChunkLds<kOffset> lds[2];
     const uint32_t t = thread_index(), lane = t % kWave, wave = t / kWave;
     const uint32_t g = lane / 16, li = lane % 16;
     const uint32_t row0 = blockIdx.y * kTileM, col0 = blockIdx.x * kTileN;
-    const uint32_t wr = row0 + 32 * (wave / 2), wc = col0 + 32 * (wave % 2);  // the wave's 32 x 32 tile
     const uint32_t blocks = p.k / 32;
-    float acc[2][2][4];
+    const uint8_t* arow[4];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < 4; ++r) arow[r] = p.a + static_cast<uint64_t>(min(row0 + 16 * r + li, p.m - 1)) * p.k + 8 * g;
+    uint32_t bcol[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) bcol[c] = min(col0 + 32 * wave + 16 * c + li, p.n - 1);
+    float acc[4][2][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[r][c][i] = 0.0f;
-    for (uint32_t blk = 0; blk < blocks; ++blk) {
-        float2* rows = s_row[blk % 2];
-        if (t < kTileM) {
-            const uint32_t row = min(row0 + t, p.m - 1);
-            const uint4* codes = reinterpret_cast<const uint4*>(p.a + static_cast<uint64_t>(row) * p.k + blk * 32);
-            const float sa = ldg(p.a_scales + static_cast<uint64_t>(row) * blocks + blk);
-            float sum = 0.0f;
-            if constexpr (kOffset) sum = static_cast<float>(byte_sum(ldg(codes)) + byte_sum(ldg(codes + 1)));
-            rows[t] = make_float2(sum, sa);
-        }
-        long av[2], bv[2];
+
+    // The operands of block blk (clamped to the last block: the prefetch
+    // past the end loads something harmless).
+    const auto load_ops = [&](uint32_t blk, long (&av)[4], long (&bv)[2]) {
+        blk = min(blk, blocks - 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) av[r] = static_cast<long>(__builtin_bit_cast(uint64_t, ldg(reinterpret_cast<const uint2*>(arow[r] + blk * 32))));
+#pragma unroll
+        for (int c = 0; c < 2; ++c) bv[c] = b_codes<FMT>(p, bcol[c], blk, g);
+    };
+    // Block b of the chunk staged in st: the integer sums of its 4 x 2
+    // tiles, scaled and added in the reference's order.
+    const auto block = [&](const ChunkLds<kOffset>& st, uint32_t b, const long (&av)[4], const long (&bv)[2]) {
         float sb[2], ob[2];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const uint32_t row = min(wr + 16 * r + li, p.m - 1);
-            av[r] = static_cast<long>(__builtin_bit_cast(uint64_t, ldg(reinterpret_cast<const uint2*>(p.a + static_cast<uint64_t>(row) * p.k +
-                                                                                                      blk * 32 + 8 * g))));
+        for (int c = 0; c < 2; ++c) {
+            sb[c] = st.sb[b][32 * wave + 16 * c + li];
+            ob[c] = 0.0f;
+            if constexpr (kOffset) ob[c] = st.ob[b][32 * wave + 16 * c + li];
         }
 #pragma unroll
-        for (int c = 0; c < 2; ++c) bv[c] = b_operand<FMT, F16S>(p, min(wc + 16 * c + li, p.n - 1), blk, g, sb[c], ob[c]);
-        __syncthreads();  // rows[] of this block is written (the other buffer's readers finished a block ago)
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < 4; ++r) {
+            const float4 sa4 = *reinterpret_cast<const float4*>(&st.sa[b][16 * r + 4 * g]);
+            float4 as4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if constexpr (kOffset) as4 = *reinterpret_cast<const float4*>(&st.asum[b][16 * r + 4 * g]);
+            const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, asum[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float2 ra = rows[32 * (wave / 2) + 16 * r + 4 * g + i];  // (code sum, scale) of the output's row
                     if constexpr (kOffset) {
-                        acc[r][c][i] += ra.y * (static_cast<float>(d[i]) * sb[c] + ra.x * ob[c]);
+                        acc[r][c][i] += sa[i] * (static_cast<float>(d[i]) * sb[c] + asum[i] * ob[c]);
                     } else {
-                        acc[r][c][i] += static_cast<float>(d[i]) * (ra.y * sb[c]);
+                        acc[r][c][i] += static_cast<float>(d[i]) * (sa[i] * sb[c]);
                     }
                 }
             }
         }
+    };
+
+    ChunkStats<FMT, F16S> next;
+    next.load(p, t, 0, row0, col0);
+    next.store(lds[0], t);
+    __syncthreads();
+    long av[4], bv[2];
+    load_ops(0, av, bv);
+    for (uint32_t c0 = 0, buf = 0; c0 < blocks; c0 += kChunk, buf ^= 1) {
+        const bool more = c0 + kChunk < blocks;
+        if (more) next.load(p, t, c0 + kChunk, row0, col0);  // the next chunk's statistics, in flight meanwhile
+        if (c0 + kChunk <= blocks) {
+#pragma unroll
+            for (uint32_t b = 0; b < kChunk; ++b) {
+                long an[4], bn[2];
+                load_ops(c0 + b + 1, an, bn);
+                block(lds[buf], b, av, bv);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) av[r] = an[r];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) bv[c] = bn[c];
+            }
+        } else {
+            for (uint32_t b = 0; c0 + b < blocks; ++b) {
+                long an[4], bn[2];
+                load_ops(c0 + b + 1, an, bn);
+                block(lds[buf], b, av, bv);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) av[r] = an[r];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) bv[c] = bn[c];
+            }
+        }
+        if (more) next.store(lds[buf ^ 1], t);  // its readers finished a chunk ago, before the last barrier
+        __syncthreads();
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const uint32_t col = wc + 16 * c + li;
+            const uint32_t col = col0 + 32 * wave + 16 * c + li;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t row = wr + 16 * r + 4 * g + i;
+                const uint32_t row = row0 + 16 * r + 4 * g + i;
                 if (row < p.m && col < p.n) p.out[static_cast<uint64_t>(row) * p.n + col] = acc[r][c][i];
             }
         }

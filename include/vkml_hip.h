@@ -260,7 +260,12 @@ int vkml_gemv(const vkml_gemv_params* p, const float* d_a, const void* d_b, floa
  * quantized matrix (Q8_0/Q4_0/Q4_1/Q4_K, scales of scale_type in d_b_scales,
  * values widened as vkml_gemv's): the float path's projections of more than
  * 8 rows (matmul.cpp:96-97). Argument order is the reference's buffers
- * (a, b, c, scales; matmul.cpp:107). */
+ * (a, b, c, scales; matmul.cpp:107). causal = 1 skips the work a causal
+ * mask makes moot, row r of each batch seeing keys 0 .. r + causal_offset:
+ * with b_transposed (scores) the outputs past that are not written; else
+ * (probs . v) a's entries past it must be 0, and the sums stop where every
+ * row of a tile has passed its last key (adding the zeros would change
+ * nothing). No counterpart in the reference, which computes both. */
 typedef struct vkml_matmul_params {
     uint32_t m, n, k;
     uint32_t b_stride;
@@ -269,6 +274,8 @@ typedef struct vkml_matmul_params {
     uint32_t b_transposed;
     uint32_t b_type;
     uint32_t scale_type;
+    uint32_t causal;
+    uint32_t causal_offset;
 } vkml_matmul_params;
 int vkml_matmul(const vkml_matmul_params* p, const float* d_a, const void* d_b, float* d_out,
                 const void* d_b_scales);

@@ -655,6 +655,32 @@ def test_matmul_attention_shapes_bit_exact(kv_type, rows, keys):
         assert np.array_equal(bits(got[h]), bits(want)), h
 
 
+@pytest.mark.parametrize("rows,first", [(130, 0), (64, 70), (200, 3)])
+def test_matmul_causal_skip_changes_nothing(rows, first):
+    """The causal skip: scores on and below the diagonal (row r sees keys
+    0 .. first + r) as the full product's, and probs . v with the masked
+    probabilities 0 identical to the full sum over every key."""
+    heads, kvh, hd = 4, 2, 64
+    keys, cap, g = first + rows, first + rows + 5, 2
+    rng = np.random.default_rng(rows + first)
+    q = rng.standard_normal((heads, rows, hd)).astype(np.float32)
+    kc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    full, skip = H.empty(heads * rows * keys * 4), H.empty(heads * rows * keys * 4)
+    dq, dk = dev(q), dev(kc)
+    H.call("vkml_matmul", H.MatmulParams(rows, keys, hd, cap * hd, g, heads, 1, H.F16, H.F16, 0, 0), p(dq), p(dk), p(full), None)
+    H.call("vkml_matmul", H.MatmulParams(rows, keys, hd, cap * hd, g, heads, 1, H.F16, H.F16, 1, first), p(dq), p(dk), p(skip), None)
+    a, b = full.download(np.float32, (heads, rows, keys)), skip.download(np.float32, (heads, rows, keys))
+    seen = np.arange(keys)[None, :] <= np.arange(rows)[:, None] + first
+    assert np.array_equal(bits(a[:, seen]), bits(b[:, seen]))
+    probs = rng.random((heads, rows, keys)).astype(np.float32) * seen
+    dp = dev(probs)
+    o_full, o_skip = H.empty(heads * rows * hd * 4), H.empty(heads * rows * hd * 4)
+    H.call("vkml_matmul", H.MatmulParams(rows, hd, keys, cap * hd, g, heads, 0, H.F16, H.F16, 0, 0), p(dp), p(dev(vc)), p(o_full), None)
+    H.call("vkml_matmul", H.MatmulParams(rows, hd, keys, cap * hd, g, heads, 0, H.F16, H.F16, 1, first), p(dp), p(dev(vc)), p(o_skip), None)
+    assert np.array_equal(bits(o_full.download(np.float32, (heads, rows, hd))), bits(o_skip.download(np.float32, (heads, rows, hd))))
+
+
 @pytest.mark.parametrize("rows", [1, 5, 8])
 def test_gemv_batched_scores_bit_exact(rows):
     """Up to 8 queries' scores through gemv.comp's order, one batch per

@@ -102,9 +102,10 @@ def spec_many_heads():
                            matrix_type=gguf.Q4_K, embed_type=gguf.Q4_K, output_type=gguf.Q6_K)
 
 
-def test_long_prompt_takes_the_reference_query_chunks(tmp_path):
+@pytest.mark.parametrize("prompt", [709, 300])
+def test_long_prompt_takes_the_reference_query_chunks(tmp_path, prompt):
     path = synth.write_model(spec_many_heads(), str(tmp_path / "heads32.gguf"), seed=5)
-    tokens = np.random.default_rng(7).integers(0, 1000, 709).astype(np.int32)
+    tokens = np.random.default_rng(7).integers(0, 1000, prompt).astype(np.int32)
     gpu = Llama(path, 720, kv_f16=True)
     ref = O.Model(path, 720, kv_f16=True)
     got = gpu.forward(tokens)
@@ -115,7 +116,7 @@ def test_long_prompt_takes_the_reference_query_chunks(tmp_path):
     import ctypes
     n = int(np.prod(kv_shape))
     kr = np.ctypeslib.as_array(ctypes.cast(O.lib().orc_model_k_cache(ref._h, 0), ctypes.POINTER(ctypes.c_uint16)), (n,)).reshape(kv_shape)
-    assert np.array_equal(k[:, :709], kr[:, :709])
+    assert np.array_equal(k[:, :prompt], kr[:, :prompt])
     first = int(np.argmax(got))
     toks, _ = greedy_oracle(ref, first, 3)
     assert list(gpu.generate_greedy(first, 3)) == list(toks)

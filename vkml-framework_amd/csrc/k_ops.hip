@@ -544,6 +544,11 @@ __global__ void __launch_bounds__(256) k_matmul(vkml_matmul_params p, const floa
     __shared__ __align__(16) float ta[16][68], tb[16][68];
     const uint32_t tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
     const uint32_t row0 = blockIdx.y * 64, col0 = blockIdx.x * 64, z = blockIdx.z;
+    // Under a causal mask the tile's last row sees keys up to row0 + 63 +
+    // offset: scores past it are never read, and a's entries past it are 0.
+    const uint64_t last_key = static_cast<uint64_t>(row0) + 63 + p.causal_offset;
+    if (BT && p.causal && col0 > last_key) return;
+    const uint32_t k_end = (!BT && p.causal) ? static_cast<uint32_t>(min<uint64_t>(p.k, last_key + 1)) : p.k;
     const float* az = a + static_cast<uint64_t>(z) * p.m * p.k;
     const uint64_t b_off = static_cast<uint64_t>(z / p.b_group) * p.b_stride;
     const auto b_at = [&](uint32_t n, uint32_t k) -> float {
@@ -559,7 +564,7 @@ __global__ void __launch_bounds__(256) k_matmul(vkml_matmul_params p, const floa
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-    for (uint32_t k0 = 0; k0 < p.k; k0 += 16) {
+    for (uint32_t k0 = 0; k0 < k_end; k0 += 16) {
         // Out-of-range elements are zeros, which add nothing.
 #pragma unroll
         for (uint32_t u = 0; u < 4; ++u) {
@@ -845,6 +850,7 @@ int vkml_matmul(const vkml_matmul_params* p, const float* a, const void* b, floa
     VKML_CHECK_ARG(p->b_type <= VKML_Q4_K, "matmul: unknown b type " + std::to_string(p->b_type));
     VKML_CHECK_ARG(p->b_group >= 1 && p->batches >= 1, "matmul: bad batching");
     const bool quant = p->b_type >= VKML_Q8_0;
+    VKML_CHECK_ARG(!p->causal || !quant, "matmul: the causal skip is for attention's products, not weights");
     if (quant) {
         VKML_CHECK_ARG(p->b_transposed && p->batches == 1, "matmul: quantized b must be one transposed [n, k] matrix");
         const uint32_t unit = p->b_type == VKML_Q4_K ? 256 : 32;

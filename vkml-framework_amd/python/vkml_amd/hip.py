@@ -43,7 +43,8 @@ GemvDotParams = _struct("GemvDotParams", [("m", u32), ("n", u32), ("k", u32), ("
 GemvParams = _struct("GemvParams", [("m", u32), ("n", u32), ("k", u32), ("b_type", u32), ("scale_type", u32),
                                     ("b_stride", u32), ("b_group", u32), ("batches", u32)])
 MatmulParams = _struct("MatmulParams", [("m", u32), ("n", u32), ("k", u32), ("b_stride", u32), ("b_group", u32),
-                                        ("batches", u32), ("b_transposed", u32), ("b_type", u32), ("scale_type", u32)])
+                                        ("batches", u32), ("b_transposed", u32), ("b_type", u32), ("scale_type", u32),
+                                        ("causal", u32), ("causal_offset", u32)])
 RmsNormParams = _struct("RmsNormParams", [("rows", u32), ("cols", u32), ("eps", f32)])
 SoftmaxParams = _struct("SoftmaxParams", [("rows", u32), ("cols", u32), ("scale", f32), ("causal", u32),
                                           ("q_len", u32), ("offset", u32), ("window", u32), ("softcap", f32)])

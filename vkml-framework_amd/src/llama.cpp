@@ -567,7 +567,7 @@ struct Llama::Impl {
             const vkml_gemv_params p{u32(t), u32(w.rows), u32(w.cols), w.type_code(), w.scale_code(), 0, 1, 1};
             check(vkml_gemv(&p, a, w.values(), out, w.scales()), what);
         } else {
-            const vkml_matmul_params p{u32(t), u32(w.rows), u32(w.cols), 0, 1, 1, 1, w.type_code(), w.scale_code()};
+            const vkml_matmul_params p{u32(t), u32(w.rows), u32(w.cols), 0, 1, 1, 1, w.type_code(), w.scale_code(), 0, 0};
             check(vkml_matmul(&p, a, w.values(), out, w.scales()), what);
         }
     }

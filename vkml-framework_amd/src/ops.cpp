@@ -19,6 +19,10 @@ namespace {
 
 constexpr std::int64_t kGemvMaxRows = 8;
 
+// The scores one prompt-attention piece may take here (the reference's
+// 64 MiB budget is sized for integrated GPUs; MI355X has 288 GB of HBM).
+constexpr std::int64_t kPromptScoreBytes = std::int64_t{1} << 30;
+
 Tensor like(const Tensor& t, Shape shape, DType dtype) { return TensorAccess::empty(TensorAccess::runtime(t), std::move(shape), dtype); }
 
 std::uint32_t u32(std::int64_t v) {
@@ -287,7 +291,8 @@ namespace detail {
 
 // a [..., M, K] times b [K, N] (or [N, K] transposed), b shared when 2-D,
 // batched otherwise; b_group as the reference (src/ops/matmul.cpp:124-195).
-Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transposed, std::int64_t b_group, std::int64_t b_rows) {
+Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transposed, std::int64_t b_group, std::int64_t b_rows,
+              std::int64_t causal_offset) {
     const Shape& as = a.shape();
     Shape bs = b.shape();
     const std::string b_desc = (transposed ? "transposed " : "") + to_string(bs);
@@ -340,7 +345,8 @@ Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transpose
         return out;
     }
     const vkml_matmul_params p{u32(m), u32(n), u32(k), u32(b_stride), group, u32(batches), transposed ? 1u : 0u,
-                               detail::type_code(b.dtype()), VKML_F32};
+                               detail::type_code(b.dtype()), VKML_F32, causal_offset >= 0 ? 1u : 0u,
+                               u32(std::max<std::int64_t>(causal_offset, 0))};
     check(vkml_matmul(&p, static_cast<const float*>(a.data()), b.data(), static_cast<float*>(out.data()), nullptr), name);
     return out;
 }
@@ -407,7 +413,7 @@ Tensor matmul_transposed(const Tensor& a, const QuantizedMatrix& b) {
         const vkml_gemv_params p{u32(m), u32(b.rows), u32(b.cols), type, st, 0, 1, 1};
         check(vkml_gemv(&p, static_cast<const float*>(a.data()), b.values.data(), c, b.scales.data()), "matmul_transposed");
     } else {
-        const vkml_matmul_params p{u32(m), u32(b.rows), u32(b.cols), 0, 1, 1, 1, type, st};
+        const vkml_matmul_params p{u32(m), u32(b.rows), u32(b.cols), 0, 1, 1, 1, type, st, 0, 0};
         check(vkml_matmul(&p, static_cast<const float*>(a.data()), b.values.data(), c, b.scales.data()), "matmul_transposed");
     }
     return out;
@@ -462,27 +468,60 @@ Tensor attention_block(const Tensor& q, const Tensor& k_cache, const Tensor& v_c
     return matmul("attention", probs, v_cache, false, group, keys);
 }
 
-// detail::attention for more than one query (attention.cpp:205-226): the
-// queries in chunks whose scores [heads, rows, kv_len] f32 fit
-// max_score_bytes (whole 64s of rows when at least 64), each against the
-// keys its last query sees. The chunks leave every value as one call would
-// give it but for gemv's order on a last chunk of 8 rows or fewer.
+// detail::attention for more than one query (attention.cpp:205-226). The
+// reference runs the queries in chunks whose scores [heads, rows, kv_len]
+// f32 fit max_score_bytes (whole 64s of rows when at least 64), each
+// against the keys its last query sees. What the chunks fix is only which
+// queries' scores go through gemv.comp's order (a chunk of 8 rows or
+// fewer); keys past a chunk's last query carry probability exactly 0 and
+// add nothing. So the rows of chunks of more than 8 are run here in pieces
+// of this build's own budget (HBM is large), with the work the causal mask
+// makes moot skipped, and the rest as the reference's chunks.
 Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache, std::int64_t kv_len, bool causal,
                         std::int64_t window, float softcap, std::int64_t max_score_bytes) {
-    const std::int64_t heads = q.shape()[0], q_len = q.shape()[1];
+    const std::int64_t heads = q.shape()[0], q_len = q.shape()[1], hd = q.shape()[2];
     const std::int64_t row_bytes = heads * std::max<std::int64_t>(kv_len, 1) * 4;
     std::int64_t chunk = std::max<std::int64_t>(1, max_score_bytes / row_bytes);
     if (chunk >= 64) chunk -= chunk % 64;
-    if (q_len <= chunk) return attention_block(q, k_cache, v_cache, kv_len, causal, window, softcap);
-    Tensor out = like(q, q.shape(), DType::F32);
+    if (q_len <= chunk && (q_len <= kGemvMaxRows || !causal)) return attention_block(q, k_cache, v_cache, kv_len, causal, window, softcap);
     const std::int64_t first = kv_len - q_len;  // key position of query 0
-    for (std::int64_t q0 = 0; q0 < q_len; q0 += chunk) {
-        const std::int64_t rows = std::min(chunk, q_len - q0);
+    Tensor out = like(q, q.shape(), DType::F32);
+    const auto reference_chunk = [&](std::int64_t q0, std::int64_t rows) {
         const std::int64_t keys = causal ? first + q0 + rows : kv_len;
-        Tensor part = like(q, {heads, rows, q.shape()[2]}, DType::F32);
+        Tensor part = like(q, {heads, rows, hd}, DType::F32);
         copy_rows(q, q0, part, 0, rows);
         copy_rows(attention_block(part, k_cache, v_cache, keys, causal, window, softcap), 0, out, q0, rows);
+    };
+    if (chunk <= kGemvMaxRows || !causal) {
+        for (std::int64_t q0 = 0; q0 < q_len; q0 += chunk) reference_chunk(q0, std::min(chunk, q_len - q0));
+        return out;
     }
+    const std::int64_t tail = q_len > chunk ? q_len % chunk : 0;
+    const std::int64_t gemv_rows = tail <= kGemvMaxRows ? tail : 0;
+    const std::int64_t rows_all = q_len - gemv_rows;
+    const std::int64_t group = heads / k_cache.shape()[0];
+    std::int64_t piece = std::max<std::int64_t>(64, kPromptScoreBytes / row_bytes);
+    piece -= piece % 64;
+    for (std::int64_t r0 = 0; r0 < rows_all;) {
+        std::int64_t rows = std::min(piece, rows_all - r0);
+        if (rows_all - r0 - rows <= kGemvMaxRows) rows = rows_all - r0;  // no piece of 8 rows or fewer
+        const std::int64_t keys = first + r0 + rows;
+        Tensor part = q;
+        if (rows != q_len) {
+            part = like(q, {heads, rows, hd}, DType::F32);
+            copy_rows(q, r0, part, 0, rows);
+        }
+        const Tensor scores = matmul("attention", part, k_cache, true, group, keys, first + r0);
+        Tensor probs = like(q, scores.shape(), DType::F32);
+        const vkml_softmax_params sp{u32(heads * rows), u32(keys), 1.0f / std::sqrt(static_cast<float>(hd)), 1u, u32(rows),
+                                     u32(first + r0), u32(window), softcap};
+        check(vkml_softmax(&sp, static_cast<const float*>(scores.data()), static_cast<float*>(probs.data())), "attention");
+        const Tensor o = matmul("attention", probs, v_cache, false, group, keys, first + r0);
+        if (rows == q_len) return o;
+        copy_rows(o, 0, out, r0, rows);
+        r0 += rows;
+    }
+    if (gemv_rows) reference_chunk(rows_all, gemv_rows);
     return out;
 }
 

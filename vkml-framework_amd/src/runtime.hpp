@@ -70,7 +70,10 @@ inline constexpr std::int64_t kMaxScoreBytes = std::int64_t{64} << 20;
 
 // a [..., M, K] times b [K, N] (or [N, K] transposed); with b_group > 1, a's
 // batch z against b's z / b_group; b_rows >= 0 uses b's first rows only.
-Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transposed, std::int64_t b_group = 1, std::int64_t b_rows = -1);
+// causal_offset >= 0: row r of each batch sees keys 0 .. r + causal_offset
+// only (vkml_matmul's causal skip; no effect on up to 8 rows).
+Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transposed, std::int64_t b_group = 1, std::int64_t b_rows = -1,
+              std::int64_t causal_offset = -1);
 
 // Queries q [heads, q_len, hd] against keys 0..kv_len of caches [kv_heads,
 // capacity, hd], query i at key position kv_len - q_len + i, in the

@@ -20,11 +20,14 @@
 // column l % 16 at the block's values 8 (l / 16) .. 8 (l / 16) + 7 (one
 // 8-byte operand each), and gets the results for rows 4 (l / 16) .. + 3 of
 // column l % 16. The operands are loaded straight from memory (L2 serves the
-// reuse across workgroups), each block's while the block before is scaled.
-// K runs in chunks of 8 blocks: every row's (scale, code sum) and every
-// column's (scale, offset) per block are staged in LDS for a chunk,
-// double-buffered, their loads in flight during the chunk before, one
-// barrier a chunk; the scaling reads four rows' values as one 16-byte word.
+// reuse across workgroups). K runs in chunks of 8 blocks: for each chunk the
+// workgroup first stages every row's (scale, code sum) and every column's
+// (scale, offset) per block in LDS, double-buffered, one barrier a chunk;
+// the scaling then reads four rows' values as one 16-byte word. The kernel
+// is bound by those f32 scalings on the VALU (4 operations per output and
+// block, 6 with offsets): at about 120 VGPRs four waves share a SIMD, which
+// measured faster than prefetching operands and statistics a block ahead
+// at two waves.
 #include <algorithm>
 
 #include "../../include/vkml_hip.h"
@@ -121,72 +124,16 @@ __device__ __forceinline__ void q4k_block_scale(const uint4& h, uint32_t j, floa
 
 constexpr uint32_t kChunk = 8;  // blocks of K a chunk (a q4_K super-block)
 
-// A thread's share of one chunk's statistics, loaded ahead of the chunk:
-// two (row, block) entries and one column's four blocks.
-template <int FMT, bool F16S>
-struct ChunkStats {
-    static constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
-    float sa[2];
-    uint4 codes[2][2];  // the two rows' 32 codes (code sums, for offsets)
-    uint4 header;       // q4_K: the column's super-block header
-    float s[4], o[4];   // other formats: the column's four blocks
-
-    __device__ __forceinline__ void load(const MatmulDotArgs& p, uint32_t t, uint32_t c0, uint32_t row0, uint32_t col0) {
-        const uint32_t blocks = p.k / 32;
-#pragma unroll
-        for (uint32_t u = 0; u < 2; ++u) {
-            const uint32_t e = t + kT * u, r = e % kTileM, blk = min(c0 + e / kTileM, blocks - 1);
-            const uint32_t row = min(row0 + r, p.m - 1);
-            sa[u] = ldg(p.a_scales + static_cast<uint64_t>(row) * blocks + blk);
-            if constexpr (kOffset) {
-                const uint4* c = reinterpret_cast<const uint4*>(p.a + static_cast<uint64_t>(row) * p.k + blk * 32);
-                codes[u][0] = ldg(c);
-                codes[u][1] = ldg(c + 1);
-            }
-        }
-        const uint32_t col = min(col0 + t / 2, p.n - 1), b0 = 4 * (t % 2);
-        if constexpr (FMT == VKML_Q4_K) {
-            header = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.b_scales) +
-                                                        (static_cast<uint64_t>(col) * (p.k / 256) + c0 / 8) * 16));
-        } else {
-#pragma unroll
-            for (uint32_t b = 0; b < 4; ++b) b_block_scale<FMT, F16S>(p, col, min(c0 + b0 + b, blocks - 1), s[b], o[b]);
-        }
-    }
-
-    template <class L>
-    __device__ __forceinline__ void store(L& lds, uint32_t t) const {
-#pragma unroll
-        for (uint32_t u = 0; u < 2; ++u) {
-            const uint32_t e = t + kT * u, r = e % kTileM, b = e / kTileM;
-            lds.sa[b][r] = sa[u];
-            if constexpr (kOffset) lds.asum[b][r] = static_cast<float>(byte_sum(codes[u][0]) + byte_sum(codes[u][1]));
-        }
-        const uint32_t cl = t / 2, b0 = 4 * (t % 2);
-#pragma unroll
-        for (uint32_t b = 0; b < 4; ++b) {
-            float sv = s[b], ov = o[b];
-            if constexpr (FMT == VKML_Q4_K) q4k_block_scale(header, b0 + b, sv, ov);
-            lds.sb[b0 + b][cl] = sv;
-            if constexpr (kOffset) lds.ob[b0 + b][cl] = ov;
-        }
-    }
-};
-
-// One chunk's statistics in LDS, [block of the chunk][row or column].
-template <bool kOffset>
-struct ChunkLds {
-    float sa[kChunk][kTileM];
-    float asum[kChunk][kOffset ? kTileM : 4];
-    float sb[kChunk][kTileN];
-    float ob[kChunk][kOffset ? kTileN : 1];
-};
-
 template <int FMT, bool F16S>
 __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
 #pragma clang fp contract(off)
     constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
-    __shared__ __align__(16) ChunkLds<kOffset> lds[2];
+    // Per chunk, double-buffered: rows' scales and code sums, columns'
+    // scales and offsets, [block of the chunk][row or column].
+    __shared__ __align__(16) float s_sa[2][kChunk][kTileM];
+    __shared__ __align__(16) float s_asum[2][kChunk][kOffset ? kTileM : 4];
+    __shared__ float s_sb[2][kChunk][kTileN];
+    __shared__ float s_ob[2][kChunk][kOffset ? kTileN : 1];
     const uint32_t t = thread_index(), lane = t % kWave, wave = t / kWave;
     const uint32_t g = lane / 16, li = lane % 16;
     const uint32_t row0 = blockIdx.y * kTileM, col0 = blockIdx.x * kTileN;
@@ -205,79 +152,77 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[r][c][i] = 0.0f;
 
-    // The operands of block blk (clamped to the last block: the prefetch
-    // past the end loads something harmless).
-    const auto load_ops = [&](uint32_t blk, long (&av)[4], long (&bv)[2]) {
-        blk = min(blk, blocks - 1);
+    for (uint32_t c0 = 0, buf = 0; c0 < blocks; c0 += kChunk, buf ^= 1) {
+        // Stage the chunk's statistics: 64 rows x 8 blocks (two each) and
+        // 128 columns x 8 blocks (four each: one column, half the blocks).
 #pragma unroll
-        for (int r = 0; r < 4; ++r) av[r] = static_cast<long>(__builtin_bit_cast(uint64_t, ldg(reinterpret_cast<const uint2*>(arow[r] + blk * 32))));
-#pragma unroll
-        for (int c = 0; c < 2; ++c) bv[c] = b_codes<FMT>(p, bcol[c], blk, g);
-    };
-    // Block b of the chunk staged in st: the integer sums of its 4 x 2
-    // tiles, scaled and added in the reference's order.
-    const auto block = [&](const ChunkLds<kOffset>& st, uint32_t b, const long (&av)[4], const long (&bv)[2]) {
-        float sb[2], ob[2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            sb[c] = st.sb[b][32 * wave + 16 * c + li];
-            ob[c] = 0.0f;
-            if constexpr (kOffset) ob[c] = st.ob[b][32 * wave + 16 * c + li];
+        for (uint32_t u = 0; u < 2; ++u) {
+            const uint32_t e = t + kT * u, r = e % kTileM, b = e / kTileM, blk = c0 + b;
+            if (blk < blocks) {
+                const uint32_t row = min(row0 + r, p.m - 1);
+                s_sa[buf][b][r] = ldg(p.a_scales + static_cast<uint64_t>(row) * blocks + blk);
+                if constexpr (kOffset) {
+                    const uint4* codes = reinterpret_cast<const uint4*>(p.a + static_cast<uint64_t>(row) * p.k + blk * 32);
+                    s_asum[buf][b][r] = static_cast<float>(byte_sum(ldg(codes)) + byte_sum(ldg(codes + 1)));
+                }
+            }
         }
+        {
+            const uint32_t cl = t / 2, b0 = 4 * (t % 2), col = min(col0 + cl, p.n - 1);
+            if constexpr (FMT == VKML_Q4_K) {
+                const uint4 h = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.b_scales) +
+                                                                   (static_cast<uint64_t>(col) * (p.k / 256) + c0 / 8) * 16));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float4 sa4 = *reinterpret_cast<const float4*>(&st.sa[b][16 * r + 4 * g]);
-            float4 as4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if constexpr (kOffset) as4 = *reinterpret_cast<const float4*>(&st.asum[b][16 * r + 4 * g]);
-            const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, asum[4] = {as4.x, as4.y, as4.z, as4.w};
+                for (uint32_t b = 0; b < 4; ++b) q4k_block_scale(h, b0 + b, s_sb[buf][b0 + b][cl], s_ob[buf][b0 + b][cl]);
+            } else {
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if constexpr (kOffset) {
-                        acc[r][c][i] += sa[i] * (static_cast<float>(d[i]) * sb[c] + asum[i] * ob[c]);
-                    } else {
-                        acc[r][c][i] += static_cast<float>(d[i]) * (sa[i] * sb[c]);
+                for (uint32_t b = 0; b < 4; ++b) {
+                    if (c0 + b0 + b < blocks) {
+                        float s, o;
+                        b_block_scale<FMT, F16S>(p, col, c0 + b0 + b, s, o);
+                        s_sb[buf][b0 + b][cl] = s;
+                        if constexpr (kOffset) s_ob[buf][b0 + b][cl] = o;
                     }
                 }
             }
         }
-    };
-
-    ChunkStats<FMT, F16S> next;
-    next.load(p, t, 0, row0, col0);
-    next.store(lds[0], t);
-    __syncthreads();
-    long av[4], bv[2];
-    load_ops(0, av, bv);
-    for (uint32_t c0 = 0, buf = 0; c0 < blocks; c0 += kChunk, buf ^= 1) {
-        const bool more = c0 + kChunk < blocks;
-        if (more) next.load(p, t, c0 + kChunk, row0, col0);  // the next chunk's statistics, in flight meanwhile
-        if (c0 + kChunk <= blocks) {
+        __syncthreads();  // the chunk's statistics are staged (the other buffer's readers finished a chunk ago)
 #pragma unroll
-            for (uint32_t b = 0; b < kChunk; ++b) {
-                long an[4], bn[2];
-                load_ops(c0 + b + 1, an, bn);
-                block(lds[buf], b, av, bv);
+        for (uint32_t b = 0; b < kChunk; ++b) {
+            const uint32_t blk = c0 + b;
+            if (blk >= blocks) break;
+            long av[4], bv[2];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) av[r] = an[r];
+            for (int r = 0; r < 4; ++r) av[r] = static_cast<long>(__builtin_bit_cast(uint64_t, ldg(reinterpret_cast<const uint2*>(arow[r] + blk * 32))));
 #pragma unroll
-                for (int c = 0; c < 2; ++c) bv[c] = bn[c];
+            for (int c = 0; c < 2; ++c) bv[c] = b_codes<FMT>(p, bcol[c], blk, g);
+            float sb[2], ob[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                sb[c] = s_sb[buf][b][32 * wave + 16 * c + li];
+                ob[c] = 0.0f;
+                if constexpr (kOffset) ob[c] = s_ob[buf][b][32 * wave + 16 * c + li];
             }
-        } else {
-            for (uint32_t b = 0; c0 + b < blocks; ++b) {
-                long an[4], bn[2];
-                load_ops(c0 + b + 1, an, bn);
-                block(lds[buf], b, av, bv);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) av[r] = an[r];
+            for (int r = 0; r < 4; ++r) {
+                const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[buf][b][16 * r + 4 * g]);
+                float4 as4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if constexpr (kOffset) as4 = *reinterpret_cast<const float4*>(&s_asum[buf][b][16 * r + 4 * g]);
+                const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, asum[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
-                for (int c = 0; c < 2; ++c) bv[c] = bn[c];
+                for (int c = 0; c < 2; ++c) {
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if constexpr (kOffset) {
+                            acc[r][c][i] += sa[i] * (static_cast<float>(d[i]) * sb[c] + asum[i] * ob[c]);
+                        } else {
+                            acc[r][c][i] += static_cast<float>(d[i]) * (sa[i] * sb[c]);
+                        }
+                    }
+                }
             }
         }
-        if (more) next.store(lds[buf ^ 1], t);  // its readers finished a chunk ago, before the last barrier
-        __syncthreads();
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)

@@ -274,3 +274,15 @@ def test_persistent_layers_match_oracle(files):
     toks = gpu.generate_greedy(first, 6)
     want_toks, _ = greedy_oracle(ref, first, 6)
     assert list(toks) == list(want_toks)
+
+
+def test_vkml_bench_app_results_are_exact():
+    """bin/vkml-bench's decode, m-sweep and prefill cases (gemv_dot and the
+    matrix-core matmul_dot) against the "quarters" closed form: every output
+    is 0.25 x K exactly."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(__file__), "..", "vkml-framework_amd", "bin", "vkml-bench")
+    r = subprocess.run([exe, "3"], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr
+    lines = [ln for ln in r.stdout.splitlines()[1:] if ln.strip()]
+    assert len(lines) == 18 and all(ln.split()[-1] == "ok" for ln in lines), r.stdout

@@ -39,7 +39,6 @@ using namespace vkml::dev;
 namespace {
 
 constexpr uint32_t kT = 256;      // four waves
-constexpr uint32_t kTileM = 64, kTileN = 128;
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct MatmulDotArgs {
@@ -124,40 +123,44 @@ __device__ __forceinline__ void q4k_block_scale(const uint4& h, uint32_t j, floa
 
 constexpr uint32_t kChunk = 8;  // blocks of K a chunk (a q4_K super-block)
 
-template <int FMT, bool F16S>
+// One kernel per per-wave tile: RT row tiles of 16 by CT column tiles of
+// 16; a workgroup's four waves take 4 CT column tiles side by side, so its
+// tile is 16 RT x 64 CT.
+template <int FMT, bool F16S, int RT, int CT>
 __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
 #pragma clang fp contract(off)
     constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
+    constexpr uint32_t TM = 16 * RT, TN = 64 * CT;
     // Per chunk, double-buffered: rows' scales and code sums, columns'
     // scales and offsets, [block of the chunk][row or column].
-    __shared__ __align__(16) float s_sa[2][kChunk][kTileM];
-    __shared__ __align__(16) float s_asum[2][kChunk][kOffset ? kTileM : 4];
-    __shared__ float s_sb[2][kChunk][kTileN];
-    __shared__ float s_ob[2][kChunk][kOffset ? kTileN : 1];
+    __shared__ __align__(16) float s_sa[2][kChunk][TM];
+    __shared__ __align__(16) float s_asum[2][kChunk][kOffset ? TM : 4];
+    __shared__ float s_sb[2][kChunk][TN];
+    __shared__ float s_ob[2][kChunk][kOffset ? TN : 1];
     const uint32_t t = thread_index(), lane = t % kWave, wave = t / kWave;
     const uint32_t g = lane / 16, li = lane % 16;
-    const uint32_t row0 = blockIdx.y * kTileM, col0 = blockIdx.x * kTileN;
+    const uint32_t row0 = blockIdx.y * TM, col0 = blockIdx.x * TN;
     const uint32_t blocks = p.k / 32;
-    const uint8_t* arow[4];
+    const uint8_t* arow[RT];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) arow[r] = p.a + static_cast<uint64_t>(min(row0 + 16 * r + li, p.m - 1)) * p.k + 8 * g;
-    uint32_t bcol[2];
+    for (int r = 0; r < RT; ++r) arow[r] = p.a + static_cast<uint64_t>(min(row0 + 16 * r + li, p.m - 1)) * p.k + 8 * g;
+    uint32_t bcol[CT];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) bcol[c] = min(col0 + 32 * wave + 16 * c + li, p.n - 1);
-    float acc[4][2][4];
+    for (int c = 0; c < CT; ++c) bcol[c] = min(col0 + 16 * CT * wave + 16 * c + li, p.n - 1);
+    float acc[RT][CT][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < CT; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[r][c][i] = 0.0f;
 
     for (uint32_t c0 = 0, buf = 0; c0 < blocks; c0 += kChunk, buf ^= 1) {
-        // Stage the chunk's statistics: 64 rows x 8 blocks (two each) and
-        // 128 columns x 8 blocks (four each: one column, half the blocks).
+        // Stage the chunk's statistics: TM rows x 8 blocks, and TN columns x
+        // 8 blocks (a column's four blocks a thread).
 #pragma unroll
-        for (uint32_t u = 0; u < 2; ++u) {
-            const uint32_t e = t + kT * u, r = e % kTileM, b = e / kTileM, blk = c0 + b;
+        for (uint32_t e = t; e < TM * kChunk; e += kT) {
+            const uint32_t r = e % TM, b = e / TM, blk = c0 + b;
             if (blk < blocks) {
                 const uint32_t row = min(row0 + r, p.m - 1);
                 s_sa[buf][b][r] = ldg(p.a_scales + static_cast<uint64_t>(row) * blocks + blk);
@@ -167,8 +170,9 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
                 }
             }
         }
-        {
-            const uint32_t cl = t / 2, b0 = 4 * (t % 2), col = min(col0 + cl, p.n - 1);
+#pragma unroll
+        for (uint32_t e = t; e < TN * 2; e += kT) {
+            const uint32_t cl = e / 2, b0 = 4 * (e % 2), col = min(col0 + cl, p.n - 1);
             if constexpr (FMT == VKML_Q4_K) {
                 const uint4 h = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.b_scales) +
                                                                    (static_cast<uint64_t>(col) * (p.k / 256) + c0 / 8) * 16));
@@ -191,26 +195,26 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
         for (uint32_t b = 0; b < kChunk; ++b) {
             const uint32_t blk = c0 + b;
             if (blk >= blocks) break;
-            long av[4], bv[2];
+            long av[RT], bv[CT];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) av[r] = static_cast<long>(__builtin_bit_cast(uint64_t, ldg(reinterpret_cast<const uint2*>(arow[r] + blk * 32))));
+            for (int r = 0; r < RT; ++r) av[r] = static_cast<long>(__builtin_bit_cast(uint64_t, ldg(reinterpret_cast<const uint2*>(arow[r] + blk * 32))));
 #pragma unroll
-            for (int c = 0; c < 2; ++c) bv[c] = b_codes<FMT>(p, bcol[c], blk, g);
-            float sb[2], ob[2];
+            for (int c = 0; c < CT; ++c) bv[c] = b_codes<FMT>(p, bcol[c], blk, g);
+            float sb[CT], ob[CT];
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                sb[c] = s_sb[buf][b][32 * wave + 16 * c + li];
+            for (int c = 0; c < CT; ++c) {
+                sb[c] = s_sb[buf][b][16 * CT * wave + 16 * c + li];
                 ob[c] = 0.0f;
-                if constexpr (kOffset) ob[c] = s_ob[buf][b][32 * wave + 16 * c + li];
+                if constexpr (kOffset) ob[c] = s_ob[buf][b][16 * CT * wave + 16 * c + li];
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int r = 0; r < RT; ++r) {
                 const float4 sa4 = *reinterpret_cast<const float4*>(&s_sa[buf][b][16 * r + 4 * g]);
                 float4 as4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if constexpr (kOffset) as4 = *reinterpret_cast<const float4*>(&s_asum[buf][b][16 * r + 4 * g]);
                 const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, asum[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
+                for (int c = 0; c < CT; ++c) {
                     const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -225,10 +229,10 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
         }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const uint32_t col = col0 + 32 * wave + 16 * c + li;
+        for (int c = 0; c < CT; ++c) {
+            const uint32_t col = col0 + 16 * CT * wave + 16 * c + li;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t row = row0 + 16 * r + 4 * g + i;
@@ -237,10 +241,24 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
         }
 }
 
+template <int FMT, bool F16S, int RT, int CT>
+void launch_tiles(const MatmulDotArgs& p) {
+    const dim3 grid((p.n + 64 * CT - 1) / (64 * CT), (p.m + 16 * RT - 1) / (16 * RT));
+    hipLaunchKernelGGL((k_matmul_dot<FMT, F16S, RT, CT>), grid, dim3(kT), 0, vkml::abi::stream(), p);
+}
+
+// The largest per-wave tile (the most reuse of each loaded operand and
+// statistic) that still gives the SIMDs about two waves each; short prompts
+// take the smaller tiles. (Measured: at 128 rows x 14336 columns the 32 x 32
+// tile beats 64 x 32 with half the waves and 32 x 16 with twice as many.)
 template <int FMT, bool F16S>
 void launch(const MatmulDotArgs& p) {
-    const dim3 grid((p.n + kTileN - 1) / kTileN, (p.m + kTileM - 1) / kTileM);
-    hipLaunchKernelGGL((k_matmul_dot<FMT, F16S>), grid, dim3(kT), 0, vkml::abi::stream(), p);
+    const auto waves = [&](uint64_t rt, uint64_t ct) { return ((p.m + 16 * rt - 1) / (16 * rt)) * ((p.n + 16 * ct - 1) / (16 * ct)); };
+    constexpr uint64_t kEnough = 1792;  // 256 CUs x 4 SIMDs x 1.75
+    if (waves(4, 2) >= kEnough) launch_tiles<FMT, F16S, 4, 2>(p);
+    else if (waves(2, 2) >= kEnough) launch_tiles<FMT, F16S, 2, 2>(p);
+    else if (waves(2, 1) >= kEnough) launch_tiles<FMT, F16S, 2, 1>(p);
+    else launch_tiles<FMT, F16S, 1, 1>(p);
 }
 
 }  // namespace

@@ -34,6 +34,7 @@ typedef struct vkml_llama_options {
     int32_t use_graphs;         /* 1: replay the decode step as a HIP graph (default) */
     int32_t persistent_layers;  /* 1: a step's layers in one persistent launch where the model allows (default 0) */
     const char* device_name;    /* NULL or "": VKML_DEVICE, then device 0 */
+    int64_t prompt_score_bytes; /* scores one piece of a prompt's attention may hold (default 1 GiB); no effect on results */
 } vkml_llama_options;
 
 /* LlamaConfig (llama.hpp:29-116), the fields of the llama architecture. */

@@ -102,11 +102,14 @@ def spec_many_heads():
                            matrix_type=gguf.Q4_K, embed_type=gguf.Q4_K, output_type=gguf.Q6_K)
 
 
-@pytest.mark.parametrize("prompt", [709, 300])
-def test_long_prompt_takes_the_reference_query_chunks(tmp_path, prompt):
+@pytest.mark.parametrize("prompt,pieces", [(709, 1), (300, 1), (709, 11), (300, 4)])
+def test_long_prompt_takes_the_reference_query_chunks(tmp_path, prompt, pieces):
+    # pieces: this build's own split of the queries past the gemv tail (a
+    # score budget of that many 64-query pieces), which must change nothing
     path = synth.write_model(spec_many_heads(), str(tmp_path / "heads32.gguf"), seed=5)
     tokens = np.random.default_rng(7).integers(0, 1000, prompt).astype(np.int32)
-    gpu = Llama(path, 720, kv_f16=True)
+    budget = 0 if pieces == 1 else 32 * prompt * 4 * 64
+    gpu = Llama(path, 720, kv_f16=True, prompt_score_bytes=budget)
     ref = O.Model(path, 720, kv_f16=True)
     got = gpu.forward(tokens)
     want = ref.forward(tokens)

@@ -79,6 +79,11 @@ struct LlamaOptions {
     // int8 activations for this model's quantized weights, when the Context
     // allows them too (ContextOptions::integer_dot_product).
     bool integer_dot_product = true;
+    // The f32 scores one piece of a prompt's attention may hold ([heads,
+    // queries, keys]); longer prompts run in pieces of whole 64s of queries.
+    // The results do not depend on it (the reference's own 64 MiB chunks
+    // decide which queries take gemv's order).
+    std::int64_t prompt_score_bytes = std::int64_t{1} << 30;
 };
 
 class Llama {

@@ -16,7 +16,7 @@ i32, i64, u32, u64, vp = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_void_
 
 class Options(C.Structure):
     _fields_ = [("kv_cache_f16", i32), ("quantize", i32), ("integer_dot", i32), ("use_graphs", i32),
-                ("persistent_layers", i32), ("device_name", C.c_char_p)]
+                ("persistent_layers", i32), ("device_name", C.c_char_p), ("prompt_score_bytes", i64)]
 
 
 class Config(C.Structure):
@@ -80,11 +80,13 @@ def _ptr(a: np.ndarray):
 
 class Llama:
     def __init__(self, path: str, context: int, kv_f16: bool = False, quantize: int = -1, integer_dot: bool = True,
-                 use_graphs: bool = True, persistent_layers: bool = False):
+                 use_graphs: bool = True, persistent_layers: bool = False, prompt_score_bytes: int = 0):
         o = Options()
         lib().vkml_llama_default_options(C.byref(o))
         o.kv_cache_f16, o.quantize, o.integer_dot = int(kv_f16), int(quantize), int(integer_dot)
         o.use_graphs, o.persistent_layers = int(use_graphs), int(persistent_layers)
+        if prompt_score_bytes:
+            o.prompt_score_bytes = int(prompt_score_bytes)
         self._h = vp()
         _check(lib().vkml_llama_load(path.encode(), int(context), C.byref(o), C.byref(self._h)))
         cfg = Config()

@@ -623,7 +623,8 @@ struct Llama::Impl {
                                       const_cast<void*>(L.k_cache.data()), const_cast<void*>(L.v_cache.data())),
                   "rope_kv");
             tag("attention");
-            const Tensor attn = detail::attention_prompt(q, L.k_cache, L.v_cache, end, true, 0, 0.0f, detail::kMaxScoreBytes);
+            const Tensor attn =
+                detail::attention_prompt(q, L.k_cache, L.v_cache, end, true, 0, 0.0f, detail::kMaxScoreBytes, options.prompt_score_bytes);
             const Tensor merged = permute(attn, {1, 0, 2}).reshape({t, qd});
             const Rows m_in = rows_of(merged, t, qd, int_dot && quantized_input(L.o) && qd % 32 == 0);
             project_rows(L.o, m_in, t, yp, "o");
@@ -703,6 +704,7 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
         throw Error("Llama::load: no model at " + path.string() + ": give a .gguf file");
     }
     if (path.extension() != ".gguf") throw Error("Llama::load: " + path.string() + " is not a .gguf file (this build reads GGUF)");
+    if (options.prompt_score_bytes <= 0) throw Error("Llama: prompt_score_bytes must be positive");
     if (options.kv_cache != DType::F32 && options.kv_cache != DType::F16) {
         throw Error("Llama: a KV cache of " + std::string(to_string(options.kv_cache)) + " is not implemented (f32 and f16 are)");
     }

@@ -19,9 +19,6 @@ namespace {
 
 constexpr std::int64_t kGemvMaxRows = 8;
 
-// The scores one prompt-attention piece may take here (the reference's
-// 64 MiB budget is sized for integrated GPUs; MI355X has 288 GB of HBM).
-constexpr std::int64_t kPromptScoreBytes = std::int64_t{1} << 30;
 
 Tensor like(const Tensor& t, Shape shape, DType dtype) { return TensorAccess::empty(TensorAccess::runtime(t), std::move(shape), dtype); }
 
@@ -476,9 +473,11 @@ Tensor attention_block(const Tensor& q, const Tensor& k_cache, const Tensor& v_c
 // fewer); keys past a chunk's last query carry probability exactly 0 and
 // add nothing. So the rows of chunks of more than 8 are run here in pieces
 // of this build's own budget (HBM is large), with the work the causal mask
-// makes moot skipped, and the rest as the reference's chunks.
+// makes moot skipped, and the rest as the reference's chunks. piece_bytes
+// defaults to 1 GiB: the reference's 64 MiB budget is sized for integrated
+// GPUs, and MI355X has 288 GB of HBM.
 Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache, std::int64_t kv_len, bool causal,
-                        std::int64_t window, float softcap, std::int64_t max_score_bytes) {
+                        std::int64_t window, float softcap, std::int64_t max_score_bytes, std::int64_t piece_bytes) {
     const std::int64_t heads = q.shape()[0], q_len = q.shape()[1], hd = q.shape()[2];
     const std::int64_t row_bytes = heads * std::max<std::int64_t>(kv_len, 1) * 4;
     std::int64_t chunk = std::max<std::int64_t>(1, max_score_bytes / row_bytes);
@@ -500,7 +499,7 @@ Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_
     const std::int64_t gemv_rows = tail <= kGemvMaxRows ? tail : 0;
     const std::int64_t rows_all = q_len - gemv_rows;
     const std::int64_t group = heads / k_cache.shape()[0];
-    std::int64_t piece = std::max<std::int64_t>(64, kPromptScoreBytes / row_bytes);
+    std::int64_t piece = std::max<std::int64_t>(64, piece_bytes / row_bytes);
     piece -= piece % 64;
     for (std::int64_t r0 = 0; r0 < rows_all;) {
         std::int64_t rows = std::min(piece, rows_all - r0);

@@ -78,7 +78,10 @@ Tensor matmul(const char* name, const Tensor& a, const Tensor& b, bool transpose
 // Queries q [heads, q_len, hd] against keys 0..kv_len of caches [kv_heads,
 // capacity, hd], query i at key position kv_len - q_len + i, in the
 // reference's query chunks (attention.cpp:205-226).
+// piece_bytes: this build's budget for one piece of the queries (results
+// do not depend on it).
 Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_cache, std::int64_t kv_len, bool causal,
-                        std::int64_t window, float softcap, std::int64_t max_score_bytes);
+                        std::int64_t window, float softcap, std::int64_t max_score_bytes,
+                        std::int64_t piece_bytes = std::int64_t{1} << 30);
 
 }  // namespace vkml::detail

@@ -158,6 +158,27 @@ def bits(x):
     return np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
 
 
+@pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_0, H.Q4_1, H.Q4_K])
+@pytest.mark.parametrize("m,n,k", [(2, 300, 512), (8, 1000, 4096), (5, 77, 768)])
+def test_gemv_dot_several_rows_in_one_launch(fmt, m, n, k):
+    # gemv_dot.comp's M rows (2 .. 8) in one launch, each row in the
+    # single-row order: against the oracle bit for bit, f16 scales, ragged
+    # n and a K that is not whole rounds of 512
+    v, s, quant, words, scales = weights(fmt, n, k, m + n)
+    a, aw, asc = activation(k, 9, m)
+    out = H.empty(m * n * 4)
+    H.call("vkml_gemv_dot", H.GemvDotParams(m, n, k, fmt, H.F16), p(dev(aw)), p(v), p(out), p(s), p(dev(asc)))
+    got = out.download(np.float32, (m, n))
+    assert np.array_equal(bits(got), bits(O.gemv_dot(quant, aw, asc, m, words, scales, n, k)))
+    # and each row as the single-row launch gives it
+    one = H.empty(n * 4)
+    for i in (0, m - 1):
+        aw1 = np.ascontiguousarray(aw.reshape(-1)[i * k // 4:(i + 1) * k // 4])
+        as1 = np.ascontiguousarray(asc.reshape(-1)[i * k // 32:(i + 1) * k // 32])
+        H.call("vkml_gemv_dot", H.GemvDotParams(1, n, k, fmt, H.F16), p(dev(aw1)), p(v), p(one), p(s), p(dev(as1)))
+        assert np.array_equal(bits(one.download(np.float32, n)), bits(got[i]))
+
+
 @pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_0, H.Q4_1])
 def test_gemv_dot_f32_scales_and_several_rows(fmt):
     n, k, m = 300, 512, 3

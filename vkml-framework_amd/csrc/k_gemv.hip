@@ -98,6 +98,75 @@ int check_dot_params(const vkml_gemv_dot_params* p, const char* what) {
     return VKML_OK;
 }
 
+// ---------------------------------------------------------------- several rows
+
+// gemv_dot for 2 .. 8 activation rows in one launch (gemv_dot.comp handles
+// its M rows in one dispatch): each round of a weight row is loaded once and
+// applied to every activation row, each row with its own accumulators in
+// the single-row kernel's order (the same lanes, terms and halving tree).
+// LPR lanes an output row (32 for q8_0 and q4_K, 16 for q4_0 and q4_1);
+// the activation codes are read from memory (the workgroup's rows share
+// them in L1), the next round's weights in flight during this one.
+template <int FMT, bool F16S, int LPR, bool FULL>
+__global__ void __launch_bounds__(256) k_gemv_dot_rows(GemvArgs g, uint32_t m) {
+    constexpr int NS = Plan<FMT, LPR>::NS;
+    constexpr uint32_t kRows = 256 / LPR;
+    const uint32_t t = thread_index(), l = t % LPR, grp = t / LPR;
+    const uint32_t out_row = blockIdx.x * kRows + grp, row = min(out_row, g.n - 1);
+    const uint32_t K = g.k, halves = K / 16, rounds = (halves + 31) / 32;
+    const Q4kField jf = q4k_field((l % 16) / 2);
+    float acc[8][NS];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int e = 0; e < NS; ++e) acc[i][e] = 0.0f;
+    RoundW<FMT, LPR> w;
+    load_round<FMT, F16S, LPR>(g.b_values, g.b_scales, K, row, 0, l, w);
+    for (uint32_t r = 0; r < rounds; ++r) {
+        RoundW<FMT, LPR> next;
+        load_round<FMT, F16S, LPR>(g.b_values, g.b_scales, K, row, min(r + 1, rounds - 1), l, next);
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            if (i >= m) break;
+            RoundA<FMT, LPR> x;
+#pragma unroll
+            for (int e = 0; e < NS; ++e) {
+                const uint32_t hb = min(32 * r + acc_index<FMT, LPR>(l, e), halves - 1);
+                x.a[e] = ldg(g.a_values + static_cast<uint64_t>(i) * halves + hb);
+                x.ss[e] = make_float2(static_cast<float>(byte_sum(x.a[e])), ldg(g.a_scales + static_cast<uint64_t>(i) * (K / 32) + hb / 2));
+            }
+            round_terms<FMT, F16S, LPR, FULL>(w, x, r, l, K, jf, acc[i]);
+        }
+        w = next;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        if (i >= m) break;
+        const float v = row_tree<FMT, LPR>(acc[i]);
+        if (l == 0 && out_row < g.n) g.out[static_cast<uint64_t>(i) * g.n + out_row] = v;
+    }
+}
+
+template <int FMT, bool F16S>
+int launch_rows(const GemvArgs& g, uint32_t m) {
+    constexpr int LPR = FMT == VKML_Q8_0 || FMT == VKML_Q4_K ? 32 : 16;
+    const dim3 grid((g.n + 256 / LPR - 1) / (256 / LPR));
+    vkml::abi::ProfileScope prof("gemv_dot");
+    if (g.k % 512 == 0) hipLaunchKernelGGL((k_gemv_dot_rows<FMT, F16S, LPR, true>), grid, dim3(256), 0, vkml::abi::stream(), g, m);
+    else hipLaunchKernelGGL((k_gemv_dot_rows<FMT, F16S, LPR, false>), grid, dim3(256), 0, vkml::abi::stream(), g, m);
+    return vkml::abi::check_launch("gemv_dot");
+}
+
+int dispatch_rows(uint32_t fmt, uint32_t st, const GemvArgs& g, uint32_t m) {
+    const bool f16 = st == VKML_F16;
+    switch (fmt) {
+        case VKML_Q8_0: return f16 ? launch_rows<VKML_Q8_0, true>(g, m) : launch_rows<VKML_Q8_0, false>(g, m);
+        case VKML_Q4_0: return f16 ? launch_rows<VKML_Q4_0, true>(g, m) : launch_rows<VKML_Q4_0, false>(g, m);
+        case VKML_Q4_1: return f16 ? launch_rows<VKML_Q4_1, true>(g, m) : launch_rows<VKML_Q4_1, false>(g, m);
+        default: return launch_rows<VKML_Q4_K, true>(g, m);
+    }
+}
+
 // ---------------------------------------------------------------- float path
 
 // gemv.comp's order: 32 lanes per output, lane l taking the 4-element
@@ -160,13 +229,12 @@ int vkml_gemv_dot(const vkml_gemv_dot_params* p, const void* a_values, const voi
     VKML_CHECK_ARG(p->m >= 1 && p->m <= 8, "gemv_dot: m must be 1 to 8, got " + std::to_string(p->m));
     if (p->n == 0) return VKML_OK;
     VKML_CHECK_ARG(a_values && b_values && out && b_scales && a_scales, "gemv_dot: null buffer");
-    for (uint32_t r = 0; r < p->m; ++r) {
-        GemvArgs g{reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a_values) + static_cast<uint64_t>(r) * p->k),
-                   a_scales + static_cast<uint64_t>(r) * (p->k / 32), b_values, b_scales, nullptr, nullptr,
-                   out + static_cast<uint64_t>(r) * p->n, nullptr, p->n, p->k};
-        if (int e = dispatch_format<kStore>(p->b_type, p->scale_type, g, "gemv_dot")) return e;
+    if (p->m > 1) {
+        const GemvArgs g{static_cast<const uint4*>(a_values), a_scales, b_values, b_scales, nullptr, nullptr, out, nullptr, p->n, p->k};
+        return dispatch_rows(p->b_type, p->scale_type, g, p->m);
     }
-    return VKML_OK;
+    const GemvArgs g{static_cast<const uint4*>(a_values), a_scales, b_values, b_scales, nullptr, nullptr, out, nullptr, p->n, p->k};
+    return dispatch_format<kStore>(p->b_type, p->scale_type, g, "gemv_dot");
 }
 
 int vkml_gemv_dot_add(const vkml_gemv_dot_params* p, const void* a_values, const void* b_values, float* out,

@@ -285,6 +285,8 @@ def test_vkml_bench_app_results_are_exact():
     is 0.25 x K exactly."""
     import subprocess
     exe = os.path.join(os.path.dirname(__file__), "..", "vkml-framework_amd", "bin", "vkml-bench")
+    if not os.path.exists(exe):
+        pytest.skip("bin/vkml-bench is not built (__graft_entry__.build() builds it)")
     r = subprocess.run([exe, "3"], capture_output=True, text=True, timeout=240)
     assert r.returncode == 0, r.stderr
     lines = [ln for ln in r.stdout.splitlines()[1:] if ln.strip()]

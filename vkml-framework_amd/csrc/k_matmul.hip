@@ -14,20 +14,22 @@
 // 16 x 16 tile of outputs exactly, so the matrix cores do the dot products
 // and the VALU applies the scales per block, in the reference's order.
 //
-// Mapping. A workgroup (four waves) computes a 64 x 128 tile of c, each wave
-// all 64 rows and 32 of the columns (4 x 2 matrix instructions a block).
+// Mapping. A workgroup of four waves computes a tile of c, each wave 16 RT
+// rows by 16 CT columns (RT x CT matrix instructions a block; 64 x 32 for
+// large products, smaller tiles for short prompts so every SIMD gets work).
 // Lane l of a wave holds, for a 16 x 16 instruction, a's row l % 16 and b's
 // column l % 16 at the block's values 8 (l / 16) .. 8 (l / 16) + 7 (one
 // 8-byte operand each), and gets the results for rows 4 (l / 16) .. + 3 of
-// column l % 16. The operands are loaded straight from memory (L2 serves the
-// reuse across workgroups). K runs in chunks of 8 blocks: for each chunk the
-// workgroup first stages every row's (scale, code sum) and every column's
-// (scale, offset) per block in LDS, double-buffered, one barrier a chunk;
-// the scaling then reads four rows' values as one 16-byte word. The kernel
-// is bound by those f32 scalings on the VALU (4 operations per output and
-// block, 6 with offsets): at about 120 VGPRs four waves share a SIMD, which
-// measured faster than prefetching operands and statistics a block ahead
-// at two waves.
+// column l % 16. K runs in chunks of 8 blocks; for each chunk the
+// workgroup stages every row's (scale, code sum) and every column's (scale,
+// offset) per block in LDS, and the scaling reads four rows' values as one
+// 16-byte word. The large-product kernel also stages the chunk's operands
+// in LDS, copied with 16-byte loads a chunk ahead in registers (2x the
+// kernel that loads each block's 8-byte operands from memory, whose waves
+// spent twice their issue time waiting for them); the small tiles load
+// operands straight from memory (L2 serves the reuse across workgroups).
+// The scaling costs 4 VALU operations per output and block, 6 with
+// offsets; the matrix instructions are idle most of the time.
 #include <algorithm>
 
 #include "../../include/vkml_hip.h"
@@ -241,22 +243,233 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
         }
 }
 
+// The 64 x 128 tile with its operands staged in LDS: per 8-block chunk the
+// workgroup copies the chunk's A rows (64 x 256 bytes) and B columns (128 x
+// 128 bytes, 256 for q8_0) with 16-byte loads, a chunk ahead in registers,
+// and the matrix instructions read their operands from LDS. Each thread's
+// A bytes are two blocks of one row, so it also sums their codes.
+template <int FMT, bool F16S>
+struct StagedChunk {
+    static constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
+    static constexpr uint32_t kBBytes = FMT == VKML_Q8_0 ? 256 : 128;  // a column's bytes a chunk
+    static constexpr uint32_t kAStride = 272, kBStride = kBBytes + 16;  // padded rows: no bank conflicts
+    static constexpr uint32_t kBLoads = kBBytes * 128 / 16 / kT;        // 16-byte B loads a thread
+    uint4 a[4];
+    uint4 b[kBLoads];
+    float sa[2];
+    uint4 header;
+    float s[4], o[4];
+};
+
+template <int FMT, bool F16S>
+struct StagedLds {
+    static constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
+    alignas(16) uint8_t a[64 * StagedChunk<FMT, F16S>::kAStride];
+    alignas(16) uint8_t b[128 * StagedChunk<FMT, F16S>::kBStride];
+    alignas(16) float sa[kChunk][64];
+    alignas(16) float asum[kChunk][kOffset ? 64 : 4];
+    float sb[kChunk][128];
+    float ob[kChunk][kOffset ? 128 : 1];
+};
+
+template <int FMT, bool F16S>
+__device__ __forceinline__ void staged_load(const MatmulDotArgs& p, uint32_t t, uint32_t c0, uint32_t row0, uint32_t col0,
+                                            StagedChunk<FMT, F16S>& r) {
+    using S = StagedChunk<FMT, F16S>;
+    const uint32_t blocks = p.k / 32;
+    {
+        // A: row t / 4, blocks 2 (t % 4) and 2 (t % 4) + 1 of the chunk
+        const uint32_t row = min(row0 + t / 4, p.m - 1);
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h) {
+            const uint32_t b = 2 * (t % 4) + h, blk = min(c0 + b, blocks - 1);
+            const uint4* src = reinterpret_cast<const uint4*>(p.a + static_cast<uint64_t>(row) * p.k + blk * 32);
+            r.a[2 * h] = ldg(src);
+            r.a[2 * h + 1] = ldg(src + 1);
+            r.sa[h] = ldg(p.a_scales + static_cast<uint64_t>(row) * blocks + blk);
+        }
+    }
+    // B: 16-byte pieces of the columns' chunk bytes, consecutive threads along a column
+#pragma unroll
+    for (uint32_t u = 0; u < S::kBLoads; ++u) {
+        const uint32_t e = t + kT * u, cl = e / (S::kBBytes / 16), piece = e % (S::kBBytes / 16);
+        const uint32_t col = min(col0 + cl, p.n - 1);
+        const uint8_t* src;
+        if constexpr (FMT == VKML_Q8_0) {
+            const uint32_t blk = min(c0 + piece / 2, blocks - 1);
+            src = p.b + static_cast<uint64_t>(col) * p.k + blk * 32 + 16 * (piece % 2);
+        } else if constexpr (FMT == VKML_Q4_K) {
+            src = p.b + static_cast<uint64_t>(col) * (p.k / 2) + (c0 / 8) * 128 + 16 * piece;
+        } else {
+            const uint32_t blk = min(c0 + piece, blocks - 1);
+            src = p.b + static_cast<uint64_t>(col) * (p.k / 2) + blk * 16;
+        }
+        r.b[u] = ldg(reinterpret_cast<const uint4*>(src));
+    }
+    {
+        const uint32_t col = min(col0 + t / 2, p.n - 1), b0 = 4 * (t % 2);
+        if constexpr (FMT == VKML_Q4_K) {
+            r.header = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.b_scales) +
+                                                          (static_cast<uint64_t>(col) * (p.k / 256) + c0 / 8) * 16));
+        } else {
+#pragma unroll
+            for (uint32_t b = 0; b < 4; ++b) b_block_scale<FMT, F16S>(p, col, min(c0 + b0 + b, blocks - 1), r.s[b], r.o[b]);
+        }
+    }
+}
+
+template <int FMT, bool F16S>
+__device__ __forceinline__ void staged_store(const StagedChunk<FMT, F16S>& r, uint32_t t, StagedLds<FMT, F16S>& l) {
+    using S = StagedChunk<FMT, F16S>;
+    constexpr bool kOffset = S::kOffset;
+    {
+        const uint32_t row = t / 4;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4*>(l.a + row * S::kAStride + (t % 4) * 64 + 16 * i) = r.a[i];
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h) {
+            const uint32_t b = 2 * (t % 4) + h;
+            l.sa[b][row] = r.sa[h];
+            if constexpr (kOffset) l.asum[b][row] = static_cast<float>(byte_sum(r.a[2 * h]) + byte_sum(r.a[2 * h + 1]));
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < S::kBLoads; ++u) {
+        const uint32_t e = t + kT * u, cl = e / (S::kBBytes / 16), piece = e % (S::kBBytes / 16);
+        *reinterpret_cast<uint4*>(l.b + cl * S::kBStride + 16 * piece) = r.b[u];
+    }
+    const uint32_t cl = t / 2, b0 = 4 * (t % 2);
+#pragma unroll
+    for (uint32_t b = 0; b < 4; ++b) {
+        float sv = r.s[b], ov = r.o[b];
+        if constexpr (FMT == VKML_Q4_K) q4k_block_scale(r.header, b0 + b, sv, ov);
+        l.sb[b0 + b][cl] = sv;
+        if constexpr (kOffset) l.ob[b0 + b][cl] = ov;
+    }
+}
+
+// Column cl's operand for block b of the staged chunk (as b_codes).
+template <int FMT, bool F16S>
+__device__ __forceinline__ long staged_b(const StagedLds<FMT, F16S>& l, uint32_t cl, uint32_t b, uint32_t g) {
+    using S = StagedChunk<FMT, F16S>;
+    const uint8_t* col = l.b + cl * S::kBStride;
+    uint32_t lo, hi;
+    if constexpr (FMT == VKML_Q8_0) {
+        const uint2 w = *reinterpret_cast<const uint2*>(col + b * 32 + 8 * g);
+        lo = w.x;
+        hi = w.y;
+    } else if constexpr (FMT == VKML_Q4_K) {
+        const uint2 w = *reinterpret_cast<const uint2*>(col + 32 * (b / 2) + 8 * g);
+        const uint32_t sh = 4 * (b % 2);
+        lo = (w.x >> sh) & 0x0F0F0F0Fu;
+        hi = (w.y >> sh) & 0x0F0F0F0Fu;
+    } else {
+        const uint32_t q = *reinterpret_cast<const uint32_t*>(col + b * 16 + 4 * g);
+        if constexpr (FMT == VKML_Q4_0) {
+            lo = q4_signed(q, 0);
+            hi = q4_signed(q, 4);
+        } else {
+            lo = q & 0x0F0F0F0Fu;
+            hi = (q >> 4) & 0x0F0F0F0Fu;
+        }
+    }
+    return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <int FMT, bool F16S>
+__global__ void __launch_bounds__(kT) k_matmul_dot_staged(MatmulDotArgs p) {
+#pragma clang fp contract(off)
+    using S = StagedChunk<FMT, F16S>;
+    constexpr bool kOffset = S::kOffset;
+    __shared__ StagedLds<FMT, F16S> l;
+    const uint32_t t = thread_index(), lane = t % kWave, wave = t / kWave;
+    const uint32_t g = lane / 16, li = lane % 16;
+    const uint32_t row0 = blockIdx.y * 64, col0 = blockIdx.x * 128;
+    const uint32_t blocks = p.k / 32;
+    float acc[4][2][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[r][c][i] = 0.0f;
+    StagedChunk<FMT, F16S> next;
+    staged_load<FMT, F16S>(p, t, 0, row0, col0, next);
+    for (uint32_t c0 = 0; c0 < blocks; c0 += kChunk) {
+        __syncthreads();  // the last chunk's readers are done
+        staged_store<FMT, F16S>(next, t, l);
+        __syncthreads();
+        if (c0 + kChunk < blocks) staged_load<FMT, F16S>(p, t, c0 + kChunk, row0, col0, next);  // in flight meanwhile
+#pragma unroll
+        for (uint32_t b = 0; b < kChunk; ++b) {
+            if (c0 + b >= blocks) break;
+            long av[4], bv[2];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) av[r] = *reinterpret_cast<const long*>(l.a + (16 * r + li) * S::kAStride + b * 32 + 8 * g);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) bv[c] = staged_b<FMT, F16S>(l, 32 * wave + 16 * c + li, b, g);
+            float sb[2], ob[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                sb[c] = l.sb[b][32 * wave + 16 * c + li];
+                ob[c] = 0.0f;
+                if constexpr (kOffset) ob[c] = l.ob[b][32 * wave + 16 * c + li];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float4 sa4 = *reinterpret_cast<const float4*>(&l.sa[b][16 * r + 4 * g]);
+                float4 as4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if constexpr (kOffset) as4 = *reinterpret_cast<const float4*>(&l.asum[b][16 * r + 4 * g]);
+                const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, asum[4] = {as4.x, as4.y, as4.z, as4.w};
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if constexpr (kOffset) {
+                            acc[r][c][i] += sa[i] * (static_cast<float>(d[i]) * sb[c] + asum[i] * ob[c]);
+                        } else {
+                            acc[r][c][i] += static_cast<float>(d[i]) * (sa[i] * sb[c]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint32_t col = col0 + 32 * wave + 16 * c + li;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t row = row0 + 16 * r + 4 * g + i;
+                if (row < p.m && col < p.n) p.out[static_cast<uint64_t>(row) * p.n + col] = acc[r][c][i];
+            }
+        }
+}
+
 template <int FMT, bool F16S, int RT, int CT>
 void launch_tiles(const MatmulDotArgs& p) {
     const dim3 grid((p.n + 64 * CT - 1) / (64 * CT), (p.m + 16 * RT - 1) / (16 * RT));
     hipLaunchKernelGGL((k_matmul_dot<FMT, F16S, RT, CT>), grid, dim3(kT), 0, vkml::abi::stream(), p);
 }
 
-// The largest per-wave tile (the most reuse of each loaded operand and
-// statistic) that still gives the SIMDs about two waves each; short prompts
-// take the smaller tiles. (Measured: at 128 rows x 14336 columns the 32 x 32
-// tile beats 64 x 32 with half the waves and 32 x 16 with twice as many.)
+// The 64 x 128 tile with its operands staged in LDS (2x the direct-load
+// kernel at large prompts) wherever it gives the SIMDs half a wave each;
+// below that, the largest direct-load tile that still gives them about two
+// waves each. (Measured: the staged tile wins from 512 of its waves on; at
+// 128 rows x 14336 columns the 32 x 32 tile beats 64 x 32 with half the
+// waves and 32 x 16 with twice as many.)
 template <int FMT, bool F16S>
 void launch(const MatmulDotArgs& p) {
     const auto waves = [&](uint64_t rt, uint64_t ct) { return ((p.m + 16 * rt - 1) / (16 * rt)) * ((p.n + 16 * ct - 1) / (16 * ct)); };
     constexpr uint64_t kEnough = 1792;  // 256 CUs x 4 SIMDs x 1.75
-    if (waves(4, 2) >= kEnough) launch_tiles<FMT, F16S, 4, 2>(p);
-    else if (waves(2, 2) >= kEnough) launch_tiles<FMT, F16S, 2, 2>(p);
+    if (waves(4, 2) >= 512) {
+        const dim3 grid((p.n + 127) / 128, (p.m + 63) / 64);
+        hipLaunchKernelGGL((k_matmul_dot_staged<FMT, F16S>), grid, dim3(kT), 0, vkml::abi::stream(), p);
+    } else if (waves(2, 2) >= kEnough) launch_tiles<FMT, F16S, 2, 2>(p);
     else if (waves(2, 1) >= kEnough) launch_tiles<FMT, F16S, 2, 1>(p);
     else launch_tiles<FMT, F16S, 1, 1>(p);
 }

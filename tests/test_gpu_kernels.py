@@ -194,13 +194,14 @@ def test_gemv_dot_f32_scales_and_several_rows(fmt):
 
 @pytest.mark.parametrize("fmt,f16", [(H.Q8_0, True), (H.Q8_0, False), (H.Q4_0, True), (H.Q4_1, True), (H.Q4_1, False), (H.Q4_K, True)])
 @pytest.mark.parametrize("m,n,k", [(9, 64, 256), (37, 100, 512), (130, 1000, 2048), (512, 4096, 4096), (64, 16384, 256),
-                                   (250, 16400, 256)])
+                                   (250, 16400, 256), (100, 4100, 256)])
 def test_matmul_dot_bit_exact(fmt, f16, m, n, k):
     # matmul_dot.comp's order (the reference's int8 product for m > 8) on the
     # matrix cores, against the oracle bit for bit, and within the f32 dot
     # bound of the exact product; ragged tiles at m = 9, 37, 130, 250 and
-    # n = 100, 1000, 16400. The shapes take every per-wave tile: 16 x 16
-    # (the first three), 32 x 32 (512 rows), 32 x 16 (64 rows) and 64 x 32.
+    # n = 100, 1000, 16400, 4100. The shapes take every kernel: operands
+    # from memory at 16 x 16 a wave (the first three), operands staged in
+    # LDS at 64 x 32 (512, 64 and 250 rows) and 32 x 32 (100 rows).
     v, s, quant, words, scales = weights(fmt, n, k, m + n, f16_scales=f16)
     a, aw, asc = activation(k, m, m)
     out = H.empty(m * n * 4)

@@ -248,41 +248,44 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
 // 128 bytes, 256 for q8_0) with 16-byte loads, a chunk ahead in registers,
 // and the matrix instructions read their operands from LDS. Each thread's
 // A bytes are two blocks of one row, so it also sums their codes.
-template <int FMT, bool F16S>
+template <int FMT, bool F16S, int RT>
 struct StagedChunk {
     static constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
+    static constexpr uint32_t TM = 16 * RT;      // rows of the tile
+    static constexpr uint32_t kABlocks = RT / 2;  // a thread's A blocks (of one row)
     static constexpr uint32_t kBBytes = FMT == VKML_Q8_0 ? 256 : 128;  // a column's bytes a chunk
     static constexpr uint32_t kAStride = 272, kBStride = kBBytes + 16;  // padded rows: no bank conflicts
     static constexpr uint32_t kBLoads = kBBytes * 128 / 16 / kT;        // 16-byte B loads a thread
-    uint4 a[4];
+    uint4 a[2 * kABlocks];
     uint4 b[kBLoads];
-    float sa[2];
+    float sa[kABlocks];
     uint4 header;
     float s[4], o[4];
 };
 
-template <int FMT, bool F16S>
+template <int FMT, bool F16S, int RT>
 struct StagedLds {
     static constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
-    alignas(16) uint8_t a[64 * StagedChunk<FMT, F16S>::kAStride];
-    alignas(16) uint8_t b[128 * StagedChunk<FMT, F16S>::kBStride];
-    alignas(16) float sa[kChunk][64];
-    alignas(16) float asum[kChunk][kOffset ? 64 : 4];
+    alignas(16) uint8_t a[16 * RT * StagedChunk<FMT, F16S, RT>::kAStride];
+    alignas(16) uint8_t b[128 * StagedChunk<FMT, F16S, RT>::kBStride];
+    alignas(16) float sa[kChunk][16 * RT];
+    alignas(16) float asum[kChunk][kOffset ? 16 * RT : 4];
     float sb[kChunk][128];
     float ob[kChunk][kOffset ? 128 : 1];
 };
 
-template <int FMT, bool F16S>
+template <int FMT, bool F16S, int RT>
 __device__ __forceinline__ void staged_load(const MatmulDotArgs& p, uint32_t t, uint32_t c0, uint32_t row0, uint32_t col0,
-                                            StagedChunk<FMT, F16S>& r) {
-    using S = StagedChunk<FMT, F16S>;
+                                            StagedChunk<FMT, F16S, RT>& r) {
+    using S = StagedChunk<FMT, F16S, RT>;
+    constexpr uint32_t AB = S::kABlocks, kPerRow = kChunk / AB;  // threads a row
     const uint32_t blocks = p.k / 32;
     {
-        // A: row t / 4, blocks 2 (t % 4) and 2 (t % 4) + 1 of the chunk
-        const uint32_t row = min(row0 + t / 4, p.m - 1);
+        // A: row t / kPerRow, blocks AB (t % kPerRow) .. of the chunk
+        const uint32_t row = min(row0 + t / kPerRow, p.m - 1);
 #pragma unroll
-        for (uint32_t h = 0; h < 2; ++h) {
-            const uint32_t b = 2 * (t % 4) + h, blk = min(c0 + b, blocks - 1);
+        for (uint32_t h = 0; h < AB; ++h) {
+            const uint32_t b = AB * (t % kPerRow) + h, blk = min(c0 + b, blocks - 1);
             const uint4* src = reinterpret_cast<const uint4*>(p.a + static_cast<uint64_t>(row) * p.k + blk * 32);
             r.a[2 * h] = ldg(src);
             r.a[2 * h + 1] = ldg(src + 1);
@@ -318,18 +321,19 @@ __device__ __forceinline__ void staged_load(const MatmulDotArgs& p, uint32_t t, 
     }
 }
 
-template <int FMT, bool F16S>
-__device__ __forceinline__ void staged_store(const StagedChunk<FMT, F16S>& r, uint32_t t, StagedLds<FMT, F16S>& l) {
-    using S = StagedChunk<FMT, F16S>;
+template <int FMT, bool F16S, int RT>
+__device__ __forceinline__ void staged_store(const StagedChunk<FMT, F16S, RT>& r, uint32_t t, StagedLds<FMT, F16S, RT>& l) {
+    using S = StagedChunk<FMT, F16S, RT>;
     constexpr bool kOffset = S::kOffset;
+    constexpr uint32_t AB = S::kABlocks, kPerRow = kChunk / AB;
     {
-        const uint32_t row = t / 4;
+        const uint32_t row = t / kPerRow;
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i)
-            *reinterpret_cast<uint4*>(l.a + row * S::kAStride + (t % 4) * 64 + 16 * i) = r.a[i];
+        for (uint32_t i = 0; i < 2 * AB; ++i)
+            *reinterpret_cast<uint4*>(l.a + row * S::kAStride + (t % kPerRow) * 32 * AB + 16 * i) = r.a[i];
 #pragma unroll
-        for (uint32_t h = 0; h < 2; ++h) {
-            const uint32_t b = 2 * (t % 4) + h;
+        for (uint32_t h = 0; h < AB; ++h) {
+            const uint32_t b = AB * (t % kPerRow) + h;
             l.sa[b][row] = r.sa[h];
             if constexpr (kOffset) l.asum[b][row] = static_cast<float>(byte_sum(r.a[2 * h]) + byte_sum(r.a[2 * h + 1]));
         }
@@ -350,9 +354,9 @@ __device__ __forceinline__ void staged_store(const StagedChunk<FMT, F16S>& r, ui
 }
 
 // Column cl's operand for block b of the staged chunk (as b_codes).
-template <int FMT, bool F16S>
-__device__ __forceinline__ long staged_b(const StagedLds<FMT, F16S>& l, uint32_t cl, uint32_t b, uint32_t g) {
-    using S = StagedChunk<FMT, F16S>;
+template <int FMT, bool F16S, int RT>
+__device__ __forceinline__ long staged_b(const StagedLds<FMT, F16S, RT>& l, uint32_t cl, uint32_t b, uint32_t g) {
+    using S = StagedChunk<FMT, F16S, RT>;
     const uint8_t* col = l.b + cl * S::kBStride;
     uint32_t lo, hi;
     if constexpr (FMT == VKML_Q8_0) {
@@ -377,38 +381,38 @@ __device__ __forceinline__ long staged_b(const StagedLds<FMT, F16S>& l, uint32_t
     return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-template <int FMT, bool F16S>
+template <int FMT, bool F16S, int RT>
 __global__ void __launch_bounds__(kT) k_matmul_dot_staged(MatmulDotArgs p) {
 #pragma clang fp contract(off)
-    using S = StagedChunk<FMT, F16S>;
+    using S = StagedChunk<FMT, F16S, RT>;
     constexpr bool kOffset = S::kOffset;
-    __shared__ StagedLds<FMT, F16S> l;
+    __shared__ StagedLds<FMT, F16S, RT> l;
     const uint32_t t = thread_index(), lane = t % kWave, wave = t / kWave;
     const uint32_t g = lane / 16, li = lane % 16;
-    const uint32_t row0 = blockIdx.y * 64, col0 = blockIdx.x * 128;
+    const uint32_t row0 = blockIdx.y * S::TM, col0 = blockIdx.x * 128;
     const uint32_t blocks = p.k / 32;
-    float acc[4][2][4];
+    float acc[RT][2][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[r][c][i] = 0.0f;
-    StagedChunk<FMT, F16S> next;
-    staged_load<FMT, F16S>(p, t, 0, row0, col0, next);
+    StagedChunk<FMT, F16S, RT> next;
+    staged_load<FMT, F16S, RT>(p, t, 0, row0, col0, next);
     for (uint32_t c0 = 0; c0 < blocks; c0 += kChunk) {
         __syncthreads();  // the last chunk's readers are done
-        staged_store<FMT, F16S>(next, t, l);
+        staged_store<FMT, F16S, RT>(next, t, l);
         __syncthreads();
-        if (c0 + kChunk < blocks) staged_load<FMT, F16S>(p, t, c0 + kChunk, row0, col0, next);  // in flight meanwhile
+        if (c0 + kChunk < blocks) staged_load<FMT, F16S, RT>(p, t, c0 + kChunk, row0, col0, next);  // in flight meanwhile
 #pragma unroll
         for (uint32_t b = 0; b < kChunk; ++b) {
             if (c0 + b >= blocks) break;
-            long av[4], bv[2];
+            long av[RT], bv[2];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) av[r] = *reinterpret_cast<const long*>(l.a + (16 * r + li) * S::kAStride + b * 32 + 8 * g);
+            for (int r = 0; r < RT; ++r) av[r] = *reinterpret_cast<const long*>(l.a + (16 * r + li) * S::kAStride + b * 32 + 8 * g);
 #pragma unroll
-            for (int c = 0; c < 2; ++c) bv[c] = staged_b<FMT, F16S>(l, 32 * wave + 16 * c + li, b, g);
+            for (int c = 0; c < 2; ++c) bv[c] = staged_b<FMT, F16S, RT>(l, 32 * wave + 16 * c + li, b, g);
             float sb[2], ob[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
@@ -417,7 +421,7 @@ __global__ void __launch_bounds__(kT) k_matmul_dot_staged(MatmulDotArgs p) {
                 if constexpr (kOffset) ob[c] = l.ob[b][32 * wave + 16 * c + li];
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int r = 0; r < RT; ++r) {
                 const float4 sa4 = *reinterpret_cast<const float4*>(&l.sa[b][16 * r + 4 * g]);
                 float4 as4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if constexpr (kOffset) as4 = *reinterpret_cast<const float4*>(&l.asum[b][16 * r + 4 * g]);
@@ -438,7 +442,7 @@ __global__ void __launch_bounds__(kT) k_matmul_dot_staged(MatmulDotArgs p) {
         }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const uint32_t col = col0 + 32 * wave + 16 * c + li;
@@ -468,7 +472,10 @@ void launch(const MatmulDotArgs& p) {
     constexpr uint64_t kEnough = 1792;  // 256 CUs x 4 SIMDs x 1.75
     if (waves(4, 2) >= 512) {
         const dim3 grid((p.n + 127) / 128, (p.m + 63) / 64);
-        hipLaunchKernelGGL((k_matmul_dot_staged<FMT, F16S>), grid, dim3(kT), 0, vkml::abi::stream(), p);
+        hipLaunchKernelGGL((k_matmul_dot_staged<FMT, F16S, 4>), grid, dim3(kT), 0, vkml::abi::stream(), p);
+    } else if (waves(2, 2) >= 512) {
+        const dim3 grid((p.n + 127) / 128, (p.m + 31) / 32);
+        hipLaunchKernelGGL((k_matmul_dot_staged<FMT, F16S, 2>), grid, dim3(kT), 0, vkml::abi::stream(), p);
     } else if (waves(2, 2) >= kEnough) launch_tiles<FMT, F16S, 2, 2>(p);
     else if (waves(2, 1) >= kEnough) launch_tiles<FMT, F16S, 2, 1>(p);
     else launch_tiles<FMT, F16S, 1, 1>(p);

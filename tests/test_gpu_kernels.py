@@ -616,6 +616,36 @@ def test_softmax_and_matmul():
     assert np.allclose(out.download(np.float32, want.shape), want, atol=1e-5)
 
 
+@pytest.mark.parametrize("window,softcap", [(0, 0.0), (300, 0.0), (0, 20.0), (300, 20.0)])
+def test_softmax_register_rows_match_long_rows(window, softcap):
+    """Rows of up to 1024, 2048 and 4096 columns take the kernel that holds a
+    row in registers; longer rows take the one that rereads it. Causal rows
+    that see at most 964 keys must come out bit-identical from all four."""
+    rng = np.random.default_rng(61)
+    rows, q_len, offset = 192, 64, 900
+    x = (rng.standard_normal((rows, 5000)) * 3).astype(np.float32)
+    results = []
+    for cols in (1024, 2048, 4096, 5000):
+        xc = np.ascontiguousarray(x[:, :cols])
+        out = H.empty(xc.nbytes)
+        H.call("vkml_softmax", H.SoftmaxParams(rows, cols, 0.7, 1, q_len, offset, window, softcap), p(dev(xc)), p(out))
+        got = out.download(np.float32, xc.shape)
+        assert not got[:, 964:].any()
+        results.append(got[:, :964])
+    for got in results[:-1]:
+        assert np.array_equal(bits(got), bits(results[-1]))
+    for r in (0, 63, 100):
+        vis = r % q_len + offset + 1
+        lo = vis - window if window and vis > window else 0
+        sc = x[r, lo:vis].astype(np.float64) * 0.7
+        if softcap:
+            sc = softcap * np.tanh(np.clip(sc / softcap, -10, 10))
+        e = np.exp(sc - sc.max())
+        want = np.zeros(964)
+        want[lo:vis] = e / e.sum()
+        assert np.allclose(results[0][r], want, atol=1e-6)
+
+
 def _float_b(bt, n, k, rng):
     """(device values, device scales, oracle type, oracle values, oracle scales) of a float or quantized [n, k]."""
     if bt in (H.F32, H.F16, H.BF16):

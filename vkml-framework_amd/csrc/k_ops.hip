@@ -264,6 +264,61 @@ __global__ void __launch_bounds__(kRowThreads) k_softmax(vkml_softmax_params p, 
     }
 }
 
+// k_softmax for rows of at most 256 * NV columns, in the same order with
+// the same operations: a thread's scores (columns first + t, + 256, ...)
+// are loaded once, all at once, into registers, and each exp is evaluated
+// once and kept for the output, instead of reading the row three times and
+// evaluating each exp twice.
+template <uint32_t NV>
+__global__ void __launch_bounds__(kRowThreads) k_softmax_held(vkml_softmax_params p, const float* x, float* out) {
+    __shared__ float scratch[kRowThreads + 1];
+    __shared__ float s_max[16];
+    for (uint32_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
+        const float* xr = x + static_cast<uint64_t>(row) * p.cols;
+        float* orow = out + static_cast<uint64_t>(row) * p.cols;
+        uint32_t visible = p.cols, first = 0;
+        if (p.causal) {
+            visible = min(p.cols, row % p.q_len + p.offset + 1);
+            if (p.window != 0 && visible > p.window) first = visible - p.window;
+        }
+        float v[NV];
+#pragma unroll
+        for (uint32_t i = 0; i < NV; ++i) {
+            const uint32_t c = first + threadIdx.x + kRowThreads * i;
+            v[i] = c < visible ? xr[c] : 0.0f;
+        }
+        float m = -__builtin_inff();
+#pragma unroll
+        for (uint32_t i = 0; i < NV; ++i) {
+            if (first + threadIdx.x + kRowThreads * i < visible) {
+                float s = p.scale * v[i];
+                if (p.softcap > 0.0f) s = p.softcap * tanhf(fminf(fmaxf(s / p.softcap, -10.0f), 10.0f));
+                v[i] = s;
+                m = fmaxf(m, s);
+            }
+        }
+        m = block_max(m, s_max);
+        float s = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < NV; ++i) {
+            if (first + threadIdx.x + kRowThreads * i < visible) {
+                v[i] = vk_expf(v[i] - m);
+                s += v[i];
+            }
+        }
+        s = tree256_sum(s, scratch);
+        const float inv = 1.0f / s;
+#pragma unroll
+        for (uint32_t i = 0; i < NV; ++i) {
+            const uint32_t c = first + threadIdx.x + kRowThreads * i;
+            if (c < visible) orow[c] = v[i] * inv;
+        }
+        for (uint32_t c = threadIdx.x; c < first; c += kRowThreads) orow[c] = 0.0f;
+        for (uint32_t c = visible + threadIdx.x; c < p.cols; c += kRowThreads) orow[c] = 0.0f;
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------- argmax
 
 // (value, column) of the winner of two candidates: larger, or equal and
@@ -676,7 +731,11 @@ int vkml_softmax(const vkml_softmax_params* p, const float* x, float* out) {
     if (p->rows == 0 || p->cols == 0) return VKML_OK;
     VKML_CHECK_ARG(x && out, "softmax: null buffer");
     ProfileScope prof("softmax");
-    hipLaunchKernelGGL(k_softmax, dim3(std::min<uint32_t>(p->rows, 65535)), dim3(kRowThreads), 0, S(), *p, x, out);
+    const dim3 grid(std::min<uint32_t>(p->rows, 65535)), block(kRowThreads);
+    if (p->cols <= kRowThreads * 4) hipLaunchKernelGGL(k_softmax_held<4>, grid, block, 0, S(), *p, x, out);
+    else if (p->cols <= kRowThreads * 8) hipLaunchKernelGGL(k_softmax_held<8>, grid, block, 0, S(), *p, x, out);
+    else if (p->cols <= kRowThreads * 16) hipLaunchKernelGGL(k_softmax_held<16>, grid, block, 0, S(), *p, x, out);
+    else hipLaunchKernelGGL(k_softmax, grid, block, 0, S(), *p, x, out);
     return vkml::abi::check_launch("softmax");
 }
 

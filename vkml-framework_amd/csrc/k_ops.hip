@@ -593,7 +593,22 @@ __global__ void k_embedding(vkml_embedding_params p, const void* values, const v
 // k-major so a thread reads its 4 rows and 4 columns as one 16-byte word
 // each. b is f32/f16/bf16, or (transposed, one batch) a quantized matrix
 // widened as gemv's weights are.
-template <bool BT, uint32_t BTYPE>
+// Four consecutive elements of a float b (f32, or f16/bf16 bits) at element e
+// (a multiple of 4, the row's base aligned), widened to f32.
+template <uint32_t BTYPE>
+__device__ __forceinline__ float4 load_b4(const void* b, uint64_t e) {
+    if constexpr (BTYPE == VKML_F32) {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(b) + e);
+    } else {
+        const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(b) + e);
+        return make_float4(half_to_float(w.x & 0xFFFFu, BTYPE), half_to_float(w.x >> 16, BTYPE), half_to_float(w.y & 0xFFFFu, BTYPE),
+                           half_to_float(w.y >> 16, BTYPE));
+    }
+}
+
+// VEC (float b, rows of a and of b whole vec4s, aligned): each thread loads
+// a's and b's tile elements as one vec4 each instead of four scalars.
+template <bool BT, uint32_t BTYPE, bool VEC = false>
 __global__ void __launch_bounds__(256) k_matmul(vkml_matmul_params p, const float* a, const void* b, const void* bs, float* c) {
     // Rows of 68: stores that run along k hit 16 different banks.
     __shared__ __align__(16) float ta[16][68], tb[16][68];
@@ -621,6 +636,31 @@ __global__ void __launch_bounds__(256) k_matmul(vkml_matmul_params p, const floa
         for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
     for (uint32_t k0 = 0; k0 < k_end; k0 += 16) {
         // Out-of-range elements are zeros, which add nothing.
+        if constexpr (VEC) {
+            {  // a: row tid / 4, k0 + 4 (tid % 4) ..
+                const uint32_t r = tid / 4, kq = tid % 4, row = row0 + r, k = k0 + 4 * kq;
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (row < p.m && k < p.k) v = *reinterpret_cast<const float4*>(az + static_cast<uint64_t>(row) * p.k + k);
+                ta[4 * kq][r] = v.x;
+                ta[4 * kq + 1][r] = v.y;
+                ta[4 * kq + 2][r] = v.z;
+                ta[4 * kq + 3][r] = v.w;
+            }
+            if constexpr (BT) {  // b [n, k]: column tid / 4, k0 + 4 (tid % 4) ..
+                const uint32_t col = tid / 4, kq = tid % 4, n = col0 + col, kg = k0 + 4 * kq;
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (n < p.n && kg < p.k) v = load_b4<BTYPE>(b, b_off + static_cast<uint64_t>(n) * p.k + kg);
+                tb[4 * kq][col] = v.x;
+                tb[4 * kq + 1][col] = v.y;
+                tb[4 * kq + 2][col] = v.z;
+                tb[4 * kq + 3][col] = v.w;
+            } else {  // b [k, n]: k0 + tid / 16, columns 4 (tid % 16) ..
+                const uint32_t kb = tid / 16, cq = tid % 16, n = col0 + 4 * cq, kg = k0 + kb;
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (n < p.n && kg < p.k) v = load_b4<BTYPE>(b, b_off + static_cast<uint64_t>(kg) * p.n + n);
+                *reinterpret_cast<float4*>(&tb[kb][4 * cq]) = v;
+            }
+        } else {
 #pragma unroll
         for (uint32_t u = 0; u < 4; ++u) {
             const uint32_t e = tid + 256 * u;
@@ -636,6 +676,7 @@ __global__ void __launch_bounds__(256) k_matmul(vkml_matmul_params p, const floa
             }
             const uint32_t n = col0 + col, kg = k0 + kb;
             tb[kb][col] = (n < p.n && kg < p.k) ? b_at(n, kg) : 0.0f;
+        }
         }
         __syncthreads();
 #pragma unroll
@@ -924,6 +965,17 @@ int vkml_matmul(const vkml_matmul_params* p, const float* a, const void* b, floa
     const dim3 grid((p->n + 63) / 64, (p->m + 63) / 64, p->batches);
     ProfileScope prof("matmul");
     const bool t = p->b_transposed != 0;
+    // Whole, aligned vec4s along k in a's rows (and b's when transposed),
+    // along n in b's rows otherwise.
+    const bool vec = p->b_type <= VKML_BF16 && p->k % 4 == 0 && (t || p->n % 4 == 0) && p->b_stride % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % (p->b_type == VKML_F32 ? 16 : 8) == 0;
+    if (vec) {
+        const auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, S(), *p, a, b, b_scales, c); };
+        if (p->b_type == VKML_F32) t ? launch(k_matmul<true, VKML_F32, true>) : launch(k_matmul<false, VKML_F32, true>);
+        else if (p->b_type == VKML_F16) t ? launch(k_matmul<true, VKML_F16, true>) : launch(k_matmul<false, VKML_F16, true>);
+        else t ? launch(k_matmul<true, VKML_BF16, true>) : launch(k_matmul<false, VKML_BF16, true>);
+        return vkml::abi::check_launch("matmul");
+    }
     switch (p->b_type) {
         case VKML_F32:
             if (t) hipLaunchKernelGGL((k_matmul<true, VKML_F32>), grid, dim3(256), 0, S(), *p, a, b, b_scales, c);

@@ -232,8 +232,6 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=3, help="decode tokens the CPU oracle is timed on (0: skip)")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (for quick local checks only)")
-    ap.add_argument("--persistent", action="store_true",
-                    help="run the decode step's layers as one persistent launch (LlamaOptions::persistent_layers; off by default)")
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch every kernel from the host instead of replaying the captured step (for profilers "
                          "that cannot follow graph launches; the kernels are the same)")
@@ -267,7 +265,7 @@ def main():
     log(f"model written in {time.time() - t0:.1f} s ({os.path.getsize(path) / 1e9:.2f} GB)")
     try:
         t0 = time.time()
-        model = L.Llama(path, context, kv_f16=True, use_graphs=not args.no_graphs, persistent_layers=args.persistent)
+        model = L.Llama(path, context, kv_f16=True, use_graphs=not args.no_graphs)
         log(f"loaded in {time.time() - t0:.1f} s; kv cache {model.kv_cache_bytes / 1e6:.0f} MB")
         prompt = np.random.default_rng(6).integers(0, spec.vocab, args.prompt).astype(np.int32)
         t0 = time.time()

@@ -457,7 +457,6 @@ int vkml_attend_step_o(const vkml_attend_step_params* p, const float* d_qkv, con
  * earlier vkml_attend_step_o on this sync buffer that timed out. */
 int vkml_attend_o_check(uint32_t* d_sync);
 
-
 /* ---------------------------------------------------------------------- */
 /* Fused decode-step kernels (no single reference counterpart: each       */
 /* replaces a sequence of the reference's dispatches, cited).             */
@@ -498,72 +497,6 @@ int vkml_embedding_state(const vkml_embedding_params* p, const void* d_values,
 int vkml_step_finish(uint32_t vocab, const float* d_logits, vkml_decode_state* d_state,
                      int32_t* d_token_log, uint32_t log_capacity);
 
-/* Every layer of one decode step in one persistent launch: the layer loop of
- * llama.cpp:310-395 for the token in d_state, in the step's order. Per
- * layer: the q|k|v GEMV with the attention RMSNorm + Q8_0 folded in
- * (vkml_gemv_fused), attention over 128-key chunks with RoPE of q and the
- * new key and the KV append, each head's merge + Q8_0 (vkml_attend_step),
- * the o GEMV + residual (vkml_gemv_dot_add), the gate|up GEMV with the ffn
- * RMSNorm + Q8_0, SwiGLU and Q8_0 of h (vkml_gemv_fused), and the down GEMV
- * + residual. The arithmetic, and so every bit of x, the caches and the
- * intermediate buffers, is that of those separate launches; a grid barrier
- * separates the phases, each workgroup issuing its first weight loads of
- * the next phase before it waits.
- *
- * Weights q4_K (f16 headers) with the q, k and v matrices stacked into one
- * [(heads + 2 kv_heads) head_dim, hidden]; f16 KV caches; head_dim 128, an
- * multiple of 4 query heads per KV head; hidden a multiple of 256 up to
- * 4096; ffn a multiple of 256. d_layers: a device array of `layers` entries.
- * d_sync: vkml_decode_sync_bytes(p) bytes of device memory, zeroed once
- * before first use; its first word is a sticky error flag that
- * vkml_decode_layers_check reads and clears. */
-typedef struct vkml_decode_layer {
-    const float* attn_norm;
-    const float* ffn_norm;
-    const void* qkv_values;
-    const void* qkv_scales;
-    const void* o_values;
-    const void* o_scales;
-    const void* gate_values;
-    const void* gate_scales;
-    const void* up_values;
-    const void* up_scales;
-    const void* down_values;
-    const void* down_scales;
-    void* k_cache;
-    void* v_cache;
-} vkml_decode_layer;
-typedef struct vkml_decode_layers_params {
-    uint32_t layers;
-    uint32_t hidden;
-    uint32_t heads;
-    uint32_t kv_heads;
-    uint32_t head_dim;
-    uint32_t ffn;
-    uint32_t weight_type; /* VKML_Q4_K */
-    uint32_t kv_type;     /* VKML_F16 */
-    uint32_t capacity;    /* cache rows per KV head */
-    uint32_t chunks;      /* partial / stats stride: ceil(capacity / 128) */
-    uint32_t rope_style;  /* 0 interleaved pairs, 1 rotate-half */
-    uint32_t rotate;      /* 0: no rope */
-    float eps;
-    float scale;
-} vkml_decode_layers_params;
-typedef struct vkml_decode_buffers {
-    float* x;             /* [hidden] the residual stream: the step's input, then its output */
-    float* partial;       /* [heads, chunks, head_dim] */
-    float* stats;         /* [heads, chunks, 2] */
-    void* work;           /* vkml_decode_work_bytes(p): every layer's intermediate values */
-    const float* rope_table; /* cos/sin pairs [capacity, head_dim / 2, 2] */
-    uint32_t* sync;       /* vkml_decode_sync_bytes(p) */
-} vkml_decode_buffers;
-uint64_t vkml_decode_sync_bytes(const vkml_decode_layers_params* p);
-uint64_t vkml_decode_work_bytes(const vkml_decode_layers_params* p);
-int vkml_decode_layers(const vkml_decode_layers_params* p, const vkml_decode_layer* d_layers,
-                       const vkml_decode_buffers* b, const vkml_decode_state* d_state);
-/* Synchronizes, then reports (VKML_ERROR_DEVICE) and clears a grid barrier
- * that timed out in an earlier vkml_decode_layers on this sync buffer. */
-int vkml_decode_layers_check(uint32_t* d_sync);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,6 @@ typedef struct vkml_llama_options {
     int32_t quantize;           /* -1 none; 0 q8_0, 1 q4_0, 2 q4_1: float weights on load */
     int32_t integer_dot;        /* 1: int8 activations for quantized weights (default) */
     int32_t use_graphs;         /* 1: replay the decode step as a HIP graph (default) */
-    int32_t persistent_layers;  /* 1: a step's layers in one persistent launch where the model allows (default 0) */
     const char* device_name;    /* NULL or "": VKML_DEVICE, then device 0 */
     int64_t prompt_score_bytes; /* scores one piece of a prompt's attention may hold (default 1 GiB); no effect on results */
 } vkml_llama_options;
@@ -53,6 +52,10 @@ int vkml_llama_load(const char* gguf_path, int64_t context_length, const vkml_ll
 void vkml_llama_free(vkml_llama* model);
 /* Destroys the process's device context; fails while models are alive. */
 int vkml_llama_shutdown(void);
+
+/* LlamaConfig::from_gguf (llama.hpp:115, config.cpp:14-140 there): a GGUF
+ * file's model config, read from its header alone (no device needed). */
+int vkml_llama_read_config(const char* gguf_path, vkml_llama_config* out);
 
 /* Llama::config, context_length, position, kv_cache_bytes (llama.hpp:155-180). */
 int vkml_llama_get_config(const vkml_llama* model, vkml_llama_config* out);

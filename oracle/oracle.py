@@ -81,8 +81,10 @@ def _declare(L):
         "orc_model_rewind": (i64, [vp, i64]),
         "orc_model_reset": (None, [vp]),
         "orc_model_vocab": (i64, [vp]),
+        "orc_model_dims": (None, [vp, vp]),
         "orc_model_k_cache": (vp, [vp, i32]),
         "orc_model_v_cache": (vp, [vp, i32]),
+        "orc_model_set_kv": (i32, [vp, i32, vp, vp]),
         "orc_model_reference_f64": (i32, [C.c_char_p, vp, i64, vp]),
     }
     for name, (res, args) in sig.items():
@@ -300,6 +302,10 @@ class Model:
         if not self._h:
             raise RuntimeError(last_error())
         self.vocab = int(lib().orc_model_vocab(self._h))
+        dims = np.zeros(8, np.int64)
+        lib().orc_model_dims(self._h, _p(dims))
+        (_, self.hidden, self.ffn, self.layers, self.heads, self.kv_heads, self.head_dim, self.context) = (int(x) for x in dims)
+        self.kv_f16 = bool(kv_f16)
 
     def forward(self, tokens) -> np.ndarray:
         t = np.ascontiguousarray(tokens, dtype=np.int32)
@@ -334,6 +340,25 @@ class Model:
 
     def reset(self) -> None:
         lib().orc_model_reset(self._h)
+
+    def kv_cache(self, layer: int):
+        """Layer `layer`'s caches [kv_heads, context, head_dim] as the model
+        holds them (f16 bits as uint16, or f32), copied."""
+        k = lib().orc_model_k_cache(self._h, layer)
+        v = lib().orc_model_v_cache(self._h, layer)
+        n = self.kv_heads * self.context * self.head_dim
+        t = C.c_uint16 if self.kv_f16 else C.c_float
+        shape = (self.kv_heads, self.context, self.head_dim)
+        return tuple(np.ctypeslib.as_array(C.cast(p, C.POINTER(t)), (n,)).reshape(shape).copy() for p in (k, v))
+
+    def set_kv(self, layer: int, k, v) -> None:
+        """Layer `layer`'s caches from k and v (the kv_cache layout)."""
+        dt = np.uint16 if self.kv_f16 else np.float32
+        shape = (self.kv_heads, self.context, self.head_dim)
+        k, v = np.ascontiguousarray(k, dt), np.ascontiguousarray(v, dt)
+        assert k.shape == shape and v.shape == shape, (k.shape, shape)
+        if lib().orc_model_set_kv(self._h, layer, _p(k), _p(v)) != 0:
+            raise RuntimeError("set_kv: layer %d" % layer)
 
     def close(self) -> None:
         if self._h:

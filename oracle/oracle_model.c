@@ -318,6 +318,10 @@ int orc_model_set_position(orc_model* m, int64_t position) {
     return 0;
 }
 int64_t orc_model_vocab(const orc_model* m) { return m->vocab; }
+void orc_model_dims(const orc_model* m, int64_t out[8]) {
+    const int64_t d[8] = {m->vocab, m->d, m->ff, m->n_layers, m->heads, m->kv_heads, m->hd, m->context};
+    memcpy(out, d, sizeof d);
+}
 void orc_model_reset(orc_model* m) { m->position = 0; }
 int64_t orc_model_rewind(orc_model* m, int64_t position) {
     if (position < 0 || position > m->position) {
@@ -329,6 +333,13 @@ int64_t orc_model_rewind(orc_model* m, int64_t position) {
     return position;
 }
 const void* orc_model_k_cache(const orc_model* m, int l) { return m->layers[l].k_cache; }
+int orc_model_set_kv(orc_model* m, int l, const void* k, const void* v) {
+    if (l < 0 || l >= m->n_layers || !k || !v) return -1;
+    const size_t bytes = (size_t)(m->kv_heads * m->context * m->hd) * (m->kv_f16 ? 2 : 4);
+    memcpy(m->layers[l].k_cache, k, bytes);
+    memcpy(m->layers[l].v_cache, v, bytes);
+    return 0;
+}
 const void* orc_model_v_cache(const orc_model* m, int l) { return m->layers[l].v_cache; }
 
 /* SharedInput::times_transposed (matmul.cpp:207-272): x [t, K] times w^T. The

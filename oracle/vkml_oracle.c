@@ -24,12 +24,18 @@ int orc_get_threads(void) { return g_threads; }
  * results do not depend on the thread count. */
 typedef void (*range_fn)(void* ctx, int64_t begin, int64_t end);
 typedef struct { range_fn fn; void* ctx; int64_t begin, end; } range_job;
+/* Set on the threads of a parallel_for while they run its ranges: a
+ * parallel_for inside one runs serially there. */
+static __thread int t_in_parallel;
+
 static void* range_thread(void* p) {
     range_job* j = (range_job*)p;
+    t_in_parallel = 1;
     j->fn(j->ctx, j->begin, j->end);
     return NULL;
 }
 static void parallel_for(int64_t n, range_fn fn, void* ctx) {
+    if (t_in_parallel) { fn(ctx, 0, n); return; }
     int threads = g_threads;
     if (threads > n) threads = (int)(n > 0 ? n : 1);
     if (threads <= 1) { fn(ctx, 0, n); return; }
@@ -47,7 +53,9 @@ static void parallel_for(int64_t n, range_fn fn, void* ctx) {
         }
         started = t;
     }
+    t_in_parallel = 1;
     fn(ctx, 0, per < n ? per : n);
+    t_in_parallel = 0;
     for (int t = 1; t <= started; ++t) if (jobs[t].fn) pthread_join(tid[t], NULL);
 }
 
@@ -597,47 +605,83 @@ void orc_gemv_dot(int quant, int f16, const uint32_t* a_words, const float* a_sc
 }
 
 /* matmul_dot.comp:75-170: per output, one 32-value block per step, the
- * block's exact integer sum scaled in f32 and added in block order. */
+ * block's exact integer sum scaled in f32 and added in block order. The
+ * integer sums are formed from codes unpacked to bytes once per column (and
+ * the scales widened once per column), CT columns at a time so that each row
+ * of a is read once per tile; an exact integer sum does not depend on how it
+ * is formed, and the f32 steps per output are matmul_dot.comp's, in its
+ * order. */
+enum { MM_CT = 16 };
+
+static int32_t dot32_i8(const int8_t* a, const int8_t* b) {
+    int32_t s = 0;
+    for (int k = 0; k < 32; ++k) s += (int32_t)a[k] * (int32_t)b[k];
+    return s;
+}
+
 static void matmul_dot_range(void* p, int64_t c0, int64_t c1) {
     const prod_ctx* c = (const prod_ctx*)p;
     const int quant = c->quant, f16 = c->f16;
-    const uint32_t* a_words = c->a_words; const float* a_scales = c->a_scales;
+    const int8_t* a = (const int8_t*)c->a_words; const float* a_scales = c->a_scales;
     const uint32_t* b_words = (const uint32_t*)c->b; const void* b_scales = c->sc;
     const int64_t M = c->M, N = c->N, K = c->K;
     float* out = c->out;
-    const int64_t blocks = K / 32, a_row_words = K / 4;
-    const int q4 = quant != ORC_Q8_0;
+    const int64_t blocks = K / 32;
+    const int q4 = quant != ORC_Q8_0, offs = quant == ORC_Q4_1;
     const int64_t b_row_words = q4 ? K / 8 : K / 4;
-    for (int64_t row = 0; row < M; ++row) {
-        for (int64_t col = c0; col < c1; ++col) {
-            float acc = 0.0f;
+    int8_t* bq = (int8_t*)malloc((size_t)(MM_CT * K));
+    float* bs = (float*)malloc((size_t)(MM_CT * blocks) * 4);
+    float* bo = (float*)malloc((size_t)(MM_CT * blocks) * 4);
+    int32_t* asum = offs ? (int32_t*)malloc((size_t)(M * blocks) * 4) : NULL;
+    if (offs) {
+        for (int64_t r = 0; r < M; ++r)
             for (int64_t blk = 0; blk < blocks; ++blk) {
-                int32_t sums = 0, a_sums = 0;
+                int32_t t = 0;
+                for (int k = 0; k < 32; ++k) t += a[r * K + blk * 32 + k];
+                asum[r * blocks + blk] = t;
+            }
+    }
+    for (int64_t t0 = c0; t0 < c1; t0 += MM_CT) {
+        const int64_t nt = c1 - t0 < MM_CT ? c1 - t0 : MM_CT;
+        for (int64_t j = 0; j < nt; ++j) {
+            const int64_t col = t0 + j;
+            int8_t* dst = bq + j * K;
+            for (int64_t blk = 0; blk < blocks; ++blk) {
                 for (int w = 0; w < 8; ++w) {
-                    const uint32_t av = a_words[row * a_row_words + blk * 8 + w];
                     uint32_t bv;
                     if (q4) {
                         const uint32_t q = b_words[col * b_row_words + blk * 4 + w / 2];
-                        if (quant == ORC_Q4_1) bv = (w % 2 == 0) ? (q & 0x0F0F0F0Fu) : ((q >> 4) & 0x0F0F0F0Fu);
-                        else bv = q4_bytes(q, (w % 2) * 4);
+                        if (offs) bv = (w % 2 == 0) ? (q & 0x0F0F0F0Fu) : ((q >> 4) & 0x0F0F0F0Fu);
+                        else bv = q4_bytes(q, (uint32_t)(w % 2) * 4);
                     } else {
                         bv = b_words[col * b_row_words + blk * 8 + w];
                     }
-                    sums += dot4(av, bv);
-                    if (quant == ORC_Q4_1) a_sums += dot4(av, 0x01010101u);
+                    for (int k = 0; k < 4; ++k) dst[blk * 32 + 4 * w + k] = (int8_t)(bv >> (8 * k));
                 }
-                const float sa = a_scales[row * blocks + blk];
                 const int64_t block = col * blocks + blk;
-                if (quant == ORC_Q4_1) {
-                    acc += sa * ((float)sums * scale_at(b_scales, f16, 2 * block) +
-                                 (float)a_sums * scale_at(b_scales, f16, 2 * block + 1));
-                } else {
-                    acc += (float)sums * (sa * scale_at(b_scales, f16, block));
-                }
+                bs[j * blocks + blk] = scale_at(b_scales, f16, offs ? 2 * block : block);
+                bo[j * blocks + blk] = offs ? scale_at(b_scales, f16, 2 * block + 1) : 0.0f;
             }
-            out[row * N + col] = acc;
+        }
+        for (int64_t row = 0; row < M; ++row) {
+            const int8_t* ar = a + row * K;
+            for (int64_t j = 0; j < nt; ++j) {
+                const int8_t* br = bq + j * K;
+                float acc = 0.0f;
+                for (int64_t blk = 0; blk < blocks; ++blk) {
+                    const int32_t sums = dot32_i8(ar + blk * 32, br + blk * 32);
+                    const float sa = a_scales[row * blocks + blk];
+                    if (offs) {
+                        acc += sa * ((float)sums * bs[j * blocks + blk] + (float)asum[row * blocks + blk] * bo[j * blocks + blk]);
+                    } else {
+                        acc += (float)sums * (sa * bs[j * blocks + blk]);
+                    }
+                }
+                out[row * N + t0 + j] = acc;
+            }
         }
     }
+    free(bq); free(bs); free(bo); free(asum);
 }
 
 void orc_matmul_dot(int quant, int f16, const uint32_t* a_words, const float* a_scales, int64_t M,
@@ -972,22 +1016,25 @@ void orc_attend_decode(const float* q, int64_t heads, const void* k, const void*
  * softmax.comp's causal rows (max; sum of exp in the shader's 256-wide
  * order; times 1/sum); then probs v in key order (matmul.comp). */
 static void prefill_block(const float* q, int64_t q_len, int64_t q0, int64_t rows, int64_t h, const void* k,
-                          const void* v, int f16, int64_t capacity, int64_t hd, int64_t keys,
-                          int64_t kv_row0, float* s, float* out) {
+                          const void* v, int f16, int64_t hd, int64_t keys, int64_t kv_row0, float* s,
+                          float* kf, float* vf, float* out) {
     const float scale = 1.0f / sqrtf((float)hd);
     const float* qh = q + (h * q_len + q0) * hd;
+    /* the head's keys and values widened to f32 once (exact) */
+    for (int64_t e = 0; e < keys * hd; ++e) {
+        kf[e] = kv_at(k, f16, kv_row0 * hd + e);
+        vf[e] = kv_at(v, f16, kv_row0 * hd + e);
+    }
     if (rows <= 8) {
-        const void* kh = f16 ? (const void*)((const uint16_t*)k + kv_row0 * hd) : (const void*)((const float*)k + kv_row0 * hd);
-        orc_gemv_float(f16 ? ORC_T_F16 : ORC_T_F32, 0, qh, rows, kh, NULL, keys, hd, s);
+        orc_gemv_float(ORC_T_F32, 0, qh, rows, kf, NULL, keys, hd, s);
     } else {
         for (int64_t i = 0; i < rows; ++i)
             for (int64_t j = 0; j < keys; ++j) {
                 float acc = 0.0f;
-                for (int64_t c = 0; c < hd; ++c) acc += qh[i * hd + c] * kv_at(k, f16, (kv_row0 + j) * hd + c);
+                for (int64_t c = 0; c < hd; ++c) acc += qh[i * hd + c] * kf[j * hd + c];
                 s[i * keys + j] = acc;
             }
     }
-    (void)capacity;
     for (int64_t i = 0; i < rows; ++i) {
         float* si = s + i * keys;
         const int64_t position = i + keys - rows;
@@ -1011,10 +1058,27 @@ static void prefill_block(const float* q, int64_t q_len, int64_t q0, int64_t row
         for (int64_t j = 0; j < keys; ++j) si[j] = j < visible ? orc_expf(si[j] * scale - m) * inv : 0.0f;
         for (int64_t c = 0; c < hd; ++c) {
             float acc = 0.0f;
-            for (int64_t j = 0; j < keys; ++j) acc += si[j] * kv_at(v, f16, (kv_row0 + j) * hd + c);
+            for (int64_t j = 0; j < keys; ++j) acc += si[j] * vf[j * hd + c];
             out[(h * q_len + q0 + i) * hd + c] = acc;
         }
     }
+}
+
+typedef struct {
+    const float* q; int64_t q_len, q0, rows; const void* k; const void* v; int f16;
+    int64_t hd, keys, group, capacity; float* out;
+} prefill_ctx;
+
+/* Heads h0 .. h1 of one query chunk, each with buffers of its own. */
+static void prefill_heads(void* p, int64_t h0, int64_t h1) {
+    const prefill_ctx* c = (const prefill_ctx*)p;
+    float* s = (float*)malloc(sizeof(float) * (size_t)(c->rows * (c->keys > 0 ? c->keys : 1)));
+    float* kf = (float*)malloc(sizeof(float) * (size_t)(c->keys * c->hd + 1));
+    float* vf = (float*)malloc(sizeof(float) * (size_t)(c->keys * c->hd + 1));
+    for (int64_t h = h0; h < h1; ++h)
+        prefill_block(c->q, c->q_len, c->q0, c->rows, h, c->k, c->v, c->f16, c->hd, c->keys, (h / c->group) * c->capacity,
+                      s, kf, vf, c->out);
+    free(s); free(kf); free(vf);
 }
 
 /* detail::attention for q_len > 1 (attention.cpp:205-226): queries in chunks
@@ -1029,13 +1093,11 @@ void orc_attention_prefill(const float* q, int64_t heads, int64_t q_len, const v
     if (chunk < 1) chunk = 1;
     if (chunk >= 64) chunk -= chunk % 64;
     if (q_len <= chunk) chunk = q_len;
-    float* s = (float*)malloc(sizeof(float) * (size_t)(chunk * (kv_len > 0 ? kv_len : 1)));
     const int64_t first_position = kv_len - q_len;
     for (int64_t q0 = 0; q0 < q_len; q0 += chunk) {
         const int64_t rows = chunk < q_len - q0 ? chunk : q_len - q0;
         const int64_t keys = q_len <= chunk ? kv_len : first_position + q0 + rows;
-        for (int64_t h = 0; h < heads; ++h)
-            prefill_block(q, q_len, q0, rows, h, k, v, f16, capacity, hd, keys, (h / group) * capacity, s, out);
+        prefill_ctx c = {q, q_len, q0, rows, k, v, f16, hd, keys, group, capacity, out};
+        parallel_for(heads, prefill_heads, &c);
     }
-    free(s);
 }

@@ -146,9 +146,15 @@ int orc_model_set_position(orc_model* m, int64_t position); /* timing samples on
 int64_t orc_model_rewind(orc_model* m, int64_t position); /* -1 on error */
 void orc_model_reset(orc_model* m);
 int64_t orc_model_vocab(const orc_model* m);
+/* vocab, hidden, ffn, layers, heads, kv_heads, head_dim, context. */
+void orc_model_dims(const orc_model* m, int64_t out[8]);
 /* The layer-0 k cache as the model holds it (f32 or f16 bits), for cache tests. */
 const void* orc_model_k_cache(const orc_model* m, int layer);
 const void* orc_model_v_cache(const orc_model* m, int layer);
+/* Copies layer l's caches [kv_heads, context, hd] in (f16 bits or f32, as the
+ * model holds them), so that a cache computed elsewhere -- the GPU's prefill
+ * of a long prompt -- is continued here with orc_model_set_position. */
+int orc_model_set_kv(orc_model* m, int layer, const void* k, const void* v);
 
 /* Double-precision forward of the dequantized weights from scratch, no
  * activation quantization (tests/test_llama.cpp:585-755): logits of the last

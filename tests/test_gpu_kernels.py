@@ -7,6 +7,7 @@ results are also held to the f32 dot-product error bound against exact sums
 (tests/test_quantize.cpp:197-224 in the reference: 2 k 2^-24 sum|a b|), which
 pins the oracle itself. Only the matmul and softmax of the prefill-shaped ops,
 whose order this build does not follow, are checked within a tolerance."""
+import ctypes as C
 import math
 
 import numpy as np
@@ -617,21 +618,26 @@ def test_softmax_and_matmul():
 
 
 @pytest.mark.parametrize("window,softcap", [(0, 0.0), (300, 0.0), (0, 20.0), (300, 20.0)])
-def test_softmax_register_rows_match_long_rows(window, softcap):
+@pytest.mark.parametrize("offset", [900, 1500, 3500])
+def test_softmax_register_rows_match_long_rows(window, softcap, offset):
     """Rows of up to 1024, 2048 and 4096 columns take the kernel that holds a
-    row in registers; longer rows take the one that rereads it. Causal rows
-    that see at most 964 keys must come out bit-identical from all four."""
+    row in registers (4, 8 or 16 values a thread); longer rows take the one
+    that rereads it. Causal rows that see up to offset + 64 keys (past 1024
+    and 2048 with the larger offsets, so every register slot holds data) must
+    come out bit-identical from every kernel whose width holds them."""
     rng = np.random.default_rng(61)
-    rows, q_len, offset = 192, 64, 900
+    rows, q_len = 192, 64
+    seen = offset + q_len
     x = (rng.standard_normal((rows, 5000)) * 3).astype(np.float32)
     results = []
-    for cols in (1024, 2048, 4096, 5000):
+    for cols in [c for c in (1024, 2048, 4096) if c >= seen] + [5000]:
         xc = np.ascontiguousarray(x[:, :cols])
         out = H.empty(xc.nbytes)
         H.call("vkml_softmax", H.SoftmaxParams(rows, cols, 0.7, 1, q_len, offset, window, softcap), p(dev(xc)), p(out))
         got = out.download(np.float32, xc.shape)
-        assert not got[:, 964:].any()
-        results.append(got[:, :964])
+        assert not got[:, seen:].any()
+        results.append(got[:, :seen])
+    assert len(results) >= 2
     for got in results[:-1]:
         assert np.array_equal(bits(got), bits(results[-1]))
     for r in (0, 63, 100):
@@ -641,7 +647,7 @@ def test_softmax_register_rows_match_long_rows(window, softcap):
         if softcap:
             sc = softcap * np.tanh(np.clip(sc / softcap, -10, 10))
         e = np.exp(sc - sc.max())
-        want = np.zeros(964)
+        want = np.zeros(seen)
         want[lo:vis] = e / e.sum()
         assert np.allclose(results[0][r], want, atol=1e-6)
 
@@ -708,6 +714,34 @@ def test_matmul_attention_shapes_bit_exact(kv_type, rows, keys):
         # b [k, n] in k order equals b^T [n, k] in k order
         want = O.matmul_float(ot, probs[h], np.ascontiguousarray(vb[h // g, :keys].T), None, hd, keys)
         assert np.array_equal(bits(got[h]), bits(want)), h
+
+
+@pytest.mark.parametrize("bt", [H.F32, H.F16])
+def test_matmul_vec4_and_scalar_loads_agree(bt):
+    """The same product with a's rows whole aligned vec4s (the vec4 tile
+    loads) and with a 4 bytes off alignment (scalar loads): bit-identical,
+    and both the oracle's k order, for scores (b transposed) and probs . v."""
+    heads, kvh, hd, rows, keys = 4, 2, 64, 70, 132
+    cap, g = keys + 4, 2
+    rng = np.random.default_rng(bt + 91)
+    dt = np.float16 if bt == H.F16 else np.float32
+    ot = O.T_F16 if bt == H.F16 else O.T_F32
+    kc = rng.standard_normal((kvh, cap, hd)).astype(dt)
+    kb = kc.view(np.uint16) if bt == H.F16 else kc
+    for transposed, m, n, k in ((1, rows, keys, hd), (0, rows, hd, keys)):
+        a = rng.standard_normal((heads, m, k)).astype(np.float32)
+        shifted = dev(np.concatenate([np.zeros(1, np.float32), a.ravel()]))
+        aligned = dev(a)
+        outs = []
+        for ptr in (p(aligned), C.c_void_p(p(shifted).value + 4)):
+            out = H.empty(heads * m * n * 4)
+            H.call("vkml_matmul", H.MatmulParams(m, n, k, cap * hd, g, heads, transposed, bt, H.F16), ptr, p(dev(kb)), p(out), None)
+            outs.append(out.download(np.float32, (heads, m, n)))
+        assert np.array_equal(bits(outs[0]), bits(outs[1]))
+        for h in range(heads):
+            b = kb[h // g, :n] if transposed else kb[h // g, :k].T
+            want = O.matmul_float(ot, a[h], np.ascontiguousarray(b), None, n, k)
+            assert np.array_equal(bits(outs[0][h]), bits(want)), h
 
 
 @pytest.mark.parametrize("rows,first", [(130, 0), (64, 70), (200, 3)])

@@ -224,59 +224,26 @@ def test_no_dot_path_uses_f32_activations(files, prompt):
         same(gpu.forward(np.array([t])), ref.forward(np.array([t])))
 
 
-def _labels_of_one_step(m, token):
-    from vkml_amd import llama as L
-    L.set_profiling(True)
-    L.reset_profile()
-    try:
-        m.forward(np.array([token], np.int32))
-        L.synchronize()
-        return {name for name, _, _ in L.profile()}
-    finally:
-        L.set_profiling(False)
-
-
 @pytest.mark.parametrize("ctx,prompt,steps", [(40, 8, 8), (300, 130, 6), (260, 254, 5)])
-def test_persistent_layers_equal_separate_launches(files, ctx, prompt, steps):
-    """vkml_decode_layers (every layer of a step in one persistent launch)
-    against the separate launches on the cfg5-shaped model: the same logits,
-    greedy tokens and KV-cache rows, bit for bit, with prompts and generations
-    that cross 128-key chunk boundaries (the last case ends at the cache's
-    final row)."""
+def test_decode_steps_across_chunk_boundaries_match_oracle(files, ctx, prompt, steps):
+    """The cfg5-shaped model's decode steps against the oracle, bit for bit,
+    with prompts and generations that cross 128-key chunk boundaries (the
+    last case ends at the cache's final row): logits, greedy tokens and the
+    KV-cache rows."""
     path = files["cfg5"]
     tokens = np.random.default_rng(12).integers(0, 32768, prompt).astype(np.int32)
-    a = Llama(path, ctx, kv_f16=True, persistent_layers=True)
-    b = Llama(path, ctx, kv_f16=True, persistent_layers=False)
-    la, lb = a.forward(tokens), b.forward(tokens)
-    same(la, lb)
-    first = int(np.argmax(la))
-    ga, gb = a.generate_greedy(first, steps - 1), b.generate_greedy(first, steps - 1)
-    assert list(ga) == list(gb)
-    for layer in range(2):
-        ka, va = a.read_kv_cache(layer)
-        kb, vb = b.read_kv_cache(layer)
-        n = prompt + steps - 1
-        assert np.array_equal(ka[:, :n], kb[:, :n]) and np.array_equal(va[:, :n], vb[:, :n])
-    if prompt + steps < ctx:
-        # the paths taken: one persistent launch a step, or the separate kernels
-        assert any(n.startswith("decode_layers") for n in _labels_of_one_step(a, first))
-        assert not any(n.startswith("decode_layers") for n in _labels_of_one_step(b, first))
-
-
-def test_persistent_layers_match_oracle(files):
-    """The persistent launch against the CPU oracle directly: prompt, then
-    greedy tokens, bit for bit."""
-    path = files["cfg5"]
-    tokens = np.random.default_rng(13).integers(0, 32768, 10).astype(np.int32)
-    gpu = Llama(path, 40, kv_f16=True, persistent_layers=True)
-    ref = O.Model(path, 40, kv_f16=True)
+    gpu = Llama(path, ctx, kv_f16=True)
+    ref = O.Model(path, ctx, kv_f16=True)
     got = gpu.forward(tokens)
-    want = ref.forward(tokens)
-    same(got, want)
+    same(got, ref.forward(tokens))
     first = int(np.argmax(got))
-    toks = gpu.generate_greedy(first, 6)
-    want_toks, _ = greedy_oracle(ref, first, 6)
-    assert list(toks) == list(want_toks)
+    toks, _ = greedy_oracle(ref, first, steps - 1)
+    assert list(gpu.generate_greedy(first, steps - 1)) == list(toks)
+    n = prompt + steps - 1
+    for layer in range(2):
+        k, v = gpu.read_kv_cache(layer)
+        kr, vr = ref.kv_cache(layer)
+        assert np.array_equal(k[:, :n], kr[:, :n]) and np.array_equal(v[:, :n], vr[:, :n])
 
 
 def test_vkml_bench_app_results_are_exact():

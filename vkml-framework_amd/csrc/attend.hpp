@@ -1,7 +1,6 @@
 // attend.hpp -- decode attention's device code (the reference's
 // shaders/attend.comp + attend_merge.comp, src/ops/attention.cpp:54-84),
-// shared by the attention kernels (k_attend.hip) and the persistent decode
-// kernel (k_decode.hip).
+// used by the attention kernels (k_attend.hip).
 //
 // Bit-exact by construction: keys are taken in the reference's chunks of 128
 // from kv_start, and every f32 value follows its order: each score sums four

@@ -216,7 +216,8 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
 
 // threadIdx.x through an empty asm: what a function derives from it is
 // computed where that function runs, not hoisted to a kernel's entry and
-// kept live (or spilled) across the phases of a persistent kernel.
+// kept live (or spilled) across the phases of a kernel that does several
+// things in turn (the merge + o launch).
 __device__ __forceinline__ uint32_t thread_index() {
     uint32_t t = threadIdx.x;
     asm volatile("" : "+v"(t));
@@ -250,7 +251,7 @@ __device__ __forceinline__ void stg(T* p, T v) {
 // ---------------------------------------------------------------- coherent access
 
 // Loads and stores of the values one workgroup of a launch produces for
-// another (the persistent decode kernel's activations). Each XCD has its own
+// another (the merge + o launch's attention output). Each XCD has its own
 // L2, which may hold a stale line of a buffer another XCD has since written;
 // agent-scope relaxed atomics (sc1 accesses) are coherent across XCDs. With
 // COH false these are plain accesses.

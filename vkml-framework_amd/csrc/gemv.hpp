@@ -1,6 +1,6 @@
 // gemv.hpp -- the int8 GEMV's device code (the reference's
 // shaders/gemv_dot.comp), shared by the GEMV kernels (k_gemv.hip) and the
-// persistent decode kernel (k_decode.hip).
+// merge + o launch (k_attend.hip).
 //
 // Bit-exact by construction. The reference sums each output over 32
 // accumulators: accumulator L takes the terms of half-blocks (16 values) L,

@@ -71,11 +71,6 @@ struct LlamaOptions {
     std::int64_t sliding_extra_rows = 1024;
     // Replay each decode step as a captured HIP graph.
     bool use_graphs = true;
-    // Run a decode step's layers as one persistent launch (vkml_decode_layers)
-    // when the model's formats and shapes allow it; the results are the same.
-    // Off by default: on the MI355X it is not yet faster than the separate
-    // launches.
-    bool persistent_layers = false;
     // int8 activations for this model's quantized weights, when the Context
     // allows them too (ContextOptions::integer_dot_product).
     bool integer_dot_product = true;

@@ -63,13 +63,6 @@ RopeKvParams = _struct("RopeKvParams", [("heads", u32), ("kv_heads", u32), ("hea
                                         ("position", u32), ("style", u32), ("kv_type", u32), ("rotate", u32)])
 GemvFusedParams = _struct("GemvFusedParams", [("n", u32), ("k", u32), ("b_type", u32), ("scale_type", u32),
                                               ("epilogue", u32), ("norm", u32), ("eps", f32), ("quantize_out", u32)])
-DecodeLayer = _struct("DecodeLayer", [(f, vp) for f in ("attn_norm", "ffn_norm", "qkv_values", "qkv_scales", "o_values",
-                                                        "o_scales", "gate_values", "gate_scales", "up_values", "up_scales",
-                                                        "down_values", "down_scales", "k_cache", "v_cache")])
-DecodeLayersParams = _struct("DecodeLayersParams", [(f, u32) for f in ("layers", "hidden", "heads", "kv_heads", "head_dim", "ffn",
-                                                                      "weight_type", "kv_type", "capacity", "chunks",
-                                                                      "rope_style", "rotate")] + [("eps", f32), ("scale", f32)])
-DecodeBuffers = _struct("DecodeBuffers", [(f, vp) for f in ("x", "partial", "stats", "work", "rope_table", "sync")])
 AttendStepParams = _struct("AttendStepParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
                                                 ("kv_start", u32), ("position", u32), ("kv_type", u32), ("chunks", u32),
                                                 ("rope_style", u32), ("rotate", u32), ("scale", f32), ("softcap", f32)])
@@ -95,10 +88,6 @@ SIGNATURES = {
     "vkml_completed": [P(u64)],
     "vkml_synchronize": [],
     "vkml_stream": [],
-    "vkml_decode_sync_bytes": [vp],
-    "vkml_decode_work_bytes": [vp],
-    "vkml_decode_layers": [vp, vp, vp, vp],
-    "vkml_decode_layers_check": [vp],
     "vkml_set_profiling": [C.c_int],
     "vkml_get_profiling": [],
     "vkml_set_profile_tag": [C.c_char_p],
@@ -161,9 +150,7 @@ def lib() -> C.CDLL:
             fn.argtypes = args
             fn.restype = C.c_int
         _lib.vkml_stream.restype = C.c_void_p
-        _lib.vkml_decode_sync_bytes.restype = C.c_uint64
         _lib.vkml_attend_o_sync_bytes.restype = C.c_uint64
-        _lib.vkml_decode_work_bytes.restype = C.c_uint64
     return _lib
 
 

@@ -16,7 +16,7 @@ i32, i64, u32, u64, vp = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_void_
 
 class Options(C.Structure):
     _fields_ = [("kv_cache_f16", i32), ("quantize", i32), ("integer_dot", i32), ("use_graphs", i32),
-                ("persistent_layers", i32), ("device_name", C.c_char_p), ("prompt_score_bytes", i64)]
+                ("device_name", C.c_char_p), ("prompt_score_bytes", i64)]
 
 
 class Config(C.Structure):
@@ -32,6 +32,7 @@ SIGNATURES = {
     "vkml_llama_free": (None, [vp]),
     "vkml_llama_shutdown": (C.c_int, []),
     "vkml_llama_get_config": (C.c_int, [vp, P(Config)]),
+    "vkml_llama_read_config": (C.c_int, [C.c_char_p, P(Config)]),
     "vkml_llama_context_length": (i64, [vp]),
     "vkml_llama_position": (i64, [vp]),
     "vkml_llama_kv_cache_bytes": (i64, [vp]),
@@ -80,11 +81,11 @@ def _ptr(a: np.ndarray):
 
 class Llama:
     def __init__(self, path: str, context: int, kv_f16: bool = False, quantize: int = -1, integer_dot: bool = True,
-                 use_graphs: bool = True, persistent_layers: bool = False, prompt_score_bytes: int = 0):
+                 use_graphs: bool = True, prompt_score_bytes: int = 0):
         o = Options()
         lib().vkml_llama_default_options(C.byref(o))
         o.kv_cache_f16, o.quantize, o.integer_dot = int(kv_f16), int(quantize), int(integer_dot)
-        o.use_graphs, o.persistent_layers = int(use_graphs), int(persistent_layers)
+        o.use_graphs = int(use_graphs)
         if prompt_score_bytes:
             o.prompt_score_bytes = int(prompt_score_bytes)
         self._h = vp()
@@ -150,6 +151,13 @@ class Llama:
             self.close()
         except Exception:
             pass
+
+
+def read_config(path: str) -> dict:
+    """LlamaConfig::from_gguf: a GGUF file's model config, from its header."""
+    cfg = Config()
+    _check(lib().vkml_llama_read_config(path.encode(), C.byref(cfg)))
+    return {f: getattr(cfg, f) for f, _ in Config._fields_}
 
 
 def set_profiling(on: bool) -> None:

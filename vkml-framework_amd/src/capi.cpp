@@ -37,6 +37,12 @@ vkml::Context& context(const vkml_llama_options& o) {
     return *g_context;
 }
 
+vkml_llama_config c_config(const vkml::LlamaConfig& c) {
+    return vkml_llama_config{c.vocab_size, c.hidden_size, c.intermediate_size, c.num_layers, c.num_heads, c.num_kv_heads, c.head_dim,
+                             c.max_positions, c.rms_norm_eps, c.rope_theta, c.tie_word_embeddings ? 1 : 0,
+                             c.rope_style == vkml::RopeStyle::Interleaved ? 1 : 0};
+}
+
 }  // namespace
 
 extern "C" {
@@ -45,7 +51,7 @@ const char* vkml_llama_last_error(void) { return g_error.c_str(); }
 
 void vkml_llama_default_options(vkml_llama_options* out) {
     if (!out) return;
-    *out = vkml_llama_options{0, -1, 1, 1, 0, nullptr, std::int64_t{1} << 30};
+    *out = vkml_llama_options{0, -1, 1, 1, nullptr, std::int64_t{1} << 30};
 }
 
 int vkml_llama_load(const char* path, int64_t context_length, const vkml_llama_options* options, vkml_llama** out) {
@@ -61,7 +67,6 @@ int vkml_llama_load(const char* path, int64_t context_length, const vkml_llama_o
             lo.quantize = static_cast<vkml::QuantType>(o.quantize);
         }
         lo.use_graphs = o.use_graphs != 0;
-        lo.persistent_layers = o.persistent_layers != 0;
         lo.integer_dot_product = o.integer_dot != 0;
         if (o.prompt_score_bytes <= 0) throw vkml::Error("vkml_llama_load: prompt_score_bytes must be positive");
         lo.prompt_score_bytes = o.prompt_score_bytes;
@@ -84,13 +89,17 @@ int vkml_llama_shutdown(void) {
     });
 }
 
+int vkml_llama_read_config(const char* path, vkml_llama_config* out) {
+    return guarded([&] {
+        if (!path || !out) throw vkml::Error("vkml_llama_read_config: null argument");
+        *out = c_config(vkml::LlamaConfig::from_gguf(path));
+    });
+}
+
 int vkml_llama_get_config(const vkml_llama* m, vkml_llama_config* out) {
     return guarded([&] {
         if (!m || !out) throw vkml::Error("vkml_llama_get_config: null argument");
-        const vkml::LlamaConfig& c = m->model.config();
-        *out = vkml_llama_config{c.vocab_size, c.hidden_size, c.intermediate_size, c.num_layers, c.num_heads, c.num_kv_heads, c.head_dim,
-                                 c.max_positions, c.rms_norm_eps, c.rope_theta, c.tie_word_embeddings ? 1 : 0,
-                                 c.rope_style == vkml::RopeStyle::Interleaved ? 1 : 0};
+        *out = c_config(m->model.config());
     });
 }
 

@@ -1,10 +1,20 @@
 // gguf.cpp -- GGUF reading and host decoding for the loader.
+//
+// The file is mapped read-only and its header parsed in place through a
+// cursor that checks every read against the mapping's end, so a damaged
+// length or count shows up as "truncated" instead of a huge allocation.
+// Tensor data is handed out as views of the mapping (no copy).
 #include "gguf.hpp"
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <array>
+#include <bit>
 #include <cmath>
 #include <cstring>
-#include <fstream>
 
 #include "vkml/error.hpp"
 
@@ -12,65 +22,82 @@ namespace vkml::detail {
 
 namespace {
 
-constexpr std::uint64_t kMaxDimension = std::uint64_t{1} << 40;
-constexpr std::uint64_t kMaxString = std::uint64_t{1} << 30;
-constexpr std::uint64_t kMaxArray = std::uint64_t{1} << 28;
-
-class Reader {
+// A read-only view of the header bytes with a position.
+class Cursor {
 public:
-    Reader(std::ifstream& in, std::string where) : in_(in), where_(std::move(where)) {}
-    template <class T>
-    T get() {
-        T v{};
-        bytes(&v, sizeof v);
+    Cursor(const std::uint8_t* begin, const std::uint8_t* end, const std::string& where) : at_(begin), end_(end), where_(where) {}
+
+    std::uint64_t remaining() const { return static_cast<std::uint64_t>(end_ - at_); }
+    const std::uint8_t* here() const { return at_; }
+
+    // n bytes from here, or an error naming what was being read.
+    const std::uint8_t* take(std::uint64_t n, const char* what) {
+        if (n > remaining()) truncated(std::string("reading ") + what);
+        const std::uint8_t* p = at_;
+        at_ += n;
+        return p;
+    }
+    // A little-endian unsigned integer of `width` bytes.
+    std::uint64_t uint(unsigned width, const char* what) {
+        const std::uint8_t* p = take(width, what);
+        std::uint64_t v = 0;
+        for (unsigned i = 0; i < width; ++i) v |= std::uint64_t(p[i]) << (8 * i);
         return v;
     }
-    std::string str() {
-        const auto size = get<std::uint64_t>();
-        if (size > kMaxString) fail("a string of " + std::to_string(size) + " bytes");
-        std::string s(size, '\0');
-        bytes(s.data(), size);
-        return s;
+    std::uint32_t u32(const char* what) { return static_cast<std::uint32_t>(uint(4, what)); }
+    std::uint64_t u64(const char* what) { return uint(8, what); }
+    // A GGUF string: u64 length, then that many bytes.
+    std::string text(const char* what) {
+        const std::uint64_t n = u64(what);
+        const std::uint8_t* p = take(n, what);
+        return std::string(reinterpret_cast<const char*>(p), static_cast<std::size_t>(n));
     }
-    void bytes(void* out, std::uint64_t n) {
-        if (!in_.read(static_cast<char*>(out), static_cast<std::streamsize>(n))) throw Error(where_ + ": truncated");
-    }
-    std::uint64_t position() { return static_cast<std::uint64_t>(in_.tellg()); }
-    [[noreturn]] void fail(const std::string& what) { throw Error(where_ + ": malformed header: " + what); }
-
-    // Metadata value of type t (0-12: u8 i8 u16 i16 u32 i32 f32 bool string array u64 i64 f64).
-    GgufValue value(std::uint32_t t, int depth = 0) {
-        switch (t) {
-            case 0: return {double(get<std::uint8_t>())};
-            case 1: return {double(get<std::int8_t>())};
-            case 2: return {double(get<std::uint16_t>())};
-            case 3: return {double(get<std::int16_t>())};
-            case 4: return {double(get<std::uint32_t>())};
-            case 5: return {double(get<std::int32_t>())};
-            case 6: return {double(get<float>())};
-            case 7: return {double(get<std::uint8_t>() != 0)};
-            case 8: return {str()};
-            case 9: {
-                if (depth > 4) fail("arrays nested too deep");
-                const auto element = get<std::uint32_t>();
-                const auto count = get<std::uint64_t>();
-                if (count > kMaxArray) fail("an array of " + std::to_string(count) + " values");
-                std::vector<GgufValue> out;
-                out.reserve(static_cast<std::size_t>(std::min<std::uint64_t>(count, 1 << 20)));
-                for (std::uint64_t i = 0; i < count; ++i) out.push_back(value(element, depth + 1));
-                return {std::move(out)};
-            }
-            case 10: return {double(get<std::uint64_t>())};
-            case 11: return {double(get<std::int64_t>())};
-            case 12: return {get<double>()};
-            default: fail("a value of unknown type " + std::to_string(t));
-        }
-    }
+    [[noreturn]] void malformed(const std::string& what) const { throw Error(where_ + ": malformed header: " + what); }
+    [[noreturn]] void truncated(const std::string& what) const { throw Error(where_ + ": truncated (" + what + ")"); }
 
 private:
-    std::ifstream& in_;
-    std::string where_;
+    const std::uint8_t* at_;
+    const std::uint8_t* end_;
+    const std::string& where_;
 };
+
+// GGUF metadata value types 0..12 (gguf.md): for scalars, the width in bytes
+// and how the bits read: u unsigned, i signed, f IEEE float, b bool; 8 is a
+// string and 9 an array.
+struct ValueKind {
+    unsigned width;
+    char kind;
+};
+constexpr std::array<ValueKind, 13> kValueKinds{{{1, 'u'}, {1, 'i'}, {2, 'u'}, {2, 'i'}, {4, 'u'}, {4, 'i'}, {4, 'f'}, {1, 'b'},
+                                                 {0, 's'}, {0, 'a'}, {8, 'u'}, {8, 'i'}, {8, 'f'}}};
+constexpr int kMaxArrayDepth = 8;
+
+GgufValue parse_value(Cursor& c, std::uint32_t type, int depth) {
+    if (type >= kValueKinds.size()) c.malformed("a value of unknown type " + std::to_string(type));
+    const ValueKind k = kValueKinds[type];
+    if (k.kind == 's') return {c.text("a string value")};
+    if (k.kind == 'a') {
+        if (depth >= kMaxArrayDepth) c.malformed("arrays nested more than " + std::to_string(kMaxArrayDepth) + " deep");
+        const std::uint32_t element = c.u32("an array's element type");
+        const std::uint64_t count = c.u64("an array's length");
+        if (count > c.remaining()) c.truncated("an array of " + std::to_string(count) + " values");
+        std::vector<GgufValue> items;
+        items.reserve(static_cast<std::size_t>(count));
+        for (std::uint64_t i = 0; i < count; ++i) items.push_back(parse_value(c, element, depth + 1));
+        return {std::move(items)};
+    }
+    const std::uint64_t raw = c.uint(k.width, "a number");
+    switch (k.kind) {
+        case 'b': return {raw != 0 ? 1.0 : 0.0};
+        case 'i': {
+            const unsigned shift = 64 - 8 * k.width;  // sign-extend from the value's width
+            return {double(static_cast<std::int64_t>(raw << shift) >> shift)};
+        }
+        case 'f':
+            return {k.width == 4 ? double(std::bit_cast<float>(static_cast<std::uint32_t>(raw))) : std::bit_cast<double>(raw)};
+        default: return {double(raw)};
+    }
+}
 
 std::uint16_t rd16(const std::uint8_t* p) {
     std::uint16_t v;
@@ -143,53 +170,38 @@ void block_q6_k(const std::uint8_t* b, float* y) {
     }
 }
 
-// x rounded half to even for |x| < 2^22 by the 1.5 * 2^23 addition
-// (src/io/host_quant.cpp:63-70); volatile keeps the two roundings.
-float round_even(float x) {
-    volatile float t = x + 12582912.0f;
-    return t - 12582912.0f;
-}
-
 }  // namespace
 
+// IEEE binary16 <-> binary32. Widening is exact: normal halves move their
+// exponent and fraction into place, subnormal ones are their fraction times
+// 2^-24 (a float computes that exactly).
 float f16_to_float(std::uint16_t h) {
-    const std::uint32_t sign = std::uint32_t(h & 0x8000u) << 16;
-    const std::uint32_t exponent = (h >> 10) & 0x1Fu, mantissa = h & 0x3FFu;
-    std::uint32_t bits;
-    if (exponent == 0) {
-        float f = float(mantissa) * 5.9604644775390625e-8f;
-        std::memcpy(&bits, &f, 4);
-        bits |= sign;
-    } else if (exponent == 31) {
-        bits = sign | 0x7F800000u | (mantissa << 13);
-    } else {
-        bits = sign | ((exponent + 112u) << 23) | (mantissa << 13);
-    }
-    float f;
-    std::memcpy(&f, &bits, 4);
-    return f;
+    const std::uint32_t sign = std::uint32_t(h >> 15) << 31;
+    const std::uint32_t exponent = (h >> 10) & 0x1Fu, fraction = h & 0x3FFu;
+    if (exponent == 0x1Fu) return std::bit_cast<float>(sign | 0x7F800000u | (fraction << 13));
+    if (exponent != 0) return std::bit_cast<float>(sign | ((exponent + 112u) << 23) | (fraction << 13));
+    return std::bit_cast<float>(sign | std::bit_cast<std::uint32_t>(std::ldexp(float(fraction), -24)));
 }
 
+// Narrowing rounds to nearest, ties to even. Normal results: rebias the
+// exponent and round the 23-bit fraction to 10 by adding just under half an
+// ulp plus the kept ulp's low bit (a carry out of the fraction bumps the
+// exponent, as it should). Subnormal results: the value times 2^24, which a
+// float holds exactly, rounded to an integer in the default rounding mode.
+// 65520 and above go to infinity; NaN stays a quiet NaN.
 std::uint16_t float_to_f16(float f) {
-    std::uint32_t x;
-    std::memcpy(&x, &f, 4);
-    const std::uint32_t sign = (x >> 16) & 0x8000u;
-    const std::uint32_t biased = (x >> 23) & 0xFFu;
-    std::uint32_t mantissa = x & 0x7FFFFFu;
-    if (biased == 0xFFu) return std::uint16_t(sign | 0x7C00u | (mantissa ? 0x200u : 0u));
-    const int exponent = int(biased) - 127 + 15;
-    if (exponent >= 31) return std::uint16_t(sign | 0x7C00u);
-    const auto round = [](std::uint32_t value, int shift) {
-        const std::uint32_t kept = value >> shift, rest = value & ((1u << shift) - 1);
-        const std::uint32_t half = 1u << (shift - 1);
-        return kept + (rest > half || (rest == half && (kept & 1u)) ? 1u : 0u);
-    };
-    if (exponent <= 0) {
-        if (exponent < -10) return std::uint16_t(sign);
-        mantissa |= 0x800000u;
-        return std::uint16_t(sign | round(mantissa, 14 - exponent));
+    const std::uint32_t x = std::bit_cast<std::uint32_t>(f);
+    const auto sign = static_cast<std::uint16_t>((x >> 16) & 0x8000u);
+    const std::uint32_t magnitude = x & 0x7FFFFFFFu;
+    if (magnitude > 0x7F800000u) return sign | 0x7E00u;    // NaN
+    if (magnitude >= 0x477FF000u) return sign | 0x7C00u;   // 65520 and above, infinity
+    if (magnitude < 0x38800000u) {                          // below 2^-14
+        const float scaled = std::bit_cast<float>(magnitude) * 16777216.0f;
+        return sign | static_cast<std::uint16_t>(std::nearbyint(scaled));
     }
-    return std::uint16_t(sign | round((std::uint32_t(exponent) << 23) | mantissa, 13));
+    std::uint32_t r = magnitude - (112u << 23);
+    r += 0xFFFu + ((r >> 13) & 1u);
+    return sign | static_cast<std::uint16_t>(r >> 13);
 }
 
 const char* ggml_type_name(std::uint32_t t) {
@@ -233,65 +245,94 @@ std::pair<std::uint64_t, std::uint64_t> ggml_block(std::uint32_t t) {
     }
 }
 
-Gguf::Gguf(const std::filesystem::path& path) : path_(path) {
+// The file's bytes, mapped read-only for the life of the Gguf.
+struct Gguf::Mapping {
+    const std::uint8_t* data = nullptr;
+    std::uint64_t size = 0;
+    ~Mapping() {
+        if (data) munmap(const_cast<std::uint8_t*>(data), static_cast<std::size_t>(size));
+    }
+};
+
+Gguf::Gguf(const std::filesystem::path& path) : path_(path), map_(std::make_shared<Mapping>()) {
     const std::string where = "gguf: " + path.string();
-    std::ifstream in(path, std::ios::binary);
-    if (!in) throw Error(where + ": cannot open file");
-    std::error_code ec;
-    const std::uint64_t file_size = std::filesystem::file_size(path, ec);
-    if (ec) throw Error(where + ": cannot read file size");
-    Reader r{in, where};
-    std::array<char, 4> magic{};
-    if (file_size < 4 || !in.read(magic.data(), 4) || std::string(magic.data(), 4) != "GGUF") throw Error(where + ": not a GGUF file");
-    version_ = r.get<std::uint32_t>();
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) throw Error(where + ": cannot open file");
+    struct stat st {};
+    if (fstat(fd, &st) != 0) {
+        ::close(fd);
+        throw Error(where + ": cannot read file size");
+    }
+    map_->size = static_cast<std::uint64_t>(st.st_size);
+    if (map_->size > 0) {
+        void* p = mmap(nullptr, static_cast<std::size_t>(map_->size), PROT_READ, MAP_PRIVATE, fd, 0);
+        if (p == MAP_FAILED) {
+            ::close(fd);
+            throw Error(where + ": cannot map file");
+        }
+        map_->data = static_cast<const std::uint8_t*>(p);
+    }
+    ::close(fd);
+    const std::uint8_t* base = map_->data;
+    if (map_->size < 4 || std::memcmp(base, "GGUF", 4) != 0) throw Error(where + ": not a GGUF file");
+    Cursor c(base + 4, base + map_->size, where);
+    version_ = c.u32("the version");
     if (version_ < 2 || version_ > 3) throw Error(where + ": GGUF version " + std::to_string(version_) + " is not supported (2 and 3 are)");
-    const auto tensors = r.get<std::uint64_t>();
-    const auto kvs = r.get<std::uint64_t>();
-    if (tensors > (std::uint64_t{1} << 24) || kvs > (std::uint64_t{1} << 24)) {
-        r.fail("counts of " + std::to_string(tensors) + " tensors and " + std::to_string(kvs) + " metadata entries");
+    const std::uint64_t tensors = c.u64("the tensor count"), entries = c.u64("the metadata count");
+    // every metadata entry and tensor record takes well over 8 bytes
+    if (tensors > c.remaining() / 8 || entries > c.remaining() / 8) {
+        throw Error(where + ": truncated (" + std::to_string(tensors) + " tensors and " + std::to_string(entries) +
+                    " metadata entries do not fit the file)");
     }
-    for (std::uint64_t i = 0; i < kvs; ++i) {
-        std::string key = r.str();
-        const auto type = r.get<std::uint32_t>();
-        metadata_[key] = r.value(type);
+    for (std::uint64_t i = 0; i < entries; ++i) {
+        std::string key = c.text("a metadata key");
+        const std::uint32_t type = c.u32("a metadata type");
+        metadata_.insert_or_assign(std::move(key), parse_value(c, type, 0));
     }
-    std::vector<std::pair<std::string, Entry>> infos;
+    struct Record {
+        std::string name;
+        Entry entry;
+    };
+    std::vector<Record> records;
+    records.reserve(static_cast<std::size_t>(tensors));
     for (std::uint64_t i = 0; i < tensors; ++i) {
-        std::string name = r.str();
-        const auto dims = r.get<std::uint32_t>();
-        if (dims > 4) r.fail("tensor " + name + " has " + std::to_string(dims) + " dimensions");
-        Shape shape(dims);
+        Record r;
+        r.name = c.text("a tensor name");
+        const std::uint32_t dims = c.u32("a tensor's rank");
+        if (dims == 0 || dims > 4) c.malformed("tensor " + r.name + " has " + std::to_string(dims) + " dimensions (1 to 4 are allowed)");
+        r.entry.shape.assign(dims, 0);
+        // GGUF lists the fastest-varying dimension first; Shape is row-major.
         for (std::uint32_t d = 0; d < dims; ++d) {
-            const auto n = r.get<std::uint64_t>();
-            if (n > kMaxDimension) r.fail("tensor " + name + " has a dimension of " + std::to_string(n));
-            shape[dims - 1 - d] = static_cast<std::int64_t>(n);
+            const std::uint64_t n = c.u64("a tensor dimension");
+            if (n > std::uint64_t(INT64_MAX)) c.malformed("tensor " + r.name + " has a dimension of " + std::to_string(n));
+            r.entry.shape[dims - 1 - d] = static_cast<std::int64_t>(n);
         }
-        const auto type = r.get<std::uint32_t>();
-        const auto offset = r.get<std::uint64_t>();
-        infos.emplace_back(std::move(name), Entry{std::move(shape), type, offset, 0});
+        r.entry.type = c.u32("a tensor type");
+        r.entry.offset = c.u64("a tensor offset");
+        records.push_back(std::move(r));
     }
-    const auto align_it = metadata_.find("general.alignment");
-    const std::uint64_t alignment = align_it != metadata_.end() && align_it->second.is_number() ? std::uint64_t(align_it->second.number()) : 32;
-    if (alignment == 0 || alignment > (std::uint64_t{1} << 30)) r.fail("general.alignment is " + std::to_string(alignment));
-    data_start_ = (r.position() + alignment - 1) / alignment * alignment;
-    for (auto& [name, e] : infos) {
-        const auto too_large = [&] { throw Error(where + ": tensor " + name + " is too large"); };
+    std::uint64_t alignment = 32;
+    if (const auto it = metadata_.find("general.alignment"); it != metadata_.end() && it->second.is_number()) {
+        alignment = static_cast<std::uint64_t>(it->second.number());
+        if (alignment == 0 || (alignment & (alignment - 1)) != 0) c.malformed("general.alignment is " + std::to_string(alignment));
+    }
+    const auto header_end = static_cast<std::uint64_t>(c.here() - base);
+    data_start_ = (header_end + alignment - 1) / alignment * alignment;
+    const std::uint64_t data_bytes = data_start_ <= map_->size ? map_->size - data_start_ : 0;
+    for (Record& r : records) {
         std::uint64_t count = 1;
-        for (const std::int64_t d : e.shape) {
-            const auto n = static_cast<std::uint64_t>(d);
-            if (n != 0 && count > UINT64_MAX / n) too_large();
-            count *= n;
+        bool overflow = false;
+        for (const std::int64_t d : r.entry.shape) overflow |= __builtin_mul_overflow(count, static_cast<std::uint64_t>(d), &count);
+        const auto [per_block, block_bytes] = ggml_block(r.entry.type);
+        if (per_block) {
+            const std::uint64_t blocks = count / per_block + (count % per_block ? 1 : 0);
+            overflow |= __builtin_mul_overflow(blocks, block_bytes, &r.entry.bytes);
         }
-        const auto [values, size] = ggml_block(e.type);
-        if (values) {
-            const std::uint64_t blocks = count / values + (count % values != 0);
-            if (blocks > UINT64_MAX / size) too_large();
-            e.bytes = blocks * size;
+        if (overflow) throw Error(where + ": tensor " + r.name + " is too large");
+        if (r.entry.offset > data_bytes || r.entry.bytes > data_bytes - r.entry.offset) {
+            throw Error(where + ": tensor " + r.name + " runs past the end of the file");
         }
-        if (data_start_ > file_size || e.offset > file_size - data_start_ || e.bytes > file_size - data_start_ - e.offset) {
-            throw Error(where + ": tensor " + name + " runs past the end of the file");
-        }
-        entries_.emplace(std::move(name), std::move(e));
+        entries_.insert_or_assign(std::move(r.name), std::move(r.entry));
     }
 }
 
@@ -317,15 +358,9 @@ std::string Gguf::type_name(const std::string& name) const {
     return n ? n : "type " + std::to_string(e.type);
 }
 
-std::vector<std::uint8_t> Gguf::read(const std::string& name) const {
+std::span<const std::uint8_t> Gguf::bytes(const std::string& name) const {
     const Entry& e = entry(name);
-    std::vector<std::uint8_t> out(e.bytes);
-    std::ifstream in(path_, std::ios::binary);
-    in.seekg(static_cast<std::streamoff>(data_start_ + e.offset));
-    if (!in.read(reinterpret_cast<char*>(out.data()), static_cast<std::streamsize>(out.size()))) {
-        throw Error("gguf: reading tensor \"" + name + "\" from " + path_.string() + " failed");
-    }
-    return out;
+    return {map_->data + data_start_ + e.offset, static_cast<std::size_t>(e.bytes)};
 }
 
 void dequantize_blocks(std::uint32_t type, const std::uint8_t* blocks, std::size_t count, float* out) {
@@ -374,7 +409,7 @@ void requantize_q8(std::uint32_t type, const std::uint8_t* data, std::int64_t ro
                 for (int w = 0; w < 8; ++w) {
                     std::uint32_t word = 0;
                     for (int k = 0; k < 4; ++k) {
-                        const float v = std::clamp(round_even(x[4 * w + k] * inv), -127.0f, 127.0f);
+                        const float v = std::clamp(std::nearbyint(x[4 * w + k] * inv), -127.0f, 127.0f);
                         word |= (std::uint32_t(std::int32_t(v)) & 0xFFu) << (8 * k);
                     }
                     words[group * 8 + w] = word;

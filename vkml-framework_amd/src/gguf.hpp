@@ -1,11 +1,15 @@
-// gguf.hpp -- GGUF v2/v3 files (llama.cpp's format), as the reference reads
-// them (src/io/gguf.hpp:22-71), without a JSON dependency: metadata values
-// are kept as numbers, strings, or arrays of them.
+// gguf.hpp -- GGUF v2/v3 files (llama.cpp's format), the reader behind
+// Llama::load and LlamaConfig::from_gguf (the reference's src/io/gguf.hpp:
+// 22-71 is its counterpart). Metadata values are kept as numbers, strings,
+// or arrays of them; tensor data is viewed in place in a read-only mapping
+// of the file.
 #pragma once
 
 #include <cstdint>
 #include <filesystem>
 #include <map>
+#include <memory>
+#include <span>
 #include <string>
 #include <variant>
 #include <vector>
@@ -49,12 +53,15 @@ public:
     const Shape& shape(const std::string& name) const { return entry(name).shape; }
     std::string type_name(const std::string& name) const;
 
-    // The raw bytes of a tensor.
-    std::vector<std::uint8_t> read(const std::string& name) const;
+    // The raw bytes of a tensor, in the file's mapping (valid while this
+    // Gguf, or a copy of it, lives).
+    std::span<const std::uint8_t> bytes(const std::string& name) const;
     const std::filesystem::path& path() const noexcept { return path_; }
 
 private:
+    struct Mapping;
     std::filesystem::path path_;
+    std::shared_ptr<Mapping> map_;
     std::uint32_t version_ = 0;
     std::map<std::string, GgufValue> metadata_;
     std::map<std::string, Entry> entries_;

@@ -11,14 +11,10 @@
 //   merge + Q8_0 -> o GEMV + residual -> gate|up GEMV (rms_norm + Q8_0
 //   prologue, SwiGLU + Q8_0 epilogue) -> down GEMV + residual,
 // then the final norm, the lm_head GEMV and (greedy) an argmax that writes
-// the next token into the state. When the model's formats and shapes allow
-// (q4_K matrices, f16 caches, head_dim 128: vkml_decode_layers), the layers
-// instead run as one persistent launch that walks the same phases between
-// grid barriers, with the same arithmetic. The step is captured once as a HIP graph
-// and replayed, so a prompt or a greedy generation is a stream of graph
-// launches with no host round trip between tokens. Prompts run one token per
-// step through the same graph; the arithmetic per token is the reference's
-// (activations quantized per row, so one row at a time is the same sum).
+// the next token into the state. The step is captured once as a HIP graph
+// and replayed, so a greedy generation is a stream of graph launches with no
+// host round trip between tokens. A prompt of several tokens runs at once,
+// as the reference's Llama::run does (prefill below).
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -78,14 +74,14 @@ HostMatrix host_matrix(const Gguf& file, const std::string& name, std::int64_t r
     if (e.shape != Shape{rows, cols}) {
         throw Error("Llama: weight " + name + " is " + to_string(e.shape) + ", but the config needs " + to_string(Shape{rows, cols}));
     }
-    const std::vector<std::uint8_t> data = file.read(name);
+    const std::span<const std::uint8_t> data = file.bytes(name);
     HostMatrix m;
     m.rows = rows;
     m.cols = cols;
     const std::size_t count = std::size_t(rows * cols);
     if (e.type == detail::kGgmlF32 || e.type == detail::kGgmlF16 || e.type == detail::kGgmlBF16) {
         m.dtype = e.type == detail::kGgmlF32 ? DType::F32 : e.type == detail::kGgmlF16 ? DType::F16 : DType::BF16;
-        m.values = data;
+        m.values.assign(data.begin(), data.end());
         return m;
     }
     m.quantized = true;
@@ -199,7 +195,7 @@ std::vector<float> read_vector(const Gguf& file, const std::string& name, std::i
     if (e.shape != Shape{size}) {
         throw Error("Llama: weight " + name + " is " + to_string(e.shape) + ", but the config needs " + to_string(Shape{size}));
     }
-    const std::vector<std::uint8_t> data = file.read(name);
+    const std::span<const std::uint8_t> data = file.bytes(name);
     std::vector<float> out(static_cast<std::size_t>(size));
     for (std::size_t i = 0; i < out.size(); ++i) {
         if (e.type == detail::kGgmlF32) {
@@ -312,10 +308,6 @@ struct Llama::Impl {
     Tensor o_sync;  // vkml_attend_step_o: the merge + o launch's sync words
     std::int64_t chunks = 1;  // decode attention's 128-key chunks over the whole cache
     std::uint64_t graph_logits = 0, graph_greedy = 0;
-    // The persistent layers launch (vkml_decode_layers): its per-layer
-    // pointer table and its barrier / error words, when the model allows it.
-    bool persistent = false;
-    Tensor layer_table, sync, work;
 
     const Weight& lm_head() const { return tied ? embed : *lm_head_own; }
 
@@ -348,53 +340,11 @@ struct Llama::Impl {
 
     bool quantized_input(const Weight& w) const { return int_dot && w.int_dot_ok(); }
 
-    // What vkml_decode_layers takes: every layer matrix q4_K on the int8
-    // path (q|k|v stacked), f16 caches, head_dim 128, a multiple of 4 query
-    // heads per KV head, hidden a multiple of 256 up to 4096, ffn a multiple
-    // of 256.
-    bool persistent_ok() const {
-        const LlamaConfig& c = config;
-        const auto q4k = [&](const Weight& w) { return quantized_input(w) && w.type_code() == VKML_Q4_K; };
-        if (!options.persistent_layers || !int_dot || options.kv_cache != DType::F16 || c.head_dim != 128) return false;
-        if (c.num_kv_heads <= 0 || c.num_heads % c.num_kv_heads != 0 || (c.num_heads / c.num_kv_heads) % 4 != 0) return false;
-        if (c.num_heads / 4 > 64) return false;
-        if (c.hidden_size % 256 != 0 || c.hidden_size > 4096 || c.intermediate_size % 256 != 0 || c.intermediate_size > 32768) return false;
-        if ((c.num_heads * c.head_dim) % 256 != 0 || chunks > 1024) return false;
-        return std::all_of(layers.begin(), layers.end(), [&](const Layer& L) {
-            return L.qkv.size() == 1 && q4k(L.qkv[0].first) && q4k(L.o) && q4k(L.gate) && q4k(L.up) && q4k(L.down);
-        });
-    }
-
-    // Uploads the layer table and clears the sync words.
-    void setup_persistent(Context& context) {
-        std::vector<vkml_decode_layer> table;
-        for (const Layer& L : layers) {
-            table.push_back({static_cast<const float*>(L.attn_norm.data()), static_cast<const float*>(L.ffn_norm.data()),
-                             L.qkv[0].first.values(), L.qkv[0].first.scales(), L.o.values(), L.o.scales(), L.gate.values(),
-                             L.gate.scales(), L.up.values(), L.up.scales(), L.down.values(), L.down.scales(),
-                             const_cast<void*>(L.k_cache.data()), const_cast<void*>(L.v_cache.data())});
-        }
-        const std::uint64_t bytes = table.size() * sizeof(vkml_decode_layer);
-        layer_table = Tensor::zeros(context, {static_cast<std::int64_t>((bytes + 3) / 4)}, DType::I32);
-        check(vkml_memcpy_h2d(layer_table.data(), table.data(), bytes), "Llama: layer table");
-        const vkml_decode_layers_params p = layers_params();
-        sync = Tensor::zeros(context, {static_cast<std::int64_t>(vkml_decode_sync_bytes(&p) / 4)}, DType::I32);
-        work = Tensor::zeros(context, {static_cast<std::int64_t>((vkml_decode_work_bytes(&p) + 3) / 4)}, DType::I32);
-    }
-
-    vkml_decode_layers_params layers_params() const {
-        const LlamaConfig& c = config;
-        return vkml_decode_layers_params{u32(c.num_layers), u32(c.hidden_size), u32(c.num_heads), u32(c.num_kv_heads), u32(c.head_dim),
-                                         u32(c.intermediate_size), VKML_Q4_K, VKML_F16, u32(context_length), u32(chunks),
-                                         c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1, c.rms_norm_eps,
-                                         1.0f / std::sqrt(static_cast<float>(c.head_dim))};
-    }
-
-    // Reports a grid barrier of the persistent launch that timed out.
-    void check_persistent() const {
-        if (persistent) check(vkml_decode_layers_check(static_cast<std::uint32_t*>(const_cast<void*>(sync.data()))), "Llama: decode step");
-        if (!persistent && int_dot)
-            check(vkml_attend_o_check(static_cast<std::uint32_t*>(const_cast<void*>(o_sync.data()))), "Llama: decode step");
+    // Reports a merge + o launch whose wait for the merge gave up (the
+    // step's KV rows and logits from that step on are then invalid and must
+    // be recomputed: the caller's position does not advance past them).
+    void check_attend_o() const {
+        if (int_dot) check(vkml_attend_o_check(static_cast<std::uint32_t*>(const_cast<void*>(o_sync.data()))), "Llama: decode step");
     }
 
     // One token: the state's token at the state's position.
@@ -422,13 +372,6 @@ struct Llama::Impl {
         // GEMV (rms_norm + Q8_0 in the kernel's prologue, vkml_gemv_fused);
         // not the lm_head's, whose thousands of workgroups would each redo it.
         const bool fold = quant_d && d <= 4096;
-        if (persistent) {
-            tag("layers");
-            const vkml_decode_layers_params lp = layers_params();
-            const vkml_decode_buffers b{xp, static_cast<float*>(partial.data()), static_cast<float*>(stats.data()), work.data(),
-                                        static_cast<const float*>(rope.data()), static_cast<std::uint32_t*>(sync.data())};
-            check(vkml_decode_layers(&lp, static_cast<const vkml_decode_layer*>(layer_table.data()), &b, st), "decode_layers");
-        }
         const auto fused = [&](const Weight& w, const Tensor& nw, float* out, const char* t) {
             tag(t);
             const vkml_gemv_fused_params fp{u32(w.rows), u32(w.cols), w.type_code(), w.scale_code(), 0, 1, c.rms_norm_eps, 0};
@@ -437,7 +380,6 @@ struct Llama::Impl {
                   t);
         };
         for (const Layer& L : layers) {
-            if (persistent) break;
             const bool fold_qkv =
                 fold && std::all_of(L.qkv.begin(), L.qkv.end(), [&](const auto& wr) { return quantized_input(wr.first); });
             if (fold_qkv) {
@@ -807,8 +749,6 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
     m.chunks = (context_length + 127) / 128;
     m.partial = f32(c.num_heads * m.chunks * hd);
     m.stats = f32(c.num_heads * m.chunks * 2);
-    m.persistent = m.persistent_ok();
-    if (m.persistent) m.setup_persistent(context);
     context.synchronize();
     return Llama(std::move(impl));
 }
@@ -826,13 +766,13 @@ Tensor Llama::forward(std::span<const std::int32_t> tokens) {
         // 366 with attention.cpp:199-203).
         m.set_state(tokens[0], m.position);
         m.run_step(false);
+        m.check_attend_o();
         ++m.position;
     } else {
         m.prefill(tokens, nullptr);
     }
     Tensor out = Tensor::empty(*m.context, {m.config.vocab_size}, DType::F32);
     check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward");
-    m.check_persistent();
     return out;
 }
 
@@ -844,12 +784,12 @@ Tensor Llama::forward_all(std::span<const std::int32_t> tokens) {
     if (t == 1) {
         m.set_state(tokens[0], m.position);
         m.run_step(false);
+        m.check_attend_o();
         ++m.position;
         check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward_all");
     } else {
         m.prefill(tokens, &out);
     }
-    m.check_persistent();
     return out;
 }
 
@@ -861,7 +801,7 @@ std::vector<std::int32_t> Llama::generate_greedy(std::int32_t first, std::int64_
     for (std::int64_t i = 0; i < count; ++i) m.run_step(true);
     std::vector<std::int32_t> out(static_cast<std::size_t>(count));
     check(vkml_memcpy_d2h(out.data(), m.log.data(), out.size() * 4), "Llama::generate_greedy");
-    m.check_persistent();
+    m.check_attend_o();
     m.position += count;
     return out;
 }

@@ -457,6 +457,23 @@ int vkml_attend_step_o(const vkml_attend_step_params* p, const float* d_qkv, con
  * earlier vkml_attend_step_o on this sync buffer that timed out. */
 int vkml_attend_o_check(uint32_t* d_sync);
 
+/* vkml_attend_step without the d_partial / d_stats workspace, allocating
+ * nothing: no counterpart in the reference. For callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation). The partials and statistics live in the
+ * library's own device scratch of VKML_ATTEND_SCRATCH_BYTES per GPU (held
+ * until the process ends): heads * chunks * head_dim * 4 bytes rounded up to
+ * 256, plus heads * chunks * 8, must fit (VKML_ERROR_INVALID_ARGUMENT
+ * otherwise; 32 heads of 128 at 32768 positions need 4.3 MB). Results are
+ * bit for bit vkml_attend_step's. Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (graphs replayed on other streams)
+ * race; calls on the library's stream are ordered and do not. */
+#define VKML_ATTEND_SCRATCH_BYTES (8u << 20)
+int vkml_attend_step_noalloc(const vkml_attend_step_params* p, const float* d_qkv, const float* d_rope_table,
+                             void* d_k_cache, void* d_v_cache, float* d_out, void* d_values, float* d_scales,
+                             const vkml_decode_state* d_state);
+
+
 /* ---------------------------------------------------------------------- */
 /* Fused decode-step kernels (no single reference counterpart: each       */
 /* replaces a sequence of the reference's dispatches, cited).             */

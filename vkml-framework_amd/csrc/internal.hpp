@@ -32,6 +32,10 @@ struct ProfileScope {
 // Checks the launch that just happened.
 int check_launch(const char* what);
 
+// The device address of vkml_attend_step_noalloc's scratch on the current
+// device (k_attend.hip); vkml_init calls it once per device.
+int attend_scratch_setup(int device);
+
 }  // namespace vkml::abi
 
 #define VKML_REQUIRE_INIT()                                                              \

@@ -339,6 +339,77 @@ int vkml_attend_step_o(const vkml_attend_step_params* p, const float* qkv, const
     return vkml_gemv_dot_add(o, values, o_values, x, o_scales, scales, x);
 }
 
+}  // extern "C"
+
+// ------------------------------------------------- attend_step, no allocation
+
+// The chunk partials and statistics of vkml_attend_step_noalloc: device
+// memory of the library itself, so that a call allocates nothing. Each GPU
+// holds its own copy until the process ends; host code never passes the
+// array's name to a kernel (that is a host-side stand-in, not the device
+// address) but the address hipGetSymbolAddress gives per device.
+static __device__ __align__(256) uint8_t scratch[VKML_ATTEND_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+void* g_scratch[kMaxDevices] = {};
+
+// Bytes of the partials [heads, chunks, hd] f32, then the statistics
+// [heads, chunks, 2] f32 from the next 256-byte boundary.
+uint64_t partial_bytes(const vkml_attend_step_params* p) {
+    return (static_cast<uint64_t>(p->heads) * p->chunks * p->head_dim * 4 + 255) / 256 * 256;
+}
+
+}  // namespace
+
+namespace vkml::abi {
+
+// Called by vkml_init with the chosen device current: the device address of
+// this device's scratch.
+int attend_scratch_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return fail(VKML_ERROR_DEVICE, "vkml_init: device index out of range");
+    if (g_scratch[device]) return VKML_OK;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "vkml_init: scratch address");
+    g_scratch[device] = ptr;
+    return VKML_OK;
+}
+
+}  // namespace vkml::abi
+
+extern "C" {
+
+int vkml_attend_step_noalloc(const vkml_attend_step_params* p, const float* qkv, const float* rope_table, void* k_cache,
+                             void* v_cache, float* out, void* values, float* scales, const vkml_decode_state* state) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "attend_step_noalloc: null params");
+    const uint64_t need = partial_bytes(p) + static_cast<uint64_t>(p->heads) * p->chunks * 8;
+    VKML_CHECK_ARG(need <= VKML_ATTEND_SCRATCH_BYTES,
+                   "attend_step_noalloc: " + std::to_string(p->heads) + " heads x " + std::to_string(p->chunks) + " chunks of head_dim " +
+                       std::to_string(p->head_dim) + " need " + std::to_string(need) + " bytes of partials and statistics, more than the " +
+                       std::to_string(VKML_ATTEND_SCRATCH_BYTES) + " bytes of scratch");
+    const int device = vkml::abi::device_index();
+    VKML_CHECK_ARG(device >= 0 && device < kMaxDevices && g_scratch[device], "attend_step_noalloc: no scratch on this device");
+    auto* base = static_cast<uint8_t*>(g_scratch[device]);
+    float* partial = reinterpret_cast<float*>(base);
+    float* stats = reinterpret_cast<float*>(base + partial_bytes(p));
+    // Every chunk slot of the scratch is written by the chunk pass (live
+    // results, or a max of -inf past the live keys) before the merge reads
+    // it, so nothing left by an earlier call is read.
+    if (int r = check_step(p, qkv, rope_table, k_cache, v_cache, partial, stats, out, values, scales, state, "attend_step_noalloc")) return r;
+    const ChunkArgs args = step_args(p, qkv, rope_table, k_cache, v_cache, partial, stats, state, nullptr);
+    {
+        vkml::abi::ProfileScope prof("attend_step");
+        launch_chunks(p->head_dim, p->kv_type == VKML_F16, args);
+        if (int r = vkml::abi::check_launch("attend_step_noalloc")) return r;
+    }
+    vkml::abi::ProfileScope prof("attend_merge");
+    launch_merge(p->heads, p->head_dim, p->chunks, partial, stats, out, values, scales);
+    return vkml::abi::check_launch("attend_step_noalloc");
+}
+
 int vkml_attend_o_check(uint32_t* sync) {
     VKML_REQUIRE_INIT();
     VKML_CHECK_ARG(sync, "attend_o_check: null buffer");

@@ -196,6 +196,11 @@ int vkml_init(const char* device_name) {
     info.integer_dot_product = 1;
     info.timestamps = 1;
     info.timestamp_period_ns = 1.0;
+    if (int r = attend_scratch_setup(chosen)) {
+        (void)hipStreamDestroy(g.stream);
+        g.stream = nullptr;
+        return r;
+    }
     g.device = chosen;
     g.ready = true;
     return VKML_OK;

@@ -124,6 +124,7 @@ SIGNATURES = {
     "vkml_attend_step": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step_o": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp],
     "vkml_attend_o_check": [vp],
+    "vkml_attend_step_noalloc": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_o_sync_bytes": [],
     "vkml_state_set": [vp, i32, i32, i32],
     "vkml_embedding_state": [P(EmbeddingParams), vp, vp, vp, vp],

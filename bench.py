@@ -11,7 +11,15 @@ at the end.
 Prints one JSON line: tokens/s, the whole step's algorithmic HBM rate (GGUF
 bytes of every weight plus the KV rows read) against 8 TB/s, a roofline
 entry for the dominant kernel, and the CPU oracle's decode rate on the host
-cores as a reported baseline.
+cores as a reported baseline. The oracle continues from the GPU's KV cache
+(handed over after the GPU's prefill) and its greedy tokens must equal the
+timed run's: "parity" says whether they do.
+
+Under "configs" the line also carries BASELINE.json's other measured
+configs: cfg2's isolated GEMVs and cfg4's decode attention (each launched
+back to back over rotating distinct copies of at least 512 MB, so no cache
+holds the operands; best and median per launch over the rotations), and
+cfg3's decode rate with its 512-token prefill on the matrix cores.
 
 The dominant kernel is the fused gate/up GEMV (66 MB of q4_K weights a
 layer, the largest share of a step's bytes and of its time): the ffn RMSNorm
@@ -42,9 +50,13 @@ PROMPT = 4096
 # HBM bytes one gate/up launch moves (reads + writes): FETCH_SIZE and
 # WRITE_SIZE passes of rocprofv3 over `bench.py --roofline-only`, each scaled
 # by the same counter's reading for a 256 MiB device copy; the readings and
-# commands are in profiles/gate_up_cfg5_hbm_traffic.md. Valid for the kernel
-# they were taken on; measured again after a change to it.
+# commands are in profiles/gate_up_cfg5_hbm_traffic.md. Valid only for the
+# kernel sources they were taken on: GATE_UP_TRAFFIC_SOURCES is the SHA-256
+# (first 16 hex digits) of those files, and the line reports no traffic
+# when the sources have changed since.
 GATE_UP_TRAFFIC = 67_141_422
+GATE_UP_TRAFFIC_SOURCES = "unmeasured"
+TRAFFIC_FILES = ("vkml-framework_amd/csrc/gemv.hpp", "vkml-framework_amd/csrc/k_gemv.hip", "vkml-framework_amd/csrc/device.hpp")
 
 # GGUF-native bytes per weight (q4_K 144 B / 256, q6_K 210 B / 256).
 Q4K, Q6K = 144 / 256, 210 / 256
@@ -52,6 +64,25 @@ Q4K, Q6K = 144 / 256, 210 / 256
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def sources_hash(files=TRAFFIC_FILES):
+    import hashlib
+    h = hashlib.sha256()
+    for f in files:
+        with open(os.path.join(ROOT, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def host_cores():
+    """(threads the CPU baseline uses, the host's logical CPUs): the box's
+    share of its host is 16 threads for one GPU, whatever the host has."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return min(16, avail), os.cpu_count() or avail
 
 
 def algorithmic_bytes(spec):
@@ -169,6 +200,146 @@ def roofline_only(spec):
     log(f"copy: 3 x {n} bytes")
 
 
+def rotation_times(n_copies, launch, rotations=5):
+    """Per-launch microseconds of each of `rotations` passes over n_copies
+    back-to-back launches (launch(i) issues copy i's), between HIP events on
+    the library's stream, after one untimed pass: (best, median)."""
+    from vkml_amd import hip as H
+    ev = _Events()
+    try:
+        for i in range(n_copies):
+            launch(i)
+        H.synchronize()
+        per = []
+        for _ in range(rotations):
+            ms = ev.elapsed_ms(H.stream(), lambda: [launch(i) for i in range(n_copies)])
+            per.append(ms * 1e3 / n_copies)
+    finally:
+        ev.close()
+    per.sort()
+    return per[0], per[len(per) // 2]
+
+
+def filled(nbytes, word):
+    from vkml_amd import hip as H
+    b = H.Buffer(nbytes)
+    H.call("vkml_fill_u32", b.p, word, (nbytes + 3) // 4)
+    return b
+
+
+def bench_gemv_cfg2(min_bytes=512 << 20):
+    """cfg2: y = W x for W 4096x4096, 14336x4096 and 4096x14336 in Q8_0 and
+    Q4_K, x f32. Two figures each: the GEMV kernel on the Q8_0 activation
+    (the decode step's unit of work), and the op as matmul_transposed runs
+    it (the activation quantized, then the GEMV). Algorithmic bytes are the
+    GGUF-native weight bytes plus x in and y out."""
+    from vkml_amd import hip as H
+    out = []
+    for fmt in ("q8_0", "q4_K"):
+        for n, k in ((4096, 4096), (14336, 4096), (4096, 14336)):
+            if fmt == "q8_0":
+                codes, scales, bt, wbytes = n * k, n * k // 32 * 2, H.Q8_0, n * k * 34 // 32
+                patt = (0x7F81C03E, 0x1C231C17)
+            else:
+                codes, scales, bt, wbytes = n * k // 2, n * k // 256 * 16, H.Q4_K, n * k * 144 // 256
+                patt = (0x5A3C96E1, 0x2C1F2C00)
+            copies = max(2, -(-min_bytes // (codes + scales)))
+            mats = [(filled(codes, patt[0] + i), filled(scales, patt[1])) for i in range(copies)]
+            x, xq, xs, y = filled(k * 4, 0x3F000000), filled(k, 0), filled(k // 32 * 4, 0), filled(n * 4, 0)
+            dp = H.GemvDotParams(1, n, k, bt, H.F16)
+            qp = H.QuantizeParams(k // 32, H.F32, H.Q8_0, H.F32)
+            H.call("vkml_quantize", qp, x.p, xq.p, xs.p)
+            kern = rotation_times(copies, lambda i: H.call("vkml_gemv_dot", dp, xq.p, mats[i][0].p, y.p, mats[i][1].p, xs.p))
+
+            def op(i):
+                H.call("vkml_quantize", qp, x.p, xq.p, xs.p)
+                H.call("vkml_gemv_dot", dp, xq.p, mats[i][0].p, y.p, mats[i][1].p, xs.p)
+            opt = rotation_times(copies, op)
+            alg = wbytes + 4 * k + 4 * n
+            out.append({"format": fmt, "n": n, "k": k, "bytes": alg,
+                        "kernel_us": {"best": round(kern[0], 3), "median": round(kern[1], 3)},
+                        "kernel_frac": round(alg / (kern[0] * 1e-6) / 1e9 / PEAK_HBM, 4),
+                        "op_us": {"best": round(opt[0], 3), "median": round(opt[1], 3)},
+                        "op_frac": round(alg / (opt[0] * 1e-6) / 1e9 / PEAK_HBM, 4)})
+            log(f"cfg2 {fmt} {n}x{k}: gemv {kern[0]:.2f} us ({alg / (kern[0] * 1e-6) / 1e9:.0f} GB/s), "
+                f"quantize + gemv {opt[0]:.2f} us")
+            for m in mats:
+                for b in m:
+                    b.close()
+            for b in (x, xq, xs, y):
+                b.close()
+    return out
+
+
+def bench_attention_cfg4(min_bytes=512 << 20):
+    """cfg4: decode attention of 32 query heads on 8 KV heads, head_dim 128,
+    over f16 caches of T = 4096, 16384 and 32768 positions: the chunk pass
+    and the merge (vkml_attend + vkml_attend_merge). Algorithmic bytes: K
+    and V (4096 T) plus q in and the output out."""
+    import math
+    from vkml_amd import hip as H
+    heads, kvh, hd = 32, 8, 128
+    out = []
+    for T in (4096, 16384, 32768):
+        cache = kvh * T * hd * 2
+        copies = max(2, -(-min_bytes // (2 * cache)))
+        caches = [(filled(cache, 0x3C003800 + i), filled(cache, 0x38003C00 + i)) for i in range(copies)]
+        chunks = (T + 127) // 128
+        q = filled(heads * hd * 4, 0x3F000000)
+        part, stats, o = filled(heads * chunks * hd * 4, 0), filled(heads * chunks * 8, 0), filled(heads * hd * 4, 0)
+        prm = H.AttendParams(0, T, T, heads, kvh, hd, H.F16, chunks, 1.0 / math.sqrt(hd), 0.0)
+
+        def call(i):
+            H.call("vkml_attend", prm, q.p, caches[i][0].p, caches[i][1].p, part.p, stats.p, None)
+            H.call("vkml_attend_merge", prm, part.p, stats.p, o.p, None, None)
+        best, med = rotation_times(copies, call)
+        alg = 2 * cache + 2 * heads * hd * 4
+        out.append({"positions": T, "bytes": alg, "us": {"best": round(best, 3), "median": round(med, 3)},
+                    "frac": round(alg / (best * 1e-6) / 1e9 / PEAK_HBM, 4)})
+        log(f"cfg4 attention at {T}: {best:.2f} us ({alg / (best * 1e-6) / 1e9:.0f} GB/s)")
+        for c in caches:
+            for b in c:
+                b.close()
+        for b in (q, part, stats, o):
+            b.close()
+    return out
+
+
+def bench_cfg3(L, steps=128, prompt_len=512):
+    """cfg3: the Llama-3.2-1B-shaped model (16 layers, tied q6_K vocabulary
+    of 128256) with a 512-token prompt prefilled on the matrix cores, then
+    `steps` greedy decode tokens timed back to back."""
+    from vkml_amd import synth
+    spec = synth.CONFIGS["cfg3"]
+    path = os.path.join(synth.scratch_dir(), f"vkml_bench_cfg3_{os.getpid()}.gguf")
+    synth.write_model(spec, path, seed=4)
+    try:
+        model = L.Llama(path, prompt_len + steps + 1, kv_f16=True)
+        prompt = np.random.default_rng(4).integers(0, spec.vocab, prompt_len).astype(np.int32)
+        pre = prefill_rates(model, spec, prompt, [prompt_len], L)
+        model.rewind(0)
+        first = int(np.argmax(model.forward(prompt)))
+        model.generate_greedy(first, 8)
+        model.rewind(prompt_len)
+        L.synchronize()
+        t0 = time.perf_counter()
+        model.generate_greedy(first, steps)
+        secs = time.perf_counter() - t0
+        d, ff, layers = spec.hidden, spec.ffn, spec.n_layers
+        qd, kvd = spec.heads * spec.head_dim, spec.kv_heads * spec.head_dim
+        weights = layers * ((qd + 2 * kvd) * d + d * qd + 3 * ff * d) * Q4K + spec.vocab * d * Q6K + d * Q6K
+        kv = layers * 2 * kvd * 2 * (prompt_len + (steps + 1) / 2)
+        tok_s = steps / secs
+        gbs = (weights + kv) * tok_s / 1e9
+        log(f"cfg3 decode: {tok_s:.1f} tokens/s, {gbs:.0f} GB/s algorithmic")
+        model.close()
+        return {"decode_tokens_per_s": round(tok_s, 1), "ms_per_token": round(secs * 1e3 / steps, 4),
+                "bytes_per_token": round(weights + kv), "hbm_gb_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM, 4),
+                "prefill": pre[0] if pre else None}
+    finally:
+        os.remove(path)
+
+
 def matrix_macs(spec):
     """Multiply-accumulates of one token's layer projections (q|k|v, o,
     gate, up, down) over all layers: matmul_dot's work per prompt row."""
@@ -237,6 +408,8 @@ def main():
                          "that cannot follow graph launches; the kernels are the same)")
     ap.add_argument("--prefill", type=int, nargs="*", default=[512, 4096],
                     help="prompt lengths whose prefill rate is measured after the decode run (none: skip)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the cfg2, cfg3 and cfg4 measurements")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the dominant kernel's timed launches and a 256 MiB device copy of known size, "
                          "for hardware-counter passes (FETCH_SIZE, WRITE_SIZE) that scale the kernel's HBM bytes "
@@ -320,26 +493,47 @@ def main():
 
         pre = prefill_rates(model, spec, prompt, args.prefill, L) if args.prefill else None
 
-        cpu = None
+        cpu, parity = None, None
         if args.cpu_tokens > 0:
+            # The oracle continues from the GPU's cache: rows 0 .. prompt - 1
+            # hold the prompt's keys and values (the prefill passes above
+            # rewrote them with the same prompt).
             sys.path.insert(0, os.path.join(ROOT, "oracle"))
             import oracle as O
-            threads = min(16, os.cpu_count() or 1)
+            threads, nproc = host_cores()
             O.set_threads(threads)
             t0 = time.time()
             ref = O.Model(path, context, kv_f16=True)
-            log(f"oracle loaded in {time.time() - t0:.1f} s")
+            for layer in range(spec.n_layers):
+                k, v = model.read_kv_cache(layer)
+                ref.set_kv(layer, k, v)
             ref.set_position(args.prompt)
+            log(f"oracle loaded with the GPU's KV cache in {time.time() - t0:.1f} s")
             t0 = time.perf_counter()
+            cpu_tokens, nxt = [], first
             for i in range(args.cpu_tokens):
-                ref.forward(np.array([first], np.int32))
+                nxt = int(O.argmax(ref.forward(np.array([nxt], np.int32))))
+                cpu_tokens.append(nxt)
             cpu_s = time.perf_counter() - t0
-            cpu = {"value": round(args.cpu_tokens / cpu_s, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
-                   "sample": f"{args.cpu_tokens} decode tokens of the same model at positions {args.prompt}.. "
-                             f"(CPU oracle, int8 path, {threads} threads, {cpu_s:.1f} s)"}
+            parity = cpu_tokens == [int(t) for t in tokens[:args.cpu_tokens]]
+            cpu = {"value": round(args.cpu_tokens / cpu_s, 4), "unit": "tokens/s", "cores": threads, "host_cpus": nproc,
+                   "kind": "port",
+                   "sample": f"{args.cpu_tokens} greedy decode tokens of the same model at positions {args.prompt}.. from the "
+                             f"GPU's KV cache (CPU oracle, the reference's int8 path, {threads} threads of the box's "
+                             f"{nproc} logical CPUs, {cpu_s:.1f} s)",
+                   "tokens": cpu_tokens}
             ref.close()
-            log(f"cpu oracle: {cpu['value']} tokens/s on {threads} threads")
+            log(f"cpu oracle: {cpu['value']} tokens/s on {threads} threads; tokens {cpu_tokens} "
+                f"{'equal' if parity else 'DIFFER FROM'} the GPU's {[int(t) for t in tokens[:args.cpu_tokens]]}")
 
+        configs = None
+        if not args.no_configs:
+            configs = {"cfg2_gemv": bench_gemv_cfg2(), "cfg4_attention": bench_attention_cfg4()}
+            model.close()
+            model = None
+            configs["cfg3"] = bench_cfg3(L)
+
+        traffic = GATE_UP_TRAFFIC if sources_hash() == GATE_UP_TRAFFIC_SOURCES else None
         result = {
             "metric": "batch-1 decode tokens/s + achieved HBM GB/s (% of 8 TB/s), 1xMI355X",
             "value": round(tok_s, 2),
@@ -363,15 +557,19 @@ def main():
             "gpu_busy_ms_per_step": round(busy_ms, 4),
             "roofline": {"bound": "hbm", "kernel": "gemv_fused gate/up (k_gemv_dot<q4_K, f16, 8 lanes, swiglu, norm, q8_0 out>)",
                          "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s",
-                         "frac": round(achieved / PEAK_HBM, 4), "traffic": GATE_UP_TRAFFIC,
-                         "traffic_over_algorithmic": round(GATE_UP_TRAFFIC / dom_bytes, 4),
+                         "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
+                         "traffic_over_algorithmic": round(traffic / dom_bytes, 4) if traffic else None,
+                         "traffic_sources": sources_hash(),
                          "bytes_per_launch": round(dom_bytes), "avg_launch_us": round(dom_us, 3)},
             "cpu_baseline": cpu,
+            "parity": parity,
             "prefill": pre,
+            "configs": configs,
             "tokens_head": [int(t) for t in tokens[:8]],
         }
         print(json.dumps(result), flush=True)
-        model.close()
+        if model is not None:
+            model.close()
     finally:
         try:
             os.remove(path)

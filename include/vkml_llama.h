@@ -78,6 +78,46 @@ int vkml_llama_rewind(vkml_llama* model, int64_t position, int64_t* out);
  * host (element size 2 for an f16 cache, 4 for f32). */
 int vkml_llama_read_kv_cache(const vkml_llama* model, int64_t layer, void* k_out, void* v_out, uint64_t bytes);
 
+/* ---- Sampling and serving (include/vkml/sampling.hpp:14-31 and
+ * src/io/sampling.cpp:17-139 there; apps/generation.hpp:139-202 there). ---- */
+
+/* SamplingOptions: temperature 0 (or top_k 1) is greedy; top_k 0 keeps all;
+ * top_p 1 and min_p 0 are off; penalties 1 (repetition) and 0 are off. */
+typedef struct vkml_sampling_options {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float repetition_penalty;
+    float min_p;
+    float frequency_penalty;
+    float presence_penalty;
+    uint64_t seed;
+} vkml_sampling_options;
+void vkml_sampling_default_options(vkml_sampling_options* out);
+
+/* Sampler: host code, no device needed. sample() is Sampler::sample over
+ * logits[vocab] with previous[n_previous] (the tokens so far) for the
+ * repetition penalty; each call advances the sampler's generator. */
+typedef struct vkml_sampler vkml_sampler;
+int vkml_sampler_create(const vkml_sampling_options* options, vkml_sampler** out);
+void vkml_sampler_free(vkml_sampler* sampler);
+int vkml_sampler_sample(vkml_sampler* sampler, const float* logits, int64_t vocab, const int32_t* previous,
+                        int64_t n_previous, int32_t* token_out);
+
+/* A model with the tokens its KV cache holds, for one request after another
+ * (ChatModel::generate): each prompt reuses the cache of its longest common
+ * prefix with the last; the reply (without the stop token) goes to
+ * reply[capacity], its length to *reply_len, and *finish is 0 for a stop
+ * token, 1 for max_tokens (negative: none) or the context's end. The model
+ * must outlive the session; one thread at a time. */
+typedef struct vkml_session vkml_session;
+int vkml_session_create(vkml_llama* model, const int32_t* stop, int64_t n_stop, vkml_session** out);
+void vkml_session_free(vkml_session* session);
+int vkml_session_generate(vkml_session* session, const int32_t* prompt, int64_t n_prompt, vkml_sampler* sampler,
+                          int64_t max_tokens, int32_t* reply, int64_t capacity, int64_t* reply_len, int32_t* finish);
+/* The tokens the cache holds: writes up to capacity, returns how many. */
+int64_t vkml_session_cached(const vkml_session* session, int32_t* out, int64_t capacity);
+
 /* Context::set_profiling / profile / reset_profile (context.hpp:120-126):
  * up to capacity labels, slowest first; *count gets how many exist. */
 int vkml_llama_set_profiling(int32_t enabled);

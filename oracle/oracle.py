@@ -86,6 +86,11 @@ def _declare(L):
         "orc_model_v_cache": (vp, [vp, i32]),
         "orc_model_set_kv": (i32, [vp, i32, vp, vp]),
         "orc_model_reference_f64": (i32, [C.c_char_p, vp, i64, vp]),
+        "orc_sampler_new": (vp, [f32, i32, f32, C.c_uint64, f32, f32, f32, f32]),
+        "orc_sampler_free": (None, [vp]),
+        "orc_sampler_sample": (i32, [vp, vp, i64, vp, i64]),
+        "orc_sampler_draw_u64": (C.c_uint64, [vp]),
+        "orc_sampler_draw_uniform": (C.c_double, [vp, C.c_double]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -382,3 +387,34 @@ def reference_f64(gguf_path: str, tokens) -> np.ndarray:
     if lib().orc_model_reference_f64(gguf_path.encode(), _p(t), t.size, _p(out)) != 0:
         raise RuntimeError(last_error())
     return out
+
+
+class Sampler:
+    """orc_sampler: the reference's Sampler (src/io/sampling.cpp:17-139)."""
+
+    def __init__(self, temperature=0.0, top_k=0, top_p=1.0, seed=0, repetition_penalty=1.0, min_p=0.0,
+                 frequency_penalty=0.0, presence_penalty=0.0):
+        self._h = lib().orc_sampler_new(temperature, top_k, top_p, seed, repetition_penalty, min_p,
+                                        frequency_penalty, presence_penalty)
+
+    def sample(self, logits, previous=()) -> int:
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        pv = np.ascontiguousarray(previous, dtype=np.int32)
+        return int(lib().orc_sampler_sample(self._h, _p(lg), lg.size, _p(pv), pv.size))
+
+    def draw_u64(self) -> int:
+        return int(lib().orc_sampler_draw_u64(self._h))
+
+    def draw_uniform(self, total: float) -> float:
+        return float(lib().orc_sampler_draw_uniform(self._h, total))
+
+    def close(self) -> None:
+        if self._h:
+            lib().orc_sampler_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

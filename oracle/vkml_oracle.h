@@ -156,6 +156,18 @@ const void* orc_model_v_cache(const orc_model* m, int layer);
  * of a long prompt -- is continued here with orc_model_set_position. */
 int orc_model_set_kv(orc_model* m, int layer, const void* k, const void* v);
 
+/* ---- the sampler: src/io/sampling.cpp:17-139 (oracle_sampling.c) ---- */
+typedef struct orc_sampler orc_sampler;
+orc_sampler* orc_sampler_new(float temperature, int top_k, float top_p, uint64_t seed, float repetition_penalty,
+                             float min_p, float frequency_penalty, float presence_penalty);
+void orc_sampler_free(orc_sampler* s);
+int32_t orc_sampler_sample(orc_sampler* s, const float* logits, int64_t n, const int32_t* previous,
+                           int64_t n_previous);
+/* The generator alone, for its pins: the next 64-bit output, and a
+ * uniform_real_distribution<double>(0, total) draw. */
+uint64_t orc_sampler_draw_u64(orc_sampler* s);
+double orc_sampler_draw_uniform(orc_sampler* s, double total);
+
 /* Double-precision forward of the dequantized weights from scratch, no
  * activation quantization (tests/test_llama.cpp:585-755): logits of the last
  * token. Returns 0 or -1. */

@@ -19,6 +19,11 @@ class Options(C.Structure):
                 ("device_name", C.c_char_p), ("prompt_score_bytes", i64)]
 
 
+class SamplingOptions(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", i32), ("top_p", C.c_float), ("repetition_penalty", C.c_float),
+                ("min_p", C.c_float), ("frequency_penalty", C.c_float), ("presence_penalty", C.c_float), ("seed", u64)]
+
+
 class Config(C.Structure):
     _fields_ = [(n, i64) for n in ("vocab_size", "hidden_size", "intermediate_size", "num_layers", "num_heads",
                                    "num_kv_heads", "head_dim", "max_positions")] + \
@@ -46,6 +51,14 @@ SIGNATURES = {
     "vkml_llama_profile": (C.c_int, [vp, u32, vp, vp, u32, P(u32)]),
     "vkml_llama_reset_profile": (C.c_int, []),
     "vkml_llama_synchronize": (C.c_int, []),
+    "vkml_sampling_default_options": (None, [vp]),
+    "vkml_sampler_create": (C.c_int, [vp, P(vp)]),
+    "vkml_sampler_free": (None, [vp]),
+    "vkml_sampler_sample": (C.c_int, [vp, vp, i64, vp, i64, vp]),
+    "vkml_session_create": (C.c_int, [vp, vp, i64, P(vp)]),
+    "vkml_session_free": (None, [vp]),
+    "vkml_session_generate": (C.c_int, [vp, vp, i64, vp, i64, vp, i64, vp, vp]),
+    "vkml_session_cached": (i64, [vp, vp, i64]),
 }
 
 _lib = None
@@ -187,3 +200,73 @@ def profile() -> list[tuple[str, int, float]]:
 
 def shutdown() -> None:
     _check(lib().vkml_llama_shutdown())
+
+
+class Sampler:
+    """vkml::Sampler (host code: no device needed)."""
+
+    def __init__(self, **options):
+        o = SamplingOptions()
+        lib().vkml_sampling_default_options(C.byref(o))
+        for k, v in options.items():
+            setattr(o, k, v)
+        self._h = vp()
+        _check(lib().vkml_sampler_create(C.byref(o), C.byref(self._h)))
+
+    def sample(self, logits, previous=()) -> int:
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        pv = np.ascontiguousarray(previous, dtype=np.int32)
+        out = i32()
+        _check(lib().vkml_sampler_sample(self._h, _ptr(lg), lg.size, _ptr(pv), pv.size, C.byref(out)))
+        return int(out.value)
+
+    def close(self) -> None:
+        if self._h:
+            lib().vkml_sampler_free(self._h)
+            self._h = vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Session:
+    """vkml::Session: requests against one model, reusing its KV cache."""
+
+    STOP, LENGTH = 0, 1
+
+    def __init__(self, model: Llama, stop=()):
+        st = np.ascontiguousarray(stop, dtype=np.int32)
+        self.model = model
+        self._h = vp()
+        _check(lib().vkml_session_create(model._h, _ptr(st), st.size, C.byref(self._h)))
+
+    def generate(self, prompt, sampler: Sampler, max_tokens: int):
+        """(reply tokens, finish: STOP or LENGTH)."""
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        cap = max(max_tokens, 0) if max_tokens >= 0 else self.model.context_length
+        out = np.empty(max(cap, 1), np.int32)
+        n, fin = i64(), i32()
+        _check(lib().vkml_session_generate(self._h, _ptr(p), p.size, sampler._h, int(max_tokens), _ptr(out), cap,
+                                           C.byref(n), C.byref(fin)))
+        return out[:n.value].copy(), int(fin.value)
+
+    @property
+    def cached(self) -> np.ndarray:
+        n = lib().vkml_session_cached(self._h, None, 0)
+        out = np.empty(max(n, 1), np.int32)
+        lib().vkml_session_cached(self._h, _ptr(out), n)
+        return out[:n].copy()
+
+    def close(self) -> None:
+        if self._h:
+            lib().vkml_session_free(self._h)
+            self._h = vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -4,11 +4,21 @@
 #include <string>
 
 #include "runtime.hpp"
+#include "vkml/generation.hpp"
 #include "vkml/llama.hpp"
+#include "vkml/sampling.hpp"
 #include "vkml_llama.h"
 
 struct vkml_llama {
     vkml::Llama model;
+};
+
+struct vkml_sampler {
+    vkml::Sampler sampler;
+};
+
+struct vkml_session {
+    vkml::Session session;
 };
 
 namespace {
@@ -156,6 +166,72 @@ int vkml_llama_read_kv_cache(const vkml_llama* m, int64_t layer, void* k_out, vo
         if (k_out) std::memcpy(k_out, kb.data(), kb.size());
         if (v_out) std::memcpy(v_out, vb.data(), vb.size());
     });
+}
+
+void vkml_sampling_default_options(vkml_sampling_options* out) {
+    if (!out) return;
+    const vkml::SamplingOptions d;
+    *out = vkml_sampling_options{d.temperature, d.top_k, d.top_p, d.repetition_penalty, d.min_p, d.frequency_penalty, d.presence_penalty,
+                                 d.seed};
+}
+
+int vkml_sampler_create(const vkml_sampling_options* o, vkml_sampler** out) {
+    return guarded([&] {
+        if (!o || !out) throw vkml::Error("vkml_sampler_create: null argument");
+        vkml::SamplingOptions s;
+        s.temperature = o->temperature;
+        s.top_k = o->top_k;
+        s.top_p = o->top_p;
+        s.repetition_penalty = o->repetition_penalty;
+        s.min_p = o->min_p;
+        s.frequency_penalty = o->frequency_penalty;
+        s.presence_penalty = o->presence_penalty;
+        s.seed = o->seed;
+        *out = new vkml_sampler{vkml::Sampler(s)};
+    });
+}
+
+void vkml_sampler_free(vkml_sampler* s) { delete s; }
+
+int vkml_sampler_sample(vkml_sampler* s, const float* logits, int64_t vocab, const int32_t* previous, int64_t n_previous,
+                        int32_t* token_out) {
+    return guarded([&] {
+        if (!s || !logits || vocab < 0 || !token_out || n_previous < 0 || (n_previous && !previous))
+            throw vkml::Error("vkml_sampler_sample: null or negative argument");
+        *token_out = s->sampler.sample({logits, std::size_t(vocab)}, {previous, std::size_t(n_previous)});
+    });
+}
+
+int vkml_session_create(vkml_llama* m, const int32_t* stop, int64_t n_stop, vkml_session** out) {
+    return guarded([&] {
+        if (!m || !out || n_stop < 0 || (n_stop && !stop)) throw vkml::Error("vkml_session_create: null or negative argument");
+        *out = new vkml_session{vkml::Session(m->model, std::vector<std::int32_t>(stop, stop + n_stop))};
+    });
+}
+
+void vkml_session_free(vkml_session* s) { delete s; }
+
+int vkml_session_generate(vkml_session* s, const int32_t* prompt, int64_t n_prompt, vkml_sampler* sampler, int64_t max_tokens,
+                          int32_t* reply, int64_t capacity, int64_t* reply_len, int32_t* finish) {
+    return guarded([&] {
+        if (!s || !prompt || n_prompt <= 0 || !sampler || (!reply && capacity) || !reply_len)
+            throw vkml::Error("vkml_session_generate: null argument or empty prompt");
+        std::vector<std::int32_t> out;
+        const auto f = s->session.generate({prompt, std::size_t(n_prompt)}, sampler->sampler, max_tokens, out);
+        if (std::int64_t(out.size()) > capacity)
+            throw vkml::Error("vkml_session_generate: a reply of " + std::to_string(out.size()) + " tokens exceeds the capacity of " +
+                              std::to_string(capacity));
+        std::copy(out.begin(), out.end(), reply);
+        *reply_len = std::int64_t(out.size());
+        if (finish) *finish = f == vkml::Session::Finish::stop ? 0 : 1;
+    });
+}
+
+int64_t vkml_session_cached(const vkml_session* s, int32_t* out, int64_t capacity) {
+    if (!s) return -1;
+    const auto& c = s->session.cached();
+    for (std::int64_t i = 0; out && i < capacity && i < std::int64_t(c.size()); ++i) out[i] = c[std::size_t(i)];
+    return std::int64_t(c.size());
 }
 
 int vkml_llama_set_profiling(int32_t enabled) {

@@ -294,7 +294,10 @@ int vkml_rms_norm_quantize(const vkml_rms_norm_params* p, const float* d_x, cons
 
 /* shaders/softmax.comp, src/ops/norms.cpp:176-211: rows of scale * x, with
  * an optional causal mask (query row % q_len at key position offset + that)
- * and window; -inf entries become 0. */
+ * and window; -inf entries become 0. With ring (and causal), the columns
+ * are a ring of that many keys holding key position p in column p % ring
+ * (CausalMask::ring, ops/internal.hpp:67-74): row r sees positions up to
+ * r % q_len + offset, the last `window` of them with a window. */
 typedef struct vkml_softmax_params {
     uint32_t rows, cols;
     float scale;
@@ -303,6 +306,7 @@ typedef struct vkml_softmax_params {
     uint32_t offset;
     uint32_t window;
     float softcap;
+    uint32_t ring;
 } vkml_softmax_params;
 int vkml_softmax(const vkml_softmax_params* p, const float* d_x, float* d_out);
 
@@ -372,9 +376,10 @@ int vkml_embedding(const vkml_embedding_params* p, const void* d_values, const v
 
 /* ---------------------------------------------------------------------- */
 /* Decode attention (shaders/attend.comp + attend_merge.comp,             */
-/* src/ops/attention.cpp:22-84). Keys kv_start..kv_len of caches          */
-/* [kv_heads, capacity, head_dim] (F32 or F16), key position p at row     */
-/* p % capacity, in the reference's chunks of 128 keys from kv_start, a   */
+/* src/ops/attention.cpp:22-84). Keys kv_start..kv_len (at most capacity  */
+/* of them) of caches [kv_heads, capacity, head_dim] (F32 or F16), key    */
+/* position p at row p % capacity (a sliding window's ring), in the       */
+/* reference's chunks of 128 keys from kv_start, a                        */
 /* workgroup per (chunk, query head). With d_state non-NULL, kv_len is    */
 /* d_state->position + 1 (the replayed decode step) and the launch covers */
 /* the whole cache. chunks: the partial buffers' stride, at least         */
@@ -431,6 +436,12 @@ typedef struct vkml_attend_step_params {
     uint32_t rotate;     /* 0: no rope in this layer */
     float scale;
     float softcap;
+    /* Sliding window: the step's query sees keys max(kv_start, position + 1
+     * - window) .. position (attention.cpp:40-47 with a window), in chunks of
+     * 128 from the first (0: no window). With a window the caches can be a
+     * ring (capacity rows, position p at row p % capacity), and chunks must
+     * cover min(window, capacity) keys. */
+    uint32_t window;
 } vkml_attend_step_params;
 int vkml_attend_step(const vkml_attend_step_params* p, const float* d_qkv, const float* d_rope_table,
                      void* d_k_cache, void* d_v_cache, float* d_partial, float* d_stats,
@@ -500,7 +511,9 @@ int vkml_rope_kv_append(const vkml_rope_kv_params* p, const float* d_qkv, const 
  * t of d_qkv (row_stride floats apart) holds token t's q | k | v; q is
  * rotated into d_q [heads, tokens, head_dim] (heads first, llama.cpp:
  * 320-327), k rotated and v rounded to the cache type and written at rows
- * position + t (llama.cpp:344-355). position + tokens <= capacity. */
+ * (position + t) % capacity (llama.cpp:344-355; a ring wraps around,
+ * attention.cpp:260-266). tokens <= capacity; the RoPE table holds
+ * position + tokens rows. */
 int vkml_rope_kv_prompt(const vkml_rope_kv_params* p, uint32_t tokens, uint32_t row_stride,
                         const float* d_qkv, const float* d_table, float* d_q, void* d_k_cache,
                         void* d_v_cache);

@@ -34,6 +34,7 @@ typedef struct vkml_llama_options {
     int32_t use_graphs;         /* 1: replay the decode step as a HIP graph (default) */
     const char* device_name;    /* NULL or "": VKML_DEVICE, then device 0 */
     int64_t prompt_score_bytes; /* scores one piece of a prompt's attention may hold (default 1 GiB); no effect on results */
+    int64_t sliding_extra_rows; /* a sliding window's rings hold window + this many rows (default 1024) */
 } vkml_llama_options;
 
 /* LlamaConfig (llama.hpp:29-116), the fields of the llama architecture. */

@@ -70,7 +70,10 @@ def _declare(L):
         "orc_argmax": (C.c_int32, [vp, i64]),
         "orc_embedding_quantized": (None, [i32, vp, vp, i64, i64, vp, i64, vp]),
         "orc_attend_decode": (None, [vp, i64, vp, vp, i32, i64, i64, i64, i64, i64, f32, vp]),
-        "orc_attention_prefill": (None, [vp, i64, i64, vp, vp, i32, i64, i64, i64, i64, i64, vp]),
+        "orc_attention_prefill": (None, [vp, i64, i64, vp, vp, i32, i64, i64, i64, i64, i64, f32, vp]),
+        "orc_attention_sliding": (None, [vp, i64, i64, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, f32, vp]),
+        "orc_model_load_ex": (vp, [C.c_char_p, i64, i32, i32, i64]),
+        "orc_model_ring": (i64, [vp]),
         "orc_model_load": (vp, [C.c_char_p, i64, i32, i32]),
         "orc_model_free": (None, [vp]),
         "orc_model_forward": (i32, [vp, vp, i64, vp]),
@@ -215,7 +218,7 @@ def matmul_float(b_type, a, b, b_scales, N, K) -> np.ndarray:
     return out
 
 
-def attention_prefill(q, k_cache, v_cache, kv_len: int, max_score_bytes: int = 64 << 20) -> np.ndarray:
+def attention_prefill(q, k_cache, v_cache, kv_len: int, max_score_bytes: int = 64 << 20, softcap: float = 0.0) -> np.ndarray:
     """q [heads, q_len, hd] f32; caches [kv_heads, capacity, hd] f32 or uint16
     (f16 bits); query i at key position kv_len - q_len + i."""
     q = np.ascontiguousarray(q, dtype=np.float32)
@@ -226,7 +229,24 @@ def attention_prefill(q, k_cache, v_cache, kv_len: int, max_score_bytes: int = 6
     v = np.ascontiguousarray(v_cache)
     out = np.empty((heads, q_len, hd), np.float32)
     lib().orc_attention_prefill(_p(q), heads, q_len, _p(k), _p(v), f16, kv_heads, capacity, hd, kv_len,
-                                max_score_bytes, _p(out))
+                                max_score_bytes, softcap, _p(out))
+    return out
+
+
+def attention_sliding(q, k, v, k_ring, v_ring, start: int, window: int, softcap: float = 0.0,
+                      max_score_bytes: int = 64 << 20) -> np.ndarray:
+    """detail::sliding_attention: q [heads, t, hd] f32 at positions start..;
+    k, v [kv_heads, t, hd] in the rings' type (f32, or f16 bits as uint16),
+    appended in place to k_ring / v_ring [kv_heads, ring, hd]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    heads, t, hd = q.shape
+    kv_heads, ring = k_ring.shape[0], k_ring.shape[1]
+    f16 = int(k_ring.dtype == np.uint16)
+    k, v = np.ascontiguousarray(k), np.ascontiguousarray(v)
+    assert k_ring.flags.c_contiguous and v_ring.flags.c_contiguous
+    out = np.empty((heads, t, hd), np.float32)
+    lib().orc_attention_sliding(_p(q), heads, t, _p(k), _p(v), _p(k_ring), _p(v_ring), f16, kv_heads, ring, hd, start,
+                                window, max_score_bytes, softcap, _p(out))
     return out
 
 
@@ -302,8 +322,9 @@ def attend_decode(q, k_cache, v_cache, kv_start: int, kv_len: int, softcap: floa
 class Model:
     """orc_model: the reference's Llama::run restated on the CPU."""
 
-    def __init__(self, gguf_path: str, context: int, kv_f16: bool = True, int_dot: bool = True):
-        self._h = lib().orc_model_load(gguf_path.encode(), context, int(kv_f16), int(int_dot))
+    def __init__(self, gguf_path: str, context: int, kv_f16: bool = True, int_dot: bool = True,
+                 sliding_extra_rows: int = 1024):
+        self._h = lib().orc_model_load_ex(gguf_path.encode(), context, int(kv_f16), int(int_dot), sliding_extra_rows)
         if not self._h:
             raise RuntimeError(last_error())
         self.vocab = int(lib().orc_model_vocab(self._h))
@@ -311,6 +332,7 @@ class Model:
         lib().orc_model_dims(self._h, _p(dims))
         (_, self.hidden, self.ffn, self.layers, self.heads, self.kv_heads, self.head_dim, self.context) = (int(x) for x in dims)
         self.kv_f16 = bool(kv_f16)
+        self.ring = int(lib().orc_model_ring(self._h))  # rows of each cache
 
     def forward(self, tokens) -> np.ndarray:
         t = np.ascontiguousarray(tokens, dtype=np.int32)
@@ -351,15 +373,15 @@ class Model:
         holds them (f16 bits as uint16, or f32), copied."""
         k = lib().orc_model_k_cache(self._h, layer)
         v = lib().orc_model_v_cache(self._h, layer)
-        n = self.kv_heads * self.context * self.head_dim
+        n = self.kv_heads * self.ring * self.head_dim
         t = C.c_uint16 if self.kv_f16 else C.c_float
-        shape = (self.kv_heads, self.context, self.head_dim)
+        shape = (self.kv_heads, self.ring, self.head_dim)
         return tuple(np.ctypeslib.as_array(C.cast(p, C.POINTER(t)), (n,)).reshape(shape).copy() for p in (k, v))
 
     def set_kv(self, layer: int, k, v) -> None:
         """Layer `layer`'s caches from k and v (the kv_cache layout)."""
         dt = np.uint16 if self.kv_f16 else np.float32
-        shape = (self.kv_heads, self.context, self.head_dim)
+        shape = (self.kv_heads, self.ring, self.head_dim)
         k, v = np.ascontiguousarray(k, dt), np.ascontiguousarray(v, dt)
         assert k.shape == shape and v.shape == shape, (k.shape, shape)
         if lib().orc_model_set_kv(self._h, layer, _p(k), _p(v)) != 0:

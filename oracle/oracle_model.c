@@ -165,9 +165,16 @@ struct orc_model {
     layer* layers;
     int64_t position;
     int64_t max_score_bytes; /* attention's score budget (ORC_MAX_SCORE_BYTES) */
+    /* Sliding window (every layer, 0: none): the caches are rings of
+     * min(context, window + extra rows) rows; oldest_kept is the first
+     * position the rings still hold (llama.cpp:236-241,273-285,356-364). */
+    int64_t window, ring, oldest_kept;
+    float attn_softcap, final_softcap;
 };
 
 static void weight_free(weight* w) { free(w->data); free(w->scales); }
+
+static float clamp10(float v) { return v < -10.0f ? -10.0f : (10.0f < v ? 10.0f : v); }
 
 /* weights.cpp:136-149 (quantized_named) and 128-134 (tensor_named): matrices
  * the file quantizes load quantized (q8_0/q4_0/q4_1/q4_K as they are or
@@ -239,8 +246,17 @@ void orc_model_free(orc_model* m) {
     free(m);
 }
 
-/* config.cpp:14-140 for arch "llama", then llama.cpp:170-271. */
+/* config.cpp:14-140 for arch "llama", then llama.cpp:170-271. A sliding
+ * window is read from llama.attention.sliding_window (the key the
+ * reference reads for the Gemma architectures, config.cpp:124-125), applied
+ * to every layer as the reference's HF Mistral configs do, and the soft
+ * caps from llama.attn_logit_softcapping and llama.final_logit_softcapping
+ * (config.cpp:130-131). */
 orc_model* orc_model_load(const char* path, int64_t context_length, int kv_f16, int int_dot) {
+    return orc_model_load_ex(path, context_length, kv_f16, int_dot, 1024);
+}
+
+orc_model* orc_model_load_ex(const char* path, int64_t context_length, int kv_f16, int int_dot, int64_t sliding_extra_rows) {
     gguf* g = gguf_open(path);
     if (!g) return NULL;
     const gkv* arch = gguf_kv(g, "general.architecture");
@@ -261,6 +277,9 @@ orc_model* orc_model_load(const char* path, int64_t context_length, int kv_f16, 
     m->max_pos = (int64_t)kv_num(g, "llama.context_length", 0, &f); ok &= f;
     m->eps = (float)kv_num(g, "llama.attention.layer_norm_rms_epsilon", 1e-5f, NULL);
     m->theta = (float)kv_num(g, "llama.rope.freq_base", 10000.0f, NULL);
+    m->window = (int64_t)kv_num(g, "llama.attention.sliding_window", 0, NULL);
+    m->attn_softcap = (float)kv_num(g, "llama.attn_logit_softcapping", 0.0, NULL);
+    m->final_softcap = (float)kv_num(g, "llama.final_logit_softcapping", 0.0, NULL);
     const gtensor* te = gguf_tensor(g, "token_embd.weight");
     if (!ok || !te) { orc_error("Llama: %s lacks config keys", path, 0, 0); gguf_free(g); free(m); return NULL; }
     m->vocab = te->shape[0];
@@ -273,6 +292,8 @@ orc_model* orc_model_load(const char* path, int64_t context_length, int kv_f16, 
         gguf_free(g); free(m); return NULL;
     }
     const int64_t d = m->d, qd = m->heads * m->hd, kvd = m->kv_heads * m->hd;
+    m->ring = m->window ? (context_length < m->window + sliding_extra_rows ? context_length : m->window + sliding_extra_rows)
+                        : context_length;
     m->layers = (layer*)calloc((size_t)m->n_layers, sizeof(layer));
     int err = load_matrix(g, "token_embd.weight", m->vocab, d, &m->embed);
     if (!err) {
@@ -299,8 +320,8 @@ orc_model* orc_model_load(const char* path, int64_t context_length, int kv_f16, 
         MAT(up, "ffn_up.weight", m->ff, d)
         MAT(down, "ffn_down.weight", d, m->ff)
 #undef MAT
-        L->k_cache = calloc((size_t)(m->kv_heads * context_length * m->hd), esz);
-        L->v_cache = calloc((size_t)(m->kv_heads * context_length * m->hd), esz);
+        L->k_cache = calloc((size_t)(m->kv_heads * m->ring * m->hd), esz);
+        L->v_cache = calloc((size_t)(m->kv_heads * m->ring * m->hd), esz);
     }
     gguf_free(g);
     if (err) { m->n_layers = 0; orc_model_free(m); return NULL; }
@@ -322,20 +343,25 @@ void orc_model_dims(const orc_model* m, int64_t out[8]) {
     const int64_t d[8] = {m->vocab, m->d, m->ff, m->n_layers, m->heads, m->kv_heads, m->hd, m->context};
     memcpy(out, d, sizeof d);
 }
-void orc_model_reset(orc_model* m) { m->position = 0; }
+void orc_model_reset(orc_model* m) { m->position = 0; m->oldest_kept = 0; }
 int64_t orc_model_rewind(orc_model* m, int64_t position) {
     if (position < 0 || position > m->position) {
         orc_error("Llama::rewind: cannot rewind to position %s%lld of a sequence at %lld", "",
                   (long long)position, (long long)m->position);
         return -1;
     }
+    /* the window of position's query must still be in the rings */
+    const int64_t window = m->window ? m->window : 1;
+    if ((position - window + 1 > 0 ? position - window + 1 : 0) < m->oldest_kept) position = 0;
+    if (position == 0) m->oldest_kept = 0;
     m->position = position;
     return position;
 }
+int64_t orc_model_ring(const orc_model* m) { return m->ring; }
 const void* orc_model_k_cache(const orc_model* m, int l) { return m->layers[l].k_cache; }
 int orc_model_set_kv(orc_model* m, int l, const void* k, const void* v) {
     if (l < 0 || l >= m->n_layers || !k || !v) return -1;
-    const size_t bytes = (size_t)(m->kv_heads * m->context * m->hd) * (m->kv_f16 ? 2 : 4);
+    const size_t bytes = (size_t)(m->kv_heads * m->ring * m->hd) * (m->kv_f16 ? 2 : 4);
     memcpy(m->layers[l].k_cache, k, bytes);
     memcpy(m->layers[l].v_cache, v, bytes);
     return 0;
@@ -425,6 +451,33 @@ static int model_run(orc_model* m, const int32_t* tokens, int64_t t, int all, fl
             for (int64_t hh = 0; hh < H; ++hh)
                 memcpy(qh + (hh * t + i) * hd, tmp + (i * H + hh) * hd, (size_t)hd * 4);
         orc_rope(k, m->rope, t * KVH, KVH, t, hd, hd / 2, m->position, 0, tmp);
+        if (m->window) {
+            /* heads-first k and v in the cache type, appended to the rings
+             * chunk by chunk by sliding_attention (llama.cpp:356-364). */
+            const size_t esz = m->kv_f16 ? 2 : 4;
+            char* kh_rows = (char*)malloc((size_t)(t * kvd) * esz);
+            char* vh_rows = (char*)malloc((size_t)(t * kvd) * esz);
+            for (int64_t i = 0; i < t; ++i)
+                for (int64_t kh = 0; kh < KVH; ++kh)
+                    for (int64_t c = 0; c < hd; ++c) {
+                        const float kv_k = tmp[(i * KVH + kh) * hd + c], kv_v = v[(i * KVH + kh) * hd + c];
+                        const int64_t at = (kh * t + i) * hd + c;
+                        if (m->kv_f16) {
+                            ((uint16_t*)kh_rows)[at] = orc_f32_to_f16(kv_k);
+                            ((uint16_t*)vh_rows)[at] = orc_f32_to_f16(kv_v);
+                        } else {
+                            ((float*)kh_rows)[at] = kv_k;
+                            ((float*)vh_rows)[at] = kv_v;
+                        }
+                    }
+            if (end - m->ring > m->oldest_kept) m->oldest_kept = end - m->ring;
+            orc_attention_sliding(qh, H, t, kh_rows, vh_rows, L->k_cache, L->v_cache, m->kv_f16, KVH, m->ring, hd,
+                                  m->position, m->window < m->ring ? m->window : m->ring, m->max_score_bytes,
+                                  m->attn_softcap, att);
+            free(kh_rows);
+            free(vh_rows);
+            goto attended;
+        }
         /* cast to the cache type and write_rows at position (llama.cpp:344-355). */
         for (int64_t i = 0; i < t; ++i) {
             for (int64_t kh = 0; kh < KVH; ++kh) {
@@ -443,9 +496,10 @@ static int model_run(orc_model* m, const int32_t* tokens, int64_t t, int all, fl
         }
         /* detail::attention (attention.cpp:167-227): the fused decode kernel
          * for one query, attention_block otherwise. */
-        if (t == 1) orc_attend_decode(qh, H, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, 0, end, 0.0f, att);
+        if (t == 1) orc_attend_decode(qh, H, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, 0, end, m->attn_softcap, att);
         else orc_attention_prefill(qh, H, t, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, end,
-                                   m->max_score_bytes, att);
+                                   m->max_score_bytes, m->attn_softcap, att);
+    attended:
         for (int64_t i = 0; i < t; ++i)
             for (int64_t hh = 0; hh < H; ++hh)
                 memcpy(merged + (i * H + hh) * hd, att + (hh * t + i) * hd, (size_t)hd * 4);
@@ -477,6 +531,11 @@ static int model_run(orc_model* m, const int32_t* tokens, int64_t t, int all, fl
         project(m, h, 1, &al, &m->lm_head, logits);
     }
     act_free(&al);
+    /* the final soft cap (llama.cpp:405, unary.comp:35) */
+    if (m->final_softcap > 0.0f) {
+        const float cap = m->final_softcap;
+        for (int64_t i = 0; i < (all ? t : 1) * m->vocab; ++i) logits[i] = cap * tanhf(clamp10(logits[i] / cap));
+    }
     free(x); free(h); free(q); free(k); free(v); free(tmp); free(qh); free(att); free(merged);
     free(y); free(gate); free(up);
     return 0;

@@ -1016,7 +1016,7 @@ void orc_attend_decode(const float* q, int64_t heads, const void* k, const void*
  * softmax.comp's causal rows (max; sum of exp in the shader's 256-wide
  * order; times 1/sum); then probs v in key order (matmul.comp). */
 static void prefill_block(const float* q, int64_t q_len, int64_t q0, int64_t rows, int64_t h, const void* k,
-                          const void* v, int f16, int64_t hd, int64_t keys, int64_t kv_row0, float* s,
+                          const void* v, int f16, int64_t hd, int64_t keys, int64_t kv_row0, float softcap, float* s,
                           float* kf, float* vf, float* out) {
     const float scale = 1.0f / sqrtf((float)hd);
     const float* qh = q + (h * q_len + q0) * hd;
@@ -1039,14 +1039,18 @@ static void prefill_block(const float* q, int64_t q_len, int64_t q0, int64_t row
         float* si = s + i * keys;
         const int64_t position = i + keys - rows;
         const int64_t visible = position + 1 < keys ? position + 1 : keys;
+        for (int64_t j = 0; j < visible; ++j) {
+            const float sc = si[j] * scale;
+            si[j] = softcap > 0.0f ? softcap * tanhf(clampf(sc / softcap, -10.0f, 10.0f)) : sc;
+        }
         float m = -INFINITY;
-        for (int64_t j = 0; j < visible; ++j) m = fmaxf(m, si[j] * scale);
+        for (int64_t j = 0; j < visible; ++j) m = fmaxf(m, si[j]);
         /* softmax.comp:104-108: invocation t of 256 sums keys t, t+256, ..;
          * then the halving tree over the 256 partial sums. */
         float part[256];
         for (int64_t t = 0; t < 256; ++t) {
             float acc = 0.0f;
-            for (int64_t j = t; j < visible; j += 256) acc += orc_expf(si[j] * scale - m);
+            for (int64_t j = t; j < visible; j += 256) acc += orc_expf(si[j] - m);
             part[t] = acc;
         }
         for (int64_t n = 256; n > 1;) {
@@ -1055,7 +1059,7 @@ static void prefill_block(const float* q, int64_t q_len, int64_t q0, int64_t row
             n = half;
         }
         const float inv = 1.0f / part[0];
-        for (int64_t j = 0; j < keys; ++j) si[j] = j < visible ? orc_expf(si[j] * scale - m) * inv : 0.0f;
+        for (int64_t j = 0; j < keys; ++j) si[j] = j < visible ? orc_expf(si[j] - m) * inv : 0.0f;
         for (int64_t c = 0; c < hd; ++c) {
             float acc = 0.0f;
             for (int64_t j = 0; j < keys; ++j) acc += si[j] * vf[j * hd + c];
@@ -1066,7 +1070,7 @@ static void prefill_block(const float* q, int64_t q_len, int64_t q0, int64_t row
 
 typedef struct {
     const float* q; int64_t q_len, q0, rows; const void* k; const void* v; int f16;
-    int64_t hd, keys, group, capacity; float* out;
+    int64_t hd, keys, group, capacity; float softcap; float* out;
 } prefill_ctx;
 
 /* Heads h0 .. h1 of one query chunk, each with buffers of its own. */
@@ -1077,7 +1081,7 @@ static void prefill_heads(void* p, int64_t h0, int64_t h1) {
     float* vf = (float*)malloc(sizeof(float) * (size_t)(c->keys * c->hd + 1));
     for (int64_t h = h0; h < h1; ++h)
         prefill_block(c->q, c->q_len, c->q0, c->rows, h, c->k, c->v, c->f16, c->hd, c->keys, (h / c->group) * c->capacity,
-                      s, kf, vf, c->out);
+                      c->softcap, s, kf, vf, c->out);
     free(s); free(kf); free(vf);
 }
 
@@ -1086,7 +1090,7 @@ static void prefill_heads(void* p, int64_t h0, int64_t h1) {
  * 64 rows when at least 64), each chunk over the keys its last query sees. */
 void orc_attention_prefill(const float* q, int64_t heads, int64_t q_len, const void* k,
                            const void* v, int f16, int64_t kv_heads, int64_t capacity, int64_t hd,
-                           int64_t kv_len, int64_t max_score_bytes, float* out) {
+                           int64_t kv_len, int64_t max_score_bytes, float softcap, float* out) {
     const int64_t group = heads / kv_heads;
     const int64_t row_bytes = heads * (kv_len > 1 ? kv_len : 1) * 4;
     int64_t chunk = max_score_bytes / row_bytes;
@@ -1097,7 +1101,121 @@ void orc_attention_prefill(const float* q, int64_t heads, int64_t q_len, const v
     for (int64_t q0 = 0; q0 < q_len; q0 += chunk) {
         const int64_t rows = chunk < q_len - q0 ? chunk : q_len - q0;
         const int64_t keys = q_len <= chunk ? kv_len : first_position + q0 + rows;
-        prefill_ctx c = {q, q_len, q0, rows, k, v, f16, hd, keys, group, capacity, out};
+        prefill_ctx c = {q, q_len, q0, rows, k, v, f16, hd, keys, group, capacity, softcap, out};
         parallel_for(heads, prefill_heads, &c);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Sliding-window attention over a ring: detail::sliding_attention            */
+/* (attention.cpp:229-294) with attention_block's ring mask (:127-138,         */
+/* softmax.comp:85-124 with CausalMask::ring).                                 */
+/* ------------------------------------------------------------------------ */
+
+/* attention_block over a ring of kv_len columns (rows 0 .. kv_len of the
+ * caches), queries at positions first .. first + rows, each seeing the
+ * last `window` positions up to its own, position p in column p % ring. */
+static void ring_block(const float* q, int64_t heads, int64_t rows, const void* k, const void* v, int f16,
+                       int64_t kv_heads, int64_t ring, int64_t hd, int64_t kv_len, int64_t first, int64_t window,
+                       float softcap, float* out) {
+    const int64_t group = heads / kv_heads;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* s = (float*)malloc(sizeof(float) * (size_t)(rows * kv_len));
+    float* kf = (float*)malloc(sizeof(float) * (size_t)(kv_len * hd));
+    float* vf = (float*)malloc(sizeof(float) * (size_t)(kv_len * hd));
+    for (int64_t h = 0; h < heads; ++h) {
+        const int64_t kv_row0 = (h / group) * ring;
+        for (int64_t e = 0; e < kv_len * hd; ++e) {
+            kf[e] = kv_at(k, f16, kv_row0 * hd + e);
+            vf[e] = kv_at(v, f16, kv_row0 * hd + e);
+        }
+        const float* qh = q + h * rows * hd;
+        /* scores: gemv.comp's order for up to 8 rows, matmul.comp's beyond */
+        if (rows <= 8) {
+            orc_gemv_float(ORC_T_F32, 0, qh, rows, kf, NULL, kv_len, hd, s);
+        } else {
+            for (int64_t i = 0; i < rows; ++i)
+                for (int64_t j = 0; j < kv_len; ++j) {
+                    float acc = 0.0f;
+                    for (int64_t c = 0; c < hd; ++c) acc += qh[i * hd + c] * kf[j * hd + c];
+                    s[i * kv_len + j] = acc;
+                }
+        }
+        for (int64_t i = 0; i < rows; ++i) {
+            float* si = s + i * kv_len;
+            const int64_t visible = first + i + 1;
+            const int64_t lo = window != 0 && visible > window ? visible - window : 0;
+#define SCORE(col) (softcap > 0.0f ? softcap * tanhf(clampf(si[(col)] * scale / softcap, -10.0f, 10.0f)) : si[(col)] * scale)
+            float m = -INFINITY;
+            for (int64_t c = lo; c < visible; ++c) m = fmaxf(m, SCORE(c % ring));
+            float part[256];
+            for (int64_t t = 0; t < 256; ++t) {
+                float acc = 0.0f;
+                for (int64_t c = lo + t; c < visible; c += 256) acc += orc_expf(SCORE(c % ring) - m);
+                part[t] = acc;
+            }
+            for (int64_t n = 256; n > 1;) {
+                const int64_t half = (n + 1) / 2;
+                for (int64_t t = 0; t < n - half; ++t) part[t] += part[t + half];
+                n = half;
+            }
+            const float inv = 1.0f / part[0];
+            const int64_t first_col = lo % ring;
+            float* pr = (float*)malloc(sizeof(float) * (size_t)kv_len);
+            for (int64_t c = 0; c < kv_len; ++c) {
+                const int64_t from_first = c >= first_col ? c - first_col : c + ring - first_col;
+                pr[c] = from_first < visible - lo ? orc_expf(SCORE(c) - m) * inv : 0.0f;
+            }
+#undef SCORE
+            /* probs . v in key (column) order */
+            for (int64_t c = 0; c < hd; ++c) {
+                float acc = 0.0f;
+                for (int64_t j = 0; j < kv_len; ++j) acc += pr[j] * vf[j * hd + c];
+                out[(h * rows + i) * hd + c] = acc;
+            }
+            free(pr);
+        }
+    }
+    free(s); free(kf); free(vf);
+}
+
+static void ring_append(const void* src, int64_t src_rows, int64_t row0, void* ring_cache, int64_t ring,
+                        int64_t kv_heads, int64_t hd, int f16, int64_t from, int64_t rows) {
+    const size_t esz = f16 ? 2 : 4;
+    for (int64_t kh = 0; kh < kv_heads; ++kh)
+        for (int64_t r = 0; r < rows; ++r)
+            memcpy((char*)ring_cache + (size_t)((kh * ring + (from + r) % ring) * hd) * esz,
+                   (const char*)src + (size_t)((kh * src_rows + row0 + r) * hd) * esz, (size_t)hd * esz);
+}
+
+void orc_attention_sliding(const float* q, int64_t heads, int64_t t, const void* k, const void* v, void* k_ring,
+                           void* v_ring, int f16, int64_t kv_heads, int64_t ring, int64_t hd, int64_t start,
+                           int64_t window, int64_t max_score_bytes, float softcap, float* out) {
+    for (int64_t q0 = 0; q0 < t;) {
+        const int64_t first = start + q0;
+        const int64_t unwrapped = ring - first;
+        int64_t chunk = ring - window + 1 > unwrapped ? ring - window + 1 : unwrapped;
+        const int64_t keys = first + chunk < ring ? first + chunk : ring;
+        int64_t budget = max_score_bytes / (heads * keys * 4);
+        if (budget < 1) budget = 1;
+        if (chunk > budget) chunk = budget;
+        if (chunk >= 64) chunk -= chunk % 64;
+        const int64_t rows = chunk < t - q0 ? chunk : t - q0;
+        const int64_t end = first + rows;
+        ring_append(k, t, q0, k_ring, ring, kv_heads, hd, f16, first, rows);
+        ring_append(v, t, q0, v_ring, ring, kv_heads, hd, f16, first, rows);
+        float* block = (float*)malloc(sizeof(float) * (size_t)(heads * rows * hd));
+        float* qc = (float*)malloc(sizeof(float) * (size_t)(heads * rows * hd));
+        for (int64_t h = 0; h < heads; ++h) memcpy(qc + h * rows * hd, q + (h * t + q0) * hd, sizeof(float) * (size_t)(rows * hd));
+        if (rows == 1) {
+            orc_attend_decode(qc, heads, k_ring, v_ring, f16, kv_heads, ring, hd, end - window > 0 ? end - window : 0, end,
+                              softcap, block);
+        } else {
+            ring_block(qc, heads, rows, k_ring, v_ring, f16, kv_heads, ring, hd, end < ring ? end : ring, first, window,
+                       softcap, block);
+        }
+        for (int64_t h = 0; h < heads; ++h) memcpy(out + (h * t + q0) * hd, block + h * rows * hd, sizeof(float) * (size_t)(rows * hd));
+        free(block); free(qc);
+        q0 += rows;
     }
 }

@@ -122,7 +122,15 @@ void orc_attend_decode(const float* q, int64_t heads, const void* k, const void*
                        int64_t kv_len, float softcap, float* out);
 void orc_attention_prefill(const float* q, int64_t heads, int64_t q_len, const void* k,
                            const void* v, int kv_f16, int64_t kv_heads, int64_t capacity,
-                           int64_t hd, int64_t kv_len, int64_t max_score_bytes, float* out);
+                           int64_t hd, int64_t kv_len, int64_t max_score_bytes, float softcap, float* out);
+/* detail::sliding_attention (attention.cpp:229-294): queries q [heads, t, hd]
+ * at positions start.., their keys and values k, v [kv_heads, t, hd] (in the
+ * caches' type) appended chunk by chunk to rings [kv_heads, ring, hd]
+ * (position p in row p % ring), each query seeing the last `window`
+ * positions up to its own; out [heads, t, hd]. */
+void orc_attention_sliding(const float* q, int64_t heads, int64_t t, const void* k, const void* v, void* k_ring,
+                           void* v_ring, int f16, int64_t kv_heads, int64_t ring, int64_t hd, int64_t start,
+                           int64_t window, int64_t max_score_bytes, float softcap, float* out);
 /* The reference's score budget per attention call (ops/internal.hpp:92). */
 #define ORC_MAX_SCORE_BYTES ((int64_t)64 << 20)
 
@@ -131,6 +139,12 @@ void orc_attention_prefill(const float* q, int64_t heads, int64_t q_len, const v
  * matmul_dot), 0 multiplies them in f32 (gemv.comp). */
 typedef struct orc_model orc_model;
 orc_model* orc_model_load(const char* gguf_path, int64_t context_length, int kv_f16, int int_dot);
+/* The same with LlamaOptions::sliding_extra_rows (llama.hpp:133 there): a
+ * sliding window's rings hold window + that many rows (at most the context). */
+orc_model* orc_model_load_ex(const char* gguf_path, int64_t context_length, int kv_f16, int int_dot,
+                             int64_t sliding_extra_rows);
+/* Rows of each layer's caches (the ring's with a sliding window). */
+int64_t orc_model_ring(const orc_model* m);
 void orc_model_free(orc_model* m);
 /* Runs t tokens after those processed; logits of the last token -> logits[vocab].
  * Returns 0, or -1 with orc_last_error set (llama.cpp:300-305 errors). */

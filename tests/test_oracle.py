@@ -556,3 +556,55 @@ def test_model_int8_path_tracks_the_double_reference(tiny_q4k):
     with pytest.raises(RuntimeError, match="rewind"):
         m2.rewind(17)
     assert m2.rewind(3) == 3
+
+
+# ---------------------------------------------------------------- sliding window
+
+def _windowed_f64(q, k, v, first, window, softcap):
+    """float64 causal attention of queries at positions first.. over keys
+    0..first + rows, each seeing the last `window` positions."""
+    heads, rows, hd = q.shape
+    group = heads // k.shape[0]
+    out = np.zeros((heads, rows, hd))
+    for h in range(heads):
+        for i in range(rows):
+            pos = first + i
+            lo = max(0, pos + 1 - window)
+            s = k[h // group, lo:pos + 1].astype(np.float64) @ q[h, i].astype(np.float64) / np.sqrt(hd)
+            if softcap:
+                s = softcap * np.tanh(np.clip(s / softcap, -10, 10))
+            w = np.exp(s - s.max())
+            out[h, i] = (w / w.sum()) @ v[h // group, lo:pos + 1].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("hd", [16, 132, 260])
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("softcap", [0.0, 0.5])
+def test_sliding_attention_over_a_ring_equals_it_over_the_whole_cache(hd, f16, softcap):
+    """tests/test_kv_cache.cpp:215-266 of the reference, restated on the
+    oracle: a window of 5 keys in a ring of 8 rows poisoned with NaN, 31
+    positions fed in steps of every kind, against float64 attention over
+    the whole cache (the reference's bound, 1e-5 (1 + |want|))."""
+    heads, kv_heads, total, window, ring = 4, 2, 31, 5, 8
+    steps = [7, 1, 1, 1, 3, 10, 1, 2, 4, 1]
+    rng = np.random.default_rng(71 + hd)
+    q = rng.standard_normal((heads, total, hd)).astype(np.float32)
+    k = rng.standard_normal((kv_heads, total, hd)).astype(np.float32)
+    v = rng.standard_normal((kv_heads, total, hd)).astype(np.float32)
+    if f16:
+        kc, vc = k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16)
+        kw, vw = kc.view(np.float16).astype(np.float32), vc.view(np.float16).astype(np.float32)
+        k_ring = np.full((kv_heads, ring, hd), 0x7E00, np.uint16)
+    else:
+        kc, vc, kw, vw = k, v, k, v
+        k_ring = np.full((kv_heads, ring, hd), np.nan, np.float32)
+    v_ring = k_ring.copy()
+    start = 0
+    for n in steps:
+        got = O.attention_sliding(q[:, start:start + n], kc[:, start:start + n], vc[:, start:start + n], k_ring, v_ring, start,
+                                  window, softcap)
+        want = _windowed_f64(q[:, start:start + n], kw, vw, start, window, softcap)
+        assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want))), (start, n)
+        start += n
+    assert start == total

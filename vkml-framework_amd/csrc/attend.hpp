@@ -48,6 +48,8 @@ struct ChunkArgs {
     // When non-null: the sync words of the merge + o launch that follows
     // (OSync), whose counter and flags workgroup 0 zeroes.
     uint32_t* o_sync;
+    // A sliding window (0: none): keys from max(kv_start, kv_len - window).
+    uint32_t window;
 };
 
 // Sync words of the launch that merges the chunks and runs the o GEMV on

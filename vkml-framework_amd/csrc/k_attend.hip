@@ -48,6 +48,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_chunk(ChunkArgs a) {
     const uint32_t chunk = pair / a.kv_heads, kvh = pair % a.kv_heads, head0 = kvh * G + hl * HPW;
     const uint32_t pos = a.step ? (a.state ? static_cast<uint32_t>(a.state->position) : a.position) : 0u;
     const uint32_t kv_len = a.step ? pos + 1 : (a.state ? static_cast<uint32_t>(a.state->position) + 1u : a.kv_len);
+    if (a.window != 0 && kv_len > a.window) a.kv_start = max(a.kv_start, kv_len - a.window);
     if (a.kv_start + chunk * kChunk >= kv_len) {
         // A chunk past the live keys (the grid covers the whole cache, so a
         // replayed graph serves every position): a max of -inf, which the
@@ -229,9 +230,12 @@ int vkml_attend(const vkml_attend_params* p, const float* q, const void* k_cache
     VKML_CHECK_ARG(p, "attend: null params");
     if (int r = check_heads(p->heads, p->kv_heads, p->head_dim, "attend")) return r;
     VKML_CHECK_ARG(p->kv_type == VKML_F16 || p->kv_type == VKML_F32, "attend: caches must be f16 or f32");
-    VKML_CHECK_ARG(p->chunks > 0 && p->capacity > 0 && p->kv_start < p->capacity, "attend: chunks and capacity must be positive, kv_start inside the cache");
-    VKML_CHECK_ARG(state || (p->kv_len <= p->capacity && p->kv_start < p->kv_len),
-                   "attend: keys " + std::to_string(p->kv_start) + ".." + std::to_string(p->kv_len) + " do not fit the cache");
+    VKML_CHECK_ARG(p->chunks > 0 && p->capacity > 0, "attend: chunks and capacity must be positive");
+    // Key position p sits at row p % capacity (a ring, when positions pass
+    // the capacity): the keys seen must fit the rows.
+    VKML_CHECK_ARG(state ? p->kv_start < p->capacity : p->kv_start < p->kv_len && p->kv_len - p->kv_start <= p->capacity,
+                   "attend: keys " + std::to_string(p->kv_start) + ".." + std::to_string(p->kv_len) + " do not fit the cache of " +
+                       std::to_string(p->capacity) + " rows");
     // With a decode state, kv_len can reach the capacity: cover every chunk of it.
     const uint64_t keys = state ? p->capacity - p->kv_start : p->kv_len - p->kv_start;
     VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= keys,
@@ -240,7 +244,7 @@ int vkml_attend(const vkml_attend_params* p, const float* q, const void* k_cache
     VKML_CHECK_ARG(q && k_cache && v_cache && partial && stats, "attend: null buffer");
     ChunkArgs args{q, nullptr, const_cast<void*>(k_cache), const_cast<void*>(v_cache), partial, stats, state,
                    p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity, p->kv_start, p->kv_len, 0, p->chunks,
-                   0, 0, 0, p->scale, p->softcap, nullptr};
+                   0, 0, 0, p->scale, p->softcap, nullptr, 0};
     vkml::abi::ProfileScope prof("attend");
     launch_chunks(p->head_dim, p->kv_type == VKML_F16, args);
     return vkml::abi::check_launch("attend");
@@ -275,8 +279,9 @@ int check_step(const vkml_attend_step_params* p, const float* qkv, const float* 
     VKML_CHECK_ARG(p->capacity > 0 && p->kv_start < p->capacity, w + ": kv_start must lie inside the cache");
     VKML_CHECK_ARG(state || (p->position < p->capacity && p->kv_start <= p->position),
                    w + ": position " + std::to_string(p->position) + " is outside the cache");
-    VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= p->capacity - p->kv_start && p->chunks <= kMergeMaxChunks,
-                   w + ": " + std::to_string(p->chunks) + " chunks do not cover the cache (or exceed " +
+    const uint64_t span = p->window ? std::min<uint64_t>(p->window, p->capacity - p->kv_start) : p->capacity - p->kv_start;
+    VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= span && p->chunks <= kMergeMaxChunks,
+                   w + ": " + std::to_string(p->chunks) + " chunks do not cover the " + std::to_string(span) + " keys a step can see (or exceed " +
                        std::to_string(kMergeMaxChunks) + ")");
     VKML_CHECK_ARG(qkv && rope_table && k_cache && v_cache && partial && stats && out, w + ": null buffer");
     VKML_CHECK_ARG(!values || scales, w + ": quantized output needs scales");
@@ -286,7 +291,8 @@ int check_step(const vkml_attend_step_params* p, const float* qkv, const float* 
 ChunkArgs step_args(const vkml_attend_step_params* p, const float* qkv, const float* rope_table, void* k_cache, void* v_cache,
                     float* partial, float* stats, const vkml_decode_state* state, uint32_t* o_sync) {
     return ChunkArgs{qkv, rope_table, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads,
-                     p->capacity, p->kv_start, 0, p->position, p->chunks, 1, p->rope_style, p->rotate, p->scale, p->softcap, o_sync};
+                     p->capacity, p->kv_start, 0, p->position, p->chunks, 1, p->rope_style, p->rotate, p->scale, p->softcap, o_sync,
+                     p->window};
 }
 
 }  // namespace

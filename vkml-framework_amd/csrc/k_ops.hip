@@ -234,32 +234,41 @@ __global__ void __launch_bounds__(kRowThreads) k_rms_norm_quantize(vkml_rms_norm
     }
 }
 
-// shaders/softmax.comp:85-124 (no ring: causal rows see keys offset + row %
-// q_len and before), with its order: strided per-invocation max and sum of
-// exp over 256 invocations, the halving tree, then exp(score - m) * (1 / s).
+// shaders/softmax.comp:85-124, with its order: strided per-invocation max
+// and sum of exp over 256 invocations (over key positions first .. visible,
+// column p % ring for a ring), the halving tree, then exp(score - m) *
+// (1 / s) in each visible column and 0 elsewhere.
 __global__ void __launch_bounds__(kRowThreads) k_softmax(vkml_softmax_params p, const float* x, float* out) {
     __shared__ float scratch[kRowThreads + 1];
     __shared__ float s_max[16];
+    const bool ring = p.causal && p.ring != 0;
     for (uint32_t row = blockIdx.x; row < p.rows; row += gridDim.x) {
         const float* xr = x + static_cast<uint64_t>(row) * p.cols;
         uint32_t visible = p.cols, first = 0;
         if (p.causal) {
-            visible = min(p.cols, row % p.q_len + p.offset + 1);
+            visible = row % p.q_len + p.offset + 1;
+            if (!ring) visible = min(p.cols, visible);
             if (p.window != 0 && visible > p.window) first = visible - p.window;
         }
-        const auto score = [&](uint32_t c) {
+        const auto col = [&](uint32_t c) { return ring ? c % p.ring : c; };
+        const auto score = [&](uint32_t c) {  // c: a column
             const float s = p.scale * xr[c];
             return p.softcap > 0.0f ? p.softcap * tanhf(fminf(fmaxf(s / p.softcap, -10.0f), 10.0f)) : s;
         };
         float m = -__builtin_inff();
-        for (uint32_t c = first + threadIdx.x; c < visible; c += kRowThreads) m = fmaxf(m, score(c));
+        for (uint32_t c = first + threadIdx.x; c < visible; c += kRowThreads) m = fmaxf(m, score(col(c)));
         m = block_max(m, s_max);
         float s = 0.0f;
-        for (uint32_t c = first + threadIdx.x; c < visible; c += kRowThreads) s += vk_expf(score(c) - m);
+        for (uint32_t c = first + threadIdx.x; c < visible; c += kRowThreads) s += vk_expf(score(col(c)) - m);
         s = tree256_sum(s, scratch);
         const float inv = 1.0f / s;
-        for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads)
-            out[static_cast<uint64_t>(row) * p.cols + c] = (c >= first && c < visible) ? vk_expf(score(c) - m) * inv : 0.0f;
+        // column c holds a visible key if it lies within visible - first
+        // columns of first's, going round the ring
+        const uint32_t first_col = col(first);
+        for (uint32_t c = threadIdx.x; c < p.cols; c += kRowThreads) {
+            const bool seen = ring ? (c >= first_col ? c - first_col : c + p.ring - first_col) < visible - first : (c >= first && c < visible);
+            out[static_cast<uint64_t>(row) * p.cols + c] = seen ? vk_expf(score(c) - m) * inv : 0.0f;
+        }
         __syncthreads();
     }
 }
@@ -769,11 +778,13 @@ int vkml_softmax(const vkml_softmax_params* p, const float* x, float* out) {
     VKML_REQUIRE_INIT();
     VKML_CHECK_ARG(p, "softmax: null params");
     VKML_CHECK_ARG(!p->causal || p->q_len > 0, "softmax: causal rows need q_len");
+    VKML_CHECK_ARG(!p->ring || (p->causal && p->cols <= p->ring), "softmax: a ring needs the causal mask and at most ring columns");
     if (p->rows == 0 || p->cols == 0) return VKML_OK;
     VKML_CHECK_ARG(x && out, "softmax: null buffer");
     ProfileScope prof("softmax");
     const dim3 grid(std::min<uint32_t>(p->rows, 65535)), block(kRowThreads);
-    if (p->cols <= kRowThreads * 4) hipLaunchKernelGGL(k_softmax_held<4>, grid, block, 0, S(), *p, x, out);
+    if (p->ring) hipLaunchKernelGGL(k_softmax, grid, block, 0, S(), *p, x, out);
+    else if (p->cols <= kRowThreads * 4) hipLaunchKernelGGL(k_softmax_held<4>, grid, block, 0, S(), *p, x, out);
     else if (p->cols <= kRowThreads * 8) hipLaunchKernelGGL(k_softmax_held<8>, grid, block, 0, S(), *p, x, out);
     else if (p->cols <= kRowThreads * 16) hipLaunchKernelGGL(k_softmax_held<16>, grid, block, 0, S(), *p, x, out);
     else hipLaunchKernelGGL(k_softmax, grid, block, 0, S(), *p, x, out);
@@ -824,8 +835,8 @@ int vkml_rope_kv_prompt(const vkml_rope_kv_params* p, uint32_t tokens, uint32_t 
                    "rope_kv_prompt: bad head layout");
     VKML_CHECK_ARG(p->kv_type == VKML_F16 || p->kv_type == VKML_F32, "rope_kv_prompt: caches must be f16 or f32");
     VKML_CHECK_ARG(row_stride >= (p->heads + 2 * p->kv_heads) * p->head_dim, "rope_kv_prompt: rows overlap");
-    VKML_CHECK_ARG(static_cast<uint64_t>(p->position) + tokens <= p->capacity,
-                   "rope_kv_prompt: positions " + std::to_string(p->position) + ".." + std::to_string(p->position + tokens) +
+    VKML_CHECK_ARG(tokens <= p->capacity,
+                   "rope_kv_prompt: " + std::to_string(tokens) + " tokens from position " + std::to_string(p->position) +
                        " do not fit a cache of " + std::to_string(p->capacity) + " rows");
     if (tokens == 0) return VKML_OK;
     VKML_CHECK_ARG(qkv && q && k_cache && v_cache && (table || !p->rotate), "rope_kv_prompt: null buffer");

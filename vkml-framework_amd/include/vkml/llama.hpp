@@ -67,7 +67,9 @@ struct LlamaOptions {
     std::optional<QuantType> quantize;
     // The KV cache's element type: f32 (the reference's default) or f16.
     DType kv_cache = DType::F32;
-    // Kept for source compatibility (sliding-window rings are not built here).
+    // A sliding window's caches are rings of window + this many rows (at
+    // most the context), so that a prompt's keys append in large pieces and
+    // rewinding that far keeps the window (reference: llama.hpp:133).
     std::int64_t sliding_extra_rows = 1024;
     // Replay each decode step as a captured HIP graph.
     bool use_graphs = true;

@@ -47,7 +47,8 @@ MatmulParams = _struct("MatmulParams", [("m", u32), ("n", u32), ("k", u32), ("b_
                                         ("causal", u32), ("causal_offset", u32)])
 RmsNormParams = _struct("RmsNormParams", [("rows", u32), ("cols", u32), ("eps", f32)])
 SoftmaxParams = _struct("SoftmaxParams", [("rows", u32), ("cols", u32), ("scale", f32), ("causal", u32),
-                                          ("q_len", u32), ("offset", u32), ("window", u32), ("softcap", f32)])
+                                          ("q_len", u32), ("offset", u32), ("window", u32), ("softcap", f32),
+                                          ("ring", u32)])
 RopeParams = _struct("RopeParams", [("pairs", u32), ("half_dim", u32), ("dim", u32), ("heads", u32), ("seq", u32),
                                     ("start_pos", u32), ("copies", u32), ("style", u32)])
 CopyRowsParams = _struct("CopyRowsParams", [("count", u32), ("block", u32), ("src_stride", u32), ("src_start", u32),
@@ -65,7 +66,8 @@ GemvFusedParams = _struct("GemvFusedParams", [("n", u32), ("k", u32), ("b_type",
                                               ("epilogue", u32), ("norm", u32), ("eps", f32), ("quantize_out", u32)])
 AttendStepParams = _struct("AttendStepParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
                                                 ("kv_start", u32), ("position", u32), ("kv_type", u32), ("chunks", u32),
-                                                ("rope_style", u32), ("rotate", u32), ("scale", f32), ("softcap", f32)])
+                                                ("rope_style", u32), ("rotate", u32), ("scale", f32), ("softcap", f32),
+                                                ("window", u32)])
 
 P = C.POINTER
 # name -> argtypes (all return int status unless noted)

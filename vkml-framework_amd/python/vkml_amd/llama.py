@@ -16,7 +16,7 @@ i32, i64, u32, u64, vp = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_void_
 
 class Options(C.Structure):
     _fields_ = [("kv_cache_f16", i32), ("quantize", i32), ("integer_dot", i32), ("use_graphs", i32),
-                ("device_name", C.c_char_p), ("prompt_score_bytes", i64)]
+                ("device_name", C.c_char_p), ("prompt_score_bytes", i64), ("sliding_extra_rows", i64)]
 
 
 class SamplingOptions(C.Structure):
@@ -94,13 +94,15 @@ def _ptr(a: np.ndarray):
 
 class Llama:
     def __init__(self, path: str, context: int, kv_f16: bool = False, quantize: int = -1, integer_dot: bool = True,
-                 use_graphs: bool = True, prompt_score_bytes: int = 0):
+                 use_graphs: bool = True, prompt_score_bytes: int = 0, sliding_extra_rows: int = -1):
         o = Options()
         lib().vkml_llama_default_options(C.byref(o))
         o.kv_cache_f16, o.quantize, o.integer_dot = int(kv_f16), int(quantize), int(integer_dot)
         o.use_graphs = int(use_graphs)
         if prompt_score_bytes:
             o.prompt_score_bytes = int(prompt_score_bytes)
+        if sliding_extra_rows >= 0:
+            o.sliding_extra_rows = int(sliding_extra_rows)
         self._h = vp()
         _check(lib().vkml_llama_load(path.encode(), int(context), C.byref(o), C.byref(self._h)))
         cfg = Config()
@@ -148,7 +150,8 @@ class Llama:
 
     def read_kv_cache(self, layer: int):
         c = self.config
-        shape = (c["num_kv_heads"], self.context_length, c["head_dim"])
+        rows = int(lib().vkml_llama_kv_cache_bytes(self._h)) // (2 * c["num_layers"] * c["num_kv_heads"] * c["head_dim"] * (2 if self.kv_f16 else 4))
+        shape = (c["num_kv_heads"], rows, c["head_dim"])
         dt = np.uint16 if self.kv_f16 else np.float32
         k, v = np.empty(shape, dt), np.empty(shape, dt)
         _check(lib().vkml_llama_read_kv_cache(self._h, int(layer), _ptr(k), _ptr(v), k.nbytes))

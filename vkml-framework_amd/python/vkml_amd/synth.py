@@ -40,6 +40,9 @@ class ModelSpec:
     matrix_type: int = gguf.Q4_K   # attention and FFN matrices
     embed_type: int = gguf.Q4_K    # token_embd
     output_type: int = gguf.Q6_K   # output (ignored when tied)
+    sliding_window: int = 0        # llama.attention.sliding_window (every layer), 0: none
+    attn_softcap: float = 0.0      # llama.attn_logit_softcapping, 0: none
+    final_softcap: float = 0.0     # llama.final_logit_softcapping, 0: none
 
 
 # BASELINE.json configs 1, 3 and 5.
@@ -122,6 +125,12 @@ def write_model(spec: ModelSpec, path: str, seed: int = 6) -> str:
     w.add("llama.attention.value_length", spec.head_dim)
     w.add("llama.attention.layer_norm_rms_epsilon", float(spec.eps))
     w.add("llama.rope.freq_base", float(spec.theta))
+    if spec.sliding_window:
+        w.add("llama.attention.sliding_window", int(spec.sliding_window))
+    if spec.attn_softcap:
+        w.add("llama.attn_logit_softcapping", float(spec.attn_softcap))
+    if spec.final_softcap:
+        w.add("llama.final_logit_softcapping", float(spec.final_softcap))
     d, qd, kvd = spec.hidden, spec.heads * spec.head_dim, spec.kv_heads * spec.head_dim
     ones = np.ones(d, np.float32)
     index = 0

@@ -61,7 +61,7 @@ const char* vkml_llama_last_error(void) { return g_error.c_str(); }
 
 void vkml_llama_default_options(vkml_llama_options* out) {
     if (!out) return;
-    *out = vkml_llama_options{0, -1, 1, 1, nullptr, std::int64_t{1} << 30};
+    *out = vkml_llama_options{0, -1, 1, 1, nullptr, std::int64_t{1} << 30, 1024};
 }
 
 int vkml_llama_load(const char* path, int64_t context_length, const vkml_llama_options* options, vkml_llama** out) {
@@ -80,6 +80,7 @@ int vkml_llama_load(const char* path, int64_t context_length, const vkml_llama_o
         lo.integer_dot_product = o.integer_dot != 0;
         if (o.prompt_score_bytes <= 0) throw vkml::Error("vkml_llama_load: prompt_score_bytes must be positive");
         lo.prompt_score_bytes = o.prompt_score_bytes;
+        lo.sliding_extra_rows = o.sliding_extra_rows;
         vkml::Context& ctx = context(o);
         *out = new vkml_llama{vkml::Llama::load(ctx, path, context_length, lo)};
         ++g_models;

@@ -229,8 +229,11 @@ const LlamaConfig& validated(const LlamaConfig& c, std::int64_t context_length) 
     if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) {
         throw Error("Llama: head_dim " + std::to_string(c.head_dim) + " is not implemented (64, 128 and 256 are)");
     }
-    if (c.sliding_window || c.qkv_bias || c.o_bias || c.qk_norm || c.sandwich_norms || !c.pre_norms || c.embedding_scale != 1.0f ||
-        c.residual_scale != 1.0f || c.logit_divisor != 1.0f || c.attn_logit_softcap != 0.0f || c.final_logit_softcap != 0.0f ||
+    if (c.sliding_window && (*c.sliding_window < 1 || !c.sliding_layers.empty())) {
+        throw Error("Llama: a sliding window must be positive and cover every layer in this build");
+    }
+    if (c.qkv_bias || c.o_bias || c.qk_norm || c.sandwich_norms || !c.pre_norms || c.embedding_scale != 1.0f ||
+        c.residual_scale != 1.0f || c.logit_divisor != 1.0f || c.attn_logit_softcap < 0.0f || c.final_logit_softcap < 0.0f ||
         c.activation != Activation::silu || c.rotary_dim != 0 || c.norm_weight_offset != 0.0f || !c.rope_layers.empty() ||
         c.query_pre_attn_scalar) {
         throw Error("Llama: this config uses features of another model family, which this build does not implement");
@@ -269,6 +272,13 @@ LlamaConfig LlamaConfig::from_gguf(const std::filesystem::path& path) {
     c.max_positions = need("context_length");
     c.rms_norm_eps = static_cast<float>(file.number(key("attention.layer_norm_rms_epsilon"), c.rms_norm_eps));
     c.rope_theta = static_cast<float>(file.number(key("rope.freq_base"), c.rope_theta));
+    // A sliding window over every layer, and soft caps: the keys the
+    // reference reads for the Gemma architectures (config.cpp:124-131),
+    // here for llama files that carry them (Mistral's window).
+    if (file.has(key("attention.sliding_window")))
+        c.sliding_window = static_cast<std::int64_t>(file.number(key("attention.sliding_window"), 0));
+    c.attn_logit_softcap = static_cast<float>(file.number(key("attn_logit_softcapping"), 0.0));
+    c.final_logit_softcap = static_cast<float>(file.number(key("final_logit_softcapping"), 0.0));
     if (!file.contains("token_embd.weight")) throw Error(where + " has no token_embd.weight");
     c.vocab_size = file.shape("token_embd.weight").at(0);
     c.tie_word_embeddings = !file.contains("output.weight");
@@ -296,7 +306,19 @@ struct Llama::Impl {
         std::vector<std::pair<Weight, std::int64_t>> qkv;  // fused q|k|v, or parts at row offsets
         Weight o, gate, up, down;
         Tensor k_cache, v_cache;
+        // A sliding layer's caches are rings of `rows` rows (position p at
+        // row p % rows); else rows = context_length.
+        bool slides = false;
+        std::int64_t rows = 0;
+        // The keys a query sees: the window (at most the ring), or 0 for all.
+        std::int64_t window = 0;
+        // Decode attention's 128-key chunks: over the window, or the cache.
+        std::int64_t chunks() const { return ((slides ? window : rows) + 127) / 128; }
     };
+    // With a sliding window: the window (at most the rings' rows), the
+    // rings' rows, and the first position they still hold (llama.cpp:
+    // 236-241,273-285,361).
+    std::int64_t window = 0, ring_rows = 0, oldest_kept = 0;
     Weight embed;
     std::shared_ptr<Weight> lm_head_own;  // when not tied to embed
     bool tied = false;
@@ -317,6 +339,19 @@ struct Llama::Impl {
     }
 
     void tag(const char* t) const { (void)vkml_set_profile_tag(t); }
+
+    // The final soft cap of the logits (llama.cpp:405), when the model has one.
+    void final_softcap(float* logits_p, std::int64_t count) const {
+        if (config.final_logit_softcap <= 0.0f) return;
+        tag("softcap");
+        check(vkml_unary(2, u32(count), config.final_logit_softcap, logits_p, logits_p), "softcap");
+    }
+
+    // Notes that positions up to end have run: a sliding layer's rings keep
+    // only the last ring_rows of them.
+    void ran_to(std::int64_t end) {
+        if (ring_rows) oldest_kept = std::max(oldest_kept, end - ring_rows);
+    }
 
     // y = w . in (+ residual), in given as f32 (xn-like) and, for the int8
     // path, Q8_0 (values, scales).
@@ -393,9 +428,9 @@ struct Llama::Impl {
             const uint32_t kv_code = detail::type_code(L.k_cache.dtype());
             // rope, append and attention in one launch, then the merge
             tag("attention");
-            const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(context_length), 0, 0, kv_code,
-                                             u32(chunks), c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
-                                             1.0f / std::sqrt(static_cast<float>(hd)), 0.0f};
+            const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), 0, 0, kv_code,
+                                             u32(L.chunks()), c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
+                                             1.0f / std::sqrt(static_cast<float>(hd)), c.attn_logit_softcap, u32(L.window)};
             if (int_dot && o_q && L.o.int_dot_ok()) {
                 // ... and the merge shares a launch with the o projection + residual
                 const vkml_gemv_dot_params op{1, u32(L.o.rows), u32(L.o.cols), L.o.type_code(), L.o.scale_code()};
@@ -445,6 +480,7 @@ struct Llama::Impl {
         }
         norm(final_norm, "final_norm");
         project(lm_head(), xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(logits.data()), nullptr, "lm_head");
+        final_softcap(static_cast<float*>(logits.data()), c.vocab_size);
         tag("finish");
         check(vkml_step_finish(u32(c.vocab_size), greedy ? static_cast<const float*>(logits.data()) : nullptr,
                                static_cast<vkml_decode_state*>(state.data()), static_cast<std::int32_t*>(log.data()), u32(context_length)),
@@ -524,6 +560,7 @@ struct Llama::Impl {
     // probs v in the reference's query chunks. The last row's logits go to
     // `logits`, or with all every row's to *all [t, vocab].
     void prefill(std::span<const std::int32_t> tokens, Tensor* all) {
+        ran_to(position + static_cast<std::int64_t>(tokens.size()));
         const LlamaConfig& c = config;
         Context& ctx = *context;
         const auto t = static_cast<std::int64_t>(tokens.size());
@@ -557,16 +594,35 @@ struct Llama::Impl {
             }
             // heads_first + rope of q and k, k and v to the caches' type at
             // rows position.. (llama.cpp:320-355)
-            tag("rope_kv");
-            Tensor q = f32({heads, t, hd});
-            const vkml_rope_kv_params rp{u32(heads), u32(c.num_kv_heads), u32(hd), u32(context_length), u32(position),
-                                         c.rope_style == RopeStyle::Interleaved ? 0u : 1u, detail::type_code(L.k_cache.dtype()), 1};
-            check(vkml_rope_kv_prompt(&rp, u32(t), u32(width), qkv_p, static_cast<const float*>(rope.data()), static_cast<float*>(q.data()),
-                                      const_cast<void*>(L.k_cache.data()), const_cast<void*>(L.v_cache.data())),
-                  "rope_kv");
-            tag("attention");
-            const Tensor attn =
-                detail::attention_prompt(q, L.k_cache, L.v_cache, end, true, 0, 0.0f, detail::kMaxScoreBytes, options.prompt_score_bytes);
+            const auto rope_kv = [&](std::int64_t t0, std::int64_t rows, Tensor& q_rows) {
+                tag("rope_kv");
+                const vkml_rope_kv_params rp{u32(heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), u32(position + t0),
+                                             c.rope_style == RopeStyle::Interleaved ? 0u : 1u, detail::type_code(L.k_cache.dtype()), 1};
+                check(vkml_rope_kv_prompt(&rp, u32(rows), u32(width), qkv_p + t0 * width, static_cast<const float*>(rope.data()),
+                                          static_cast<float*>(q_rows.data()), const_cast<void*>(L.k_cache.data()),
+                                          const_cast<void*>(L.v_cache.data())),
+                      "rope_kv");
+                tag("attention");
+            };
+            Tensor attn;
+            if (!L.slides) {
+                Tensor q = f32({heads, t, hd});
+                rope_kv(0, t, q);
+                attn = detail::attention_prompt(q, L.k_cache, L.v_cache, end, true, 0, c.attn_logit_softcap, detail::kMaxScoreBytes,
+                                                options.prompt_score_bytes);
+            } else {
+                // detail::sliding_attention (llama.cpp:356-364): each piece's
+                // keys join the rings just before its queries see them
+                attn = f32({heads, t, hd});
+                for (std::int64_t q0 = 0; q0 < t;) {
+                    const std::int64_t rows = detail::sliding_rows(heads, t, q0, position, L.rows, L.window, detail::kMaxScoreBytes);
+                    Tensor q = f32({heads, rows, hd});
+                    rope_kv(q0, rows, q);
+                    detail::copy_rows(detail::ring_attention(q, L.k_cache, L.v_cache, position + q0, L.window, c.attn_logit_softcap), 0,
+                                      attn, q0, rows);
+                    q0 += rows;
+                }
+            }
             const Tensor merged = permute(attn, {1, 0, 2}).reshape({t, qd});
             const Rows m_in = rows_of(merged, t, qd, int_dot && quantized_input(L.o) && qd % 32 == 0);
             project_rows(L.o, m_in, t, yp, "o");
@@ -592,11 +648,13 @@ struct Llama::Impl {
         if (all) {
             const Rows hn = norm_rows(x, final_norm, t, q_head);
             project_rows(lm_head(), hn, t, static_cast<float*>(all->data()), "lm_head");
+            final_softcap(static_cast<float*>(all->data()), t * c.vocab_size);
         } else {
             Tensor row = f32({1, d});
             check(vkml_memcpy_d2d(row.data(), xp + (t - 1) * d, static_cast<std::uint64_t>(d) * 4), "final_norm");
             const Rows hn = norm_rows(row, final_norm, 1, q_head);
             project_rows(lm_head(), hn, 1, static_cast<float*>(logits.data()), "lm_head");
+            final_softcap(static_cast<float*>(logits.data()), c.vocab_size);
         }
         tag("");
     }
@@ -700,7 +758,16 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
         for (float& f : divisors) f *= c.rope_linear_factor;
     }
     m.rope = rope_table(context, context_length, hd, c.rope_theta, c.rope_scaling, divisors);
-    const Shape cache_shape{c.num_kv_heads, context_length, hd};
+    if (c.sliding_window) {
+        if (options.sliding_extra_rows < 0) throw Error("Llama: sliding_extra_rows must not be negative");
+        m.ring_rows = std::min(context_length, *c.sliding_window + options.sliding_extra_rows);
+        m.window = std::min(*c.sliding_window, m.ring_rows);
+    }
+    // Decode attention merges at most 1024 chunks of 128 keys per head.
+    if ((c.sliding_window ? m.window : context_length) > 131072) {
+        throw Error("Llama: a step attends to at most 131072 keys; a context of " + std::to_string(context_length) +
+                    " needs a sliding window of at most that");
+    }
     for (std::int64_t l = 0; l < c.num_layers; ++l) {
         const std::string p = "blk." + std::to_string(l) + ".";
         Impl::Layer L;
@@ -720,8 +787,11 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
         L.gate = matrix(p + "ffn_gate.weight", ff, d);
         L.up = matrix(p + "ffn_up.weight", ff, d);
         L.down = matrix(p + "ffn_down.weight", d, ff);
-        L.k_cache = Tensor::zeros(context, cache_shape, options.kv_cache);
-        L.v_cache = Tensor::zeros(context, cache_shape, options.kv_cache);
+        L.slides = c.sliding_window.has_value();
+        L.rows = L.slides ? m.ring_rows : context_length;
+        L.window = L.slides ? m.window : 0;
+        L.k_cache = Tensor::zeros(context, {c.num_kv_heads, L.rows, hd}, options.kv_cache);
+        L.v_cache = Tensor::zeros(context, {c.num_kv_heads, L.rows, hd}, options.kv_cache);
         m.layers.push_back(std::move(L));
     }
 
@@ -767,7 +837,7 @@ Tensor Llama::forward(std::span<const std::int32_t> tokens) {
         m.set_state(tokens[0], m.position);
         m.run_step(false);
         m.check_attend_o();
-        ++m.position;
+        m.ran_to(++m.position);
     } else {
         m.prefill(tokens, nullptr);
     }
@@ -785,7 +855,7 @@ Tensor Llama::forward_all(std::span<const std::int32_t> tokens) {
         m.set_state(tokens[0], m.position);
         m.run_step(false);
         m.check_attend_o();
-        ++m.position;
+        m.ran_to(++m.position);
         check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward_all");
     } else {
         m.prefill(tokens, &out);
@@ -803,16 +873,26 @@ std::vector<std::int32_t> Llama::generate_greedy(std::int32_t first, std::int64_
     check(vkml_memcpy_d2h(out.data(), m.log.data(), out.size() * 4), "Llama::generate_greedy");
     m.check_attend_o();
     m.position += count;
+    m.ran_to(m.position);
     return out;
 }
 
-void Llama::reset() noexcept { impl_->position = 0; }
+void Llama::reset() noexcept {
+    impl_->position = 0;
+    impl_->oldest_kept = 0;
+}
 
 std::int64_t Llama::rewind(std::int64_t position) {
     Impl& m = *impl_;
     if (position < 0 || position > m.position) {
         throw Error("Llama::rewind: cannot rewind to position " + std::to_string(position) + " of a sequence at " + std::to_string(m.position));
     }
+    // Later cache rows are overwritten when those positions come again; a
+    // sliding window's rings must still hold the window of position's
+    // query, or the model starts over (llama.cpp:273-285).
+    const std::int64_t window = m.window ? m.window : 1;
+    if (std::max<std::int64_t>(0, position - window + 1) < m.oldest_kept) position = 0;
+    if (position == 0) m.oldest_kept = 0;
     m.position = position;
     return position;
 }

@@ -126,7 +126,7 @@ Tensor softmax(const Tensor& x) {
     const Rows r = row_shape("softmax", x);
     Tensor out = like(x, x.shape(), DType::F32);
     if (out.numel() == 0) return out;
-    const vkml_softmax_params p{r.rows, r.cols, 1.0f, 0, 1, 0, 0, 0.0f};
+    const vkml_softmax_params p{r.rows, r.cols, 1.0f, 0, 1, 0, 0, 0.0f, 0};
     check(vkml_softmax(&p, static_cast<const float*>(x.data()), static_cast<float*>(out.data())), "softmax");
     return out;
 }
@@ -459,7 +459,7 @@ Tensor attention_block(const Tensor& q, const Tensor& k_cache, const Tensor& v_c
     Tensor probs = like(q, scores.shape(), DType::F32);
     if (probs.numel() > 0) {
         const vkml_softmax_params p{u32(heads * rows), u32(keys), 1.0f / std::sqrt(static_cast<float>(hd)), causal ? 1u : 0u,
-                                    u32(rows), u32(keys - rows), u32(window), softcap};
+                                    u32(rows), u32(keys - rows), u32(window), softcap, 0};
         check(vkml_softmax(&p, static_cast<const float*>(scores.data()), static_cast<float*>(probs.data())), "attention");
     }
     return matmul("attention", probs, v_cache, false, group, keys);
@@ -513,7 +513,7 @@ Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_
         const Tensor scores = matmul("attention", part, k_cache, true, group, keys, first + r0);
         Tensor probs = like(q, scores.shape(), DType::F32);
         const vkml_softmax_params sp{u32(heads * rows), u32(keys), 1.0f / std::sqrt(static_cast<float>(hd)), 1u, u32(rows),
-                                     u32(first + r0), u32(window), softcap};
+                                     u32(first + r0), u32(window), softcap, 0};
         check(vkml_softmax(&sp, static_cast<const float*>(scores.data()), static_cast<float*>(probs.data())), "attention");
         const Tensor o = matmul("attention", probs, v_cache, false, group, keys, first + r0);
         if (rows == q_len) return o;
@@ -521,6 +521,76 @@ Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_
         r0 += rows;
     }
     if (gemv_rows) reference_chunk(rows_all, gemv_rows);
+    return out;
+}
+
+std::int64_t sliding_rows(std::int64_t heads, std::int64_t t, std::int64_t q0, std::int64_t start, std::int64_t ring, std::int64_t window,
+                          std::int64_t max_score_bytes) {
+    // Rows written for positions up to the piece's end overwrite those
+    // before end - ring, which its first query no longer needs as long as
+    // they are before its window, or no row wraps yet.
+    const std::int64_t first = start + q0;
+    std::int64_t rows = std::max(ring - window + 1, ring - first);
+    const std::int64_t keys = std::min(first + rows, ring);
+    rows = std::min(rows, std::max<std::int64_t>(1, max_score_bytes / (heads * keys * 4)));
+    if (rows >= 64) rows -= rows % 64;  // whole blocks of the tiled matmul
+    return std::min(rows, t - q0);
+}
+
+Tensor ring_attention(const Tensor& q, const Tensor& k_ring, const Tensor& v_ring, std::int64_t first, std::int64_t window, float softcap) {
+    const std::int64_t heads = q.shape()[0], rows = q.shape()[1], hd = q.shape()[2], ring = k_ring.shape()[1];
+    const std::int64_t end = first + rows;
+    if (rows == 1) return attend_one_query(q, k_ring, v_ring, std::max<std::int64_t>(0, end - window), end, softcap);
+    // attention_block with the ring mask (attention.cpp:127-138): every row
+    // of the ring written so far, in column order
+    const std::int64_t keys = std::min(end, ring), group = heads / k_ring.shape()[0];
+    const Tensor scores = matmul("attention", q, k_ring, true, group, keys);
+    Tensor probs = like(q, scores.shape(), DType::F32);
+    const vkml_softmax_params p{u32(heads * rows), u32(keys), 1.0f / std::sqrt(static_cast<float>(hd)), 1u, u32(rows), u32(first),
+                                u32(window), softcap, u32(ring)};
+    check(vkml_softmax(&p, static_cast<const float*>(scores.data()), static_cast<float*>(probs.data())), "attention");
+    return matmul("attention", probs, v_ring, false, group, keys);
+}
+
+Tensor sliding_attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& k_ring, const Tensor& v_ring, std::int64_t start,
+                         std::int64_t window, std::int64_t max_score_bytes, float softcap) {
+    const Shape& qs = q.shape();
+    const Shape& ks = k_ring.shape();
+    const bool shapes = qs.size() == 3 && ks.size() == 3 && k.shape().size() == 3 && v.shape() == k.shape() && v_ring.shape() == ks &&
+                        k.shape()[0] == ks[0] && k.shape()[1] == qs[1] && k.shape()[2] == qs[2] && ks[2] == qs[2] && ks[0] > 0 &&
+                        qs[0] % ks[0] == 0;
+    if (!shapes || k.dtype() != k_ring.dtype() || v.dtype() != k_ring.dtype() || v_ring.dtype() != k_ring.dtype()) {
+        throw Error("sliding_attention: cannot append " + std::string(to_string(k.dtype())) + " k " + to_string(k.shape()) + " and " +
+                    std::string(to_string(v.dtype())) + " v " + to_string(v.shape()) + " to " + std::string(to_string(k_ring.dtype())) +
+                    " and " + std::string(to_string(v_ring.dtype())) + " caches " + to_string(ks) + " for q " + to_string(qs));
+    }
+    const std::int64_t ring = ks[1], t = qs[1], heads = qs[0];
+    if (window < 1 || window > ring || start < 0) {
+        throw Error("sliding_attention: a window of " + std::to_string(window) + " keys must be positive and fit a ring of " +
+                    std::to_string(ring) + " rows, from position " + std::to_string(start));
+    }
+    // positions from.. of rows row.. of src into the ring, in at most two
+    // pieces where it wraps around
+    const auto append = [&](const Tensor& src, const Tensor& cache, std::int64_t row, std::int64_t from, std::int64_t n) {
+        const std::int64_t at = from % ring, head = std::min(n, ring - at);
+        copy_rows(src, row, cache, at, head);
+        copy_rows(src, row + head, cache, 0, n - head);
+    };
+    Tensor out = like(q, qs, DType::F32);
+    for (std::int64_t q0 = 0; q0 < t;) {
+        const std::int64_t rows = sliding_rows(heads, t, q0, start, ring, window, max_score_bytes);
+        append(k, k_ring, q0, start + q0, rows);
+        append(v, v_ring, q0, start + q0, rows);
+        Tensor qc = q;
+        if (rows != t) {
+            qc = like(q, {heads, rows, qs[2]}, DType::F32);
+            copy_rows(q, q0, qc, 0, rows);
+        }
+        const Tensor block = ring_attention(qc, k_ring, v_ring, start + q0, window, softcap);
+        if (rows == t) return block;
+        copy_rows(block, 0, out, q0, rows);
+        q0 += rows;
+    }
     return out;
 }
 

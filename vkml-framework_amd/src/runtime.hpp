@@ -84,4 +84,21 @@ Tensor attention_prompt(const Tensor& q, const Tensor& k_cache, const Tensor& v_
                         std::int64_t window, float softcap, std::int64_t max_score_bytes,
                         std::int64_t piece_bytes = std::int64_t{1} << 30);
 
+// Sliding-window attention over rings [kv_heads, ring, hd] that hold key
+// position p in row p % ring (attention.cpp:229-294), in pieces:
+// sliding_rows gives how many of t queries from q0 (positions start + q0..)
+// the next piece takes, so that the keys it appends overwrite no row a
+// query of the piece still sees; ring_attention runs such a piece once its
+// keys are in the rings.
+// Rows start.. of every batch of src [B, *, width] into rows at.. of dst.
+void copy_rows(const Tensor& src, std::int64_t start, const Tensor& dst, std::int64_t at, std::int64_t rows);
+
+std::int64_t sliding_rows(std::int64_t heads, std::int64_t t, std::int64_t q0, std::int64_t start, std::int64_t ring, std::int64_t window,
+                          std::int64_t max_score_bytes);
+Tensor ring_attention(const Tensor& q, const Tensor& k_ring, const Tensor& v_ring, std::int64_t first, std::int64_t window, float softcap);
+// The whole of it: q [heads, t, hd] at positions start.., their keys and
+// values k, v [kv_heads, t, hd] appended to the rings piece by piece.
+Tensor sliding_attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& k_ring, const Tensor& v_ring, std::int64_t start,
+                         std::int64_t window, std::int64_t max_score_bytes, float softcap);
+
 }  // namespace vkml::detail

@@ -130,19 +130,28 @@ struct ChunkShape {
     static constexpr uint32_t kPasses = kChunk / kSlots;
 };
 
-// A chunk's K rows (lane g of a key's four holds vec4s g, g + 4, ...) and,
-// when it is staged, its V tile, in registers: every load of the chunk,
-// issued at once. Keys past the live ones re-read the last live key.
+// A chunk's K rows in registers (lane g of a key's four holds vec4s g, g +
+// 4, ...), and, when it is staged, its V tile copied straight into LDS by
+// the memory unit (global_load_lds: no registers, nothing to store
+// afterwards): every load of the chunk, issued at once. Keys past the live
+// ones re-read the last live key.
 template <int HD, bool F16>
 struct ChunkLoads {
     using S = ChunkShape<HD, F16>;
     KRaw<F16> k[S::kPasses][S::KPL];
-    uint4 v[S::kVLoads];
 };
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes at src into LDS: lane l of the wave writes lds_wave + 16 l
+// (lds_wave the same for the whole wave).
+__device__ __forceinline__ void load_to_lds16(const void* src, void* lds_wave) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_wave, 16, 0, 0);
+}
 
 template <int HD, bool F16>
 __device__ __forceinline__ void attend_chunk_load(const ChunkArgs& a, uint32_t chunk, uint32_t kvh, uint32_t kv_len,
-                                                  ChunkLoads<HD, F16>& r) {
+                                                  ChunkLoads<HD, F16>& r, uint8_t* v_lds) {
     using S = ChunkShape<HD, F16>;
     constexpr uint32_t RB = S::kRowBytes;
     const uint32_t t = thread_index();
@@ -162,10 +171,13 @@ __device__ __forceinline__ void attend_chunk_load(const ChunkArgs& a, uint32_t c
         }
     }
     if constexpr (S::kStageV) {
+        // the tile row-major, as the cache rows: piece u = t + j * kThreads
+        // (16 bytes) of the tile at byte 16 u, lane by lane within a wave
+        const uint32_t wave_first = t - t % kWave;
 #pragma unroll
         for (uint32_t j = 0; j < S::kVLoads; ++j) {
             const uint32_t u = t + j * kThreads, key = min(u / (RB / 16), n - 1), col = u % (RB / 16);
-            r.v[j] = ldg(reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.v_cache) + row_of(key) * RB + 16ull * col));
+            load_to_lds16(static_cast<const uint8_t*>(a.v_cache) + row_of(key) * RB + 16ull * col, v_lds + 16 * (j * kThreads + wave_first));
         }
     }
 }
@@ -225,7 +237,6 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
 #pragma clang fp contract(off)
     using S = ChunkShape<HD, F16>;
     constexpr bool kStageV = S::kStageV;
-    constexpr uint32_t kVLoads = S::kVLoads;
     constexpr uint32_t KPL = S::KPL;
     constexpr uint32_t kSlots = S::kSlots;
     constexpr uint32_t kPasses = S::kPasses;
@@ -337,12 +348,9 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
             }
         }
     }
-    // V goes to LDS only now: the scores wait for the K loads alone, while
-    // the V loads (issued last) are still in flight.
-    if constexpr (kStageV) {
-#pragma unroll
-        for (uint32_t j = 0; j < kVLoads; ++j) reinterpret_cast<uint4*>(sm.v)[t + j * kThreads] = ld.v[j];
-    }
+    // The V tile's copies into LDS (issued last, after the K loads the
+    // scores waited for) have landed once the wave's loads are all done.
+    if constexpr (kStageV) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (kStageV && holds_new) {
         for (uint32_t i = t; i < HD; i += kThreads) {

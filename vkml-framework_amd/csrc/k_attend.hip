@@ -63,7 +63,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_chunk(ChunkArgs a) {
     QLoads<HD, HPW> qv;  // first: the item waits for them before K and V
     attend_q_load<HD, HPW>(a, kvh, hl, pos, qv);
     ChunkLoads<HD, F16> ld;
-    attend_chunk_load<HD, F16>(a, chunk, kvh, kv_len, ld);
+    attend_chunk_load<HD, F16>(a, chunk, kvh, kv_len, ld, sm.v);
     attend_chunk_item<HD, F16, HPW, false>(a, chunk, kvh, hl, pos, kv_len, qv, ld, sm);
 }
 

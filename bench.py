@@ -486,7 +486,7 @@ def main():
         log("per-label HIP-event profile of eager steps (includes launch gaps):")
         for r in sorted(rows, key=lambda r: -r["calls"] * r["avg_us"])[:14]:
             log(f"  {r['kernel']:<28} calls {r['calls']:>6}  avg {r['avg_us']:9.2f} us  {r['gb_s'] or '':>8} GB/s")
-        busy_ms = sum(ms for _, _, ms in prof) / args.profile_steps
+        busy_ms = sum(ms for _, _, ms in prof) / args.profile_steps if args.profile_steps else None
         dom_us, dom_bytes = time_gate_up(spec)
         achieved = dom_bytes / (dom_us * 1e-6) / 1e9
         log(f"gemv_fused (norm + gate/up + swiglu + q8_0) back to back: {dom_us:.2f} us a launch, {achieved:.0f} GB/s")
@@ -554,7 +554,7 @@ def main():
             "hbm_gb_s": round(hbm, 1),
             "hbm_frac": round(hbm / PEAK_HBM, 4),
             "bytes_per_step": round(step_bytes),
-            "gpu_busy_ms_per_step": round(busy_ms, 4),
+            "gpu_busy_ms_per_step": round(busy_ms, 4) if busy_ms is not None else None,
             "roofline": {"bound": "hbm", "kernel": "gemv_fused gate/up (k_gemv_dot<q4_K, f16, 8 lanes, swiglu, norm, q8_0 out>)",
                          "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s",
                          "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,

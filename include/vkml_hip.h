@@ -468,6 +468,29 @@ int vkml_attend_step_o(const vkml_attend_step_params* p, const float* d_qkv, con
  * earlier vkml_attend_step_o on this sync buffer that timed out. */
 int vkml_attend_o_check(uint32_t* d_sync);
 
+/* vkml_attend_step_o (llama.cpp:313-374, attention.cpp:54-84) in one
+ * launch where the shapes allow it (q4_K, or q8_0 with f16 scales, o
+ * weights; a decode state): the chunk pass, then per KV head and head
+ * group the last chunk item to finish merges its heads (attend_merge.comp's
+ * order), and the o GEMV + residual, whose workgroups load their weights
+ * at once and wait (bounded) for every merge. Same results bit for bit.
+ * d_sync holds `blocks` (>= 2) blocks of vkml_attend_fused_sync_bytes(1)
+ * bytes, zeroed before the first call; a call uses block `block` and
+ * zeroes the counters of block (block + 1) % blocks, so consecutive calls
+ * on the stream take consecutive blocks, cyclically (in a model, layer L
+ * takes block L of one block per layer). Other shapes: the chunk pass, the
+ * merge and vkml_gemv_dot_add as separate launches, with the same block
+ * bookkeeping. */
+uint64_t vkml_attend_fused_sync_bytes(uint32_t blocks);
+int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* d_qkv, const float* d_rope_table,
+                           void* d_k_cache, void* d_v_cache, float* d_partial, float* d_stats, float* d_out,
+                           void* d_values, float* d_scales, const vkml_decode_state* d_state,
+                           const vkml_gemv_dot_params* o, const void* d_o_values, const void* d_o_scales,
+                           float* d_x, uint32_t* d_sync, uint32_t block, uint32_t blocks);
+/* Synchronizes, then reports (VKML_ERROR_DEVICE) and clears (every block) a
+ * wait of an earlier vkml_attend_step_fused on these blocks that timed out. */
+int vkml_attend_fused_check(uint32_t* d_sync, uint32_t blocks);
+
 /* vkml_attend_step without the d_partial / d_stats workspace, allocating
  * nothing: no counterpart in the reference. For callers that cannot call
  * hipMalloc (code under HIP graph capture, tight serving loops, harnesses

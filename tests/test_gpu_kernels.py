@@ -522,6 +522,85 @@ def test_attend_step_o_bit_exact(hd, heads, kvh, pos, kv_type, fmt, n):
         assert np.array_equal(bits(got), bits(x2.download(np.float32, n)))
 
 
+@pytest.mark.parametrize("hd,heads,kvh,pos,kv_type,fmt,n,window,blocks", [
+    (128, 32, 8, 4096, H.F16, H.Q4_K, 4096, 0, 2), (128, 32, 8, 300, H.F16, H.Q8_0, 4096, 0, 3),
+    (64, 32, 8, 200, H.F16, H.Q4_K, 2048, 0, 2), (256, 8, 4, 300, H.F16, H.Q4_K, 2048, 0, 2),
+    (128, 16, 2, 700, H.F32, H.Q4_K, 1024, 0, 2), (128, 16, 4, 130, H.F16, H.Q4_0, 2048, 0, 2),
+    (128, 12, 4, 260, H.F16, H.Q4_K, 1536, 0, 2), (64, 8, 8, 0, H.F32, H.Q4_K, 256, 0, 2),
+    (128, 16, 4, 500, H.F16, H.Q4_K, 2048, 200, 3)])
+def test_attend_step_fused_bit_exact(hd, heads, kvh, pos, kv_type, fmt, n, window, blocks):
+    # the chunk pass, the merges (by each head set's last chunk item) and the
+    # o GEMV + residual in one launch, four steps in a row cycling through
+    # the sync blocks: against the oracle and against vkml_attend_step_o on
+    # copies of the caches; q4_0 o weights take the separate launches (with
+    # the next block cleared all the same); 12 heads over 4 KV heads take
+    # one head a workgroup
+    k = heads * hd
+    cap = pos + 67
+    chunks = (cap + 127) // 128
+    rng = np.random.default_rng(pos + hd + n + 1)
+    dt = np.uint16 if kv_type == H.F16 else np.float32
+    prior = rng.standard_normal((2, kvh, cap, hd)).astype(np.float32)
+    caches = [prior[i].astype(np.float16).view(np.uint16) if kv_type == H.F16 else prior[i] for i in range(2)]
+    kc, vc, kc2, vc2 = dev(caches[0]), dev(caches[1]), dev(caches[0]), dev(caches[1])
+    table = O.rope_table(cap, hd, 1e6)
+    dtab = dev(table)
+    v, s_, quant, words, scales = weights(fmt, n, k, pos + 5)
+    x0 = rng.standard_normal(n).astype(np.float32)
+    x, x2 = dev(x0), dev(x0)
+    fbytes = H.lib().vkml_attend_fused_sync_bytes(blocks)
+    fsync = H.empty(fbytes)
+    H.call("vkml_fill_u32", p(fsync), 0, fbytes // 4)
+    sync = H.empty(H.lib().vkml_attend_o_sync_bytes())
+    H.call("vkml_fill_u32", p(sync), 0, H.lib().vkml_attend_o_sync_bytes() // 4)
+    part, stats = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8)
+    part2, stats2 = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8)
+    st = H.empty(16)
+    op = H.GemvDotParams(1, n, k, fmt, H.F16)
+    want_x = x0.copy()
+    for step in range(4):
+        p_now = pos + step
+        print(f"fused case hd={hd} heads={heads} kvh={kvh} pos={p_now} n={n} window={window} block={step % blocks}", flush=True)
+        H.call("vkml_state_set", p(st), 0, p_now, 0)
+        qkv = rng.standard_normal((heads + 2 * kvh) * hd).astype(np.float32)
+        dq = dev(qkv)
+        out, vals, scs = H.empty(k * 4), H.empty(k), H.empty(k // 32 * 4)
+        out2, vals2, scs2 = H.empty(k * 4), H.empty(k), H.empty(k // 32 * 4)
+        prm = H.AttendStepParams(heads, kvh, hd, cap, 0, 0, kv_type, chunks, 0, 1, 1.0 / math.sqrt(hd), 0.0, window)
+        H.call("vkml_attend_step_fused", prm, p(dq), p(dtab), p(kc), p(vc), p(part), p(stats), p(out), p(vals), p(scs), p(st),
+               op, p(v), p(s_), p(x), p(fsync), step % blocks, blocks)
+        H.call("vkml_attend_step_o", prm, p(dq), p(dtab), p(kc2), p(vc2), p(part2), p(stats2), p(out2), p(vals2), p(scs2), p(st),
+               op, p(v), p(s_), p(x2), p(sync))
+        H.call("vkml_attend_fused_check", p(fsync), blocks)  # no wait gave up
+        q = O.rope(qkv[:k].reshape(1, heads, hd), table, p_now, 0).reshape(heads, hd)
+        kn = O.rope(qkv[k:k + kvh * hd].reshape(1, kvh, hd), table, p_now, 0).reshape(kvh, hd)
+        vn = qkv[k + kvh * hd:].reshape(kvh, hd)
+        for c, new in ((caches[0], kn), (caches[1], vn)):
+            c[:, p_now] = O.f32_to_f16(new) if kv_type == H.F16 else new
+        assert np.array_equal(kc.download(dt, caches[0].shape), caches[0])
+        assert np.array_equal(vc.download(dt, caches[1].shape), caches[1])
+        start = max(0, p_now + 1 - window) if window else 0
+        want = O.attend_decode(q, caches[0], caches[1], start, p_now + 1)
+        assert np.array_equal(bits(out.download(np.float32, (heads, hd))), bits(want))
+        ww, ws = O.quantize(O.Q8_0, want.reshape(1, k), False)
+        assert np.array_equal(vals.download(np.uint32, ww.shape), ww)
+        assert np.array_equal(scs.download(np.float32, ws.shape).view(np.uint32), ws.view(np.uint32))
+        want_x = want_x + O.gemv_dot(quant, ww, ws, 1, words, scales, n, k)[0]
+        got = x.download(np.float32, n)
+        assert np.array_equal(bits(got), bits(want_x))
+        assert np.array_equal(bits(got), bits(x2.download(np.float32, n)))
+
+
+def test_attend_step_fused_rejects_bad_blocks():
+    prm = H.AttendStepParams(8, 8, 64, 64, 0, 0, H.F16, 1, 0, 1, 0.125, 0.0, 0)
+    op = H.GemvDotParams(1, 256, 512, H.Q4_K, H.F16)
+    b = H.empty(1 << 16)
+    for block, blocks in ((0, 1), (2, 2)):
+        with pytest.raises(H.VkmlError, match="two blocks at least"):
+            H.call("vkml_attend_step_fused", prm, p(b), p(b), p(b), p(b), p(b), p(b), p(b), p(b), p(b), p(b), op, p(b), p(b), p(b),
+                   p(b), block, blocks)
+
+
 # ---------------------------------------------------------------- small ops
 
 def test_argmax_and_step_finish():

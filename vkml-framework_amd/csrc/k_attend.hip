@@ -123,21 +123,22 @@ constexpr uint32_t kOSpinCap = 1u << 20;
 
 // Lane 0 polls counter copy wg % kCopies until every merging workgroup has
 // arrived; false if the wait gave up (the spin limit, or another
-// workgroup's error). Called by every thread; ends with a workgroup barrier
+// workgroup's error). The error flag is the sync words' own unless given. Called by every thread; ends with a workgroup barrier
 // (the weight loads issued before it stay in flight).
-__device__ bool await_merged(uint32_t* sync, uint32_t wg, uint32_t arrivals) {
+__device__ bool await_merged(uint32_t* sync, uint32_t wg, uint32_t arrivals, uint32_t* error = nullptr) {
     __shared__ uint32_t s_ok;
+    if (!error) error = OSync::error(sync);
     if (threadIdx.x == 0) {
         uint32_t ok = 1;
         uint32_t* c = OSync::counter(sync, wg % OSync::kCopies);
         for (uint32_t spins = 0;; ++spins) {
             if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= arrivals) break;
-            if (spins % 64 == 63 && __hip_atomic_load(OSync::error(sync), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+            if (spins % 64 == 63 && __hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
                 ok = 0;
                 break;
             }
             if (spins >= kOSpinCap) {
-                __hip_atomic_store(OSync::error(sync), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 ok = 0;
                 break;
             }
@@ -210,6 +211,166 @@ bool launch_merge_o(const MergeOArgs& m, const vkml::gemv::GemvArgs& g, uint32_t
     const bool full = g.k % 2048 == 0;  // whole pairs of 2-round batches
     if (q4k) return full ? launch_merge_o_as<VKML_Q4_K, true>(m, g, grid, lds) : launch_merge_o_as<VKML_Q4_K, false>(m, g, grid, lds);
     return full ? launch_merge_o_as<VKML_Q8_0, true>(m, g, grid, lds) : launch_merge_o_as<VKML_Q8_0, false>(m, g, grid, lds);
+}
+
+// ------------------------------------------- chunks + merge + o, one launch
+
+// One block of the sync words of vkml_attend_step_fused: the OSync words
+// (the o GEMV's arrival counters), then an arrival counter per set of chunk
+// items (KV head, head group), kArriveStride words apart. The sticky error
+// flag of every block is word 0 of block 0.
+struct FusedSync {
+    static constexpr uint32_t kArriveStride = 8;
+    static constexpr uint32_t kMaxSets = 256;
+    static constexpr uint32_t kWords = OSync::kWords + kArriveStride * kMaxSets;
+    __device__ static uint32_t* arrive(uint32_t* s, uint32_t set) { return s + OSync::kWords + kArriveStride * set; }
+};
+
+struct FusedArgs {
+    uint32_t attn_wgs;  // workgroups of the chunk pass (grid padding included), first in the grid
+    uint32_t merges;    // sets of chunk items: merging workgroups, one a set
+    uint32_t* sync;     // this launch's block: every counter zero at the start
+    uint32_t* next;     // the next launch's block, whose o GEMV counters this one zeroes
+    uint32_t* error;    // the sticky error flag
+    float* out;         // the merged outputs [heads, hd] f32
+    uint8_t* values;    // and their Q8_0 codes and f32 scales: the o GEMV's input
+    float* scales;
+};
+
+// Workgroups [0, attn_wgs): the chunk pass, as k_attend_chunk, its partials
+// and statistics stored write-through; then each adds one to its set's
+// arrival counter, and the set's last to arrive (every other item of the
+// set has stored its results) resets the counter, merges the set's HPW
+// heads in chunk order (attend_merge.comp's arithmetic, merge_head) with
+// the Q8_0 of the outputs stored write-through, and adds one to every copy
+// of the o GEMV counter. The rest: the o GEMV + residual, as in k_merge_o,
+// waiting (bounded) for all merges. Chunk items never wait, so the GEMV's
+// workgroups, fewer than the resident slots, cannot keep an item from
+// running, in whatever order workgroups are dispatched.
+template <int HD, bool F16, int HPW, int FMT, bool FULL>
+__global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArgs f, vkml::gemv::GemvArgs g) {
+    extern __shared__ uint4 smem[];
+    if (blockIdx.x >= f.attn_wgs) {
+        const uint32_t wg = blockIdx.x - f.attn_wgs;
+        vkml::gemv::GemvRows<FMT, true, 32, vkml::gemv::kAdd, 2, kThreads, false, false, 1, FULL> rows;
+        rows.start(g, wg);
+        if (!await_merged(f.sync, wg, f.merges, f.error)) return;
+        vkml::gemv::stage_activation<kThreads, false, true>(g, smem);
+        rows.finish(g, smem, vkml::gemv::staged_ss(smem, g.k));
+        return;
+    }
+    auto& sm = *reinterpret_cast<AttendSmem<HD, F16, HPW>*>(smem);
+    const uint32_t G = a.group, groups = G / HPW, pairs = a.chunks * a.kv_heads;
+    const uint32_t L = blockIdx.x, pair_lo = L % kXcds, rest = L / kXcds;
+    if (L == 0 && threadIdx.x < OSync::kCopies) OSync::counter(f.next, threadIdx.x)[0] = 0u;
+    const uint32_t hl = rest % groups, pair = (rest / groups) * kXcds + pair_lo;
+    if (pair >= pairs) return;
+    const uint32_t chunk = pair / a.kv_heads, kvh = pair % a.kv_heads, head0 = kvh * G + hl * HPW;
+    const uint32_t pos = static_cast<uint32_t>(a.state->position);
+    const uint32_t kv_len = pos + 1;
+    if (a.window != 0 && kv_len > a.window) a.kv_start = max(a.kv_start, kv_len - a.window);
+    if (a.kv_start + chunk * kChunk >= kv_len) {
+        if (threadIdx.x < HPW) {  // past the live keys: a max of -inf, which the merge skips
+            const uint64_t at = static_cast<uint64_t>(head0 + threadIdx.x) * a.chunks + chunk;
+            st_f32<true>(a.stats + at * 2, -__builtin_inff());
+            st_f32<true>(a.stats + at * 2 + 1, 0.0f);
+        }
+    } else {
+        QLoads<HD, HPW> qv;
+        attend_q_load<HD, HPW>(a, kvh, hl, pos, qv);
+        ChunkLoads<HD, F16> ld;
+        attend_chunk_load<HD, F16>(a, chunk, kvh, kv_len, ld, sm.v);
+        attend_chunk_item<HD, F16, HPW, true>(a, chunk, kvh, hl, pos, kv_len, qv, ld, sm);
+    }
+    __shared__ uint32_t s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the write-through stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t* c = FusedSync::arrive(f.sync, kvh * groups + hl);
+        const bool last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.chunks - 1;
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // The merge, kThreads / HD heads at a time (thread element d of head
+    // `half`); threads past the heads of a pass redo its first head without
+    // storing, to keep the barriers whole.
+    constexpr uint32_t kHalves = kThreads / HD;
+    constexpr uint32_t kAtOnce = kHalves < HPW ? kHalves : HPW;
+    const uint32_t half = threadIdx.x / HD, d = threadIdx.x % HD;
+    float* fl = reinterpret_cast<float*>(smem);
+    float* s_r = fl + half * 2 * a.chunks;
+    float* s_l = s_r + a.chunks;
+    float* s_wmax = fl + kHalves * 2 * a.chunks + half * (HD / kWave);
+#pragma unroll
+    for (uint32_t h0 = 0; h0 < HPW; h0 += kAtOnce) {
+        const bool mine = half < kAtOnce;
+        if (h0 > 0) __syncthreads();  // the previous pass is done with s_r, s_l
+        merge_head<true, 48>(a.partial, a.stats, mine ? f.out : nullptr, mine ? f.values : nullptr, f.scales,
+                             head0 + h0 + (mine ? half : 0), a.chunks, a.chunks, HD, d, s_r, s_l, s_wmax);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x < OSync::kCopies)
+        __hip_atomic_fetch_add(OSync::counter(f.sync, threadIdx.x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int HD, bool F16, int HPW, int FMT, bool FULL>
+bool launch_fused_as(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs) {
+    const void* fn = reinterpret_cast<const void*>(&k_attend_fused<HD, F16, HPW, FMT, FULL>);
+    constexpr uint32_t kHalves = kThreads / HD;
+    const size_t merge_lds = (static_cast<size_t>(kHalves) * 2 * a.chunks + kHalves * (HD / kWave)) * 4;
+    const size_t lds = std::max({sizeof(AttendSmem<HD, F16, HPW>), merge_lds, static_cast<size_t>(vkml::gemv::stage_bytes(g.k, false))});
+    if (lds > 64 * 1024) return false;
+    static int per_cu = -1;  // resident workgroups a CU at this LDS size
+    static size_t per_cu_lds = 0;
+    if (per_cu < 0 || per_cu_lds != lds) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, lds) != hipSuccess) per_cu = 0;
+        per_cu_lds = lds;
+    }
+    // the waiting GEMV workgroups must leave slots for the chunk items
+    if (static_cast<uint64_t>(per_cu) * vkml::abi::compute_units() <= gemv_wgs) return false;
+    hipLaunchKernelGGL((k_attend_fused<HD, F16, HPW, FMT, FULL>), dim3(f.attn_wgs + gemv_wgs), dim3(kThreads), lds,
+                       vkml::abi::stream(), a, f, g);
+    return true;
+}
+
+template <int HD, bool F16, int HPW>
+bool launch_fused_hpw(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs, bool q4k) {
+    const bool full = g.k % 2048 == 0;  // whole pairs of 2-round batches
+    if (q4k)
+        return full ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true>(a, f, g, gemv_wgs)
+                    : launch_fused_as<HD, F16, HPW, VKML_Q4_K, false>(a, f, g, gemv_wgs);
+    return full ? launch_fused_as<HD, F16, HPW, VKML_Q8_0, true>(a, f, g, gemv_wgs)
+                : launch_fused_as<HD, F16, HPW, VKML_Q8_0, false>(a, f, g, gemv_wgs);
+}
+
+// The one-launch form, if the shapes allow it; false otherwise (nothing launched).
+bool launch_fused(uint32_t head_dim, bool f16, const ChunkArgs& a, FusedArgs f, const vkml::gemv::GemvArgs& g, uint32_t b_type,
+                  uint32_t scale_type) {
+    using namespace vkml::gemv;
+    if (b_type != VKML_Q4_K && !(b_type == VKML_Q8_0 && scale_type == VKML_F16)) return false;
+    const bool q4k = b_type == VKML_Q4_K;
+    if (g.k != a.heads * head_dim || g.n == 0) return false;
+    if ((q4k ? code_bytes<VKML_Q4_K>(g.n, g.k) : code_bytes<VKML_Q8_0>(g.n, g.k)) >= (1ull << 32) ||
+        (q4k ? scale_bytes<VKML_Q4_K, true>(g.n, g.k) : scale_bytes<VKML_Q8_0, true>(g.n, g.k)) >= (1ull << 32))
+        return false;
+    const uint32_t hpw = a.group % 2 == 0 ? 2 : 1;
+    f.merges = a.kv_heads * (a.group / hpw);
+    if (f.merges > FusedSync::kMaxSets) return false;
+    const uint32_t pair_blocks = (a.chunks * a.kv_heads + kXcds - 1) / kXcds;
+    f.attn_wgs = pair_blocks * kXcds * (a.group / hpw);
+    const uint32_t gemv_wgs = (g.n + kThreads / 32 - 1) / (kThreads / 32);
+#define VKML_FUSED(HD)                                                                                             \
+    (f16 ? (hpw == 2 ? launch_fused_hpw<HD, true, 2>(a, f, g, gemv_wgs, q4k) : launch_fused_hpw<HD, true, 1>(a, f, g, gemv_wgs, q4k)) \
+         : (hpw == 2 ? launch_fused_hpw<HD, false, 2>(a, f, g, gemv_wgs, q4k) : launch_fused_hpw<HD, false, 1>(a, f, g, gemv_wgs, q4k)))
+    switch (head_dim) {
+        case 64: return VKML_FUSED(64);
+        case 128: return VKML_FUSED(128);
+        default: return VKML_FUSED(256);
+    }
+#undef VKML_FUSED
 }
 
 int check_heads(uint32_t heads, uint32_t kv_heads, uint32_t head_dim, const char* what) {
@@ -343,6 +504,62 @@ int vkml_attend_step_o(const vkml_attend_step_params* p, const float* qkv, const
         if (int r = vkml::abi::check_launch("attend_merge")) return r;
     }
     return vkml_gemv_dot_add(o, values, o_values, x, o_scales, scales, x);
+}
+
+uint64_t vkml_attend_fused_sync_bytes(uint32_t blocks) { return static_cast<uint64_t>(FusedSync::kWords) * 4 * blocks; }
+
+int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* qkv, const float* rope_table, void* k_cache, void* v_cache,
+                           float* partial, float* stats, float* out, void* values, float* scales, const vkml_decode_state* state,
+                           const vkml_gemv_dot_params* o, const void* o_values, const void* o_scales, float* x, uint32_t* sync,
+                           uint32_t block, uint32_t blocks) {
+    if (int r = check_step(p, qkv, rope_table, k_cache, v_cache, partial, stats, out, values, scales, state, "attend_step_fused")) return r;
+    VKML_CHECK_ARG(state, "attend_step_fused: needs the decode state");
+    VKML_CHECK_ARG(o && values && scales && o_values && o_scales && x && sync, "attend_step_fused: null buffer");
+    VKML_CHECK_ARG(blocks >= 2 && block < blocks, "attend_step_fused: block " + std::to_string(block) + " of " + std::to_string(blocks) +
+                                                      " (two blocks at least)");
+    VKML_CHECK_ARG(o->m == 1 && o->k == p->heads * p->head_dim,
+                   "attend_step_fused: the o projection must take the " + std::to_string(p->heads * p->head_dim) + " attention outputs");
+    uint32_t* own = sync + static_cast<uint64_t>(block) * FusedSync::kWords;
+    uint32_t* next = sync + static_cast<uint64_t>((block + 1) % blocks) * FusedSync::kWords;
+    const ChunkArgs args = step_args(p, qkv, rope_table, k_cache, v_cache, partial, stats, state, nullptr);
+    const FusedArgs f{0, 0, own, next, sync, out, static_cast<uint8_t*>(values), scales};
+    const vkml::gemv::GemvArgs g{static_cast<const uint4*>(values), scales, o_values, o_scales, nullptr, nullptr, x, x, o->n, o->k};
+    {
+        vkml::abi::ProfileScope prof("attend_fused");
+        if (launch_fused(p->head_dim, p->kv_type == VKML_F16, args, f, g, o->b_type, o->scale_type))
+            return vkml::abi::check_launch("attend_step_fused");
+    }
+    // Shapes the one launch does not take: the chunk pass, the merge and the
+    // o GEMV; the next block's counters zeroed all the same.
+    {
+        vkml::abi::ProfileScope prof("attend_step");
+        launch_chunks(p->head_dim, p->kv_type == VKML_F16, args);
+        if (int r = vkml::abi::check_launch("attend_step")) return r;
+    }
+    {
+        vkml::abi::ProfileScope prof("attend_merge");
+        launch_merge(p->heads, p->head_dim, p->chunks, partial, stats, out, values, scales);
+        if (int r = vkml::abi::check_launch("attend_merge")) return r;
+    }
+    if (int r = vkml_fill_u32(next + OSync::kLine, 0u, OSync::kWords - OSync::kLine)) return r;
+    return vkml_gemv_dot_add(o, values, o_values, x, o_scales, scales, x);
+}
+
+int vkml_attend_fused_check(uint32_t* sync, uint32_t blocks) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(sync && blocks >= 2, "attend_fused_check: null buffer or fewer than two blocks");
+    hipStream_t s = vkml::abi::stream();
+    uint32_t flag = 0;
+    hipError_t e = hipMemcpyAsync(&flag, sync, 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_fused_check");
+    if (flag == 0) return VKML_OK;
+    // A wait gave up: every block starts over (flag and counters).
+    e = hipMemsetAsync(sync, 0, vkml_attend_fused_sync_bytes(blocks), s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_fused_check");
+    return vkml::abi::fail(VKML_ERROR_DEVICE,
+                           "attend_step_fused: the o GEMV's wait for the merges timed out; the step's results are invalid");
 }
 
 }  // extern "C"

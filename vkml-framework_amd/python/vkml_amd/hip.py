@@ -126,6 +126,9 @@ SIGNATURES = {
     "vkml_attend_step": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step_o": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp],
     "vkml_attend_o_check": [vp],
+    "vkml_attend_fused_sync_bytes": [u32],
+    "vkml_attend_step_fused": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp, u32, u32],
+    "vkml_attend_fused_check": [vp, u32],
     "vkml_attend_step_noalloc": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_o_sync_bytes": [],
     "vkml_state_set": [vp, i32, i32, i32],
@@ -154,6 +157,7 @@ def lib() -> C.CDLL:
             fn.restype = C.c_int
         _lib.vkml_stream.restype = C.c_void_p
         _lib.vkml_attend_o_sync_bytes.restype = C.c_uint64
+        _lib.vkml_attend_fused_sync_bytes.restype = C.c_uint64
     return _lib
 
 

@@ -327,7 +327,8 @@ struct Llama::Impl {
 
     // Decode buffers.
     Tensor x, xn, xq, xs, qkv, q, attn, aq, as, partial, stats, h, hq, hs, gate_tmp, up_tmp, ytmp, logits, state, log;
-    Tensor o_sync;  // vkml_attend_step_o: the merge + o launch's sync words
+    Tensor o_sync;      // vkml_attend_step_o: the merge + o launch's sync words
+    Tensor fused_sync;  // vkml_attend_step_fused: a block per layer (empty: not used)
     std::int64_t chunks = 1;  // decode attention's 128-key chunks over the whole cache
     std::uint64_t graph_logits = 0, graph_greedy = 0;
 
@@ -379,7 +380,11 @@ struct Llama::Impl {
     // step's KV rows and logits from that step on are then invalid and must
     // be recomputed: the caller's position does not advance past them).
     void check_attend_o() const {
-        if (int_dot) check(vkml_attend_o_check(static_cast<std::uint32_t*>(const_cast<void*>(o_sync.data()))), "Llama: decode step");
+        if (!int_dot) return;
+        check(vkml_attend_o_check(static_cast<std::uint32_t*>(const_cast<void*>(o_sync.data()))), "Llama: decode step");
+        if (fused_sync.numel())
+            check(vkml_attend_fused_check(static_cast<std::uint32_t*>(const_cast<void*>(fused_sync.data())), u32(layers.size())),
+                  "Llama: decode step");
     }
 
     // One token: the state's token at the state's position.
@@ -414,7 +419,10 @@ struct Llama::Impl {
                                   out, nullptr, nullptr),
                   t);
         };
-        for (const Layer& L : layers) {
+        auto* fsync = fused_sync.numel() ? static_cast<std::uint32_t*>(fused_sync.data()) : nullptr;
+        const auto blocks = u32(layers.size());
+        for (std::size_t li = 0; li < layers.size(); ++li) {
+            const Layer& L = layers[li];
             const bool fold_qkv =
                 fold && std::all_of(L.qkv.begin(), L.qkv.end(), [&](const auto& wr) { return quantized_input(wr.first); });
             if (fold_qkv) {
@@ -431,7 +439,17 @@ struct Llama::Impl {
             const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), 0, 0, kv_code,
                                              u32(L.chunks()), c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
                                              1.0f / std::sqrt(static_cast<float>(hd)), c.attn_logit_softcap, u32(L.window)};
-            if (int_dot && o_q && L.o.int_dot_ok()) {
+            const bool merge_o = int_dot && o_q && L.o.int_dot_ok();
+            if (merge_o && fsync) {
+                // ... and the merge and the o projection + residual too (block
+                // li of the fused sync words, whose next block it zeroes)
+                const vkml_gemv_dot_params op{1, u32(L.o.rows), u32(L.o.cols), L.o.type_code(), L.o.scale_code()};
+                check(vkml_attend_step_fused(&sp, static_cast<const float*>(qkv.data()), static_cast<const float*>(rope.data()),
+                                             L.k_cache.data(), L.v_cache.data(), static_cast<float*>(partial.data()),
+                                             static_cast<float*>(stats.data()), static_cast<float*>(attn.data()), aq.data(),
+                                             static_cast<float*>(as.data()), st, &op, L.o.values(), L.o.scales(), xp, fsync, u32(li), blocks),
+                      "attention");
+            } else if (merge_o) {
                 // ... and the merge shares a launch with the o projection + residual
                 const vkml_gemv_dot_params op{1, u32(L.o.rows), u32(L.o.cols), L.o.type_code(), L.o.scale_code()};
                 check(vkml_attend_step_o(&sp, static_cast<const float*>(qkv.data()), static_cast<const float*>(rope.data()),
@@ -815,6 +833,10 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
     m.logits = f32(c.vocab_size);
     m.state = Tensor::zeros(context, {4}, DType::I32);
     m.o_sync = Tensor::zeros(context, {static_cast<std::int64_t>(vkml_attend_o_sync_bytes() / 4)}, DType::I32);
+    // Every layer's attention in one launch each (vkml_attend_step_fused)
+    // when every layer can take it: layer L uses block L and clears block L + 1.
+    if (m.layers.size() >= 2 && std::all_of(m.layers.begin(), m.layers.end(), [&](const auto& L) { return m.quantized_input(L.o); }))
+        m.fused_sync = Tensor::zeros(context, {static_cast<std::int64_t>(vkml_attend_fused_sync_bytes(u32(m.layers.size())) / 4)}, DType::I32);
     m.log = Tensor::zeros(context, {context_length}, DType::I32);
     m.chunks = (context_length + 127) / 128;
     m.partial = f32(c.num_heads * m.chunks * hd);

@@ -340,6 +340,27 @@ def bench_cfg3(L, steps=128, prompt_len=512):
         os.remove(path)
 
 
+def bench_short_position(L, path, contexts=(1024, 32768), prompt_len=512, steps=64):
+    """The cfg5 model decoding at positions 512.. with caches of different
+    lengths: a step launches the attention chunks its position needs, so
+    the rate should not fall with the cache's length."""
+    prompt = np.random.default_rng(5).integers(0, 32768, prompt_len).astype(np.int32)
+    out = {}
+    for ctx in contexts:
+        model = L.Llama(path, ctx, kv_f16=True)
+        first = int(np.argmax(model.forward(prompt)))
+        model.generate_greedy(first, 8)
+        model.rewind(prompt_len)
+        L.synchronize()
+        t0 = time.perf_counter()
+        model.generate_greedy(first, steps)
+        secs = time.perf_counter() - t0
+        model.close()
+        out[f"context_{ctx}"] = round(steps / secs, 1)
+        log(f"cfg5 decode at positions {prompt_len}..{prompt_len + steps} with a {ctx}-row cache: {steps / secs:.1f} tokens/s")
+    return {"tokens_per_s": out, "positions": [prompt_len, prompt_len + steps]}
+
+
 def matrix_macs(spec):
     """Multiply-accumulates of one token's layer projections (q|k|v, o,
     gate, up, down) over all layers: matmul_dot's work per prompt row."""
@@ -531,6 +552,7 @@ def main():
             configs = {"cfg2_gemv": bench_gemv_cfg2(), "cfg4_attention": bench_attention_cfg4()}
             model.close()
             model = None
+            configs["cfg5_short_position"] = bench_short_position(L, path)
             configs["cfg3"] = bench_cfg3(L)
 
         traffic = GATE_UP_TRAFFIC if sources_hash() == GATE_UP_TRAFFIC_SOURCES else None

@@ -480,7 +480,11 @@ int vkml_attend_o_check(uint32_t* d_sync);
  * on the stream take consecutive blocks, cyclically (in a model, layer L
  * takes block L of one block per layer). Other shapes: the chunk pass, the
  * merge and vkml_gemv_dot_add as separate launches, with the same block
- * bookkeeping. */
+ * bookkeeping. p->chunks may cover fewer keys than the cache (a launch sized
+ * for the position rather than the capacity): keys past kv_start + 128 *
+ * chunks are then not attended, and a step whose position reaches them
+ * raises the error vkml_attend_fused_check reports (the one launch only;
+ * the separate launches need chunks covering the cache). */
 uint64_t vkml_attend_fused_sync_bytes(uint32_t blocks);
 int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* d_qkv, const float* d_rope_table,
                            void* d_k_cache, void* d_v_cache, float* d_partial, float* d_stats, float* d_out,

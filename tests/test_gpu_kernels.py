@@ -591,6 +591,38 @@ def test_attend_step_fused_bit_exact(hd, heads, kvh, pos, kv_type, fmt, n, windo
         assert np.array_equal(bits(got), bits(x2.download(np.float32, n)))
 
 
+def test_attend_step_fused_reports_a_position_past_its_chunks():
+    # launched for 2 chunks (256 keys) at position 300: the step is flagged,
+    # every workgroup still ends (the o GEMV's waits stop at the flag), and
+    # the check clears the blocks for the next call
+    heads, kvh, hd, cap, n = 8, 4, 128, 512, 1024
+    rng = np.random.default_rng(3)
+    kc = dev(rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16))
+    vc = dev(rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16))
+    dtab = dev(O.rope_table(cap, hd, 1e6))
+    v, s_, _, _, _ = weights(H.Q4_K, n, heads * hd, 9)
+    x = dev(rng.standard_normal(n).astype(np.float32))
+    fbytes = H.lib().vkml_attend_fused_sync_bytes(2)
+    fsync = H.empty(fbytes)
+    H.call("vkml_fill_u32", p(fsync), 0, fbytes // 4)
+    part, stats = H.empty(heads * 4 * hd * 4), H.empty(heads * 4 * 8)
+    out, vals, scs = H.empty(heads * hd * 4), H.empty(heads * hd), H.empty(heads * hd // 32 * 4)
+    st = H.empty(16)
+    op = H.GemvDotParams(1, n, heads * hd, H.Q4_K, H.F16)
+    dq = dev(rng.standard_normal((heads + 2 * kvh) * hd).astype(np.float32))
+    for i, (chunks, pos, ok) in enumerate(((2, 300, False), (3, 300, True), (2, 255, True))):
+        print(f"fused chunks={chunks} pos={pos}", flush=True)
+        H.call("vkml_state_set", p(st), 0, pos, 0)
+        prm = H.AttendStepParams(heads, kvh, hd, cap, 0, 0, H.F16, chunks, 0, 1, 1.0 / math.sqrt(hd), 0.0, 0)
+        H.call("vkml_attend_step_fused", prm, p(dq), p(dtab), p(kc), p(vc), p(part), p(stats), p(out), p(vals), p(scs), p(st), op,
+               p(v), p(s_), p(x), p(fsync), i % 2, 2)
+        if ok:
+            H.call("vkml_attend_fused_check", p(fsync), 2)
+        else:
+            with pytest.raises(H.VkmlError, match="past the keys of the launched chunks"):
+                H.call("vkml_attend_fused_check", p(fsync), 2)
+
+
 def test_attend_step_fused_rejects_bad_blocks():
     prm = H.AttendStepParams(8, 8, 64, 64, 0, 0, H.F16, 1, 0, 1, 0.125, 0.0, 0)
     op = H.GemvDotParams(1, 256, 512, H.Q4_K, H.F16)

@@ -246,6 +246,35 @@ def test_decode_steps_across_chunk_boundaries_match_oracle(files, ctx, prompt, s
         assert np.array_equal(k[:, :n], kr[:, :n]) and np.array_equal(v[:, :n], vr[:, :n])
 
 
+def test_chunk_launch_follows_the_position(files):
+    """A 4096-row cache decoding near position 1000: each step launches the
+    128-key chunks its position needs, in powers of two (8 chunks up to
+    position 1023, then 16), not the cache's 32. Greedy steps and single
+    steps across the 1024 boundary, graph replays and eager launches, equal
+    the oracle's bit for bit."""
+    path = files["cfg5"]
+    tokens = np.random.default_rng(13).integers(0, 32768, 1000).astype(np.int32)
+    gpu = Llama(path, 4096, kv_f16=True)
+    eager = Llama(path, 4096, kv_f16=True, use_graphs=False)
+    ref = O.Model(path, 4096, kv_f16=True)
+    got = gpu.forward(tokens)
+    same(got, ref.forward(tokens))
+    same(eager.forward(tokens), got)
+    first = int(np.argmax(got))
+    toks, _ = greedy_oracle(ref, first, 30)
+    assert list(gpu.generate_greedy(first, 30)) == list(toks)
+    assert list(eager.generate_greedy(first, 30)) == list(toks)
+    assert gpu.position == 1030
+    for t in toks[-1:] + [5, 77]:
+        want = ref.forward(np.array([t], np.int32))
+        same(gpu.forward(np.array([t], np.int32)), want)
+        same(eager.forward(np.array([t], np.int32)), want)
+    for layer in range(2):
+        k, v = gpu.read_kv_cache(layer)
+        kr, vr = ref.kv_cache(layer)
+        assert np.array_equal(k[:, :1033], kr[:, :1033]) and np.array_equal(v[:, :1033], vr[:, :1033])
+
+
 def test_vkml_bench_app_results_are_exact():
     """bin/vkml-bench's decode, m-sweep and prefill cases (gemv_dot and the
     matrix-core matmul_dot) against the "quarters" closed form: every output

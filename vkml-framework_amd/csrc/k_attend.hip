@@ -269,6 +269,10 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
     const uint32_t pos = static_cast<uint32_t>(a.state->position);
     const uint32_t kv_len = pos + 1;
     if (a.window != 0 && kv_len > a.window) a.kv_start = max(a.kv_start, kv_len - a.window);
+    // Launched for fewer chunks than the cache holds: keys past them would
+    // be left out, so the launch reports it (the results are invalid).
+    if (L == 0 && threadIdx.x == 0 && kv_len - a.kv_start > a.chunks * kChunk)
+        __hip_atomic_store(f.error, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (a.kv_start + chunk * kChunk >= kv_len) {
         if (threadIdx.x < HPW) {  // past the live keys: a max of -inf, which the merge skips
             const uint64_t at = static_cast<uint64_t>(head0 + threadIdx.x) * a.chunks + chunk;
@@ -431,7 +435,7 @@ namespace {
 
 int check_step(const vkml_attend_step_params* p, const float* qkv, const float* rope_table, const void* k_cache, const void* v_cache,
                const float* partial, const float* stats, const float* out, const void* values, const float* scales,
-               const vkml_decode_state* state, const char* what) {
+               const vkml_decode_state* state, const char* what, bool fewer_chunks = false) {
     VKML_REQUIRE_INIT();
     const std::string w(what);
     VKML_CHECK_ARG(p, w + ": null params");
@@ -441,7 +445,7 @@ int check_step(const vkml_attend_step_params* p, const float* qkv, const float* 
     VKML_CHECK_ARG(state || (p->position < p->capacity && p->kv_start <= p->position),
                    w + ": position " + std::to_string(p->position) + " is outside the cache");
     const uint64_t span = p->window ? std::min<uint64_t>(p->window, p->capacity - p->kv_start) : p->capacity - p->kv_start;
-    VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= span && p->chunks <= kMergeMaxChunks,
+    VKML_CHECK_ARG((fewer_chunks ? p->chunks > 0 : static_cast<uint64_t>(p->chunks) * kChunk >= span) && p->chunks <= kMergeMaxChunks,
                    w + ": " + std::to_string(p->chunks) + " chunks do not cover the " + std::to_string(span) + " keys a step can see (or exceed " +
                        std::to_string(kMergeMaxChunks) + ")");
     VKML_CHECK_ARG(qkv && rope_table && k_cache && v_cache && partial && stats && out, w + ": null buffer");
@@ -512,7 +516,8 @@ int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* qkv, c
                            float* partial, float* stats, float* out, void* values, float* scales, const vkml_decode_state* state,
                            const vkml_gemv_dot_params* o, const void* o_values, const void* o_scales, float* x, uint32_t* sync,
                            uint32_t block, uint32_t blocks) {
-    if (int r = check_step(p, qkv, rope_table, k_cache, v_cache, partial, stats, out, values, scales, state, "attend_step_fused")) return r;
+    if (int r = check_step(p, qkv, rope_table, k_cache, v_cache, partial, stats, out, values, scales, state, "attend_step_fused", true))
+        return r;
     VKML_CHECK_ARG(state, "attend_step_fused: needs the decode state");
     VKML_CHECK_ARG(o && values && scales && o_values && o_scales && x && sync, "attend_step_fused: null buffer");
     VKML_CHECK_ARG(blocks >= 2 && block < blocks, "attend_step_fused: block " + std::to_string(block) + " of " + std::to_string(blocks) +
@@ -530,7 +535,13 @@ int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* qkv, c
             return vkml::abi::check_launch("attend_step_fused");
     }
     // Shapes the one launch does not take: the chunk pass, the merge and the
-    // o GEMV; the next block's counters zeroed all the same.
+    // o GEMV (over every chunk of the cache); the next block's counters
+    // zeroed all the same.
+    {
+        const uint64_t span = p->window ? std::min<uint64_t>(p->window, p->capacity - p->kv_start) : p->capacity - p->kv_start;
+        VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= span,
+                       "attend_step_fused: these weights take separate launches, which need chunks covering the cache");
+    }
     {
         vkml::abi::ProfileScope prof("attend_step");
         launch_chunks(p->head_dim, p->kv_type == VKML_F16, args);
@@ -554,10 +565,14 @@ int vkml_attend_fused_check(uint32_t* sync, uint32_t blocks) {
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_fused_check");
     if (flag == 0) return VKML_OK;
-    // A wait gave up: every block starts over (flag and counters).
+    // A wait gave up, or a position outran the chunks: every block starts
+    // over (flag and counters).
     e = hipMemsetAsync(sync, 0, vkml_attend_fused_sync_bytes(blocks), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_fused_check");
+    if (flag == 2)
+        return vkml::abi::fail(VKML_ERROR_DEVICE,
+                               "attend_step_fused: a position lay past the keys of the launched chunks; the step's results are invalid");
     return vkml::abi::fail(VKML_ERROR_DEVICE,
                            "attend_step_fused: the o GEMV's wait for the merges timed out; the step's results are invalid");
 }

@@ -16,6 +16,7 @@
 // host round trip between tokens. A prompt of several tokens runs at once,
 // as the reference's Llama::run does (prefill below).
 #include <algorithm>
+#include <map>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -330,13 +331,28 @@ struct Llama::Impl {
     Tensor o_sync;      // vkml_attend_step_o: the merge + o launch's sync words
     Tensor fused_sync;  // vkml_attend_step_fused: a block per layer (empty: not used)
     std::int64_t chunks = 1;  // decode attention's 128-key chunks over the whole cache
-    std::uint64_t graph_logits = 0, graph_greedy = 0;
+    // With the one-launch attention on every layer, a step launches the
+    // chunks its position needs, in powers of two from kMinTier (each tier
+    // its own captured graph); 0: every chunk of the cache.
+    static constexpr std::int64_t kMinTier = 8;
+    bool tiered = false;
+    std::int64_t step_tier = 0;
+    std::map<std::pair<bool, std::int64_t>, std::uint64_t> graphs;  // (greedy, tier) -> captured step
 
     const Weight& lm_head() const { return tied ? embed : *lm_head_own; }
 
     ~Impl() {
-        if (graph_logits) (void)vkml_graph_destroy(graph_logits);
-        if (graph_greedy) (void)vkml_graph_destroy(graph_greedy);
+        for (const auto& [key, g] : graphs) (void)vkml_graph_destroy(g);
+    }
+
+    // The chunk tier of a step at position pos: 128-key chunks covering its
+    // pos + 1 keys, rounded up to a power of two (0 when not tiered).
+    std::int64_t tier_for(std::int64_t pos) const {
+        if (!tiered) return 0;
+        const std::int64_t need = (pos + 1 + 127) / 128;
+        std::int64_t t = kMinTier;
+        while (t < need) t *= 2;
+        return t;
     }
 
     void tag(const char* t) const { (void)vkml_set_profile_tag(t); }
@@ -436,10 +452,11 @@ struct Llama::Impl {
             const uint32_t kv_code = detail::type_code(L.k_cache.dtype());
             // rope, append and attention in one launch, then the merge
             tag("attention");
-            const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), 0, 0, kv_code,
-                                             u32(L.chunks()), c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
-                                             1.0f / std::sqrt(static_cast<float>(hd)), c.attn_logit_softcap, u32(L.window)};
             const bool merge_o = int_dot && o_q && L.o.int_dot_ok();
+            const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), 0, 0, kv_code,
+                                             u32(merge_o && fsync && step_tier ? std::min(L.chunks(), step_tier) : L.chunks()),
+                                             c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
+                                             1.0f / std::sqrt(static_cast<float>(hd)), c.attn_logit_softcap, u32(L.window)};
             if (merge_o && fsync) {
                 // ... and the merge and the o projection + residual too (block
                 // li of the fused sync words, whose next block it zeroes)
@@ -677,13 +694,15 @@ struct Llama::Impl {
         tag("");
     }
 
-    void run_step(bool greedy) {
-        const bool graphs = options.use_graphs && !vkml_get_profiling();
-        if (!graphs) {
+    // The decode step at position pos (the state's position).
+    void run_step(bool greedy, std::int64_t pos) {
+        step_tier = tier_for(pos);
+        const bool use_graphs = options.use_graphs && !vkml_get_profiling();
+        if (!use_graphs) {
             step(greedy);
             return;
         }
-        std::uint64_t& g = greedy ? graph_greedy : graph_logits;
+        std::uint64_t& g = graphs[{greedy, step_tier}];
         if (!g) {
             check(vkml_graph_begin(), "Llama: graph capture");
             try {
@@ -837,6 +856,11 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
     // when every layer can take it: layer L uses block L and clears block L + 1.
     if (m.layers.size() >= 2 && std::all_of(m.layers.begin(), m.layers.end(), [&](const auto& L) { return m.quantized_input(L.o); }))
         m.fused_sync = Tensor::zeros(context, {static_cast<std::int64_t>(vkml_attend_fused_sync_bytes(u32(m.layers.size())) / 4)}, DType::I32);
+    // Launches sized by position need the one launch on every layer (o
+    // weights q4_K, or q8_0 with f16 scales).
+    m.tiered = m.fused_sync.numel() && std::all_of(m.layers.begin(), m.layers.end(), [](const auto& L) {
+        return L.o.type_code() == VKML_Q4_K || (L.o.type_code() == VKML_Q8_0 && L.o.scale_code() == VKML_F16);
+    });
     m.log = Tensor::zeros(context, {context_length}, DType::I32);
     m.chunks = (context_length + 127) / 128;
     m.partial = f32(c.num_heads * m.chunks * hd);
@@ -857,7 +881,7 @@ Tensor Llama::forward(std::span<const std::int32_t> tokens) {
         // One token: the decode step (fused decode attention, llama.cpp:
         // 366 with attention.cpp:199-203).
         m.set_state(tokens[0], m.position);
-        m.run_step(false);
+        m.run_step(false, m.position);
         m.check_attend_o();
         m.ran_to(++m.position);
     } else {
@@ -875,7 +899,7 @@ Tensor Llama::forward_all(std::span<const std::int32_t> tokens) {
     Tensor out = Tensor::empty(*m.context, {t, m.config.vocab_size}, DType::F32);
     if (t == 1) {
         m.set_state(tokens[0], m.position);
-        m.run_step(false);
+        m.run_step(false, m.position);
         m.check_attend_o();
         m.ran_to(++m.position);
         check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward_all");
@@ -890,7 +914,7 @@ std::vector<std::int32_t> Llama::generate_greedy(std::int32_t first, std::int64_
     if (count <= 0) return {};
     m.check_room(count);
     m.set_state(first, m.position);
-    for (std::int64_t i = 0; i < count; ++i) m.run_step(true);
+    for (std::int64_t i = 0; i < count; ++i) m.run_step(true, m.position + i);
     std::vector<std::int32_t> out(static_cast<std::size_t>(count));
     check(vkml_memcpy_d2h(out.data(), m.log.data(), out.size() * 4), "Llama::generate_greedy");
     m.check_attend_o();

@@ -177,6 +177,13 @@ typedef struct vkml_dequantize_params {
 int vkml_dequantize(const vkml_dequantize_params* p, const void* d_values, const void* d_scales,
                     float* d_out);
 
+/* The largest k the one-row int8 GEMVs stage in LDS. Above it (any
+ * multiple of 32 for q8_0 / q4_0 / q4_1, of 256 for q4_K), vkml_gemv_dot
+ * and vkml_gemv_dot_add take the rows kernel, which reads the activation
+ * from memory, in the same order; the fused forms (SwiGLU, RMSNorm
+ * prologue) take k up to this bound. */
+#define VKML_GEMV_STAGED_MAX_K 32768u
+
 /* shaders/gemv_dot.comp, src/ops/matmul.cpp:225-245: c[m, n] = a_q[m] . b[n]
  * for m <= 8 rows of Q8_0 activations (f32 scales) and weights b [n, k] of
  * b_type Q8_0/Q4_0/Q4_1/Q4_K (scales F16, or F32 for Q8_0/Q4_0/Q4_1).

@@ -633,6 +633,31 @@ def test_attend_step_fused_rejects_bad_blocks():
                    p(b), block, blocks)
 
 
+@pytest.mark.parametrize("fmt,f16", [(H.Q8_0, True), (H.Q8_0, False), (H.Q4_0, True), (H.Q4_1, True), (H.Q4_K, True)])
+@pytest.mark.parametrize("k", [96, 4128, 33280])
+@pytest.mark.parametrize("m", [1, 3, 12])
+def test_int8_gemv_takes_every_k_the_reference_does(fmt, f16, k, m):
+    # k a multiple of 32 but not of 64 (an odd last block), and k past the
+    # LDS-staged bound (the rows kernel): gemv_dot (m <= 8), matmul_dot
+    # (m > 8) and, for one row, gemv_dot_add, bit for bit with the oracle
+    if fmt == H.Q4_K and k % 256:
+        pytest.skip("q4_K rows are whole 256-value super-blocks")
+    n = 72
+    v, s_, quant, words, scales = weights(fmt, n, k, k + m, f16_scales=f16)
+    a, aw, asc = activation(k, k + 7, m)
+    want = (O.gemv_dot if m <= 8 else O.matmul_dot)(quant, aw, asc, m, words, scales, n, k)
+    out = H.empty(m * n * 4)
+    prm = H.GemvDotParams(m, n, k, fmt, H.F16 if f16 else H.F32)
+    call = "vkml_gemv_dot" if m <= 8 else "vkml_matmul_dot"
+    H.call(call, prm, p(dev(aw)), p(v), p(out), p(s_), p(dev(asc)))
+    assert np.array_equal(bits(out.download(np.float32, (m, n))), bits(want))
+    if m == 1:
+        res = np.random.default_rng(k).standard_normal(n).astype(np.float32)
+        x = dev(res)
+        H.call("vkml_gemv_dot_add", prm, p(dev(aw)), p(v), p(x), p(s_), p(dev(asc)), p(x))
+        assert np.array_equal(bits(x.download(np.float32, n)), bits(res + want[0]))
+
+
 # ---------------------------------------------------------------- small ops
 
 def test_argmax_and_step_finish():

@@ -275,6 +275,25 @@ def test_chunk_launch_follows_the_position(files):
         assert np.array_equal(k[:, :1033], kr[:, :1033]) and np.array_equal(v[:, :1033], vr[:, :1033])
 
 
+@pytest.mark.parametrize("hidden,ffn", [(288, 544), (256, 33280)])
+def test_widths_off_the_64_grid_and_past_the_staged_bound_take_the_int8_path(tmp_path, hidden, ffn):
+    """q8_0 matrices whose K is 32 mod 64 (hidden 288, ffn 544) or above the
+    LDS-staged bound (ffn 33280): the reference takes its int8 path for every
+    K a multiple of 32 (matmul.cpp:226-259), so prompts of 6 rows (gemv_dot)
+    and 12 rows (matmul_dot) and decode steps equal the oracle's int8 path
+    bit for bit."""
+    spec = synth.ModelSpec(f"odd-{hidden}-{ffn}", 2, hidden, 4, 2, 64, ffn, 1000, 10000.0, max_positions=256,
+                           matrix_type=gguf.Q8_0, embed_type=gguf.Q8_0, output_type=gguf.Q8_0)
+    path = synth.write_model(spec, str(tmp_path / "odd.gguf"), seed=14)
+    tokens = np.random.default_rng(14).integers(0, 1000, 22).astype(np.int32)
+    for prompt in (6, 12):
+        gpu = Llama(path, 64, kv_f16=True)
+        ref = O.Model(path, 64, kv_f16=True)
+        same(gpu.forward(tokens[:prompt]), ref.forward(tokens[:prompt]))
+        for t in tokens[prompt:prompt + 4]:
+            same(gpu.forward(np.array([t])), ref.forward(np.array([t])))
+
+
 def test_vkml_bench_app_results_are_exact():
     """bin/vkml-bench's decode, m-sweep and prefill cases (gemv_dot and the
     matrix-core matmul_dot) against the "quarters" closed form: every output

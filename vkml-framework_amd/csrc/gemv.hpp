@@ -45,7 +45,7 @@ namespace vkml::gemv {
 
 using namespace vkml::dev;
 
-constexpr uint32_t kMaxK = 32768;  // LDS staging: K + K / 16 * 4 + K / 32 * 4 bytes
+constexpr uint32_t kMaxK = VKML_GEMV_STAGED_MAX_K;  // LDS staging: K + K / 16 * 8 bytes
 constexpr uint32_t kLow = 0x0F0F0F0Fu;
 
 struct GemvArgs {

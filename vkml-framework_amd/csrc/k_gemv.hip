@@ -84,17 +84,17 @@ int dispatch_format(uint32_t b_type, uint32_t scale_type, const GemvArgs& g, con
     }
 }
 
-int check_dot_params(const vkml_gemv_dot_params* p, const char* what) {
+int check_dot_params(const vkml_gemv_dot_params* p, const char* what, bool any_k = false) {
     VKML_REQUIRE_INIT();
     VKML_CHECK_ARG(p, std::string(what) + ": null params");
     VKML_CHECK_ARG(p->b_type == VKML_Q8_0 || p->b_type == VKML_Q4_0 || p->b_type == VKML_Q4_1 || p->b_type == VKML_Q4_K,
                    std::string(what) + ": weights must be q8_0, q4_0, q4_1 or q4_K, got type " + std::to_string(p->b_type));
     VKML_CHECK_ARG(p->b_type == VKML_Q4_K || p->scale_type == VKML_F16 || p->scale_type == VKML_F32,
                    std::string(what) + ": scales must be f16 or f32");
-    const uint32_t unit = p->b_type == VKML_Q4_K ? 256 : 64;
-    VKML_CHECK_ARG(p->k > 0 && p->k % unit == 0 && p->k <= kMaxK,
+    const uint32_t unit = p->b_type == VKML_Q4_K ? 256 : 32;
+    VKML_CHECK_ARG(p->k > 0 && p->k % unit == 0 && (any_k || p->k <= kMaxK),
                    std::string(what) + ": k = " + std::to_string(p->k) + " must be a positive multiple of " +
-                       std::to_string(unit) + " up to " + std::to_string(kMaxK));
+                       std::to_string(unit) + (any_k ? std::string() : " up to " + std::to_string(kMaxK)));
     return VKML_OK;
 }
 
@@ -143,7 +143,8 @@ __global__ void __launch_bounds__(256) k_gemv_dot_rows(GemvArgs g, uint32_t m) {
     for (uint32_t i = 0; i < 8; ++i) {
         if (i >= m) break;
         const float v = row_tree<FMT, LPR>(acc[i]);
-        if (l == 0 && out_row < g.n) g.out[static_cast<uint64_t>(i) * g.n + out_row] = v;
+        // + residual (one activation row): add(x, y), llama.cpp:374,386
+        if (l == 0 && out_row < g.n) g.out[static_cast<uint64_t>(i) * g.n + out_row] = g.residual ? ldg(g.residual + out_row) + v : v;
     }
 }
 
@@ -225,11 +226,11 @@ extern "C" {
 
 int vkml_gemv_dot(const vkml_gemv_dot_params* p, const void* a_values, const void* b_values, float* out,
                   const void* b_scales, const float* a_scales) {
-    if (int r = check_dot_params(p, "gemv_dot")) return r;
+    if (int r = check_dot_params(p, "gemv_dot", true)) return r;
     VKML_CHECK_ARG(p->m >= 1 && p->m <= 8, "gemv_dot: m must be 1 to 8, got " + std::to_string(p->m));
     if (p->n == 0) return VKML_OK;
     VKML_CHECK_ARG(a_values && b_values && out && b_scales && a_scales, "gemv_dot: null buffer");
-    if (p->m > 1) {
+    if (p->m > 1 || p->k > kMaxK) {
         const GemvArgs g{static_cast<const uint4*>(a_values), a_scales, b_values, b_scales, nullptr, nullptr, out, nullptr, p->n, p->k};
         return dispatch_rows(p->b_type, p->scale_type, g, p->m);
     }
@@ -239,11 +240,12 @@ int vkml_gemv_dot(const vkml_gemv_dot_params* p, const void* a_values, const voi
 
 int vkml_gemv_dot_add(const vkml_gemv_dot_params* p, const void* a_values, const void* b_values, float* out,
                       const void* b_scales, const float* a_scales, const float* residual) {
-    if (int r = check_dot_params(p, "gemv_dot_add")) return r;
+    if (int r = check_dot_params(p, "gemv_dot_add", true)) return r;
     VKML_CHECK_ARG(p->m == 1, "gemv_dot_add: m must be 1");
     if (p->n == 0) return VKML_OK;
     VKML_CHECK_ARG(a_values && b_values && out && b_scales && a_scales && residual, "gemv_dot_add: null buffer");
     GemvArgs g{static_cast<const uint4*>(a_values), a_scales, b_values, b_scales, nullptr, nullptr, out, residual, p->n, p->k};
+    if (p->k > kMaxK) return dispatch_rows(p->b_type, p->scale_type, g, 1);  // the activation read from memory
     return dispatch_format<kAdd>(p->b_type, p->scale_type, g, "gemv_dot_add");
 }
 

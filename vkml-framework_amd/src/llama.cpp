@@ -55,7 +55,11 @@ struct Weight {
     std::uint32_t scale_code() const { return q.type == QuantType::q4_K ? std::uint32_t(VKML_F16) : detail::type_code(q.scales.dtype()); }
     const void* values() const { return quantized ? q.values.data() : t.data(); }
     const void* scales() const { return quantized ? q.scales.data() : nullptr; }
-    bool int_dot_ok() const { return quantized && cols % (q.type == QuantType::q4_K ? 256 : 64) == 0 && cols <= 32768; }
+    // The int8 path takes K a multiple of 32 (q4_K: 256), as the reference's
+    // (matmul.cpp:226-259); above VKML_GEMV_STAGED_MAX_K only gemv_dot and
+    // gemv_dot_add, whose rows kernel reads the activation from memory.
+    bool int_dot_ok() const { return quantized && cols % (q.type == QuantType::q4_K ? 256 : 32) == 0; }
+    bool staged_ok() const { return int_dot_ok() && cols <= VKML_GEMV_STAGED_MAX_K; }
 };
 
 // Host-side form of a matrix before upload: bytes of values and scales.
@@ -486,7 +490,8 @@ struct Llama::Impl {
             auto* hp = static_cast<float*>(h.data());
             const bool down_q = quantized_input(L.down) && ff % 32 == 0;
             bool h_quantized = false;
-            if (quantized_input(L.gate) && quantized_input(L.up) && L.gate.type_code() == L.up.type_code() && quant_d) {
+            if (quantized_input(L.gate) && quantized_input(L.up) && L.gate.staged_ok() && L.up.staged_ok() &&
+                L.gate.type_code() == L.up.type_code() && quant_d) {
                 // gate|up GEMV + SwiGLU (+ the ffn norm before, + Q8_0 of h after)
                 if (!fold) norm(L.ffn_norm, "ffn_norm");
                 tag("gate_up");

@@ -391,7 +391,7 @@ Tensor matmul_transposed(const Tensor& a, const QuantizedMatrix& b) {
     const std::int64_t m = product(as, as.size() - 1);
     const std::uint32_t type = quant_code(b.type), st = scale_code(b);
     detail::Runtime& rt = TensorAccess::runtime(a);
-    const bool dot_ok = b.cols % (b.type == QuantType::q4_K ? 256 : 64) == 0;
+    const bool dot_ok = b.cols % (b.type == QuantType::q4_K ? 256 : 32) == 0;  // every matrix the reference's int8 path takes
     float* c = static_cast<float*>(out.data());
     if (rt.integer_dot() && dot_ok) {
         // Quantize a too and multiply int8 by int8 (matmul.cpp:225-259):

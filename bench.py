@@ -230,9 +230,10 @@ def filled(nbytes, word):
 def bench_gemv_cfg2(min_bytes=512 << 20):
     """cfg2: y = W x for W 4096x4096, 14336x4096 and 4096x14336 in Q8_0 and
     Q4_K, x f32. Two figures each: the GEMV kernel on the Q8_0 activation
-    (the decode step's unit of work), and the op as matmul_transposed runs
-    it (the activation quantized, then the GEMV). Algorithmic bytes are the
-    GGUF-native weight bytes plus x in and y out."""
+    (the decode step's unit of work), and the op on the f32 x as
+    matmul_transposed runs it for one row (k <= 4096: the Q8_0 of x inside
+    the GEMV, one launch; else the activation quantized, then the GEMV).
+    Algorithmic bytes are the GGUF-native weight bytes plus x in and y out."""
     from vkml_amd import hip as H
     out = []
     for fmt in ("q8_0", "q4_K"):
@@ -251,9 +252,14 @@ def bench_gemv_cfg2(min_bytes=512 << 20):
             H.call("vkml_quantize", qp, x.p, xq.p, xs.p)
             kern = rotation_times(copies, lambda i: H.call("vkml_gemv_dot", dp, xq.p, mats[i][0].p, y.p, mats[i][1].p, xs.p))
 
+            fp = H.GemvFusedParams(n, k, bt, H.F16, 0, 2, 0.0, 0)
+
             def op(i):
-                H.call("vkml_quantize", qp, x.p, xq.p, xs.p)
-                H.call("vkml_gemv_dot", dp, xq.p, mats[i][0].p, y.p, mats[i][1].p, xs.p)
+                if k <= 4096:
+                    H.call("vkml_gemv_fused", fp, x.p, None, None, mats[i][0].p, mats[i][1].p, None, None, None, y.p, None, None)
+                else:
+                    H.call("vkml_quantize", qp, x.p, xq.p, xs.p)
+                    H.call("vkml_gemv_dot", dp, xq.p, mats[i][0].p, y.p, mats[i][1].p, xs.p)
             opt = rotation_times(copies, op)
             alg = wbytes + 4 * k + 4 * n
             out.append({"format": fmt, "n": n, "k": k, "bytes": alg,
@@ -262,7 +268,7 @@ def bench_gemv_cfg2(min_bytes=512 << 20):
                         "op_us": {"best": round(opt[0], 3), "median": round(opt[1], 3)},
                         "op_frac": round(alg / (opt[0] * 1e-6) / 1e9 / PEAK_HBM, 4)})
             log(f"cfg2 {fmt} {n}x{k}: gemv {kern[0]:.2f} us ({alg / (kern[0] * 1e-6) / 1e9:.0f} GB/s), "
-                f"quantize + gemv {opt[0]:.2f} us")
+                f"f32 x to y {opt[0]:.2f} us ({'one launch' if k <= 4096 else 'quantize + gemv'})")
             for m in mats:
                 for b in m:
                     b.close()

@@ -233,6 +233,21 @@ def test_gemv_dot_add_and_swiglu(fmt):
     assert np.array_equal(bits(got), bits(O.silu(g) * u))
 
 
+@pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 4096, 4096), (H.Q4_K, 384, 256), (H.Q8_0, 4096, 4096), (H.Q4_0, 1024, 2048),
+                                     (H.Q4_1, 72, 96), (H.Q8_0, 72, 96)])
+def test_gemv_fused_quantize_prologue_bit_exact(fmt, n, k):
+    # norm = 2: the Q8_0 of the f32 row inside the GEMV (the ops API's one
+    # launch for a row), against quantize.comp + gemv_dot in the oracle
+    v, s, quant, words, scales = weights(fmt, n, k, n + 11)
+    a = (np.random.default_rng(k + 1).standard_normal(k) * 3).astype(np.float32)
+    aw, asc = O.quantize(O.Q8_0, a.reshape(1, k), False)
+    want = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)[0]
+    out = H.empty(n * 4)
+    prm = H.GemvFusedParams(n, k, fmt, H.F16, 0, 2, 0.0, 0)
+    H.call("vkml_gemv_fused", prm, p(dev(a)), None, None, p(v), p(s), None, None, None, p(out), None, None)
+    assert np.array_equal(bits(out.download(np.float32, n)), bits(want))
+
+
 @pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 6144, 4096), (H.Q4_K, 384, 256), (H.Q8_0, 8192, 4096), (H.Q4_0, 1024, 2048)])
 def test_gemv_fused_norm_prologue_bit_exact(fmt, n, k):
     # rms_norm + Q8_0 inside the GEMV == the separate kernels' results

@@ -59,7 +59,8 @@ struct GemvArgs {
     const float* residual;
     uint32_t n, k;
     // With the RMSNorm prologue: the f32 input row, its norm weight and eps
-    // (the activation codes are then computed, not read).
+    // (the activation codes are then computed, not read); a null norm
+    // weight: Q8_0 of the row itself, no norm.
     const float* x;
     const float* norm_weight;
     float eps;
@@ -415,9 +416,9 @@ __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint3
     for (uint32_t i = 0; i < NormLoads<T>::Q4; ++i) {
         const uint32_t q = min(t + T * i, K / 4 - 1);
         r.xq[i] = ld_f32x4<COH>(reinterpret_cast<const float4*>(x) + q);
-        r.wq[i] = ldg(reinterpret_cast<const float4*>(w) + q);
+        r.wq[i] = w ? ldg(reinterpret_cast<const float4*>(w) + q) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
-    if (T <= 256 || t < 256) {  // threads past the 256 invocations load none
+    if (w && (T <= 256 || t < 256)) {  // threads past the 256 invocations load none; no sum without the norm
 #pragma unroll
         for (uint32_t v = 0; v < NormLoads<T>::V; ++v)
 #pragma unroll
@@ -426,29 +427,33 @@ __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint3
 }
 
 template <uint32_t T>
-__device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float2* s_ss, float* s_red) {
+__device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float2* s_ss, float* s_red,
+                                       bool norm = true) {
 #pragma clang fp contract(off)
     static_assert(T >= 128 && T % 64 == 0, "workgroup width");
     const uint32_t t = thread_index();
+    float scale = 1.0f;  // without the norm (quantize.comp on x itself): unused
+    if (norm) {
 #pragma unroll
-    for (uint32_t v = 0; v < NormLoads<T>::V; ++v) {
-        const uint32_t inv = t + v * T;
-        float part = 0.0f;
+        for (uint32_t v = 0; v < NormLoads<T>::V; ++v) {
+            const uint32_t inv = t + v * T;
+            float part = 0.0f;
 #pragma unroll
-        for (uint32_t j = 0; j < NormLoads<T>::kMaxPer; ++j)
-            if (inv + 256 * j < K) part += r.xv[v][j] * r.xv[v][j];
-        if (inv < 256) s_red[inv] = part;
+            for (uint32_t j = 0; j < NormLoads<T>::kMaxPer; ++j)
+                if (inv + 256 * j < K) part += r.xv[v][j] * r.xv[v][j];
+            if (inv < 256) s_red[inv] = part;
+        }
+        // The halving tree over the 256 invocations: strides 128, 64, then 32 .. 1 in wave 0.
+        __syncthreads();
+        if (t < 128) s_red[t] = s_red[t] + s_red[t + 128];
+        __syncthreads();
+        if (t < 64) {
+            const float v = tree_to_first<64>(s_red[t] + s_red[t + 64]);
+            if (t == 0) s_red[256] = v;
+        }
+        __syncthreads();
+        scale = 1.0f / sqrtf(s_red[256] / static_cast<float>(K) + eps);
     }
-    // The halving tree over the 256 invocations: strides 128, 64, then 32 .. 1 in wave 0.
-    __syncthreads();
-    if (t < 128) s_red[t] = s_red[t] + s_red[t + 128];
-    __syncthreads();
-    if (t < 64) {
-        const float v = tree_to_first<64>(s_red[t] + s_red[t + 64]);
-        if (t == 0) s_red[256] = v;
-    }
-    __syncthreads();
-    const float scale = 1.0f / sqrtf(s_red[256] / static_cast<float>(K) + eps);
     uint32_t* s_words = reinterpret_cast<uint32_t*>(s_codes);
 #pragma unroll
     for (uint32_t i = 0; i < NormLoads<T>::Q4; ++i) {
@@ -458,7 +463,7 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
         float absmax = 0.0f;
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e) {
-            y[e] = xs[e] * scale * ws[e];
+            y[e] = norm ? xs[e] * scale * ws[e] : xs[e];  // without the norm: quantize.comp on x itself
             absmax = fmaxf(absmax, fabsf(y[e]));
         }
         absmax = group_max<8>(absmax);  // the block's 8 lanes (T is a multiple of 8)
@@ -714,7 +719,7 @@ __device__ __forceinline__ void stage_store(const GemvArgs& g, uint4* smem, cons
     const uint32_t halves = K / 16, t = thread_index();
     if constexpr (NORM) {
         float* s_red = reinterpret_cast<float*>(s_ss + K / 16);  // 257 floats
-        norm_quantize_prologue<T>(r, g.eps, K, s_codes, s_ss, s_red);
+        norm_quantize_prologue<T>(r, g.eps, K, s_codes, s_ss, s_red, g.norm_weight != nullptr);
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

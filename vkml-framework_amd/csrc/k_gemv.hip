@@ -271,16 +271,18 @@ int vkml_gemv_fused(const vkml_gemv_fused_params* p, const void* a, const float*
     VKML_CHECK_ARG(p->epilogue <= 2, "gemv_fused: epilogue must be 0 (store), 1 (+ residual) or 2 (SwiGLU)");
     VKML_CHECK_ARG(!p->quantize_out || p->epilogue == 2, "gemv_fused: quantize_out needs the SwiGLU epilogue");
     VKML_CHECK_ARG(!p->quantize_out || p->n % 32 == 0, "gemv_fused: quantize_out needs n a multiple of 32");
-    VKML_CHECK_ARG(!p->norm || p->k <= 4096, "gemv_fused: the RMSNorm prologue takes k up to 4096");
-    VKML_CHECK_ARG(!(p->norm && p->epilogue == 1), "gemv_fused: the RMSNorm prologue goes with the store or SwiGLU epilogue");
+    VKML_CHECK_ARG(p->norm <= 2, "gemv_fused: norm must be 0 (quantized input), 1 (RMSNorm + Q8_0) or 2 (Q8_0)");
+    VKML_CHECK_ARG(!p->norm || p->k <= 4096, "gemv_fused: the RMSNorm / Q8_0 prologue takes k up to 4096");
+    VKML_CHECK_ARG(!(p->norm && p->epilogue == 1), "gemv_fused: the RMSNorm / Q8_0 prologue goes with the store or SwiGLU epilogue");
     if (p->n == 0) return VKML_OK;
     VKML_CHECK_ARG(a && b_values && b_scales && out, "gemv_fused: null buffer");
-    VKML_CHECK_ARG(p->norm ? norm_weight != nullptr : a_scales != nullptr, "gemv_fused: the input needs its norm weight or scales");
+    VKML_CHECK_ARG(p->norm == 1 ? norm_weight != nullptr : p->norm == 2 || a_scales != nullptr,
+                   "gemv_fused: the input needs its norm weight or scales");
     VKML_CHECK_ARG(p->epilogue != 1 || residual, "gemv_fused: the residual epilogue needs the residual");
     VKML_CHECK_ARG(p->epilogue != 2 || (b2_values && b2_scales), "gemv_fused: SwiGLU needs the up matrix");
     VKML_CHECK_ARG(!p->quantize_out || (out_values && out_scales), "gemv_fused: quantize_out needs its buffers");
     GemvArgs g{p->norm ? nullptr : static_cast<const uint4*>(a), a_scales, b_values, b_scales, b2_values, b2_scales, out, residual,
-               p->n, p->k, p->norm ? static_cast<const float*>(a) : nullptr, norm_weight, p->eps,
+               p->n, p->k, p->norm ? static_cast<const float*>(a) : nullptr, p->norm == 1 ? norm_weight : nullptr, p->eps,
                static_cast<uint8_t*>(out_values), out_scales};
     const char* label = "gemv_fused";
     switch (p->epilogue) {

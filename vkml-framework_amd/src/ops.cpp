@@ -393,6 +393,14 @@ Tensor matmul_transposed(const Tensor& a, const QuantizedMatrix& b) {
     detail::Runtime& rt = TensorAccess::runtime(a);
     const bool dot_ok = b.cols % (b.type == QuantType::q4_K ? 256 : 32) == 0;  // every matrix the reference's int8 path takes
     float* c = static_cast<float*>(out.data());
+    if (rt.integer_dot() && dot_ok && m == 1 && b.cols <= 4096) {
+        // One row: the Q8_0 of a computed inside the GEMV (one launch).
+        const vkml_gemv_fused_params p{u32(b.rows), u32(b.cols), type, st, 0, 2, 0.0f, 0};
+        check(vkml_gemv_fused(&p, a.data(), nullptr, nullptr, b.values.data(), b.scales.data(), nullptr, nullptr, nullptr, c, nullptr,
+                              nullptr),
+              "matmul_transposed");
+        return out;
+    }
     if (rt.integer_dot() && dot_ok) {
         // Quantize a too and multiply int8 by int8 (matmul.cpp:225-259):
         // gemv_dot for up to 8 rows, matmul_dot on the matrix cores beyond.

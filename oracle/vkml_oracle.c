@@ -113,13 +113,6 @@ uint16_t orc_f32_to_f16(float f) {
 
 float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); } /* halves.glsl:93 */
 
-/* shaders/cast.comp:30-35 (to_bf16). */
-uint16_t orc_f32_to_bf16(float f) {
-    const uint32_t bits = f2u(f);
-    if ((bits & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((bits >> 16) | 0x40u);
-    return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
-}
-
 /* e^x as a fixed sequence of f32 operations, shared bit for bit with the GPU
  * kernels. The reference calls GLSL exp (unary.comp:22, attend.comp:129,
  * attend_merge.comp:34, softmax.comp), whose accuracy its driver defines:

@@ -46,7 +46,6 @@ int orc_get_threads(void);
 float orc_f16_to_f32(uint16_t h);
 uint16_t orc_f32_to_f16(float f);
 float orc_bf16_to_f32(uint16_t h);
-uint16_t orc_f32_to_bf16(float f); /* shaders/cast.comp:30-35 */
 void orc_cast_f32_to_f16(const float* x, uint16_t* y, int64_t n);
 void orc_cast_f16_to_f32(const uint16_t* x, float* y, int64_t n);
 

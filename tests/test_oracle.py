@@ -608,3 +608,31 @@ def test_sliding_attention_over_a_ring_equals_it_over_the_whole_cache(hd, f16, s
         assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want))), (start, n)
         start += n
     assert start == total
+
+
+def test_a_handed_over_cache_continues_as_the_prompt_would(tiny_q4k):
+    """orc_model_set_kv + set_position (how the full-size tests hand the
+    GPU's prefilled cache to the oracle): a model given another's caches
+    after a prompt, at the prompt's end, decodes exactly as the model that
+    ran the prompt; with one layer's cache disturbed, it does not."""
+    prompt = np.random.default_rng(21).integers(0, 1000, 13).astype(np.int32)
+    ran = O.Model(tiny_q4k, 32, kv_f16=True)
+    ran.forward(prompt)
+    caches = [ran.kv_cache(layer) for layer in range(2)]
+    given = O.Model(tiny_q4k, 32, kv_f16=True)
+    for layer, (k, v) in enumerate(caches):
+        given.set_kv(layer, k, v)
+    given.set_position(len(prompt))
+    for t in (5, 9, 700):
+        a, b = ran.forward(np.array([t], np.int32)), given.forward(np.array([t], np.int32))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    off = O.Model(tiny_q4k, 32, kv_f16=True)
+    k, v = caches[1]
+    k = k.copy()
+    k[0, 3] ^= 0x0400  # one f16 exponent bit of one key element
+    off.set_kv(0, *caches[0])
+    off.set_kv(1, k, v)
+    off.set_position(len(prompt))
+    ref = O.Model(tiny_q4k, 32, kv_f16=True)
+    ref.forward(prompt)
+    assert not np.array_equal(ref.forward(np.array([5], np.int32)), off.forward(np.array([5], np.int32)))

@@ -461,16 +461,20 @@ void launch_tiles(const MatmulDotArgs& p) {
 }
 
 // The 64 x 128 tile with its operands staged in LDS (2x the direct-load
-// kernel at large prompts) wherever it gives the SIMDs half a wave each;
-// below that, the largest direct-load tile that still gives them about two
-// waves each. (Measured: the staged tile wins from 512 of its waves on; at
-// 128 rows x 14336 columns the 32 x 32 tile beats 64 x 32 with half the
-// waves and 32 x 16 with twice as many.)
+// kernel at large prompts) wherever it gives every CU about four
+// workgroups; below that the 32 x 128 staged tile, wherever it gives the
+// SIMDs half a wave each; below that, the largest direct-load tile that
+// still gives them about two waves each. (Measured: the staged tiles win
+// from 512 of their waves on; a 512-token cfg5 prompt's projections take
+// 21.6 ms with 32 x 128 tiles against 27.3 ms with 64 x 128, a 4096-token
+// prompt's 140 ms against 146 ms the other way round; at 128 rows x 14336
+// columns the 32 x 32 tile beats 64 x 32 with half the waves and 32 x 16
+// with twice as many.)
 template <int FMT, bool F16S>
 void launch(const MatmulDotArgs& p) {
     const auto waves = [&](uint64_t rt, uint64_t ct) { return ((p.m + 16 * rt - 1) / (16 * rt)) * ((p.n + 16 * ct - 1) / (16 * ct)); };
     constexpr uint64_t kEnough = 1792;  // 256 CUs x 4 SIMDs x 1.75
-    if (waves(4, 2) >= 512) {
+    if (waves(4, 2) >= 4096) {
         const dim3 grid((p.n + 127) / 128, (p.m + 63) / 64);
         hipLaunchKernelGGL((k_matmul_dot_staged<FMT, F16S, 4>), grid, dim3(kT), 0, vkml::abi::stream(), p);
     } else if (waves(2, 2) >= 512) {

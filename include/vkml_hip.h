@@ -223,8 +223,9 @@ int vkml_gemv_dot_swiglu(const vkml_gemv_dot_params* p, const void* d_a_values,
  * binary/unary + quantize.comp after, as llama.cpp:313-386 dispatches them).
  * norm = 1: d_a is the f32 row x [k], RMS-normalized with d_norm_weight and
  * eps and quantized to Q8_0 inside the kernel (k <= 4096), bit for bit as
- * vkml_rms_norm_quantize; norm = 2: d_a is the f32 row, quantized to Q8_0
- * inside the kernel without a norm (k <= 4096), bit for bit as vkml_quantize
+ * vkml_rms_norm_quantize; norm = 2 (store epilogue only): d_a is the f32
+ * row, quantized to Q8_0 inside the kernel without a norm (k <= 4096), bit
+ * for bit as vkml_quantize
  * (quantize.comp; matmul.cpp:225-229's activation quantize folded into the
  * product); norm = 0: d_a / d_a_scales are its Q8_0 codes and
  * f32 scales. epilogue 0 stores y, 1 adds d_residual (not with norm), 2 is

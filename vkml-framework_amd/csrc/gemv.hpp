@@ -58,9 +58,8 @@ struct GemvArgs {
     float* out;
     const float* residual;
     uint32_t n, k;
-    // With the RMSNorm prologue: the f32 input row, its norm weight and eps
-    // (the activation codes are then computed, not read); a null norm
-    // weight: Q8_0 of the row itself, no norm.
+    // With the RMSNorm (or plain Q8_0) prologue: the f32 input row, its norm
+    // weight and eps (the activation codes are then computed, not read).
     const float* x;
     const float* norm_weight;
     float eps;
@@ -409,16 +408,16 @@ struct NormLoads {
     float xv[V][kMaxPer];                                  // its invocations' strided elements
 };
 
-template <uint32_t T, bool COH>
+template <uint32_t T, bool COH, bool PLAIN = false>
 __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint32_t K, NormLoads<T>& r) {
     const uint32_t t = thread_index();
 #pragma unroll
     for (uint32_t i = 0; i < NormLoads<T>::Q4; ++i) {
         const uint32_t q = min(t + T * i, K / 4 - 1);
         r.xq[i] = ld_f32x4<COH>(reinterpret_cast<const float4*>(x) + q);
-        r.wq[i] = w ? ldg(reinterpret_cast<const float4*>(w) + q) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        if constexpr (!PLAIN) r.wq[i] = ldg(reinterpret_cast<const float4*>(w) + q);
     }
-    if (w && (T <= 256 || t < 256)) {  // threads past the 256 invocations load none; no sum without the norm
+    if (!PLAIN && (T <= 256 || t < 256)) {  // threads past the 256 invocations load none; no sum without the norm
 #pragma unroll
         for (uint32_t v = 0; v < NormLoads<T>::V; ++v)
 #pragma unroll
@@ -426,14 +425,13 @@ __device__ __forceinline__ void norm_loads(const float* x, const float* w, uint3
     }
 }
 
-template <uint32_t T>
-__device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float2* s_ss, float* s_red,
-                                       bool norm = true) {
+template <uint32_t T, bool PLAIN = false>
+__device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_t K, uint4* s_codes, float2* s_ss, float* s_red) {
 #pragma clang fp contract(off)
     static_assert(T >= 128 && T % 64 == 0, "workgroup width");
     const uint32_t t = thread_index();
-    float scale = 1.0f;  // without the norm (quantize.comp on x itself): unused
-    if (norm) {
+    float scale = 1.0f;  // PLAIN (quantize.comp on x itself, no norm): unused
+    if constexpr (!PLAIN) {
 #pragma unroll
         for (uint32_t v = 0; v < NormLoads<T>::V; ++v) {
             const uint32_t inv = t + v * T;
@@ -458,12 +456,16 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
 #pragma unroll
     for (uint32_t i = 0; i < NormLoads<T>::Q4; ++i) {
         const uint32_t q = t + T * i;  // values 4q .. 4q + 3: block q / 8, half-block q / 4
-        const float xs[4] = {r.xq[i].x, r.xq[i].y, r.xq[i].z, r.xq[i].w}, ws[4] = {r.wq[i].x, r.wq[i].y, r.wq[i].z, r.wq[i].w};
+        const float xs[4] = {r.xq[i].x, r.xq[i].y, r.xq[i].z, r.xq[i].w};
+        float ws[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (!PLAIN) {
+            ws[0] = r.wq[i].x; ws[1] = r.wq[i].y; ws[2] = r.wq[i].z; ws[3] = r.wq[i].w;
+        }
         float y[4];
         float absmax = 0.0f;
 #pragma unroll
         for (uint32_t e = 0; e < 4; ++e) {
-            y[e] = norm ? xs[e] * scale * ws[e] : xs[e];  // without the norm: quantize.comp on x itself
+            y[e] = PLAIN ? xs[e] : xs[e] * scale * ws[e];  // PLAIN: quantize.comp on x itself
             absmax = fmaxf(absmax, fabsf(y[e]));
         }
         absmax = group_max<8>(absmax);  // the block's 8 lanes (T is a multiple of 8)
@@ -688,13 +690,15 @@ struct ActLoads {
     uint4 c[4];
     float sa[4];
 };
-template <uint32_t T, bool NORM>
-using StageLoads = std::conditional_t<NORM, NormLoads<T>, ActLoads<T>>;
+// NORM: 0, the activation's Q8_0 codes and scales are read; 1, RMSNorm +
+// Q8_0 of the f32 row g.x; 2, Q8_0 of g.x alone.
+template <uint32_t T, int NORM>
+using StageLoads = std::conditional_t<NORM != 0, NormLoads<T>, ActLoads<T>>;
 
-template <uint32_t T, bool NORM, bool COH>
+template <uint32_t T, int NORM, bool COH>
 __device__ __forceinline__ void stage_load(const GemvArgs& g, StageLoads<T, NORM>& r) {
-    if constexpr (NORM) {
-        norm_loads<T, COH>(g.x, g.norm_weight, g.k, r);
+    if constexpr (NORM != 0) {
+        norm_loads<T, COH, NORM == 2>(g.x, g.norm_weight, g.k, r);
     } else {
         const uint32_t halves = g.k / 16, t = thread_index();
 #pragma unroll
@@ -711,15 +715,15 @@ __device__ __forceinline__ void stage_load(const GemvArgs& g, StageLoads<T, NORM
 // (norm_quantize_prologue); otherwise the codes, and per half-block its
 // (code sum, block scale), with half-blocks past 4 T loaded here. Ends with
 // a barrier.
-template <uint32_t T, bool NORM, bool COH>
+template <uint32_t T, int NORM, bool COH>
 __device__ __forceinline__ void stage_store(const GemvArgs& g, uint4* smem, const StageLoads<T, NORM>& r) {
     const uint32_t K = g.k;
     uint4* s_codes = smem;                                     // K / 16 half-blocks of codes
     float2* s_ss = reinterpret_cast<float2*>(smem + K / 16);   // each half-block's (code sum, block scale)
     const uint32_t halves = K / 16, t = thread_index();
-    if constexpr (NORM) {
+    if constexpr (NORM != 0) {
         float* s_red = reinterpret_cast<float*>(s_ss + K / 16);  // 257 floats
-        norm_quantize_prologue<T>(r, g.eps, K, s_codes, s_ss, s_red, g.norm_weight != nullptr);
+        norm_quantize_prologue<T, NORM == 2>(r, g.eps, K, s_codes, s_ss, s_red);
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -752,7 +756,7 @@ __device__ __forceinline__ void stage_store(const GemvArgs& g, uint4* smem, cons
 }
 
 // stage_load then stage_store.
-template <uint32_t T, bool NORM, bool COH>
+template <uint32_t T, int NORM, bool COH>
 __device__ __forceinline__ void stage_activation(const GemvArgs& g, uint4* smem) {
     StageLoads<T, NORM> r;
     stage_load<T, NORM, COH>(g, r);

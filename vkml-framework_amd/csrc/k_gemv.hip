@@ -16,14 +16,14 @@ using namespace vkml::gemv;
 
 namespace {
 
-template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, bool NORM, bool QOUT, bool FULL>
+template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, int NORM, bool QOUT, bool FULL>
 __global__ void __launch_bounds__(T) k_gemv_dot(GemvArgs g) {
     extern __shared__ uint4 smem[];
     GemvRows<FMT, F16S, LPR, EPI, B, T, QOUT, false, 1, FULL> rows;
-    if constexpr (NORM) {
+    if constexpr (NORM != 0) {
         // (the norm prologue's loads after the weights': measured faster)
         rows.start(g, blockIdx.x);  // the first batch of weights is in flight while the activation is staged
-        stage_activation<T, true, false>(g, smem);
+        stage_activation<T, NORM, false>(g, smem);
     } else {
         StageLoads<T, false> act;
         stage_load<T, false, false>(g, act);  // first: staging waits for these alone
@@ -33,14 +33,14 @@ __global__ void __launch_bounds__(T) k_gemv_dot(GemvArgs g) {
     rows.finish(g, smem, staged_ss(smem, g.k));
 }
 
-template <int FMT, bool F16S, int LPR, int EPI, bool NORM, bool QOUT>
+template <int FMT, bool F16S, int LPR, int EPI, int NORM, bool QOUT>
 int launch(const GemvArgs& g, const char* label) {
     constexpr int B = LPR == 16 ? 4 : 2;  // rounds per batch (2 measured best at 32 lanes)
     // (512 threads with the norm prologue at 32 lanes: half the workgroups
     // redo RMSNorm + Q8_0 of x, each over twice the threads)
-    constexpr uint32_t T = QOUT ? 32 * LPR : LPR == 32 ? (NORM ? 512 : 256) : 128;
+    constexpr uint32_t T = QOUT ? 32 * LPR : LPR == 32 ? (NORM != 0 ? 512 : 256) : 128;
     const dim3 grid((g.n + T / LPR - 1) / (T / LPR));
-    const size_t lds = stage_bytes(g.k, NORM);
+    const size_t lds = stage_bytes(g.k, NORM != 0);
     vkml::abi::ProfileScope prof(label);
     // Whole pairs of whole batches (K a multiple of 1024 B) need no per-lane
     // tail check and no per-round test (q4_K and q8_0 kernels are built both
@@ -53,7 +53,7 @@ int launch(const GemvArgs& g, const char* label) {
     return vkml::abi::check_launch(label);
 }
 
-template <int FMT, bool F16S, int EPI, bool NORM, bool QOUT>
+template <int FMT, bool F16S, int EPI, int NORM, bool QOUT>
 int dispatch(const GemvArgs& g, const char* label) {
     // 8 lanes a row unless that leaves fewer than one wave per SIMD; 32
     // (q4_K, q8_0) when 16 would leave fewer than two, so that one wave's
@@ -72,7 +72,7 @@ int dispatch(const GemvArgs& g, const char* label) {
     return launch<FMT, F16S, 8, EPI, NORM, QOUT>(g, label);
 }
 
-template <int EPI, bool NORM = false, bool QOUT = false>
+template <int EPI, int NORM = 0, bool QOUT = false>
 int dispatch_format(uint32_t b_type, uint32_t scale_type, const GemvArgs& g, const char* label) {
     const bool f16 = scale_type == VKML_F16;
     switch (b_type) {
@@ -274,6 +274,7 @@ int vkml_gemv_fused(const vkml_gemv_fused_params* p, const void* a, const float*
     VKML_CHECK_ARG(p->norm <= 2, "gemv_fused: norm must be 0 (quantized input), 1 (RMSNorm + Q8_0) or 2 (Q8_0)");
     VKML_CHECK_ARG(!p->norm || p->k <= 4096, "gemv_fused: the RMSNorm / Q8_0 prologue takes k up to 4096");
     VKML_CHECK_ARG(!(p->norm && p->epilogue == 1), "gemv_fused: the RMSNorm / Q8_0 prologue goes with the store or SwiGLU epilogue");
+    VKML_CHECK_ARG(p->norm != 2 || p->epilogue == 0, "gemv_fused: the plain Q8_0 prologue (norm 2) goes with the store epilogue");
     if (p->n == 0) return VKML_OK;
     VKML_CHECK_ARG(a && b_values && b_scales && out, "gemv_fused: null buffer");
     VKML_CHECK_ARG(p->norm == 1 ? norm_weight != nullptr : p->norm == 2 || a_scales != nullptr,
@@ -286,8 +287,9 @@ int vkml_gemv_fused(const vkml_gemv_fused_params* p, const void* a, const float*
                static_cast<uint8_t*>(out_values), out_scales};
     const char* label = "gemv_fused";
     switch (p->epilogue) {
-        case 0: return p->norm ? dispatch_format<kStore, true>(p->b_type, p->scale_type, g, label)
-                               : dispatch_format<kStore>(p->b_type, p->scale_type, g, label);
+        case 0: return p->norm == 1 ? dispatch_format<kStore, 1>(p->b_type, p->scale_type, g, label)
+                       : p->norm == 2 ? dispatch_format<kStore, 2>(p->b_type, p->scale_type, g, label)
+                                      : dispatch_format<kStore>(p->b_type, p->scale_type, g, label);
         case 1: return dispatch_format<kAdd>(p->b_type, p->scale_type, g, label);
         default:
             if (p->norm) {

@@ -54,8 +54,8 @@ PROMPT = 4096
 # kernel sources they were taken on: GATE_UP_TRAFFIC_SOURCES is the SHA-256
 # (first 16 hex digits) of those files, and the line reports no traffic
 # when the sources have changed since.
-GATE_UP_TRAFFIC = 67_459_814
-GATE_UP_TRAFFIC_SOURCES = "ede88abe2ebf3fbb"
+GATE_UP_TRAFFIC = 67_470_468
+GATE_UP_TRAFFIC_SOURCES = "9e26e08ed55b2f46"
 TRAFFIC_FILES = ("vkml-framework_amd/csrc/gemv.hpp", "vkml-framework_amd/csrc/k_gemv.hip", "vkml-framework_amd/csrc/device.hpp")
 
 # GGUF-native bytes per weight (q4_K 144 B / 256, q6_K 210 B / 256).

@@ -403,7 +403,7 @@ template <uint32_t T>
 struct NormLoads {
     static constexpr uint32_t V = T >= 256 ? 1 : 256 / T;  // invocations per thread (t, t + T, ... below 256)
     static constexpr uint32_t kMaxPer = 4096 / 256;        // elements per invocation at K <= 4096
-    static constexpr uint32_t Q4 = 4096 / 4 / T;           // float4s of x (and w) per thread
+    static constexpr uint32_t Q4 = (4096 / 4 + T - 1) / T; // float4s of x (and w) per thread
     float4 xq[Q4], wq[Q4];                                 // x and w at float4 t + T i
     float xv[V][kMaxPer];                                  // its invocations' strided elements
 };
@@ -490,11 +490,13 @@ __device__ void norm_quantize_prologue(const NormLoads<T>& r, float eps, uint32_
 // nothing computed at run time, so a caller can issue them early (before the
 // activation is staged, or before a grid barrier); finish() sums the rounds
 // over the staged activation and applies the epilogue, keeping two batches
-// in flight. With COH, the outputs (and the Q8_0 output) are stored
+// in flight. PRE = 0: the row's every round is one batch (K at most 512 B),
+// all issued by start(), so a short row costs one round trip to memory, not
+// one a batch. With COH, the outputs (and the Q8_0 output) are stored
 // write-through, coherently across XCDs, for readers in other workgroups of
 // the same launch; g.out may then be null (no f32 output). FULL: K a
 // multiple of 1024 B (every round whole, and the rounds whole pairs of
-// batches, so no round is skipped).
+// batches, so no round is skipped); with PRE = 0, K = 512 B.
 //
 // q4_K and q8_0 weights are read with buffer loads: a lane's byte offset
 // into the matrix is computed once per item, and each round adds a scalar
@@ -613,7 +615,9 @@ struct GemvRows {
                 }
             }
         };
-        if constexpr (PRE == 2) {
+        if constexpr (PRE == 0) {
+            sum_batch(wa, 0);  // every round in flight since start()
+        } else if constexpr (PRE == 2) {
             // Both batches are in flight on entry; the last pair of batches
             // is peeled so that no load is issued past the rows' end.
             uint32_t r0 = 0;

@@ -247,12 +247,13 @@ struct FusedArgs {
 // waiting (bounded) for all merges. Chunk items never wait, so the GEMV's
 // workgroups, fewer than the resident slots, cannot keep an item from
 // running, in whatever order workgroups are dispatched.
-template <int HD, bool F16, int HPW, int FMT, bool FULL>
+template <int HD, bool F16, int HPW, int FMT, bool FULL, int DEEP>
 __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArgs f, vkml::gemv::GemvArgs g) {
     extern __shared__ uint4 smem[];
     if (blockIdx.x >= f.attn_wgs) {
+        // DEEP (K = 512 DEEP): the rows' every weight load is in flight before the wait
         const uint32_t wg = blockIdx.x - f.attn_wgs;
-        vkml::gemv::GemvRows<FMT, true, 32, vkml::gemv::kAdd, 2, kThreads, false, false, 1, FULL> rows;
+        vkml::gemv::GemvRows<FMT, true, 32, vkml::gemv::kAdd, DEEP ? DEEP : 2, kThreads, false, false, DEEP ? 0 : 1, FULL> rows;
         rows.start(g, wg);
         if (!await_merged(f.sync, wg, f.merges, f.error)) return;
         vkml::gemv::stage_activation<kThreads, false, true>(g, smem);
@@ -320,9 +321,9 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
         __hip_atomic_fetch_add(OSync::counter(f.sync, threadIdx.x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int HD, bool F16, int HPW, int FMT, bool FULL>
+template <int HD, bool F16, int HPW, int FMT, bool FULL, int DEEP = 0>
 bool launch_fused_as(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs) {
-    const void* fn = reinterpret_cast<const void*>(&k_attend_fused<HD, F16, HPW, FMT, FULL>);
+    const void* fn = reinterpret_cast<const void*>(&k_attend_fused<HD, F16, HPW, FMT, FULL, DEEP>);
     constexpr uint32_t kHalves = kThreads / HD;
     const size_t merge_lds = (static_cast<size_t>(kHalves) * 2 * a.chunks + kHalves * (HD / kWave)) * 4;
     const size_t lds = std::max({sizeof(AttendSmem<HD, F16, HPW>), merge_lds, static_cast<size_t>(vkml::gemv::stage_bytes(g.k, false))});
@@ -335,7 +336,7 @@ bool launch_fused_as(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::G
     }
     // the waiting GEMV workgroups must leave slots for the chunk items
     if (static_cast<uint64_t>(per_cu) * vkml::abi::compute_units() <= gemv_wgs) return false;
-    hipLaunchKernelGGL((k_attend_fused<HD, F16, HPW, FMT, FULL>), dim3(f.attn_wgs + gemv_wgs), dim3(kThreads), lds,
+    hipLaunchKernelGGL((k_attend_fused<HD, F16, HPW, FMT, FULL, DEEP>), dim3(f.attn_wgs + gemv_wgs), dim3(kThreads), lds,
                        vkml::abi::stream(), a, f, g);
     return true;
 }
@@ -343,6 +344,13 @@ bool launch_fused_as(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::G
 template <int HD, bool F16, int HPW>
 bool launch_fused_hpw(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs, bool q4k) {
     const bool full = g.k % 2048 == 0;  // whole pairs of 2-round batches
+    // o rows of 2048 or 4096 values: every round's weights in flight at once
+    if (g.k == 4096)
+        return q4k ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true, 8>(a, f, g, gemv_wgs)
+                   : launch_fused_as<HD, F16, HPW, VKML_Q8_0, true, 8>(a, f, g, gemv_wgs);
+    if (g.k == 2048)
+        return q4k ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true, 4>(a, f, g, gemv_wgs)
+                   : launch_fused_as<HD, F16, HPW, VKML_Q8_0, true, 4>(a, f, g, gemv_wgs);
     if (q4k)
         return full ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true>(a, f, g, gemv_wgs)
                     : launch_fused_as<HD, F16, HPW, VKML_Q4_K, false>(a, f, g, gemv_wgs);

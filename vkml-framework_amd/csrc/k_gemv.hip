@@ -16,11 +16,18 @@ using namespace vkml::gemv;
 
 namespace {
 
-template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, int NORM, bool QOUT, bool FULL>
+template <int FMT, bool F16S, int LPR, int EPI, int B, uint32_t T, int NORM, bool QOUT, bool FULL, int PRE = 1>
 __global__ void __launch_bounds__(T) k_gemv_dot(GemvArgs g) {
     extern __shared__ uint4 smem[];
-    GemvRows<FMT, F16S, LPR, EPI, B, T, QOUT, false, 1, FULL> rows;
-    if constexpr (NORM != 0) {
+    GemvRows<FMT, F16S, LPR, EPI, B, T, QOUT, false, PRE, FULL> rows;
+    if constexpr (PRE == 0) {
+        // Every weight load of the row is issued at once: the activation's
+        // loads go first, so that staging waits for them alone.
+        StageLoads<T, NORM> act;
+        stage_load<T, NORM, false>(g, act);
+        rows.start(g, blockIdx.x);
+        stage_store<T, NORM, false>(g, smem, act);
+    } else if constexpr (NORM != 0) {
         // (the norm prologue's loads after the weights': measured faster)
         rows.start(g, blockIdx.x);  // the first batch of weights is in flight while the activation is staged
         stage_activation<T, NORM, false>(g, smem);
@@ -33,15 +40,32 @@ __global__ void __launch_bounds__(T) k_gemv_dot(GemvArgs g) {
     rows.finish(g, smem, staged_ss(smem, g.k));
 }
 
-template <int FMT, bool F16S, int LPR, int EPI, int NORM, bool QOUT>
-int launch(const GemvArgs& g, const char* label) {
+// Rows of up to 4096 values at 32 lanes a row: every round of the row is
+// one batch, all in flight at once (T threads, T / 32 rows a workgroup).
+template <int FMT, bool F16S, int EPI, int NORM, bool QOUT, uint32_t T>
+int launch_deep(const GemvArgs& g, const char* label) {
+    const dim3 grid((g.n + T / 32 - 1) / (T / 32));
+    const size_t lds = stage_bytes(g.k, NORM != 0);
+    if (g.k <= 2048) {
+        if (g.k == 2048)
+            hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, 32, EPI, 4, T, NORM, QOUT, true, 0>), grid, dim3(T), lds, vkml::abi::stream(), g);
+        else
+            hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, 32, EPI, 4, T, NORM, QOUT, false, 0>), grid, dim3(T), lds, vkml::abi::stream(), g);
+    } else {
+        if (g.k == 4096)
+            hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, 32, EPI, 8, T, NORM, QOUT, true, 0>), grid, dim3(T), lds, vkml::abi::stream(), g);
+        else
+            hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, 32, EPI, 8, T, NORM, QOUT, false, 0>), grid, dim3(T), lds, vkml::abi::stream(), g);
+    }
+    return vkml::abi::check_launch(label);
+}
+
+// The batch pipeline (B rounds a batch, two batches in flight), T threads.
+template <int FMT, bool F16S, int LPR, int EPI, int NORM, bool QOUT, uint32_t T>
+int launch_batched(const GemvArgs& g, const char* label) {
     constexpr int B = LPR == 16 ? 4 : 2;  // rounds per batch (2 measured best at 32 lanes)
-    // (512 threads with the norm prologue at 32 lanes: half the workgroups
-    // redo RMSNorm + Q8_0 of x, each over twice the threads)
-    constexpr uint32_t T = QOUT ? 32 * LPR : LPR == 32 ? (NORM != 0 ? 512 : 256) : 128;
     const dim3 grid((g.n + T / LPR - 1) / (T / LPR));
     const size_t lds = stage_bytes(g.k, NORM != 0);
-    vkml::abi::ProfileScope prof(label);
     // Whole pairs of whole batches (K a multiple of 1024 B) need no per-lane
     // tail check and no per-round test (q4_K and q8_0 kernels are built both
     // ways).
@@ -51,6 +75,28 @@ int launch(const GemvArgs& g, const char* label) {
     else
         hipLaunchKernelGGL((k_gemv_dot<FMT, F16S, LPR, EPI, B, T, NORM, QOUT, false>), grid, dim3(T), lds, vkml::abi::stream(), g);
     return vkml::abi::check_launch(label);
+}
+
+template <int FMT, bool F16S, int LPR, int EPI, int NORM, bool QOUT>
+int launch(const GemvArgs& g, const char* label) {
+    // (512 threads with the norm prologue at 32 lanes: half the workgroups
+    // redo RMSNorm + Q8_0 of x, each over twice the threads)
+    constexpr uint32_t T = QOUT ? 32 * LPR : LPR == 32 ? (NORM != 0 ? 512 : 256) : 128;
+    vkml::abi::ProfileScope prof(label);
+    const uint32_t cus = vkml::abi::compute_units();
+    constexpr bool kWhole = FMT == VKML_Q4_K || FMT == VKML_Q8_0;
+    if constexpr (kWhole && LPR == 32) {
+        if (g.k <= 4096) {
+            // With the norm prologue, which every workgroup computes over the
+            // whole row: 24 rows a workgroup where that makes one workgroup a
+            // compute unit (the N = 6144 q|k|v projection of a 7B model).
+            if constexpr (NORM != 0) {
+                if ((g.n + 15) / 16 > cus && (g.n + 23) / 24 <= cus) return launch_deep<FMT, F16S, EPI, NORM, QOUT, 768>(g, label);
+            }
+            return launch_deep<FMT, F16S, EPI, NORM, QOUT, T>(g, label);
+        }
+    }
+    return launch_batched<FMT, F16S, LPR, EPI, NORM, QOUT, T>(g, label);
 }
 
 template <int FMT, bool F16S, int EPI, int NORM, bool QOUT>

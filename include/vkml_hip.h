@@ -246,6 +246,38 @@ int vkml_gemv_fused(const vkml_gemv_fused_params* p, const void* d_a, const floa
                     const void* d_b2_values, const void* d_b2_scales, const float* d_residual,
                     float* d_out, void* d_out_values, float* d_out_scales);
 
+/* A decode step's q|k|v projection with the work that follows it in the
+ * reference folded into the epilogue: llama.cpp:313-355's rms_norm +
+ * quantize (as vkml_gemv_fused norm 1), the projection, RoPE of q and k at
+ * d_state->position (interleaved pairs, rope.comp:94-118, as
+ * vkml_rope_kv_append rotates them) and the new key and value rounded to
+ * the cache type and written at row position % capacity of each KV head
+ * (cast.comp + write_rows.comp, llama.cpp:344-355). The b rows are rows
+ * row0 .. row0 + n of [q | k | v] (heads * head_dim, then kv_heads *
+ * head_dim each); d_qkv receives rows row0 .. row0 + n of the rotated q and
+ * k and of v. With rotate = 0 nothing is rotated. A step whose attention
+ * then reads q and the caches as left here sets prepared in
+ * vkml_attend_step_params. No reference counterpart as one call. */
+typedef struct vkml_gemv_rope_params {
+    uint32_t n;
+    uint32_t k;
+    uint32_t b_type;
+    uint32_t scale_type;
+    float eps;
+    uint32_t row0;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t capacity;
+    uint32_t kv_type;
+    uint32_t rotate;
+} vkml_gemv_rope_params;
+struct vkml_decode_state;
+int vkml_gemv_rope(const vkml_gemv_rope_params* p, const float* d_x, const float* d_norm_weight,
+                   const void* d_b_values, const void* d_b_scales, float* d_qkv,
+                   const float* d_rope_table, const struct vkml_decode_state* d_state,
+                   void* d_k_cache, void* d_v_cache);
+
 /* shaders/gemv.comp, src/ops/matmul.cpp:88-120: the float path, c[m, n] =
  * a[m] . b[n] with f32 a (m <= 8) and b [n, k] of b_type F32/F16/BF16 or
  * Q8_0/Q4_0/Q4_1/Q4_K decoded in registers (ContextOptions::
@@ -453,6 +485,14 @@ typedef struct vkml_attend_step_params {
      * ring (capacity rows, position p at row p % capacity), and chunks must
      * cover min(window, capacity) keys. */
     uint32_t window;
+    /* 1: q in d_qkv is already rotated and the new key and value are already
+     * in the caches (vkml_gemv_rope ran before, with d_state); the step then
+     * neither rotates nor appends. */
+    uint32_t prepared;
+    /* vkml_attend_step_fused: chunks that hold keys at every position the
+     * call may see (a hint; 0: none); their items load q, K and V before
+     * reading the position. Prepared steps without a window only. */
+    uint32_t ready_chunks;
 } vkml_attend_step_params;
 int vkml_attend_step(const vkml_attend_step_params* p, const float* d_qkv, const float* d_rope_table,
                      void* d_k_cache, void* d_v_cache, float* d_partial, float* d_stats,

@@ -50,6 +50,14 @@ struct ChunkArgs {
     uint32_t* o_sync;
     // A sliding window (0: none): keys from max(kv_start, kv_len - window).
     uint32_t window;
+    // A step whose q was rotated and whose new key and value were appended
+    // by the q|k|v GEMV before (vkml_gemv_rope): q is read as it is and the
+    // caches as they are.
+    uint32_t prepared;
+    // Chunks live at every position the launch may see (a hint): the one
+    // launch's items of these issue their q, K and V loads before reading
+    // the position (prepared steps without a window).
+    uint32_t ready;
 };
 
 // Sync words of the launch that merges the chunks and runs the o GEMV on
@@ -198,7 +206,7 @@ template <int HD, int HPW>
 __device__ __forceinline__ void attend_q_load(const ChunkArgs& a, uint32_t kvh, uint32_t hl, uint32_t pos, QLoads<HD, HPW>& r) {
     using Q = QLoads<HD, HPW>;
     const uint32_t t = thread_index(), head0 = kvh * a.group + hl * HPW, half = HD / 2;
-    if (a.step) {
+    if (a.step && !a.prepared) {
         const float* tab = a.table + static_cast<uint64_t>(pos) * half * 2;
         const float* ksrc = a.q + static_cast<uint64_t>(a.heads) * HD + static_cast<uint64_t>(kvh) * HD;
         const float* vsrc = a.q + static_cast<uint64_t>(a.heads + a.kv_heads) * HD + static_cast<uint64_t>(kvh) * HD;
@@ -245,7 +253,8 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     const uint32_t key0 = a.kv_start + chunk * kChunk;
     const auto stats_at = [&](uint32_t h) -> uint64_t { return static_cast<uint64_t>(head0 + h) * a.chunks + chunk; };
     const uint32_t n = min(kChunk, kv_len - key0);
-    const bool holds_new = a.step && key0 + n == kv_len;  // the appended key is this chunk's last
+    const bool rot = a.step && !a.prepared;            // rotate q and append the new key and value here
+    const bool holds_new = rot && key0 + n == kv_len;  // the appended key is this chunk's last
     const uint64_t kv_row0 = static_cast<uint64_t>(kvh) * a.capacity;
     const auto row_of = [&](uint32_t key) -> uint64_t { return kv_row0 + (key0 + key) % a.capacity; };
 
@@ -255,7 +264,7 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     // 0's workgroup.
     const uint32_t half = HD / 2;
     using Q = QLoads<HD, HPW>;
-    if (a.step) {
+    if (rot) {
         const uint64_t new_row = (kv_row0 + pos % a.capacity) * HD;
 #pragma unroll
         for (uint32_t u = 0; u < Q::kItems; ++u) {
@@ -511,24 +520,30 @@ __device__ __forceinline__ void merge_head(const float* partial, const float* st
     __syncthreads();
     // sum += r_c * partial_c and weight += r_c * l_c over the live chunks in
     // order (every thread carries the weight chain too: the same value).
+    // Branch-free: a skipped chunk (and a slot past count) adds +0 * +0 to
+    // each chain instead, which leaves it unchanged: both start at +0 and an
+    // f32 sum is -0 only when both addends are, so neither is ever -0 and
+    // x + (+0) = x.
     float sum = 0.0f, weight = 0.0f;
     for (uint32_t c0 = 0; c0 < count; c0 += B) {
         if (c0 > 0) {
 #pragma unroll
             for (uint32_t j = 0; j < B; ++j) p[j] = ld_f32<COH>(pc + static_cast<uint64_t>(min(c0 + j, count - 1)) * hd);
         }
-        float r[B], l[B];
+        // (eight chunks at a time, each group's LDS reads kept after the
+        // previous group's arithmetic, so that they do not all take registers)
 #pragma unroll
-        for (uint32_t j = 0; j < B; ++j) {
-            r[j] = s_r[min(c0 + j, count - 1)];
-            l[j] = s_l[min(c0 + j, count - 1)];
-        }
+        for (uint32_t j0 = 0; j0 < B; j0 += 8) {
 #pragma unroll
-        for (uint32_t j = 0; j < B; ++j) {
-            if (c0 + j < count && r[j] >= 0.0f) {
-                sum += r[j] * p[j];
-                weight += r[j] * l[j];
+            for (uint32_t j = j0; j < j0 + 8 && j < B; ++j) {
+                const uint32_t c = min(c0 + j, count - 1);
+                const float rj = s_r[c], lj = s_l[c];
+                const bool live = c0 + j < count && rj >= 0.0f;
+                const float rr = live ? rj : 0.0f;
+                sum += rr * (live ? p[j] : 0.0f);
+                weight += rr * (live ? lj : 0.0f);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     const float o = sum / weight;

@@ -248,6 +248,14 @@ __device__ __forceinline__ void stg(T* p, T v) {
     else *(global_t<T>*)p = v;
 }
 
+// A 32-bit value that no workgroup of the launch writes (the decode state's
+// position, written by an earlier launch), read through the scalar unit:
+// its wait counts scalar loads, so it does not also wait for (or hold up)
+// the vector loads in flight around it.
+__device__ __forceinline__ int32_t ld_scalar_i32(const int32_t* p) {
+    return *reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(reinterpret_cast<uintptr_t>(p));
+}
+
 // ---------------------------------------------------------------- coherent access
 
 // Loads and stores of the values one workgroup of a launch produces for

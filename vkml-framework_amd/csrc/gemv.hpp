@@ -66,6 +66,17 @@ struct GemvArgs {
     // SwiGLU with the Q8_0 epilogue: the codes and f32 scales of h.
     uint8_t* out_values;
     float* out_scales;
+    // The store epilogue of a decode step's q|k|v projection with RoPE and
+    // the KV append (vkml_gemv_rope), when table is not null: output row j
+    // is row row0 + j of [q | k | v] (q_rows + 2 kv_rows rows, heads of hd
+    // values); q and k rows are rotated in interleaved pairs (rows 2i, 2i + 1
+    // of a head) by the state's position, and the k and v rows also go to
+    // the caches' row position % capacity, as f16 or f32 bits.
+    const float* table;  // cos/sin pairs [positions, hd / 2, 2]
+    const vkml_decode_state* state;
+    void* k_cache;
+    void* v_cache;
+    uint32_t row0, q_rows, kv_rows, hd, capacity, kv_f16, rotate;
 };
 
 // The accumulator (= half-block of the round) held in slot e of lane l.
@@ -509,6 +520,8 @@ struct GemvRows {
     static constexpr bool kBuf = FMT == VKML_Q4_K || FMT == VKML_Q8_0;
     RoundW<FMT, LPR> wa[B][NM], wb[B][NM];
     uint32_t item, row, r_row, l, rounds;
+    float res;     // + residual: the row's residual, loaded by start()
+    int32_t pos;   // RoPE epilogue: the state's position, loaded by start()
     __amdgpu_buffer_rsrc_t rc[NM], rs[NM];  // kBuf: codes and scales of each matrix
     uint32_t vq, vs;                        // kBuf: the lane's byte offsets at round 0
 
@@ -580,8 +593,40 @@ struct GemvRows {
                 vs = (R * (K / 32) + hb / 2) * (F16S ? 2 : 4);
             }
         }
+        // (the RoPE epilogue's position first, so that waiting for it later
+        // does not wait for the weights)
+        if constexpr (EPI == kStore) {
+            if (g.table) pos = ld_scalar_i32(&g.state->position);
+        }
         load_batch(g, wa, 0);
         if constexpr (PRE == 2) load_batch(g, wb, B);
+        // The residual is read now, not after the sums: one round trip less
+        // at the end of the kernel.
+        if constexpr (EPI == kAdd) res = ldg(g.residual + r_row);
+    }
+
+    // The RoPE epilogue: the row's rotated value (q and k rows; v rows as
+    // they are) given the row's sum y and the pair's other row's sum other,
+    // with (c, s) its cos/sin (rope.comp:94-118, vkml_rope_kv_append's
+    // arithmetic); then the k and v rows' cache bits stored at the
+    // position's cache row.
+    __device__ __forceinline__ float rope_store(const GemvArgs& g, uint32_t gr, float y, float other, float2 cs) const {
+#pragma clang fp contract(off)
+        float v = y;
+        if (g.rotate && gr < g.q_rows + g.kv_rows) {
+            const bool odd = gr & 1u;
+            const float a = odd ? other : y, b = odd ? y : other;
+            v = odd ? a * cs.y + b * cs.x : a * cs.x - b * cs.y;
+        }
+        if (gr >= g.q_rows) {
+            const bool is_k = gr < g.q_rows + g.kv_rows;
+            const uint32_t kr = gr - g.q_rows - (is_k ? 0u : g.kv_rows);  // row within the kv heads' [kv_heads, hd]
+            const uint64_t at = (static_cast<uint64_t>(kr / g.hd) * g.capacity + static_cast<uint32_t>(pos) % g.capacity) * g.hd + kr % g.hd;
+            void* cache = is_k ? g.k_cache : g.v_cache;
+            if (g.kv_f16) stg(static_cast<uint16_t*>(cache) + at, static_cast<uint16_t>(f32_to_f16_bits(__float_as_uint(v))));
+            else stg(static_cast<uint32_t*>(cache) + at, __float_as_uint(v));
+        }
+        return v;
     }
 
     __device__ __forceinline__ void finish(const GemvArgs& g, const uint4* s_codes, const float2* s_ss) {
@@ -593,6 +638,16 @@ struct GemvRows {
 #pragma unroll
             for (int e = 0; e < NS; ++e) acc[m][e] = 0.0f;
         const Q4kField jf = q4k_field((l % 16) / 2);
+        // RoPE epilogue: the row's cos/sin, in flight during the sums (the
+        // position arrived long before).
+        float2 cs = make_float2(0.0f, 0.0f);
+        if constexpr (EPI == kStore) {
+            if (g.table && g.rotate) {
+                const uint32_t gr = g.row0 + r_row;
+                if (gr < g.q_rows + g.kv_rows)
+                    cs = ldg(reinterpret_cast<const float2*>(g.table + static_cast<uint64_t>(pos) * g.hd + (gr % g.hd & ~1u)));
+            }
+        }
         const auto sum_batch = [&](const RoundW<FMT, LPR> (&w)[B][NM], uint32_t r0) {
             if constexpr (FULL && LPR == 32) {
                 // one slot a lane: the batch's activation reads fit in registers
@@ -646,12 +701,18 @@ struct GemvRows {
         float y[NM];
 #pragma unroll
         for (int m = 0; m < NM; ++m) y[m] = row_tree<FMT, LPR>(acc[m]);
+        // RoPE epilogue: rows 2i and 2i + 1 (the item's rows start even) are
+        // LPR lanes apart in one wave; lane 0 of each gets the other's sum.
+        float other = 0.0f;
+        if constexpr (EPI == kStore) {
+            if (g.table) other = __shfl_xor(y[0], LPR);
+        }
         float result = 0.0f;
         if (l == 0 && row < g.n) {
             if constexpr (EPI == kStore) {
-                result = y[0];
+                result = g.table ? rope_store(g, g.row0 + row, y[0], other, cs) : y[0];
             } else if constexpr (EPI == kAdd) {
-                result = ldg(g.residual + row) + y[0];  // add(x, attn_out), llama.cpp:374,386
+                result = res + y[0];  // add(x, attn_out), llama.cpp:374,386
             } else {
                 // silu(gate) * up (unary.comp:21-24, then binary.comp's mul)
                 const float gate = y[0], up = y[NM - 1];

@@ -46,8 +46,9 @@ __global__ void __launch_bounds__(kThreads) k_attend_chunk(ChunkArgs a) {
     const uint32_t hl = rest % groups, pair = (rest / groups) * kXcds + pair_lo;
     if (pair >= pairs) return;
     const uint32_t chunk = pair / a.kv_heads, kvh = pair % a.kv_heads, head0 = kvh * G + hl * HPW;
-    const uint32_t pos = a.step ? (a.state ? static_cast<uint32_t>(a.state->position) : a.position) : 0u;
-    const uint32_t kv_len = a.step ? pos + 1 : (a.state ? static_cast<uint32_t>(a.state->position) + 1u : a.kv_len);
+    const uint32_t spos = a.state ? static_cast<uint32_t>(ld_scalar_i32(&a.state->position)) : 0u;
+    const uint32_t pos = a.step ? (a.state ? spos : a.position) : 0u;
+    const uint32_t kv_len = a.step ? pos + 1 : (a.state ? spos + 1u : a.kv_len);
     if (a.window != 0 && kv_len > a.window) a.kv_start = max(a.kv_start, kv_len - a.window);
     if (a.kv_start + chunk * kChunk >= kv_len) {
         // A chunk past the live keys (the grid covers the whole cache, so a
@@ -75,7 +76,7 @@ k_attend_merge(const float* partial, const float* stats, float* out, uint8_t* va
     __shared__ float s_r[kMergeMaxChunks];   // exp(m_c - M), or -1 for a chunk past the live keys
     __shared__ float s_l[kMergeMaxChunks];   // the chunk's sum of weights
     __shared__ float s_wmax[8];
-    merge_head<false>(partial, stats, out, values, scales, blockIdx.x, chunks, chunks, hd, threadIdx.x, s_r, s_l, s_wmax);
+    merge_head<false, 48>(partial, stats, out, values, scales, blockIdx.x, chunks, chunks, hd, threadIdx.x, s_r, s_l, s_wmax);
 }
 
 template <int HD, bool F16>
@@ -163,7 +164,7 @@ __global__ void __launch_bounds__(kThreads) k_merge_o(MergeOArgs m, vkml::gemv::
         float* s_r = f + half * 2 * m.chunks;
         float* s_l = s_r + m.chunks;
         float* s_wmax = f + hpw * 2 * m.chunks + half * (m.hd / kWave);
-        merge_head<true, 48>(m.partial, m.stats, m.out, m.values, m.scales, blockIdx.x * hpw + half, m.chunks, m.chunks, m.hd, d, s_r,
+        merge_head<true, 36>(m.partial, m.stats, m.out, m.values, m.scales, blockIdx.x * hpw + half, m.chunks, m.chunks, m.hd, d, s_r,
                          s_l, s_wmax);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the write-through stores have completed
         __syncthreads();
@@ -267,7 +268,18 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
     const uint32_t hl = rest % groups, pair = (rest / groups) * kXcds + pair_lo;
     if (pair >= pairs) return;
     const uint32_t chunk = pair / a.kv_heads, kvh = pair % a.kv_heads, head0 = kvh * G + hl * HPW;
-    const uint32_t pos = static_cast<uint32_t>(a.state->position);
+    // Items of chunks that hold keys at any position the launch may see
+    // issue their loads before reading the position: q as the q|k|v GEMV
+    // left it, K and V over the whole chunk (rows past the live keys, read
+    // modulo the capacity, are masked out by the item).
+    QLoads<HD, HPW> qv;
+    ChunkLoads<HD, F16> ld;
+    const bool early = chunk < a.ready;
+    if (early) {
+        attend_q_load<HD, HPW>(a, kvh, hl, 0, qv);
+        attend_chunk_load<HD, F16>(a, chunk, kvh, a.kv_start + (chunk + 1) * kChunk, ld, sm.v);
+    }
+    const uint32_t pos = static_cast<uint32_t>(ld_scalar_i32(&a.state->position));
     const uint32_t kv_len = pos + 1;
     if (a.window != 0 && kv_len > a.window) a.kv_start = max(a.kv_start, kv_len - a.window);
     // Launched for fewer chunks than the cache holds: keys past them would
@@ -281,10 +293,10 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
             st_f32<true>(a.stats + at * 2 + 1, 0.0f);
         }
     } else {
-        QLoads<HD, HPW> qv;
-        attend_q_load<HD, HPW>(a, kvh, hl, pos, qv);
-        ChunkLoads<HD, F16> ld;
-        attend_chunk_load<HD, F16>(a, chunk, kvh, kv_len, ld, sm.v);
+        if (!early) {
+            attend_q_load<HD, HPW>(a, kvh, hl, pos, qv);
+            attend_chunk_load<HD, F16>(a, chunk, kvh, kv_len, ld, sm.v);
+        }
         attend_chunk_item<HD, F16, HPW, true>(a, chunk, kvh, hl, pos, kv_len, qv, ld, sm);
     }
     __shared__ uint32_t s_last;
@@ -308,12 +320,15 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
     float* s_r = fl + half * 2 * a.chunks;
     float* s_l = s_r + a.chunks;
     float* s_wmax = fl + kHalves * 2 * a.chunks + half * (HD / kWave);
+    // Chunks past the live keys hold a max of -inf, which the merge skips:
+    // it walks the live ones only.
+    const uint32_t live = min(a.chunks, (kv_len - a.kv_start + kChunk - 1) / kChunk);
 #pragma unroll
     for (uint32_t h0 = 0; h0 < HPW; h0 += kAtOnce) {
         const bool mine = half < kAtOnce;
         if (h0 > 0) __syncthreads();  // the previous pass is done with s_r, s_l
-        merge_head<true, 48>(a.partial, a.stats, mine ? f.out : nullptr, mine ? f.values : nullptr, f.scales,
-                             head0 + h0 + (mine ? half : 0), a.chunks, a.chunks, HD, d, s_r, s_l, s_wmax);
+        merge_head<true, 36>(a.partial, a.stats, mine ? f.out : nullptr, mine ? f.values : nullptr, f.scales,
+                             head0 + h0 + (mine ? half : 0), a.chunks, live, HD, d, s_r, s_l, s_wmax);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -456,7 +471,8 @@ int check_step(const vkml_attend_step_params* p, const float* qkv, const float* 
     VKML_CHECK_ARG((fewer_chunks ? p->chunks > 0 : static_cast<uint64_t>(p->chunks) * kChunk >= span) && p->chunks <= kMergeMaxChunks,
                    w + ": " + std::to_string(p->chunks) + " chunks do not cover the " + std::to_string(span) + " keys a step can see (or exceed " +
                        std::to_string(kMergeMaxChunks) + ")");
-    VKML_CHECK_ARG(qkv && rope_table && k_cache && v_cache && partial && stats && out, w + ": null buffer");
+    VKML_CHECK_ARG(qkv && (rope_table || p->prepared) && k_cache && v_cache && partial && stats && out, w + ": null buffer");
+    VKML_CHECK_ARG(!p->prepared || state, w + ": a prepared step reads its position from the decode state");
     VKML_CHECK_ARG(!values || scales, w + ": quantized output needs scales");
     return VKML_OK;
 }
@@ -465,7 +481,7 @@ ChunkArgs step_args(const vkml_attend_step_params* p, const float* qkv, const fl
                     float* partial, float* stats, const vkml_decode_state* state, uint32_t* o_sync) {
     return ChunkArgs{qkv, rope_table, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads,
                      p->capacity, p->kv_start, 0, p->position, p->chunks, 1, p->rope_style, p->rotate, p->scale, p->softcap, o_sync,
-                     p->window};
+                     p->window, p->prepared, p->prepared && !p->window ? std::min(p->ready_chunks, p->chunks) : 0u};
 }
 
 }  // namespace

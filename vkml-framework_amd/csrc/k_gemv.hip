@@ -347,6 +347,42 @@ int vkml_gemv_fused(const vkml_gemv_fused_params* p, const void* a, const float*
     }
 }
 
+int vkml_gemv_rope(const vkml_gemv_rope_params* p, const float* x, const float* norm_weight, const void* b_values,
+                   const void* b_scales, float* qkv, const float* rope_table, const vkml_decode_state* state, void* k_cache,
+                   void* v_cache) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(p, "gemv_rope: null params");
+    const vkml_gemv_dot_params dp{1, p->n, p->k, p->b_type, p->scale_type};
+    if (int r = check_dot_params(&dp, "gemv_rope")) return r;
+    VKML_CHECK_ARG(p->k <= 4096, "gemv_rope: the RMSNorm + Q8_0 prologue takes k up to 4096");
+    VKML_CHECK_ARG(p->head_dim > 0 && p->head_dim % 2 == 0 && p->heads > 0 && p->kv_heads > 0 && p->capacity > 0,
+                   "gemv_rope: heads, kv_heads, capacity and an even head_dim must be positive");
+    VKML_CHECK_ARG(p->kv_type == VKML_F16 || p->kv_type == VKML_F32, "gemv_rope: caches must be f16 or f32");
+    const uint64_t q_rows = static_cast<uint64_t>(p->heads) * p->head_dim, kv_rows = static_cast<uint64_t>(p->kv_heads) * p->head_dim;
+    // Pairs of rows share a workgroup when the first row is even.
+    VKML_CHECK_ARG(p->row0 % 2 == 0 && p->n % 2 == 0 && p->row0 + static_cast<uint64_t>(p->n) <= q_rows + 2 * kv_rows,
+                   "gemv_rope: rows " + std::to_string(p->row0) + " .. " + std::to_string(p->row0 + p->n) + " must be even-aligned rows of the " +
+                       std::to_string(q_rows + 2 * kv_rows) + " of [q | k | v]");
+    if (p->n == 0) return VKML_OK;
+    VKML_CHECK_ARG(x && norm_weight && b_values && b_scales && qkv && state && k_cache && v_cache && (rope_table || !p->rotate),
+                   "gemv_rope: null buffer");
+    GemvArgs g{nullptr, nullptr, b_values, b_scales, nullptr, nullptr, qkv + p->row0, nullptr, p->n, p->k, x, norm_weight, p->eps,
+               nullptr, nullptr};
+    // (a non-null table selects the epilogue; with rotate = 0 it is not read)
+    g.table = rope_table ? rope_table : x;
+    g.state = state;
+    g.k_cache = k_cache;
+    g.v_cache = v_cache;
+    g.row0 = p->row0;
+    g.q_rows = static_cast<uint32_t>(q_rows);
+    g.kv_rows = static_cast<uint32_t>(kv_rows);
+    g.hd = p->head_dim;
+    g.capacity = p->capacity;
+    g.kv_f16 = p->kv_type == VKML_F16;
+    g.rotate = p->rotate;
+    return dispatch_format<kStore, 1>(p->b_type, p->scale_type, g, "gemv_rope");
+}
+
 int vkml_gemv(const vkml_gemv_params* p, const float* a, const void* b, float* out, const void* b_scales) {
     VKML_REQUIRE_INIT();
     VKML_CHECK_ARG(p, "gemv: null params");

@@ -67,7 +67,10 @@ GemvFusedParams = _struct("GemvFusedParams", [("n", u32), ("k", u32), ("b_type",
 AttendStepParams = _struct("AttendStepParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
                                                 ("kv_start", u32), ("position", u32), ("kv_type", u32), ("chunks", u32),
                                                 ("rope_style", u32), ("rotate", u32), ("scale", f32), ("softcap", f32),
-                                                ("window", u32)])
+                                                ("window", u32), ("prepared", u32), ("ready_chunks", u32)])
+GemvRopeParams = _struct("GemvRopeParams", [("n", u32), ("k", u32), ("b_type", u32), ("scale_type", u32), ("eps", f32),
+                                            ("row0", u32), ("heads", u32), ("kv_heads", u32), ("head_dim", u32),
+                                            ("capacity", u32), ("kv_type", u32), ("rotate", u32)])
 
 P = C.POINTER
 # name -> argtypes (all return int status unless noted)
@@ -123,6 +126,7 @@ SIGNATURES = {
     "vkml_rope_kv_append": [P(RopeKvParams), vp, vp, vp, vp, vp, vp],
     "vkml_rope_kv_prompt": [P(RopeKvParams), u32, u32, vp, vp, vp, vp, vp],
     "vkml_gemv_fused": [P(GemvFusedParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "vkml_gemv_rope": [P(GemvRopeParams), vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step_o": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp],
     "vkml_attend_o_check": [vp],

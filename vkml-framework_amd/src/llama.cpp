@@ -445,7 +445,22 @@ struct Llama::Impl {
             const Layer& L = layers[li];
             const bool fold_qkv =
                 fold && std::all_of(L.qkv.begin(), L.qkv.end(), [&](const auto& wr) { return quantized_input(wr.first); });
-            if (fold_qkv) {
+            // With interleaved RoPE the q|k|v GEMV also rotates q and k and
+            // appends the new key and value (vkml_gemv_rope): the attention
+            // then starts from q and the caches as they are.
+            const bool prepared = fold_qkv && c.rope_style == RopeStyle::Interleaved;
+            const uint32_t kv_code = detail::type_code(L.k_cache.dtype());
+            if (prepared) {
+                for (const auto& [w, row] : L.qkv) {
+                    tag("qkv");
+                    const vkml_gemv_rope_params rp{u32(w.rows), u32(w.cols), w.type_code(), w.scale_code(), c.rms_norm_eps, u32(row),
+                                                   u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), kv_code, 1};
+                    check(vkml_gemv_rope(&rp, xp, static_cast<const float*>(L.attn_norm.data()), w.values(), w.scales(),
+                                         static_cast<float*>(qkv.data()), static_cast<const float*>(rope.data()), st, L.k_cache.data(),
+                                         L.v_cache.data()),
+                          "qkv");
+                }
+            } else if (fold_qkv) {
                 for (const auto& [w, row] : L.qkv) fused(w, L.attn_norm, static_cast<float*>(qkv.data()) + row, "qkv");
             } else {
                 norm(L.attn_norm, "attn_norm");
@@ -453,14 +468,18 @@ struct Llama::Impl {
                     project(w, xn, quant_d ? &xq : nullptr, &xs, static_cast<float*>(qkv.data()) + row, nullptr, "qkv");
             }
             const bool o_q = quantized_input(L.o);
-            const uint32_t kv_code = detail::type_code(L.k_cache.dtype());
             // rope, append and attention in one launch, then the merge
             tag("attention");
             const bool merge_o = int_dot && o_q && L.o.int_dot_ok();
-            const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), 0, 0, kv_code,
-                                             u32(merge_o && fsync && step_tier ? std::min(L.chunks(), step_tier) : L.chunks()),
+            const std::int64_t launched = merge_o && fsync && step_tier ? std::min(L.chunks(), step_tier) : L.chunks();
+            // A tier above the smallest serves positions whose keys fill at
+            // least half its chunks: those chunks' items may load before
+            // reading the position.
+            const std::int64_t ready = step_tier > kMinTier ? std::min(step_tier / 2, launched) : 0;
+            const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), 0, 0, kv_code, u32(launched),
                                              c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
-                                             1.0f / std::sqrt(static_cast<float>(hd)), c.attn_logit_softcap, u32(L.window)};
+                                             1.0f / std::sqrt(static_cast<float>(hd)), c.attn_logit_softcap, u32(L.window),
+                                             prepared ? 1u : 0u, u32(ready)};
             if (merge_o && fsync) {
                 // ... and the merge and the o projection + residual too (block
                 // li of the fused sync words, whose next block it zeroes)

@@ -481,15 +481,15 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
 // leaves each element its chain sum += r_c * partial_c. Its partials are
 // loaded B chunks at a time with every load in flight. Optionally quantizes
 // the result to Q8_0 with f32 scales (quantize.comp:100-111), the o
-// projection's input. s_r, s_l: count floats of LDS each; s_wmax: nt / 64.
-// Every thread of the workgroup calls it (it synchronizes the workgroup).
-// With COH, the partials and stats are read and the results stored
-// coherently across XCDs (they come from, and go to, other workgroups of
-// the same launch), and out may be null (no f32 output).
+// projection's input. s_rl: count (factor, weight sum) pairs of LDS; s_wmax:
+// nt / 64 floats. Every thread of the workgroup calls it (it synchronizes
+// the workgroup). With COH, the partials and stats are read and the results
+// stored coherently across XCDs (they come from, and go to, other
+// workgroups of the same launch), and out may be null (no f32 output).
 template <bool COH, uint32_t B = 64>
 __device__ __forceinline__ void merge_head(const float* partial, const float* stats, float* out, uint8_t* values, float* scales,
-                                           uint32_t h, uint32_t stride, uint32_t count, uint32_t hd, uint32_t d, float* s_r,
-                                           float* s_l, float* s_wmax) {
+                                           uint32_t h, uint32_t stride, uint32_t count, uint32_t hd, uint32_t d, float2* s_rl,
+                                           float* s_wmax) {
 #pragma clang fp contract(off)
     const uint32_t nt = hd;
     const uint64_t first = static_cast<uint64_t>(h) * stride;
@@ -514,34 +514,33 @@ __device__ __forceinline__ void merge_head(const float* partial, const float* st
     for (uint32_t c = d; c < count; c += nt) {
         const uint64_t ml = c == d ? ml0 : ld_u64<COH>(st + c);
         const float mc = __uint_as_float(static_cast<uint32_t>(ml)), lc = __uint_as_float(static_cast<uint32_t>(ml >> 32));
-        s_r[c] = mc == -__builtin_inff() ? -1.0f : vk_expf(mc - top);
-        s_l[c] = lc;
+        s_rl[c] = make_float2(mc == -__builtin_inff() ? -1.0f : vk_expf(mc - top), lc);
     }
     __syncthreads();
     // sum += r_c * partial_c and weight += r_c * l_c over the live chunks in
     // order (every thread carries the weight chain too: the same value).
     // Branch-free: a skipped chunk (and a slot past count) adds +0 * +0 to
-    // each chain instead, which leaves it unchanged: both start at +0 and an
-    // f32 sum is -0 only when both addends are, so neither is ever -0 and
-    // x + (+0) = x.
+    // each chain instead (its operands' bits masked off), which leaves it
+    // unchanged: both start at +0 and an f32 sum is -0 only when both
+    // addends are, so neither is ever -0 and x + (+0) = x. Eight chunks'
+    // (factor, weight sum) pairs are read from LDS at once, then summed.
     float sum = 0.0f, weight = 0.0f;
     for (uint32_t c0 = 0; c0 < count; c0 += B) {
         if (c0 > 0) {
 #pragma unroll
             for (uint32_t j = 0; j < B; ++j) p[j] = ld_f32<COH>(pc + static_cast<uint64_t>(min(c0 + j, count - 1)) * hd);
         }
-        // (eight chunks at a time, each group's LDS reads kept after the
-        // previous group's arithmetic, so that they do not all take registers)
 #pragma unroll
         for (uint32_t j0 = 0; j0 < B; j0 += 8) {
+            float2 f[8];
 #pragma unroll
-            for (uint32_t j = j0; j < j0 + 8 && j < B; ++j) {
-                const uint32_t c = min(c0 + j, count - 1);
-                const float rj = s_r[c], lj = s_l[c];
-                const bool live = c0 + j < count && rj >= 0.0f;
-                const float rr = live ? rj : 0.0f;
-                sum += rr * (live ? p[j] : 0.0f);
-                weight += rr * (live ? lj : 0.0f);
+            for (uint32_t j = 0; j < 8; ++j) f[j] = s_rl[min(c0 + j0 + j, count - 1)];
+#pragma unroll
+            for (uint32_t j = 0; j < 8 && j0 + j < B; ++j) {
+                const uint32_t keep = c0 + j0 + j < count && f[j].x >= 0.0f ? ~0u : 0u;
+                const float rr = __uint_as_float(__float_as_uint(f[j].x) & keep);
+                sum += rr * __uint_as_float(__float_as_uint(p[j0 + j]) & keep);
+                weight += rr * __uint_as_float(__float_as_uint(f[j].y) & keep);
             }
             __builtin_amdgcn_sched_barrier(0);
         }

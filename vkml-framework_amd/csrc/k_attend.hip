@@ -73,10 +73,10 @@ constexpr uint32_t kMergeMaxChunks = 1024;  // 131072 keys
 // The merge as its own launch: head blockIdx.x, element threadIdx.x.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_attend_merge(const float* partial, const float* stats, float* out, uint8_t* values, float* scales, uint32_t chunks, uint32_t hd) {
-    __shared__ float s_r[kMergeMaxChunks];   // exp(m_c - M), or -1 for a chunk past the live keys
-    __shared__ float s_l[kMergeMaxChunks];   // the chunk's sum of weights
+    // (exp(m_c - M), or -1 for a chunk past the live keys; the chunk's sum of weights)
+    __shared__ float2 s_rl[kMergeMaxChunks];
     __shared__ float s_wmax[8];
-    merge_head<false, 48>(partial, stats, out, values, scales, blockIdx.x, chunks, chunks, hd, threadIdx.x, s_r, s_l, s_wmax);
+    merge_head<false, 48>(partial, stats, out, values, scales, blockIdx.x, chunks, chunks, hd, threadIdx.x, s_rl, s_wmax);
 }
 
 template <int HD, bool F16>
@@ -161,11 +161,10 @@ __global__ void __launch_bounds__(kThreads) k_merge_o(MergeOArgs m, vkml::gemv::
     if (blockIdx.x < m.merge_wgs) {
         const uint32_t hpw = kThreads / m.hd, half = threadIdx.x / m.hd, d = threadIdx.x % m.hd;
         float* f = reinterpret_cast<float*>(smem);
-        float* s_r = f + half * 2 * m.chunks;
-        float* s_l = s_r + m.chunks;
+        float2* s_rl = reinterpret_cast<float2*>(f + half * 2 * m.chunks);
         float* s_wmax = f + hpw * 2 * m.chunks + half * (m.hd / kWave);
-        merge_head<true, 36>(m.partial, m.stats, m.out, m.values, m.scales, blockIdx.x * hpw + half, m.chunks, m.chunks, m.hd, d, s_r,
-                         s_l, s_wmax);
+        merge_head<true, 36>(m.partial, m.stats, m.out, m.values, m.scales, blockIdx.x * hpw + half, m.chunks, m.chunks, m.hd, d, s_rl,
+                         s_wmax);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the write-through stores have completed
         __syncthreads();
         if (threadIdx.x < OSync::kCopies)
@@ -317,8 +316,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
     constexpr uint32_t kAtOnce = kHalves < HPW ? kHalves : HPW;
     const uint32_t half = threadIdx.x / HD, d = threadIdx.x % HD;
     float* fl = reinterpret_cast<float*>(smem);
-    float* s_r = fl + half * 2 * a.chunks;
-    float* s_l = s_r + a.chunks;
+    float2* s_rl = reinterpret_cast<float2*>(fl + half * 2 * a.chunks);
     float* s_wmax = fl + kHalves * 2 * a.chunks + half * (HD / kWave);
     // Chunks past the live keys hold a max of -inf, which the merge skips:
     // it walks the live ones only.
@@ -326,9 +324,9 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
 #pragma unroll
     for (uint32_t h0 = 0; h0 < HPW; h0 += kAtOnce) {
         const bool mine = half < kAtOnce;
-        if (h0 > 0) __syncthreads();  // the previous pass is done with s_r, s_l
+        if (h0 > 0) __syncthreads();  // the previous pass is done with s_rl
         merge_head<true, 36>(a.partial, a.stats, mine ? f.out : nullptr, mine ? f.values : nullptr, f.scales,
-                             head0 + h0 + (mine ? half : 0), a.chunks, live, HD, d, s_r, s_l, s_wmax);
+                             head0 + h0 + (mine ? half : 0), a.chunks, live, HD, d, s_rl, s_wmax);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();

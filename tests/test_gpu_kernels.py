@@ -380,6 +380,52 @@ def test_rope_kv_append_bit_exact(kv_type):
         assert np.array_equal(kg.view(np.uint32), kr.view(np.uint32)) and np.array_equal(vg.view(np.uint32), vr.view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt,heads,kvh,hd,kv_type,split", [
+    (H.Q4_K, 32, 8, 128, H.F16, False), (H.Q8_0, 16, 4, 64, H.F32, False), (H.Q4_K, 8, 8, 64, H.F16, True)])
+def test_gemv_rope_bit_exact(fmt, heads, kvh, hd, kv_type, split):
+    # the q|k|v GEMV with the RMSNorm + Q8_0 prologue and the RoPE + KV append
+    # epilogue: q and k rotated as rope.comp does at the state's position, v
+    # as is, the new key and value in the caches' row position % capacity;
+    # split: q, k and v as three matrices at their row offsets
+    k, cap, pos = 2048 if hd == 128 else 512, 96, 133
+    rows = (heads + 2 * kvh) * hd
+    rng = np.random.default_rng(heads + hd + kvh)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    nw = rng.standard_normal(k).astype(np.float32)
+    table = O.rope_table(pos + 1, hd, 1e6)
+    aw, asc = O.quantize(O.Q8_0, O.rms_norm(x.reshape(1, k), nw, 1e-5), False)
+    dt = np.uint16 if kv_type == H.F16 else np.float32
+    kc, vc = dev(np.zeros((kvh, cap, hd), dt)), dev(np.zeros((kvh, cap, hd), dt))
+    st, qkv = H.empty(16), H.empty(rows * 4)
+    H.call("vkml_state_set", p(st), 0, pos, 0)
+    parts = [(0, heads * hd), (heads * hd, kvh * hd), ((heads + kvh) * hd, kvh * hd)] if split else [(0, rows)]
+    y = np.empty(rows, np.float32)
+    for i, (row0, n) in enumerate(parts):
+        v, s_, quant, words, scales = weights(fmt, n, k, 60 + i)
+        y[row0:row0 + n] = O.gemv_dot(quant, aw, asc, 1, words, scales, n, k)[0]
+        prm = H.GemvRopeParams(n, k, fmt, H.F16, 1e-5, row0, heads, kvh, hd, cap, kv_type, 1)
+        H.call("vkml_gemv_rope", prm, p(dev(x)), p(dev(nw)), p(v), p(s_), p(qkv), p(dev(table)), p(st), p(kc), p(vc))
+    q = O.rope(y[:heads * hd].reshape(1, heads, hd), table, pos, 0).ravel()
+    kr = O.rope(y[heads * hd:(heads + kvh) * hd].reshape(1, kvh, hd), table, pos, 0).reshape(kvh, hd)
+    vr = y[(heads + kvh) * hd:].reshape(kvh, hd)
+    want = np.concatenate([q, kr.ravel(), vr.ravel()])
+    assert np.array_equal(bits(qkv.download(np.float32, rows)), bits(want))
+    row = pos % cap
+    kg, vg = kc.download(dt, (kvh, cap, hd)), vc.download(dt, (kvh, cap, hd))
+    if kv_type == H.F16:
+        assert np.array_equal(kg[:, row], O.f32_to_f16(kr)) and np.array_equal(vg[:, row], O.f32_to_f16(vr))
+    else:
+        assert np.array_equal(bits(kg[:, row]), bits(kr)) and np.array_equal(bits(vg[:, row]), bits(vr))
+    others = np.delete(np.arange(cap), row)
+    assert not kg[:, others].any() and not vg[:, others].any()
+
+
+def test_gemv_rope_rejects_odd_rows():
+    prm = H.GemvRopeParams(63, 256, H.Q4_K, H.F16, 1e-5, 1, 4, 2, 32, 16, H.F16, 1)
+    with pytest.raises(H.VkmlError, match="even-aligned"):
+        H.call("vkml_gemv_rope", prm, None, None, None, None, None, None, None, None, None)
+
+
 # ---------------------------------------------------------------- attention
 
 @pytest.mark.parametrize("hd,heads,kvh,kv_len,kv_type,extra", [
@@ -604,6 +650,44 @@ def test_attend_step_fused_bit_exact(hd, heads, kvh, pos, kv_type, fmt, n, windo
         got = x.download(np.float32, n)
         assert np.array_equal(bits(got), bits(want_x))
         assert np.array_equal(bits(got), bits(x2.download(np.float32, n)))
+
+
+@pytest.mark.parametrize("pos,ready,kv_type", [(4096, 16, H.F16), (300, 2, H.F32), (100, 8, H.F16), (1000, 4, H.F16)])
+def test_attend_step_fused_prepared_bit_exact(pos, ready, kv_type):
+    # a prepared step (q already rotated, the new key and value already in
+    # the caches, as vkml_gemv_rope leaves them) whose first `ready` chunks
+    # load before reading the position; the hint may name chunks past the
+    # live keys (position 100 with 8), whose rows are then masked out
+    hd, heads, kvh, n = 128, 32, 8, 4096
+    k, cap = heads * hd, pos + 200
+    chunks = (cap + 127) // 128
+    rng = np.random.default_rng(pos + ready)
+    dt = np.uint16 if kv_type == H.F16 else np.float32
+    prior = rng.standard_normal((2, kvh, cap, hd)).astype(np.float32)
+    caches = [prior[i].astype(np.float16).view(np.uint16) if kv_type == H.F16 else prior[i] for i in range(2)]
+    kc, vc = dev(caches[0]), dev(caches[1])
+    v, s_, quant, words, scales = weights(H.Q4_K, n, k, pos + 7)
+    x0 = rng.standard_normal(n).astype(np.float32)
+    x = dev(x0)
+    fbytes = H.lib().vkml_attend_fused_sync_bytes(2)
+    fsync = H.empty(fbytes)
+    H.call("vkml_fill_u32", p(fsync), 0, fbytes // 4)
+    part, stats, st = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8), H.empty(16)
+    H.call("vkml_state_set", p(st), 0, pos, 0)
+    q = rng.standard_normal((heads, hd)).astype(np.float32)
+    qkv = np.concatenate([q.ravel(), rng.standard_normal(2 * kvh * hd).astype(np.float32)])
+    out, vals, scs = H.empty(k * 4), H.empty(k), H.empty(k // 32 * 4)
+    prm = H.AttendStepParams(heads, kvh, hd, cap, 0, 0, kv_type, chunks, 0, 1, 1.0 / math.sqrt(hd), 0.0, 0, 1, ready)
+    H.call("vkml_attend_step_fused", prm, p(dev(qkv)), None, p(kc), p(vc), p(part), p(stats), p(out), p(vals), p(scs), p(st),
+           H.GemvDotParams(1, n, k, H.Q4_K, H.F16), p(v), p(s_), p(x), p(fsync), 0, 2)
+    H.call("vkml_attend_fused_check", p(fsync), 2)
+    want = O.attend_decode(q, caches[0], caches[1], 0, pos + 1)
+    assert np.array_equal(bits(out.download(np.float32, (heads, hd))), bits(want))
+    ww, ws = O.quantize(O.Q8_0, want.reshape(1, k), False)
+    assert np.array_equal(bits(x.download(np.float32, n)), bits(x0 + O.gemv_dot(quant, ww, ws, 1, words, scales, n, k)[0]))
+    # nothing was appended: the caches are as they were
+    assert np.array_equal(kc.download(dt, caches[0].shape), caches[0])
+    assert np.array_equal(vc.download(dt, caches[1].shape), caches[1])
 
 
 def test_attend_step_fused_reports_a_position_past_its_chunks():

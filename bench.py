@@ -54,8 +54,8 @@ PROMPT = 4096
 # kernel sources they were taken on: GATE_UP_TRAFFIC_SOURCES is the SHA-256
 # (first 16 hex digits) of those files, and the line reports no traffic
 # when the sources have changed since.
-GATE_UP_TRAFFIC = 67_470_468
-GATE_UP_TRAFFIC_SOURCES = "9e26e08ed55b2f46"
+GATE_UP_TRAFFIC = 67_605_054
+GATE_UP_TRAFFIC_SOURCES = "b8ec832d8172fb19"
 TRAFFIC_FILES = ("vkml-framework_amd/csrc/gemv.hpp", "vkml-framework_amd/csrc/k_gemv.hip", "vkml-framework_amd/csrc/device.hpp")
 
 # GGUF-native bytes per weight (q4_K 144 B / 256, q6_K 210 B / 256).

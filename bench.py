@@ -21,14 +21,17 @@ back to back over rotating distinct copies of at least 512 MB, so no cache
 holds the operands; best and median per launch over the rotations), and
 cfg3's decode rate with its 512-token prefill on the matrix cores.
 
-The dominant kernel is the fused gate/up GEMV (66 MB of q4_K weights a
-layer, the largest share of a step's bytes and of its time): the ffn RMSNorm
-and the activation's Q8_0 in its prologue, gate and up dot products, SwiGLU,
-and h's Q8_0 in its epilogue, as the step launches it. Its average launch
-duration is measured here with two HIP events on the library's stream
-around back-to-back launches at the step's exact shape over 32 distinct
-weight pairs (2.1 GB, more than any cache holds), the way the step streams
-one layer's matrices after another. A per-kernel table of extra
+The dominant kernel, the one taking the largest share of a step's time, is
+the one attention launch a layer (k_attend_fused: the chunk pass over the
+f16 caches, the merges, and the o GEMV + residual add). Its average launch
+duration is measured here with two HIP events on the library's stream around
+back-to-back launches at the step's exact shape, at the middle position of
+the timed run, over 32 distinct KV caches and o matrices (873 MB, more than
+any cache holds), the way the step goes from one layer to the next. The
+fused gate/up GEMV, the kernel moving the most bytes (66 MB of q4_K weights
+a layer, with the ffn RMSNorm and the activation's Q8_0 in its prologue and
+SwiGLU and h's Q8_0 in its epilogue), gets a second entry measured the same
+way over 32 distinct weight pairs (2.1 GB). A per-kernel table of extra
 eager steps (HIP events around each launch, so with launch gaps) goes to
 stderr.
 """
@@ -47,16 +50,22 @@ PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
 PEAK_INT8_TOPS = 5000.0  # dense int8 MFMA, TOP/s
 PROMPT = 4096
 
-# HBM bytes one gate/up launch moves (reads + writes): FETCH_SIZE and
-# WRITE_SIZE passes of rocprofv3 over `bench.py --roofline-only`, each scaled
-# by the same counter's reading for a 256 MiB device copy; the readings and
-# commands are in profiles/gate_up_cfg5_hbm_traffic.md. Valid only for the
-# kernel sources they were taken on: GATE_UP_TRAFFIC_SOURCES is the SHA-256
-# (first 16 hex digits) of those files, and the line reports no traffic
-# when the sources have changed since.
+# HBM bytes one launch of each roofline kernel moves (reads + writes):
+# FETCH_SIZE and WRITE_SIZE passes of rocprofv3 over `bench.py
+# --roofline-only`, each scaled by the same counter's reading for a 256 MiB
+# device copy; the readings and commands are in
+# profiles/attend_step_cfg5_hbm_traffic.md and
+# profiles/gate_up_cfg5_hbm_traffic.md. Each figure holds only for the
+# kernel sources it was taken on: its hash is the SHA-256 (first 16 hex
+# digits) of those files, and the line reports no traffic when they have
+# changed since.
 GATE_UP_TRAFFIC = 67_605_054
 GATE_UP_TRAFFIC_SOURCES = "b8ec832d8172fb19"
 TRAFFIC_FILES = ("vkml-framework_amd/csrc/gemv.hpp", "vkml-framework_amd/csrc/k_gemv.hip", "vkml-framework_amd/csrc/device.hpp")
+ATTEND_TRAFFIC = 28_573_079
+ATTEND_TRAFFIC_SOURCES = "d1520404944f2028"
+ATTEND_FILES = ("vkml-framework_amd/csrc/k_attend.hip", "vkml-framework_amd/csrc/attend.hpp", "vkml-framework_amd/csrc/gemv.hpp",
+                "vkml-framework_amd/csrc/device.hpp")
 
 # GGUF-native bytes per weight (q4_K 144 B / 256, q6_K 210 B / 256).
 Q4K, Q6K = 144 / 256, 210 / 256
@@ -179,13 +188,86 @@ def time_gate_up(spec, layers=32, rounds=3):
     return ms * 1e3 / (layers * rounds), weight_bytes + io_bytes
 
 
+def attention_shape(spec, prompt, steps):
+    """The decode step's one attention launch a layer at the middle of the
+    timed positions: (position, cache rows, chunks launched, chunks that
+    load before reading the position), as src/llama.cpp sizes them (chunks
+    of 128 keys in power-of-two tiers from 8; a tier above the smallest
+    lets its lower half load early)."""
+    position = prompt + steps // 2
+    rows = prompt + steps + 1
+    chunks = (rows + 127) // 128
+    tier = 8
+    while tier * 128 < position + 1:
+        tier *= 2
+    launched = min(chunks, tier)
+    ready = min(tier // 2, launched) if tier > 8 else 0
+    return position, rows, launched, ready
+
+
+def time_attention_step(spec, prompt=PROMPT, steps=256, layers=32, rounds=3):
+    """Average duration of vkml_attend_step_fused as the decode step
+    launches it (k_attend_fused: the chunk pass over the f16 caches, the
+    merges, and the o GEMV + residual add of q4_K o weights), over `layers`
+    distinct KV caches and o matrices launched back to back (873 MB, more
+    than any cache holds), `rounds` times, between two HIP events, at the
+    middle position of the timed run. The caches and weights hold fixed
+    patterns (finite f16 values). Algorithmic bytes of one launch: the K
+    and V rows of positions 0 .. position (f16), the o matrix (GGUF q4_K),
+    q in, and the residual read and written; the chunk partials (split-K
+    overhead) are not counted."""
+    import math
+    from vkml_amd import hip as H
+    heads, kvh, hd, d = spec.heads, spec.kv_heads, spec.head_dim, spec.hidden
+    position, rows, chunks, ready = attention_shape(spec, prompt, steps)
+    cache = kvh * rows * hd * 2
+    o_codes, o_hdr = d * heads * hd // 2, d * heads * hd // 256 * 16
+    caches = [(filled(cache, 0x3C003800 + i), filled(cache, 0x38003C00 + i)) for i in range(layers)]
+    mats = [(filled(o_codes, 0x5A3C96E1 + i), filled(o_hdr, 0x2C1F2C00)) for i in range(layers)]
+    qkv = filled((heads + 2 * kvh) * hd * 4, 0x3F000000)
+    x = filled(d * 4, 0x3F000000)
+    part, stats = filled(heads * chunks * hd * 4, 0), filled(heads * chunks * 8, 0)
+    attn, aq, as_ = filled(heads * hd * 4, 0), filled(heads * hd, 0), filled(heads * hd // 32 * 4, 0)
+    st = filled(16, 0)
+    H.call("vkml_state_set", st.p, 0, position, 0)
+    fbytes = H.lib().vkml_attend_fused_sync_bytes(layers)
+    fsync = filled(fbytes, 0)
+    prm = H.AttendStepParams(heads, kvh, hd, rows, 0, 0, H.F16, chunks, 0, 1, 1.0 / math.sqrt(hd), 0.0, 0, 1, ready)
+    op = H.GemvDotParams(1, d, heads * hd, H.Q4_K, H.F16)
+
+    def launches():
+        for _ in range(rounds):
+            for li in range(layers):
+                H.call("vkml_attend_step_fused", prm, qkv.p, None, caches[li][0].p, caches[li][1].p, part.p, stats.p, attn.p,
+                       aq.p, as_.p, st.p, op, mats[li][0].p, mats[li][1].p, x.p, fsync.p, li, layers)
+
+    ev = _Events()
+    try:
+        launches()  # warm
+        H.synchronize()
+        ms = ev.elapsed_ms(H.stream(), launches)
+        H.call("vkml_attend_fused_check", fsync.p, layers)
+    finally:
+        ev.close()
+        for pair in caches + mats:
+            for b in pair:
+                b.close()
+        for b in (qkv, x, part, stats, attn, aq, as_, st, fsync):
+            b.close()
+    alg = 2 * kvh * (position + 1) * hd * 2 + d * heads * hd * 144 // 256 + heads * hd * 4 + 2 * d * 4
+    return ms * 1e3 / (layers * rounds), alg, {"position": position, "chunks": chunks, "ready_chunks": ready}
+
+
 def roofline_only(spec):
-    """The dominant kernel's measurement alone, then a device copy of 256 MiB
-    (hipMemcpy device to device, the runtime's copy kernel) launched three
-    times: per dispatch it reads and writes exactly 268,435,456 bytes, the
-    known size against which a counter's reading is scaled."""
+    """The dominant kernels' measurements alone, then a device copy of 256
+    MiB (hipMemcpy device to device, the runtime's copy kernel) launched
+    three times: per dispatch it reads and writes exactly 268,435,456 bytes,
+    the known size against which a counter's reading is scaled."""
     from vkml_amd import hip as H
     H.init()
+    att_us, att_bytes, shape = time_attention_step(spec, rounds=1)
+    log(f"attend_step_fused at position {shape['position']}: {att_us:.2f} us a launch, "
+        f"{att_bytes / (att_us * 1e-6) / 1e9:.0f} GB/s ({att_bytes} algorithmic bytes)")
     dom_us, dom_bytes = time_gate_up(spec, layers=32, rounds=1)
     log(f"gemv_fused gate/up: {dom_us:.2f} us a launch, {dom_bytes / (dom_us * 1e-6) / 1e9:.0f} GB/s "
         f"({dom_bytes} algorithmic bytes)")
@@ -500,9 +582,9 @@ def main():
         n_layers = spec.n_layers
         kv_mean = args.prompt + (args.profile_steps + 1) / 2
         launch_bytes = {
-            "gemv_fused:qkv": per_layer["qkv"], "gemv_dot_add:o": per_layer["o"], "gemv_fused:gate_up": per_layer["gate_up"],
+            "gemv_rope:qkv": per_layer["qkv"], "gemv_fused:gate_up": per_layer["gate_up"],
             "gemv_dot_add:down": per_layer["down"], "gemv_dot:lm_head": spec.vocab * spec.hidden * Q6K,
-            "attend_step:attention": kv_pos / n_layers * kv_mean,
+            "attend_fused:attention": kv_pos / n_layers * kv_mean + per_layer["o"],
         }
         rows = []
         for name, calls, ms in prof:
@@ -514,9 +596,13 @@ def main():
         for r in sorted(rows, key=lambda r: -r["calls"] * r["avg_us"])[:14]:
             log(f"  {r['kernel']:<28} calls {r['calls']:>6}  avg {r['avg_us']:9.2f} us  {r['gb_s'] or '':>8} GB/s")
         busy_ms = sum(ms for _, _, ms in prof) / args.profile_steps if args.profile_steps else None
-        dom_us, dom_bytes = time_gate_up(spec)
-        achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-        log(f"gemv_fused (norm + gate/up + swiglu + q8_0) back to back: {dom_us:.2f} us a launch, {achieved:.0f} GB/s")
+        att_us, att_bytes, att_shape = time_attention_step(spec, args.prompt, args.steps)
+        att_rate = att_bytes / (att_us * 1e-6) / 1e9
+        log(f"attend_step_fused (chunks, merge, o GEMV + residual) back to back at position {att_shape['position']}: "
+            f"{att_us:.2f} us a launch, {att_rate:.0f} GB/s")
+        gu_us, gu_bytes = time_gate_up(spec)
+        gu_rate = gu_bytes / (gu_us * 1e-6) / 1e9
+        log(f"gemv_fused (norm + gate/up + swiglu + q8_0) back to back: {gu_us:.2f} us a launch, {gu_rate:.0f} GB/s")
 
         pre = prefill_rates(model, spec, prompt, args.prefill, L) if args.prefill else None
 
@@ -561,7 +647,8 @@ def main():
             configs["cfg5_short_position"] = bench_short_position(L, path)
             configs["cfg3"] = bench_cfg3(L)
 
-        traffic = GATE_UP_TRAFFIC if sources_hash() == GATE_UP_TRAFFIC_SOURCES else None
+        gu_traffic = GATE_UP_TRAFFIC if sources_hash() == GATE_UP_TRAFFIC_SOURCES else None
+        att_traffic = ATTEND_TRAFFIC if ATTEND_TRAFFIC and sources_hash(ATTEND_FILES) == ATTEND_TRAFFIC_SOURCES else None
         result = {
             "metric": "batch-1 decode tokens/s + achieved HBM GB/s (% of 8 TB/s), 1xMI355X",
             "value": round(tok_s, 2),
@@ -583,12 +670,20 @@ def main():
             "hbm_frac": round(hbm / PEAK_HBM, 4),
             "bytes_per_step": round(step_bytes),
             "gpu_busy_ms_per_step": round(busy_ms, 4) if busy_ms is not None else None,
-            "roofline": {"bound": "hbm", "kernel": "gemv_fused gate/up (k_gemv_dot<q4_K, f16, 8 lanes, swiglu, norm, q8_0 out>)",
-                         "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s",
-                         "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
-                         "traffic_over_algorithmic": round(traffic / dom_bytes, 4) if traffic else None,
-                         "traffic_sources": sources_hash(),
-                         "bytes_per_launch": round(dom_bytes), "avg_launch_us": round(dom_us, 3)},
+            "roofline": {"bound": "hbm",
+                         "kernel": "attend_step_fused (k_attend_fused: chunk pass, merges, o GEMV + residual; one launch a layer)",
+                         "achieved": round(att_rate, 1), "peak": PEAK_HBM, "unit": "GB/s",
+                         "frac": round(att_rate / PEAK_HBM, 4), "traffic": att_traffic,
+                         "traffic_over_algorithmic": round(att_traffic / att_bytes, 4) if att_traffic else None,
+                         "traffic_sources": sources_hash(ATTEND_FILES),
+                         "bytes_per_launch": round(att_bytes), "avg_launch_us": round(att_us, 3), "shape": att_shape},
+            "roofline_gate_up": {"bound": "hbm",
+                                 "kernel": "gemv_fused gate/up (k_gemv_dot<q4_K, f16, 8 lanes, swiglu, norm, q8_0 out>)",
+                                 "achieved": round(gu_rate, 1), "peak": PEAK_HBM, "unit": "GB/s",
+                                 "frac": round(gu_rate / PEAK_HBM, 4), "traffic": gu_traffic,
+                                 "traffic_over_algorithmic": round(gu_traffic / gu_bytes, 4) if gu_traffic else None,
+                                 "traffic_sources": sources_hash(),
+                                 "bytes_per_launch": round(gu_bytes), "avg_launch_us": round(gu_us, 3)},
             "cpu_baseline": cpu,
             "parity": parity,
             "prefill": pre,

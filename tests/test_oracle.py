@@ -448,7 +448,7 @@ def test_attend_first_key_alone_returns_v0_exactly():
 
 # ---------------------------------------------------------------- whole model
 
-def _hf_logits(path, tokens):
+def _hf_logits(path, tokens, all_rows=False):
     """Hugging Face's LlamaForCausalLM in float64 on the file's dequantized
     weights: an implementation independent of the oracle. GGUF's llama
     rotates interleaved pairs; HF rotates halves, so q and k rows are put
@@ -495,7 +495,8 @@ def _hf_logits(path, tokens):
         sd[p + "mlp.down_proj.weight"] = val(g + "ffn_down.weight")
     model.load_state_dict({k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in sd.items()}, strict=False)
     with torch.no_grad():
-        out = model(torch.tensor([list(tokens)], dtype=torch.long)).logits[0, -1]
+        out = model(torch.tensor([list(tokens)], dtype=torch.long)).logits[0]
+    out = out if all_rows else out[-1]
     return out.numpy()
 
 
@@ -636,3 +637,71 @@ def test_a_handed_over_cache_continues_as_the_prompt_would(tiny_q4k):
     ref = O.Model(tiny_q4k, 32, kv_f16=True)
     ref.forward(prompt)
     assert not np.array_equal(ref.forward(np.array([5], np.int32)), off.forward(np.array([5], np.int32)))
+
+
+def test_legacy_blocks_load_dequantize_and_embed_to_the_reference_values():
+    """test_gguf.cpp:105-165's known answers, through the oracle's loader
+    (orc_load_quantized), dequantize and quantized embedding: Q8_0 rows
+    of codes 8i - 127 with f16 scales 0.5 and -2, and a Q4_0 row with scale
+    0.25 whose byte j holds element j (low nibble) and j + 16 (high). Ids
+    outside the vocabulary embed as zeros (embedding.cpp:63-91)."""
+    q = np.array([8 * i - 127 for i in range(32)], np.int8)
+    q8 = b"".join(np.uint16(s).tobytes() + q.tobytes() for s in (0x3800, 0xC000))
+    quant, words, halves = O.load_quantized(O.GGML_Q8_0, q8, 2, 32)
+    assert quant == O.Q8_0 and list(halves) == [0x3800, 0xC000]
+    want8 = np.stack([q.astype(np.float32) * 0.5, q.astype(np.float32) * -2.0])
+    assert np.array_equal(O.dequantize(quant, words, halves, 2, 32), want8)
+    got = O.embedding_quantized(quant, words, halves, 2, 32, [1, 0, 2, -1])
+    assert np.array_equal(got, np.stack([want8[1], want8[0], np.zeros(32), np.zeros(32)]).astype(np.float32))
+
+    q4 = np.uint16(0x3400).tobytes() + bytes(j | ((15 - j) << 4) for j in range(16))
+    quant, words, halves = O.load_quantized(O.GGML_Q4_0, q4, 1, 32)
+    assert quant == O.Q4_0 and list(halves) == [0x3400]
+    want4 = np.array([(j - 8) * 0.25 for j in range(16)] + [(15 - j - 8) * 0.25 for j in range(16)], np.float32)
+    assert np.array_equal(O.dequantize(quant, words, halves, 1, 32)[0], want4)
+    assert np.array_equal(O.embedding_quantized(quant, words, halves, 1, 32, [0, 1])[0], want4)
+    assert not O.embedding_quantized(quant, words, halves, 1, 32, [0, 1])[1].any()
+    # test_gguf.cpp:160-162: a row of ones times it sums to -4
+    assert float(want4.sum()) == -4.0
+
+
+def test_quantized_embedding_rows_are_the_dequantized_rows():
+    """Every id of a random table embeds as that row of the dequantized
+    table, bit for bit, in each QuantizedMatrix format (embedding_quantized.
+    comp reads the same codes and scales as dequantize.comp)."""
+    rng = np.random.default_rng(11)
+    vocab, dim = 37, 96
+    x = (rng.standard_normal((vocab, dim)) * 3).astype(np.float32)
+    ids = np.array([0, 36, 5, 5, 17, 37, -3, 2], np.int32)
+    for quant in (O.Q8_0, O.Q4_0, O.Q4_1):
+        words, scales = O.quantize(quant, x, True)
+        table = O.dequantize(quant, words, scales, vocab, dim)
+        got = O.embedding_quantized(quant, words, scales, vocab, dim, ids)
+        for r, i in enumerate(ids):
+            want = table[i] if 0 <= i < vocab else np.zeros(dim, np.float32)
+            assert np.array_equal(got[r].view(np.uint32), want.view(np.uint32)), (quant, i)
+        # and the table is within half a step of what was quantized
+        step = np.abs(x).reshape(vocab, -1, 32).max(axis=2, keepdims=True) / (127 if quant == O.Q8_0 else 7)
+        assert np.all(np.abs(table - x).reshape(vocab, -1, 32) <= step * (0.51 if quant == O.Q8_0 else 2.2))
+
+
+def test_forward_all_rows_match_transformers(tiny_f32):
+    """Every row of forward_all (a 9-token prompt through the f32 path's
+    matmul), not only the last, within test_llama.cpp:758-764's 1e-4 of
+    Hugging Face's logits at that position."""
+    tokens = np.random.default_rng(5).integers(0, 4096, 9).astype(np.int32)
+    got = O.Model(tiny_f32, 64, kv_f16=False).forward_all(tokens)
+    want = _hf_logits(tiny_f32, tokens, all_rows=True)
+    assert got.shape == want.shape == (9, 4096)
+    assert np.all(np.abs(got - want) <= 1e-4 * (1 + np.abs(want)))
+
+
+def test_forward_all_rows_of_the_int8_path_track_the_double_reference(tiny_q4k):
+    """forward_all's rows on the int8 path (16 rows through matmul_dot)
+    each within test_llama.cpp:1281-1312's few percent of the largest logit
+    of the double-precision reference on that row's prefix."""
+    tokens = np.random.default_rng(6).integers(0, 1000, 16).astype(np.int32)
+    rows = O.Model(tiny_q4k, 32, kv_f16=True).forward_all(tokens)
+    for i in (0, 3, 8, 15):
+        want = O.reference_f64(tiny_q4k, tokens[:i + 1])
+        assert np.max(np.abs(rows[i] - want)) <= 0.04 * np.abs(want).max(), i

@@ -188,7 +188,7 @@ def time_gate_up(spec, layers=32, rounds=3):
     return ms * 1e3 / (layers * rounds), weight_bytes + io_bytes
 
 
-def attention_shape(spec, prompt, steps):
+def attention_shape(prompt, steps):
     """The decode step's one attention launch a layer at the middle of the
     timed positions: (position, cache rows, chunks launched, chunks that
     load before reading the position), as src/llama.cpp sizes them (chunks
@@ -219,7 +219,7 @@ def time_attention_step(spec, prompt=PROMPT, steps=256, layers=32, rounds=3):
     import math
     from vkml_amd import hip as H
     heads, kvh, hd, d = spec.heads, spec.kv_heads, spec.head_dim, spec.hidden
-    position, rows, chunks, ready = attention_shape(spec, prompt, steps)
+    position, rows, chunks, ready = attention_shape(prompt, steps)
     cache = kvh * rows * hd * 2
     o_codes, o_hdr = d * heads * hd // 2, d * heads * hd // 256 * 16
     caches = [(filled(cache, 0x3C003800 + i), filled(cache, 0x38003C00 + i)) for i in range(layers)]

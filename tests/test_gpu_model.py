@@ -306,3 +306,23 @@ def test_vkml_bench_app_results_are_exact():
     assert r.returncode == 0, r.stderr
     lines = [ln for ln in r.stdout.splitlines()[1:] if ln.strip()]
     assert len(lines) == 18 and all(ln.split()[-1] == "ok" for ln in lines), r.stdout
+
+
+def test_context_past_the_merge_limit_is_rejected_at_load(tmp_path):
+    """Decode attention merges at most 1024 chunks of 128 keys a head, so a
+    model loads with a context of 131072 positions and is refused at
+    131073 with a message naming the limit (not later, at a step)."""
+    spec = synth.ModelSpec("long-ctx", 1, 256, 4, 2, 64, 512, 1000, 10000.0, max_positions=140000,
+                           matrix_type=gguf.Q8_0, embed_type=gguf.Q8_0, output_type=gguf.Q8_0)
+    path = synth.write_model(spec, str(tmp_path / "long.gguf"), seed=9)
+    with pytest.raises(VkmlError, match="at most 131072 keys"):
+        Llama(path, 131073)
+    m = Llama(path, 131072)
+    ref = O.Model(path, 64)
+    tokens = np.array([3, 17, 5], np.int32)
+    for t in tokens:
+        got = m.forward(np.array([t], np.int32))
+        want = ref.forward(np.array([t], np.int32))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    m.close()
+    ref.close()

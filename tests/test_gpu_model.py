@@ -316,9 +316,9 @@ def test_context_past_the_merge_limit_is_rejected_at_load(tmp_path):
                            matrix_type=gguf.Q8_0, embed_type=gguf.Q8_0, output_type=gguf.Q8_0)
     path = synth.write_model(spec, str(tmp_path / "long.gguf"), seed=9)
     with pytest.raises(VkmlError, match="at most 131072 keys"):
-        Llama(path, 131073)
-    m = Llama(path, 131072)
-    ref = O.Model(path, 64)
+        Llama(path, 131073, kv_f16=True)
+    m = Llama(path, 131072, kv_f16=True)
+    ref = O.Model(path, 64, kv_f16=True)
     tokens = np.array([3, 17, 5], np.int32)
     for t in tokens:
         got = m.forward(np.array([t], np.int32))

@@ -205,7 +205,7 @@ def attention_shape(prompt, steps):
     return position, rows, launched, ready
 
 
-def time_attention_step(spec, prompt=PROMPT, steps=256, layers=32, rounds=3):
+def time_attention_step(spec, prompt=PROMPT, steps=256, layers=32, rounds=3, fast=False):
     """Average duration of vkml_attend_step_fused as the decode step
     launches it (k_attend_fused: the chunk pass over the f16 caches, the
     merges, and the o GEMV + residual add of q4_K o weights), over `layers`
@@ -215,7 +215,8 @@ def time_attention_step(spec, prompt=PROMPT, steps=256, layers=32, rounds=3):
     patterns (finite f16 values). Algorithmic bytes of one launch: the K
     and V rows of positions 0 .. position (f16), the o matrix (GGUF q4_K),
     q in, and the residual read and written; the chunk partials (split-K
-    overhead) are not counted."""
+    overhead) are not counted. With fast, vkml_attend_step_fast (the
+    matrix-core attention option) instead."""
     import math
     from vkml_amd import hip as H
     heads, kvh, hd, d = spec.heads, spec.kv_heads, spec.head_dim, spec.hidden
@@ -238,8 +239,12 @@ def time_attention_step(spec, prompt=PROMPT, steps=256, layers=32, rounds=3):
     def launches():
         for _ in range(rounds):
             for li in range(layers):
-                H.call("vkml_attend_step_fused", prm, qkv.p, None, caches[li][0].p, caches[li][1].p, part.p, stats.p, attn.p,
-                       aq.p, as_.p, st.p, op, mats[li][0].p, mats[li][1].p, x.p, fsync.p, li, layers)
+                if fast:
+                    H.call("vkml_attend_step_fast", prm, qkv.p, caches[li][0].p, caches[li][1].p, part.p, stats.p, attn.p,
+                           aq.p, as_.p, st.p, op, mats[li][0].p, mats[li][1].p, x.p, fsync.p, li, layers)
+                else:
+                    H.call("vkml_attend_step_fused", prm, qkv.p, None, caches[li][0].p, caches[li][1].p, part.p, stats.p,
+                           attn.p, aq.p, as_.p, st.p, op, mats[li][0].p, mats[li][1].p, x.p, fsync.p, li, layers)
 
     ev = _Events()
     try:

@@ -545,6 +545,46 @@ int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* d_qkv,
 /* Synchronizes, then reports (VKML_ERROR_DEVICE) and clears (every block) a
  * wait of an earlier vkml_attend_step_fused on these blocks that timed out. */
 int vkml_attend_fused_check(uint32_t* d_sync, uint32_t blocks);
+/* 1 when vkml_attend_step_fused takes these shapes in its one launch on
+ * this device (the o format, the item's LDS, the merge's chunk count and a
+ * grid whose waiting o workgroups leave the chunk items a slot); 0 when it
+ * would take the separate launches, which need p->chunks covering the
+ * cache. No reference counterpart (a host-side plan query). */
+int vkml_attend_step_fused_supported(const vkml_attend_step_params* p, const vkml_gemv_dot_params* o);
+
+/* Decode attention on the matrix cores, the tolerance form of
+ * vkml_attend + vkml_attend_merge (attend.comp + attend_merge.comp,
+ * attention.cpp:54-84 there): not the reference's order of f32 operations
+ * but f32 attention to within f32 rounding (the products exact, f16 x f16
+ * with q and the softmax weights split in two f16 terms; the sums in f32 in
+ * the matrix unit's order). An option beside the bit-exact kernels, which
+ * stay the default. f16 caches, head_dim 64 or 128, at most 8 query heads
+ * a KV head, at most 1024 chunks of 128 keys. One launch: the chunk items,
+ * then per KV head a merge by its last item into d_out [heads, head_dim]
+ * f32 (may be NULL) and, when d_values is non-NULL, its Q8_0 form with f32
+ * scales. d_partial [heads, chunks, head_dim] and d_stats [heads, chunks, 2]
+ * f32 are its workspace; d_sync: vkml_attend_fused_sync_bytes(1) bytes,
+ * zeroed before the first call (each call leaves it zeroed). Position
+ * from d_state (kv_len = position + 1) if non-NULL; chunks cover kv_len -
+ * kv_start (with d_state, capacity - kv_start). */
+int vkml_attend_fast(const vkml_attend_params* p, const float* d_q, const void* d_k_cache, const void* d_v_cache,
+                     float* d_partial, float* d_stats, float* d_out, void* d_values, float* d_scales, uint32_t* d_sync,
+                     const vkml_decode_state* d_state);
+/* vkml_attend_step_fused's one launch (chunks, merges, o GEMV + residual)
+ * with vkml_attend_fast's items and merges: a prepared step (vkml_gemv_rope
+ * rotated q and appended the new key and value) without a window, at the
+ * decode state's position; the same sync blocks, check
+ * (vkml_attend_fused_check) and chunk tiers (p->chunks may cover fewer keys
+ * than the cache; p->ready_chunks as there). The o GEMV and residual are
+ * vkml_gemv_dot_add's bit for bit on the attention output it is given. */
+int vkml_attend_step_fast(const vkml_attend_step_params* p, const float* d_qkv, void* d_k_cache, void* d_v_cache,
+                          float* d_partial, float* d_stats, float* d_out, void* d_values, float* d_scales,
+                          const vkml_decode_state* d_state, const vkml_gemv_dot_params* o, const void* d_o_values,
+                          const void* d_o_scales, float* d_x, uint32_t* d_sync, uint32_t block, uint32_t blocks);
+/* 1 when vkml_attend_step_fast takes these shapes on this device (cache
+ * type, head_dim, group, window, prepared, o format, and a grid whose o
+ * workgroups leave the chunk items a slot); 0 otherwise. */
+int vkml_attend_step_fast_supported(const vkml_attend_step_params* p, const vkml_gemv_dot_params* o);
 
 /* vkml_attend_step without the d_partial / d_stats workspace, allocating
  * nothing: no counterpart in the reference. For callers that cannot call

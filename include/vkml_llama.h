@@ -35,6 +35,16 @@ typedef struct vkml_llama_options {
     const char* device_name;    /* NULL or "": VKML_DEVICE, then device 0 */
     int64_t prompt_score_bytes; /* scores one piece of a prompt's attention may hold (default 1 GiB); no effect on results */
     int64_t sliding_extra_rows; /* a sliding window's rings hold window + this many rows (default 1024) */
+    /* 1: decode attention on the matrix cores (vkml_attend_step_fast in
+     * vkml_hip.h), f32 attention within f32 rounding instead of the
+     * reference's order of f32 operations; 0 (default): bit-exact. */
+    int32_t fast_attention;
+    /* A sliding window over every layer and logit soft caps (0: none). The
+     * reference reads these only from Gemma files (config.cpp:114-133 there)
+     * and ignores them in a llama file, as here; they are set explicitly. */
+    int64_t sliding_window;
+    float attn_logit_softcap;
+    float final_logit_softcap;
 } vkml_llama_options;
 
 /* LlamaConfig (llama.hpp:29-116), the fields of the llama architecture. */

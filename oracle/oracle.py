@@ -73,6 +73,7 @@ def _declare(L):
         "orc_attention_prefill": (None, [vp, i64, i64, vp, vp, i32, i64, i64, i64, i64, i64, f32, vp]),
         "orc_attention_sliding": (None, [vp, i64, i64, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, f32, vp]),
         "orc_model_load_ex": (vp, [C.c_char_p, i64, i32, i32, i64]),
+        "orc_model_load_opts": (vp, [C.c_char_p, i64, i32, i32, i64, i64, f32, f32]),
         "orc_model_ring": (i64, [vp]),
         "orc_model_load": (vp, [C.c_char_p, i64, i32, i32]),
         "orc_model_free": (None, [vp]),
@@ -323,8 +324,10 @@ class Model:
     """orc_model: the reference's Llama::run restated on the CPU."""
 
     def __init__(self, gguf_path: str, context: int, kv_f16: bool = True, int_dot: bool = True,
-                 sliding_extra_rows: int = 1024):
-        self._h = lib().orc_model_load_ex(gguf_path.encode(), context, int(kv_f16), int(int_dot), sliding_extra_rows)
+                 sliding_extra_rows: int = 1024, sliding_window: int = 0, attn_softcap: float = 0.0,
+                 final_softcap: float = 0.0):
+        self._h = lib().orc_model_load_opts(gguf_path.encode(), context, int(kv_f16), int(int_dot), sliding_extra_rows,
+                                            int(sliding_window), float(attn_softcap), float(final_softcap))
         if not self._h:
             raise RuntimeError(last_error())
         self.vocab = int(lib().orc_model_vocab(self._h))

@@ -246,17 +246,21 @@ void orc_model_free(orc_model* m) {
     free(m);
 }
 
-/* config.cpp:14-140 for arch "llama", then llama.cpp:170-271. A sliding
- * window is read from llama.attention.sliding_window (the key the
- * reference reads for the Gemma architectures, config.cpp:124-125), applied
- * to every layer as the reference's HF Mistral configs do, and the soft
- * caps from llama.attn_logit_softcapping and llama.final_logit_softcapping
- * (config.cpp:130-131). */
+/* config.cpp:14-140 for arch "llama", then llama.cpp:170-271. The
+ * reference reads a sliding window and soft caps from Gemma files only
+ * (config.cpp:114-133) and ignores those keys in a llama file, as here: a
+ * window over every layer (as the reference's HF Mistral configs apply it)
+ * and the soft caps come from the caller (0: none). */
 orc_model* orc_model_load(const char* path, int64_t context_length, int kv_f16, int int_dot) {
-    return orc_model_load_ex(path, context_length, kv_f16, int_dot, 1024);
+    return orc_model_load_opts(path, context_length, kv_f16, int_dot, 1024, 0, 0.0f, 0.0f);
 }
 
 orc_model* orc_model_load_ex(const char* path, int64_t context_length, int kv_f16, int int_dot, int64_t sliding_extra_rows) {
+    return orc_model_load_opts(path, context_length, kv_f16, int_dot, sliding_extra_rows, 0, 0.0f, 0.0f);
+}
+
+orc_model* orc_model_load_opts(const char* path, int64_t context_length, int kv_f16, int int_dot, int64_t sliding_extra_rows,
+                               int64_t window, float attn_softcap, float final_softcap) {
     gguf* g = gguf_open(path);
     if (!g) return NULL;
     const gkv* arch = gguf_kv(g, "general.architecture");
@@ -277,9 +281,9 @@ orc_model* orc_model_load_ex(const char* path, int64_t context_length, int kv_f1
     m->max_pos = (int64_t)kv_num(g, "llama.context_length", 0, &f); ok &= f;
     m->eps = (float)kv_num(g, "llama.attention.layer_norm_rms_epsilon", 1e-5f, NULL);
     m->theta = (float)kv_num(g, "llama.rope.freq_base", 10000.0f, NULL);
-    m->window = (int64_t)kv_num(g, "llama.attention.sliding_window", 0, NULL);
-    m->attn_softcap = (float)kv_num(g, "llama.attn_logit_softcapping", 0.0, NULL);
-    m->final_softcap = (float)kv_num(g, "llama.final_logit_softcapping", 0.0, NULL);
+    m->window = window > 0 ? window : 0;
+    m->attn_softcap = attn_softcap > 0.0f ? attn_softcap : 0.0f;
+    m->final_softcap = final_softcap > 0.0f ? final_softcap : 0.0f;
     const gtensor* te = gguf_tensor(g, "token_embd.weight");
     if (!ok || !te) { orc_error("Llama: %s lacks config keys", path, 0, 0); gguf_free(g); free(m); return NULL; }
     m->vocab = te->shape[0];

@@ -142,6 +142,10 @@ orc_model* orc_model_load(const char* gguf_path, int64_t context_length, int kv_
  * sliding window's rings hold window + that many rows (at most the context). */
 orc_model* orc_model_load_ex(const char* gguf_path, int64_t context_length, int kv_f16, int int_dot,
                              int64_t sliding_extra_rows);
+/* As orc_model_load_ex with a sliding window over every layer and the
+ * attention / final logit soft caps given (0: none). */
+orc_model* orc_model_load_opts(const char* gguf_path, int64_t context_length, int kv_f16, int int_dot, int64_t sliding_extra_rows,
+                               int64_t window, float attn_softcap, float final_softcap);
 /* Rows of each layer's caches (the ring's with a sliding window). */
 int64_t orc_model_ring(const orc_model* m);
 void orc_model_free(orc_model* m);

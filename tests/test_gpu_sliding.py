@@ -153,8 +153,8 @@ def test_sliding_model_matches_the_oracle_through_ring_wraps(tmp_path, kv_f16, p
     oracle's."""
     path = synth.write_model(sliding_spec(), str(tmp_path / "slide.gguf"), seed=8)
     ctx = 256
-    gpu = Llama(path, ctx, kv_f16=kv_f16, sliding_extra_rows=8)
-    ref = O.Model(path, ctx, kv_f16=kv_f16, sliding_extra_rows=8)
+    gpu = Llama(path, ctx, kv_f16=kv_f16, sliding_extra_rows=8, sliding_window=24)
+    ref = O.Model(path, ctx, kv_f16=kv_f16, sliding_extra_rows=8, sliding_window=24)
     assert ref.ring == 32
     prompt = np.random.default_rng(prompt_len).integers(0, 1000, prompt_len).astype(np.int32)
     same(gpu.forward(prompt), ref.forward(prompt), "prompt")
@@ -175,8 +175,8 @@ def test_rewind_keeps_the_window_or_starts_over(tmp_path):
     model starts over at position 0 (llama.cpp:273-285), as the oracle."""
     path = synth.write_model(sliding_spec(), str(tmp_path / "slide.gguf"), seed=9)
     ctx = 200
-    gpu = Llama(path, ctx, kv_f16=True, sliding_extra_rows=8)
-    ref = O.Model(path, ctx, kv_f16=True, sliding_extra_rows=8)
+    gpu = Llama(path, ctx, kv_f16=True, sliding_extra_rows=8, sliding_window=24)
+    ref = O.Model(path, ctx, kv_f16=True, sliding_extra_rows=8, sliding_window=24)
     prompt = np.random.default_rng(3).integers(0, 1000, 60).astype(np.int32)
     same(gpu.forward(prompt), ref.forward(prompt))
     # rings of 32 hold positions 28..59; position 55's window is 32..55
@@ -192,11 +192,33 @@ def test_soft_caps_track_the_oracle(tmp_path):
     """Attention and final logit soft caps (tanh from the device's and the
     host's libraries: within 1e-4 of the largest logit, same argmax)."""
     path = synth.write_model(sliding_spec(window=0, softcaps=(50.0, 30.0)), str(tmp_path / "caps.gguf"), seed=10)
-    gpu = Llama(path, 64, kv_f16=True)
-    ref = O.Model(path, 64, kv_f16=True)
+    gpu = Llama(path, 64, kv_f16=True, attn_softcap=50.0, final_softcap=30.0)
+    ref = O.Model(path, 64, kv_f16=True, attn_softcap=50.0, final_softcap=30.0)
     prompt = np.random.default_rng(5).integers(0, 1000, 20).astype(np.int32)
     for tokens in (prompt, np.array([7], np.int32), np.array([9], np.int32)):
         got, want = gpu.forward(tokens), ref.forward(tokens)
         assert np.max(np.abs(got - want)) <= 1e-4 * np.abs(want).max()
         assert int(np.argmax(got)) == int(np.argmax(want))
         assert np.abs(want).max() <= 30.0
+
+
+def test_llama_file_window_and_cap_keys_are_ignored(tmp_path):
+    """A llama GGUF carrying llama.attention.sliding_window and the
+    soft-capping keys runs full attention without caps, as the reference
+    (it reads those keys for Gemma only, config.cpp:114-133): the same
+    logits as the file without them, on the GPU and in the oracle."""
+    with_keys = synth.write_model(sliding_spec(window=8, softcaps=(5.0, 3.0)), str(tmp_path / "keys.gguf"), seed=11)
+    plain = synth.write_model(sliding_spec(window=0), str(tmp_path / "plain.gguf"), seed=11)
+    prompt = np.random.default_rng(6).integers(0, 1000, 40).astype(np.int32)
+    a, b = Llama(with_keys, 64, kv_f16=True), Llama(plain, 64, kv_f16=True)
+    ref = O.Model(with_keys, 64, kv_f16=True)
+    assert ref.ring == 64
+    want = ref.forward(prompt)
+    same(a.forward(prompt), want, "prompt")
+    same(b.forward(prompt), want, "prompt, plain file")
+    step = ref.forward(np.array([5], np.int32))
+    same(a.forward(np.array([5], np.int32)), step, "step")
+    same(b.forward(np.array([5], np.int32)), step, "step, plain file")
+    a.close()
+    b.close()
+    ref.close()

@@ -556,4 +556,48 @@ __device__ __forceinline__ void merge_head(const float* partial, const float* st
     }
 }
 
+// ------------------------------------------------------------ launch sync
+
+// One block of the sync words of vkml_attend_step_fused: the OSync words
+// (the o GEMV's arrival counters), then an arrival counter per set of chunk
+// items (KV head, head group), kArriveStride words apart. The sticky error
+// flag of every block is word 0 of block 0.
+struct FusedSync {
+    static constexpr uint32_t kArriveStride = 8;
+    static constexpr uint32_t kMaxSets = 256;
+    static constexpr uint32_t kWords = OSync::kWords + kArriveStride * kMaxSets;
+    __host__ __device__ static uint32_t* arrive(uint32_t* s, uint32_t set) { return s + OSync::kWords + kArriveStride * set; }
+};
+
+constexpr uint32_t kOSpinCap = 1u << 20;
+
+// Lane 0 polls counter copy wg % kCopies until every merging workgroup has
+// arrived; false if the wait gave up (the spin limit, or another
+// workgroup's error). The error flag is the sync words' own unless given. Called by every thread; ends with a workgroup barrier
+// (the weight loads issued before it stay in flight).
+__device__ inline bool await_merged(uint32_t* sync, uint32_t wg, uint32_t arrivals, uint32_t* error = nullptr) {
+    __shared__ uint32_t s_ok;
+    if (!error) error = OSync::error(sync);
+    if (threadIdx.x == 0) {
+        uint32_t ok = 1;
+        uint32_t* c = OSync::counter(sync, wg % OSync::kCopies);
+        for (uint32_t spins = 0;; ++spins) {
+            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= arrivals) break;
+            if (spins % 64 == 63 && __hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                ok = 0;
+                break;
+            }
+            if (spins >= kOSpinCap) {
+                __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        s_ok = ok;
+    }
+    __syncthreads();
+    return s_ok != 0;
+}
+
 }  // namespace vkml::attend

@@ -120,37 +120,6 @@ struct MergeOArgs {
     uint32_t* sync;
 };
 
-constexpr uint32_t kOSpinCap = 1u << 20;
-
-// Lane 0 polls counter copy wg % kCopies until every merging workgroup has
-// arrived; false if the wait gave up (the spin limit, or another
-// workgroup's error). The error flag is the sync words' own unless given. Called by every thread; ends with a workgroup barrier
-// (the weight loads issued before it stay in flight).
-__device__ bool await_merged(uint32_t* sync, uint32_t wg, uint32_t arrivals, uint32_t* error = nullptr) {
-    __shared__ uint32_t s_ok;
-    if (!error) error = OSync::error(sync);
-    if (threadIdx.x == 0) {
-        uint32_t ok = 1;
-        uint32_t* c = OSync::counter(sync, wg % OSync::kCopies);
-        for (uint32_t spins = 0;; ++spins) {
-            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= arrivals) break;
-            if (spins % 64 == 63 && __hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-                ok = 0;
-                break;
-            }
-            if (spins >= kOSpinCap) {
-                __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        s_ok = ok;
-    }
-    __syncthreads();
-    return s_ok != 0;
-}
-
 // Workgroups [0, merge_wgs): the merge (kThreads / hd heads each, thread
 // element d of head h), its Q8_0 output stored write-through; then the
 // arrival on every counter copy. The rest: the o GEMV (32
@@ -214,17 +183,6 @@ bool launch_merge_o(const MergeOArgs& m, const vkml::gemv::GemvArgs& g, uint32_t
 }
 
 // ------------------------------------------- chunks + merge + o, one launch
-
-// One block of the sync words of vkml_attend_step_fused: the OSync words
-// (the o GEMV's arrival counters), then an arrival counter per set of chunk
-// items (KV head, head group), kArriveStride words apart. The sticky error
-// flag of every block is word 0 of block 0.
-struct FusedSync {
-    static constexpr uint32_t kArriveStride = 8;
-    static constexpr uint32_t kMaxSets = 256;
-    static constexpr uint32_t kWords = OSync::kWords + kArriveStride * kMaxSets;
-    __device__ static uint32_t* arrive(uint32_t* s, uint32_t set) { return s + OSync::kWords + kArriveStride * set; }
-};
 
 struct FusedArgs {
     uint32_t attn_wgs;  // workgroups of the chunk pass (grid padding included), first in the grid
@@ -335,7 +293,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
 }
 
 template <int HD, bool F16, int HPW, int FMT, bool FULL, int DEEP = 0>
-bool launch_fused_as(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs) {
+bool launch_fused_as(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs, bool dry) {
     const void* fn = reinterpret_cast<const void*>(&k_attend_fused<HD, F16, HPW, FMT, FULL, DEEP>);
     constexpr uint32_t kHalves = kThreads / HD;
     const size_t merge_lds = (static_cast<size_t>(kHalves) * 2 * a.chunks + kHalves * (HD / kWave)) * 4;
@@ -349,31 +307,32 @@ bool launch_fused_as(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::G
     }
     // the waiting GEMV workgroups must leave slots for the chunk items
     if (static_cast<uint64_t>(per_cu) * vkml::abi::compute_units() <= gemv_wgs) return false;
+    if (dry) return true;
     hipLaunchKernelGGL((k_attend_fused<HD, F16, HPW, FMT, FULL, DEEP>), dim3(f.attn_wgs + gemv_wgs), dim3(kThreads), lds,
                        vkml::abi::stream(), a, f, g);
     return true;
 }
 
 template <int HD, bool F16, int HPW>
-bool launch_fused_hpw(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs, bool q4k) {
+bool launch_fused_hpw(const ChunkArgs& a, const FusedArgs& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs, bool q4k, bool dry) {
     const bool full = g.k % 2048 == 0;  // whole pairs of 2-round batches
     // o rows of 2048 or 4096 values: every round's weights in flight at once
     if (g.k == 4096)
-        return q4k ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true, 8>(a, f, g, gemv_wgs)
-                   : launch_fused_as<HD, F16, HPW, VKML_Q8_0, true, 8>(a, f, g, gemv_wgs);
+        return q4k ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true, 8>(a, f, g, gemv_wgs, dry)
+                   : launch_fused_as<HD, F16, HPW, VKML_Q8_0, true, 8>(a, f, g, gemv_wgs, dry);
     if (g.k == 2048)
-        return q4k ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true, 4>(a, f, g, gemv_wgs)
-                   : launch_fused_as<HD, F16, HPW, VKML_Q8_0, true, 4>(a, f, g, gemv_wgs);
+        return q4k ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true, 4>(a, f, g, gemv_wgs, dry)
+                   : launch_fused_as<HD, F16, HPW, VKML_Q8_0, true, 4>(a, f, g, gemv_wgs, dry);
     if (q4k)
-        return full ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true>(a, f, g, gemv_wgs)
-                    : launch_fused_as<HD, F16, HPW, VKML_Q4_K, false>(a, f, g, gemv_wgs);
-    return full ? launch_fused_as<HD, F16, HPW, VKML_Q8_0, true>(a, f, g, gemv_wgs)
-                : launch_fused_as<HD, F16, HPW, VKML_Q8_0, false>(a, f, g, gemv_wgs);
+        return full ? launch_fused_as<HD, F16, HPW, VKML_Q4_K, true>(a, f, g, gemv_wgs, dry)
+                    : launch_fused_as<HD, F16, HPW, VKML_Q4_K, false>(a, f, g, gemv_wgs, dry);
+    return full ? launch_fused_as<HD, F16, HPW, VKML_Q8_0, true>(a, f, g, gemv_wgs, dry)
+                : launch_fused_as<HD, F16, HPW, VKML_Q8_0, false>(a, f, g, gemv_wgs, dry);
 }
 
 // The one-launch form, if the shapes allow it; false otherwise (nothing launched).
 bool launch_fused(uint32_t head_dim, bool f16, const ChunkArgs& a, FusedArgs f, const vkml::gemv::GemvArgs& g, uint32_t b_type,
-                  uint32_t scale_type) {
+                  uint32_t scale_type, bool dry = false) {
     using namespace vkml::gemv;
     if (b_type != VKML_Q4_K && !(b_type == VKML_Q8_0 && scale_type == VKML_F16)) return false;
     const bool q4k = b_type == VKML_Q4_K;
@@ -388,8 +347,8 @@ bool launch_fused(uint32_t head_dim, bool f16, const ChunkArgs& a, FusedArgs f, 
     f.attn_wgs = pair_blocks * kXcds * (a.group / hpw);
     const uint32_t gemv_wgs = (g.n + kThreads / 32 - 1) / (kThreads / 32);
 #define VKML_FUSED(HD)                                                                                             \
-    (f16 ? (hpw == 2 ? launch_fused_hpw<HD, true, 2>(a, f, g, gemv_wgs, q4k) : launch_fused_hpw<HD, true, 1>(a, f, g, gemv_wgs, q4k)) \
-         : (hpw == 2 ? launch_fused_hpw<HD, false, 2>(a, f, g, gemv_wgs, q4k) : launch_fused_hpw<HD, false, 1>(a, f, g, gemv_wgs, q4k)))
+    (f16 ? (hpw == 2 ? launch_fused_hpw<HD, true, 2>(a, f, g, gemv_wgs, q4k, dry) : launch_fused_hpw<HD, true, 1>(a, f, g, gemv_wgs, q4k, dry)) \
+         : (hpw == 2 ? launch_fused_hpw<HD, false, 2>(a, f, g, gemv_wgs, q4k, dry) : launch_fused_hpw<HD, false, 1>(a, f, g, gemv_wgs, q4k, dry)))
     switch (head_dim) {
         case 64: return VKML_FUSED(64);
         case 128: return VKML_FUSED(128);
@@ -576,6 +535,17 @@ int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* qkv, c
     }
     if (int r = vkml_fill_u32(next + OSync::kLine, 0u, OSync::kWords - OSync::kLine)) return r;
     return vkml_gemv_dot_add(o, values, o_values, x, o_scales, scales, x);
+}
+
+int vkml_attend_step_fused_supported(const vkml_attend_step_params* p, const vkml_gemv_dot_params* o) {
+    if (!vkml::abi::initialized() || !p || !o || o->m != 1 || p->kv_heads == 0 || p->heads % p->kv_heads || p->chunks == 0 ||
+        p->chunks > kMergeMaxChunks || (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) ||
+        (p->kv_type != VKML_F16 && p->kv_type != VKML_F32))
+        return 0;
+    const ChunkArgs args = step_args(p, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+    const FusedArgs f{0, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    const vkml::gemv::GemvArgs g{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, o->n, o->k};
+    return launch_fused(p->head_dim, p->kv_type == VKML_F16, args, f, g, o->b_type, o->scale_type, true) ? 1 : 0;
 }
 
 int vkml_attend_fused_check(uint32_t* sync, uint32_t blocks) {

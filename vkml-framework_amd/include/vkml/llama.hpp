@@ -81,6 +81,18 @@ struct LlamaOptions {
     // The results do not depend on it (the reference's own 64 MiB chunks
     // decide which queries take gemv's order).
     std::int64_t prompt_score_bytes = std::int64_t{1} << 30;
+    // Decode attention on the matrix cores: f32 attention to within f32
+    // rounding, not the reference's order of f32 operations (so logits are
+    // no longer its bits). f16 caches, head_dim 64 or 128, no sliding
+    // window; other models keep the exact kernels. Off by default.
+    bool fast_attention = false;
+    // A sliding window over every layer and the attention / final logit
+    // soft caps (0: none). The reference takes these from Gemma files only
+    // (config.cpp:114-133) and ignores them in a llama file, as from_gguf
+    // does here; a llama model gets them from these options.
+    std::int64_t sliding_window = 0;
+    float attn_logit_softcap = 0.0f;
+    float final_logit_softcap = 0.0f;
 };
 
 class Llama {

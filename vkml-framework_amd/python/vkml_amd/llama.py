@@ -16,7 +16,9 @@ i32, i64, u32, u64, vp = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_void_
 
 class Options(C.Structure):
     _fields_ = [("kv_cache_f16", i32), ("quantize", i32), ("integer_dot", i32), ("use_graphs", i32),
-                ("device_name", C.c_char_p), ("prompt_score_bytes", i64), ("sliding_extra_rows", i64)]
+                ("device_name", C.c_char_p), ("prompt_score_bytes", i64), ("sliding_extra_rows", i64),
+                ("fast_attention", i32), ("sliding_window", i64), ("attn_logit_softcap", C.c_float),
+                ("final_logit_softcap", C.c_float)]
 
 
 class SamplingOptions(C.Structure):
@@ -94,7 +96,8 @@ def _ptr(a: np.ndarray):
 
 class Llama:
     def __init__(self, path: str, context: int, kv_f16: bool = False, quantize: int = -1, integer_dot: bool = True,
-                 use_graphs: bool = True, prompt_score_bytes: int = 0, sliding_extra_rows: int = -1):
+                 use_graphs: bool = True, prompt_score_bytes: int = 0, sliding_extra_rows: int = -1,
+                 fast_attention: bool = False, sliding_window: int = 0, attn_softcap: float = 0.0, final_softcap: float = 0.0):
         o = Options()
         lib().vkml_llama_default_options(C.byref(o))
         o.kv_cache_f16, o.quantize, o.integer_dot = int(kv_f16), int(quantize), int(integer_dot)
@@ -103,6 +106,9 @@ class Llama:
             o.prompt_score_bytes = int(prompt_score_bytes)
         if sliding_extra_rows >= 0:
             o.sliding_extra_rows = int(sliding_extra_rows)
+        o.fast_attention = int(fast_attention)
+        o.sliding_window = int(sliding_window)
+        o.attn_logit_softcap, o.final_logit_softcap = float(attn_softcap), float(final_softcap)
         self._h = vp()
         _check(lib().vkml_llama_load(path.encode(), int(context), C.byref(o), C.byref(self._h)))
         cfg = Config()

@@ -61,7 +61,7 @@ const char* vkml_llama_last_error(void) { return g_error.c_str(); }
 
 void vkml_llama_default_options(vkml_llama_options* out) {
     if (!out) return;
-    *out = vkml_llama_options{0, -1, 1, 1, nullptr, std::int64_t{1} << 30, 1024};
+    *out = vkml_llama_options{0, -1, 1, 1, nullptr, std::int64_t{1} << 30, 1024, 0, 0, 0.0f, 0.0f};
 }
 
 int vkml_llama_load(const char* path, int64_t context_length, const vkml_llama_options* options, vkml_llama** out) {
@@ -81,6 +81,10 @@ int vkml_llama_load(const char* path, int64_t context_length, const vkml_llama_o
         if (o.prompt_score_bytes <= 0) throw vkml::Error("vkml_llama_load: prompt_score_bytes must be positive");
         lo.prompt_score_bytes = o.prompt_score_bytes;
         lo.sliding_extra_rows = o.sliding_extra_rows;
+        lo.fast_attention = o.fast_attention != 0;
+        lo.sliding_window = o.sliding_window;
+        lo.attn_logit_softcap = o.attn_logit_softcap;
+        lo.final_logit_softcap = o.final_logit_softcap;
         vkml::Context& ctx = context(o);
         *out = new vkml_llama{vkml::Llama::load(ctx, path, context_length, lo)};
         ++g_models;

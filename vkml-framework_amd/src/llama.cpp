@@ -277,13 +277,9 @@ LlamaConfig LlamaConfig::from_gguf(const std::filesystem::path& path) {
     c.max_positions = need("context_length");
     c.rms_norm_eps = static_cast<float>(file.number(key("attention.layer_norm_rms_epsilon"), c.rms_norm_eps));
     c.rope_theta = static_cast<float>(file.number(key("rope.freq_base"), c.rope_theta));
-    // A sliding window over every layer, and soft caps: the keys the
-    // reference reads for the Gemma architectures (config.cpp:124-131),
-    // here for llama files that carry them (Mistral's window).
-    if (file.has(key("attention.sliding_window")))
-        c.sliding_window = static_cast<std::int64_t>(file.number(key("attention.sliding_window"), 0));
-    c.attn_logit_softcap = static_cast<float>(file.number(key("attn_logit_softcapping"), 0.0));
-    c.final_logit_softcap = static_cast<float>(file.number(key("final_logit_softcapping"), 0.0));
+    // A llama file's attention.sliding_window and soft-capping keys are
+    // ignored, as the reference ignores them (it reads them for Gemma only,
+    // config.cpp:114-133): LlamaOptions sets a window or soft caps.
     if (!file.contains("token_embd.weight")) throw Error(where + " has no token_embd.weight");
     c.vocab_size = file.shape("token_embd.weight").at(0);
     c.tie_word_embeddings = !file.contains("output.weight");
@@ -319,6 +315,10 @@ struct Llama::Impl {
         std::int64_t window = 0;
         // Decode attention's 128-key chunks: over the window, or the cache.
         std::int64_t chunks() const { return ((slides ? window : rows) + 127) / 128; }
+        // The decode step's attention: in one launch with the o GEMV
+        // (vkml_attend_step_fused's, or with fast, vkml_attend_step_fast's),
+        // as decided at load for every chunk count up to chunks().
+        bool one_launch = false, fast = false;
     };
     // With a sliding window: the window (at most the rings' rows), the
     // rings' rows, and the first position they still hold (llama.cpp:
@@ -480,7 +480,15 @@ struct Llama::Impl {
                                              c.rope_style == RopeStyle::Interleaved ? 0u : 1u, 1,
                                              1.0f / std::sqrt(static_cast<float>(hd)), c.attn_logit_softcap, u32(L.window),
                                              prepared ? 1u : 0u, u32(ready)};
-            if (merge_o && fsync) {
+            if (merge_o && fsync && L.fast) {
+                // ... on the matrix cores (the fast_attention option)
+                const vkml_gemv_dot_params op{1, u32(L.o.rows), u32(L.o.cols), L.o.type_code(), L.o.scale_code()};
+                check(vkml_attend_step_fast(&sp, static_cast<const float*>(qkv.data()), L.k_cache.data(), L.v_cache.data(),
+                                            static_cast<float*>(partial.data()), static_cast<float*>(stats.data()),
+                                            static_cast<float*>(attn.data()), aq.data(), static_cast<float*>(as.data()), st, &op,
+                                            L.o.values(), L.o.scales(), xp, fsync, u32(li), blocks),
+                      "attention");
+            } else if (merge_o && fsync) {
                 // ... and the merge and the o projection + residual too (block
                 // li of the fused sync words, whose next block it zeroes)
                 const vkml_gemv_dot_params op{1, u32(L.o.rows), u32(L.o.cols), L.o.type_code(), L.o.scale_code()};
@@ -773,6 +781,12 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
     Impl& m = *impl;
     m.context = &context;
     m.config = LlamaConfig::from_gguf(path);
+    if (options.sliding_window < 0 || options.attn_logit_softcap < 0.0f || options.final_logit_softcap < 0.0f) {
+        throw Error("Llama: sliding_window and the logit soft caps must not be negative (0: none)");
+    }
+    if (options.sliding_window > 0) m.config.sliding_window = options.sliding_window;
+    m.config.attn_logit_softcap = options.attn_logit_softcap;
+    m.config.final_logit_softcap = options.final_logit_softcap;
     validated(m.config, context_length);
     m.context_length = context_length;
     m.options = options;
@@ -880,11 +894,27 @@ Llama Llama::load(Context& context, const std::filesystem::path& path, std::int6
     // when every layer can take it: layer L uses block L and clears block L + 1.
     if (m.layers.size() >= 2 && std::all_of(m.layers.begin(), m.layers.end(), [&](const auto& L) { return m.quantized_input(L.o); }))
         m.fused_sync = Tensor::zeros(context, {static_cast<std::int64_t>(vkml_attend_fused_sync_bytes(u32(m.layers.size())) / 4)}, DType::I32);
-    // Launches sized by position need the one launch on every layer (o
-    // weights q4_K, or q8_0 with f16 scales).
-    m.tiered = m.fused_sync.numel() && std::all_of(m.layers.begin(), m.layers.end(), [](const auto& L) {
-        return L.o.type_code() == VKML_Q4_K || (L.o.type_code() == VKML_Q8_0 && L.o.scale_code() == VKML_F16);
-    });
+    // Which layers take the one launch: the library's own plan for the
+    // shapes (the o format, LDS, occupancy, the merge's sets) at the
+    // layer's largest chunk count, the one a step may launch. Launches sized
+    // by position need it on every layer (the separate launches need
+    // chunks covering the cache).
+    if (m.fused_sync.numel()) {
+        const bool fold = d % 32 == 0 && d <= 4096;
+        for (auto& L : m.layers) {
+            const bool prepared = fold && c.rope_style == RopeStyle::Interleaved &&
+                                  std::all_of(L.qkv.begin(), L.qkv.end(), [&](const auto& wr) { return m.quantized_input(wr.first); });
+            const vkml_attend_step_params sp{u32(c.num_heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), 0, 0,
+                                             detail::type_code(L.k_cache.dtype()), u32(L.chunks()), 0, 1,
+                                             1.0f / std::sqrt(static_cast<float>(hd)), c.attn_logit_softcap, u32(L.window),
+                                             prepared ? 1u : 0u, 0};
+            const vkml_gemv_dot_params op{1, u32(L.o.rows), u32(L.o.cols), L.o.type_code(), L.o.scale_code()};
+            const bool o_ok = m.int_dot && L.o.int_dot_ok();
+            L.fast = o_ok && options.fast_attention && vkml_attend_step_fast_supported(&sp, &op) == 1;
+            L.one_launch = L.fast || (o_ok && vkml_attend_step_fused_supported(&sp, &op) == 1);
+        }
+    }
+    m.tiered = m.fused_sync.numel() && std::all_of(m.layers.begin(), m.layers.end(), [](const auto& L) { return L.one_launch; });
     m.log = Tensor::zeros(context, {context_length}, DType::I32);
     m.chunks = (context_length + 127) / 128;
     m.partial = f32(c.num_heads * m.chunks * hd);

@@ -119,13 +119,35 @@ int vkml_sampler_sample(vkml_sampler* sampler, const float* logits, int64_t voca
  * (ChatModel::generate): each prompt reuses the cache of its longest common
  * prefix with the last; the reply (without the stop token) goes to
  * reply[capacity], its length to *reply_len, and *finish is 0 for a stop
- * token, 1 for max_tokens (negative: none) or the context's end. The model
- * must outlive the session; one thread at a time. */
+ * token, 1 for max_tokens (negative: none), capacity or the context's end:
+ * the reply stops at capacity tokens, so it always fits. The model must
+ * outlive the session; one thread at a time. */
 typedef struct vkml_session vkml_session;
 int vkml_session_create(vkml_llama* model, const int32_t* stop, int64_t n_stop, vkml_session** out);
 void vkml_session_free(vkml_session* session);
 int vkml_session_generate(vkml_session* session, const int32_t* prompt, int64_t n_prompt, vkml_sampler* sampler,
                           int64_t max_tokens, int32_t* reply, int64_t capacity, int64_t* reply_len, int32_t* finish);
+/* vkml_session_generate with each reply token's log probability under the
+ * model's logits (before any sampling setting) in logprobs[i] and its top
+ * likeliest tokens and theirs in top_ids / top_logprobs[i * top + j]
+ * (ChatModel::generate with logprobs, apps/generation.hpp:139-142,176-190
+ * there; -1 / NaN past a row's alternatives). Any of the three may be NULL;
+ * every step's logits are read back when one is not. */
+int vkml_session_generate_logprobs(vkml_session* session, const int32_t* prompt, int64_t n_prompt, vkml_sampler* sampler,
+                                   int64_t max_tokens, int32_t top, int32_t* reply, int64_t capacity, int64_t* reply_len,
+                                   int32_t* finish, float* logprobs, int32_t* top_ids, float* top_logprobs);
+/* ChatModel::score (apps/generation.hpp:104-131 there): each prompt token's
+ * log probability given the ones before (logprobs[0] is NaN) and the top
+ * alternatives at its position (top_ids / top_logprobs [n_prompt * top]),
+ * from forward_all; the model starts over and ends holding the prompt. */
+int vkml_session_score(vkml_session* session, const int32_t* prompt, int64_t n_prompt, int32_t top, float* logprobs,
+                       int32_t* top_ids, float* top_logprobs);
+/* token_logprobs (include/vkml/sampling.hpp there): token's log-softmax
+ * probability under logits[vocab] and the top likeliest tokens with theirs.
+ * Host code, no device needed. */
+int vkml_token_logprobs(const float* logits, int64_t vocab, int32_t token, int32_t top, float* logprob, int32_t* top_ids,
+                        float* top_logprobs);
+
 /* The tokens the cache holds: writes up to capacity, returns how many. */
 int64_t vkml_session_cached(const vkml_session* session, int32_t* out, int64_t capacity);
 

@@ -74,6 +74,7 @@ def _declare(L):
         "orc_attention_sliding": (None, [vp, i64, i64, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, f32, vp]),
         "orc_model_load_ex": (vp, [C.c_char_p, i64, i32, i32, i64]),
         "orc_model_load_opts": (vp, [C.c_char_p, i64, i32, i32, i64, i64, f32, f32]),
+        "orc_token_logprobs": (f32, [vp, i64, i32, i32, vp, vp]),
         "orc_model_ring": (i64, [vp]),
         "orc_model_load": (vp, [C.c_char_p, i64, i32, i32]),
         "orc_model_free": (None, [vp]),
@@ -412,6 +413,16 @@ def reference_f64(gguf_path: str, tokens) -> np.ndarray:
     if lib().orc_model_reference_f64(gguf_path.encode(), _p(t), t.size, _p(out)) != 0:
         raise RuntimeError(last_error())
     return out
+
+
+def token_logprobs(logits, token: int, top: int):
+    """(logprob, top ids, top logprobs) of the reference's token_logprobs."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    ti = np.zeros(max(top, 1), np.int32)
+    tl = np.zeros(max(top, 1), np.float32)
+    lp = lib().orc_token_logprobs(_p(lg), lg.size, int(token), int(top), _p(ti), _p(tl))
+    k = min(top, lg.size)
+    return float(lp), ti[:k].copy(), tl[:k].copy()
 
 
 class Sampler:

@@ -185,3 +185,27 @@ int32_t orc_sampler_sample(orc_sampler* s, const float* given, int64_t n, const 
     }
     return id;
 }
+
+/* token_logprobs (src/io/sampling.cpp:141-164): token's log-softmax
+ * probability, max + log(sum exp(l - max)) in double over the logits in
+ * order, each result rounded to float; and the top most likely tokens with
+ * theirs (equal logits by ascending id). */
+float orc_token_logprobs(const float* logits, int64_t n, int32_t token, int top, int32_t* top_ids, float* top_logprobs) {
+    double max = logits[0];
+    for (int64_t i = 1; i < n; ++i) if (logits[i] > max) max = logits[i];
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; ++i) sum += exp((double)logits[i] - max);
+    const double log_total = max + log(sum);
+    if (top > 0) {
+        int32_t* order = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+        for (int64_t i = 0; i < n; ++i) order[i] = (int32_t)i;
+        g_sort_logits = logits;
+        qsort(order, (size_t)n, sizeof(int32_t), by_logit);
+        for (int j = 0; j < top && j < n; ++j) {
+            top_ids[j] = order[j];
+            top_logprobs[j] = (float)((double)logits[order[j]] - log_total);
+        }
+        free(order);
+    }
+    return (float)((double)logits[token] - log_total);
+}

@@ -180,6 +180,8 @@ orc_sampler* orc_sampler_new(float temperature, int top_k, float top_p, uint64_t
 void orc_sampler_free(orc_sampler* s);
 int32_t orc_sampler_sample(orc_sampler* s, const float* logits, int64_t n, const int32_t* previous,
                            int64_t n_previous);
+/* token_logprobs (src/io/sampling.cpp:141-164); writes min(top, n) entries. */
+float orc_token_logprobs(const float* logits, int64_t n, int32_t token, int top, int32_t* top_ids, float* top_logprobs);
 /* The generator alone, for its pins: the next 64-bit output, and a
  * uniform_real_distribution<double>(0, total) draw. */
 uint64_t orc_sampler_draw_u64(orc_sampler* s);

@@ -124,3 +124,65 @@ def test_a_second_request_reuses_the_common_prefix(path, greedy):
     _, _, cached = oracle_reply(ref, [], p1, O.Sampler(**opts), 9, [])
     want, _, wcached = oracle_reply(ref, cached, p2, O.Sampler(**opts), 9, [])
     assert list(r2) == want and list(session.cached) == wcached
+
+
+def oracle_reply_logprobs(model, prompt, sampler, max_tokens, top):
+    """oracle_reply from an empty cache, with each reply token's
+    token_logprobs under the step's logits (generate with logprobs,
+    apps/generation.hpp:176-190)."""
+    model.rewind(0)
+    logits = model.forward(np.array(prompt, np.int32))
+    cached, reply, rows = list(prompt), [], []
+    while len(reply) < max_tokens and model.position < model.context:
+        nxt = sampler.sample(logits, cached)
+        reply.append(nxt)
+        rows.append(O.token_logprobs(logits, nxt, top))
+        logits = model.forward(np.array([nxt], np.int32))
+        cached.append(nxt)
+    return reply, rows
+
+
+@pytest.mark.parametrize("opts", [dict(), dict(temperature=0.8, top_k=40, seed=5)])
+def test_reply_logprobs_match_the_oracle(path, opts):
+    """Each reply token's log probability and top alternatives, from the
+    model's own logits (before sampling settings), bit for bit as the
+    oracle's model and token_logprobs give them; a greedy sampler reads the
+    logits back and still replies as on the device."""
+    ctx, top, n = 64, 5, 12
+    prompt = list(np.random.default_rng(6).integers(0, 1000, 10))
+    gpu = L.Llama(path, ctx, kv_f16=True)
+    session = L.Session(gpu)
+    reply, finish, lp, ids, lps = session.generate_logprobs(prompt, L.Sampler(**opts), n, top)
+    ref = O.Model(path, ctx, kv_f16=True)
+    want, rows = oracle_reply_logprobs(ref, prompt, O.Sampler(**opts), n, top)
+    assert list(reply) == want and finish == LENGTH
+    for i, (wl, wi, wls) in enumerate(rows):
+        assert np.float32(lp[i]).view(np.uint32) == np.float32(wl).view(np.uint32), i
+        assert list(ids[i]) == list(wi) and np.array_equal(lps[i].view(np.uint32), wls.view(np.uint32)), i
+    if not opts:
+        plain, _ = L.Session(L.Llama(path, ctx, kv_f16=True)).generate(prompt, L.Sampler(), n)
+        assert list(plain) == list(reply)
+
+
+@pytest.mark.parametrize("length", [1, 9, 37])
+def test_score_matches_the_oracle(path, length):
+    """Session.score (ChatModel::score, apps/generation.hpp:104-131): each
+    prompt token's log probability given the ones before from forward_all's
+    rows, NaN for the first; the session then holds the prompt and a
+    request extending it runs only the new tokens."""
+    ctx, top = 64, 3
+    prompt = list(np.random.default_rng(length).integers(0, 1000, length))
+    gpu = L.Llama(path, ctx, kv_f16=True)
+    session = L.Session(gpu)
+    session.generate(list(np.random.default_rng(99).integers(0, 1000, 5)), L.Sampler(), 3)  # something cached first
+    lp, ids, lps = session.score(prompt, top)
+    assert np.isnan(lp[0]) and np.all(ids[0] == -1) and np.all(np.isnan(lps[0]))
+    assert list(session.cached) == prompt and gpu.position == length
+    ref = O.Model(path, ctx, kv_f16=True)
+    rows = ref.forward_all(np.array(prompt, np.int32))
+    for i in range(1, length):
+        wl, wi, wls = O.token_logprobs(rows[i - 1], prompt[i], top)
+        assert np.float32(lp[i]).view(np.uint32) == np.float32(wl).view(np.uint32), i
+        assert list(ids[i]) == list(wi) and np.array_equal(lps[i].view(np.uint32), wls.view(np.uint32)), i
+    reply, _ = session.generate(prompt + [5], L.Sampler(), 4)
+    assert list(session.cached) == prompt + [5] + list(reply) and gpu.position == length + 1 + len(reply)

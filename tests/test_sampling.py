@@ -90,6 +90,11 @@ OPTIONS = [
     dict(temperature=0.9, top_p=0.95, frequency_penalty=0.7, presence_penalty=-0.4),
     dict(temperature=2.0, min_p=0.2, repetition_penalty=0.8, presence_penalty=1.5),
     dict(temperature=0.7, top_k=1000, top_p=0.8),
+    dict(temperature=1.0, min_p=0.01),
+    dict(temperature=0.6, top_k=200000),
+    dict(temperature=1.1, top_p=1e-6),
+    dict(temperature=0.9, top_k=30, min_p=0.1),
+    dict(temperature=3.0),
 ]
 
 
@@ -121,3 +126,42 @@ def test_options_are_checked():
             L.Sampler(**kw)
     with pytest.raises(L.VkmlError, match="empty"):
         L.Sampler(temperature=1.0).sample(np.zeros(0, np.float32))
+
+
+def test_oracle_logprobs_are_the_log_softmax():
+    """The oracle's token_logprobs (the reference's, sampling.cpp:141-164)
+    against float64 log-softmax (scipy), and exact on equal logits."""
+    from scipy.special import log_softmax
+    rng = np.random.default_rng(4)
+    for vocab in (7, 1000, 32768):
+        logits = (rng.standard_normal(vocab) * 4).astype(np.float32)
+        want = log_softmax(logits.astype(np.float64))
+        tok = int(rng.integers(0, vocab))
+        lp, ids, lps = O.token_logprobs(logits, tok, 5)
+        assert abs(lp - want[tok]) <= 1e-6 * (1 + abs(want[tok]))
+        order = np.lexsort((np.arange(vocab), -logits))[:5]
+        assert list(ids) == list(order)
+        assert np.allclose(lps, want[order], rtol=1e-6, atol=1e-6)
+    flat = np.zeros(10, np.float32)
+    lp, ids, lps = O.token_logprobs(flat, 3, 4)
+    assert lp == np.float32(-np.log(10.0)) and list(ids) == [0, 1, 2, 3]
+
+
+@pytest.mark.parametrize("vocab", [3, 4096, 128256])
+def test_product_logprobs_equal_the_oracles(vocab):
+    rng = np.random.default_rng(vocab)
+    for rep in range(5):
+        logits = (rng.standard_normal(vocab) * 5).astype(np.float32)
+        if rep == 2:
+            logits[: min(vocab, 9)] = logits.max()  # ties at the top: by ascending id
+        tok = int(rng.integers(0, vocab))
+        top = min(8, vocab + 2)
+        got = L.token_logprobs(logits, tok, top)
+        want = O.token_logprobs(logits, tok, top)
+        assert np.float32(got[0]).view(np.uint32) == np.float32(want[0]).view(np.uint32)
+        k = min(top, vocab)
+        assert list(got[1][:k]) == list(want[1])
+        assert np.array_equal(got[2][:k].view(np.uint32), want[2].view(np.uint32))
+        assert all(i == -1 for i in got[1][k:]) and np.all(np.isnan(got[2][k:]))
+    with pytest.raises(L.VkmlError, match="outside the logits"):
+        L.token_logprobs(np.zeros(4, np.float32), 4, 1)

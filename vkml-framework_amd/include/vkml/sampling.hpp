@@ -50,14 +50,17 @@ public:
 
 private:
     std::int32_t pick(std::span<const float> logits);
+    // Counts a picked token for the frequency and presence penalties.
+    std::int32_t remember(std::int32_t id);
 
     SamplingOptions options_;
     std::mt19937_64 rng_;
     std::unordered_map<std::int32_t, int> picked_;  // times each token was picked, for the penalties
 };
 
-// A token's log probability under logits (their log-softmax), and the `top`
-// most likely tokens with theirs, most likely first (reference:
+// A token's log probability under logits (their log-softmax, computed in
+// double and rounded to float), and the `top` most likely tokens with
+// theirs, most likely first, equal logits by ascending id (reference:
 // src/io/sampling.cpp:141-164).
 struct TokenLogprobs {
     float logprob = 0.0f;

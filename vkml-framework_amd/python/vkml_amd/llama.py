@@ -61,6 +61,9 @@ SIGNATURES = {
     "vkml_session_free": (None, [vp]),
     "vkml_session_generate": (C.c_int, [vp, vp, i64, vp, i64, vp, i64, vp, vp]),
     "vkml_session_cached": (i64, [vp, vp, i64]),
+    "vkml_session_generate_logprobs": (C.c_int, [vp, vp, i64, vp, i64, i32, vp, i64, vp, vp, vp, vp, vp]),
+    "vkml_session_score": (C.c_int, [vp, vp, i64, i32, vp, vp, vp]),
+    "vkml_token_logprobs": (C.c_int, [vp, i64, i32, i32, vp, vp, vp]),
 }
 
 _lib = None
@@ -241,6 +244,16 @@ class Sampler:
             pass
 
 
+def token_logprobs(logits, token: int, top: int):
+    """vkml::token_logprobs (host code): (logprob, top ids, top logprobs)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    lp = np.empty(1, np.float32)
+    ti = np.empty(max(top, 1), np.int32)
+    tl = np.empty(max(top, 1), np.float32)
+    _check(lib().vkml_token_logprobs(_ptr(lg), lg.size, int(token), int(top), _ptr(lp), _ptr(ti), _ptr(tl)))
+    return float(lp[0]), ti[:top].copy(), tl[:top].copy()
+
+
 class Session:
     """vkml::Session: requests against one model, reusing its KV cache."""
 
@@ -261,6 +274,29 @@ class Session:
         _check(lib().vkml_session_generate(self._h, _ptr(p), p.size, sampler._h, int(max_tokens), _ptr(out), cap,
                                            C.byref(n), C.byref(fin)))
         return out[:n.value].copy(), int(fin.value)
+
+    def generate_logprobs(self, prompt, sampler: Sampler, max_tokens: int, top: int):
+        """(reply tokens, finish, logprobs [n], top ids [n, top], top logprobs [n, top])."""
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        cap = max(max_tokens, 0) if max_tokens >= 0 else self.model.context_length
+        out = np.empty(max(cap, 1), np.int32)
+        lp = np.empty(max(cap, 1), np.float32)
+        ti = np.empty((max(cap, 1), max(top, 1)), np.int32)
+        tl = np.empty((max(cap, 1), max(top, 1)), np.float32)
+        n, fin = i64(), i32()
+        _check(lib().vkml_session_generate_logprobs(self._h, _ptr(p), p.size, sampler._h, int(max_tokens), int(top), _ptr(out),
+                                                    cap, C.byref(n), C.byref(fin), _ptr(lp), _ptr(ti), _ptr(tl)))
+        k = n.value
+        return out[:k].copy(), int(fin.value), lp[:k].copy(), ti[:k, :top].copy(), tl[:k, :top].copy()
+
+    def score(self, prompt, top: int):
+        """(logprobs [n] (NaN first), top ids [n, top], top logprobs [n, top])."""
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        lp = np.empty(p.size, np.float32)
+        ti = np.empty((p.size, max(top, 1)), np.int32)
+        tl = np.empty((p.size, max(top, 1)), np.float32)
+        _check(lib().vkml_session_score(self._h, _ptr(p), p.size, int(top), _ptr(lp), _ptr(ti), _ptr(tl)))
+        return lp, ti[:, :top].copy(), tl[:, :top].copy()
 
     @property
     def cached(self) -> np.ndarray:

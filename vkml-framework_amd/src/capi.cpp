@@ -1,5 +1,6 @@
 // capi.cpp -- the C entry points of include/vkml_llama.h over vkml::Llama.
 #include <cstring>
+#include <limits>
 #include <memory>
 #include <string>
 
@@ -51,6 +52,21 @@ vkml_llama_config c_config(const vkml::LlamaConfig& c) {
     return vkml_llama_config{c.vocab_size, c.hidden_size, c.intermediate_size, c.num_layers, c.num_heads, c.num_kv_heads, c.head_dim,
                              c.max_positions, c.rms_norm_eps, c.rope_theta, c.tie_word_embeddings ? 1 : 0,
                              c.rope_style == vkml::RopeStyle::Interleaved ? 1 : 0};
+}
+
+// Copies rows of TokenLogprobs out: logprob[i], and top_ids / top_logprobs
+// [i * top + j] (-1 and NaN past a row's alternatives).
+void copy_logprobs(const std::vector<vkml::TokenLogprobs>& rows, int32_t top, float* logprobs, int32_t* top_ids, float* top_logprobs) {
+    for (std::size_t i = 0; i < rows.size(); ++i) {
+        if (logprobs) logprobs[i] = rows[i].logprob;
+        for (int32_t j = 0; j < top; ++j) {
+            const bool has = std::size_t(j) < rows[i].top.size();
+            if (top_ids) top_ids[i * std::size_t(top) + std::size_t(j)] = has ? rows[i].top[std::size_t(j)].first : -1;
+            if (top_logprobs)
+                top_logprobs[i * std::size_t(top) + std::size_t(j)] =
+                    has ? rows[i].top[std::size_t(j)].second : std::numeric_limits<float>::quiet_NaN();
+        }
+    }
 }
 
 }  // namespace
@@ -216,19 +232,45 @@ int vkml_session_create(vkml_llama* m, const int32_t* stop, int64_t n_stop, vkml
 
 void vkml_session_free(vkml_session* s) { delete s; }
 
+
 int vkml_session_generate(vkml_session* s, const int32_t* prompt, int64_t n_prompt, vkml_sampler* sampler, int64_t max_tokens,
                           int32_t* reply, int64_t capacity, int64_t* reply_len, int32_t* finish) {
+    return vkml_session_generate_logprobs(s, prompt, n_prompt, sampler, max_tokens, 0, reply, capacity, reply_len, finish, nullptr,
+                                          nullptr, nullptr);
+}
+
+int vkml_session_generate_logprobs(vkml_session* s, const int32_t* prompt, int64_t n_prompt, vkml_sampler* sampler,
+                                   int64_t max_tokens, int32_t top, int32_t* reply, int64_t capacity, int64_t* reply_len,
+                                   int32_t* finish, float* logprobs, int32_t* top_ids, float* top_logprobs) {
     return guarded([&] {
-        if (!s || !prompt || n_prompt <= 0 || !sampler || (!reply && capacity) || !reply_len)
-            throw vkml::Error("vkml_session_generate: null argument or empty prompt");
+        if (!s || !prompt || n_prompt <= 0 || !sampler || capacity < 0 || (!reply && capacity) || !reply_len || top < 0)
+            throw vkml::Error("vkml_session_generate: null or negative argument, or an empty prompt");
+        // The reply never outgrows the caller's buffer: at most capacity tokens.
+        const std::int64_t limit = max_tokens < 0 ? capacity : std::min(max_tokens, capacity);
+        const bool want = logprobs || top_ids || top_logprobs;
         std::vector<std::int32_t> out;
-        const auto f = s->session.generate({prompt, std::size_t(n_prompt)}, sampler->sampler, max_tokens, out);
-        if (std::int64_t(out.size()) > capacity)
-            throw vkml::Error("vkml_session_generate: a reply of " + std::to_string(out.size()) + " tokens exceeds the capacity of " +
-                              std::to_string(capacity));
+        std::vector<vkml::TokenLogprobs> lp;
+        const auto f = s->session.generate({prompt, std::size_t(n_prompt)}, sampler->sampler, limit, out, want ? &lp : nullptr, top);
         std::copy(out.begin(), out.end(), reply);
         *reply_len = std::int64_t(out.size());
         if (finish) *finish = f == vkml::Session::Finish::stop ? 0 : 1;
+        if (want) copy_logprobs(lp, top, logprobs, top_ids, top_logprobs);
+    });
+}
+
+int vkml_session_score(vkml_session* s, const int32_t* prompt, int64_t n_prompt, int32_t top, float* logprobs, int32_t* top_ids,
+                       float* top_logprobs) {
+    return guarded([&] {
+        if (!s || !prompt || n_prompt <= 0 || top < 0) throw vkml::Error("vkml_session_score: null or negative argument, or an empty prompt");
+        copy_logprobs(s->session.score({prompt, std::size_t(n_prompt)}, top), top, logprobs, top_ids, top_logprobs);
+    });
+}
+
+int vkml_token_logprobs(const float* logits, int64_t vocab, int32_t token, int32_t top, float* logprob, int32_t* top_ids,
+                        float* top_logprobs) {
+    return guarded([&] {
+        if (!logits || vocab <= 0 || top < 0) throw vkml::Error("vkml_token_logprobs: null or empty logits, or a negative top");
+        copy_logprobs({vkml::token_logprobs({logits, std::size_t(vocab)}, token, top)}, top, logprob, top_ids, top_logprobs);
     });
 }
 

@@ -3,6 +3,8 @@
 #include "vkml/generation.hpp"
 
 #include <algorithm>
+#include <limits>
+#include <string>
 
 #include "vkml/error.hpp"
 #include "vkml/ops.hpp"
@@ -21,7 +23,7 @@ Session::Session(Llama& model, std::vector<std::int32_t> stop) : model_(&model),
 bool Session::is_stop(std::int32_t id) const { return std::find(stop_.begin(), stop_.end(), id) != stop_.end(); }
 
 Session::Finish Session::generate(std::span<const std::int32_t> prompt, Sampler& sampler, std::int64_t max_tokens,
-                                  std::vector<std::int32_t>& reply) {
+                                  std::vector<std::int32_t>& reply, std::vector<TokenLogprobs>* logprobs, int top) {
     if (prompt.empty()) throw Error("Session::generate: the prompt is empty");
     // Only the tokens after the part the cache already holds run; at least
     // one, for the logits. The model may start over instead (a sliding
@@ -32,20 +34,24 @@ Session::Finish Session::generate(std::span<const std::int32_t> prompt, Sampler&
     common = std::size_t(model_->rewind(std::int64_t(common)));
     cached_.assign(prompt.begin(), prompt.end());
     try {
-        return decode(model_->forward(prompt.subspan(common)), sampler, max_tokens, reply);
+        return decode(model_->forward(prompt.subspan(common)), sampler, max_tokens, reply, logprobs, top);
     } catch (...) {
         cached_.clear();  // what the cache holds is unknown: start over next time
         throw;
     }
 }
 
-Session::Finish Session::decode(Tensor logits, Sampler& sampler, std::int64_t max_tokens, std::vector<std::int32_t>& reply) {
+Session::Finish Session::decode(Tensor logits, Sampler& sampler, std::int64_t max_tokens, std::vector<std::int32_t>& reply,
+                                std::vector<TokenLogprobs>* logprobs, int top) {
     reply.clear();
+    if (logprobs) logprobs->clear();
     Llama& m = *model_;
-    const bool greedy = sampler.greedy();
+    // Greedy steps stay on the device unless the logits are wanted anyway.
+    const bool greedy = sampler.greedy() && !logprobs;
+    std::vector<float> host;
     const auto pick = [&](const Tensor& l) {
         if (greedy) return argmax(l).to_vector<std::int32_t>()[0];
-        const std::vector<float> host = l.to_vector<float>();
+        host = l.to_vector<float>();
         return sampler.sample(host, cached_);
     };
     std::int32_t next = pick(logits);
@@ -56,6 +62,7 @@ Session::Finish Session::decode(Tensor logits, Sampler& sampler, std::int64_t ma
         if (m.position() >= m.context_length()) return Finish::length;
         if (is_stop(next)) return Finish::stop;
         reply.push_back(next);
+        if (logprobs) logprobs->push_back(token_logprobs(host, next, top));
         if (!greedy) {
             logits = m.forward({&next, 1});
             cached_.push_back(next);
@@ -81,6 +88,31 @@ Session::Finish Session::decode(Tensor logits, Sampler& sampler, std::int64_t ma
         }
         next = picks.back();
     }
+}
+
+std::vector<TokenLogprobs> Session::score(std::span<const std::int32_t> prompt, int top) {
+    if (prompt.empty()) throw Error("Session::score: the prompt is empty");
+    Llama& m = *model_;
+    if (std::int64_t(prompt.size()) > m.context_length()) {
+        throw Error("Session::score: a prompt of " + std::to_string(prompt.size()) + " tokens exceeds the context length of " +
+                    std::to_string(m.context_length()));
+    }
+    m.reset();
+    cached_.clear();
+    std::vector<TokenLogprobs> out;
+    out.reserve(prompt.size());
+    out.push_back(TokenLogprobs{std::numeric_limits<float>::quiet_NaN(), {}});
+    // Row r of a piece's logits scores the token after it.
+    const std::size_t vocab = std::size_t(m.config().vocab_size);
+    const std::size_t rows = std::max<std::size_t>(1, (std::size_t{128} << 20) / (4 * vocab));
+    for (std::size_t begin = 0; begin < prompt.size(); begin += rows) {
+        const std::size_t n = std::min(rows, prompt.size() - begin);
+        const std::vector<float> logits = m.forward_all(prompt.subspan(begin, n)).to_vector<float>();
+        for (std::size_t r = 0; r < n && begin + r + 1 < prompt.size(); ++r)
+            out.push_back(token_logprobs({logits.data() + r * vocab, vocab}, prompt[begin + r + 1], top));
+    }
+    cached_.assign(prompt.begin(), prompt.end());
+    return out;
 }
 
 }  // namespace vkml

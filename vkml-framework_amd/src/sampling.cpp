@@ -1,12 +1,24 @@
-// sampling.cpp -- the host-side token sampler (the reference's
-// src/io/sampling.cpp:17-164). The logits of a sampled step are read back
-// from the device (the greedy case never needs them: the device argmax
-// does); the picking is a few hundred microseconds of host work per token.
+// sampling.cpp -- picking the next token from a step's logits on the host,
+// with the semantics of the reference's Sampler (src/io/sampling.cpp:17-139)
+// and its log probabilities (:141-164).
+//
+// Design. Candidates leave a binary max-heap over token ids one at a time,
+// in the order (larger logit first, then smaller id) -- a total order, so no
+// result depends on how ties are sorted. Building the heap is linear, and a
+// request then orders only as many tokens as its cuts look at: top_k, the
+// fewest whose mass reaches top_p, those within min_p of the first, or, with
+// no cut, as many as the draw walks past. Which token comes out is fixed by
+// the arithmetic, which is the reference's: a candidate's weight
+// exp((l - max) / T) in double; the softmax's denominator summed in token
+// order when no top_k applies, else (and after any cut) over the kept
+// candidates in their order; one std::uniform_real_distribution<double>
+// (0, total) draw from std::mt19937_64; then the kept weights subtracted in
+// order until the draw drops below zero (the last kept one if rounding
+// leaves it at or above zero).
 #include "vkml/sampling.hpp"
 
 #include <algorithm>
 #include <cmath>
-#include <numeric>
 #include <string>
 #include <unordered_set>
 
@@ -20,15 +32,43 @@ void require(bool ok, const std::string& what, float value) {
     if (!ok) throw Error("Sampler: " + what + ", got " + std::to_string(value));
 }
 
-// Descending logit, then ascending id: a total order, so the candidates
-// (and hence the draws) do not depend on the sort's handling of ties.
-struct ByLogit {
+// The heap's "less": token a is ranked after token b.
+struct RankedAfter {
     std::span<const float> logits;
     bool operator()(std::int32_t a, std::int32_t b) const {
         const float la = logits[std::size_t(a)], lb = logits[std::size_t(b)];
-        return la > lb || (la == lb && a < b);
+        return la < lb || (la == lb && a > b);
     }
 };
+
+// Token ids by descending logit, then ascending id, popped one at a time.
+class Ranking {
+public:
+    explicit Ranking(std::span<const float> logits) : after_{logits}, heap_(logits.size()) {
+        for (std::size_t i = 0; i < heap_.size(); ++i) heap_[i] = static_cast<std::int32_t>(i);
+        std::make_heap(heap_.begin(), heap_.end(), after_);
+    }
+    bool empty() const noexcept { return heap_.empty(); }
+    std::int32_t next() {
+        std::pop_heap(heap_.begin(), heap_.end(), after_);
+        const std::int32_t id = heap_.back();
+        heap_.pop_back();
+        return id;
+    }
+
+private:
+    RankedAfter after_;
+    std::vector<std::int32_t> heap_;
+};
+
+// max + log(sum exp(l - max)) in double, summed in token order: the log of
+// the softmax's denominator.
+double log_partition(std::span<const float> logits) {
+    const double peak = *std::max_element(logits.begin(), logits.end());
+    double sum = 0.0;
+    for (const float l : logits) sum += std::exp(double(l) - peak);
+    return peak + std::log(sum);
+}
 
 }  // namespace
 
@@ -44,109 +84,127 @@ Sampler::Sampler(SamplingOptions options) : options_(options), rng_(options.seed
 
 bool Sampler::greedy() const noexcept {
     const SamplingOptions& o = options_;
-    return (o.temperature == 0.0f || o.top_k == 1) && o.repetition_penalty == 1.0f && o.frequency_penalty == 0.0f &&
-           o.presence_penalty == 0.0f;
+    const bool no_penalty = o.repetition_penalty == 1.0f && o.frequency_penalty == 0.0f && o.presence_penalty == 0.0f;
+    return no_penalty && (o.temperature == 0.0f || o.top_k == 1);
 }
 
 std::int32_t Sampler::sample(std::span<const float> logits, std::span<const std::int32_t> previous) {
     if (logits.empty()) throw Error("Sampler: the logits are empty");
-    std::vector<float> adjusted;
-    const auto own = [&] {
-        if (adjusted.empty()) adjusted.assign(logits.begin(), logits.end());
-    };
-    // The repetition penalty: each distinct token seen, once.
-    if (options_.repetition_penalty != 1.0f && !previous.empty()) {
-        own();
-        std::unordered_set<std::int32_t> seen;
+    const bool repeat = options_.repetition_penalty != 1.0f && !previous.empty();
+    if (!repeat && picked_.empty()) return remember(pick(logits));
+    // The penalties change a copy: the repetition penalty once for each
+    // distinct token seen (a positive logit divided by it, a negative one
+    // multiplied), then the frequency and presence penalties of the tokens
+    // this sampler has picked.
+    std::vector<float> adjusted(logits.begin(), logits.end());
+    if (repeat) {
+        std::unordered_set<std::int32_t> done;
         for (const std::int32_t id : previous) {
-            if (id < 0 || std::size_t(id) >= adjusted.size() || !seen.insert(id).second) continue;
+            if (id < 0 || std::size_t(id) >= adjusted.size() || !done.insert(id).second) continue;
             float& l = adjusted[std::size_t(id)];
             l = l < 0.0f ? l * options_.repetition_penalty : l / options_.repetition_penalty;
         }
     }
-    // The frequency and presence penalties of the tokens this sampler picked.
-    if (!picked_.empty()) {
-        own();
-        for (const auto& [id, count] : picked_) {
-            if (std::size_t(id) < adjusted.size())
-                adjusted[std::size_t(id)] -= float(count) * options_.frequency_penalty + options_.presence_penalty;
-        }
+    for (const auto& [id, times] : picked_) {
+        if (std::size_t(id) < adjusted.size()) adjusted[std::size_t(id)] -= float(times) * options_.frequency_penalty + options_.presence_penalty;
     }
-    const std::int32_t id = pick(adjusted.empty() ? logits : std::span<const float>(adjusted));
+    return remember(pick(adjusted));
+}
+
+std::int32_t Sampler::remember(std::int32_t id) {
     if (options_.frequency_penalty != 0.0f || options_.presence_penalty != 0.0f) ++picked_[id];
     return id;
 }
 
 std::int32_t Sampler::pick(std::span<const float> logits) {
-    const std::size_t n = logits.size();
     if (options_.temperature == 0.0f || options_.top_k == 1)
         return static_cast<std::int32_t>(std::max_element(logits.begin(), logits.end()) - logits.begin());
 
-    const double top = *std::max_element(logits.begin(), logits.end());
-    const double temperature = options_.temperature;
-    const auto weight = [&](std::int32_t id) { return std::exp((double(logits[std::size_t(id)]) - top) / temperature); };
-    // Without top_k, the weights of every token (the softmax's denominator).
-    double everything = 0.0;
-    if (options_.top_k == 0)
-        for (std::size_t i = 0; i < n; ++i) everything += weight(static_cast<std::int32_t>(i));
+    const double peak = *std::max_element(logits.begin(), logits.end());
+    const double t = options_.temperature;
+    const auto weight = [&](std::int32_t id) { return std::exp((double(logits[std::size_t(id)]) - peak) / t); };
+    const auto sum_of = [](const std::vector<double>& w) {
+        double s = 0.0;
+        for (const double x : w) s += x;
+        return s;
+    };
+    Ranking ranking(logits);
+    std::vector<std::int32_t> ids;  // the kept candidates, in rank order
+    std::vector<double> w;          // and their weights
+    const auto take = [&] {
+        const std::int32_t id = ranking.next();
+        ids.push_back(id);
+        w.push_back(weight(id));
+    };
 
-    // The candidates, most likely first: top_k of them, or without top_k
-    // for top_p only as many as reach top_p of the total (256, then four
-    // times as many until they do), or all.
-    std::vector<std::int32_t> order(n);
-    std::iota(order.begin(), order.end(), 0);
-    const bool grow = options_.top_k == 0 && options_.top_p < 1.0f;
-    std::size_t keep = options_.top_k > 0 ? std::size_t(options_.top_k) : grow ? 256 : n;
-    for (;;) {
-        keep = std::min(keep, n);
-        std::partial_sort(order.begin(), order.begin() + std::ptrdiff_t(keep), order.end(), ByLogit{logits});
-        if (!grow || keep == n) break;
+    double total = 0.0;
+    if (options_.top_k > 0) {
+        while (ids.size() < std::size_t(options_.top_k) && !ranking.empty()) take();
+        total = sum_of(w);
+    } else {
+        for (std::size_t i = 0; i < logits.size(); ++i) total += weight(static_cast<std::int32_t>(i));
+    }
+    const bool from_heap = options_.top_k == 0;  // candidates still come off the ranking on demand
+    bool cut = options_.top_k > 0;
+    if (options_.top_p < 1.0f) {
+        // the fewest candidates whose mass reaches top_p of the total (at least one)
+        const double target = double(options_.top_p) * total;
         double mass = 0.0;
-        for (std::size_t i = 0; i < keep; ++i) mass += weight(order[i]);
-        if (mass >= options_.top_p * everything) break;
-        keep *= 4;
-    }
-    order.resize(keep);
-
-    std::vector<double> p(keep);
-    for (std::size_t i = 0; i < keep; ++i) p[i] = weight(order[i]);
-    double total = options_.top_k > 0 ? std::accumulate(p.begin(), p.end(), 0.0) : everything;
-    if (options_.top_p < 1.0f) {  // the fewest candidates whose mass reaches top_p (at least one)
-        double cumulative = 0.0;
         std::size_t m = 0;
-        while (m < p.size() && cumulative < options_.top_p * total) cumulative += p[m++];
-        p.resize(std::max<std::size_t>(m, 1));
-        total = std::accumulate(p.begin(), p.end(), 0.0);
+        while (mass < target) {
+            if (m == ids.size()) {
+                if (!from_heap || ranking.empty()) break;
+                take();
+            }
+            mass += w[m++];
+        }
+        m = std::max<std::size_t>(m, 1);
+        if (from_heap && ids.empty()) take();
+        ids.resize(m);
+        w.resize(m);
+        total = sum_of(w);
+        cut = true;
     }
-    if (options_.min_p > 0.0f) {  // at least min_p times as likely as the first
+    if (options_.min_p > 0.0f) {
+        // the candidates at least min_p times as likely as the first
+        if (ids.empty()) take();
+        const double floor = double(options_.min_p) * w[0];
         std::size_t m = 1;
-        while (m < p.size() && p[m] >= options_.min_p * p[0]) ++m;
-        p.resize(m);
-        total = std::accumulate(p.begin(), p.end(), 0.0);
+        for (;; ++m) {
+            if (m == ids.size()) {
+                if (cut || ranking.empty()) break;
+                take();
+            }
+            if (!(w[m] >= floor)) break;
+        }
+        ids.resize(m);
+        w.resize(m);
+        total = sum_of(w);
+        cut = true;
     }
     double draw = std::uniform_real_distribution<double>(0.0, total)(rng_);
-    for (std::size_t i = 0; i < p.size(); ++i) {
-        draw -= p[i];
-        if (draw < 0.0) return order[i];
+    for (std::size_t i = 0;; ++i) {
+        if (i == ids.size()) {
+            if (cut || ranking.empty()) return ids.back();
+            take();
+        }
+        draw -= w[i];
+        if (draw < 0.0) return ids[i];
     }
-    return order[p.size() - 1];  // rounding left the draw at the very end
 }
 
 TokenLogprobs token_logprobs(std::span<const float> logits, std::int32_t token, int top) {
     if (token < 0 || std::size_t(token) >= logits.size())
         throw Error("token_logprobs: token " + std::to_string(token) + " is outside the logits");
-    const double peak = *std::max_element(logits.begin(), logits.end());
-    double sum = 0.0;
-    for (const float l : logits) sum += std::exp(double(l) - peak);
-    const double log_total = peak + std::log(sum);
-    const auto logprob = [&](std::int32_t id) { return float(double(logits[std::size_t(id)]) - log_total); };
+    const double lz = log_partition(logits);
+    const auto logprob = [&](std::int32_t id) { return static_cast<float>(double(logits[std::size_t(id)]) - lz); };
     TokenLogprobs out;
     out.logprob = logprob(token);
-    std::vector<std::int32_t> order(logits.size());
-    std::iota(order.begin(), order.end(), 0);
-    const std::size_t k = std::min<std::size_t>(std::size_t(std::max(top, 0)), order.size());
-    std::partial_sort(order.begin(), order.begin() + std::ptrdiff_t(k), order.end(), ByLogit{logits});
-    for (std::size_t i = 0; i < k; ++i) out.top.emplace_back(order[i], logprob(order[i]));
+    Ranking ranking(logits);
+    for (int i = 0; i < top && !ranking.empty(); ++i) {
+        const std::int32_t id = ranking.next();
+        out.top.emplace_back(id, logprob(id));
+    }
     return out;
 }
 

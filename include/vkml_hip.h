@@ -131,6 +131,15 @@ typedef struct vkml_kernel_time {
 
 int vkml_set_profiling(int enabled);
 int vkml_get_profiling(void);
+
+/* Polls a workgroup that waits for another workgroup of its launch (the o
+ * GEMV of vkml_attend_step_o / _fused / _fast waiting for the merges)
+ * makes before it gives up and sets the launch's error flag (0: the default,
+ * 1 << 20). Launches made afterwards take the new limit, captured graphs
+ * the one they were captured with. No reference counterpart: the
+ * reference's dispatches never wait on one another. For tests that force
+ * a timeout from the host, and callers sharing the GPU's compute units. */
+int vkml_set_wait_limit(uint32_t polls);
 /* While tag is non-empty, profiled launches are labelled "kernel:tag" (the
  * model tags its projections: "gemv_dot:qkv", "gemv_dot_add:down", ...). */
 int vkml_set_profile_tag(const char* tag);
@@ -518,6 +527,9 @@ int vkml_attend_step_o(const vkml_attend_step_params* p, const float* d_qkv, con
 /* Synchronizes, then reports (VKML_ERROR_DEVICE) and clears a wait of an
  * earlier vkml_attend_step_o on this sync buffer that timed out. */
 int vkml_attend_o_check(uint32_t* d_sync);
+/* The same check without the error: *flag gets 0, or 1 for a wait that
+ * gave up (then cleared). */
+int vkml_attend_o_status(uint32_t* d_sync, uint32_t* flag);
 
 /* vkml_attend_step_o (llama.cpp:313-374, attention.cpp:54-84) in one
  * launch where the shapes allow it (q4_K, or q8_0 with f16 scales, o
@@ -545,6 +557,10 @@ int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* d_qkv,
 /* Synchronizes, then reports (VKML_ERROR_DEVICE) and clears (every block) a
  * wait of an earlier vkml_attend_step_fused on these blocks that timed out. */
 int vkml_attend_fused_check(uint32_t* d_sync, uint32_t blocks);
+/* The same check without the error: *flag gets 0, 1 for a wait that gave
+ * up, or 2 for a position past the launched chunks (then every block is
+ * cleared). */
+int vkml_attend_fused_status(uint32_t* d_sync, uint32_t blocks, uint32_t* flag);
 /* 1 when vkml_attend_step_fused takes these shapes in its one launch on
  * this device (the o format, the item's LDS, the merge's chunk count and a
  * grid whose waiting o workgroups leave the chunk items a slot); 0 when it

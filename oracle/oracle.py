@@ -75,6 +75,7 @@ def _declare(L):
         "orc_model_load_ex": (vp, [C.c_char_p, i64, i32, i32, i64]),
         "orc_model_load_opts": (vp, [C.c_char_p, i64, i32, i32, i64, i64, f32, f32]),
         "orc_token_logprobs": (f32, [vp, i64, i32, i32, vp, vp]),
+        "orc_model_set_attention_noise": (None, [vp, i32]),
         "orc_model_ring": (i64, [vp]),
         "orc_model_load": (vp, [C.c_char_p, i64, i32, i32]),
         "orc_model_free": (None, [vp]),
@@ -344,6 +345,11 @@ class Model:
         if lib().orc_model_forward(self._h, _p(t), t.size, _p(out)) != 0:
             raise RuntimeError(last_error())
         return out
+
+    def set_attention_noise(self, ulps: int) -> None:
+        """Test instrumentation: decode attention outputs moved by up to
+        `ulps` ulps before they are quantized (0: off)."""
+        lib().orc_model_set_attention_noise(self._h, int(ulps))
 
     def forward_all(self, tokens) -> np.ndarray:
         t = np.ascontiguousarray(tokens, dtype=np.int32)

@@ -164,6 +164,7 @@ struct orc_model {
     float* rope;
     layer* layers;
     int64_t position;
+    int attention_noise; /* test instrumentation (orc_model_set_attention_noise); 0: none */
     int64_t max_score_bytes; /* attention's score budget (ORC_MAX_SCORE_BYTES) */
     /* Sliding window (every layer, 0: none): the caches are rings of
      * min(context, window + extra rows) rows; oldest_kept is the first
@@ -245,6 +246,25 @@ void orc_model_free(orc_model* m) {
     free(m->layers);
     free(m);
 }
+
+/* Test instrumentation, not the reference's arithmetic: moves each of
+ * x[0 .. n) by a pseudo-random whole number of ulps in [-ulps, ulps] (a
+ * linear congruential sequence seeded by seed; zeros stay), to measure how
+ * far a change of an f32 result's last bits carries through the model. */
+static void add_ulp_noise(float* x, int64_t n, int ulps, uint32_t seed) {
+    uint32_t s = 12345u + seed;
+    for (int64_t i = 0; i < n; ++i) {
+        s = s * 1103515245u + 12345u;
+        const int32_t d = (int32_t)((s >> 16) % (uint32_t)(2 * ulps + 1)) - ulps;
+        if (x[i] == 0.0f) continue;
+        uint32_t b;
+        memcpy(&b, &x[i], 4);
+        b = (uint32_t)((int32_t)b + d);
+        memcpy(&x[i], &b, 4);
+    }
+}
+
+void orc_model_set_attention_noise(orc_model* m, int ulps) { m->attention_noise = ulps; }
 
 /* config.cpp:14-140 for arch "llama", then llama.cpp:170-271. The
  * reference reads a sliding window and soft caps from Gemma files only
@@ -500,7 +520,10 @@ static int model_run(orc_model* m, const int32_t* tokens, int64_t t, int all, fl
         }
         /* detail::attention (attention.cpp:167-227): the fused decode kernel
          * for one query, attention_block otherwise. */
-        if (t == 1) orc_attend_decode(qh, H, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, 0, end, m->attn_softcap, att);
+        if (t == 1) {
+            orc_attend_decode(qh, H, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, 0, end, m->attn_softcap, att);
+            if (m->attention_noise > 0) add_ulp_noise(att, H * hd, m->attention_noise, (uint32_t)(l * 7919 + m->position * 31));
+        }
         else orc_attention_prefill(qh, H, t, L->k_cache, L->v_cache, m->kv_f16, KVH, m->context, hd, end,
                                    m->max_score_bytes, m->attn_softcap, att);
     attended:

@@ -146,6 +146,11 @@ orc_model* orc_model_load_ex(const char* gguf_path, int64_t context_length, int 
  * attention / final logit soft caps given (0: none). */
 orc_model* orc_model_load_opts(const char* gguf_path, int64_t context_length, int kv_f16, int int_dot, int64_t sliding_extra_rows,
                                int64_t window, float attn_softcap, float final_softcap);
+/* Test instrumentation: decode steps move each attention output by up to
+ * ulps units in the last place (pseudo-random, fixed by layer and
+ * position) before it is quantized; 0 turns it off. Not the reference's
+ * arithmetic: it measures how far last-bit changes carry. */
+void orc_model_set_attention_noise(orc_model* m, int ulps);
 /* Rows of each layer's caches (the ring's with a sliding window). */
 int64_t orc_model_ring(const orc_model* m);
 void orc_model_free(orc_model* m);

@@ -326,3 +326,53 @@ def test_context_past_the_merge_limit_is_rejected_at_load(tmp_path):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     m.close()
     ref.close()
+
+
+@pytest.mark.parametrize("name,ctx", [("cfg5", 2048), ("q4k", 64)])
+def test_a_wait_that_gives_up_reruns_through_launches_that_never_wait(files, name, ctx):
+    """Forced from the host: with a poll limit of 1 (vkml_set_wait_limit)
+    the o GEMV's workgroups give up waiting for the merges almost at once,
+    set the launch's error flag and exit (every kernel still ends). The
+    model notices at the end of the steps, runs them again through the
+    separate chunk, merge and o launches (which never wait), and keeps
+    those: logits and greedy ids equal the oracle's bit for bit, and the
+    profile shows the separate launches. Then the limit is restored and a
+    fresh model takes the one launch again."""
+    from vkml_amd import hip as H
+    from vkml_amd import llama as LL
+    path = files[name]
+    vocab = gguf.read(path)[1]["token_embd.weight"][0][0]
+    prompt = np.random.default_rng(12).integers(0, vocab, 9).astype(np.int32)
+    ref = O.Model(path, ctx, kv_f16=True)
+    want = ref.forward(prompt)
+    H.lib().vkml_set_wait_limit(1)
+    try:
+        gpu = Llama(path, ctx, kv_f16=True)
+        same(gpu.forward(prompt), want)
+        tok = int(O.argmax(want))
+        for i in range(4):
+            if i == 3:  # by now the model has fallen back
+                LL.set_profiling(True)
+                LL.reset_profile()
+            got, exp = gpu.forward(np.array([tok], np.int32)), ref.forward(np.array([tok], np.int32))
+            same(got, exp)
+            tok = int(O.argmax(exp))
+        labels = {n.split(":")[0] for n, _, _ in LL.profile()}
+        LL.set_profiling(False)
+        assert "attend_merge" in labels and "attend_fused" not in labels, labels
+        g = gpu.generate_greedy(tok, 6)
+        w, _ = greedy_oracle(ref, tok, 6)
+        assert list(g) == list(w)
+        gpu.close()
+    finally:
+        H.lib().vkml_set_wait_limit(0)
+        LL.set_profiling(False)
+    fresh = Llama(path, ctx, kv_f16=True)
+    LL.set_profiling(True)
+    LL.reset_profile()
+    fresh.forward(prompt[:1])
+    labels = {n.split(":")[0] for n, _, _ in LL.profile()}
+    LL.set_profiling(False)
+    assert "attend_fused" in labels, labels
+    fresh.close()
+    ref.close()

@@ -705,3 +705,27 @@ def test_forward_all_rows_of_the_int8_path_track_the_double_reference(tiny_q4k):
     for i in (0, 3, 8, 15):
         want = O.reference_f64(tiny_q4k, tokens[:i + 1])
         assert np.max(np.abs(rows[i] - want)) <= 0.04 * np.abs(want).max(), i
+
+
+def test_one_ulp_in_the_attention_output_carries_to_the_logits(tmp_path):
+    """Why only a bit-exact decode meets a 1e-4 bar on an int8 model: the
+    oracle's own attention outputs moved by at most one ulp (test
+    instrumentation, before their Q8_0 quantization) change the logits of
+    a 4-layer q4_K model by well over 1e-4 of the largest within a few
+    steps -- a moved value crosses a rounding boundary of the activation
+    quantizer, and later layers and the KV cache carry the changed code on.
+    Without the noise the same runs are identical."""
+    spec = synth.ModelSpec("noise", 4, 512, 8, 2, 64, 1536, 4096, 10000.0, max_positions=512,
+                           matrix_type=gguf.Q4_K, embed_type=gguf.Q4_K, output_type=gguf.Q6_K)
+    path = synth.write_model(spec, str(tmp_path / "noise.gguf"), seed=21)
+    prompt = np.random.default_rng(3).integers(0, 4096, 48).astype(np.int32)
+    runs = []
+    for ulps in (0, 0, 1):
+        m = O.Model(path, 128, kv_f16=True)
+        m.forward(prompt)
+        m.set_attention_noise(ulps)
+        runs.append([m.forward(np.array([t], np.int32)) for t in (5, 77, 901, 13, 2, 640, 31, 7, 4000, 9, 12, 100)])
+        m.close()
+    assert all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(runs[0], runs[1]))
+    dev = max(float(np.max(np.abs(a - b)) / np.abs(a).max()) for a, b in zip(runs[0], runs[2]))
+    assert dev > 1e-3, dev

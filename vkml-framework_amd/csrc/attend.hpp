@@ -569,13 +569,15 @@ struct FusedSync {
     __host__ __device__ static uint32_t* arrive(uint32_t* s, uint32_t set) { return s + OSync::kWords + kArriveStride * set; }
 };
 
+// Polls a waiting workgroup makes before it gives up, unless the host set
+// another limit (vkml_set_wait_limit).
 constexpr uint32_t kOSpinCap = 1u << 20;
 
 // Lane 0 polls counter copy wg % kCopies until every merging workgroup has
 // arrived; false if the wait gave up (the spin limit, or another
 // workgroup's error). The error flag is the sync words' own unless given. Called by every thread; ends with a workgroup barrier
 // (the weight loads issued before it stay in flight).
-__device__ inline bool await_merged(uint32_t* sync, uint32_t wg, uint32_t arrivals, uint32_t* error = nullptr) {
+__device__ inline bool await_merged(uint32_t* sync, uint32_t wg, uint32_t arrivals, uint32_t* error, uint32_t cap) {
     __shared__ uint32_t s_ok;
     if (!error) error = OSync::error(sync);
     if (threadIdx.x == 0) {
@@ -587,7 +589,7 @@ __device__ inline bool await_merged(uint32_t* sync, uint32_t wg, uint32_t arriva
                 ok = 0;
                 break;
             }
-            if (spins >= kOSpinCap) {
+            if (spins >= cap) {
                 __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 ok = 0;
                 break;

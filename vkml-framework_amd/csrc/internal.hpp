@@ -32,6 +32,11 @@ struct ProfileScope {
 // Checks the launch that just happened.
 int check_launch(const char* what);
 
+// Polls a workgroup waiting for another of its launch makes before giving
+// up (vkml_set_wait_limit; default 1 << 20).
+uint32_t wait_limit();
+void set_wait_limit(uint32_t polls);
+
 // The device address of vkml_attend_step_noalloc's scratch on the current
 // device (k_attend.hip); vkml_init calls it once per device.
 int attend_scratch_setup(int device);

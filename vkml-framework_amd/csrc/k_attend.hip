@@ -118,6 +118,7 @@ struct MergeOArgs {
     float* scales;
     uint32_t hd, chunks, merge_wgs;
     uint32_t* sync;
+    uint32_t wait_cap;  // polls before the GEMV's wait gives up
 };
 
 // Workgroups [0, merge_wgs): the merge (kThreads / hd heads each, thread
@@ -143,7 +144,7 @@ __global__ void __launch_bounds__(kThreads) k_merge_o(MergeOArgs m, vkml::gemv::
     const uint32_t wg = blockIdx.x - m.merge_wgs;
     vkml::gemv::GemvRows<FMT, true, 32, vkml::gemv::kAdd, 2, kThreads, false, false, 1, FULL> rows;
     rows.start(g, wg);
-    if (!await_merged(m.sync, wg, m.merge_wgs)) return;
+    if (!await_merged(m.sync, wg, m.merge_wgs, OSync::error(m.sync), m.wait_cap)) return;
     vkml::gemv::stage_activation<kThreads, false, true>(g, smem);
     rows.finish(g, smem, vkml::gemv::staged_ss(smem, g.k));
 }
@@ -193,6 +194,7 @@ struct FusedArgs {
     float* out;         // the merged outputs [heads, hd] f32
     uint8_t* values;    // and their Q8_0 codes and f32 scales: the o GEMV's input
     float* scales;
+    uint32_t wait_cap;  // polls before the GEMV's wait gives up
 };
 
 // Workgroups [0, attn_wgs): the chunk pass, as k_attend_chunk, its partials
@@ -213,7 +215,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_fused(ChunkArgs a, FusedArg
         const uint32_t wg = blockIdx.x - f.attn_wgs;
         vkml::gemv::GemvRows<FMT, true, 32, vkml::gemv::kAdd, DEEP ? DEEP : 2, kThreads, false, false, DEEP ? 0 : 1, FULL> rows;
         rows.start(g, wg);
-        if (!await_merged(f.sync, wg, f.merges, f.error)) return;
+        if (!await_merged(f.sync, wg, f.merges, f.error, f.wait_cap)) return;
         vkml::gemv::stage_activation<kThreads, false, true>(g, smem);
         rows.finish(g, smem, vkml::gemv::staged_ss(smem, g.k));
         return;
@@ -469,7 +471,7 @@ int vkml_attend_step_o(const vkml_attend_step_params* p, const float* qkv, const
     VKML_CHECK_ARG(o->m == 1 && o->k == p->heads * p->head_dim,
                    "attend_step_o: the o projection must take the " + std::to_string(p->heads * p->head_dim) + " attention outputs");
     const MergeOArgs m{partial, stats, out, static_cast<uint8_t*>(values), scales, p->head_dim, p->chunks,
-                       p->heads / (kThreads / p->head_dim), sync};
+                       p->heads / (kThreads / p->head_dim), sync, vkml::abi::wait_limit()};
     const vkml::gemv::GemvArgs g{static_cast<const uint4*>(values), scales, o_values, o_scales, nullptr, nullptr, x, x, o->n, o->k};
     // The chunk pass clears the merge + o sync words only when that launch follows.
     const bool fusable = o->b_type == VKML_Q4_K || (o->b_type == VKML_Q8_0 && o->scale_type == VKML_F16);
@@ -508,7 +510,7 @@ int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* qkv, c
     uint32_t* own = sync + static_cast<uint64_t>(block) * FusedSync::kWords;
     uint32_t* next = sync + static_cast<uint64_t>((block + 1) % blocks) * FusedSync::kWords;
     const ChunkArgs args = step_args(p, qkv, rope_table, k_cache, v_cache, partial, stats, state, nullptr);
-    const FusedArgs f{0, 0, own, next, sync, out, static_cast<uint8_t*>(values), scales};
+    const FusedArgs f{0, 0, own, next, sync, out, static_cast<uint8_t*>(values), scales, vkml::abi::wait_limit()};
     const vkml::gemv::GemvArgs g{static_cast<const uint4*>(values), scales, o_values, o_scales, nullptr, nullptr, x, x, o->n, o->k};
     {
         vkml::abi::ProfileScope prof("attend_fused");
@@ -543,25 +545,35 @@ int vkml_attend_step_fused_supported(const vkml_attend_step_params* p, const vkm
         (p->kv_type != VKML_F16 && p->kv_type != VKML_F32))
         return 0;
     const ChunkArgs args = step_args(p, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
-    const FusedArgs f{0, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    const FusedArgs f{0, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
     const vkml::gemv::GemvArgs g{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, o->n, o->k};
     return launch_fused(p->head_dim, p->kv_type == VKML_F16, args, f, g, o->b_type, o->scale_type, true) ? 1 : 0;
 }
 
-int vkml_attend_fused_check(uint32_t* sync, uint32_t blocks) {
+int vkml_attend_fused_status(uint32_t* sync, uint32_t blocks, uint32_t* flag_out) {
     VKML_REQUIRE_INIT();
-    VKML_CHECK_ARG(sync && blocks >= 2, "attend_fused_check: null buffer or fewer than two blocks");
+    VKML_CHECK_ARG(sync && blocks >= 2 && flag_out, "attend_fused_status: null buffer or fewer than two blocks");
     hipStream_t s = vkml::abi::stream();
     uint32_t flag = 0;
     hipError_t e = hipMemcpyAsync(&flag, sync, 4, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_fused_check");
+    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_fused_status");
+    *flag_out = flag;
     if (flag == 0) return VKML_OK;
     // A wait gave up, or a position outran the chunks: every block starts
     // over (flag and counters).
     e = hipMemsetAsync(sync, 0, vkml_attend_fused_sync_bytes(blocks), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_fused_check");
+    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_fused_status");
+    return VKML_OK;
+}
+
+int vkml_attend_fused_check(uint32_t* sync, uint32_t blocks) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(sync && blocks >= 2, "attend_fused_check: null buffer or fewer than two blocks");
+    uint32_t flag = 0;
+    if (int r = vkml_attend_fused_status(sync, blocks, &flag)) return r;
+    if (flag == 0) return VKML_OK;
     if (flag == 2)
         return vkml::abi::fail(VKML_ERROR_DEVICE,
                                "attend_step_fused: a position lay past the keys of the launched chunks; the step's results are invalid");
@@ -640,19 +652,29 @@ int vkml_attend_step_noalloc(const vkml_attend_step_params* p, const float* qkv,
     return vkml::abi::check_launch("attend_step_noalloc");
 }
 
-int vkml_attend_o_check(uint32_t* sync) {
+int vkml_attend_o_status(uint32_t* sync, uint32_t* flag_out) {
     VKML_REQUIRE_INIT();
-    VKML_CHECK_ARG(sync, "attend_o_check: null buffer");
+    VKML_CHECK_ARG(sync && flag_out, "attend_o_status: null buffer");
     hipStream_t s = vkml::abi::stream();
     uint32_t flag = 0;
     hipError_t e = hipMemcpyAsync(&flag, sync, 4, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_o_check");
+    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_o_status");
+    *flag_out = flag;
     if (flag == 0) return VKML_OK;
     const uint32_t zero = 0;
     e = hipMemcpyAsync(sync, &zero, 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_o_check");
+    if (e != hipSuccess) return vkml::abi::hip_fail(e, "attend_o_status");
+    return VKML_OK;
+}
+
+int vkml_attend_o_check(uint32_t* sync) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(sync, "attend_o_check: null buffer");
+    uint32_t flag = 0;
+    if (int r = vkml_attend_o_status(sync, &flag)) return r;
+    if (flag == 0) return VKML_OK;
     return vkml::abi::fail(VKML_ERROR_DEVICE, "attend_step_o: the o GEMV's wait for the merge timed out; the step's results are invalid");
 }
 

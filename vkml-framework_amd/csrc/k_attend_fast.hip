@@ -28,6 +28,7 @@ struct FastLaunch {
     uint32_t* sync;  // the o GEMV's counters and error flag (null: no o GEMV)
     uint32_t* next;  // the next launch's block, whose o counters this one zeroes (may be null)
     uint32_t* error;
+    uint32_t wait_cap;  // polls before the GEMV's wait gives up
 };
 
 constexpr int kNoGemv = -1;
@@ -40,7 +41,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_fast(FastArgs a, FastLaunch
             const uint32_t wg = blockIdx.x - f.items;
             vkml::gemv::GemvRows<FMT, true, 32, vkml::gemv::kAdd, DEEP ? DEEP : 2, kThreads, false, false, DEEP ? 0 : 1, FULL> rows;
             rows.start(g, wg);
-            if (!await_merged(f.sync, wg, a.kv_heads, f.error)) return;
+            if (!await_merged(f.sync, wg, a.kv_heads, f.error, f.wait_cap)) return;
             vkml::gemv::stage_activation<kThreads, false, true>(g, smem);
             rows.finish(g, smem, vkml::gemv::staged_ss(smem, g.k));
             return;
@@ -177,7 +178,7 @@ int vkml_attend_fast(const vkml_attend_params* p, const float* q, const void* k_
     const FastArgs a{q, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
                      p->kv_start, p->kv_len, p->chunks, p->scale, p->softcap, 0, FusedSync::arrive(sync, 0), out,
                      static_cast<uint8_t*>(values), scales};
-    const FastLaunch f{p->chunks * p->kv_heads, nullptr, nullptr, nullptr};
+    const FastLaunch f{p->chunks * p->kv_heads, nullptr, nullptr, nullptr, 0};
     vkml::abi::ProfileScope prof("attend_fast");
     launch_fast(p->head_dim, a, f, nullptr, 0, false);
     return vkml::abi::check_launch("attend_fast");
@@ -191,7 +192,7 @@ int vkml_attend_step_fast_supported(const vkml_attend_step_params* p, const vkml
     if (!o_fusable(o, p->heads, p->head_dim)) return 0;
     const FastArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
                      0, 0, p->chunks, p->scale, p->softcap, 0, nullptr, nullptr, nullptr, nullptr};
-    const FastLaunch f{p->chunks * p->kv_heads, nullptr, nullptr, nullptr};
+    const FastLaunch f{p->chunks * p->kv_heads, nullptr, nullptr, nullptr, 0};
     const vkml::gemv::GemvArgs g{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, o->n, o->k};
     return launch_fast(p->head_dim, a, f, &g, o->b_type, true) ? 1 : 0;
 }
@@ -219,7 +220,7 @@ int vkml_attend_step_fast(const vkml_attend_step_params* p, const float* qkv, vo
     const FastArgs a{qkv, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
                      p->kv_start, 0, p->chunks, p->scale, p->softcap, std::min(p->ready_chunks, p->chunks), FusedSync::arrive(own, 0),
                      out, static_cast<uint8_t*>(values), scales};
-    const FastLaunch f{p->chunks * p->kv_heads, own, next, sync};
+    const FastLaunch f{p->chunks * p->kv_heads, own, next, sync, vkml::abi::wait_limit()};
     const vkml::gemv::GemvArgs g{static_cast<const uint4*>(values), scales, o_values, o_scales, nullptr, nullptr, x, x, o->n, o->k};
     vkml::abi::ProfileScope prof("attend_fast");
     VKML_CHECK_ARG(launch_fast(p->head_dim, a, f, &g, o->b_type, false),

@@ -135,6 +135,13 @@ int check_launch(const char* what) {
     return VKML_OK;
 }
 
+namespace {
+uint32_t g_wait_limit = 1u << 20;
+}  // namespace
+
+uint32_t wait_limit() { return g_wait_limit; }
+void set_wait_limit(uint32_t polls) { g_wait_limit = polls; }
+
 }  // namespace vkml::abi
 
 using namespace vkml::abi;
@@ -357,6 +364,11 @@ int vkml_set_profiling(int enabled) {
 }
 
 int vkml_get_profiling(void) { return g.profiling ? 1 : 0; }
+
+int vkml_set_wait_limit(uint32_t polls) {
+    vkml::abi::set_wait_limit(polls == 0 ? (1u << 20) : polls);
+    return VKML_OK;
+}
 
 int vkml_set_profile_tag(const char* tag) {
     g.tag = tag ? tag : "";

@@ -133,6 +133,9 @@ SIGNATURES = {
     "vkml_attend_fused_sync_bytes": [u32],
     "vkml_attend_step_fused": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp, u32, u32],
     "vkml_attend_fused_check": [vp, u32],
+    "vkml_attend_fused_status": [vp, u32, P(u32)],
+    "vkml_attend_o_status": [vp, P(u32)],
+    "vkml_set_wait_limit": [u32],
     "vkml_attend_step_fused_supported": [P(AttendStepParams), P(GemvDotParams)],
     "vkml_attend_fast": [P(AttendParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step_fast": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp, u32, u32],

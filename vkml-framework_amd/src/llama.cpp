@@ -340,6 +340,9 @@ struct Llama::Impl {
     // its own captured graph); 0: every chunk of the cache.
     static constexpr std::int64_t kMinTier = 8;
     bool tiered = false;
+    // Set once a device-side wait gave up: the attention no longer takes
+    // launches whose workgroups wait for others (fall_back).
+    bool no_waits = false;
     std::int64_t step_tier = 0;
     std::map<std::pair<bool, std::int64_t>, std::uint64_t> graphs;  // (greedy, tier) -> captured step
 
@@ -396,15 +399,48 @@ struct Llama::Impl {
 
     bool quantized_input(const Weight& w) const { return int_dot && w.int_dot_ok(); }
 
-    // Reports a merge + o launch whose wait for the merge gave up (the
-    // step's KV rows and logits from that step on are then invalid and must
-    // be recomputed: the caller's position does not advance past them).
-    void check_attend_o() const {
-        if (!int_dot) return;
-        check(vkml_attend_o_check(static_cast<std::uint32_t*>(const_cast<void*>(o_sync.data()))), "Llama: decode step");
-        if (fused_sync.numel())
-            check(vkml_attend_fused_check(static_cast<std::uint32_t*>(const_cast<void*>(fused_sync.data())), u32(layers.size())),
+    // Whether a device-side wait of the steps since the last check gave up
+    // (an o GEMV waiting for its merges: another process holding the GPU's
+    // compute units, say). Those steps' KV rows and logits are then invalid.
+    // A position past the launched chunks is a fault of the tiers and throws.
+    bool waits_failed() const {
+        if (!int_dot) return false;
+        std::uint32_t flag = 0;
+        check(vkml_attend_o_status(static_cast<std::uint32_t*>(const_cast<void*>(o_sync.data())), &flag), "Llama: decode step");
+        bool failed = flag != 0;
+        if (fused_sync.numel()) {
+            std::uint32_t f = 0;
+            check(vkml_attend_fused_status(static_cast<std::uint32_t*>(const_cast<void*>(fused_sync.data())), u32(layers.size()), &f),
                   "Llama: decode step");
+            if (f == 2) throw Error("Llama: decode step: a position lay past the keys of the launched chunks; the step's results are invalid");
+            failed = failed || f != 0;
+        }
+        return failed;
+    }
+
+    // From now on the attention takes the launches that never wait (the
+    // chunk pass, the merge and the o GEMV apart, over every chunk of the
+    // cache), and the captured steps that waited are dropped.
+    void fall_back() {
+        no_waits = true;
+        tiered = false;
+        for (const auto& [key, g] : graphs) (void)vkml_graph_destroy(g);
+        graphs.clear();
+    }
+
+    // count decode steps from token first at the current position (greedy:
+    // each step's argmax feeds the next, on the device). If a device-side
+    // wait gave up in them, they run again through the launches that never
+    // wait, which the model keeps using: their results replace the invalid
+    // ones (the KV rows of those positions and the token log are rewritten).
+    void decode_steps(bool greedy, std::int32_t first, std::int64_t count) {
+        for (int attempt = 0;; ++attempt) {
+            set_state(first, position);
+            for (std::int64_t i = 0; i < count; ++i) run_step(greedy, position + i);
+            if (!waits_failed()) return;
+            if (attempt > 0) throw Error("Llama: decode step: a device-side wait gave up without waiting launches");
+            fall_back();
+        }
     }
 
     // One token: the state's token at the state's position.
@@ -470,7 +506,7 @@ struct Llama::Impl {
             const bool o_q = quantized_input(L.o);
             // rope, append and attention in one launch, then the merge
             tag("attention");
-            const bool merge_o = int_dot && o_q && L.o.int_dot_ok();
+            const bool merge_o = int_dot && o_q && L.o.int_dot_ok() && !no_waits;
             const std::int64_t launched = merge_o && fsync && step_tier ? std::min(L.chunks(), step_tier) : L.chunks();
             // A tier above the smallest serves positions whose keys fill at
             // least half its chunks: those chunks' items may load before
@@ -934,9 +970,7 @@ Tensor Llama::forward(std::span<const std::int32_t> tokens) {
     if (t == 1) {
         // One token: the decode step (fused decode attention, llama.cpp:
         // 366 with attention.cpp:199-203).
-        m.set_state(tokens[0], m.position);
-        m.run_step(false, m.position);
-        m.check_attend_o();
+        m.decode_steps(false, tokens[0], 1);
         m.ran_to(++m.position);
     } else {
         m.prefill(tokens, nullptr);
@@ -952,9 +986,7 @@ Tensor Llama::forward_all(std::span<const std::int32_t> tokens) {
     m.check_room(t);
     Tensor out = Tensor::empty(*m.context, {t, m.config.vocab_size}, DType::F32);
     if (t == 1) {
-        m.set_state(tokens[0], m.position);
-        m.run_step(false, m.position);
-        m.check_attend_o();
+        m.decode_steps(false, tokens[0], 1);
         m.ran_to(++m.position);
         check(vkml_memcpy_d2d(out.data(), m.logits.data(), out.nbytes()), "Llama::forward_all");
     } else {
@@ -967,11 +999,9 @@ std::vector<std::int32_t> Llama::generate_greedy(std::int32_t first, std::int64_
     Impl& m = *impl_;
     if (count <= 0) return {};
     m.check_room(count);
-    m.set_state(first, m.position);
-    for (std::int64_t i = 0; i < count; ++i) m.run_step(true, m.position + i);
+    m.decode_steps(true, first, count);
     std::vector<std::int32_t> out(static_cast<std::size_t>(count));
     check(vkml_memcpy_d2h(out.data(), m.log.data(), out.size() * 4), "Llama::generate_greedy");
-    m.check_attend_o();
     m.position += count;
     m.ran_to(m.position);
     return out;

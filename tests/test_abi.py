@@ -58,3 +58,14 @@ def test_calls_before_init_fail_with_a_message():
     assert lib.vkml_malloc(ctypes.c_uint64(16), ctypes.byref(p)) == 4  # VKML_ERROR_STATE
     assert b"vkml_init" in lib.vkml_last_error()
     assert lib.vkml_abi_version() == 1
+
+
+def test_umbrella_header_compiles(tmp_path):
+    """include/vkml/vkml.hpp (the reference's callers include it whole,
+    apps/vkml_run.cpp:41 there) brings in the public API this build has."""
+    src = tmp_path / "use.cpp"
+    src.write_text('#include "vkml/vkml.hpp"\n'
+                   "int main() { vkml::SamplingOptions o; vkml::LlamaOptions l; (void)o; (void)l;\n"
+                   "  return sizeof(vkml::Session) > 0 && sizeof(vkml::Tensor) > 0 ? 0 : 1; }\n")
+    subprocess.run(["g++", "-std=c++20", "-fsyntax-only", "-I" + os.path.join(PKG, "include"), "-I" + os.path.join(ROOT, "include"),
+                    str(src)], check=True)

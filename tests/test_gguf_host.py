@@ -117,7 +117,10 @@ def nested_array(depth):
     ("nested", header(meta=[("k", 9, nested_array(9))]), "nested more than 8 deep"),
     ("dims", header(tensors=[("t", (1, 1, 1, 1, 1), 0, 0)]), "5 dimensions"),
     ("past_end", header(tensors=[("t", (64, 64), 0, 0)]), "runs past the end of the file"),
-    ("alignment", header(meta=[("general.alignment", 4, struct.pack("<I", 24))]), "general.alignment is 24"),
+    ("alignment", header(meta=[("general.alignment", 4, struct.pack("<I", 0))]), "general.alignment is 0"),
+    ("alignment_large", header(meta=[("general.alignment", 4, struct.pack("<I", (1 << 30) + 1))]), "general.alignment is 1073741825"),
+    ("array_count", header(meta=[("k", 9, struct.pack("<IQ", 8, 1 << 29))]), "truncated"),
+    ("array_strings", header(meta=[("k", 9, struct.pack("<IQ", 8, 3) + b"\0" * 20)]), "truncated"),
     ("too_large", header(tensors=[("t", (1 << 62, 1 << 3), 0, 0)]), "too large"),
 ])
 def test_damaged_header_fails_with_a_message(checker, tmp_path, name, data, message):
@@ -125,6 +128,15 @@ def test_damaged_header_fails_with_a_message(checker, tmp_path, name, data, mess
     path.write_bytes(data)
     rc, out = run(checker, "config", str(path))
     assert rc == 1 and out.startswith("error gguf: ") and message in out, out
+
+
+def test_what_the_reference_accepts_parses(checker, tmp_path):
+    """A rank-0 tensor and an alignment that is not a power of two are
+    accepted, as the reference's reader accepts them (gguf.cpp:341-362)."""
+    path = tmp_path / "ok.gguf"
+    path.write_bytes(header(meta=[("general.alignment", 4, struct.pack("<I", 24))], tensors=[("scalar", (), 0, 0)]) + b"\0" * 64)
+    rc, out = run(checker, "config", str(path))
+    assert rc == 0, out
 
 
 def test_nesting_up_to_the_limit_parses(checker, tmp_path):

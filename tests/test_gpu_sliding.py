@@ -222,3 +222,16 @@ def test_llama_file_window_and_cap_keys_are_ignored(tmp_path):
     a.close()
     b.close()
     ref.close()
+
+
+def test_softmax_over_a_ring_needs_a_window_inside_it():
+    """A ring's rows see at most `ring` positions: a window of 0 or past the
+    ring would wrap positions onto each other, so the call is refused
+    before anything is launched."""
+    H.init()
+    x = H.empty(4 * 8 * 4)
+    for window in (0, 9):
+        with pytest.raises(H.VkmlError, match="a ring needs a window of 1 to 8"):
+            H.call("vkml_softmax", H.SoftmaxParams(4, 8, 1.0, 1, 4, 0, window, 0.0, 8), x.p, x.p)
+    H.call("vkml_softmax", H.SoftmaxParams(4, 8, 1.0, 1, 4, 0, 8, 0.0, 8), x.p, x.p)
+    H.synchronize()

@@ -779,6 +779,9 @@ int vkml_softmax(const vkml_softmax_params* p, const float* x, float* out) {
     VKML_CHECK_ARG(p, "softmax: null params");
     VKML_CHECK_ARG(!p->causal || p->q_len > 0, "softmax: causal rows need q_len");
     VKML_CHECK_ARG(!p->ring || (p->causal && p->cols <= p->ring), "softmax: a ring needs the causal mask and at most ring columns");
+    // A row's visible positions must fit the ring, or they would wrap onto each other.
+    VKML_CHECK_ARG(!p->ring || (p->window >= 1 && p->window <= p->ring),
+                   "softmax: a ring needs a window of 1 to " + std::to_string(p->ring) + " positions, got " + std::to_string(p->window));
     if (p->rows == 0 || p->cols == 0) return VKML_OK;
     VKML_CHECK_ARG(x && out, "softmax: null buffer");
     ProfileScope prof("softmax");

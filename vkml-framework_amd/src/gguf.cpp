@@ -71,6 +71,7 @@ struct ValueKind {
 constexpr std::array<ValueKind, 13> kValueKinds{{{1, 'u'}, {1, 'i'}, {2, 'u'}, {2, 'i'}, {4, 'u'}, {4, 'i'}, {4, 'f'}, {1, 'b'},
                                                  {0, 's'}, {0, 'a'}, {8, 'u'}, {8, 'i'}, {8, 'f'}}};
 constexpr int kMaxArrayDepth = 8;
+constexpr std::uint64_t kMaxArray = std::uint64_t{1} << 28;  // values in one array (the reference's bound, gguf.cpp)
 
 GgufValue parse_value(Cursor& c, std::uint32_t type, int depth) {
     if (type >= kValueKinds.size()) c.malformed("a value of unknown type " + std::to_string(type));
@@ -80,9 +81,14 @@ GgufValue parse_value(Cursor& c, std::uint32_t type, int depth) {
         if (depth >= kMaxArrayDepth) c.malformed("arrays nested more than " + std::to_string(kMaxArrayDepth) + " deep");
         const std::uint32_t element = c.u32("an array's element type");
         const std::uint64_t count = c.u64("an array's length");
-        if (count > c.remaining()) c.truncated("an array of " + std::to_string(count) + " values");
+        if (element >= kValueKinds.size()) c.malformed("an array of unknown type " + std::to_string(element));
+        // Every element takes at least this many bytes of the file (a
+        // string its 8-byte length, an array its type and length), so a
+        // damaged count is caught before anything is reserved for it.
+        const std::uint64_t least = kValueKinds[element].kind == 's' ? 8 : kValueKinds[element].kind == 'a' ? 12 : kValueKinds[element].width;
+        if (count > kMaxArray || count > c.remaining() / least) c.truncated("an array of " + std::to_string(count) + " values");
         std::vector<GgufValue> items;
-        items.reserve(static_cast<std::size_t>(count));
+        items.reserve(static_cast<std::size_t>(std::min<std::uint64_t>(count, std::uint64_t{1} << 20)));
         for (std::uint64_t i = 0; i < count; ++i) items.push_back(parse_value(c, element, depth + 1));
         return {std::move(items)};
     }
@@ -299,7 +305,7 @@ Gguf::Gguf(const std::filesystem::path& path) : path_(path), map_(std::make_shar
         Record r;
         r.name = c.text("a tensor name");
         const std::uint32_t dims = c.u32("a tensor's rank");
-        if (dims == 0 || dims > 4) c.malformed("tensor " + r.name + " has " + std::to_string(dims) + " dimensions (1 to 4 are allowed)");
+        if (dims > 4) c.malformed("tensor " + r.name + " has " + std::to_string(dims) + " dimensions (at most 4 are allowed)");
         r.entry.shape.assign(dims, 0);
         // GGUF lists the fastest-varying dimension first; Shape is row-major.
         for (std::uint32_t d = 0; d < dims; ++d) {
@@ -314,7 +320,8 @@ Gguf::Gguf(const std::filesystem::path& path) : path_(path), map_(std::make_shar
     std::uint64_t alignment = 32;
     if (const auto it = metadata_.find("general.alignment"); it != metadata_.end() && it->second.is_number()) {
         alignment = static_cast<std::uint64_t>(it->second.number());
-        if (alignment == 0 || (alignment & (alignment - 1)) != 0) c.malformed("general.alignment is " + std::to_string(alignment));
+        // Any alignment up to 2^30 bytes, as the reference takes (GGUF writes powers of two).
+        if (alignment == 0 || alignment > (std::uint64_t{1} << 30)) c.malformed("general.alignment is " + std::to_string(alignment));
     }
     const auto header_end = static_cast<std::uint64_t>(c.here() - base);
     data_start_ = (header_end + alignment - 1) / alignment * alignment;

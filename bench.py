@@ -11,9 +11,17 @@ at the end.
 Prints one JSON line: tokens/s, the whole step's algorithmic HBM rate (GGUF
 bytes of every weight plus the KV rows read) against 8 TB/s, a roofline
 entry for the dominant kernel, and the CPU oracle's decode rate on the host
-cores as a reported baseline. The oracle continues from the GPU's KV cache
-(handed over after the GPU's prefill) and its greedy tokens must equal the
-timed run's: "parity" says whether they do.
+cores as a reported baseline.
+
+"parity" holds the timed run against the oracle's own run of the same
+model and prompt (tests/golden/headline_cfg5.npz, written by
+tests/golden/make_headline_fixture.py: its 4096-token prompt pass and 256
+greedy steps, nothing handed over from the GPU): the GPU's prompt logits
+bit for bit, and every timed greedy id. The CPU baseline's oracle, which
+continues from the GPU's KV cache, must also pick the timed run's first
+tokens. "fast_attention" reports the same decode with the matrix-core
+attention option, which is not the reference's order of f32 operations:
+its rate, its attention launch, and how many of its ids equal the oracle's.
 
 Under "configs" the line also carries BASELINE.json's other measured
 configs: cfg2's isolated GEMVs and cfg4's decode attention (each launched
@@ -64,8 +72,17 @@ GATE_UP_TRAFFIC_SOURCES = "b8ec832d8172fb19"
 TRAFFIC_FILES = ("vkml-framework_amd/csrc/gemv.hpp", "vkml-framework_amd/csrc/k_gemv.hip", "vkml-framework_amd/csrc/device.hpp")
 ATTEND_TRAFFIC = 28_573_079
 ATTEND_TRAFFIC_SOURCES = "d1520404944f2028"
+ATTEND_TRAFFIC_POSITION = 4224  # the launch's shape the figure was taken at (position; 35 chunks, 32 loading early)
 ATTEND_FILES = ("vkml-framework_amd/csrc/k_attend.hip", "vkml-framework_amd/csrc/attend.hpp", "vkml-framework_amd/csrc/gemv.hpp",
                 "vkml-framework_amd/csrc/device.hpp")
+
+# The oracle's own runs of the headline workloads (tests/golden/make_headline_fixture.py):
+# its prompt logits and every greedy id, against which each timed run is checked.
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+# The roofline entry's attention launch is timed at the configured cfg5
+# workload's middle position (4096-token prompt, 256 steps), whatever --steps is.
+ROOFLINE_STEPS = 256
 
 # GGUF-native bytes per weight (q4_K 144 B / 256, q6_K 210 B / 256).
 Q4K, Q6K = 144 / 256, 210 / 256
@@ -73,6 +90,28 @@ Q4K, Q6K = 144 / 256, 210 / 256
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def fixture(cfg):
+    """The oracle's headline run for cfg ("cfg5", "cfg3"), or None if absent."""
+    path = os.path.join(GOLDEN, f"headline_{cfg}.npz")
+    return np.load(path) if os.path.exists(path) else None
+
+
+def against_fixture(fx, prompt_logits, first, tokens):
+    """The GPU run against the oracle's own: the prompt's logits bit for bit,
+    the first greedy id and every timed id (as many as the fixture holds)."""
+    if fx is None:
+        return None
+    ids = fx["ids"]
+    n = min(len(tokens), len(ids) - 1)
+    got = [int(t) for t in tokens[:n]]
+    want = [int(t) for t in ids[1:n + 1]]
+    differ = [i for i in range(n) if got[i] != want[i]]
+    bits = bool(np.array_equal(np.asarray(prompt_logits, np.float32).view(np.uint32), fx["prompt_logits"].view(np.uint32)))
+    return {"prompt_logits_bit_identical": bits, "first_id_equal": int(first) == int(ids[0]),
+            "timed_ids_checked": n, "timed_ids_equal": n - len(differ), "first_difference": differ[0] if differ else None,
+            "all_equal": bits and int(first) == int(ids[0]) and not differ and n == len(tokens)}
 
 
 def sources_hash(files=TRAFFIC_FILES):
@@ -366,9 +405,10 @@ def bench_gemv_cfg2(min_bytes=512 << 20):
 
 def bench_attention_cfg4(min_bytes=512 << 20):
     """cfg4: decode attention of 32 query heads on 8 KV heads, head_dim 128,
-    over f16 caches of T = 4096, 16384 and 32768 positions: the chunk pass
-    and the merge (vkml_attend + vkml_attend_merge). Algorithmic bytes: K
-    and V (4096 T) plus q in and the output out."""
+    over f16 caches of T = 4096, 16384 and 32768 positions: the exact chunk
+    pass and merge (vkml_attend + vkml_attend_merge), and the matrix-core
+    form (vkml_attend_fast: items, merges by the last item, one launch).
+    Algorithmic bytes: K and V (4096 T) plus q in and the output out."""
     import math
     from vkml_amd import hip as H
     heads, kvh, hd = 32, 8, 128
@@ -386,10 +426,19 @@ def bench_attention_cfg4(min_bytes=512 << 20):
             H.call("vkml_attend", prm, q.p, caches[i][0].p, caches[i][1].p, part.p, stats.p, None)
             H.call("vkml_attend_merge", prm, part.p, stats.p, o.p, None, None)
         best, med = rotation_times(copies, call)
+        sync = filled(H.lib().vkml_attend_fused_sync_bytes(1), 0)
+
+        def call_fast(i):
+            H.call("vkml_attend_fast", prm, q.p, caches[i][0].p, caches[i][1].p, part.p, stats.p, o.p, None, None, sync.p, None)
+        fbest, fmed = rotation_times(copies, call_fast)
+        sync.close()
         alg = 2 * cache + 2 * heads * hd * 4
         out.append({"positions": T, "bytes": alg, "us": {"best": round(best, 3), "median": round(med, 3)},
-                    "frac": round(alg / (best * 1e-6) / 1e9 / PEAK_HBM, 4)})
-        log(f"cfg4 attention at {T}: {best:.2f} us ({alg / (best * 1e-6) / 1e9:.0f} GB/s)")
+                    "frac": round(alg / (best * 1e-6) / 1e9 / PEAK_HBM, 4),
+                    "fast_us": {"best": round(fbest, 3), "median": round(fmed, 3)},
+                    "fast_frac": round(alg / (fbest * 1e-6) / 1e9 / PEAK_HBM, 4)})
+        log(f"cfg4 attention at {T}: exact {best:.2f} us ({alg / (best * 1e-6) / 1e9:.0f} GB/s), "
+            f"matrix-core {fbest:.2f} us ({alg / (fbest * 1e-6) / 1e9:.0f} GB/s)")
         for c in caches:
             for b in c:
                 b.close()
@@ -411,13 +460,15 @@ def bench_cfg3(L, steps=128, prompt_len=512):
         prompt = np.random.default_rng(4).integers(0, spec.vocab, prompt_len).astype(np.int32)
         pre = prefill_rates(model, spec, prompt, [prompt_len], L)
         model.rewind(0)
-        first = int(np.argmax(model.forward(prompt)))
+        prompt_logits = model.forward(prompt)
+        first = int(np.argmax(prompt_logits))
         model.generate_greedy(first, 8)
         model.rewind(prompt_len)
         L.synchronize()
         t0 = time.perf_counter()
-        model.generate_greedy(first, steps)
+        tokens = model.generate_greedy(first, steps)
         secs = time.perf_counter() - t0
+        parity = against_fixture(fixture("cfg3"), prompt_logits, first, tokens)
         d, ff, layers = spec.hidden, spec.ffn, spec.n_layers
         qd, kvd = spec.heads * spec.head_dim, spec.kv_heads * spec.head_dim
         weights = layers * ((qd + 2 * kvd) * d + d * qd + 3 * ff * d) * Q4K + spec.vocab * d * Q6K + d * Q6K
@@ -428,9 +479,66 @@ def bench_cfg3(L, steps=128, prompt_len=512):
         model.close()
         return {"decode_tokens_per_s": round(tok_s, 1), "ms_per_token": round(secs * 1e3 / steps, 4),
                 "bytes_per_token": round(weights + kv), "hbm_gb_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM, 4),
-                "prefill": pre[0] if pre else None}
+                "prefill": pre[0] if pre else None, "parity": parity}
     finally:
         os.remove(path)
+
+
+def bench_fast_attention(L, path, spec, prompt, steps, context, fx):
+    """The same decode with LlamaOptions::fast_attention (attention on the
+    matrix cores, not the reference's f32 order): tokens/s over `steps`
+    greedy steps from the same prompt, its attention launch at the roofline
+    entry's shape, and how many of its ids equal the oracle's (the int8
+    activations carry any last-bit change on, so they part after a while)."""
+    model = L.Llama(path, context, kv_f16=True, fast_attention=True)
+    try:
+        first = int(np.argmax(model.forward(prompt)))
+        model.generate_greedy(first, 8)
+        model.rewind(len(prompt))
+        L.synchronize()
+        t0 = time.perf_counter()
+        tokens = model.generate_greedy(first, steps)
+        secs = time.perf_counter() - t0
+    finally:
+        model.close()
+    att_us, att_bytes, shape = time_attention_step(spec, len(prompt), ROOFLINE_STEPS, fast=True)
+    out = {"tokens_per_s": round(steps / secs, 2), "ms_per_step": round(secs * 1e3 / steps, 4),
+           "attention_launch_us": round(att_us, 3), "attention_gb_s": round(att_bytes / (att_us * 1e-6) / 1e9, 1),
+           "attention_frac": round(att_bytes / (att_us * 1e-6) / 1e9 / PEAK_HBM, 4), "shape": shape}
+    if fx is not None:
+        ids = [int(t) for t in fx["ids"][1:steps + 1]]
+        differ = [i for i, (a, b) in enumerate(zip(tokens, ids)) if int(a) != b]
+        out["ids_equal_to_oracle"] = len(ids) - len(differ)
+        out["first_difference"] = differ[0] if differ else None
+    log(f"fast attention: {out['tokens_per_s']} tokens/s; attention launch {att_us:.2f} us; "
+        f"ids equal to the oracle's: {out.get('ids_equal_to_oracle')} of {steps}")
+    return out
+
+
+def bench_long_position(L, path, spec, position=32696, steps=64):
+    """The cfg5 model decoding at positions 32696..32760 (Llama::advance to
+    the position: the cache rows below hold zeros, which costs the same to
+    attend over), with the exact and the matrix-core attention: the step at
+    a 32k context."""
+    out = {"positions": [position, position + steps]}
+    for fast in (False, True):
+        model = L.Llama(path, position + steps + 8, kv_f16=True, fast_attention=fast)
+        try:
+            model.advance(position)
+            model.generate_greedy(3, 8)
+            model.rewind(position)
+            L.synchronize()
+            t0 = time.perf_counter()
+            model.generate_greedy(3, steps)
+            secs = time.perf_counter() - t0
+        finally:
+            model.close()
+        weights, kv_pos, _ = algorithmic_bytes(spec)
+        step_bytes = weights + kv_pos * (position + (steps + 1) / 2)
+        key = "matrix_core" if fast else "exact"
+        out[key] = {"tokens_per_s": round(steps / secs, 1), "hbm_gb_s": round(step_bytes * steps / secs / 1e9, 1)}
+        log(f"cfg5 decode at positions {position}..{position + steps} ({key} attention): {steps / secs:.1f} tokens/s")
+    return out
 
 
 def bench_short_position(L, path, contexts=(1024, 32768), prompt_len=512, steps=64):
@@ -559,6 +667,7 @@ def main():
         logits = model.forward(prompt)
         log(f"prefill {args.prompt} tokens in {time.time() - t0:.1f} s")
         first = int(np.argmax(logits))
+        prompt_logits = logits.copy()
 
         # Warm-up, then rewind so the timed steps see positions 4096.. as configured.
         if args.warmup:
@@ -601,13 +710,20 @@ def main():
         for r in sorted(rows, key=lambda r: -r["calls"] * r["avg_us"])[:14]:
             log(f"  {r['kernel']:<28} calls {r['calls']:>6}  avg {r['avg_us']:9.2f} us  {r['gb_s'] or '':>8} GB/s")
         busy_ms = sum(ms for _, _, ms in prof) / args.profile_steps if args.profile_steps else None
-        att_us, att_bytes, att_shape = time_attention_step(spec, args.prompt, args.steps)
+        att_us, att_bytes, att_shape = time_attention_step(spec, args.prompt, ROOFLINE_STEPS)
         att_rate = att_bytes / (att_us * 1e-6) / 1e9
         log(f"attend_step_fused (chunks, merge, o GEMV + residual) back to back at position {att_shape['position']}: "
             f"{att_us:.2f} us a launch, {att_rate:.0f} GB/s")
         gu_us, gu_bytes = time_gate_up(spec)
         gu_rate = gu_bytes / (gu_us * 1e-6) / 1e9
         log(f"gemv_fused (norm + gate/up + swiglu + q8_0) back to back: {gu_us:.2f} us a launch, {gu_rate:.0f} GB/s")
+
+        headline = args.prompt == PROMPT and not args.layers
+        fx_parity = against_fixture(fixture("cfg5"), prompt_logits, first, tokens) if headline else None
+        if fx_parity:
+            log(f"against the oracle's own run: prompt logits {'bit-identical' if fx_parity['prompt_logits_bit_identical'] else 'DIFFER'}, "
+                f"{fx_parity['timed_ids_equal']} of {fx_parity['timed_ids_checked']} timed ids equal")
+        fast = bench_fast_attention(L, path, spec, prompt, args.steps, context, fixture("cfg5") if headline else None)
 
         pre = prefill_rates(model, spec, prompt, args.prefill, L) if args.prefill else None
 
@@ -650,10 +766,12 @@ def main():
             model.close()
             model = None
             configs["cfg5_short_position"] = bench_short_position(L, path)
+            configs["cfg5_long_position"] = bench_long_position(L, path, spec)
             configs["cfg3"] = bench_cfg3(L)
 
         gu_traffic = GATE_UP_TRAFFIC if sources_hash() == GATE_UP_TRAFFIC_SOURCES else None
-        att_traffic = ATTEND_TRAFFIC if ATTEND_TRAFFIC and sources_hash(ATTEND_FILES) == ATTEND_TRAFFIC_SOURCES else None
+        att_traffic = (ATTEND_TRAFFIC if ATTEND_TRAFFIC and sources_hash(ATTEND_FILES) == ATTEND_TRAFFIC_SOURCES
+                       and att_shape["position"] == ATTEND_TRAFFIC_POSITION else None)
         result = {
             "metric": "batch-1 decode tokens/s + achieved HBM GB/s (% of 8 TB/s), 1xMI355X",
             "value": round(tok_s, 2),
@@ -690,7 +808,9 @@ def main():
                                  "traffic_sources": sources_hash(),
                                  "bytes_per_launch": round(gu_bytes), "avg_launch_us": round(gu_us, 3)},
             "cpu_baseline": cpu,
-            "parity": parity,
+            "parity": (fx_parity["all_equal"] if fx_parity else parity) if parity is not False else False,
+            "parity_detail": {"oracle_fixture": fx_parity, "cpu_baseline_tokens_equal": parity},
+            "fast_attention": fast,
             "prefill": pre,
             "configs": configs,
             "tokens_head": [int(t) for t in tokens[:8]],

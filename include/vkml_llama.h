@@ -85,6 +85,10 @@ int vkml_llama_generate_greedy(vkml_llama* model, int32_t first, int64_t count, 
 /* Llama::reset and rewind (llama.hpp:171-177). *out gets the position. */
 int vkml_llama_reset(vkml_llama* model);
 int vkml_llama_rewind(vkml_llama* model, int64_t position, int64_t* out);
+/* Llama::advance: moves the sequence forward to position without running
+ * the tokens between (their KV rows keep what they hold). No reference
+ * counterpart: for benchmarks and tests that time steps at a position. */
+int vkml_llama_advance(vkml_llama* model, int64_t position);
 /* Layer l's KV caches [kv_heads, context_length, head_dim] copied to the
  * host (element size 2 for an f16 cache, 4 for f32). */
 int vkml_llama_read_kv_cache(const vkml_llama* model, int64_t layer, void* k_out, void* v_out, uint64_t bytes);

@@ -66,6 +66,9 @@ SHAPES = [
     (32, 4, 128, 0, 2048, 2048),
     (32, 32, 128, 7, 999, 1000),
     (24, 8, 64, 0, 333, 400),
+    # past 64 chunks the merge takes two levels (segments of 32 chunks)
+    (8, 2, 64, 5, 9000, 9100),
+    (32, 8, 128, 0, 20000, 20000),
 ]
 
 

@@ -186,6 +186,26 @@ def test_forward_all_reset_rewind_and_errors(files):
     same(one[0], ref.forward(tokens[:1]))
 
 
+def test_advance_keeps_the_rows_it_skips(files):
+    """Llama::advance moves the position without running tokens: rows a
+    rewind left behind still hold the prompt's keys and values, so the next
+    step equals the oracle's straight run."""
+    path = files["q4k"]
+    tokens = np.random.default_rng(12).integers(0, 1000, 8).astype(np.int32)
+    m = Llama(path, 16, kv_f16=True)
+    ref = O.Model(path, 16, kv_f16=True)
+    m.forward(tokens[:6])
+    ref.forward(tokens[:6])
+    assert m.rewind(2) == 2
+    m.advance(6)
+    assert m.position == 6
+    same(m.forward(tokens[6:7]), ref.forward(tokens[6:7]))
+    with pytest.raises(VkmlError, match="cannot advance to position 3 from 7"):
+        m.advance(3)
+    with pytest.raises(VkmlError, match="in a context of 16"):
+        m.advance(17)
+
+
 def test_graphs_and_eager_steps_agree_exactly(files):
     path = files["q4k"]
     tokens = np.random.default_rng(10).integers(0, 1000, 10).astype(np.int32)

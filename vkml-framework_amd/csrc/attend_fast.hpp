@@ -37,6 +37,8 @@ using namespace vkml::dev;
 using vkml::attend::kThreads;
 
 constexpr uint32_t kItemKeys = 128;  // keys of an item: four waves of 32
+constexpr uint32_t kSegment = 32;    // chunks a first-level merge takes (two-level merges)
+constexpr uint32_t kOneLevel = 64;   // chunks one merge takes alone
 constexpr uint32_t kWaveKeys = 32;
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -53,9 +55,15 @@ struct FastArgs {
     uint32_t heads, kv_heads, group, capacity, kv_start, kv_len, chunks;
     float scale, softcap;
     uint32_t ready;  // chunks live at every position of the launch: their loads go before the position is read
-    // Arrival counters, one per KV head, kArriveStride words apart (zero
-    // before the launch; the last item of a KV head resets its counter).
+    // Arrival counters, kArriveStride words apart (zero before the launch;
+    // the last arrival resets each): one per KV head, then with segs > 1
+    // one per (KV head, segment of kSegment chunks).
     uint32_t* arrive;
+    // 1: the last item of a KV head merges its chunks. More: the last item
+    // of each segment merges the segment's chunks, and the last of those
+    // merges the segments (long contexts, where one workgroup walking every
+    // chunk would take longer than the items).
+    uint32_t segs;
     // The merged output [heads, hd] f32 (may be null), its Q8_0 codes and f32 scales (may be null).
     float* out;
     uint8_t* values;
@@ -254,38 +262,43 @@ __device__ __forceinline__ void fast_item(const FastArgs& a, uint32_t chunk, uin
     }
 }
 
-// The merge of KV head kvh's heads over chunks 0 .. live - 1: out = sum_c
-// 2^(m_c - M) partial_c / sum_c 2^(m_c - M) l_c, and its Q8_0 (quantize.comp's
-// rule: d = absmax / 127, codes rne(x / d) clamped), stored coherently.
-// Thread t takes four consecutive elements of a head and every S-th chunk
-// (S = kThreads / (GQ hd / 4)); the S parts meet in LDS (xch: 6 kThreads
+// A merge of KV head kvh's heads over the partials in chunk slots first,
+// first + stride, ... (count of them): F = sum_c 2^(m_c - M) partial_c and
+// L = sum_c 2^(m_c - M) l_c with M the largest m_c. With to_slot >= 0 the
+// result is a partial itself (F, and (M, L)), stored in that chunk slot
+// (a two-level merge's first level); otherwise the output out = F / L and
+// its Q8_0 (quantize.comp's rule: d = absmax / 127, codes rne(x / d)
+// clamped). Everything is stored coherently. Thread t takes four
+// consecutive elements of a head and every S-th of the slots (S =
+// kThreads / (GQ hd / 4)); the S parts meet in LDS (xch: 6 kThreads
 // floats). Called by every thread of the workgroup.
 template <int HD, int GQ, uint32_t B = 18>
-__device__ __forceinline__ void fast_merge(const FastArgs& a, uint32_t kvh, uint32_t live, float* xch) {
+__device__ __forceinline__ void fast_merge(const FastArgs& a, uint32_t kvh, uint32_t first, uint32_t count, uint32_t stride,
+                                           int32_t to_slot, float* xch) {
     constexpr uint32_t V4 = GQ * HD / 4;  // float4 groups of the outputs
     constexpr uint32_t S = kThreads / V4;
     static_assert(S >= 1 && kThreads % V4 == 0, "an output group per thread");
     const uint32_t t = thread_index(), vec = t % V4, part = t / V4;
     const uint32_t h = 4 * vec / HD, d = 4 * vec % HD;
     const bool mine = h < a.group;
-    const uint64_t first = static_cast<uint64_t>(kvh * a.group + (mine ? h : 0)) * a.chunks;
-    const float4* pp = reinterpret_cast<const float4*>(a.partial + first * HD + d);
-    const uint64_t* sp = reinterpret_cast<const uint64_t*>(a.stats) + first;
+    const uint64_t row = static_cast<uint64_t>(kvh * a.group + (mine ? h : 0)) * a.chunks;  // the head's slot 0
+    const float4* pp = reinterpret_cast<const float4*>(a.partial + row * HD + d);
+    const uint64_t* sp = reinterpret_cast<const uint64_t*>(a.stats) + row;
     float M = -__builtin_inff(), L = 0.0f;
     float4 F = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t c0 = part; c0 < live; c0 += S * B) {
+    for (uint32_t j0 = part; j0 < count; j0 += S * B) {
         float4 pv[B];
         uint64_t st[B];
 #pragma unroll
         for (uint32_t b = 0; b < B; ++b) {
-            const uint32_t c = min(c0 + S * b, live - 1);
+            const uint64_t c = first + static_cast<uint64_t>(min(j0 + S * b, count - 1)) * stride;
             st[b] = ld_u64<true>(sp + c);
-            pv[b] = ld_f32x4<true>(pp + static_cast<uint64_t>(c) * (HD / 4));
+            pv[b] = ld_f32x4<true>(pp + c * (HD / 4));
         }
         float mb = M;
 #pragma unroll
         for (uint32_t b = 0; b < B; ++b)
-            if (c0 + S * b < live) mb = fmaxf(mb, __uint_as_float(static_cast<uint32_t>(st[b])));
+            if (j0 + S * b < count) mb = fmaxf(mb, __uint_as_float(static_cast<uint32_t>(st[b])));
         const float r = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(M - mb);
         F.x *= r; F.y *= r; F.z *= r; F.w *= r;
         L *= r;
@@ -293,7 +306,7 @@ __device__ __forceinline__ void fast_merge(const FastArgs& a, uint32_t kvh, uint
 #pragma unroll
         for (uint32_t b = 0; b < B; ++b) {
             const float mc = __uint_as_float(static_cast<uint32_t>(st[b]));
-            const float f = c0 + S * b < live && mc != -__builtin_inff() ? __builtin_amdgcn_exp2f(mc - M) : 0.0f;
+            const float f = j0 + S * b < count && mc != -__builtin_inff() ? __builtin_amdgcn_exp2f(mc - M) : 0.0f;
             F.x += f * pv[b].x; F.y += f * pv[b].y; F.z += f * pv[b].z; F.w += f * pv[b].w;
             L += f * __uint_as_float(static_cast<uint32_t>(st[b] >> 32));
         }
@@ -320,6 +333,19 @@ __device__ __forceinline__ void fast_merge(const FastArgs& a, uint32_t kvh, uint
         }
     }
     if (part != 0) return;
+    if (to_slot >= 0) {
+        // a partial of the segment, in the slot of its first chunk
+        if (mine) {
+            const uint64_t at = row + static_cast<uint32_t>(to_slot);
+            float* o = a.partial + at * HD + d;
+            st_f32<true>(o, F.x); st_f32<true>(o + 1, F.y); st_f32<true>(o + 2, F.z); st_f32<true>(o + 3, F.w);
+            if (d == 0) {
+                st_f32<true>(a.stats + at * 2, M);
+                st_f32<true>(a.stats + at * 2 + 1, L);
+            }
+        }
+        return;
+    }
     const float inv_l = 1.0f / L;
     const float o[4] = {F.x * inv_l, F.y * inv_l, F.z * inv_l, F.w * inv_l};
     const uint64_t out_at = static_cast<uint64_t>(kvh * a.group + h) * HD + d;

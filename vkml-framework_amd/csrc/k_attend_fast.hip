@@ -33,6 +33,22 @@ struct FastLaunch {
 
 constexpr int kNoGemv = -1;
 
+// Waits for the workgroup's stores (written through, so visible to every
+// XCD), then adds it to counter c; true on every thread for the workgroup
+// that arrives last of `arrivals` (which resets the counter).
+__device__ __forceinline__ bool arrive_last(uint32_t* c, uint32_t arrivals) {
+    __shared__ uint32_t s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const bool last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == arrivals - 1;
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    return s_last != 0;
+}
+
 template <int HD, int GQ, int FMT, bool FULL, int DEEP>
 __global__ void __launch_bounds__(kThreads) k_attend_fast(FastArgs a, FastLaunch f, vkml::gemv::GemvArgs g) {
     extern __shared__ uint4 smem[];
@@ -64,19 +80,25 @@ __global__ void __launch_bounds__(kThreads) k_attend_fast(FastArgs a, FastLaunch
         if (!early) fast_load<HD>(a, chunk, kvh, n, ld, sm.v);
         fast_item<HD, GQ>(a, chunk, kvh, n, ld, sm);
     }
-    __shared__ uint32_t s_last;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the write-through stores have completed
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t* c = a.arrive + FusedSync::kArriveStride * kvh;
-        const bool last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.chunks - 1;
-        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
     const uint32_t live = min(a.chunks, (kv_len - a.kv_start + kItemKeys - 1) / kItemKeys);
-    fast_merge<HD, GQ>(a, kvh, live, reinterpret_cast<float*>(sm.v));
+    float* xch = reinterpret_cast<float*>(sm.v);
+    if (a.segs > 1) {
+        // First level: the segment's last item merges its live chunks into
+        // the slot of the segment's first chunk.
+        const uint32_t seg = chunk / kSegment;
+        if (!arrive_last(a.arrive + FusedSync::kArriveStride * (a.kv_heads + kvh * a.segs + seg), min(kSegment, a.chunks - seg * kSegment)))
+            return;
+        if (seg * kSegment < live) {
+            fast_merge<HD, GQ>(a, kvh, seg * kSegment, min(kSegment, live - seg * kSegment), 1, static_cast<int32_t>(seg * kSegment), xch);
+            __syncthreads();  // the exchange area is read before the next merge writes it
+        }
+        // Second level: the last segment merges the live segments.
+        if (!arrive_last(a.arrive + FusedSync::kArriveStride * kvh, a.segs)) return;
+        fast_merge<HD, GQ>(a, kvh, 0, (live + kSegment - 1) / kSegment, kSegment, -1, xch);
+    } else {
+        if (!arrive_last(a.arrive + FusedSync::kArriveStride * kvh, a.chunks)) return;
+        fast_merge<HD, GQ>(a, kvh, 0, live, 1, -1, xch);
+    }
     if (f.sync) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -129,6 +151,15 @@ bool launch_gq(const FastArgs& a, const FastLaunch& f, const vkml::gemv::GemvArg
     return full ? launch_as<HD, GQ, VKML_Q8_0, true, 0>(a, f, *g, gemv_wgs, dry) : launch_as<HD, GQ, VKML_Q8_0, false, 0>(a, f, *g, gemv_wgs, dry);
 }
 
+// Merge levels for `chunks` chunks of kv_heads KV heads: one up to
+// kOneLevel chunks, else segments of kSegment when the counters fit a sync
+// block.
+uint32_t merge_segments(uint32_t chunks, uint32_t kv_heads) {
+    if (chunks <= kOneLevel) return 1;
+    const uint32_t segs = (chunks + kSegment - 1) / kSegment;
+    return kv_heads * (1 + segs) <= FusedSync::kMaxSets ? segs : 1;
+}
+
 bool launch_fast(uint32_t hd, const FastArgs& a, const FastLaunch& f, const vkml::gemv::GemvArgs* g, uint32_t b_type, bool dry) {
     const bool wide = a.group > 4;
     if (hd == 128) return wide ? launch_gq<128, 8>(a, f, g, b_type, dry) : launch_gq<128, 4>(a, f, g, b_type, dry);
@@ -176,8 +207,8 @@ int vkml_attend_fast(const vkml_attend_params* p, const float* q, const void* k_
     VKML_CHECK_ARG(q && k_cache && v_cache && partial && stats && sync && (out || values), "attend_fast: null buffer");
     VKML_CHECK_ARG(!values || scales, "attend_fast: quantized output needs scales");
     const FastArgs a{q, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
-                     p->kv_start, p->kv_len, p->chunks, p->scale, p->softcap, 0, FusedSync::arrive(sync, 0), out,
-                     static_cast<uint8_t*>(values), scales};
+                     p->kv_start, p->kv_len, p->chunks, p->scale, p->softcap, 0, FusedSync::arrive(sync, 0),
+                     merge_segments(p->chunks, p->kv_heads), out, static_cast<uint8_t*>(values), scales};
     const FastLaunch f{p->chunks * p->kv_heads, nullptr, nullptr, nullptr, 0};
     vkml::abi::ProfileScope prof("attend_fast");
     launch_fast(p->head_dim, a, f, nullptr, 0, false);
@@ -191,7 +222,7 @@ int vkml_attend_step_fast_supported(const vkml_attend_step_params* p, const vkml
         return 0;
     if (!o_fusable(o, p->heads, p->head_dim)) return 0;
     const FastArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
-                     0, 0, p->chunks, p->scale, p->softcap, 0, nullptr, nullptr, nullptr, nullptr};
+                     0, 0, p->chunks, p->scale, p->softcap, 0, nullptr, 1, nullptr, nullptr, nullptr};
     const FastLaunch f{p->chunks * p->kv_heads, nullptr, nullptr, nullptr, 0};
     const vkml::gemv::GemvArgs g{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, o->n, o->k};
     return launch_fast(p->head_dim, a, f, &g, o->b_type, true) ? 1 : 0;
@@ -219,7 +250,7 @@ int vkml_attend_step_fast(const vkml_attend_step_params* p, const float* qkv, vo
     uint32_t* next = sync + static_cast<uint64_t>((block + 1) % blocks) * FusedSync::kWords;
     const FastArgs a{qkv, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
                      p->kv_start, 0, p->chunks, p->scale, p->softcap, std::min(p->ready_chunks, p->chunks), FusedSync::arrive(own, 0),
-                     out, static_cast<uint8_t*>(values), scales};
+                     merge_segments(p->chunks, p->kv_heads), out, static_cast<uint8_t*>(values), scales};
     const FastLaunch f{p->chunks * p->kv_heads, own, next, sync, vkml::abi::wait_limit()};
     const vkml::gemv::GemvArgs g{static_cast<const uint4*>(values), scales, o_values, o_scales, nullptr, nullptr, x, x, o->n, o->k};
     vkml::abi::ProfileScope prof("attend_fast");

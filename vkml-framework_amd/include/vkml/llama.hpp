@@ -124,6 +124,12 @@ public:
 
     void reset() noexcept;
     std::int64_t rewind(std::int64_t position);
+    // Moves the sequence forward to position (at most the context length)
+    // without running the tokens in between: the KV-cache rows of those
+    // positions keep what they hold (zeros in a fresh model, or an earlier
+    // sequence's keys and values). No counterpart in the reference: for
+    // benchmarks and tests that time decode steps at a given position.
+    std::int64_t advance(std::int64_t position);
     std::int64_t kv_cache_bytes() const noexcept;
 
     // The layer-l KV caches [kv_heads, context_length, head_dim], for tests.

@@ -48,6 +48,7 @@ SIGNATURES = {
     "vkml_llama_generate_greedy": (C.c_int, [vp, i32, i64, vp]),
     "vkml_llama_reset": (C.c_int, [vp]),
     "vkml_llama_rewind": (C.c_int, [vp, i64, P(i64)]),
+    "vkml_llama_advance": (C.c_int, [vp, i64]),
     "vkml_llama_read_kv_cache": (C.c_int, [vp, i64, vp, vp, u64]),
     "vkml_llama_set_profiling": (C.c_int, [i32]),
     "vkml_llama_profile": (C.c_int, [vp, u32, vp, vp, u32, P(u32)]),
@@ -156,6 +157,10 @@ class Llama:
         out = i64()
         _check(lib().vkml_llama_rewind(self._h, int(position), C.byref(out)))
         return int(out.value)
+
+    def advance(self, position: int) -> None:
+        """Llama::advance: skip to position without running the tokens between."""
+        _check(lib().vkml_llama_advance(self._h, int(position)))
 
     def read_kv_cache(self, layer: int):
         c = self.config

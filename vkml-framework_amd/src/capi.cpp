@@ -177,6 +177,13 @@ int vkml_llama_rewind(vkml_llama* m, int64_t position, int64_t* out) {
     });
 }
 
+int vkml_llama_advance(vkml_llama* m, int64_t position) {
+    return guarded([&] {
+        if (!m) throw vkml::Error("vkml_llama_advance: null model");
+        (void)m->model.advance(position);
+    });
+}
+
 int vkml_llama_read_kv_cache(const vkml_llama* m, int64_t layer, void* k_out, void* v_out, uint64_t bytes) {
     return guarded([&] {
         if (!m) throw vkml::Error("vkml_llama_read_kv_cache: null model");

@@ -1027,6 +1027,17 @@ std::int64_t Llama::rewind(std::int64_t position) {
     return position;
 }
 
+std::int64_t Llama::advance(std::int64_t position) {
+    Impl& m = *impl_;
+    if (position < m.position || position > m.context_length) {
+        throw Error("Llama::advance: cannot advance to position " + std::to_string(position) + " from " + std::to_string(m.position) +
+                    " in a context of " + std::to_string(m.context_length));
+    }
+    m.position = position;
+    m.ran_to(position);
+    return position;
+}
+
 std::int64_t Llama::kv_cache_bytes() const noexcept {
     std::int64_t bytes = 0;
     for (const auto& L : impl_->layers) bytes += std::int64_t(L.k_cache.nbytes() + L.v_cache.nbytes());

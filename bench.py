@@ -312,9 +312,20 @@ def roofline_only(spec):
     att_us, att_bytes, shape = time_attention_step(spec, rounds=1)
     log(f"attend_step_fused at position {shape['position']}: {att_us:.2f} us a launch, "
         f"{att_bytes / (att_us * 1e-6) / 1e9:.0f} GB/s ({att_bytes} algorithmic bytes)")
+    fast_us, _, _ = time_attention_step(spec, rounds=1, fast=True)
+    log(f"attend_step_fast at position {shape['position']}: {fast_us:.2f} us a launch, "
+        f"{att_bytes / (fast_us * 1e-6) / 1e9:.0f} GB/s")
     dom_us, dom_bytes = time_gate_up(spec, layers=32, rounds=1)
     log(f"gemv_fused gate/up: {dom_us:.2f} us a launch, {dom_bytes / (dom_us * 1e-6) / 1e9:.0f} GB/s "
         f"({dom_bytes} algorithmic bytes)")
+    copy_256mib()
+
+
+def copy_256mib():
+    """hipMemcpy device to device of 256 MiB, three times: the runtime's copy
+    kernel reads and writes exactly 268,435,456 bytes a dispatch, the known
+    size a hardware counter's reading is scaled by."""
+    from vkml_amd import hip as H
     n = 256 << 20
     src, dst = H.Buffer(n), H.Buffer(n)
     H.call("vkml_fill_u32", src.p, 0x01020304, n // 4)
@@ -403,7 +414,7 @@ def bench_gemv_cfg2(min_bytes=512 << 20):
     return out
 
 
-def bench_attention_cfg4(min_bytes=512 << 20):
+def bench_attention_cfg4(min_bytes=512 << 20, lengths=(4096, 16384, 32768)):
     """cfg4: decode attention of 32 query heads on 8 KV heads, head_dim 128,
     over f16 caches of T = 4096, 16384 and 32768 positions: the exact chunk
     pass and merge (vkml_attend + vkml_attend_merge), and the matrix-core
@@ -413,7 +424,7 @@ def bench_attention_cfg4(min_bytes=512 << 20):
     from vkml_amd import hip as H
     heads, kvh, hd = 32, 8, 128
     out = []
-    for T in (4096, 16384, 32768):
+    for T in lengths:
         cache = kvh * T * hd * 2
         copies = max(2, -(-min_bytes // (2 * cache)))
         caches = [(filled(cache, 0x3C003800 + i), filled(cache, 0x38003C00 + i)) for i in range(copies)]
@@ -636,6 +647,9 @@ def main():
                     help="run only the dominant kernel's timed launches and a 256 MiB device copy of known size, "
                          "for hardware-counter passes (FETCH_SIZE, WRITE_SIZE) that scale the kernel's HBM bytes "
                          "by what the copy reads")
+    ap.add_argument("--cfg4", type=int, nargs="+", default=None, metavar="POSITIONS",
+                    help="run only cfg4's attention at these cache lengths (4096 16384 32768) and the 256 MiB device "
+                         "copy, printing cfg4's JSON entries: the command the cfg4 profiles are taken with")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (every GPU box here has one). "
@@ -649,6 +663,12 @@ def main():
     spec = synth.CONFIGS["cfg5"]
     if args.roofline_only:
         roofline_only(spec)
+        return
+    if args.cfg4:
+        from vkml_amd import hip as H
+        H.init()
+        print(json.dumps({"cfg4_attention": bench_attention_cfg4(lengths=args.cfg4)}), flush=True)
+        copy_256mib()
         return
     if args.layers:
         spec = synth.ModelSpec(spec.name, args.layers, spec.hidden, spec.heads, spec.kv_heads, spec.head_dim, spec.ffn,

@@ -431,7 +431,10 @@ def test_gemv_rope_rejects_odd_rows():
 @pytest.mark.parametrize("hd,heads,kvh,kv_len,kv_type,extra", [
     (128, 32, 8, 4096, H.F16, 0), (128, 32, 8, 1, H.F16, 3), (64, 32, 8, 640, H.F16, 0),
     (64, 4, 2, 45, H.F32, 1), (128, 32, 8, 300, H.F32, 0), (256, 8, 8, 200, H.F16, 0), (128, 8, 1, 1000, H.F16, 2),
-    (256, 16, 2, 129, H.F32, 0), (64, 16, 4, 128, H.F16, 0), (64, 8, 2, 9000, H.F16, 0)])
+    (256, 16, 2, 129, H.F32, 0), (64, 16, 4, 128, H.F16, 0), (64, 8, 2, 9000, H.F16, 0),
+    # past 16 chunks the merge spreads over (head, 32-element slice) workgroups,
+    # past 256 in passes of 256 chunks; empty chunks among them
+    (128, 8, 2, 3000, H.F32, 20), (64, 8, 2, 40000, H.F16, 2), (256, 4, 4, 33000, H.F16, 0)])
 def test_attend_bit_exact(hd, heads, kvh, kv_len, kv_type, extra):
     cap = kv_len + 7
     rng = np.random.default_rng(kv_len)

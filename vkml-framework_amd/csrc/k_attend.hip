@@ -79,6 +79,109 @@ k_attend_merge(const float* partial, const float* stats, float* out, uint8_t* va
     merge_head<false, 48>(partial, stats, out, values, scales, blockIdx.x, chunks, chunks, hd, threadIdx.x, s_rl, s_wmax);
 }
 
+// The merge spread over (head, 32-element slice) workgroups:
+// attend_merge.comp:25-38 with merge_head's arithmetic, bit for bit. The
+// head's (max, weight sum) pairs are loaded by all 256 threads and M, each
+// chunk's factor r_c = exp(m_c - M) and weight product r_c l_c formed once
+// into LDS. The slice's partials are loaded 256 chunks a pass by 8 threads
+// an element (every load of a pass in flight at once), and those threads
+// form the products r_c partial_c (f32 products: the same wherever they
+// are rounded) into LDS. Lane e of wave 0 then adds element e's products in
+// chunk order, as merge_head's chain does (a chunk past the live keys adds
+// +0 * +0 there: nothing), and the slice (one Q8_0 block) is quantized
+// across those 32 lanes. Where merge_head's threads each load their
+// element's partials in turn and do every operation of the chain, here a
+// pass's loads and products come from every thread and the chain is two
+// additions a chunk.
+constexpr uint32_t kSlice = 32;       // elements a workgroup: one Q8_0 block
+constexpr uint32_t kMergePass = 256;  // chunks whose products are in LDS at once
+
+__global__ void __launch_bounds__(256)
+k_attend_merge_wide(const float* partial, const float* stats, float* out, uint8_t* values, float* scales, uint32_t chunks, uint32_t hd) {
+#pragma clang fp contract(off)
+    __shared__ float s_r[kMergeMaxChunks];   // r_c, or -1 for a chunk past the live keys
+    __shared__ float s_wp[kMergeMaxChunks];  // r_c l_c (+0 for such a chunk)
+    __shared__ float s_p[kMergePass][kSlice];
+    __shared__ float s_wmax[4];
+    const uint32_t t = threadIdx.x, slices = hd / kSlice;
+    const uint32_t h = blockIdx.x / slices, d0 = (blockIdx.x % slices) * kSlice;
+    const uint64_t first = static_cast<uint64_t>(h) * chunks;
+    const uint64_t* st = reinterpret_cast<const uint64_t*>(stats) + first;
+    const float* pc = partial + first * hd + d0;
+    const uint32_t e = t % kSlice, g = t / kSlice;  // loader: element e, chunks g, g + 8, ...
+    // The first pass's partials, in flight while M and the factors are formed.
+    constexpr uint32_t kPer = kMergePass / (256 / kSlice);  // 32 loads a thread a pass
+    float p[kPer];
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) p[j] = ldg(pc + static_cast<uint64_t>(min(g + 8 * j, chunks - 1)) * hd + e);
+    // M = max over the chunks' maxima (exact in any order)
+    float m = -__builtin_inff();
+    for (uint32_t c = t; c < chunks; c += 256) m = fmaxf(m, __uint_as_float(static_cast<uint32_t>(ldg(st + c))));
+    m = wave_max(m);
+    if (t % kWave == 0) s_wmax[t / kWave] = m;
+    __syncthreads();
+    const float top = fmaxf(fmaxf(s_wmax[0], s_wmax[1]), fmaxf(s_wmax[2], s_wmax[3]));
+    for (uint32_t c = t; c < chunks; c += 256) {
+        const uint64_t ml = ldg(st + c);
+        const float mc = __uint_as_float(static_cast<uint32_t>(ml)), lc = __uint_as_float(static_cast<uint32_t>(ml >> 32));
+        const float r = mc == -__builtin_inff() ? -1.0f : vk_expf(mc - top);
+        const uint32_t keep = r >= 0.0f ? ~0u : 0u;
+        const float rr = __uint_as_float(__float_as_uint(r) & keep);
+        s_r[c] = r;
+        s_wp[c] = rr * __uint_as_float(__float_as_uint(lc) & keep);
+    }
+    __syncthreads();
+    float sum = 0.0f, weight = 0.0f;
+    for (uint32_t c0 = 0; c0 < chunks; c0 += kMergePass) {
+        if (c0 > 0) {
+            __syncthreads();  // the previous pass's chain is done with s_p
+#pragma unroll
+            for (uint32_t j = 0; j < kPer; ++j) p[j] = ldg(pc + static_cast<uint64_t>(min(c0 + g + 8 * j, chunks - 1)) * hd + e);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j) {
+            const uint32_t c = min(c0 + g + 8 * j, chunks - 1);
+            const float r = s_r[c];
+            const uint32_t keep = r >= 0.0f ? ~0u : 0u;
+            s_p[g + 8 * j][e] = __uint_as_float(__float_as_uint(r) & keep) * __uint_as_float(__float_as_uint(p[j]) & keep);
+        }
+        __syncthreads();
+        if (t < kSlice) {
+            const uint32_t n = min(kMergePass, chunks - c0);
+            uint32_t j0 = 0;
+            for (; j0 + 8 <= n; j0 += 8) {
+                float pv[8], wv[8];
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) {
+                    pv[j] = s_p[j0 + j][e];
+                    wv[j] = s_wp[c0 + j0 + j];
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) {
+                    sum += pv[j];
+                    weight += wv[j];
+                }
+            }
+            for (; j0 < n; ++j0) {
+                sum += s_p[j0][e];
+                weight += s_wp[c0 + j0];
+            }
+        }
+    }
+    if (t < kSlice) {
+        const float o = sum / weight;
+        const uint64_t at = static_cast<uint64_t>(h) * hd + d0 + e;
+        if (out) out[at] = o;
+        if (values) {
+            const float absmax = group_max<32>(fabsf(o));
+            const float ds = absmax / 127.0f;
+            const float inv = ds > 0.0f ? 1.0f / ds : 0.0f;
+            values[at] = static_cast<uint8_t>(static_cast<int8_t>(quant_code(o, inv)));
+            if (e == 0) scales[at / 32] = ds;
+        }
+    }
+}
+
 template <int HD, bool F16>
 void launch_hd(const ChunkArgs& args, uint32_t pair_blocks) {
     hipStream_t s = vkml::abi::stream();
@@ -103,8 +206,14 @@ int launch_chunks(uint32_t head_dim, bool f16, const ChunkArgs& args) {
 
 int launch_merge(uint32_t heads, uint32_t head_dim, uint32_t chunks, const float* partial, const float* stats, float* out,
                  void* values, float* scales) {
-    hipLaunchKernelGGL(k_attend_merge, dim3(heads), dim3(head_dim), 0, vkml::abi::stream(), partial, stats, out,
-                       static_cast<uint8_t*>(values), scales, chunks, head_dim);
+    // Past a few chunks a head, its elements' partial loads are spread over
+    // (head, slice) workgroups; few chunks keep one workgroup a head.
+    if (chunks > 16)
+        hipLaunchKernelGGL(k_attend_merge_wide, dim3(heads * (head_dim / kSlice)), dim3(256), 0, vkml::abi::stream(), partial, stats,
+                           out, static_cast<uint8_t*>(values), scales, chunks, head_dim);
+    else
+        hipLaunchKernelGGL(k_attend_merge, dim3(heads), dim3(head_dim), 0, vkml::abi::stream(), partial, stats, out,
+                           static_cast<uint8_t*>(values), scales, chunks, head_dim);
     return VKML_OK;
 }
 

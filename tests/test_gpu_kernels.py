@@ -434,7 +434,9 @@ def test_gemv_rope_rejects_odd_rows():
     (256, 16, 2, 129, H.F32, 0), (64, 16, 4, 128, H.F16, 0), (64, 8, 2, 9000, H.F16, 0),
     # past 16 chunks the merge spreads over (head, 32-element slice) workgroups,
     # past 256 in passes of 256 chunks; empty chunks among them
-    (128, 8, 2, 3000, H.F32, 20), (64, 8, 2, 40000, H.F16, 2), (256, 4, 4, 33000, H.F16, 0)])
+    (128, 8, 2, 3000, H.F32, 20), (64, 8, 2, 40000, H.F16, 2), (256, 4, 4, 33000, H.F16, 0),
+    # four heads a chunk workgroup (GQA groups of 4 and 8, enough chunks)
+    (128, 16, 2, 40000, H.F16, 0), (128, 32, 8, 20000, H.F32, 1)])
 def test_attend_bit_exact(hd, heads, kvh, kv_len, kv_type, extra):
     cap = kv_len + 7
     rng = np.random.default_rng(kv_len)

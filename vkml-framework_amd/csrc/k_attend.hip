@@ -185,7 +185,13 @@ k_attend_merge_wide(const float* partial, const float* stats, float* out, uint8_
 template <int HD, bool F16>
 void launch_hd(const ChunkArgs& args, uint32_t pair_blocks) {
     hipStream_t s = vkml::abi::stream();
-    if (args.group % 2 == 0) {
+    // Four heads a workgroup (one K and V load for a whole GQA group of 4)
+    // where that still leaves two workgroups a compute unit: measured 17%
+    // faster at 32K keys, 6% slower at 4K (fewer items to spread).
+    if (args.group % 4 == 0 && static_cast<uint64_t>(pair_blocks) * kXcds * (args.group / 4) >= 2ull * vkml::abi::compute_units()) {
+        const dim3 grid(pair_blocks * kXcds * (args.group / 4));
+        hipLaunchKernelGGL((k_attend_chunk<HD, F16, 4>), grid, dim3(kThreads), 0, s, args);
+    } else if (args.group % 2 == 0) {
         const dim3 grid(pair_blocks * kXcds * (args.group / 2));
         hipLaunchKernelGGL((k_attend_chunk<HD, F16, 2>), grid, dim3(kThreads), 0, s, args);
     } else {

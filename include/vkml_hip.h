@@ -541,13 +541,16 @@ int vkml_attend_o_status(uint32_t* d_sync, uint32_t* flag);
  * bytes, zeroed before the first call; a call uses block `block` and
  * zeroes the counters of block (block + 1) % blocks, so consecutive calls
  * on the stream take consecutive blocks, cyclically (in a model, layer L
- * takes block L of one block per layer). Other shapes: the chunk pass, the
- * merge and vkml_gemv_dot_add as separate launches, with the same block
- * bookkeeping. p->chunks may cover fewer keys than the cache (a launch sized
- * for the position rather than the capacity): keys past kv_start + 128 *
- * chunks are then not attended, and a step whose position reaches them
- * raises the error vkml_attend_fused_check reports (the one launch only;
- * the separate launches need chunks covering the cache). */
+ * takes block L of one block per layer). Other shapes, and steps of more
+ * than 64 chunks (whose one-workgroup merges would outlast separate
+ * launches): the chunk pass, the merge (spread over (head, 32-element
+ * slice) workgroups) and vkml_gemv_dot_add as separate launches, with the
+ * same block bookkeeping. p->chunks may cover fewer keys than the cache (a
+ * launch sized for the position rather than the capacity): keys past
+ * kv_start + 128 * chunks are then not attended, and a step whose position
+ * reaches them raises the error vkml_attend_fused_check reports (the one
+ * launch, and steps of more than 64 chunks; the separate launches of other
+ * shapes need chunks covering the cache). */
 uint64_t vkml_attend_fused_sync_bytes(uint32_t blocks);
 int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* d_qkv, const float* d_rope_table,
                            void* d_k_cache, void* d_v_cache, float* d_partial, float* d_stats, float* d_out,
@@ -563,9 +566,13 @@ int vkml_attend_fused_check(uint32_t* d_sync, uint32_t blocks);
 int vkml_attend_fused_status(uint32_t* d_sync, uint32_t blocks, uint32_t* flag);
 /* 1 when vkml_attend_step_fused takes these shapes in its one launch on
  * this device (the o format, the item's LDS, the merge's chunk count and a
- * grid whose waiting o workgroups leave the chunk items a slot); 0 when it
- * would take the separate launches, which need p->chunks covering the
- * cache. No reference counterpart (a host-side plan query). */
+ * grid whose waiting o workgroups leave the chunk items a slot) at every
+ * chunk count up to min(p->chunks, 64); 0 when it would take the separate
+ * launches, which then need p->chunks covering the cache. Steps of more
+ * than 64 chunks always take the separate launches (the merge spread over
+ * many workgroups); those may be sized below the cache, and a position
+ * past their chunks sets the error flag as the one launch does. No
+ * reference counterpart (a host-side plan query). */
 int vkml_attend_step_fused_supported(const vkml_attend_step_params* p, const vkml_gemv_dot_params* o);
 
 /* Decode attention on the matrix cores, the tolerance form of

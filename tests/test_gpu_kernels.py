@@ -727,6 +727,55 @@ def test_attend_step_fused_reports_a_position_past_its_chunks():
                 H.call("vkml_attend_fused_check", p(fsync), 2)
 
 
+def test_attend_step_fused_long_steps_take_separate_launches():
+    # past 64 chunks a step runs the chunk pass, the spread merge and the o
+    # GEMV apart, bit for bit the one launch's results; a launch sized below
+    # the cache (128 chunks of a 134-chunk cache) serves positions up to its
+    # chunks and flags one past them, as the one launch does
+    hd, heads, kvh, n = 128, 32, 8, 4096
+    k, cap, chunks = heads * hd, 17100, 128
+    rng = np.random.default_rng(21)
+    prior = rng.standard_normal((2, kvh, cap, hd)).astype(np.float32)
+    caches = [prior[i].astype(np.float16).view(np.uint16) for i in range(2)]
+    kc, vc = dev(caches[0]), dev(caches[1])
+    table = O.rope_table(cap, hd, 1e6)
+    dtab = dev(table)
+    v, s_, quant, words, scales = weights(H.Q4_K, n, k, 23)
+    x0 = rng.standard_normal(n).astype(np.float32)
+    x = dev(x0)
+    fbytes = H.lib().vkml_attend_fused_sync_bytes(2)
+    fsync = H.empty(fbytes)
+    H.call("vkml_fill_u32", p(fsync), 0, fbytes // 4)
+    part, stats, st = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8), H.empty(16)
+    op = H.GemvDotParams(1, n, k, H.Q4_K, H.F16)
+    want_x = x0.copy()
+    for step, p_now in enumerate((12000, 16383)):
+        print(f"long fused step pos={p_now} chunks={chunks}", flush=True)
+        H.call("vkml_state_set", p(st), 0, p_now, 0)
+        qkv = rng.standard_normal((heads + 2 * kvh) * hd).astype(np.float32)
+        out, vals, scs = H.empty(k * 4), H.empty(k), H.empty(k // 32 * 4)
+        prm = H.AttendStepParams(heads, kvh, hd, cap, 0, 0, H.F16, chunks, 0, 1, 1.0 / math.sqrt(hd), 0.0, 0)
+        H.call("vkml_attend_step_fused", prm, p(dev(qkv)), p(dtab), p(kc), p(vc), p(part), p(stats), p(out), p(vals), p(scs),
+               p(st), op, p(v), p(s_), p(x), p(fsync), step % 2, 2)
+        H.call("vkml_attend_fused_check", p(fsync), 2)
+        q = O.rope(qkv[:k].reshape(1, heads, hd), table, p_now, 0).reshape(heads, hd)
+        kn = O.rope(qkv[k:k + kvh * hd].reshape(1, kvh, hd), table, p_now, 0).reshape(kvh, hd)
+        caches[0][:, p_now] = O.f32_to_f16(kn)
+        caches[1][:, p_now] = O.f32_to_f16(qkv[k + kvh * hd:].reshape(kvh, hd))
+        want = O.attend_decode(q, caches[0], caches[1], 0, p_now + 1)
+        assert np.array_equal(bits(out.download(np.float32, (heads, hd))), bits(want))
+        ww, ws = O.quantize(O.Q8_0, want.reshape(1, k), False)
+        assert np.array_equal(vals.download(np.uint32, ww.shape), ww)
+        want_x = want_x + O.gemv_dot(quant, ww, ws, 1, words, scales, n, k)[0]
+        assert np.array_equal(bits(x.download(np.float32, n)), bits(want_x))
+    H.call("vkml_state_set", p(st), 0, 16384, 0)
+    prm = H.AttendStepParams(heads, kvh, hd, cap, 0, 0, H.F16, chunks, 0, 1, 1.0 / math.sqrt(hd), 0.0, 0)
+    H.call("vkml_attend_step_fused", prm, p(dev(rng.standard_normal((heads + 2 * kvh) * hd).astype(np.float32))), p(dtab), p(kc),
+           p(vc), p(part), p(stats), p(out), p(vals), p(scs), p(st), op, p(v), p(s_), p(x), p(fsync), 0, 2)
+    with pytest.raises(H.VkmlError, match="past the keys of the launched chunks"):
+        H.call("vkml_attend_fused_check", p(fsync), 2)
+
+
 def test_attend_step_fused_rejects_bad_blocks():
     prm = H.AttendStepParams(8, 8, 64, 64, 0, 0, H.F16, 1, 0, 1, 0.125, 0.0, 0)
     op = H.GemvDotParams(1, 256, 512, H.Q4_K, H.F16)

@@ -58,6 +58,10 @@ struct ChunkArgs {
     // launch's items of these issue their q, K and V loads before reading
     // the position (prepared steps without a window).
     uint32_t ready;
+    // When non-null: the sticky error flag the chunk pass sets to 2 when the
+    // position lies past the keys of its chunks (a launch sized for fewer
+    // chunks than the cache holds), as the one-launch form does.
+    uint32_t* error;
 };
 
 // Sync words of the launch that merges the chunks and runs the o GEMV on

@@ -50,6 +50,8 @@ __global__ void __launch_bounds__(kThreads) k_attend_chunk(ChunkArgs a) {
     const uint32_t pos = a.step ? (a.state ? spos : a.position) : 0u;
     const uint32_t kv_len = a.step ? pos + 1 : (a.state ? spos + 1u : a.kv_len);
     if (a.window != 0 && kv_len > a.window) a.kv_start = max(a.kv_start, kv_len - a.window);
+    if (a.error && L == 0 && threadIdx.x == 0 && kv_len - a.kv_start > a.chunks * kChunk)
+        __hip_atomic_store(a.error, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (a.kv_start + chunk * kChunk >= kv_len) {
         // A chunk past the live keys (the grid covers the whole cache, so a
         // replayed graph serves every position): a max of -inf, which the
@@ -69,6 +71,14 @@ __global__ void __launch_bounds__(kThreads) k_attend_chunk(ChunkArgs a) {
 }
 
 constexpr uint32_t kMergeMaxChunks = 1024;  // 131072 keys
+// Chunks up to which a decode step's attention, merges and o GEMV run as one
+// launch (vkml_attend_step_fused). Its merges are one workgroup per head set
+// walking every chunk; the separate launches spread the merge. Measured at
+// the 7B shape (32 heads on 8 KV heads, q4_K o), one launch against apart:
+// 50 chunks 24.2 / 22.4 us, 66 chunks 27.1 / 28.2, 96 chunks 35.1 / 34.1,
+// 131 chunks 44.0 / 37.5, 256 chunks 70.5 / 52.6. Launches are sized in
+// power-of-two tiers of chunks, so the bound sits at a tier.
+constexpr uint32_t kFusedMaxChunks = 64;
 
 // The merge as its own launch: head blockIdx.x, element threadIdx.x.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -624,22 +634,26 @@ int vkml_attend_step_fused(const vkml_attend_step_params* p, const float* qkv, c
                    "attend_step_fused: the o projection must take the " + std::to_string(p->heads * p->head_dim) + " attention outputs");
     uint32_t* own = sync + static_cast<uint64_t>(block) * FusedSync::kWords;
     uint32_t* next = sync + static_cast<uint64_t>((block + 1) % blocks) * FusedSync::kWords;
-    const ChunkArgs args = step_args(p, qkv, rope_table, k_cache, v_cache, partial, stats, state, nullptr);
+    ChunkArgs args = step_args(p, qkv, rope_table, k_cache, v_cache, partial, stats, state, nullptr);
     const FusedArgs f{0, 0, own, next, sync, out, static_cast<uint8_t*>(values), scales, vkml::abi::wait_limit()};
     const vkml::gemv::GemvArgs g{static_cast<const uint4*>(values), scales, o_values, o_scales, nullptr, nullptr, x, x, o->n, o->k};
-    {
+    // Past kFusedMaxChunks chunks each head set's merge, one workgroup
+    // walking every chunk, outlasts launching it apart (spread over (head,
+    // slice) workgroups): those steps take the separate launches below,
+    // which report a position past their chunks on the same flag.
+    const bool long_merge = p->chunks > kFusedMaxChunks;
+    if (!long_merge) {
         vkml::abi::ProfileScope prof("attend_fused");
         if (launch_fused(p->head_dim, p->kv_type == VKML_F16, args, f, g, o->b_type, o->scale_type))
             return vkml::abi::check_launch("attend_step_fused");
-    }
-    // Shapes the one launch does not take: the chunk pass, the merge and the
-    // o GEMV (over every chunk of the cache); the next block's counters
-    // zeroed all the same.
-    {
+        // Shapes the one launch does not take: the chunk pass, the merge and
+        // the o GEMV over every chunk of the cache.
         const uint64_t span = p->window ? std::min<uint64_t>(p->window, p->capacity - p->kv_start) : p->capacity - p->kv_start;
         VKML_CHECK_ARG(static_cast<uint64_t>(p->chunks) * kChunk >= span,
                        "attend_step_fused: these weights take separate launches, which need chunks covering the cache");
     }
+    // The separate launches; the next block's counters zeroed all the same.
+    args.error = sync;
     {
         vkml::abi::ProfileScope prof("attend_step");
         launch_chunks(p->head_dim, p->kv_type == VKML_F16, args);
@@ -659,7 +673,11 @@ int vkml_attend_step_fused_supported(const vkml_attend_step_params* p, const vkm
         p->chunks > kMergeMaxChunks || (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256) ||
         (p->kv_type != VKML_F16 && p->kv_type != VKML_F32))
         return 0;
-    const ChunkArgs args = step_args(p, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+    // (past kFusedMaxChunks a step takes the separate launches: the one
+    // launch is asked for the largest count it serves)
+    vkml_attend_step_params q = *p;
+    q.chunks = std::min(q.chunks, kFusedMaxChunks);
+    const ChunkArgs args = step_args(&q, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
     const FusedArgs f{0, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
     const vkml::gemv::GemvArgs g{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, o->n, o->k};
     return launch_fused(p->head_dim, p->kv_type == VKML_F16, args, f, g, o->b_type, o->scale_type, true) ? 1 : 0;

@@ -67,11 +67,11 @@ PROMPT = 4096
 # kernel sources it was taken on: its hash is the SHA-256 (first 16 hex
 # digits) of those files, and the line reports no traffic when they have
 # changed since.
-GATE_UP_TRAFFIC = 67_605_054
+GATE_UP_TRAFFIC = 67_530_123
 GATE_UP_TRAFFIC_SOURCES = "b8ec832d8172fb19"
 TRAFFIC_FILES = ("vkml-framework_amd/csrc/gemv.hpp", "vkml-framework_amd/csrc/k_gemv.hip", "vkml-framework_amd/csrc/device.hpp")
-ATTEND_TRAFFIC = 28_573_079
-ATTEND_TRAFFIC_SOURCES = "d1520404944f2028"
+ATTEND_TRAFFIC = 28_572_130
+ATTEND_TRAFFIC_SOURCES = "c977512c9dd933cd"
 ATTEND_TRAFFIC_POSITION = 4224  # the launch's shape the figure was taken at (position; 35 chunks, 32 loading early)
 ATTEND_FILES = ("vkml-framework_amd/csrc/k_attend.hip", "vkml-framework_amd/csrc/attend.hpp", "vkml-framework_amd/csrc/gemv.hpp",
                 "vkml-framework_amd/csrc/device.hpp")

@@ -496,14 +496,21 @@ def bench_cfg3(L, steps=128, prompt_len=512):
 
 
 def bench_fast_attention(L, path, spec, prompt, steps, context, fx):
-    """The same decode with LlamaOptions::fast_attention (attention on the
-    matrix cores, not the reference's f32 order): tokens/s over `steps`
+    """The same run with LlamaOptions::fast_attention (attention on the
+    matrix cores, not the reference's f32 order): the prompt's prefill time
+    (its attention by vkml_attend_prompt_fast), tokens/s over `steps`
     greedy steps from the same prompt, its attention launch at the roofline
     entry's shape, and how many of its ids equal the oracle's (the int8
     activations carry any last-bit change on, so they part after a while)."""
     model = L.Llama(path, context, kv_f16=True, fast_attention=True)
     try:
-        first = int(np.argmax(model.forward(prompt)))
+        model.forward(prompt)  # warm
+        model.rewind(0)
+        L.synchronize()
+        t0 = time.perf_counter()
+        first = int(np.argmax(model.forward(prompt)))  # the prompt's attention on the matrix cores too
+        L.synchronize()
+        prefill_s = time.perf_counter() - t0
         model.generate_greedy(first, 8)
         model.rewind(len(prompt))
         L.synchronize()
@@ -514,6 +521,7 @@ def bench_fast_attention(L, path, spec, prompt, steps, context, fx):
         model.close()
     att_us, att_bytes, shape = time_attention_step(spec, len(prompt), ROOFLINE_STEPS, fast=True)
     out = {"tokens_per_s": round(steps / secs, 2), "ms_per_step": round(secs * 1e3 / steps, 4),
+           "prefill": {"tokens": len(prompt), "ms": round(prefill_s * 1e3, 2), "tokens_per_s": round(len(prompt) / prefill_s, 1)},
            "attention_launch_us": round(att_us, 3), "attention_gb_s": round(att_bytes / (att_us * 1e-6) / 1e9, 1),
            "attention_frac": round(att_bytes / (att_us * 1e-6) / 1e9 / PEAK_HBM, 4), "shape": shape}
     if fx is not None:
@@ -521,7 +529,8 @@ def bench_fast_attention(L, path, spec, prompt, steps, context, fx):
         differ = [i for i, (a, b) in enumerate(zip(tokens, ids)) if int(a) != b]
         out["ids_equal_to_oracle"] = len(ids) - len(differ)
         out["first_difference"] = differ[0] if differ else None
-    log(f"fast attention: {out['tokens_per_s']} tokens/s; attention launch {att_us:.2f} us; "
+    log(f"fast attention: prefill of {len(prompt)} tokens {prefill_s * 1e3:.1f} ms; {out['tokens_per_s']} tokens/s; "
+        f"attention launch {att_us:.2f} us; "
         f"ids equal to the oracle's: {out.get('ids_equal_to_oracle')} of {steps}")
     return out
 

@@ -609,6 +609,33 @@ int vkml_attend_step_fast(const vkml_attend_step_params* p, const float* d_qkv, 
  * workgroups leave the chunk items a slot); 0 otherwise. */
 int vkml_attend_step_fast_supported(const vkml_attend_step_params* p, const vkml_gemv_dot_params* o);
 
+/* A prompt's causal attention on the matrix cores: the tolerance form of
+ * the reference's chunked q.k^T, causal softmax and probs.v
+ * (attention.cpp:127-138,205-226; softmax.comp's soft cap), f32 attention
+ * within f32 rounding, online over blocks of keys (not the reference's
+ * order of f32 operations). d_q [heads, t, head_dim] f32 (rotated, heads
+ * first, as vkml_rope_kv_prompt leaves it); the caches [kv_heads,
+ * capacity, head_dim] f16 hold keys 0 .. first + t - 1 at rows of the same
+ * number; query i sees keys 0 .. first + i. d_out [t, heads, head_dim] f32:
+ * the o projection's input rows (no permute after it). head_dim 64 or 128,
+ * a multiple of 4 query heads a KV head. No reference counterpart as one
+ * call. */
+typedef struct vkml_attend_prompt_params {
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t capacity;
+    uint32_t t;      /* queries */
+    uint32_t first;  /* key position of query 0 */
+    uint32_t kv_type;
+    float scale;
+    float softcap;   /* 0: none */
+} vkml_attend_prompt_params;
+int vkml_attend_prompt_fast(const vkml_attend_prompt_params* p, const float* d_q, const void* d_k_cache, const void* d_v_cache,
+                            float* d_out);
+/* 1 when vkml_attend_prompt_fast takes these shapes. */
+int vkml_attend_prompt_fast_supported(const vkml_attend_prompt_params* p);
+
 /* vkml_attend_step without the d_partial / d_stats workspace, allocating
  * nothing: no counterpart in the reference. For callers that cannot call
  * hipMalloc (code under HIP graph capture, tight serving loops, harnesses

@@ -199,3 +199,68 @@ def test_fast_step_reports_a_position_past_its_chunks():
     with pytest.raises(H.VkmlError, match="past the keys"):
         H.call("vkml_attend_fused_check", sync.p, 2)
     H.synchronize()
+
+
+def prompt_attention_f64(q, kc, vc, first, group, softcap=0.0):
+    """float64 causal attention of a prompt: query i sees keys 0 .. first + i."""
+    heads, t, hd = q.shape
+    k = kc.view(np.float16).astype(np.float64)
+    v = vc.view(np.float16).astype(np.float64)
+    out = np.empty((t, heads, hd))
+    keys = first + t
+    mask = np.arange(keys)[None, :] > (first + np.arange(t))[:, None]
+    for h in range(heads):
+        s = q[h].astype(np.float64) @ k[h // group, :keys].T / math.sqrt(hd)
+        if softcap:
+            s = softcap * np.tanh(np.clip(s / softcap, -10.0, 10.0))
+        s[mask] = -np.inf
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p @ v[h // group, :keys]) / p.sum(axis=1, keepdims=True)
+    return out
+
+
+PROMPT_SHAPES = [
+    # (heads, kv_heads, hd, first, t, capacity)
+    (32, 8, 128, 0, 1, 64),
+    (32, 8, 128, 0, 17, 64),
+    (32, 8, 128, 0, 300, 512),
+    (32, 8, 128, 100, 64, 200),
+    (8, 2, 64, 0, 1000, 1024),
+    (16, 2, 128, 5, 130, 200),
+    (32, 8, 128, 0, 2048, 2048),
+]
+
+
+@pytest.mark.parametrize("shape", PROMPT_SHAPES)
+@pytest.mark.parametrize("softcap", [0.0, 30.0])
+def test_prompt_fast_attention_within_bound_of_f64(shape, softcap):
+    """vkml_attend_prompt_fast against float64 causal attention, under the
+    same bound as the decode form (every product exact, sums in f32)."""
+    H.init()
+    heads, kvh, hd, first, t, cap = shape
+    print(f"attend_prompt_fast shape {shape} softcap {softcap}", flush=True)
+    rng = np.random.default_rng(11 + t + first + hd)
+    q = rng.standard_normal((heads, t, hd)).astype(np.float32)
+    kc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
+    prm = H.AttendPromptParams(heads, kvh, hd, cap, t, first, H.F16, 1.0 / math.sqrt(hd), softcap)
+    assert H.lib().vkml_attend_prompt_fast_supported(prm) == 1
+    dq, dk, dv, out = H.to_device(q), H.to_device(kc), H.to_device(vc), H.empty(t * heads * hd * 4)
+    H.call("vkml_attend_prompt_fast", prm, dq.p, dk.p, dv.p, out.p)
+    got = out.download(np.float32, (t, heads, hd))
+    want = prompt_attention_f64(q, kc, vc, first, heads // kvh, softcap)
+    err = within(got, want, np.abs(vc.view(np.float16)).max(), f"shape {shape}")
+    print(f"max |err| {err:.3g}", flush=True)
+    H.synchronize()
+
+
+def test_prompt_fast_attention_rejects_what_it_does_not_take():
+    H.init()
+    for prm, msg in ((H.AttendPromptParams(32, 8, 128, 64, 65, 0, H.F16, 0.1, 0.0), "do not fit"),
+                     (H.AttendPromptParams(32, 8, 128, 64, 8, 0, H.F32, 0.1, 0.0), "f16"),
+                     (H.AttendPromptParams(12, 4, 128, 64, 8, 0, H.F16, 0.1, 0.0), "multiple of 4"),
+                     (H.AttendPromptParams(32, 8, 256, 64, 8, 0, H.F16, 0.1, 0.0), "64 or 128")):
+        assert H.lib().vkml_attend_prompt_fast_supported(prm) == 0
+        b = H.empty(1 << 16)
+        with pytest.raises(H.VkmlError, match=msg):
+            H.call("vkml_attend_prompt_fast", prm, b.p, b.p, b.p, b.p)

@@ -81,8 +81,9 @@ def test_headline_exact_matches_the_oracle_bit_for_bit(models, cfg):
 
 @pytest.mark.parametrize("cfg", ["cfg5", "cfg3"])
 def test_headline_fast_attention_within_tolerance(models, cfg):
-    """Decode steps fed the oracle's ids (so one step's choice does not
-    steer the next). The matrix-core attention's outputs are within f32
+    """The prompt, then decode steps fed the oracle's ids (so one step's
+    choice does not steer the next), with every attention on the matrix
+    cores. The matrix-core attention's outputs are within f32
     rounding of the exact ones (tests/test_gpu_attend_fast.py), but a
     last-bit change upstream of an int8 activation quantizer moves codes,
     and the model carries that forward: the oracle itself, with its
@@ -97,8 +98,15 @@ def test_headline_fast_attention_within_tolerance(models, cfg):
     _, n, steps = RUNS[cfg]
     print(f"{cfg} fast attention: prompt {n}, {steps} steps", flush=True)
     gpu = Llama(models[cfg], n + steps + 1, kv_f16=True, fast_attention=True)
+    # the prompt too runs its attention on the matrix cores (vkml_attend_prompt_fast)
     got = gpu.forward(prompt_of(cfg))
-    assert np.array_equal(got.view(np.uint32), fx["prompt_logits"].view(np.uint32)), "prompt logits (exact path)"
+    want = fx["prompt_logits"]
+    big = float(np.max(np.abs(want)))
+    err = float(np.max(np.abs(got - want)))
+    assert err <= 0.3 * big, f"prompt logits off by {err:.3g}, above 30% of the largest ({big:.3g})"
+    top2 = np.sort(want)[-2:]
+    assert int(np.argmax(got)) == fx["ids"][0] or top2[1] - top2[0] <= 2 * err, "prompt argmax"
+    print(f"{cfg} fast attention: prompt logits within {err / big:.3g} of the largest", flush=True)
     ids = fx["ids"]
     worst, differ = 0.0, []
     for i in range(steps):

@@ -153,7 +153,13 @@ __device__ __forceinline__ void fast_item(const FastArgs& a, uint32_t chunk, uin
         const float x[8] = {r.q[s][0].x, r.q[s][0].y, r.q[s][0].z, r.q[s][0].w, r.q[s][1].x, r.q[s][1].y, r.q[s][1].z, r.q[s][1].w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float v = x[e] * qs;
+            // The f32 product through an empty asm: both terms come from
+            // this one value. Otherwise the compiler folds f16(x qs) into one
+            // rounding (v_fma_mixlo_f16) for the residual while the packed
+            // operand rounds the f32 product, and where the two differ by an
+            // f16 ulp the residual belongs to another high term.
+            float v = x[e] * qs;
+            asm volatile("" : "+v"(v));
             qh[s][e] = static_cast<_Float16>(v);
             ql[s][e] = static_cast<_Float16>(v - static_cast<float>(qh[s][e]));
         }

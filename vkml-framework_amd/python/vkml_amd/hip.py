@@ -68,6 +68,9 @@ AttendStepParams = _struct("AttendStepParams", [("heads", u32), ("kv_heads", u32
                                                 ("kv_start", u32), ("position", u32), ("kv_type", u32), ("chunks", u32),
                                                 ("rope_style", u32), ("rotate", u32), ("scale", f32), ("softcap", f32),
                                                 ("window", u32), ("prepared", u32), ("ready_chunks", u32)])
+AttendPromptParams = _struct("AttendPromptParams", [("heads", u32), ("kv_heads", u32), ("head_dim", u32), ("capacity", u32),
+                                                    ("t", u32), ("first", u32), ("kv_type", u32), ("scale", f32),
+                                                    ("softcap", f32)])
 GemvRopeParams = _struct("GemvRopeParams", [("n", u32), ("k", u32), ("b_type", u32), ("scale_type", u32), ("eps", f32),
                                             ("row0", u32), ("heads", u32), ("kv_heads", u32), ("head_dim", u32),
                                             ("capacity", u32), ("kv_type", u32), ("rotate", u32)])
@@ -137,6 +140,8 @@ SIGNATURES = {
     "vkml_attend_o_status": [vp, P(u32)],
     "vkml_set_wait_limit": [u32],
     "vkml_attend_step_fused_supported": [P(AttendStepParams), P(GemvDotParams)],
+    "vkml_attend_prompt_fast": [P(AttendPromptParams), vp, vp, vp, vp],
+    "vkml_attend_prompt_fast_supported": [P(AttendPromptParams)],
     "vkml_attend_fast": [P(AttendParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "vkml_attend_step_fast": [P(AttendStepParams), vp, vp, vp, vp, vp, vp, vp, vp, vp, P(GemvDotParams), vp, vp, vp, vp, u32, u32],
     "vkml_attend_step_fast_supported": [P(AttendStepParams), P(GemvDotParams)],

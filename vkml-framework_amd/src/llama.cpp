@@ -707,8 +707,20 @@ struct Llama::Impl {
                       "rope_kv");
                 tag("attention");
             };
-            Tensor attn;
-            if (!L.slides) {
+            Tensor attn, merged;
+            // With fast_attention, the prompt's attention on the matrix cores
+            // (vkml_attend_prompt_fast), written in the o projection's rows.
+            const vkml_attend_prompt_params pp{u32(heads), u32(c.num_kv_heads), u32(hd), u32(L.rows), u32(t), u32(position),
+                                               detail::type_code(L.k_cache.dtype()), 1.0f / std::sqrt(static_cast<float>(hd)),
+                                               c.attn_logit_softcap};
+            if (!L.slides && options.fast_attention && vkml_attend_prompt_fast_supported(&pp) == 1) {
+                Tensor q = f32({heads, t, hd});
+                rope_kv(0, t, q);
+                merged = f32({t, qd});
+                check(vkml_attend_prompt_fast(&pp, static_cast<const float*>(q.data()), L.k_cache.data(), L.v_cache.data(),
+                                              static_cast<float*>(merged.data())),
+                      "attention");
+            } else if (!L.slides) {
                 Tensor q = f32({heads, t, hd});
                 rope_kv(0, t, q);
                 attn = detail::attention_prompt(q, L.k_cache, L.v_cache, end, true, 0, c.attn_logit_softcap, detail::kMaxScoreBytes,
@@ -726,7 +738,7 @@ struct Llama::Impl {
                     q0 += rows;
                 }
             }
-            const Tensor merged = permute(attn, {1, 0, 2}).reshape({t, qd});
+            if (!merged.numel()) merged = permute(attn, {1, 0, 2}).reshape({t, qd});
             const Rows m_in = rows_of(merged, t, qd, int_dot && quantized_input(L.o) && qd % 32 == 0);
             project_rows(L.o, m_in, t, yp, "o");
             check(vkml_binary(0, u32(t * d), u32(t * d), xp, yp, xp), "add");

@@ -28,8 +28,14 @@
 // kernel that loads each block's 8-byte operands from memory, whose waves
 // spent twice their issue time waiting for them); the small tiles load
 // operands straight from memory (L2 serves the reuse across workgroups).
-// The scaling costs 4 VALU operations per output and block, 6 with
-// offsets; the matrix instructions are idle most of the time.
+// The scaling costs 4 VALU operations per output and block (the offset
+// formats' six folded into four, as block_term says), and it bounds the
+// kernel: a SIMD issues a wave64 f32 VALU instruction about every 4
+// cycles (measured 33.7 T lane-operations a second for fma, 36.8 T for mul,
+// 38.7 T for add over the GPU), so 4 operations per output and block cap
+// the kernel near 9 T outputs x blocks a second, about 580 TOP/s of the
+// int8 products (11.6% of the int8 peak); the matrix instructions are idle
+// most of the time.
 #include <algorithm>
 
 #include "../../include/vkml_hip.h"
@@ -125,6 +131,50 @@ __device__ __forceinline__ void q4k_block_scale(const uint4& h, uint32_t j, floa
 
 constexpr uint32_t kChunk = 8;  // blocks of K a chunk (a q4_K super-block)
 
+// The offset formats with f16 scales (q4_K, q4_1 with f16 scales) take the
+// reference's six scaling operations, cvt, mul, mul, add, mul, add, as
+// four: fma, fma, mul, add, with every result bit for bit the same.
+//  - The matrix instruction starts its accumulator at the int32 bits of the
+//    f32 1.5 * 2^23, so each block sum comes out as the bits of the f32
+//    1.5 * 2^23 + sum, exactly (|sum| <= 32 * 128 * 15 < 2^22). Then
+//    fma(that, sb, -1.5 * 2^23 * sb) forms the exact sum * sb and rounds it
+//    once: float(sum) * sb, with no conversion. -1.5 * 2^23 * sb is exact
+//    because sb is an f16 value (11 significant bits, 13 after the 3).
+//  - asum * ob is exact (|asum| <= 32 * 128 = 2^12 has at most 12
+//    significant bits, ob is an f16 value, and the smallest nonzero
+//    product, 2^-24, is a normal f32), so fma(asum, ob, x) rounds x +
+//    asum * ob once, as the reference's add of the rounded product does.
+// Signs of zero can differ in the intermediate (an exact zero sum is +0,
+// not -0 * sb), but no accumulator starting at +0 ever sees the
+// difference: +0 + -0 is +0, and a nonzero accumulator ignores both.
+constexpr int32_t kSumBiasBits = 0x4B400000;  // the f32 1.5 * 2^23
+constexpr float kSumBias = 12582912.0f;
+
+template <int FMT, bool F16S>
+constexpr bool kFoldScaling = FMT == VKML_Q4_K || (FMT == VKML_Q4_1 && F16S);
+
+template <int FMT, bool F16S>
+__device__ __forceinline__ v4i sum_start() {
+    constexpr int32_t b = kFoldScaling<FMT, F16S> ? kSumBiasBits : 0;
+    return v4i{b, b, b, b};
+}
+
+// One output's contribution of one block, sa (sum sb + asum ob) or
+// sum (sa sb) (matmul_dot.comp:155-160), from the matrix instruction's
+// result d (biased where the scaling folds; nsb = -1.5 * 2^23 * sb).
+template <int FMT, bool F16S>
+__device__ __forceinline__ float block_term(int32_t d, float sa, float asum, float sb, float nsb, float ob) {
+#pragma clang fp contract(off)
+    if constexpr (kFoldScaling<FMT, F16S>) {
+        const float x = __builtin_fmaf(__builtin_bit_cast(float, d), sb, nsb);
+        return sa * __builtin_fmaf(asum, ob, x);
+    } else if constexpr (FMT == VKML_Q4_1 || FMT == VKML_Q4_K) {
+        return sa * (static_cast<float>(d) * sb + asum * ob);
+    } else {
+        return static_cast<float>(d) * (sa * sb);
+    }
+}
+
 // One kernel per per-wave tile: RT row tiles of 16 by CT column tiles of
 // 16; a workgroup's four waves take 4 CT column tiles side by side, so its
 // tile is 16 RT x 64 CT.
@@ -202,10 +252,11 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
             for (int r = 0; r < RT; ++r) av[r] = static_cast<long>(__builtin_bit_cast(uint64_t, ldg(reinterpret_cast<const uint2*>(arow[r] + blk * 32))));
 #pragma unroll
             for (int c = 0; c < CT; ++c) bv[c] = b_codes<FMT>(p, bcol[c], blk, g);
-            float sb[CT], ob[CT];
+            float sb[CT], nsb[CT], ob[CT];
 #pragma unroll
             for (int c = 0; c < CT; ++c) {
                 sb[c] = s_sb[buf][b][16 * CT * wave + 16 * c + li];
+                nsb[c] = -kSumBias * sb[c];
                 ob[c] = 0.0f;
                 if constexpr (kOffset) ob[c] = s_ob[buf][b][16 * CT * wave + 16 * c + li];
             }
@@ -217,15 +268,9 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
                 const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, asum[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
                 for (int c = 0; c < CT; ++c) {
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], sum_start<FMT, F16S>(), 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if constexpr (kOffset) {
-                            acc[r][c][i] += sa[i] * (static_cast<float>(d[i]) * sb[c] + asum[i] * ob[c]);
-                        } else {
-                            acc[r][c][i] += static_cast<float>(d[i]) * (sa[i] * sb[c]);
-                        }
-                    }
+                    for (int i = 0; i < 4; ++i) acc[r][c][i] += block_term<FMT, F16S>(d[i], sa[i], asum[i], sb[c], nsb[c], ob[c]);
                 }
             }
         }
@@ -398,6 +443,40 @@ __global__ void __launch_bounds__(kT) k_matmul_dot_staged(MatmulDotArgs p) {
         for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[r][c][i] = 0.0f;
+    // A block's matrix instructions (RT x 2 of them) into d.
+    const auto sums = [&](uint32_t b, v4i (&d)[RT][2]) {
+        long av[RT], bv[2];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) av[r] = *reinterpret_cast<const long*>(l.a + (16 * r + li) * S::kAStride + b * 32 + 8 * g);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) bv[c] = staged_b<FMT, F16S, RT>(l, 32 * wave + 16 * c + li, b, g);
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) d[r][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], sum_start<FMT, F16S>(), 0, 0, 0);
+    };
+    // A block's scaling of d into the accumulators, in the reference's order.
+    const auto scale = [&](uint32_t b, const v4i (&d)[RT][2]) {
+        float sb[2], nsb[2], ob[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            sb[c] = l.sb[b][32 * wave + 16 * c + li];
+            nsb[c] = -kSumBias * sb[c];
+            ob[c] = 0.0f;
+            if constexpr (kOffset) ob[c] = l.ob[b][32 * wave + 16 * c + li];
+        }
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const float4 sa4 = *reinterpret_cast<const float4*>(&l.sa[b][16 * r + 4 * g]);
+            float4 as4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if constexpr (kOffset) as4 = *reinterpret_cast<const float4*>(&l.asum[b][16 * r + 4 * g]);
+            const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, asum[4] = {as4.x, as4.y, as4.z, as4.w};
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[r][c][i] += block_term<FMT, F16S>(d[r][c][i], sa[i], asum[i], sb[c], nsb[c], ob[c]);
+        }
+    };
     StagedChunk<FMT, F16S, RT> next;
     staged_load<FMT, F16S, RT>(p, t, 0, row0, col0, next);
     for (uint32_t c0 = 0; c0 < blocks; c0 += kChunk) {
@@ -408,37 +487,9 @@ __global__ void __launch_bounds__(kT) k_matmul_dot_staged(MatmulDotArgs p) {
 #pragma unroll
         for (uint32_t b = 0; b < kChunk; ++b) {
             if (c0 + b >= blocks) break;
-            long av[RT], bv[2];
-#pragma unroll
-            for (int r = 0; r < RT; ++r) av[r] = *reinterpret_cast<const long*>(l.a + (16 * r + li) * S::kAStride + b * 32 + 8 * g);
-#pragma unroll
-            for (int c = 0; c < 2; ++c) bv[c] = staged_b<FMT, F16S, RT>(l, 32 * wave + 16 * c + li, b, g);
-            float sb[2], ob[2];
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                sb[c] = l.sb[b][32 * wave + 16 * c + li];
-                ob[c] = 0.0f;
-                if constexpr (kOffset) ob[c] = l.ob[b][32 * wave + 16 * c + li];
-            }
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                const float4 sa4 = *reinterpret_cast<const float4*>(&l.sa[b][16 * r + 4 * g]);
-                float4 as4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if constexpr (kOffset) as4 = *reinterpret_cast<const float4*>(&l.asum[b][16 * r + 4 * g]);
-                const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w}, asum[4] = {as4.x, as4.y, as4.z, as4.w};
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r], bv[c], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if constexpr (kOffset) {
-                            acc[r][c][i] += sa[i] * (static_cast<float>(d[i]) * sb[c] + asum[i] * ob[c]);
-                        } else {
-                            acc[r][c][i] += static_cast<float>(d[i]) * (sa[i] * sb[c]);
-                        }
-                    }
-                }
-            }
+            v4i d[RT][2];
+            sums(b, d);
+            scale(b, d);
         }
     }
 #pragma unroll
@@ -466,10 +517,10 @@ void launch_tiles(const MatmulDotArgs& p) {
 // SIMDs half a wave each; below that, the largest direct-load tile that
 // still gives them about two waves each. (Measured: the staged tiles win
 // from 512 of their waves on; a 512-token cfg5 prompt's projections take
-// 21.6 ms with 32 x 128 tiles against 27.3 ms with 64 x 128, a 4096-token
-// prompt's 140 ms against 146 ms the other way round; at 128 rows x 14336
-// columns the 32 x 32 tile beats 64 x 32 with half the waves and 32 x 16
-// with twice as many.)
+// 19.1 ms with 32 x 128 tiles against 23.3 ms with 64 x 128, a 4096-token
+// prompt's 116-124 ms either way, the 64 x 128 tile ahead in most runs; at
+// 128 rows x 14336 columns the 32 x 32 tile beats 64 x 32 with half the
+// waves and 32 x 16 with twice as many.)
 template <int FMT, bool F16S>
 void launch(const MatmulDotArgs& p) {
     const auto waves = [&](uint64_t rt, uint64_t ct) { return ((p.m + 16 * rt - 1) / (16 * rt)) * ((p.n + 16 * ct - 1) / (16 * ct)); };

@@ -180,6 +180,70 @@ def test_gemv_dot_several_rows_in_one_launch(fmt, m, n, k):
         assert np.array_equal(bits(one.download(np.float32, n)), bits(got[i]))
 
 
+def edge_activation(m, k, seed):
+    """Q8_0 rows whose blocks take the folded scaling's corner cases: all
+    +127 and all -127 codes (the largest block sums), all-zero blocks (a
+    zero scale and zero sums), blocks of alternating +-127 (a zero code sum
+    whose dot products can also be zero), and random blocks."""
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    kind = rng.integers(0, 5, size=(m, k // 32))
+    for r in range(m):
+        for b in range(k // 32):
+            blk = a[r, 32 * b:32 * b + 32]
+            if kind[r, b] == 0:
+                blk[:] = 0.75
+            elif kind[r, b] == 1:
+                blk[:] = -1.5
+            elif kind[r, b] == 2:
+                blk[:] = 0.0
+            elif kind[r, b] == 3:
+                blk[:] = np.where(np.arange(32) % 2 == 0, 0.5, -0.5)
+    words, scales = O.quantize(O.Q8_0, a, False)
+    return words, scales
+
+
+@pytest.mark.parametrize("fmt", [H.Q4_K, H.Q4_1])
+@pytest.mark.parametrize("m,n,k", [(20, 64, 512), (512, 1024, 256), (2048, 4096, 256)])
+def test_matmul_dot_folded_scaling_corner_cases(fmt, m, n, k):
+    # q4_K and q4_1 with f16 scales take the folded scaling (the block sum
+    # biased by 1.5 * 2^23 in the matrix instruction's accumulator, two
+    # fmas): bit for bit the reference's six operations, including negative
+    # and zero (+0 and -0) scales and offsets, whole blocks of code 15 and
+    # of code 0, the largest block sums and exact zero sums (where -0 * sb
+    # and +0 differ in the intermediate). The shapes take the direct-load
+    # kernel and both staged tiles.
+    rng = np.random.default_rng(m + n + k)
+    if fmt == H.Q4_K:
+        blocks = synth.q4_k_blocks(rng, n * k // 256)
+        sel = rng.integers(0, 8, size=len(blocks))
+        blocks[sel == 0, 1] |= 0x80                # d < 0: every sub-block scale negative
+        blocks[sel == 1, 3] |= 0x80                # dmin < 0: offsets positive
+        blocks[sel == 2, 0:2] = 0                   # d = +0
+        blocks[sel == 3, 0:2] = [0x00, 0x80]        # d = -0
+        blocks[sel == 4, 16:] = 0xFF                # every code 15
+        blocks[sel == 5, 16:] = 0x00                # every code 0
+        blocks[sel == 6, 4:16] = 0                  # sub-block scales and mins 0
+        codes, hdr = q4k_layout(blocks, n, k)
+        quant, words, scales = O.load_quantized(O.GGML_Q4_K, blocks.tobytes(), n, k)
+        v, s = dev(codes), dev(hdr)
+    else:
+        w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+        quant = O.Q4_1
+        words, scales = O.quantize(quant, w, True)
+        sel = rng.integers(0, 6, size=scales.size)
+        scales[sel == 0] |= 0x8000                  # negative scales and offsets
+        scales[sel == 1] = 0x0000
+        scales[sel == 2] = 0x8000
+        v, s = dev(words), dev(scales)
+    aw, asc = edge_activation(m, k, m * 7 + k)
+    out = H.empty(m * n * 4)
+    H.call("vkml_matmul_dot", H.GemvDotParams(m, n, k, fmt, H.F16), p(dev(aw)), p(v), p(out), p(s), p(dev(asc)))
+    got = out.download(np.float32, (m, n))
+    want = O.matmul_dot(quant, aw, asc, m, words, scales, n, k)
+    assert np.array_equal(bits(got), bits(want))
+
+
 @pytest.mark.parametrize("fmt", [H.Q8_0, H.Q4_0, H.Q4_1])
 def test_gemv_dot_f32_scales_and_several_rows(fmt):
     n, k, m = 300, 512, 3

@@ -204,7 +204,7 @@ def edge_activation(m, k, seed):
 
 
 @pytest.mark.parametrize("fmt", [H.Q4_K, H.Q4_1])
-@pytest.mark.parametrize("m,n,k", [(20, 64, 512), (512, 1024, 256), (2048, 4096, 256)])
+@pytest.mark.parametrize("m,n,k", [(20, 64, 512), (256, 2048, 256), (512, 4096, 256), (2048, 4096, 256)])
 def test_matmul_dot_folded_scaling_corner_cases(fmt, m, n, k):
     # q4_K and q4_1 with f16 scales take the folded scaling (the block sum
     # biased by 1.5 * 2^23 in the matrix instruction's accumulator, two
@@ -212,7 +212,7 @@ def test_matmul_dot_folded_scaling_corner_cases(fmt, m, n, k):
     # and zero (+0 and -0) scales and offsets, whole blocks of code 15 and
     # of code 0, the largest block sums and exact zero sums (where -0 * sb
     # and +0 differ in the intermediate). The shapes take the direct-load
-    # kernel and both staged tiles.
+    # kernel and the 16-, 32- and 64-row staged tiles.
     rng = np.random.default_rng(m + n + k)
     if fmt == H.Q4_K:
         blocks = synth.q4_k_blocks(rng, n * k // 256)
@@ -264,9 +264,10 @@ def test_matmul_dot_bit_exact(fmt, f16, m, n, k):
     # matmul_dot.comp's order (the reference's int8 product for m > 8) on the
     # matrix cores, against the oracle bit for bit, and within the f32 dot
     # bound of the exact product; ragged tiles at m = 9, 37, 130, 250 and
-    # n = 100, 1000, 16400, 4100. The shapes take every kernel: operands
-    # from memory at 16 x 16 a wave (the first three), operands staged in
-    # LDS at 64 x 32 (512, 64 and 250 rows) and 32 x 32 (100 rows).
+    # n = 100, 1000, 16400, 4100. Operands from memory (the first three),
+    # staged in LDS in 32-row tiles (512 and 250 rows) and 16-row tiles (64
+    # and 100 rows); the 64-row staged tile takes the 2048 rows of
+    # test_matmul_dot_folded_scaling_corner_cases.
     v, s, quant, words, scales = weights(fmt, n, k, m + n, f16_scales=f16)
     a, aw, asc = activation(k, m, m)
     out = H.empty(m * n * 4)

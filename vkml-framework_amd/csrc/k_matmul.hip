@@ -288,16 +288,18 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
         }
 }
 
-// The 64 x 128 tile with its operands staged in LDS: per 8-block chunk the
-// workgroup copies the chunk's A rows (64 x 256 bytes) and B columns (128 x
-// 128 bytes, 256 for q8_0) with 16-byte loads, a chunk ahead in registers,
-// and the matrix instructions read their operands from LDS. Each thread's
-// A bytes are two blocks of one row, so it also sums their codes.
+// The 16 RT x 128 tile with its operands staged in LDS: per 8-block chunk
+// the workgroup copies the chunk's A rows (16 RT x 256 bytes) and B columns
+// (128 x 128 bytes, 256 for q8_0) with 16-byte loads, a chunk ahead in
+// registers, and the matrix instructions read their operands from LDS. Each
+// staging thread's A bytes are whole blocks of one row (two at RT = 4, one
+// below; at RT = 1 half the threads stage A), so it also sums their codes.
 template <int FMT, bool F16S, int RT>
 struct StagedChunk {
     static constexpr bool kOffset = FMT == VKML_Q4_1 || FMT == VKML_Q4_K;
-    static constexpr uint32_t TM = 16 * RT;      // rows of the tile
-    static constexpr uint32_t kABlocks = RT / 2;  // a thread's A blocks (of one row)
+    static constexpr uint32_t TM = 16 * RT;                   // rows of the tile
+    static constexpr uint32_t kABlocks = RT >= 2 ? RT / 2 : 1;  // a staging thread's A blocks (of one row)
+    static constexpr uint32_t kAThreads = TM * kChunk / kABlocks;  // threads that stage A
     static constexpr uint32_t kBBytes = FMT == VKML_Q8_0 ? 256 : 128;  // a column's bytes a chunk
     static constexpr uint32_t kAStride = 272, kBStride = kBBytes + 16;  // padded rows: no bank conflicts
     static constexpr uint32_t kBLoads = kBBytes * 128 / 16 / kT;        // 16-byte B loads a thread
@@ -325,7 +327,7 @@ __device__ __forceinline__ void staged_load(const MatmulDotArgs& p, uint32_t t, 
     using S = StagedChunk<FMT, F16S, RT>;
     constexpr uint32_t AB = S::kABlocks, kPerRow = kChunk / AB;  // threads a row
     const uint32_t blocks = p.k / 32;
-    {
+    if (S::kAThreads == kT || t < S::kAThreads) {
         // A: row t / kPerRow, blocks AB (t % kPerRow) .. of the chunk
         const uint32_t row = min(row0 + t / kPerRow, p.m - 1);
 #pragma unroll
@@ -371,7 +373,7 @@ __device__ __forceinline__ void staged_store(const StagedChunk<FMT, F16S, RT>& r
     using S = StagedChunk<FMT, F16S, RT>;
     constexpr bool kOffset = S::kOffset;
     constexpr uint32_t AB = S::kABlocks, kPerRow = kChunk / AB;
-    {
+    if (S::kAThreads == kT || t < S::kAThreads) {
         const uint32_t row = t / kPerRow;
 #pragma unroll
         for (uint32_t i = 0; i < 2 * AB; ++i)
@@ -514,13 +516,17 @@ void launch_tiles(const MatmulDotArgs& p) {
 // The 64 x 128 tile with its operands staged in LDS (2x the direct-load
 // kernel at large prompts) wherever it gives every CU about four
 // workgroups; below that the 32 x 128 staged tile, wherever it gives the
-// SIMDs half a wave each; below that, the largest direct-load tile that
-// still gives them about two waves each. (Measured: the staged tiles win
-// from 512 of their waves on; a 512-token cfg5 prompt's projections take
-// 19.1 ms with 32 x 128 tiles against 23.3 ms with 64 x 128, a 4096-token
-// prompt's 116-124 ms either way, the 64 x 128 tile ahead in most runs; at
-// 128 rows x 14336 columns the 32 x 32 tile beats 64 x 32 with half the
-// waves and 32 x 16 with twice as many.)
+// SIMDs two waves each; below that the 16 x 128 staged tile, wherever the
+// 32-row one would give them half a wave; below that, the largest
+// direct-load tile that still gives them about two waves each. (Measured:
+// the staged tiles win from 512 of their waves on; a 512-token cfg5
+// prompt's projections take 19.1 ms with 32 x 128 tiles against 23.3 ms
+// with 64 x 128, a 4096-token prompt's 116-124 ms either way, the 64 x 128
+// tile ahead in most runs; cfg3's 512-token q|k|v, o and down, one to one
+// and a half 32-row waves a SIMD, take 25.8, 20.6 and 74.0 us with 16-row
+// tiles against 29.9, 24.4 and 89.0 us; at 128 rows x 14336 columns the
+// 32 x 32 direct tile beats 64 x 32 with half the waves and 32 x 16 with
+// twice as many.)
 template <int FMT, bool F16S>
 void launch(const MatmulDotArgs& p) {
     const auto waves = [&](uint64_t rt, uint64_t ct) { return ((p.m + 16 * rt - 1) / (16 * rt)) * ((p.n + 16 * ct - 1) / (16 * ct)); };
@@ -528,9 +534,12 @@ void launch(const MatmulDotArgs& p) {
     if (waves(4, 2) >= 4096) {
         const dim3 grid((p.n + 127) / 128, (p.m + 63) / 64);
         hipLaunchKernelGGL((k_matmul_dot_staged<FMT, F16S, 4>), grid, dim3(kT), 0, vkml::abi::stream(), p);
-    } else if (waves(2, 2) >= 512) {
+    } else if (waves(2, 2) >= 2048) {
         const dim3 grid((p.n + 127) / 128, (p.m + 31) / 32);
         hipLaunchKernelGGL((k_matmul_dot_staged<FMT, F16S, 2>), grid, dim3(kT), 0, vkml::abi::stream(), p);
+    } else if (waves(2, 2) >= 512) {
+        const dim3 grid((p.n + 127) / 128, (p.m + 15) / 16);
+        hipLaunchKernelGGL((k_matmul_dot_staged<FMT, F16S, 1>), grid, dim3(kT), 0, vkml::abi::stream(), p);
     } else if (waves(2, 2) >= kEnough) launch_tiles<FMT, F16S, 2, 2>(p);
     else if (waves(2, 1) >= kEnough) launch_tiles<FMT, F16S, 2, 1>(p);
     else launch_tiles<FMT, F16S, 1, 1>(p);

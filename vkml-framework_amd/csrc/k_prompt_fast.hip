@@ -89,10 +89,15 @@ __global__ void __launch_bounds__(kThreads) k_attend_prompt_fast(PromptArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_v[2][kBlock * HD * 2];
     constexpr int kSteps = HD / 32;
     const uint32_t t = thread_index(), w = t / kWave, l = t % kWave, j = l % 16, g = l / 16;
-    // blockIdx.x: query tile; blockIdx.y: KV head and head quad
-    const uint32_t quads = a.group / kHeads;
-    const uint32_t kvh = blockIdx.y / quads, h = kvh * a.group + (blockIdx.y % quads) * kHeads + w;
-    const uint32_t q0 = blockIdx.x * kQueries;
+    // Workgroup L: (KV head, head quad) set L % sets, query tile from the
+    // last down. Workgroups are dealt to the 8 XCDs round-robin, so with 8
+    // (or a multiple of 8) sets each XCD serves the same KV heads and their
+    // K and V stay in its L2 (a KV head's 4096 keys are 2 MiB); the tiles
+    // whose queries see the most keys go first.
+    const uint32_t quads = a.group / kHeads, sets = a.kv_heads * quads, tiles = (a.t + kQueries - 1) / kQueries;
+    const uint32_t set = blockIdx.x % sets, tile = tiles - 1 - blockIdx.x / sets;
+    const uint32_t kvh = set / quads, h = kvh * a.group + (set % quads) * kHeads + w;
+    const uint32_t q0 = tile * kQueries;
     const uint32_t qi = q0 + j;                                      // the lane's query
     const bool qlive = qi < a.t;
     const uint32_t qpos = a.first + min(qi, a.t - 1);                // its position: keys 0 .. qpos
@@ -250,7 +255,7 @@ int vkml_attend_prompt_fast(const vkml_attend_prompt_params* p, const float* q, 
     VKML_CHECK_ARG(q && k_cache && v_cache && out, "attend_prompt_fast: null buffer");
     const PromptArgs a{q, k_cache, v_cache, out, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity, p->t, p->first,
                        p->scale, p->softcap};
-    const dim3 grid((p->t + kQueries - 1) / kQueries, p->kv_heads * (a.group / kHeads));
+    const dim3 grid((p->t + kQueries - 1) / kQueries * (p->kv_heads * (a.group / kHeads)));
     vkml::abi::ProfileScope prof("attend_prompt_fast");
     if (p->head_dim == 128)
         hipLaunchKernelGGL(k_attend_prompt_fast<128>, grid, dim3(kThreads), 0, vkml::abi::stream(), a);

@@ -12,16 +12,19 @@
 // A workgroup takes 16 queries of one KV head's four query heads, a wave a
 // head, and walks the keys its queries see in blocks of 32:
 //   - scores S^T [32 keys x 16 queries] = K . Q^T by
-//     v_mfma_f32_16x16x32_f16, K from memory into registers a block ahead,
-//     q (scaled into log2 units) as hi + lo f16 terms;
+//     v_mfma_f32_16x16x32_f16, K copied into LDS a block ahead by
+//     global_load_lds (each row's 16-byte pieces swizzled so that the 16
+//     rows of an operand read hit different banks), q (scaled into log2
+//     units) as hi + lo f16 terms;
 //   - per query (a lane column) the block's max and the running (max, sum),
 //     the accumulated output rescaled by 2^(m_old - m_new);
-//   - O^T [hd x 16 queries] += V^T . P^T, V copied into LDS a block ahead by
-//     global_load_lds (16-byte pieces swizzled so that the four lane groups
-//     of a read hit different banks), P^T straight from the score tile's
-//     registers (the accumulator layout of S^T is the B operand's of P^T,
-//     keys permuted alike in V^T's A operand). In O^T a query is a lane
-//     column, as in S^T, so its rescale needs no exchange between lanes.
+//   - O^T [hd x 16 queries] += V^T . P^T, V loaded a block ahead into
+//     registers and written into LDS transposed, [dim][key], so that a
+//     lane's operand is two 8-byte reads; P^T straight from the score
+//     tile's registers (the accumulator layout of S^T is the B operand's
+//     of P^T, keys permuted alike in V^T's A operand). In O^T a query is a
+//     lane column, as in S^T, so its rescale needs no exchange between
+//     lanes.
 // The output is written [query, head, hd]: the o projection's input rows.
 #include <algorithm>
 #include <string>
@@ -35,7 +38,6 @@ using vkml::attend::kThreads;
 using vkml::attend_fast::f32x4;
 using vkml::attend_fast::half8;
 using vkml::attend_fast::kLog2e;
-using vkml::attend_fast::v_offset;
 
 namespace {
 
@@ -52,41 +54,63 @@ struct PromptArgs {
     float scale, softcap;
 };
 
+// A block's tiles in LDS. K row-major, each row's 16-byte pieces swizzled
+// (piece p of key row r at p ^ (r % pieces)) so that the 16 rows a score
+// operand read takes hit different banks. V transposed, [dim][key] with
+// rows padded to 72 bytes, so that a lane's four keys of one dim are one
+// 8-byte read and the 16 dims of a read hit different banks.
 template <int HD>
-struct KRegs {
-    uint4 k[2][HD / 32];  // the block's two 16-key tiles, 8 f16 a lane a step
+struct PromptTiles {
+    static constexpr uint32_t kPieces = HD * 2 / 16;  // 16-byte pieces a key row
+    static constexpr uint32_t kVtStride = kBlock + 4;  // f16 a V^T row
+    alignas(16) uint8_t k[kBlock * HD * 2];
+    alignas(16) _Float16 vt[HD * kVtStride];
 };
 
-// Key block kb's K fragments (lane (j, g) of tile tt: key 16 tt + j, dims
-// 32 s + 8 g ..) and its V rows into LDS buffer `v` (the workgroup's 256
-// threads, 16 bytes each an instruction). Keys past `keys` re-read the last.
+// V of the next block in registers (8 dims of one key a 16-byte piece).
 template <int HD>
-__device__ __forceinline__ void load_block(const PromptArgs& a, uint32_t kvh, uint32_t kb, uint32_t keys, KRegs<HD>& r, uint8_t* v) {
+struct VRegs {
+    static constexpr uint32_t kLoads = kBlock * HD * 2 / 16 / kThreads;
+    uint4 v[kLoads];
+};
+
+// Key block kb's K rows into LDS (global_load_lds, swizzled) and its V rows
+// into registers. Keys past `keys` re-read the last.
+template <int HD>
+__device__ __forceinline__ void load_block(const PromptArgs& a, uint32_t kvh, uint32_t kb, uint32_t keys, PromptTiles<HD>& tl, VRegs<HD>& vr) {
+    using T = PromptTiles<HD>;
     constexpr uint32_t RB = HD * 2;
-    const uint32_t t = thread_index(), l = t % kWave, j = l % 16, g = l / 16;
+    const uint32_t t = thread_index(), wave_first = t - t % kWave;
     const uint64_t row0 = static_cast<uint64_t>(kvh) * a.capacity;
     const auto* kc = static_cast<const uint8_t*>(a.k_cache);
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const uint64_t row = row0 + min(kb * kBlock + 16 * tt + j, keys - 1);
-#pragma unroll
-        for (int s = 0; s < HD / 32; ++s) r.k[tt][s] = ldg(reinterpret_cast<const uint4*>(kc + row * RB + 64 * s + 16 * g));
-    }
     const auto* vc = static_cast<const uint8_t*>(a.v_cache);
-    const uint32_t wave_first = t - l;
 #pragma unroll
-    for (uint32_t i = 0; i < kBlock * RB / (16 * kThreads); ++i) {
-        const uint32_t at = 16 * (i * kThreads + t);  // byte in the block's rows
-        const uint32_t rr = at / RB, piece = (at % RB) / 16;
-        const uint32_t src_piece = piece ^ (2 * ((rr / 4) % 4));
+    for (uint32_t i = 0; i < VRegs<HD>::kLoads; ++i) {
+        const uint32_t u = i * kThreads + t, rr = u / T::kPieces, piece = u % T::kPieces;
         const uint64_t row = row0 + min(kb * kBlock + rr, keys - 1);
-        vkml::attend::load_to_lds16(vc + row * RB + 16 * src_piece, v + 16 * (i * kThreads + wave_first));
+        vkml::attend::load_to_lds16(kc + row * RB + 16 * (piece ^ (rr % T::kPieces)), tl.k + 16 * (i * kThreads + wave_first));
+        vr.v[i] = ldg(reinterpret_cast<const uint4*>(vc + row * RB + 16 * piece));
+    }
+}
+
+// The block's V from registers into its V^T tile.
+template <int HD>
+__device__ __forceinline__ void store_vt(const VRegs<HD>& vr, PromptTiles<HD>& tl) {
+    using T = PromptTiles<HD>;
+    const uint32_t t = thread_index();
+#pragma unroll
+    for (uint32_t i = 0; i < VRegs<HD>::kLoads; ++i) {
+        const uint32_t u = i * kThreads + t, key = u / T::kPieces, d0 = 8 * (u % T::kPieces);
+        const half8 x = __builtin_bit_cast(half8, vr.v[i]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tl.vt[(d0 + e) * T::kVtStride + key] = x[e];
     }
 }
 
 template <int HD>
 __global__ void __launch_bounds__(kThreads) k_attend_prompt_fast(PromptArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_v[2][kBlock * HD * 2];
+    using T = PromptTiles<HD>;
+    __shared__ T s_t[2];
     constexpr int kSteps = HD / 32;
     const uint32_t t = thread_index(), w = t / kWave, l = t % kWave, j = l % 16, g = l / 16;
     // Workgroup L: (KV head, head quad) set L % sets, query tile from the
@@ -105,8 +129,8 @@ __global__ void __launch_bounds__(kThreads) k_attend_prompt_fast(PromptArgs a) {
     const uint32_t blocks = (keys + kBlock - 1) / kBlock;
     const bool cap = a.softcap > 0.0f;
 
-    KRegs<HD> kr[2];
-    load_block<HD>(a, kvh, 0, keys, kr[0], s_v[0]);
+    VRegs<HD> vr;
+    load_block<HD>(a, kvh, 0, keys, s_t[0], vr);
     // q of the lane's query, scaled (in log2 units without a soft cap), as hi + lo f16
     half8 qh[kSteps], ql[kSteps];
     {
@@ -137,22 +161,25 @@ __global__ void __launch_bounds__(kThreads) k_attend_prompt_fast(PromptArgs a) {
     for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -__builtin_inff(), lsum = 0.0f;  // the lane's query: running max (log2 units) and sum
 
-    // One block: wait for its loads, issue the next block's (K into nxt, V
-    // into the other LDS buffer), then the scores, the online softmax and
-    // O^T. Blocks alternate between kr[0] and kr[1] (a pair a trip, so the
-    // registers are named statically).
-    const auto block = [&](uint32_t kb, const KRegs<HD>& kc, KRegs<HD>& nxt, const uint8_t* vb, uint8_t* vnext) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of block kb have landed
-        __syncthreads();                                   // every wave's; and block kb - 1's V is no longer read
-        if (kb + 1 < blocks) load_block<HD>(a, kvh, kb + 1, keys, nxt, vnext);
+    // One block: wait for its loads, put its V into the V^T tile, issue the
+    // next block's loads (K into the other tile's LDS, V into registers),
+    // then the scores, the online softmax and O^T. Blocks alternate between
+    // the two tiles (a pair a trip, so each is named statically).
+    const auto block = [&](uint32_t kb, T& cur, T& nxt) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's K copies and V loads of block kb have landed
+        store_vt<HD>(vr, cur);
+        __syncthreads();  // every wave's; and block kb - 1's tiles are no longer read
+        if (kb + 1 < blocks) load_block<HD>(a, kvh, kb + 1, keys, nxt, vr);
         // scores: lane (j, g) holds keys 32 kb + 16 tt + 4 g + e of query j
         f32x4 sacc[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             sacc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const uint32_t rr = 16 * tt + j;
 #pragma unroll
             for (int s = 0; s < kSteps; ++s) {
-                const half8 kf = __builtin_bit_cast(half8, kc.k[tt][s]);
+                const uint32_t piece = (4 * s + g) ^ (rr % T::kPieces);
+                const half8 kf = *reinterpret_cast<const half8*>(cur.k + rr * (HD * 2) + 16 * piece);
                 sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], sacc[tt], 0, 0, 0);
                 sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sacc[tt], 0, 0, 0);
             }
@@ -198,18 +225,13 @@ __global__ void __launch_bounds__(kThreads) k_attend_prompt_fast(PromptArgs a) {
         }
         lsum = lsum * factor + bs;
         m = mn;
-        // O^T: lane (j, g) gives V^T at dim 16 dt + j of keys 4 g + e (e < 4)
-        // and 16 + 4 g + e - 4 (e >= 4) of the block, the keys its P^T holds
-        const uint32_t r0 = 4 * g;
+        // O^T: lane (j, g) gives V^T at dim 16 dt + j of keys 4 g .. 4 g + 3
+        // and 16 + 4 g .. 16 + 4 g + 3 of the block, the keys its P^T holds
 #pragma unroll
         for (int dt = 0; dt < HD / 16; ++dt) {
-            const uint32_t d = 16 * dt + j;
-            half8 va;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t rr = r0 + (e < 4 ? e : 12 + e);
-                va[e] = *reinterpret_cast<const _Float16*>(vb + v_offset<HD>(rr, d));
-            }
+            const _Float16* row = cur.vt + (16 * dt + j) * T::kVtStride + 4 * g;
+            const uint2 lo = *reinterpret_cast<const uint2*>(row), hi = *reinterpret_cast<const uint2*>(row + 16);
+            const half8 va = __builtin_bit_cast(half8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[dt][e] *= factor;
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[dt], 0, 0, 0);
@@ -217,8 +239,8 @@ __global__ void __launch_bounds__(kThreads) k_attend_prompt_fast(PromptArgs a) {
         }
     };
     for (uint32_t kb = 0; kb < blocks; kb += 2) {
-        block(kb, kr[0], kr[1], s_v[0], s_v[1]);
-        if (kb + 1 < blocks) block(kb + 1, kr[1], kr[0], s_v[1], s_v[0]);
+        block(kb, s_t[0], s_t[1]);
+        if (kb + 1 < blocks) block(kb + 1, s_t[1], s_t[0]);
     }
     // lane (j, g) holds dims 16 dt + 4 g .. + 3 of query j
     if (qlive) {

@@ -68,7 +68,11 @@ SHAPES = [
     (24, 8, 64, 0, 333, 400),
     # past 64 chunks the merge takes two levels (segments of 32 chunks)
     (8, 2, 64, 5, 9000, 9100),
+    # past two items a CU, runs of chunks an item, streamed (3, 4 and 9
+    # chunks a run; the last run short, its last chunk partial)
     (32, 8, 128, 0, 20000, 20000),
+    (32, 8, 128, 0, 32768, 32768),
+    (16, 4, 64, 100, 70000, 70100),
 ]
 
 
@@ -119,17 +123,18 @@ def test_exact_kernel_is_within_the_same_bound():
     assert err <= TOL * np.abs(vc.view(np.float16)).max() / 10, err
 
 
-@pytest.mark.parametrize("hd,positions", [(128, [4096, 4100, 4223]), (64, [511, 512, 700])])
-def test_fast_step_with_o_projection(hd, positions):
+@pytest.mark.parametrize("hd,positions,cap", [(128, [4096, 4100, 4223], 4352), (64, [511, 512, 700], 4352),
+                                               (128, [32000, 32767, 20000], 32768)])
+def test_fast_step_with_o_projection(hd, positions, cap):
     """vkml_attend_step_fast at the decode state's position (a prepared
     step: q rotated, the new row appended) with the q4_K o GEMV + residual
     in the same launch, over four calls cycling through the sync blocks and
     a chunk tier below the cache's; the o projection equals
-    vkml_gemv_dot_add on the published Q8_0 output."""
+    vkml_gemv_dot_add on the published Q8_0 output. Near 32K keys the
+    items are runs of chunks."""
     H.init()
     heads, kvh = 32, 8
     n = heads * hd
-    cap = 4352
     rng = np.random.default_rng(hd)
     kc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)
     vc = rng.standard_normal((kvh, cap, hd)).astype(np.float16).view(np.uint16)

@@ -64,6 +64,9 @@ struct FastArgs {
     // merges the segments (long contexts, where one workgroup walking every
     // chunk would take longer than the items).
     uint32_t segs;
+    // Chunks an item takes (1, or more for long contexts: a run, whose
+    // partial lands in the slot of its first chunk; then segs is 1).
+    uint32_t run;
     // The merged output [heads, hd] f32 (may be null), its Q8_0 codes and f32 scales (may be null).
     float* out;
     uint8_t* values;
@@ -130,6 +133,32 @@ __device__ __forceinline__ void fast_load(const FastArgs& a, uint32_t chunk, uin
 #pragma unroll
     for (uint32_t i = 0; i < kWaveKeys * RB / 1024; ++i) {
         const uint32_t at = 1024 * i + 16 * l;  // byte in the wave's rows
+        const uint32_t rr = kWaveKeys * w + at / RB, piece = (at % RB) / 16;
+        const uint32_t src_piece = piece ^ (2 * ((rr / 4) % 4));
+        vkml::attend::load_to_lds16(vc + fast_row(a, kvh, key0, rr, n) * RB + 16 * src_piece, base + 1024 * i);
+    }
+}
+
+// A run's K and V loads for one chunk (fast_load without q): the wave's K
+// fragments into registers and its 32 V rows into its rows of the LDS tile.
+template <int HD>
+__device__ __forceinline__ void fast_load_kv(const FastArgs& a, uint32_t chunk, uint32_t kvh, uint32_t n, uint4 (&k)[2][HD / 32],
+                                             uint8_t* v_lds) {
+    constexpr uint32_t RB = HD * 2;
+    const uint32_t t = thread_index(), w = t / kWave, l = t % kWave, j = l % 16, g = l / 16;
+    const uint32_t key0 = a.kv_start + chunk * kItemKeys;
+    const auto* kc = static_cast<const uint8_t*>(a.k_cache);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const uint64_t row = fast_row(a, kvh, key0, kWaveKeys * w + 16 * tt + j, n);
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s) k[tt][s] = ldg(reinterpret_cast<const uint4*>(kc + row * RB + 64 * s + 16 * g));
+    }
+    const auto* vc = static_cast<const uint8_t*>(a.v_cache);
+    uint8_t* base = v_lds + kWaveKeys * w * RB;
+#pragma unroll
+    for (uint32_t i = 0; i < kWaveKeys * RB / 1024; ++i) {
+        const uint32_t at = 1024 * i + 16 * l;
         const uint32_t rr = kWaveKeys * w + at / RB, piece = (at % RB) / 16;
         const uint32_t src_piece = piece ^ (2 * ((rr / 4) % 4));
         vkml::attend::load_to_lds16(vc + fast_row(a, kvh, key0, rr, n) * RB + 16 * src_piece, base + 1024 * i);
@@ -263,6 +292,165 @@ __device__ __forceinline__ void fast_item(const FastArgs& a, uint32_t chunk, uin
         st_f32<true>(a.partial + at * HD + d + 1, o1);
         if (d == 0) {
             st_f32<true>(a.stats + at * 2, M);
+            st_f32<true>(a.stats + at * 2 + 1, ls);
+        }
+    }
+}
+
+// A run of chunks first .. first + count - 1 of KV head kvh (all holding
+// live keys; kv_len bounds the last) in one workgroup, for long contexts.
+// Each wave keeps its own online softmax per head across the run (its 32
+// keys of every chunk): running max M and sum L, and O rescaled by
+// 2^(M_old - M_new) as M grows. A wave's V rows are its own, so the chunks
+// need no barrier: each waits for its own loads, issues the next chunk's (K
+// into the other register set, V into the other LDS tile), then computes.
+// At the end the waves combine, as in fast_item, into the run's partial in
+// the slot of chunk `first`. v_other: the second V tile (kItemKeys rows).
+template <int HD, int GQ>
+__device__ __forceinline__ void fast_run(const FastArgs& a, uint32_t first, uint32_t count, uint32_t kvh, uint32_t kv_len,
+                                         FastSmem<HD, GQ>& sm, uint8_t* v_other) {
+    constexpr int kSteps = HD / 32;
+    const uint32_t t = thread_index(), w = t / kWave, l = t % kWave, j = l % 16, g = l / 16;
+    const bool cap = a.softcap > 0.0f;
+    const auto keys_of = [&](uint32_t c) { return min(kItemKeys, kv_len - (a.kv_start + c * kItemKeys)); };
+    uint4 k0[2][kSteps], k1[2][kSteps];
+    fast_load_kv<HD>(a, first, kvh, keys_of(first), k0, sm.v);
+    // q of head j, scaled (in log2 units without a soft cap), as hi + lo f16
+    half8 qh[kSteps], ql[kSteps];
+    {
+        const float qs = cap ? a.scale : a.scale * kLog2e;
+        const float* qp = a.q + static_cast<uint64_t>(kvh * a.group + min(j, a.group - 1)) * HD + 8 * g;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const float4 x0 = ldg(reinterpret_cast<const float4*>(qp + 32 * s));
+            const float4 x1 = ldg(reinterpret_cast<const float4*>(qp + 32 * s + 4));
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                // the f32 product through an empty asm, as in fast_item
+                float v = j < a.group ? x[e] * qs : 0.0f;
+                asm volatile("" : "+v"(v));
+                qh[s][e] = static_cast<_Float16>(v);
+                ql[s][e] = static_cast<_Float16>(v - static_cast<float>(qh[s][e]));
+            }
+        }
+    }
+    f32x4 o[HD / 16];
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float M = -__builtin_inff(), L = 0.0f;  // head j's running max (log2 units) and sum over the wave's keys
+    const auto chunk = [&](uint32_t c, const uint4 (&kc)[2][kSteps], uint4 (&kn)[2][kSteps], const uint8_t* vt, uint8_t* vn) {
+        const uint32_t n = keys_of(first + c);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's K and V of chunk c have landed
+        if (c + 1 < count) fast_load_kv<HD>(a, first + c + 1, kvh, keys_of(first + c + 1), kn, vn);
+        f32x4 acc[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            acc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+                const half8 kf = __builtin_bit_cast(half8, kc[tt][s]);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], acc[tt], 0, 0, 0);
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], acc[tt], 0, 0, 0);
+            }
+        }
+        float sc[2][4];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float x = acc[tt][e];
+                if (cap) x = a.softcap * tanhf(fminf(fmaxf(x / a.softcap, -10.0f), 10.0f)) * kLog2e;
+                const uint32_t kk = kWaveKeys * w + 16 * tt + 4 * g + e;
+                sc[tt][e] = kk < n && j < a.group ? x : -__builtin_inff();
+                m = fmaxf(m, sc[tt][e]);
+            }
+        {
+            const uint2 a16 = swap_rows<16>(__float_as_uint(m));
+            m = fmaxf(__uint_as_float(a16.x), __uint_as_float(a16.y));
+            const uint2 a32 = swap_rows<32>(__float_as_uint(m));
+            m = fmaxf(__uint_as_float(a32.x), __uint_as_float(a32.y));
+        }
+        const float mn = fmaxf(M, m);
+        const float factor = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
+        const bool any = mn != -__builtin_inff();
+        float bs = 0.0f;
+        half8 ph, pl;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p = any && sc[tt][e] != -__builtin_inff() ? __builtin_amdgcn_exp2f(sc[tt][e] - mn) : 0.0f;
+                bs += p;
+                const _Float16 hi = static_cast<_Float16>(p);
+                ph[4 * tt + e] = hi;
+                pl[4 * tt + e] = static_cast<_Float16>(p - static_cast<float>(hi));
+            }
+        {
+            const uint2 a16 = swap_rows<16>(__float_as_uint(bs));
+            bs = __uint_as_float(a16.x) + __uint_as_float(a16.y);
+            const uint2 a32 = swap_rows<32>(__float_as_uint(bs));
+            bs = __uint_as_float(a32.x) + __uint_as_float(a32.y);
+        }
+        L = L * factor + bs;
+        M = mn;
+        // O holds heads 4 g + e: their factors come from lanes 4 g + e
+        float f4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f4[e] = __shfl(factor, 4 * g + e, kWave);
+        const uint32_t r0 = kWaveKeys * w + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) {
+            const uint32_t d = 16 * dt + j;
+            half8 vb;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t rr = r0 + (e < 4 ? e : 12 + e);
+                vb[e] = *reinterpret_cast<const _Float16*>(vt + v_offset<HD>(rr, d));
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[dt][e] *= f4[e];
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vb, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[dt], 0, 0, 0);
+        }
+    };
+    for (uint32_t c = 0; c < count; c += 2) {
+        chunk(c, k0, k1, sm.v, v_other);
+        if (c + 1 < count) chunk(c + 1, k1, k0, v_other, sm.v);
+    }
+    // lane (j, g) holds heads 4 g .. 4 g + 3 at dim 16 dt + j
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (4 * g + e < GQ) sm.o[w][4 * g + e][16 * dt + j] = o[dt][e];
+    if (l < GQ) {
+        sm.m[w][l] = M;
+        sm.l[w][l] = L;
+    }
+    __syncthreads();
+    // The run's partial: the waves' outputs at the run's max.
+    for (uint32_t u = t; u < GQ * HD / 2; u += kThreads) {
+        const uint32_t h = 2 * u / HD, d = 2 * u % HD;
+        if (h >= a.group) continue;
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) mx = fmaxf(mx, sm.m[q][h]);
+        float o0 = 0.0f, o1 = 0.0f, ls = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float mq = sm.m[q][h];
+            const float f = mq == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mq - mx);
+            o0 += f * sm.o[q][h][d];
+            o1 += f * sm.o[q][h][d + 1];
+            ls += f * sm.l[q][h];
+        }
+        const uint64_t at = static_cast<uint64_t>(kvh * a.group + h) * a.chunks + first;
+        st_f32<true>(a.partial + at * HD + d, o0);
+        st_f32<true>(a.partial + at * HD + d + 1, o1);
+        if (d == 0) {
+            st_f32<true>(a.stats + at * 2, mx);
             st_f32<true>(a.stats + at * 2 + 1, ls);
         }
     }

@@ -49,7 +49,7 @@ __device__ __forceinline__ bool arrive_last(uint32_t* c, uint32_t arrivals) {
     return s_last != 0;
 }
 
-template <int HD, int GQ, int FMT, bool FULL, int DEEP>
+template <int HD, int GQ, int FMT, bool FULL, int DEEP, bool RUN>
 __global__ void __launch_bounds__(kThreads) k_attend_fast(FastArgs a, FastLaunch f, vkml::gemv::GemvArgs g) {
     extern __shared__ uint4 smem[];
     if constexpr (FMT != kNoGemv) {
@@ -66,6 +66,26 @@ __global__ void __launch_bounds__(kThreads) k_attend_fast(FastArgs a, FastLaunch
     auto& sm = *reinterpret_cast<FastSmem<HD, GQ>*>(smem);
     const uint32_t L = blockIdx.x, kvh = L % a.kv_heads, chunk = L / a.kv_heads;
     if (f.next && L == 0 && threadIdx.x < OSync::kCopies) OSync::counter(f.next, threadIdx.x)[0] = 0u;
+    if constexpr (RUN) {
+        // Long contexts: item `chunk` is the run of chunks run * chunk ..,
+        // its partial in the slot of the first; one merge level.
+        const uint32_t first = chunk * a.run;
+        const uint32_t kv_len = a.state ? static_cast<uint32_t>(ld_scalar_i32(&a.state->position)) + 1u : a.kv_len;
+        if (f.error && L == 0 && threadIdx.x == 0 && kv_len - a.kv_start > a.chunks * kItemKeys)
+            __hip_atomic_store(f.error, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t live = min(a.chunks, (kv_len - a.kv_start + kItemKeys - 1) / kItemKeys);
+        if (first < live)
+            fast_run<HD, GQ>(a, first, min(a.run, live - first), kvh, kv_len, sm, reinterpret_cast<uint8_t*>(smem) + sizeof(FastSmem<HD, GQ>));
+        if (!arrive_last(a.arrive + FusedSync::kArriveStride * kvh, (a.chunks + a.run - 1) / a.run)) return;
+        fast_merge<HD, GQ>(a, kvh, 0, (live + a.run - 1) / a.run, a.run, -1, reinterpret_cast<float*>(sm.v));
+        if (f.sync) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (threadIdx.x < OSync::kCopies)
+                __hip_atomic_fetch_add(OSync::counter(f.sync, threadIdx.x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    } else {
     FastLoads<HD> ld;
     // Chunks whose keys are all live at every position the launch serves
     // load before the position is read.
@@ -105,6 +125,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_fast(FastArgs a, FastLaunch
         if (threadIdx.x < OSync::kCopies)
             __hip_atomic_fetch_add(OSync::counter(f.sync, threadIdx.x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    }
 }
 
 template <int HD, int GQ>
@@ -113,12 +134,12 @@ constexpr size_t item_lds() {
 }
 
 // Resident workgroups a CU holds of kernel fn at lds bytes (cached per kernel).
-template <int HD, int GQ, int FMT, bool FULL, int DEEP>
+template <int HD, int GQ, int FMT, bool FULL, int DEEP, bool RUN>
 int per_cu(size_t lds) {
     static int n = -1;
     static size_t at = 0;
     if (n < 0 || at != lds) {
-        const void* fn = reinterpret_cast<const void*>(&k_attend_fast<HD, GQ, FMT, FULL, DEEP>);
+        const void* fn = reinterpret_cast<const void*>(&k_attend_fast<HD, GQ, FMT, FULL, DEEP, RUN>);
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, lds) != hipSuccess) n = 0;
         at = lds;
     }
@@ -128,13 +149,22 @@ int per_cu(size_t lds) {
 // Launches (or with dry, only checks) the one launch; false where the grid
 // could not make progress (the o GEMV's waiting workgroups would fill every
 // slot) -- nothing is launched then.
+template <int HD, int GQ, int FMT, bool FULL, int DEEP, bool RUN>
+bool launch_run(const FastArgs& a, const FastLaunch& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs, bool dry) {
+    const size_t item = item_lds<HD, GQ>() + (RUN ? kItemKeys * HD * 2 : 0);  // a run's second V tile
+    const size_t lds = std::max<size_t>(item, FMT == kNoGemv ? 0 : vkml::gemv::stage_bytes(g.k, false));
+    if (gemv_wgs && static_cast<uint64_t>(per_cu<HD, GQ, FMT, FULL, DEEP, RUN>(lds)) * vkml::abi::compute_units() <= gemv_wgs) return false;
+    if (dry) return true;
+    hipLaunchKernelGGL((k_attend_fast<HD, GQ, FMT, FULL, DEEP, RUN>), dim3(f.items + gemv_wgs), dim3(kThreads), lds, vkml::abi::stream(), a, f,
+                       g);
+    return true;
+}
+
+// Runs of chunks (a.run > 1) take their own kernel: its second register
+// set and V tile would cost the one-chunk items their occupancy.
 template <int HD, int GQ, int FMT, bool FULL, int DEEP>
 bool launch_as(const FastArgs& a, const FastLaunch& f, const vkml::gemv::GemvArgs& g, uint32_t gemv_wgs, bool dry) {
-    const size_t lds = std::max<size_t>(item_lds<HD, GQ>(), FMT == kNoGemv ? 0 : vkml::gemv::stage_bytes(g.k, false));
-    if (gemv_wgs && static_cast<uint64_t>(per_cu<HD, GQ, FMT, FULL, DEEP>(lds)) * vkml::abi::compute_units() <= gemv_wgs) return false;
-    if (dry) return true;
-    hipLaunchKernelGGL((k_attend_fast<HD, GQ, FMT, FULL, DEEP>), dim3(f.items + gemv_wgs), dim3(kThreads), lds, vkml::abi::stream(), a, f, g);
-    return true;
+    return a.run > 1 ? launch_run<HD, GQ, FMT, FULL, DEEP, true>(a, f, g, gemv_wgs, dry) : launch_run<HD, GQ, FMT, FULL, DEEP, false>(a, f, g, gemv_wgs, dry);
 }
 
 template <int HD, int GQ>
@@ -158,6 +188,19 @@ uint32_t merge_segments(uint32_t chunks, uint32_t kv_heads) {
     if (chunks <= kOneLevel) return 1;
     const uint32_t segs = (chunks + kSegment - 1) / kSegment;
     return kv_heads * (1 + segs) <= FusedSync::kMaxSets ? segs : 1;
+}
+
+// Chunks an item takes. One while the items fit two workgroups a CU (every
+// item's loads go out at once); past that, runs that bring the items down
+// to about that many, each workgroup streaming its chunks with the next
+// one's loads in flight (a grid of one chunk an item would run in rounds
+// whose loads all go out, and then all compute, together), and at most
+// kOneLevel runs a KV head, so that one merge level takes them.
+uint32_t run_length(uint32_t chunks, uint32_t kv_heads) {
+    const uint64_t slots = 2ull * vkml::abi::compute_units();
+    if (static_cast<uint64_t>(chunks) * kv_heads <= slots) return 1;
+    const uint32_t by_slots = static_cast<uint32_t>((static_cast<uint64_t>(chunks) * kv_heads + slots - 1) / slots);
+    return std::max(by_slots, (chunks + kOneLevel - 1) / kOneLevel);
 }
 
 bool launch_fast(uint32_t hd, const FastArgs& a, const FastLaunch& f, const vkml::gemv::GemvArgs* g, uint32_t b_type, bool dry) {
@@ -206,10 +249,11 @@ int vkml_attend_fast(const vkml_attend_params* p, const float* q, const void* k_
                    "attend_fast: " + std::to_string(p->chunks) + " chunks of 128 keys do not cover " + std::to_string(keys) + " keys");
     VKML_CHECK_ARG(q && k_cache && v_cache && partial && stats && sync && (out || values), "attend_fast: null buffer");
     VKML_CHECK_ARG(!values || scales, "attend_fast: quantized output needs scales");
+    const uint32_t run = run_length(p->chunks, p->kv_heads);
     const FastArgs a{q, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
                      p->kv_start, p->kv_len, p->chunks, p->scale, p->softcap, 0, FusedSync::arrive(sync, 0),
-                     merge_segments(p->chunks, p->kv_heads), out, static_cast<uint8_t*>(values), scales};
-    const FastLaunch f{p->chunks * p->kv_heads, nullptr, nullptr, nullptr, 0};
+                     run > 1 ? 1 : merge_segments(p->chunks, p->kv_heads), run, out, static_cast<uint8_t*>(values), scales};
+    const FastLaunch f{(p->chunks + run - 1) / run * p->kv_heads, nullptr, nullptr, nullptr, 0};
     vkml::abi::ProfileScope prof("attend_fast");
     launch_fast(p->head_dim, a, f, nullptr, 0, false);
     return vkml::abi::check_launch("attend_fast");
@@ -221,9 +265,11 @@ int vkml_attend_step_fast_supported(const vkml_attend_step_params* p, const vkml
         p->heads / p->kv_heads > 8 || p->kv_heads > FusedSync::kMaxSets || p->window || !p->prepared || p->chunks == 0 || p->chunks > 1024)
         return 0;
     if (!o_fusable(o, p->heads, p->head_dim)) return 0;
+    const uint32_t run = run_length(p->chunks, p->kv_heads);
     const FastArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
-                     0, 0, p->chunks, p->scale, p->softcap, 0, nullptr, 1, nullptr, nullptr, nullptr};
-    const FastLaunch f{p->chunks * p->kv_heads, nullptr, nullptr, nullptr, 0};
+                     0, 0, p->chunks, p->scale, p->softcap, 0, nullptr, 1, run, nullptr, nullptr, nullptr};
+    const FastLaunch f{(p->chunks + run - 1) / run * p->kv_heads, nullptr, nullptr, nullptr, 0};
+    if (run > 1) return launch_fast(p->head_dim, a, f, nullptr, 0, true) ? 1 : 0;  // the o GEMV apart
     const vkml::gemv::GemvArgs g{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, o->n, o->k};
     return launch_fast(p->head_dim, a, f, &g, o->b_type, true) ? 1 : 0;
 }
@@ -248,10 +294,25 @@ int vkml_attend_step_fast(const vkml_attend_step_params* p, const float* qkv, vo
                        " attention outputs, with q4_K or q8_0 (f16 scales) weights");
     uint32_t* own = sync + static_cast<uint64_t>(block) * FusedSync::kWords;
     uint32_t* next = sync + static_cast<uint64_t>((block + 1) % blocks) * FusedSync::kWords;
+    const uint32_t run = run_length(p->chunks, p->kv_heads);
     const FastArgs a{qkv, k_cache, v_cache, partial, stats, state, p->heads, p->kv_heads, p->heads / p->kv_heads, p->capacity,
                      p->kv_start, 0, p->chunks, p->scale, p->softcap, std::min(p->ready_chunks, p->chunks), FusedSync::arrive(own, 0),
-                     merge_segments(p->chunks, p->kv_heads), out, static_cast<uint8_t*>(values), scales};
-    const FastLaunch f{p->chunks * p->kv_heads, own, next, sync, vkml::abi::wait_limit()};
+                     run > 1 ? 1 : merge_segments(p->chunks, p->kv_heads), run, out, static_cast<uint8_t*>(values), scales};
+    if (run > 1) {
+        // Runs of chunks: the attention launch, then the o GEMV + residual
+        // apart (the run kernel's second register set and V tile leave too
+        // few slots for the GEMV's waiting workgroups). The launch zeroes the
+        // next block's o counters and reports a position past its chunks on
+        // the same flag.
+        const FastLaunch f{(p->chunks + run - 1) / run * p->kv_heads, nullptr, next, sync, 0};
+        {
+            vkml::abi::ProfileScope prof("attend_fast");
+            launch_fast(p->head_dim, a, f, nullptr, 0, false);
+            if (int r = vkml::abi::check_launch("attend_step_fast")) return r;
+        }
+        return vkml_gemv_dot_add(o, values, o_values, x, o_scales, scales, x);
+    }
+    const FastLaunch f{(p->chunks + run - 1) / run * p->kv_heads, own, next, sync, vkml::abi::wait_limit()};
     const vkml::gemv::GemvArgs g{static_cast<const uint4*>(values), scales, o_values, o_scales, nullptr, nullptr, x, x, o->n, o->k};
     vkml::abi::ProfileScope prof("attend_fast");
     VKML_CHECK_ARG(launch_fast(p->head_dim, a, f, &g, o->b_type, false),

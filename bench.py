@@ -70,8 +70,8 @@ PROMPT = 4096
 GATE_UP_TRAFFIC = 67_530_123
 GATE_UP_TRAFFIC_SOURCES = "b8ec832d8172fb19"
 TRAFFIC_FILES = ("vkml-framework_amd/csrc/gemv.hpp", "vkml-framework_amd/csrc/k_gemv.hip", "vkml-framework_amd/csrc/device.hpp")
-ATTEND_TRAFFIC = 28_572_130
-ATTEND_TRAFFIC_SOURCES = "c977512c9dd933cd"
+ATTEND_TRAFFIC = 28_566_713
+ATTEND_TRAFFIC_SOURCES = "4a8995ea2854df48"
 ATTEND_TRAFFIC_POSITION = 4224  # the launch's shape the figure was taken at (position; 35 chunks, 32 loading early)
 ATTEND_FILES = ("vkml-framework_amd/csrc/k_attend.hip", "vkml-framework_amd/csrc/attend.hpp", "vkml-framework_amd/csrc/gemv.hpp",
                 "vkml-framework_amd/csrc/device.hpp")

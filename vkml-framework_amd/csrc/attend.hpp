@@ -316,9 +316,34 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
     // -0 for the products of f32 and f16 values taken as fma(a, b, -0) (dot4h)
     float nz = -0.0f;
     asm volatile("" : "+v"(nz));
-    // Scores: part g of each head, then ((0 + p0) + p1) + p2) + p3; heads
-    // two at a time (their q in registers), sharing the K registers.
-    constexpr int HB = HPW < 2 ? HPW : 2;
+    // Scores: part g of each head, then ((0 + p0) + p1) + p2) + p3; HB heads
+    // a pass (their q in registers) over the K registers. Two a pass at two
+    // heads a workgroup; at four, one a pass keeps the chunk pass at 106
+    // VGPRs (four workgroups a CU instead of three at 137), and every
+    // product is then one v_fma_mix_f32 rather than a widening shared by
+    // two heads and two fmas.
+    constexpr int HB = HPW == 2 ? 2 : 1;
+    // K as loaded, except that in the chunk holding the appended key its
+    // row takes the new key's bits (its copy in the cache may predate the
+    // append): one patch here, branch-free scores below.
+    KRaw<F16> kr[kPasses][KPL];
+#pragma unroll
+    for (uint32_t p = 0; p < kPasses; ++p)
+#pragma unroll
+        for (uint32_t j = 0; j < KPL; ++j) kr[p][j] = ld.k[p][j];
+    if (holds_new) {
+#pragma unroll
+        for (uint32_t p = 0; p < kPasses; ++p) {
+            if (p * kSlots + slot != n - 1) continue;
+#pragma unroll
+            for (uint32_t j = 0; j < KPL; ++j) {
+                const uint32_t i = lane4 + kLanes * j;
+                if constexpr (F16) kr[p][j] = make_uint2(sm.knew[4 * i] | (sm.knew[4 * i + 1] << 16), sm.knew[4 * i + 2] | (sm.knew[4 * i + 3] << 16));
+                else kr[p][j] = make_float4(__uint_as_float(sm.knew[4 * i]), __uint_as_float(sm.knew[4 * i + 1]),
+                                            __uint_as_float(sm.knew[4 * i + 2]), __uint_as_float(sm.knew[4 * i + 3]));
+            }
+        }
+    }
 #pragma unroll
     for (int hb = 0; hb < HPW; hb += HB) {
         float4 qr[HB][KPL];
@@ -332,19 +357,12 @@ __device__ __forceinline__ void attend_chunk_item(const ChunkArgs& a, uint32_t c
 #pragma unroll
         for (uint32_t p = 0; p < kPasses; ++p) {
             const uint32_t key = p * kSlots + slot;
-            const bool fresh = holds_new && key == n - 1;
             float part[HB];
 #pragma unroll
             for (int h = 0; h < HB; ++h) part[h] = 0.0f;
 #pragma unroll
             for (uint32_t j = 0; j < KPL; ++j) {
-                KRaw<F16> kw = ld.k[p][j];
-                if (fresh) {
-                    const uint32_t i = lane4 + kLanes * j;
-                    if constexpr (F16) kw = make_uint2(sm.knew[4 * i] | (sm.knew[4 * i + 1] << 16), sm.knew[4 * i + 2] | (sm.knew[4 * i + 3] << 16));
-                    else kw = make_float4(__uint_as_float(sm.knew[4 * i]), __uint_as_float(sm.knew[4 * i + 1]),
-                                          __uint_as_float(sm.knew[4 * i + 2]), __uint_as_float(sm.knew[4 * i + 3]));
-                }
+                const KRaw<F16> kw = kr[p][j];
 #pragma unroll
                 for (int h = 0; h < HB; ++h) {
                     if constexpr (F16) part[h] += dot4h(qr[h][j], kw, nz);

@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(kThreads) k_attend_fast(FastArgs a, FastLaunch
                 __hip_atomic_fetch_add(OSync::counter(f.sync, threadIdx.x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
-    } else {
+    }
     FastLoads<HD> ld;
     // Chunks whose keys are all live at every position the launch serves
     // load before the position is read.
@@ -124,7 +124,6 @@ __global__ void __launch_bounds__(kThreads) k_attend_fast(FastArgs a, FastLaunch
         __syncthreads();
         if (threadIdx.x < OSync::kCopies)
             __hip_atomic_fetch_add(OSync::counter(f.sync, threadIdx.x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
     }
 }
 

@@ -595,8 +595,9 @@ def prefill_rates(model, spec, prompt, lengths, L):
     """Prompts of the given lengths at once from position 0 (the cache rows
     they write are the decode run's, which is over): a warm-up pass, a timed
     pass, and a HIP-event profile pass. MFMA utilisation is matmul_dot's
-    int8 operations (2 per multiply-accumulate) over its event time, against
-    the 5.0 POP/s dense int8 peak."""
+    int8 operations (2 per multiply-accumulate) over its event time (with
+    matmul_dot_add's, the o and down projections), against the 5.0 POP/s
+    dense int8 peak."""
     out = []
     for n in [n for n in lengths if 1 < n <= len(prompt)]:
         toks = prompt[:n]
@@ -620,7 +621,8 @@ def prefill_rates(model, spec, prompt, lengths, L):
             k = name.split(":")[0]
             c, t = by_kernel.get(k, (0, 0.0))
             by_kernel[k] = (c + calls, t + ms)
-        mm_ms = by_kernel.get("matmul_dot", (0, 0.0))[1]
+        # the o and down projections take matmul_dot_add (the residual add in the store)
+        mm_ms = sum(by_kernel.get(k, (0, 0.0))[1] for k in ("matmul_dot", "matmul_dot_add"))
         ops = 2.0 * n * matrix_macs(spec)
         tops = ops / (mm_ms * 1e-3) / 1e12 if mm_ms else None
         top = sorted(by_kernel.items(), key=lambda kv: -kv[1][1])[:8]

@@ -174,6 +174,15 @@ typedef struct vkml_quantize_params {
     uint32_t scale_type;
 } vkml_quantize_params;
 int vkml_quantize(const vkml_quantize_params* p, const void* d_x, void* d_values, void* d_scales);
+/* The SwiGLU product of a prompt's MLP and its Q8_0 form in one pass, as
+ * llama.cpp:381-384 dispatches silu (shaders/unary.comp:21-24), mul
+ * (binary.comp) and, for the int8 down projection, quantize.comp
+ * (matmul.cpp:225-229): h[i] = silu(gate[i]) * up[i] in those f32
+ * operations, then h's Q8_0 codes (count bytes) and f32 scales (one per 32
+ * values) as vkml_quantize's Q8_0/F32 form. count a multiple of 32; gate
+ * and up 16-byte aligned. */
+int vkml_swiglu_quantize(uint32_t count, const float* d_gate, const float* d_up, void* d_values,
+                         float* d_scales);
 
 /* shaders/dequantize.comp, src/ops/quantize.cpp:79-94: count values of a
  * [rows, cols] matrix (cols given for Q4_K's super-block rows). */
@@ -213,6 +222,14 @@ int vkml_gemv_dot(const vkml_gemv_dot_params* p, const void* d_a_values, const v
  * (v_mfma_i32_16x16x32_i8: one block of a 16 x 16 tile). */
 int vkml_matmul_dot(const vkml_gemv_dot_params* p, const void* d_a_values, const void* d_b_values,
                     float* d_out, const void* d_b_scales, const float* d_a_scales);
+/* vkml_matmul_dot with the residual add that follows a prompt's o and down
+ * projections (llama.cpp:374,386; binary.comp's add, src/ops/
+ * elementwise.cpp:23-60) done as each output is stored: d_out[m, n] =
+ * d_residual[m, n] + (a_q . b^T)[m, n], the same f32 sum (d_out may equal
+ * d_residual). */
+int vkml_matmul_dot_add(const vkml_gemv_dot_params* p, const void* d_a_values, const void* d_b_values,
+                        float* d_out, const void* d_b_scales, const float* d_a_scales,
+                        const float* d_residual);
 /* As vkml_gemv_dot for m = 1, with the residual add that follows the o and
  * down projections (llama.cpp:374,386) done in the epilogue:
  * d_out[n] = d_residual[n] + a_q . b[n] (d_out may equal d_residual). */

@@ -298,6 +298,51 @@ def test_gemv_dot_add_and_swiglu(fmt):
     assert np.array_equal(bits(got), bits(O.silu(g) * u))
 
 
+@pytest.mark.parametrize("fmt,m,n,k", [(H.Q8_0, 37, 100, 512), (H.Q4_1, 64, 16384, 256), (H.Q4_K, 512, 4096, 4096),
+                                       (H.Q4_K, 2048, 4096, 256)])
+def test_matmul_dot_add_bit_exact(fmt, m, n, k):
+    # A prompt's o / down projection with the residual add in the store:
+    # residual + matmul_dot's output, the binary add's f32 sum, into a
+    # separate buffer and in place. The shapes take each launch form: tiles
+    # read from memory (37 rows), staged 16-, 32- and 64-row tiles.
+    v, s, quant, words, scales = weights(fmt, n, k, m + 7)
+    a, aw, asc = activation(k, m, m)
+    res = np.random.default_rng(m).standard_normal((m, n)).astype(np.float32)
+    want = res + O.matmul_dot(quant, aw, asc, m, words, scales, n, k)
+    prm = H.GemvDotParams(m, n, k, fmt, H.F16)
+    dres, out = dev(res), H.empty(m * n * 4)
+    H.call("vkml_matmul_dot_add", prm, p(dev(aw)), p(v), p(out), p(s), p(dev(asc)), p(dres))
+    assert np.array_equal(bits(out.download(np.float32, (m, n))), bits(want))
+    H.call("vkml_matmul_dot_add", prm, p(dev(aw)), p(v), p(dres), p(s), p(dev(asc)), p(dres))
+    assert np.array_equal(bits(dres.download(np.float32, (m, n))), bits(want))
+    with pytest.raises(H.VkmlError, match="null residual"):
+        H.call("vkml_matmul_dot_add", prm, p(dev(aw)), p(v), p(out), p(s), p(dev(asc)), None)
+
+
+@pytest.mark.parametrize("count", [32, 4096 + 32 * 5, 512 * 14336])
+def test_swiglu_quantize_bit_exact(count):
+    # The prompt MLP's silu(gate) * up and its Q8_0 form in one pass: the
+    # codes and scales vkml_quantize gives on the oracle's silu and product,
+    # bit for bit. Blocks of zeros (scale 0), gates past exp's range both
+    # ways (silu -0 and the gate itself), a ragged tail of 32-value blocks
+    # against the 256-thread workgroups.
+    rng = np.random.default_rng(count)
+    g = (rng.standard_normal(count) * 8).astype(np.float32)
+    u = rng.standard_normal(count).astype(np.float32)
+    if count >= 128:
+        g[:32] = 0.0
+        g[32:64] = -200.0
+        g[64:96] = 200.0
+        u[96:128] = 0.0
+    want_w, want_s = O.quantize(O.Q8_0, O.silu(g) * u, False)
+    dw, ds = H.empty(count), H.empty(count // 8)
+    H.call("vkml_swiglu_quantize", count, p(dev(g)), p(dev(u)), p(dw), p(ds))
+    assert np.array_equal(dw.download(np.uint32, count // 4), want_w)
+    assert np.array_equal(bits(ds.download(np.float32, count // 32)), bits(want_s))
+    with pytest.raises(H.VkmlError, match="multiple of 32"):
+        H.call("vkml_swiglu_quantize", 48, p(dev(g)), p(dev(u)), p(dw), p(ds))
+
+
 @pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 4096, 4096), (H.Q4_K, 384, 256), (H.Q8_0, 4096, 4096), (H.Q4_0, 1024, 2048),
                                      (H.Q4_1, 72, 96), (H.Q8_0, 72, 96)])
 def test_gemv_fused_quantize_prologue_bit_exact(fmt, n, k):

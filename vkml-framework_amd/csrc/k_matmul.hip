@@ -56,7 +56,15 @@ struct MatmulDotArgs {
     const void* b_scales;  // per-block scales (q4_K: the 16-byte super-block headers)
     float* out;           // [M, N]
     uint32_t m, n, k;
+    const float* residual;  // [M, N] added to each output, or null
 };
+
+// out[row, col] = v, or residual[row, col] + v (the binary add that
+// follows the o and down projections, the same f32 sum).
+__device__ __forceinline__ void store_out(const MatmulDotArgs& p, uint32_t row, uint32_t col, float v) {
+    const uint64_t at = static_cast<uint64_t>(row) * p.n + col;
+    p.out[at] = p.residual ? p.residual[at] + v : v;
+}
 
 __device__ __forceinline__ float f16_at(const void* p, uint64_t i) { return f16_bits_to_float(ldg(static_cast<const uint16_t*>(p) + i)); }
 
@@ -283,7 +291,7 @@ __global__ void __launch_bounds__(kT) k_matmul_dot(MatmulDotArgs p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t row = row0 + 16 * r + 4 * g + i;
-                if (row < p.m && col < p.n) p.out[static_cast<uint64_t>(row) * p.n + col] = acc[r][c][i];
+                if (row < p.m && col < p.n) store_out(p, row, col, acc[r][c][i]);
             }
         }
 }
@@ -502,7 +510,7 @@ __global__ void __launch_bounds__(kT) k_matmul_dot_staged(MatmulDotArgs p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t row = row0 + 16 * r + 4 * g + i;
-                if (row < p.m && col < p.n) p.out[static_cast<uint64_t>(row) * p.n + col] = acc[r][c][i];
+                if (row < p.m && col < p.n) store_out(p, row, col, acc[r][c][i]);
             }
         }
 }
@@ -545,24 +553,21 @@ void launch(const MatmulDotArgs& p) {
     else launch_tiles<FMT, F16S, 1, 1>(p);
 }
 
-}  // namespace
-
-extern "C" {
-
-int vkml_matmul_dot(const vkml_gemv_dot_params* p, const void* a_values, const void* b_values, float* out, const void* b_scales,
-                    const float* a_scales) {
+int matmul_dot_common(const char* what, const vkml_gemv_dot_params* p, const void* a_values, const void* b_values, float* out,
+                      const void* b_scales, const float* a_scales, const float* residual) {
     VKML_REQUIRE_INIT();
-    VKML_CHECK_ARG(p, "matmul_dot: null params");
+    const std::string name = what;
+    VKML_CHECK_ARG(p, name + ": null params");
     VKML_CHECK_ARG(p->b_type == VKML_Q8_0 || p->b_type == VKML_Q4_0 || p->b_type == VKML_Q4_1 || p->b_type == VKML_Q4_K,
-                   "matmul_dot: weights must be q8_0, q4_0, q4_1 or q4_K, got type " + std::to_string(p->b_type));
-    VKML_CHECK_ARG(p->b_type == VKML_Q4_K || p->scale_type == VKML_F16 || p->scale_type == VKML_F32, "matmul_dot: scales must be f16 or f32");
+                   name + ": weights must be q8_0, q4_0, q4_1 or q4_K, got type " + std::to_string(p->b_type));
+    VKML_CHECK_ARG(p->b_type == VKML_Q4_K || p->scale_type == VKML_F16 || p->scale_type == VKML_F32, name + ": scales must be f16 or f32");
     const uint32_t unit = p->b_type == VKML_Q4_K ? 256 : 32;
-    VKML_CHECK_ARG(p->k > 0 && p->k % unit == 0, "matmul_dot: k = " + std::to_string(p->k) + " must be a positive multiple of " + std::to_string(unit));
+    VKML_CHECK_ARG(p->k > 0 && p->k % unit == 0, name + ": k = " + std::to_string(p->k) + " must be a positive multiple of " + std::to_string(unit));
     if (p->m == 0 || p->n == 0) return VKML_OK;
-    VKML_CHECK_ARG(a_values && b_values && out && b_scales && a_scales, "matmul_dot: null buffer");
+    VKML_CHECK_ARG(a_values && b_values && out && b_scales && a_scales, name + ": null buffer");
     const MatmulDotArgs args{static_cast<const uint8_t*>(a_values), a_scales, static_cast<const uint8_t*>(b_values), b_scales, out,
-                             p->m, p->n, p->k};
-    vkml::abi::ProfileScope prof("matmul_dot");
+                             p->m, p->n, p->k, residual};
+    vkml::abi::ProfileScope prof(what);
     const bool f16 = p->scale_type == VKML_F16;
     switch (p->b_type) {
         case VKML_Q8_0: f16 ? launch<VKML_Q8_0, true>(args) : launch<VKML_Q8_0, false>(args); break;
@@ -570,7 +575,23 @@ int vkml_matmul_dot(const vkml_gemv_dot_params* p, const void* a_values, const v
         case VKML_Q4_1: f16 ? launch<VKML_Q4_1, true>(args) : launch<VKML_Q4_1, false>(args); break;
         default: launch<VKML_Q4_K, true>(args); break;
     }
-    return vkml::abi::check_launch("matmul_dot");
+    return vkml::abi::check_launch(what);
+}
+
+}  // namespace
+
+extern "C" {
+
+int vkml_matmul_dot(const vkml_gemv_dot_params* p, const void* a_values, const void* b_values, float* out, const void* b_scales,
+                    const float* a_scales) {
+    return matmul_dot_common("matmul_dot", p, a_values, b_values, out, b_scales, a_scales, nullptr);
+}
+
+int vkml_matmul_dot_add(const vkml_gemv_dot_params* p, const void* a_values, const void* b_values, float* out, const void* b_scales,
+                        const float* a_scales, const float* residual) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(residual || (p && (p->m == 0 || p->n == 0)), "matmul_dot_add: null residual");
+    return matmul_dot_common("matmul_dot_add", p, a_values, b_values, out, b_scales, a_scales, residual);
 }
 
 }  // extern "C"

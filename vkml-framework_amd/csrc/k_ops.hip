@@ -132,11 +132,10 @@ __global__ void k_quantize(vkml_quantize_params p, const void* x, uint32_t* valu
     }
 }
 
-// Activations to Q8_0 with f32 scales, 8 lanes per block of 32.
-__global__ void k_quantize_act(uint32_t blocks, const float4* x, uint32_t* values, float* scales) {
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // float4 index
-    const bool live = i < static_cast<uint64_t>(blocks) * 8;
-    const float4 v = live ? x[i] : make_float4(0, 0, 0, 0);
+// Float4 i of a Q8_0 row with f32 scales, 8 lanes per block of 32 (every
+// lane of the group takes part in the absmax, live or not): the block's
+// scale absmax / 127, the four codes packed into word i.
+__device__ __forceinline__ void store_q8_lane(float4 v, bool live, uint64_t i, uint32_t* values, float* scales) {
     const float absmax = group_max<8>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     const float d = absmax / 127.0f;
     const float inv = d > 0.0f ? 1.0f / d : 0.0f;
@@ -144,6 +143,28 @@ __global__ void k_quantize_act(uint32_t blocks, const float4* x, uint32_t* value
     values[i] = (static_cast<uint32_t>(quant_code(v.x, inv)) & 0xFFu) | ((static_cast<uint32_t>(quant_code(v.y, inv)) & 0xFFu) << 8) |
                 ((static_cast<uint32_t>(quant_code(v.z, inv)) & 0xFFu) << 16) | (static_cast<uint32_t>(quant_code(v.w, inv)) << 24);
     if (i % 8 == 0) scales[i / 8] = d;
+}
+
+// Activations to Q8_0 with f32 scales.
+__global__ void k_quantize_act(uint32_t blocks, const float4* x, uint32_t* values, float* scales) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // float4 index
+    const bool live = i < static_cast<uint64_t>(blocks) * 8;
+    store_q8_lane(live ? x[i] : make_float4(0, 0, 0, 0), live, i, values, scales);
+}
+
+// silu(gate) * up, then its Q8_0 form: the f32 operations of k_unary's silu
+// and k_binary's mul, the codes and scales of k_quantize_act.
+__device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + vk_expf(-g)) * u; }
+
+__global__ void k_swiglu_quantize(uint32_t blocks, const float4* gate, const float4* up, uint32_t* values, float* scales) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // float4 index
+    const bool live = i < static_cast<uint64_t>(blocks) * 8;
+    float4 h = make_float4(0, 0, 0, 0);
+    if (live) {
+        const float4 g = gate[i], u = up[i];
+        h = make_float4(swiglu(g.x, u.x), swiglu(g.y, u.y), swiglu(g.z, u.z), swiglu(g.w, u.w));
+    }
+    store_q8_lane(h, live, i, values, scales);
 }
 
 __global__ void k_dequantize(vkml_dequantize_params p, const void* values, const void* scales, float* out) {
@@ -735,6 +756,21 @@ int vkml_quantize(const vkml_quantize_params* p, const void* x, void* values, vo
     ProfileScope prof("quantize");
     hipLaunchKernelGGL(k_quantize, dim3(blocks_for(p->blocks)), dim3(256), 0, S(), *p, x, static_cast<uint32_t*>(values), scales);
     return vkml::abi::check_launch("quantize");
+}
+
+int vkml_swiglu_quantize(uint32_t count, const float* gate, const float* up, void* values, float* scales) {
+    VKML_REQUIRE_INIT();
+    VKML_CHECK_ARG(count % 32 == 0, "swiglu_quantize: count = " + std::to_string(count) + " must be a multiple of 32");
+    if (count == 0) return VKML_OK;
+    VKML_CHECK_ARG(gate && up && values && scales, "swiglu_quantize: null buffer");
+    VKML_CHECK_ARG(reinterpret_cast<uintptr_t>(gate) % 16 == 0 && reinterpret_cast<uintptr_t>(up) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(values) % 4 == 0 && reinterpret_cast<uintptr_t>(scales) % 4 == 0,
+                   "swiglu_quantize: gate and up must be 16-byte aligned, values and scales 4-byte aligned");
+    ProfileScope prof("swiglu_quantize");
+    const uint64_t threads = count / 4;
+    hipLaunchKernelGGL(k_swiglu_quantize, dim3(static_cast<uint32_t>((threads + 255) / 256)), dim3(256), 0, S(), count / 32,
+                       reinterpret_cast<const float4*>(gate), reinterpret_cast<const float4*>(up), static_cast<uint32_t*>(values), scales);
+    return vkml::abi::check_launch("swiglu_quantize");
 }
 
 int vkml_dequantize(const vkml_dequantize_params* p, const void* values, const void* scales, float* out) {

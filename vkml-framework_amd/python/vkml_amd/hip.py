@@ -106,10 +106,12 @@ SIGNATURES = {
     "vkml_graph_launch": [u64],
     "vkml_graph_destroy": [u64],
     "vkml_quantize": [P(QuantizeParams), vp, vp, vp],
+    "vkml_swiglu_quantize": [u32, vp, vp, vp, vp],
     "vkml_dequantize": [P(DequantizeParams), vp, vp, vp],
     "vkml_gemv_dot": [P(GemvDotParams), vp, vp, vp, vp, vp],
     "vkml_gemv_dot_add": [P(GemvDotParams), vp, vp, vp, vp, vp, vp],
     "vkml_matmul_dot": [P(GemvDotParams), vp, vp, vp, vp, vp],
+    "vkml_matmul_dot_add": [P(GemvDotParams), vp, vp, vp, vp, vp, vp],
     "vkml_gemv_dot_swiglu": [P(GemvDotParams), vp, vp, vp, vp, vp, vp, vp],
     "vkml_gemv": [P(GemvParams), vp, vp, vp, vp],
     "vkml_matmul": [P(MatmulParams), vp, vp, vp, vp],

@@ -653,6 +653,22 @@ struct Llama::Impl {
         }
     }
 
+    // x [t, w.rows] += in . w^T, the o and down projections with the
+    // residual add after them (llama.cpp:374,386): the add in matmul_dot's
+    // store on the matrix-core path, else the product into tmp and a binary
+    // add (the same f32 sum either way).
+    void project_add(const Weight& w, const Rows& in, std::int64_t t, float* x, float* tmp, const char* what) const {
+        if (t > 8 && in.quantized && quantized_input(w)) {
+            tag(what);
+            const vkml_gemv_dot_params p{u32(t), u32(w.rows), u32(w.cols), w.type_code(), w.scale_code()};
+            check(vkml_matmul_dot_add(&p, in.values.data(), w.values(), x, w.scales(), static_cast<const float*>(in.scales.data()), x),
+                  what);
+            return;
+        }
+        project_rows(w, in, t, tmp, what);
+        check(vkml_binary(0, u32(t * w.rows), u32(t * w.rows), x, tmp, x), "add");
+    }
+
     bool any_quantized(const std::vector<std::pair<Weight, std::int64_t>>& ws) const {
         return std::any_of(ws.begin(), ws.end(), [&](const auto& wr) { return quantized_input(wr.first); });
     }
@@ -740,8 +756,7 @@ struct Llama::Impl {
             }
             if (!merged.numel()) merged = permute(attn, {1, 0, 2}).reshape({t, qd});
             const Rows m_in = rows_of(merged, t, qd, int_dot && quantized_input(L.o) && qd % 32 == 0);
-            project_rows(L.o, m_in, t, yp, "o");
-            check(vkml_binary(0, u32(t * d), u32(t * d), xp, yp, xp), "add");
+            project_add(L.o, m_in, t, xp, yp, "o");
             tag("ffn_norm");
             const Rows h2 = norm_rows(x, L.ffn_norm, t, int_dot && (quantized_input(L.gate) || quantized_input(L.up)));
             auto* gp = static_cast<float*>(gate.data());
@@ -749,11 +764,20 @@ struct Llama::Impl {
             project_rows(L.gate, h2, t, gp, "gate");
             project_rows(L.up, h2, t, up_p, "up");
             tag("swiglu");
-            check(vkml_unary(0, u32(t * ff), 0.0f, gp, gp), "silu");
-            check(vkml_binary(2, u32(t * ff), u32(t * ff), gp, up_p, gp), "mul");
-            const Rows g_in = rows_of(gate, t, ff, int_dot && quantized_input(L.down) && ff % 32 == 0);
-            project_rows(L.down, g_in, t, yp, "down");
-            check(vkml_binary(0, u32(t * d), u32(t * d), xp, yp, xp), "add");
+            Rows g_in;
+            if (int_dot && quantized_input(L.down) && ff % 32 == 0) {
+                // silu, mul and the down projection's Q8_0 input in one pass
+                g_in.values = Tensor::empty(ctx, {t * ff / 4}, DType::I32);
+                g_in.scales = Tensor::empty(ctx, {t * ff / 32}, DType::F32);
+                g_in.quantized = true;
+                check(vkml_swiglu_quantize(u32(t * ff), gp, up_p, g_in.values.data(), static_cast<float*>(g_in.scales.data())),
+                      "swiglu");
+            } else {
+                check(vkml_unary(0, u32(t * ff), 0.0f, gp, gp), "silu");
+                check(vkml_binary(2, u32(t * ff), u32(t * ff), gp, up_p, gp), "mul");
+                g_in = rows_of(gate, t, ff, false);
+            }
+            project_add(L.down, g_in, t, xp, yp, "down");
         }
         position = end;
         // The final norm; every row through the output projection, or the

@@ -767,6 +767,68 @@ def test_attend_step_fused_bit_exact(hd, heads, kvh, pos, kv_type, fmt, n, windo
         assert np.array_equal(bits(got), bits(x2.download(np.float32, n)))
 
 
+def test_decode_layers_chained_bit_exact():
+    # Two decode layers' attention (one launch: chunks, merges, o GEMV +
+    # residual), gate|up (RMSNorm + Q8_0 prologue reading the x the
+    # attention launch just wrote, SwiGLU, Q8_0 of h) and down (+ residual,
+    # reading h's codes) back to back on the stream with no host wait
+    # between them, at cfg5's shapes and position: each kernel reads what
+    # the one before it wrote, as in the whole model, and every x and h is
+    # checked against the oracle's layer arithmetic.
+    hd, heads, kvh, d, ff, pos, ready = 128, 32, 8, 4096, 14336, 4096, 16
+    k, cap = heads * hd, pos + 200
+    chunks = (cap + 127) // 128
+    layers = 2
+    rng = np.random.default_rng(77)
+    x0 = rng.standard_normal(d).astype(np.float32)
+    x = dev(x0)
+    fbytes = H.lib().vkml_attend_fused_sync_bytes(layers)
+    fsync = H.empty(fbytes)
+    H.call("vkml_fill_u32", p(fsync), 0, fbytes // 4)
+    part, stats, st = H.empty(heads * chunks * hd * 4), H.empty(heads * chunks * 8), H.empty(16)
+    H.call("vkml_state_set", p(st), 0, pos, 0)
+    attn, avals, ascs = H.empty(k * 4), H.empty(k), H.empty(k // 32 * 4)
+    h, hv, hsc = H.empty(ff * 4), H.empty(ff), H.empty(ff // 32 * 4)
+    # every input on the device first: the launches then follow one another
+    # on the stream with nothing between them
+    L = []
+    for layer in range(layers):
+        prior = rng.standard_normal((2, kvh, cap, hd)).astype(np.float32)
+        caches = [prior[i].astype(np.float16).view(np.uint16) for i in range(2)]
+        q = rng.standard_normal((heads, hd)).astype(np.float32)
+        qkv = np.concatenate([q.ravel(), rng.standard_normal(2 * kvh * hd).astype(np.float32)])
+        nw = rng.standard_normal(d).astype(np.float32)
+        L.append(dict(caches=caches, q=q, dqkv=dev(qkv), dk=dev(caches[0]), dv=dev(caches[1]), nw=nw, dnw=dev(nw),
+                      o=weights(H.Q4_K, d, k, 100 + 4 * layer), g=weights(H.Q4_K, ff, d, 101 + 4 * layer),
+                      u=weights(H.Q4_K, ff, d, 102 + 4 * layer), dn=weights(H.Q4_K, d, ff, 103 + 4 * layer)))
+    prm = H.AttendStepParams(heads, kvh, hd, cap, 0, 0, H.F16, chunks, 0, 1, 1.0 / math.sqrt(hd), 0.0, 0, 1, ready)
+    H.synchronize()
+    for layer, w in enumerate(L):
+        H.call("vkml_attend_step_fused", prm, p(w["dqkv"]), None, p(w["dk"]), p(w["dv"]), p(part), p(stats), p(attn), p(avals),
+               p(ascs), p(st), H.GemvDotParams(1, d, k, H.Q4_K, H.F16), p(w["o"][0]), p(w["o"][1]), p(x), p(fsync), layer, layers)
+        H.call("vkml_gemv_fused", H.GemvFusedParams(ff, d, H.Q4_K, H.F16, 2, 1, 1e-5, 1), p(x), None, p(w["dnw"]), p(w["g"][0]),
+               p(w["g"][1]), p(w["u"][0]), p(w["u"][1]), None, p(h), p(hv), p(hsc))
+        H.call("vkml_gemv_dot_add", H.GemvDotParams(1, d, ff, H.Q4_K, H.F16), p(hv), p(w["dn"][0]), p(x), p(w["dn"][1]), p(hsc),
+               p(x))
+    # the oracle's layers: attention, o + residual, ffn norm, SwiGLU, down + residual
+    want_x, want_h = x0.copy(), None
+    for w in L:
+        a = O.attend_decode(w["q"], w["caches"][0], w["caches"][1], 0, pos + 1)
+        aw, asw = O.quantize(O.Q8_0, a.reshape(1, k), False)
+        _, _, oq, ow, osc = w["o"]
+        want_x = want_x + O.gemv_dot(oq, aw, asw, 1, ow, osc, d, k)[0]
+        nq, ns = O.quantize(O.Q8_0, O.rms_norm(want_x.reshape(1, d), w["nw"], 1e-5), False)
+        _, _, gq, gw, gsc = w["g"]
+        _, _, _, uw, usc = w["u"]
+        want_h = O.silu(O.gemv_dot(gq, nq, ns, 1, gw, gsc, ff, d)[0]) * O.gemv_dot(gq, nq, ns, 1, uw, usc, ff, d)[0]
+        hq, hs = O.quantize(O.Q8_0, want_h.reshape(1, ff), False)
+        _, _, dq, dw, dsc = w["dn"]
+        want_x = want_x + O.gemv_dot(dq, hq, hs, 1, dw, dsc, d, ff)[0]
+    H.call("vkml_attend_fused_check", p(fsync), layers)
+    assert np.array_equal(bits(h.download(np.float32, ff)), bits(want_h))
+    assert np.array_equal(bits(x.download(np.float32, d)), bits(want_x))
+
+
 @pytest.mark.parametrize("pos,ready,kv_type", [(4096, 16, H.F16), (300, 2, H.F32), (100, 8, H.F16), (1000, 4, H.F16)])
 def test_attend_step_fused_prepared_bit_exact(pos, ready, kv_type):
     # a prepared step (q already rotated, the new key and value already in

@@ -298,18 +298,21 @@ def test_gemv_dot_add_and_swiglu(fmt):
     assert np.array_equal(bits(got), bits(O.silu(g) * u))
 
 
-@pytest.mark.parametrize("fmt,m,n,k", [(H.Q8_0, 37, 100, 512), (H.Q4_1, 64, 16384, 256), (H.Q4_K, 512, 4096, 4096),
-                                       (H.Q4_K, 2048, 4096, 256)])
-def test_matmul_dot_add_bit_exact(fmt, m, n, k):
+@pytest.mark.parametrize("fmt,m,n,k,f16", [(H.Q8_0, 37, 100, 512, True), (H.Q4_1, 64, 16384, 256, True),
+                                           (H.Q4_K, 512, 4096, 4096, True), (H.Q4_K, 2048, 4096, 256, True),
+                                           (H.Q8_0, 130, 1000, 2048, False), (H.Q4_0, 250, 2048, 1024, True),
+                                           (H.Q4_1, 300, 640, 512, False)])
+def test_matmul_dot_add_bit_exact(fmt, m, n, k, f16):
     # A prompt's o / down projection with the residual add in the store:
     # residual + matmul_dot's output, the binary add's f32 sum, into a
     # separate buffer and in place. The shapes take each launch form: tiles
-    # read from memory (37 rows), staged 16-, 32- and 64-row tiles.
-    v, s, quant, words, scales = weights(fmt, n, k, m + 7)
+    # read from memory (37, 130 and 300 rows), staged 16-, 32- and 64-row
+    # tiles; f16 and f32 weight scales.
+    v, s, quant, words, scales = weights(fmt, n, k, m + 7, f16_scales=f16)
     a, aw, asc = activation(k, m, m)
     res = np.random.default_rng(m).standard_normal((m, n)).astype(np.float32)
     want = res + O.matmul_dot(quant, aw, asc, m, words, scales, n, k)
-    prm = H.GemvDotParams(m, n, k, fmt, H.F16)
+    prm = H.GemvDotParams(m, n, k, fmt, H.F16 if f16 else H.F32)
     dres, out = dev(res), H.empty(m * n * 4)
     H.call("vkml_matmul_dot_add", prm, p(dev(aw)), p(v), p(out), p(s), p(dev(asc)), p(dres))
     assert np.array_equal(bits(out.download(np.float32, (m, n))), bits(want))

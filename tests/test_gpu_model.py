@@ -266,17 +266,21 @@ def test_decode_steps_across_chunk_boundaries_match_oracle(files, ctx, prompt, s
         assert np.array_equal(k[:, :n], kr[:, :n]) and np.array_equal(v[:, :n], vr[:, :n])
 
 
-def test_chunk_launch_follows_the_position(files):
+@pytest.mark.parametrize("kv_f16", [True, False])
+def test_chunk_launch_follows_the_position(files, kv_f16):
     """A 4096-row cache decoding near position 1000: each step launches the
     128-key chunks its position needs, in powers of two (8 chunks up to
     position 1023, then 16), not the cache's 32. Greedy steps and single
     steps across the 1024 boundary, graph replays and eager launches, equal
-    the oracle's bit for bit."""
+    the oracle's bit for bit. With an f32 cache (head_dim 128, q4_K o) the
+    one attention launch's f32 V tile leaves it short of LDS, and the model
+    must then size its launches for the separate chunk pass, merge and o
+    GEMV instead of by position tier."""
     path = files["cfg5"]
     tokens = np.random.default_rng(13).integers(0, 32768, 1000).astype(np.int32)
-    gpu = Llama(path, 4096, kv_f16=True)
-    eager = Llama(path, 4096, kv_f16=True, use_graphs=False)
-    ref = O.Model(path, 4096, kv_f16=True)
+    gpu = Llama(path, 4096, kv_f16=kv_f16)
+    eager = Llama(path, 4096, kv_f16=kv_f16, use_graphs=False)
+    ref = O.Model(path, 4096, kv_f16=kv_f16)
     got = gpu.forward(tokens)
     same(got, ref.forward(tokens))
     same(eager.forward(tokens), got)

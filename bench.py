@@ -67,8 +67,8 @@ PROMPT = 4096
 # kernel sources it was taken on: its hash is the SHA-256 (first 16 hex
 # digits) of those files, and the line reports no traffic when they have
 # changed since.
-GATE_UP_TRAFFIC = 67_530_123
-GATE_UP_TRAFFIC_SOURCES = "b8ec832d8172fb19"
+GATE_UP_TRAFFIC = 67_212_366
+GATE_UP_TRAFFIC_SOURCES = "558e79baed80feb0"
 TRAFFIC_FILES = ("vkml-framework_amd/csrc/gemv.hpp", "vkml-framework_amd/csrc/k_gemv.hip", "vkml-framework_amd/csrc/device.hpp")
 ATTEND_TRAFFIC = 28_566_713
 ATTEND_TRAFFIC_SOURCES = "4a8995ea2854df48"

@@ -347,10 +347,12 @@ def test_swiglu_quantize_bit_exact(count):
 
 
 @pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 4096, 4096), (H.Q4_K, 384, 256), (H.Q8_0, 4096, 4096), (H.Q4_0, 1024, 2048),
-                                     (H.Q4_1, 72, 96), (H.Q8_0, 72, 96)])
+                                     (H.Q4_1, 72, 96), (H.Q8_0, 72, 96), (H.Q4_K, 6144, 4096), (H.Q4_K, 5000, 4096)])
 def test_gemv_fused_quantize_prologue_bit_exact(fmt, n, k):
     # norm = 2: the Q8_0 of the f32 row inside the GEMV (the ops API's one
-    # launch for a row), against quantize.comp + gemv_dot in the oracle
+    # launch for a row), against quantize.comp + gemv_dot in the oracle;
+    # q4_K at 6144 and 5000 rows of 4096 take the 16-lane, 24-row form (5000:
+    # a last workgroup of 8 rows)
     v, s, quant, words, scales = weights(fmt, n, k, n + 11)
     a = (np.random.default_rng(k + 1).standard_normal(k) * 3).astype(np.float32)
     aw, asc = O.quantize(O.Q8_0, a.reshape(1, k), False)
@@ -361,7 +363,8 @@ def test_gemv_fused_quantize_prologue_bit_exact(fmt, n, k):
     assert np.array_equal(bits(out.download(np.float32, n)), bits(want))
 
 
-@pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 6144, 4096), (H.Q4_K, 384, 256), (H.Q8_0, 8192, 4096), (H.Q4_0, 1024, 2048)])
+@pytest.mark.parametrize("fmt,n,k", [(H.Q4_K, 6144, 4096), (H.Q4_K, 384, 256), (H.Q8_0, 8192, 4096), (H.Q4_0, 1024, 2048),
+                                     (H.Q4_K, 5000, 4096), (H.Q8_0, 6144, 4096)])
 def test_gemv_fused_norm_prologue_bit_exact(fmt, n, k):
     # rms_norm + Q8_0 inside the GEMV == the separate kernels' results
     v, s, quant, words, scales = weights(fmt, n, k, n + 7)
